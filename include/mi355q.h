@@ -1,0 +1,232 @@
+/*
+ * mi355q - gfx950 (MI355X) kernels for llm-compressor's calibration-time
+ * quantization path, behind a plain C ABI.
+ *
+ * Conventions
+ *  - Every pointer argument named *_dev is device memory; *_host is host
+ *    memory.  The caller owns and allocates all buffers, including the
+ *    workspaces sized by the *_workspace_size queries.
+ *  - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *    Calls are stream-ordered and never synchronise, except where a
+ *    comment says otherwise.
+ *  - Matrices are row-major with an explicit leading dimension in elements.
+ *  - bf16 data is passed as raw 16-bit patterns (uint16_t / void*).
+ *  - Every entry point returns an mi355q_status; on failure a message is
+ *    available from mi355q_last_error() (thread-local).
+ *  - The library holds no mutable global state: calls on distinct streams
+ *    from several host threads are safe.
+ *
+ * Reference citations are paths inside ANGDL/llm-compressor
+ * (src/llmcompressor/...) unless they name compressed-tensors (CT).
+ */
+#ifndef MI355Q_H
+#define MI355Q_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  MI355Q_OK = 0,
+  MI355Q_INVALID_ARGUMENT = 1,
+  MI355Q_UNSUPPORTED = 2,
+  MI355Q_NOT_POSITIVE_DEFINITE = 3,
+  MI355Q_HIP_ERROR = 4
+} mi355q_status;
+
+typedef enum { MI355Q_BF16 = 0, MI355Q_F32 = 1 } mi355q_dtype;
+
+/* Quantization strategy, as compressed-tensors QuantizationStrategy. */
+typedef enum {
+  MI355Q_TENSOR = 0,
+  MI355Q_CHANNEL = 1,
+  MI355Q_GROUP = 2,
+  MI355Q_BLOCK = 3,
+  MI355Q_TOKEN = 4
+} mi355q_strategy;
+
+/* MXFP4 shared-exponent rule (see mi355q_mxfp4_quantize_pack). */
+typedef enum { MI355Q_MX_RULE_CT = 0, MI355Q_MX_RULE_OCP = 1 } mi355q_mx_rule;
+
+const char* mi355q_last_error(void);
+int mi355q_version(void);
+
+/* ------------------------------------------------------------------ Hessian
+ * H[i][j] += alpha * sum_t x[t][i] * x[t][j] for i <= j (upper triangle,
+ * diagonal included).  Elements strictly below the diagonal are never read
+ * or written.  x is [n_tokens, d] bf16 with leading dimension ldx; products
+ * of bf16 values are exact in fp32 and accumulate in fp32 (MFMA).
+ *
+ * Replaces: modifiers/gptq/gptq_quantize.py:22-32 (_hessian_update) as
+ * called by accumulate_hessian (:63-97); the reference's 2/n scaling is
+ * alpha = 2 here plus the division by num_samples in mi355q_gptq_hinv.
+ * Requirements: d % 8 == 0, ldx % 8 == 0, x 16-byte aligned.
+ */
+size_t mi355q_hessian_workspace_size(int64_t n_tokens, int64_t d);
+int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
+                             float* h_dev, int64_t ldh, float alpha,
+                             void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/* Grouped (MoE) variant: expert e accumulates the rows
+ * x[rows_dev[k]] for k in [offsets_host[e], offsets_host[e+1]) into
+ * h_dev + e * h_stride (each d x d, leading dimension d, upper triangle).
+ * Replaces the per-expert accumulate_hessian calls that
+ * modeling/moe/linear_experts.py:244-277 triggers with routed tokens.
+ */
+size_t mi355q_hessian_grouped_workspace_size(const int64_t* offsets_host, int n_experts, int64_t d);
+int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, int64_t d,
+                                     const int32_t* rows_dev, const int64_t* offsets_host,
+                                     int n_experts, float* h_dev, int64_t h_stride, float alpha,
+                                     void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/* Mirror the upper triangle into the lower one (full symmetric matrix). */
+int mi355q_symmetrize_upper(float* h_dev, int64_t d, int64_t ldh, void* stream);
+
+/* ------------------------------------------------------------------ GPTQ
+ * mi355q_gptq_hinv: from the accumulated upper-triangle Hessian (optionally
+ * permuted by perm_dev, may be NULL), computes
+ *   H' = H * inv_num_samples (modifiers/gptq/base.py:594),
+ *   dead columns: diag(H') == 0 -> H'_ii = 1, dead_dev[i] = 1
+ *     (modifiers/gptq/gptq_quantize.py:35-38),
+ *   H' += percdamp * mean(diag(H')) * I  (:182-184),
+ *   hinv = upper Cholesky factor of inverse(H') (:185-188)
+ * using H' = R R^T with R upper (reverse-order Cholesky) and hinv = R^-1.
+ * On a non-positive-definite H' the kernels set *status_dev = 3 and hinv
+ * holds no meaningful values; the caller then uses the identity (RTN
+ * fallback, :189-196).  *status_dev is written with 0 first.
+ */
+size_t mi355q_gptq_hinv_workspace_size(int64_t d);
+int mi355q_gptq_hinv(const float* h_dev, int64_t ldh, int64_t d, const int32_t* perm_dev,
+                     float inv_num_samples, float percdamp, float* hinv_dev,
+                     int32_t* dead_dev, int32_t* status_dev, void* workspace_dev,
+                     size_t workspace_bytes, void* stream);
+
+/* mi355q_gptq_load_weight: w_work[r][j] = dead[j] ? 0 : float(w[r][perm[j]])
+ * (fp32 working copy, :121,126,142,178).  perm_dev / dead_dev may be NULL. */
+int mi355q_gptq_load_weight(const void* w_dev, mi355q_dtype w_dtype, int64_t rows, int64_t cols,
+                            int64_t ldw, const int32_t* perm_dev, const int32_t* dead_dev,
+                            float* w_work_dev, void* stream);
+
+/* mi355q_gptq_sweep: the blocked column sweep of :199-277 over the fp32
+ * working copy, in place.  Column j is quantised with
+ *   scale = scale_dev[r * ld_scale + sidx(r, j)], zp likewise,
+ * where sidx is 0 (TENSOR, ld_scale ignored -> scale_dev[0]), 0 (CHANNEL),
+ * g_idx_dev[j] (GROUP) or (BLOCK) (r / block_h) rows and g_idx_dev[j] cols.
+ *   q = clamp(rint(w / scale + zp), qmin, qmax)          (CT quantize)
+ *   w_q = (q - zp) * scale, rounded to bf16 if dequant_bf16 (CT dequantize
+ *         in the bf16 scale dtype)
+ *   err = (w - w_q) / hinv[j][j];  losses[r] += (w - w_q)^2 / hinv[j][j]^2 / 2
+ *   w[:, j+1:block_end] -= err * hinv[j, j+1:block_end]   (mul, then sub)
+ *   after each block: w[:, block_end:] -= Err_block @ hinv[block, block_end:]
+ * On return w_work holds the dequantised values, codes_dev[r][j] the integer
+ * codes q (int8, working column order) and losses_dev[r] the per-row loss
+ * (fp32, accumulated onto its input).  Integer types only (num_bits <= 8).
+ */
+size_t mi355q_gptq_sweep_workspace_size(int64_t rows, int64_t cols, int64_t blocksize);
+int mi355q_gptq_sweep(float* w_work_dev, int64_t rows, int64_t cols, const float* hinv_dev,
+                      const float* scale_dev, const float* zp_dev, int64_t ld_scale,
+                      const int32_t* g_idx_dev, int strategy, int block_h, float qmin, float qmax,
+                      int dequant_bf16, int64_t blocksize, int8_t* codes_dev, float* losses_dev,
+                      void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/* mi355q_gptq_store_weight: w_out[r][j] = w_work[r][invperm[j]] converted
+ * to out_dtype (:279-284); codes are permuted the same way when
+ * codes_in/codes_out are non-NULL.  invperm_dev may be NULL. */
+int mi355q_gptq_store_weight(const float* w_work_dev, int64_t rows, int64_t cols,
+                             const int32_t* invperm_dev, void* w_out_dev, mi355q_dtype out_dtype,
+                             int64_t ld_out, const int8_t* codes_in_dev, int8_t* codes_out_dev,
+                             void* stream);
+
+/* ------------------------------------------------------------------ observers
+ * Min/max statistics per strategy (observers/min_max.py:106-110 over
+ * observers/helpers.py:63-101 flattening).  Outputs are fp32 holding the
+ * exact input-dtype values: TENSOR -> 1, CHANNEL -> rows, GROUP ->
+ * rows * ceil(cols / group), BLOCK -> ceil(rows/bh) * ceil(cols/bw)
+ * (zero padding included, as the reference pads), TOKEN -> rows.
+ */
+int mi355q_observe_minmax(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
+                          int64_t ldx, int strategy, int64_t group_size, int block_h, int block_w,
+                          float* min_dev, float* max_dev, void* stream);
+
+/* CT calculate_qparams (observers/base.py:99-123 -> CT) over the quantized
+ * range [qmin, qmax] ((-2^(b-1), 2^(b-1)-1) for int, (-448, 448) for fp8):
+ * symmetric scale = absmax / ((qmax - qmin) / 2), asymmetric scale =
+ * (max - min) / (qmax - qmin) with zp = rint(clamp(qmin - min / scale)),
+ * min/max first widened to include 0; every step is rounded to scale_dtype
+ * (bf16 = the weight dtype for a bf16 weight); zero scales become the
+ * dtype's epsilon.  strict != 0 selects observers/min_max.py:33-55 (fp32
+ * absmax / qmax clamped at 1e-8).  scale_out is fp32 holding scale_dtype
+ * values; zp_out is fp32 integers. */
+int mi355q_calculate_qparams(const float* min_dev, const float* max_dev, int64_t n, float qmin,
+                             float qmax, int symmetric, int strict, mi355q_dtype scale_dtype,
+                             float* scale_out_dev, float* zp_out_dev, void* stream);
+
+/* MX shared scales from observer statistics: e8m0 byte per group (rule as
+ * in mi355q_mxfp4_quantize_pack, absmax = max(|min|, |max|) of bf16
+ * values) and the scale 2^(e-127) as fp32.  Either output may be NULL. */
+int mi355q_mx_scales(const float* min_dev, const float* max_dev, int64_t n, int rule,
+                     uint8_t* e8m0_out_dev, float* scale_out_dev, void* stream);
+
+/* ------------------------------------------------------------------ quantize / pack
+ * Integer quantize of a whole weight with the scale indexing of
+ * mi355q_gptq_sweep (g_idx may be NULL: column / group_size):
+ *   codes = clamp(rint(x / scale + zp), qmin, qmax), division in
+ *   div_dtype (bf16 rounds the quotient, as CT does for a bf16 weight with
+ *   a bf16 scale).  Replaces CT quantize inside the compressors called at
+ *   transformers/compression/compressed_tensors_utils.py:172-191.
+ */
+int mi355q_quantize_int(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
+                        int64_t ldx, const float* scale_dev, const float* zp_dev,
+                        int64_t ld_scale, const int32_t* g_idx_dev, int strategy,
+                        int64_t group_size, int block_h, int block_w, int num_bits,
+                        mi355q_dtype div_dtype, int8_t* codes_dev, void* stream);
+
+/* CT pack_quantized (pack_to_int32): 4-bit codes -> int32 words, eight per
+ * word, element k of a word at bits 4k, stored offset-binary (q + 8).
+ * cols % 8 == 0.  out is [rows, cols/8]. */
+int mi355q_pack_int4_int32(const int8_t* codes_dev, int64_t rows, int64_t cols,
+                           int32_t* out_dev, void* stream);
+
+/* utils/pack_int4_to_int8.py:13-28: out[r][k] = (c[r][2k+1] & 15) << 4 |
+ * (c[r][2k] & 15).  cols must be even. */
+int mi355q_pack_int4_int8(const int8_t* codes_dev, int64_t rows, int64_t cols,
+                          int8_t* out_dev, void* stream);
+
+/* MXFP4 (W4A4 / MXFP4 preset): per row, groups of 32 along columns share
+ * an e8m0 exponent e (scale 2^(e-127)); elements are rounded to e2m1
+ * (ties to even, saturating at 6, negative values rounding to zero keep the
+ * sign bit), code = sign<<3 | index in {0,.5,1,1.5,2,3,4,6}; two codes per
+ * byte, even column in the low nibble.  codes [rows, cols/2] uint8, scales
+ * [rows, cols/32] uint8.  cols % 32 == 0.  Rule MI355Q_MX_RULE_CT follows
+ * CT's generate_mx_scales (bf16 absmax rounded up to a power of two at
+ * 1.75, exponent - 2); MI355Q_MX_RULE_OCP is OCP MX v1.0 floor(log2)-2.
+ * Replaces the observer + CT mxfp4_pack_quantized path
+ * (modifiers/quantization/calibration.py:86-157 and the compressor call at
+ * compressed_tensors_utils.py:191). */
+int mi355q_mxfp4_quantize_pack(const void* x_dev, int64_t rows, int64_t cols, int64_t ldx,
+                               int rule, uint8_t* codes_dev, uint8_t* scales_dev, void* stream);
+int mi355q_mxfp4_dequantize(const uint8_t* codes_dev, const uint8_t* scales_dev, int64_t rows,
+                            int64_t cols, void* out_dev, void* stream);
+
+/* fp8 e4m3 (float8_e4m3fn) quantize: q = fp8_rne(clamp(x / scale, -448,
+ * 448)) with the scale indexing of mi355q_quantize_int; division in
+ * div_dtype.  Output bytes are e4m3fn bit patterns. */
+int mi355q_quantize_fp8(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
+                        int64_t ldx, const float* scale_dev, int64_t ld_scale, int strategy,
+                        int64_t group_size, mi355q_dtype div_dtype, uint8_t* out_dev,
+                        void* stream);
+
+/* Dynamic per-token int8 (W8A8 activations, CT TOKEN strategy): per row
+ * scale = bf16(absmax / 127.5) (epsilon if zero), codes = clamp(rint(bf16(x
+ * / scale)), -128, 127).  scale_out is bf16 bits [rows]. */
+int mi355q_quantize_int8_per_token(const void* x_dev, int64_t rows, int64_t cols, int64_t ldx,
+                                   int8_t* codes_dev, uint16_t* scale_out_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355Q_H */

@@ -1,0 +1,471 @@
+// Hessian accumulation H += alpha * X^T X (upper triangle) on gfx950.
+//
+// Replaces modifiers/gptq/gptq_quantize.py:22-32 (fp32 GEMM over the full
+// d x d matrix) with a syrk that computes and writes only the tiles on or
+// above the diagonal.  X rows are tokens (bf16, feature-contiguous); the
+// contraction runs over tokens, so both MFMA operands need token-contiguous
+// fragments: each thread loads an 8-token x 8-feature block with eight
+// 16-byte loads and transposes it in registers (v_perm) before the LDS
+// store.  bf16 x bf16 products are exact in fp32 and accumulate in fp32.
+//
+// Work decomposition: a work item is (matrix e, upper tile t, token split s).
+// Token splits are assigned by blockIdx % S, and workgroups are dispatched
+// round-robin over the 8 XCDs, so with S = 8 each XCD streams only its own
+// eighth of X through its L2.  With S > 1 each item writes its 128x128
+// partial (in MFMA fragment order) to the workspace and a second kernel sums
+// the partials in split order and updates H, so results are deterministic.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <vector>
+
+#include "common.h"
+
+namespace mi355q {
+
+namespace {
+
+constexpr int BM = 128;          // tile edge (features)
+constexpr int BK = 64;           // tokens per LDS stage
+constexpr int NT = 256;          // threads per workgroup (4 waves, 2x2)
+constexpr int LDS_ROW = BK + 8;  // bf16 elements per feature row, +16 B pad
+constexpr int TILE_FLOATS = BM * BM;
+
+struct Matrix {            // one Hessian being accumulated
+  int64_t row_begin;       // first index into rows[] (or first token)
+  int64_t row_count;       // tokens for this matrix
+  float* h;                // d x d, leading dimension ldh
+};
+
+struct Item {              // grouped work item
+  int e, t, s, S;
+  int64_t slot;            // partial slot (>= 0 when S > 1)
+};
+
+struct SyrkParams {
+  const uint16_t* x;
+  int64_t ldx;
+  int64_t d;
+  int64_t ldh;
+  int nt;                  // tiles per edge
+  float alpha;
+  const int32_t* rows;     // optional token -> row indirection
+  // single-matrix mode
+  Matrix single;
+  int S;
+  // grouped mode (items != nullptr)
+  const Item* items;
+  const Matrix* mats;
+  float* ws;               // partial tiles
+};
+
+__device__ __forceinline__ void tile_coords(int t, int nt, int& ti, int& tj) {
+  int r = 0;
+  int rowlen = nt;
+  while (t >= rowlen) {
+    t -= rowlen;
+    ++r;
+    --rowlen;
+  }
+  ti = r;
+  tj = r + t;
+}
+
+__device__ __forceinline__ unsigned perm_lo(unsigned a, unsigned b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);  // lo16(a) | lo16(b) << 16
+}
+__device__ __forceinline__ unsigned perm_hi(unsigned a, unsigned b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);  // hi16(a) | hi16(b) << 16
+}
+
+// Load one 8 (tokens) x 8 (features) block into r[8] (4 dwords each).
+__device__ __forceinline__ void load_block(const SyrkParams& p, int64_t tok0, int64_t tok_end,
+                                           int64_t row_base, int64_t f, u32x4_t r[8]) {
+#pragma unroll
+  for (int tt = 0; tt < 8; ++tt) {
+    int64_t k = tok0 + tt;
+    if (k < tok_end && f < p.d) {
+      int64_t row = p.rows ? (int64_t)p.rows[row_base + k] : (row_base + k);
+      r[tt] = *reinterpret_cast<const u32x4_t*>(p.x + row * p.ldx + f);
+    } else {
+      r[tt] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+// Transpose r (token-major) and store 8 feature rows of 8 tokens to LDS.
+__device__ __forceinline__ void store_block(uint16_t* lds, int fb, int kb, const u32x4_t r[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {     // feature pair (2j, 2j+1)
+    u32x4_t lo, hi;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {   // token pair (2q, 2q+1)
+      lo[q] = perm_lo(r[2 * q][j], r[2 * q + 1][j]);
+      hi[q] = perm_hi(r[2 * q][j], r[2 * q + 1][j]);
+    }
+    *reinterpret_cast<u32x4_t*>(lds + (8 * fb + 2 * j) * LDS_ROW + 8 * kb) = lo;
+    *reinterpret_cast<u32x4_t*>(lds + (8 * fb + 2 * j + 1) * LDS_ROW + 8 * kb) = hi;
+  }
+}
+
+__global__ __launch_bounds__(NT, 2) void syrk_bf16_kernel(SyrkParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][BM * LDS_ROW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int e = 0, t, s, S;
+  int64_t slot = -1;
+  Matrix mat;
+  if (p.items) {
+    Item it = p.items[blockIdx.x];
+    e = it.e; t = it.t; s = it.s; S = it.S; slot = it.slot;
+    mat = p.mats[e];
+  } else {
+    S = p.S;
+    s = blockIdx.x % S;
+    t = blockIdx.x / S;
+    mat = p.single;
+    slot = (S > 1) ? (int64_t)t * S + s : -1;
+  }
+  int ti, tj;
+  tile_coords(t, p.nt, ti, tj);
+
+  // token range of this split, rounded to whole stages
+  const int64_t n = mat.row_count;
+  const int64_t nst_total = (n + BK - 1) / BK;
+  const int64_t st_per = (nst_total + S - 1) / S;
+  const int64_t st_begin = (int64_t)s * st_per;
+  int64_t st_end = st_begin + st_per;
+  if (st_end > nst_total) st_end = nst_total;
+  const int64_t nst = st_end > st_begin ? st_end - st_begin : 0;
+
+  // loader role
+  const int op = tid >> 7;          // 0: row-tile operand, 1: column-tile operand
+  const int u = tid & 127;
+  const int fb = u & 15, kb = u >> 4;
+  const int64_t fbase = (int64_t)(op ? tj : ti) * BM + 8 * fb;
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+  u32x4_t regs[8];
+  if (nst > 0) {
+    load_block(p, st_begin * BK + 8 * kb, n, mat.row_begin, fbase, regs);
+    store_block(lds[0][op], fb, kb, regs);
+  }
+  __syncthreads();
+
+  for (int64_t st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) load_block(p, (st_begin + st + 1) * BK + 8 * kb, n, mat.row_begin, fbase, regs);
+
+    const uint16_t* la = lds[buf][0];
+    const uint16_t* lb = lds[buf][1];
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int koff = kk * 16 + 8 * (lane >> 5);
+      bf16x8_t fa[2], fbv[2];
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm)
+        fa[bm] = *reinterpret_cast<const bf16x8_t*>(la + (wm * 64 + bm * 32 + (lane & 31)) * LDS_ROW + koff);
+#pragma unroll
+      for (int bn = 0; bn < 2; ++bn)
+        fbv[bn] = *reinterpret_cast<const bf16x8_t*>(lb + (wn * 64 + bn * 32 + (lane & 31)) * LDS_ROW + koff);
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+        for (int bn = 0; bn < 2; ++bn)
+          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm], fbv[bn], acc[bm][bn], 0, 0, 0);
+    }
+
+    if (st + 1 < nst) store_block(lds[buf ^ 1][op], fb, kb, regs);
+    __syncthreads();
+  }
+
+  if (slot >= 0) {
+    float* dst = p.ws + (slot * NT + tid) * 64;
+#pragma unroll
+    for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+      for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          f32x4_t v = {acc[bm][bn][4 * q], acc[bm][bn][4 * q + 1], acc[bm][bn][4 * q + 2],
+                       acc[bm][bn][4 * q + 3]};
+          *reinterpret_cast<f32x4_t*>(dst + (bm * 2 + bn) * 16 + 4 * q) = v;
+        }
+    return;
+  }
+
+  // direct update of the upper triangle
+  const int64_t gi0 = (int64_t)ti * BM, gj0 = (int64_t)tj * BM;
+#pragma unroll
+  for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int nn = wn * 64 + bn * 32 + (lane & 31);
+        const int64_t gi = gi0 + m, gj = gj0 + nn;
+        if (gi < p.d && gj < p.d && gi <= gj) {
+          float* hp = mat.h + gi * p.ldh + gj;
+          *hp = *hp + p.alpha * acc[bm][bn][r];
+        }
+      }
+}
+
+struct ReduceItem {        // one tile to finish from S partial slots
+  int e, t, S;
+  int64_t slot0;           // slots slot0 .. slot0 + S - 1
+};
+
+__global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict__ ws,
+                                                         const ReduceItem* items, int single_S,
+                                                         Matrix single, const Matrix* mats,
+                                                         int64_t d, int64_t ldh, int nt, float alpha) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int t, S;
+  int64_t slot0;
+  Matrix mat;
+  if (items) {
+    ReduceItem it = items[blockIdx.x];
+    t = it.t; S = it.S; slot0 = it.slot0; mat = mats[it.e];
+  } else {
+    t = blockIdx.x; S = single_S; slot0 = (int64_t)t * S; mat = single;
+  }
+  int ti, tj;
+  tile_coords(t, nt, ti, tj);
+  float sum[64];
+#pragma unroll
+  for (int r = 0; r < 64; ++r) sum[r] = 0.f;
+  for (int s = 0; s < S; ++s) {
+    const float* src = ws + ((slot0 + s) * NT + tid) * 64;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      f32x4_t v = *reinterpret_cast<const f32x4_t*>(src + 4 * q);
+      sum[4 * q] += v[0];
+      sum[4 * q + 1] += v[1];
+      sum[4 * q + 2] += v[2];
+      sum[4 * q + 3] += v[3];
+    }
+  }
+  const int64_t gi0 = (int64_t)ti * BM, gj0 = (int64_t)tj * BM;
+#pragma unroll
+  for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int nn = wn * 64 + bn * 32 + (lane & 31);
+        const int64_t gi = gi0 + m, gj = gj0 + nn;
+        if (gi < d && gj < d && gi <= gj) {
+          float* hp = mat.h + gi * ldh + gj;
+          *hp = *hp + alpha * sum[(bm * 2 + bn) * 16 + r];
+        }
+      }
+}
+
+__global__ void symmetrize_kernel(float* h, int64_t d, int64_t ldh) {
+  __shared__ float tile[32][33];
+  const int bi = blockIdx.y, bj = blockIdx.x;  // source tile (bi <= bj) in the upper triangle
+  if (bi > bj) return;
+  const int tx = threadIdx.x, ty = threadIdx.y;  // 32 x 8
+  for (int k = ty; k < 32; k += 8) {
+    int64_t r = (int64_t)bi * 32 + k, c = (int64_t)bj * 32 + tx;
+    tile[k][tx] = (r < d && c < d) ? h[r * ldh + c] : 0.f;
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    int64_t r = (int64_t)bj * 32 + k, c = (int64_t)bi * 32 + tx;  // lower element (r, c) = upper (c, r)
+    if (r < d && c < d && r > c) h[r * ldh + c] = tile[tx][k];
+  }
+}
+
+int choose_splits(int64_t n) {
+  int64_t s = n / 2048;
+  if (s >= 8) return 8;
+  if (s >= 4) return 4;
+  if (s >= 2) return 2;
+  return 1;
+}
+
+inline int tiles_per_edge(int64_t d) { return (int)((d + BM - 1) / BM); }
+inline int upper_tiles(int nt) { return nt * (nt + 1) / 2; }
+
+}  // namespace
+
+}  // namespace mi355q
+
+using namespace mi355q;
+
+extern "C" size_t mi355q_hessian_workspace_size(int64_t n_tokens, int64_t d) {
+  if (n_tokens <= 0 || d <= 0) return 0;
+  const int S = choose_splits(n_tokens);
+  if (S == 1) return 0;
+  return (size_t)upper_tiles(tiles_per_edge(d)) * S * TILE_FLOATS * sizeof(float);
+}
+
+extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
+                                        float* h_dev, int64_t ldh, float alpha, void* workspace_dev,
+                                        size_t workspace_bytes, void* stream) {
+  MQ_CHECK_ARG(d > 0 && d % 8 == 0, "hessian: d must be a positive multiple of 8 (got %lld)", (long long)d);
+  MQ_CHECK_ARG(ldx >= d && ldx % 8 == 0, "hessian: ldx must be >= d and a multiple of 8");
+  MQ_CHECK_ARG(ldh >= d, "hessian: ldh must be >= d");
+  MQ_CHECK_ARG(n_tokens >= 0, "hessian: negative token count");
+  MQ_CHECK_ARG(h_dev != nullptr, "hessian: null H");
+  if (n_tokens == 0) return MI355Q_OK;
+  MQ_CHECK_ARG(x_dev != nullptr && aligned16(x_dev), "hessian: x must be non-null and 16-byte aligned");
+  const int nt = tiles_per_edge(d);
+  const int T = upper_tiles(nt);
+  const int S = choose_splits(n_tokens);
+  const size_t need = mi355q_hessian_workspace_size(n_tokens, d);
+  MQ_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace_dev != nullptr),
+               "hessian: workspace too small (%zu < %zu)", workspace_bytes, need);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+
+  SyrkParams p{};
+  p.x = static_cast<const uint16_t*>(x_dev);
+  p.ldx = ldx;
+  p.d = d;
+  p.ldh = ldh;
+  p.nt = nt;
+  p.alpha = alpha;
+  p.rows = nullptr;
+  p.single = Matrix{0, n_tokens, h_dev};
+  p.S = S;
+  p.items = nullptr;
+  p.mats = nullptr;
+  p.ws = static_cast<float*>(workspace_dev);
+  hipLaunchKernelGGL(syrk_bf16_kernel, dim3((unsigned)T * S), dim3(NT), 0, st, p);
+  MQ_LAUNCH_CHECK();
+  if (S > 1) {
+    hipLaunchKernelGGL(syrk_reduce_kernel, dim3((unsigned)T), dim3(NT), 0, st, p.ws,
+                       (const ReduceItem*)nullptr, S, p.single, (const Matrix*)nullptr, d, ldh, nt, alpha);
+    MQ_LAUNCH_CHECK();
+  }
+  return MI355Q_OK;
+}
+
+namespace {
+// Grouped workspace layout: [partials][items][reduce items][matrices]
+struct GroupedPlan {
+  std::vector<Item> items;
+  std::vector<ReduceItem> reduces;
+  std::vector<Matrix> mats;
+  int64_t slots = 0;
+  size_t off_items = 0, off_reduces = 0, off_mats = 0, total = 0;
+};
+
+GroupedPlan plan_grouped(const int64_t* offsets, int E, int64_t d, float* h, int64_t h_stride) {
+  GroupedPlan g;
+  const int nt = tiles_per_edge(d);
+  const int T = upper_tiles(nt);
+  for (int e = 0; e < E; ++e) {
+    int64_t n = offsets[e + 1] - offsets[e];
+    g.mats.push_back(Matrix{offsets[e], n, h ? h + (int64_t)e * h_stride : nullptr});
+    if (n <= 0) continue;
+    const int S = choose_splits(n);
+    for (int t = 0; t < T; ++t) {
+      int64_t slot0 = S > 1 ? g.slots : -1;
+      for (int s = 0; s < S; ++s) g.items.push_back(Item{e, t, s, S, S > 1 ? slot0 + s : -1});
+      if (S > 1) {
+        g.reduces.push_back(ReduceItem{e, t, S, slot0});
+        g.slots += S;
+      }
+    }
+  }
+  auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  size_t off = align((size_t)g.slots * TILE_FLOATS * sizeof(float));
+  g.off_items = off;
+  off = align(off + g.items.size() * sizeof(Item));
+  g.off_reduces = off;
+  off = align(off + g.reduces.size() * sizeof(ReduceItem));
+  g.off_mats = off;
+  off = align(off + g.mats.size() * sizeof(Matrix));
+  g.total = off;
+  return g;
+}
+}  // namespace
+
+extern "C" size_t mi355q_hessian_grouped_workspace_size(const int64_t* offsets_host, int n_experts,
+                                                        int64_t d) {
+  if (!offsets_host || n_experts <= 0 || d <= 0) return 0;
+  return plan_grouped(offsets_host, n_experts, d, nullptr, 0).total;
+}
+
+extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, int64_t d,
+                                                const int32_t* rows_dev, const int64_t* offsets_host,
+                                                int n_experts, float* h_dev, int64_t h_stride,
+                                                float alpha, void* workspace_dev,
+                                                size_t workspace_bytes, void* stream) {
+  MQ_CHECK_ARG(d > 0 && d % 8 == 0, "grouped hessian: d must be a positive multiple of 8");
+  MQ_CHECK_ARG(ldx >= d && ldx % 8 == 0, "grouped hessian: ldx must be >= d and a multiple of 8");
+  MQ_CHECK_ARG(n_experts > 0 && offsets_host != nullptr, "grouped hessian: bad expert table");
+  MQ_CHECK_ARG(h_dev != nullptr && h_stride >= d * d, "grouped hessian: bad H / stride");
+  for (int e = 0; e < n_experts; ++e)
+    MQ_CHECK_ARG(offsets_host[e + 1] >= offsets_host[e] && offsets_host[e] >= 0,
+                 "grouped hessian: offsets must be non-decreasing");
+  GroupedPlan g = plan_grouped(offsets_host, n_experts, d, h_dev, h_stride);
+  if (g.items.empty()) return MI355Q_OK;
+  MQ_CHECK_ARG(rows_dev != nullptr && x_dev != nullptr && aligned16(x_dev),
+               "grouped hessian: null or misaligned x / rows");
+  MQ_CHECK_ARG(workspace_dev != nullptr && workspace_bytes >= g.total,
+               "grouped hessian: workspace too small (%zu < %zu)", workspace_bytes, g.total);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace_dev);
+  MQ_CHECK_HIP(hipMemcpyAsync(ws + g.off_items, g.items.data(), g.items.size() * sizeof(Item),
+                              hipMemcpyHostToDevice, st));
+  if (!g.reduces.empty())
+    MQ_CHECK_HIP(hipMemcpyAsync(ws + g.off_reduces, g.reduces.data(),
+                                g.reduces.size() * sizeof(ReduceItem), hipMemcpyHostToDevice, st));
+  MQ_CHECK_HIP(hipMemcpyAsync(ws + g.off_mats, g.mats.data(), g.mats.size() * sizeof(Matrix),
+                              hipMemcpyHostToDevice, st));
+  // the host vectors die at return: wait for the copies (pageable memory
+  // is staged synchronously by HIP, but make the ordering explicit)
+  MQ_CHECK_HIP(hipStreamSynchronize(st));
+
+  const int nt = tiles_per_edge(d);
+  SyrkParams p{};
+  p.x = static_cast<const uint16_t*>(x_dev);
+  p.ldx = ldx;
+  p.d = d;
+  p.ldh = d;
+  p.nt = nt;
+  p.alpha = alpha;
+  p.rows = rows_dev;
+  p.S = 1;
+  p.items = reinterpret_cast<const Item*>(ws + g.off_items);
+  p.mats = reinterpret_cast<const Matrix*>(ws + g.off_mats);
+  p.ws = reinterpret_cast<float*>(ws);
+  hipLaunchKernelGGL(syrk_bf16_kernel, dim3((unsigned)g.items.size()), dim3(NT), 0, st, p);
+  MQ_LAUNCH_CHECK();
+  if (!g.reduces.empty()) {
+    hipLaunchKernelGGL(syrk_reduce_kernel, dim3((unsigned)g.reduces.size()), dim3(NT), 0, st,
+                       p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, Matrix{},
+                       p.mats, d, d, nt, alpha);
+    MQ_LAUNCH_CHECK();
+  }
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_symmetrize_upper(float* h_dev, int64_t d, int64_t ldh, void* stream) {
+  MQ_CHECK_ARG(h_dev != nullptr && d > 0 && ldh >= d, "symmetrize: bad arguments");
+  const unsigned nb = (unsigned)((d + 31) / 32);
+  hipLaunchKernelGGL(symmetrize_kernel, dim3(nb, nb), dim3(32, 8), 0,
+                     reinterpret_cast<hipStream_t>(stream), h_dev, d, ldh);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}

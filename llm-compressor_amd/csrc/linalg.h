@@ -1,0 +1,22 @@
+// fp32 MFMA GEMM used by the Cholesky chain and the GPTQ trailing update.
+#pragma once
+
+#include "common.h"
+
+namespace mi355q {
+
+struct GemmArgs {
+  const float* A;  // [M x K] row-major (lda)
+  const float* B;  // [K x N] row-major (ldb), or [N x K] when b_trans
+  float* C;        // [M x N] row-major (ldc)
+  int64_t lda, ldb, ldc;
+  int64_t strideA, strideB, strideC;  // batch strides (elements)
+  int64_t M, N, K;
+  float alpha, beta;  // C = beta * C + alpha * (A op(B)); beta == 0 never reads C
+  int lower_only;     // only C elements with row >= col (tiles fully above skipped)
+};
+
+// Launches the batched GEMM on `stream`; returns a status code.
+int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream);
+
+}  // namespace mi355q

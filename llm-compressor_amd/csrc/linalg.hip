@@ -1,0 +1,433 @@
+// fp32 linear algebra for the GPTQ solve on gfx950: MFMA GEMM, blocked
+// Cholesky and triangular inverse.
+//
+// The reference (modifiers/gptq/gptq_quantize.py:181-188) damps H, then runs
+// cholesky -> cholesky_inverse -> cholesky(upper) to obtain the upper
+// Cholesky factor U of H^-1.  With J the exchange matrix, F = J H J = L L^T
+// gives H = R R^T for the upper-triangular R = J L J, so H^-1 = R^-T R^-1
+// and U = R^-1 = J L^-1 J (the factor is unique for positive diagonals).
+// That is one potrf and one trtri (2 d^3 / 3 flops instead of 4 d^3 / 3),
+// with identical mathematics and fp32 rounding of the same order.
+//
+//   prepare:  F[a][b] = (H[p(d-1-a)][p(d-1-b)] / n), dead-column and
+//             damping rules on the diagonal (lower triangle of F only)
+//   potrf:    per 128-column panel: diagonal block Cholesky + its inverse
+//             (one workgroup, LDS resident), panel solve as a GEMM with the
+//             block inverse, trailing update as a lower-only MFMA GEMM
+//   trtri:    recursive doubling inv([[A,0],[B,C]]) = [[A^-1,0],[-C^-1 B A^-1, C^-1]]
+//             on top of the diagonal-block inverses, as batched GEMMs
+//   flip:     hinv[a][b] = X[d-1-a][d-1-b] for a <= b, 0 below
+#include "linalg.h"
+
+#pragma clang fp contract(off)
+
+namespace mi355q {
+namespace {
+
+// ---------------------------------------------------------------- GEMM
+constexpr int GBM = 128, GBN = 128, GBK = 32, GNT = 256;
+constexpr int LA = GBK + 1;     // LDS row stride for [m][k] tiles
+constexpr int LBN = GBN + 32;   // LDS row stride for [k][n] tiles
+
+template <bool BT>
+__global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
+  __shared__ float lds_a[2][GBM * LA];
+  __shared__ float lds_b[2][BT ? GBN * LA : GBK * LBN];
+
+  const int64_t m0 = (int64_t)blockIdx.y * GBM, n0 = (int64_t)blockIdx.x * GBN;
+  if (g.lower_only && m0 + GBM - 1 < n0) return;
+  const int bz = blockIdx.z;
+  const float* A = g.A + bz * g.strideA;
+  const float* B = g.B + bz * g.strideB;
+  float* C = g.C + bz * g.strideC;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+  f32x4_t ra[4], rb[4];
+  // A / B^T tiles: 128 rows x 32 k -> 1024 float4 (4 per thread)
+  auto load_mk = [&](const float* P, int64_t ld, int64_t rows_lim, int64_t r0, int64_t k0, f32x4_t* r) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int idx = v * GNT + tid;
+      const int row = idx >> 3, quad = idx & 7;
+      const int64_t gr = r0 + row, gk = k0 + 4 * quad;
+      f32x4_t x = {0.f, 0.f, 0.f, 0.f};
+      if (gr < rows_lim) {
+        const float* src = P + gr * ld + gk;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (gk + e < g.K) x[e] = src[e];
+      }
+      r[v] = x;
+    }
+  };
+  auto store_mk = [&](float* L, const f32x4_t* r) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int idx = v * GNT + tid;
+      const int row = idx >> 3, quad = idx & 7;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) L[row * LA + 4 * quad + e] = r[v][e];
+    }
+  };
+  // B tile (not transposed): 32 k x 128 n -> 1024 float4
+  auto load_kn = [&](int64_t k0, f32x4_t* r) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int idx = v * GNT + tid;
+      const int krow = idx >> 5, quad = idx & 31;
+      const int64_t gk = k0 + krow, gn = n0 + 4 * quad;
+      f32x4_t x = {0.f, 0.f, 0.f, 0.f};
+      if (gk < g.K) {
+        const float* src = B + gk * g.ldb + gn;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (gn + e < g.N) x[e] = src[e];
+      }
+      r[v] = x;
+    }
+  };
+  auto store_kn = [&](float* L, const f32x4_t* r) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int idx = v * GNT + tid;
+      const int krow = idx >> 5, quad = idx & 31;
+      *reinterpret_cast<f32x4_t*>(L + krow * LBN + 4 * quad) = r[v];
+    }
+  };
+
+  const int64_t nst = (g.K + GBK - 1) / GBK;
+  if (nst > 0) {
+    load_mk(A, g.lda, g.M, m0, 0, ra);
+    if (BT) load_mk(B, g.ldb, g.N, n0, 0, rb); else load_kn(0, rb);
+    store_mk(lds_a[0], ra);
+    if (BT) store_mk(lds_b[0], rb); else store_kn(lds_b[0], rb);
+  }
+  __syncthreads();
+  for (int64_t st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    const bool more = st + 1 < nst;
+    if (more) {
+      load_mk(A, g.lda, g.M, m0, (st + 1) * GBK, ra);
+      if (BT) load_mk(B, g.ldb, g.N, n0, (st + 1) * GBK, rb); else load_kn((st + 1) * GBK, rb);
+    }
+    const float* la = lds_a[buf];
+    const float* lb = lds_b[buf];
+#pragma unroll
+    for (int kk = 0; kk < GBK / 2; ++kk) {
+      const int k = 2 * kk + (lane >> 5);
+      float fa[2], fb[2];
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm) fa[bm] = la[(wm * 64 + bm * 32 + (lane & 31)) * LA + k];
+#pragma unroll
+      for (int bn = 0; bn < 2; ++bn) {
+        const int n = wn * 64 + bn * 32 + (lane & 31);
+        fb[bn] = BT ? lb[n * LA + k] : lb[k * LBN + n];
+      }
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+        for (int bn = 0; bn < 2; ++bn)
+          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[bm], fb[bn], acc[bm][bn], 0, 0, 0);
+    }
+    if (more) {
+      store_mk(lds_a[buf ^ 1], ra);
+      if (BT) store_mk(lds_b[buf ^ 1], rb); else store_kn(lds_b[buf ^ 1], rb);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gm = m0 + wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int64_t gn = n0 + wn * 64 + bn * 32 + (lane & 31);
+        if (gm < g.M && gn < g.N && (!g.lower_only || gm >= gn)) {
+          float* cp = C + gm * g.ldc + gn;
+          const float prod = g.alpha * acc[bm][bn][r];
+          *cp = g.beta == 0.f ? prod : g.beta * *cp + prod;
+        }
+      }
+}
+
+// ---------------------------------------------------------------- Cholesky pieces
+constexpr int NB = 128;        // panel width
+constexpr int PNT = 512;       // threads of the diagonal-block kernel
+constexpr int LP = NB + 1;     // LDS row stride
+
+// Lower Cholesky of the NB x NB diagonal block at (k0, k0) of F (in place,
+// lower triangle) and its inverse into linv (NB x NB, zeros above the
+// diagonal).  nb <= NB is the block size (smaller for the last block).
+__global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, int64_t k0, int nb,
+                                                        float* linv, int32_t* status) {
+  __shared__ float a[NB * LP];
+  __shared__ float x[NB * LP];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < NB * NB; e += PNT) {
+    const int i = e / NB, j = e % NB;
+    float v = 0.f;
+    if (i < nb && j <= i) v = F[(k0 + i) * ldf + (k0 + j)];
+    a[i * LP + j] = v;
+    x[i * LP + j] = (i == j) ? 1.f : 0.f;
+  }
+  __syncthreads();
+  bool bad = false;
+  for (int j = 0; j < nb; ++j) {
+    float piv = a[j * LP + j];
+    if (!(piv > 0.f) || !isfinite(piv)) {
+      bad = true;
+      piv = 1.f;
+    }
+    const float ljj = sqrtf(piv);
+    __syncthreads();
+    for (int i = j + 1 + tid; i < nb; i += PNT) a[i * LP + j] = a[i * LP + j] / ljj;
+    if (tid == 0) a[j * LP + j] = ljj;
+    __syncthreads();
+    // rank-1 update of the trailing lower triangle: rows i > j, cols j < c <= i
+    const int m = nb - 1 - j;
+    const int cnt = m * (m + 1) / 2;
+    for (int e = tid; e < cnt; e += PNT) {
+      // e -> (ii, cc) with 0 <= cc <= ii < m
+      int ii = (int)((sqrtf(8.f * e + 1.f) - 1.f) * 0.5f);
+      while ((ii + 1) * (ii + 2) / 2 <= e) ++ii;
+      while (ii * (ii + 1) / 2 > e) --ii;
+      const int cc = e - ii * (ii + 1) / 2;
+      const int i = j + 1 + ii, c = j + 1 + cc;
+      a[i * LP + c] = a[i * LP + c] - a[i * LP + j] * a[c * LP + j];
+    }
+    __syncthreads();  // updates of step j complete before step j+1 reads its pivot
+  }
+  if (bad && status && tid == 0) *status = MI355Q_NOT_POSITIVE_DEFINITE;
+  __syncthreads();
+  // inverse: X = L^-1 by row elimination of [L | I]
+  for (int j = 0; j < nb; ++j) {
+    const float ljj = a[j * LP + j];
+    for (int c = tid; c <= j; c += PNT) x[j * LP + c] = x[j * LP + c] / ljj;
+    __syncthreads();
+    const int rows = nb - 1 - j, colsn = j + 1;
+    for (int e = tid; e < rows * colsn; e += PNT) {
+      const int i = j + 1 + e / colsn, c = e % colsn;
+      x[i * LP + c] = x[i * LP + c] - a[i * LP + j] * x[j * LP + c];
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < NB * NB; e += PNT) {
+    const int i = e / NB, j = e % NB;
+    if (i < nb && j <= i) F[(k0 + i) * ldf + (k0 + j)] = a[i * LP + j];
+    linv[i * NB + j] = (i < nb && j <= i) ? x[i * LP + j] : 0.f;
+  }
+}
+
+// diag'[j] = H[p(j)][p(j)] / n with 0 -> 1 (dead), damp = percdamp * mean(diag')
+__global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t ldh, int64_t d,
+                                                         const int32_t* perm, float num_samples,
+                                                         float percdamp, int32_t* dead, float* damp_out,
+                                                         int32_t* status) {
+  __shared__ float part[1024 / 64];
+  float s = 0.f;
+  for (int64_t j = threadIdx.x; j < d; j += 1024) {
+    const int64_t pj = perm ? perm[j] : j;
+    float v = H[pj * ldh + pj] / num_samples;
+    const bool dd = v == 0.f;
+    if (dead) dead[j] = dd ? 1 : 0;
+    s += dd ? 1.f : v;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int w = 0; w < 1024 / 64; ++w) t += part[w];
+    damp_out[0] = percdamp * (t / (float)d);
+    if (status) *status = 0;
+  }
+}
+
+// F (lower) = flip(permute(H / n)) with dead / damping rules on the diagonal.
+__global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t d, const int32_t* perm,
+                                    float num_samples, const float* damp, float* F) {
+  const int64_t a = (int64_t)blockIdx.y * 16 + threadIdx.y;
+  const int64_t b = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (a >= d || b > a) return;
+  const int64_t ia = d - 1 - a, ib = d - 1 - b;
+  const int64_t pa = perm ? perm[ia] : ia, pb = perm ? perm[ib] : ib;
+  const int64_t r = pa < pb ? pa : pb, c = pa < pb ? pb : pa;
+  float v = H[r * ldh + c] / num_samples;
+  if (a == b) {
+    if (v == 0.f) v = 1.f;
+    v = v + damp[0];
+  }
+  F[a * d + b] = v;
+}
+
+// hinv[a][b] = X[d-1-a][d-1-b] (a <= b), zero below the diagonal.
+__global__ void flip_out_kernel(const float* X, int64_t d, float* hinv) {
+  const int64_t a = (int64_t)blockIdx.y * 16 + threadIdx.y;
+  const int64_t b = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (a >= d || b >= d) return;
+  hinv[a * d + b] = (a <= b) ? X[(d - 1 - a) * d + (d - 1 - b)] : 0.f;
+}
+
+__global__ void fill_kernel(float* p, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+// Place diagonal-block inverses into X.
+__global__ void place_diag_inv_kernel(const float* linv, int64_t d, float* X) {
+  const int blk = blockIdx.x;
+  const int64_t k0 = (int64_t)blk * NB;
+  for (int e = threadIdx.x; e < NB * NB; e += blockDim.x) {
+    const int i = e / NB, j = e % NB;
+    if (k0 + i < d && k0 + j < d) X[(k0 + i) * d + (k0 + j)] = linv[(int64_t)blk * NB * NB + e];
+  }
+}
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct HinvLayout {
+  size_t F, X, T, linv, damp, total;
+};
+
+HinvLayout hinv_layout(int64_t d) {
+  HinvLayout L{};
+  size_t off = 0;
+  const int64_t nblk = (d + NB - 1) / NB;
+  L.F = off; off = align256(off + (size_t)d * d * sizeof(float));
+  L.X = off; off = align256(off + (size_t)d * d * sizeof(float));
+  L.T = off; off = align256(off + (size_t)(d * ((d + 1) / 2 + NB)) * sizeof(float));
+  L.linv = off; off = align256(off + (size_t)nblk * NB * NB * sizeof(float));
+  L.damp = off; off = align256(off + 64);
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
+  if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
+  dim3 grid((unsigned)((g.N + GBN - 1) / GBN), (unsigned)((g.M + GBM - 1) / GBM), (unsigned)batch);
+  if (b_trans)
+    hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(GNT), 0, stream, g);
+  else
+    hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(GNT), 0, stream, g);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+}  // namespace mi355q
+
+using namespace mi355q;
+
+extern "C" size_t mi355q_gptq_hinv_workspace_size(int64_t d) { return d > 0 ? hinv_layout(d).total : 0; }
+
+extern "C" int mi355q_gptq_hinv(const float* h_dev, int64_t ldh, int64_t d, const int32_t* perm_dev,
+                                float num_samples, float percdamp, float* hinv_dev, int32_t* dead_dev,
+                                int32_t* status_dev, void* workspace_dev, size_t workspace_bytes,
+                                void* stream) {
+  MQ_CHECK_ARG(h_dev && hinv_dev && status_dev, "gptq_hinv: null pointer");
+  MQ_CHECK_ARG(d > 0 && ldh >= d, "gptq_hinv: bad shape");
+  MQ_CHECK_ARG(num_samples > 0.f, "gptq_hinv: num_samples must be positive");
+  const HinvLayout L = hinv_layout(d);
+  MQ_CHECK_ARG(workspace_dev && workspace_bytes >= L.total, "gptq_hinv: workspace too small (%zu < %zu)",
+               workspace_bytes, L.total);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace_dev);
+  float* F = reinterpret_cast<float*>(ws + L.F);
+  float* X = reinterpret_cast<float*>(ws + L.X);
+  float* T = reinterpret_cast<float*>(ws + L.T);
+  float* linv = reinterpret_cast<float*>(ws + L.linv);
+  float* damp = reinterpret_cast<float*>(ws + L.damp);
+
+  hipLaunchKernelGGL(diag_damp_kernel, dim3(1), dim3(1024), 0, st, h_dev, ldh, d, perm_dev, num_samples,
+                     percdamp, dead_dev, damp, status_dev);
+  MQ_LAUNCH_CHECK();
+  dim3 fb(64, 16), fg((unsigned)((d + 63) / 64), (unsigned)((d + 15) / 16));
+  hipLaunchKernelGGL(prepare_flip_kernel, fg, fb, 0, st, h_dev, ldh, d, perm_dev, num_samples, damp, F);
+  MQ_LAUNCH_CHECK();
+
+  // blocked right-looking Cholesky on F (lower)
+  const int64_t nblk = (d + NB - 1) / NB;
+  for (int64_t kb = 0; kb < nblk; ++kb) {
+    const int64_t k0 = kb * NB;
+    const int nb = (int)((d - k0) < NB ? (d - k0) : NB);
+    hipLaunchKernelGGL(potf2_inv_kernel, dim3(1), dim3(PNT), 0, st, F, d, k0, nb, linv + kb * NB * NB,
+                       status_dev);
+    MQ_LAUNCH_CHECK();
+    const int64_t rest = d - k0 - nb;
+    if (rest <= 0) break;
+    // panel: F[k0+nb:, k0:k0+nb] = F[...] * linv^T (in place, one workgroup per row tile)
+    GemmArgs p{};
+    p.A = F + (k0 + nb) * d + k0; p.lda = d;
+    p.B = linv + kb * NB * NB; p.ldb = NB;
+    p.C = F + (k0 + nb) * d + k0; p.ldc = d;
+    p.M = rest; p.N = nb; p.K = nb; p.alpha = 1.f; p.beta = 0.f;
+    int rc = gemm_f32(p, true, 1, st);
+    if (rc) return rc;
+    // trailing: F[k0+nb:, k0+nb:] -= P P^T (lower)
+    GemmArgs s{};
+    s.A = F + (k0 + nb) * d + k0; s.lda = d;
+    s.B = F + (k0 + nb) * d + k0; s.ldb = d;
+    s.C = F + (k0 + nb) * d + (k0 + nb); s.ldc = d;
+    s.M = rest; s.N = rest; s.K = nb; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
+    rc = gemm_f32(s, true, 1, st);
+    if (rc) return rc;
+  }
+
+  // triangular inverse X = L^-1 by recursive doubling over NB blocks; the
+  // doubling reads whole s x s blocks of X, so everything above the
+  // diagonal blocks must be zero
+  hipLaunchKernelGGL(fill_kernel, dim3(2048), dim3(256), 0, st, X, d * d, 0.f);
+  MQ_LAUNCH_CHECK();
+  hipLaunchKernelGGL(place_diag_inv_kernel, dim3((unsigned)nblk), dim3(256), 0, st, linv, d, X);
+  MQ_LAUNCH_CHECK();
+  for (int64_t s = NB; s < d; s *= 2) {
+    // pairs (a0 = p*2s, c0 = a0 + s); full pairs batched, ragged tail alone
+    const int64_t full = d / (2 * s);
+    const int64_t tail_c0 = full * 2 * s + s;
+    for (int pass = 0; pass < 2; ++pass) {
+      int64_t npairs, a0, s2;
+      if (pass == 0) {
+        npairs = full; a0 = 0; s2 = s;
+      } else {
+        if (tail_c0 >= d) break;
+        npairs = 1; a0 = full * 2 * s; s2 = d - tail_c0;
+      }
+      if (npairs == 0) continue;
+      const int64_t c0 = a0 + s;
+      const int64_t stride_diag = 2 * s * (d + 1);
+      // T = L[c0:c0+s2, a0:a0+s] * X[a0:a0+s, a0:a0+s]
+      GemmArgs t1{};
+      t1.A = F + c0 * d + a0; t1.lda = d; t1.strideA = stride_diag;
+      t1.B = X + a0 * d + a0; t1.ldb = d; t1.strideB = stride_diag;
+      t1.C = T; t1.ldc = s; t1.strideC = s2 * s;
+      t1.M = s2; t1.N = s; t1.K = s; t1.alpha = 1.f; t1.beta = 0.f;
+      int rc = gemm_f32(t1, false, (int)npairs, st);
+      if (rc) return rc;
+      // X[c0:c0+s2, a0:a0+s] = -X[c0:c0+s2, c0:c0+s2] * T
+      GemmArgs t2{};
+      t2.A = X + c0 * d + c0; t2.lda = d; t2.strideA = stride_diag;
+      t2.B = T; t2.ldb = s; t2.strideB = s2 * s;
+      t2.C = X + c0 * d + a0; t2.ldc = d; t2.strideC = stride_diag;
+      t2.M = s2; t2.N = s; t2.K = s2; t2.alpha = -1.f; t2.beta = 0.f;
+      rc = gemm_f32(t2, false, (int)npairs, st);
+      if (rc) return rc;
+    }
+  }
+  hipLaunchKernelGGL(flip_out_kernel, fg, fb, 0, st, X, d, hinv_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}

@@ -1,0 +1,600 @@
+// Observers, qparams, quantize and pack kernels (HBM-bound) for gfx950.
+//
+// Reference behaviour: observers/min_max.py:16-110 (min/max statistics),
+// observers/helpers.py:63-131 (per-strategy flattening),
+// modifiers/quantization/calibration.py:86-157 (observe / update_qparams),
+// utils/pack_int4_to_int8.py:13-28 (nibble pack) and the compressed-tensors
+// quantize / pack_to_int32 / MXFP4 / fp8 arithmetic those call.  Every
+// kernel reads its input once with 16-byte loads where the layout allows.
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+namespace mi355q {
+namespace {
+
+constexpr int NT = 256;
+
+// ---------------------------------------------------------------- helpers
+__device__ __forceinline__ float load_elem(const void* x, mi355q_dtype dt, int64_t i) {
+  return dt == MI355Q_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(x)[i])
+                           : static_cast<const float*>(x)[i];
+}
+
+// Total order on floats as signed ints, for atomic min/max.
+__device__ __forceinline__ int f2ord(float f) {
+  int i = __float_as_int(f);
+  return i >= 0 ? i : i ^ 0x7fffffff;
+}
+__device__ __forceinline__ float ord2f(int i) { return __int_as_float(i >= 0 ? i : i ^ 0x7fffffff); }
+
+__device__ __forceinline__ float warp_min(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Scale index for element (r, c) under a strategy.
+__device__ __forceinline__ int64_t scale_index(int strategy, int64_t r, int64_t c, int64_t ld_scale,
+                                               const int32_t* g_idx, int64_t group_size, int bh,
+                                               int bw) {
+  switch (strategy) {
+    case MI355Q_TENSOR: return 0;
+    case MI355Q_CHANNEL:
+    case MI355Q_TOKEN: return r * ld_scale;
+    case MI355Q_GROUP: return r * ld_scale + (g_idx ? (int64_t)g_idx[c] : c / group_size);
+    case MI355Q_BLOCK: return (r / bh) * ld_scale + (g_idx ? (int64_t)g_idx[c] : c / bw);
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------- min / max
+// One workgroup per row (CHANNEL / TOKEN) or the whole tensor (TENSOR, via
+// ordered-int atomics on pre-initialised outputs).
+__global__ void minmax_rows_kernel(const void* x, mi355q_dtype dt, int64_t rows, int64_t cols,
+                                   int64_t ldx, float* mn_out, float* mx_out, int tensor_mode) {
+  __shared__ float smn[NT / 64], smx[NT / 64];
+  const int64_t r = blockIdx.x;
+  if (r >= rows) return;
+  float mn = INFINITY, mx = -INFINITY;
+  const int64_t base = r * ldx;
+  const bool vec = dt == MI355Q_BF16 && (cols % 8 == 0) && (ldx % 8 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  if (vec) {
+    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + base);
+    for (int64_t c = threadIdx.x; c < cols / 8; c += NT) {
+      u32x4_t v = p[c];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float a = __uint_as_float(v[q] << 16), b = __uint_as_float(v[q] & 0xffff0000u);
+        mn = fminf(mn, fminf(a, b));
+        mx = fmaxf(mx, fmaxf(a, b));
+      }
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < cols; c += NT) {
+      float v = load_elem(x, dt, base + c);
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
+  }
+  mn = warp_min(mn);
+  mx = warp_max(mx);
+  if ((threadIdx.x & 63) == 0) {
+    smn[threadIdx.x >> 6] = mn;
+    smx[threadIdx.x >> 6] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < NT / 64; ++w) {
+      mn = fminf(mn, smn[w]);
+      mx = fmaxf(mx, smx[w]);
+    }
+    if (tensor_mode) {
+      atomicMin(reinterpret_cast<int*>(mn_out), f2ord(mn));
+      atomicMax(reinterpret_cast<int*>(mx_out), f2ord(mx));
+    } else {
+      mn_out[r] = mn;
+      mx_out[r] = mx;
+    }
+  }
+}
+
+__global__ void minmax_init_kernel(float* mn, float* mx) {
+  reinterpret_cast<int*>(mn)[0] = f2ord(INFINITY);
+  reinterpret_cast<int*>(mx)[0] = f2ord(-INFINITY);
+}
+__global__ void minmax_finish_kernel(float* mn, float* mx) {
+  mn[0] = ord2f(reinterpret_cast<int*>(mn)[0]);
+  mx[0] = ord2f(reinterpret_cast<int*>(mx)[0]);
+}
+
+// Groups along columns, vector path: LPG lanes x 8 elements per group.
+template <int LPG>
+__global__ void minmax_group_vec_kernel(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                                        float* mn_out, float* mx_out) {
+  const int64_t chunks_per_row = cols / 8;
+  const int64_t total = rows * chunks_per_row;
+  const int64_t ngroups = cols / (8 * LPG);
+  for (int64_t c = (int64_t)blockIdx.x * NT + threadIdx.x; c - (threadIdx.x & (LPG - 1)) < total;
+       c += (int64_t)gridDim.x * NT) {
+    float mn = INFINITY, mx = -INFINITY;
+    if (c < total) {
+      const int64_t r = c / chunks_per_row, k = c % chunks_per_row;
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(x + r * ldx + 8 * k);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float a = __uint_as_float(v[q] << 16), b = __uint_as_float(v[q] & 0xffff0000u);
+        mn = fminf(mn, fminf(a, b));
+        mx = fmaxf(mx, fmaxf(a, b));
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < LPG; o <<= 1) {
+      mn = fminf(mn, __shfl_xor(mn, o));
+      mx = fmaxf(mx, __shfl_xor(mx, o));
+    }
+    if (c < total && (threadIdx.x & (LPG - 1)) == 0) {
+      const int64_t r = c / chunks_per_row, k = c % chunks_per_row;
+      const int64_t g = k / LPG;
+      mn_out[r * ngroups + g] = mn;
+      mx_out[r * ngroups + g] = mx;
+    }
+  }
+}
+
+// Generic groups / blocks: one thread per output cell, zero padding counted.
+__global__ void minmax_cells_kernel(const void* x, mi355q_dtype dt, int64_t rows, int64_t cols,
+                                    int64_t ldx, int64_t cell_h, int64_t cell_w, int64_t ncr,
+                                    int64_t ncc, float* mn_out, float* mx_out) {
+  const int64_t cell = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (cell >= ncr * ncc) return;
+  const int64_t cr = cell / ncc, cc = cell % ncc;
+  float mn = INFINITY, mx = -INFINITY;
+  for (int64_t i = 0; i < cell_h; ++i) {
+    const int64_t r = cr * cell_h + i;
+    for (int64_t j = 0; j < cell_w; ++j) {
+      const int64_t c = cc * cell_w + j;
+      float v = (r < rows && c < cols) ? load_elem(x, dt, r * ldx + c) : 0.f;
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
+  }
+  mn_out[cell] = mn;
+  mx_out[cell] = mx;
+}
+
+// ---------------------------------------------------------------- qparams
+__device__ __forceinline__ float rnd(float v, bool bf16) { return bf16 ? round_to_bf16(v) : v; }
+
+__global__ void qparams_kernel(const float* mn_in, const float* mx_in, int64_t n, float qmin, float qmax,
+                               int symmetric, int strict, int bf16_scale, float* scale_out,
+                               float* zp_out) {
+  const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (i >= n) return;
+  const bool b = bf16_scale != 0;
+  float mn = fminf(mn_in[i], 0.f), mx = fmaxf(mx_in[i], 0.f);
+  float scale, zp = 0.f;
+  if (strict) {
+    float mvp = fmaxf(fabsf(mn), fabsf(mx));
+    scale = fmaxf(mvp / qmax, 1e-8f);
+    scale = rnd(scale, b);
+  } else if (symmetric) {
+    float mvp = fmaxf(fabsf(mn), fabsf(mx));
+    scale = rnd(mvp / ((qmax - qmin) / 2.f), b);
+  } else {
+    scale = rnd(rnd(mx - mn, b) / (qmax - qmin), b);
+    zp = rnd(qmin - rnd(mn / scale, b), b);
+    zp = fminf(fmaxf(zp, qmin), qmax);
+    zp = rintf(zp);
+  }
+  if (!strict && scale == 0.f) scale = b ? 0.0078125f : 1.1920928955078125e-07f;
+  scale_out[i] = scale;
+  zp_out[i] = zp;
+}
+
+// ---------------------------------------------------------------- int quantize
+__global__ void quantize_int_kernel(const void* x, mi355q_dtype dt, int64_t rows, int64_t cols,
+                                    int64_t ldx, const float* scale, const float* zp,
+                                    int64_t ld_scale, const int32_t* g_idx, int strategy,
+                                    int64_t group_size, int bh, int bw, float qmin, float qmax,
+                                    int div_bf16, int8_t* out) {
+  const int64_t total = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < total; i += (int64_t)gridDim.x * NT) {
+    const int64_t r = i / cols, c = i % cols;
+    const int64_t si = scale_index(strategy, r, c, ld_scale, g_idx, group_size, bh, bw);
+    float v = load_elem(x, dt, r * ldx + c);
+    float q = v / scale[si];
+    if (div_bf16) q = round_to_bf16(q);
+    if (zp) {
+      q = q + zp[si];
+      if (div_bf16) q = round_to_bf16(q);
+    }
+    q = fminf(fmaxf(q, qmin), qmax);
+    out[r * cols + c] = (int8_t)rintf(q);
+  }
+}
+
+// ---------------------------------------------------------------- packs
+__global__ void pack_int4_int32_kernel(const int8_t* codes, int64_t rows, int64_t cols,
+                                       int32_t* out) {
+  const int64_t words = rows * (cols / 8);
+  for (int64_t w = (int64_t)blockIdx.x * NT + threadIdx.x; w < words; w += (int64_t)gridDim.x * NT) {
+    const int64_t r = w / (cols / 8), k = w % (cols / 8);
+    const uint2 raw = *reinterpret_cast<const uint2*>(codes + r * cols + 8 * k);
+    uint32_t acc = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t byte = ((e < 4 ? raw.x : raw.y) >> (8 * (e & 3))) & 0xffu;
+      acc |= ((byte + 8u) & 0xfu) << (4 * e);
+    }
+    out[w] = (int32_t)acc;
+  }
+}
+
+__global__ void pack_int4_int8_kernel(const int8_t* codes, int64_t rows, int64_t cols, int8_t* out) {
+  const int64_t n = rows * (cols / 2);
+  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
+    const int64_t r = i / (cols / 2), k = i % (cols / 2);
+    const int lo = codes[r * cols + 2 * k] & 0x0f, hi = codes[r * cols + 2 * k + 1] & 0x0f;
+    out[i] = (int8_t)((hi << 4) | lo);
+  }
+}
+
+// ---------------------------------------------------------------- MXFP4
+__device__ __forceinline__ int mx_exponent(float amax, int rule) {
+  // amax is a bf16 value (exact in fp32), >= 0
+  if (amax == 0.f) return 0;
+  int e;
+  if (rule == MI355Q_MX_RULE_CT) {
+    uint32_t bits = (__float_as_uint(amax) >> 16) & 0xffffu;
+    bits = (bits + 32u) & 0xff80u;
+    e = (int)((bits >> 7) & 0xffu) - 127;
+  } else {
+    uint32_t u = __float_as_uint(amax);
+    int ef = (int)((u >> 23) & 0xffu);
+    if (ef == 0) {  // fp32 subnormal (not reachable from bf16 normal data)
+      e = -127 - __clz(u & 0x7fffffu) + 9 - 1;
+    } else {
+      e = ef - 127;
+    }
+  }
+  int e8 = e + 127 - 2;
+  return e8 < 0 ? 0 : (e8 > 254 ? 254 : e8);
+}
+
+__device__ __forceinline__ float exp2i(int k) {  // 2^k for k in [-149, 127]
+  if (k >= -126) return __uint_as_float((uint32_t)(k + 127) << 23);
+  return __uint_as_float(1u << (k + 149));
+}
+
+// e2m1 code of v (already divided by the shared scale), CT cast_to_fp4
+// thresholds, sign bit set for strictly negative inputs.
+__device__ __forceinline__ uint32_t e2m1_code(float v) {
+  float a = fminf(fabsf(v), 6.f);
+  uint32_t idx = a <= 0.25f ? 0u : a < 0.75f ? 1u : a <= 1.25f ? 2u : a < 1.75f ? 3u
+               : a <= 2.5f ? 4u : a < 3.5f ? 5u : a <= 5.f ? 6u : 7u;
+  return idx | (v < 0.f ? 8u : 0u);
+}
+
+// Each lane handles 8 consecutive elements; 4 lanes form a 32-element group.
+__global__ __launch_bounds__(NT) void mxfp4_quantize_pack_kernel(const uint16_t* __restrict__ x,
+                                                                  int64_t rows, int64_t cols,
+                                                                  int64_t ldx, int rule,
+                                                                  uint32_t* __restrict__ codes,
+                                                                  uint8_t* __restrict__ scales) {
+  const int64_t cpr = cols / 8;  // chunks per row
+  const int64_t total = rows * cpr;
+  const int64_t stride = (int64_t)gridDim.x * NT;
+  for (int64_t c = (int64_t)blockIdx.x * NT + threadIdx.x; c - (threadIdx.x & 3) < total; c += stride) {
+    const bool live = c < total;
+    int64_t r = 0, k = 0;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (live) {
+      r = c / cpr;
+      k = c - r * cpr;
+      v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + r * ldx + 8 * k));
+    }
+    uint32_t am = 0;  // max |x| as bf16 bits (order-preserving for non-negative)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t lo = v[q] & 0x7fffu, hi = (v[q] >> 16) & 0x7fffu;
+      am = max(am, max(lo, hi));
+    }
+    am = max(am, (uint32_t)__shfl_xor((int)am, 1));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 2));
+    if (!live) continue;
+    const int e8 = mx_exponent(__uint_as_float(am << 16), rule);
+    // e8 in [0, 254]: dividing by 2^(e8-127) is an exact multiply by 2^(127-e8)
+    const float inv = exp2i(127 - e8);
+    uint32_t word = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float a = __uint_as_float(v[q] << 16) * inv;
+      const float b = __uint_as_float(v[q] & 0xffff0000u) * inv;
+      word |= e2m1_code(a) << (8 * q);
+      word |= e2m1_code(b) << (8 * q + 4);
+    }
+    __builtin_nontemporal_store(word, codes + r * (cols / 8) + k);
+    if ((threadIdx.x & 3) == 0) scales[r * (cols / 32) + k / 4] = (uint8_t)e8;
+  }
+}
+
+__global__ void mx_scales_kernel(const float* mn, const float* mx, int64_t n, int rule, uint8_t* e8_out,
+                                 float* scale_out) {
+  const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (i >= n) return;
+  const float amax = round_to_bf16(fmaxf(fabsf(fminf(mn[i], 0.f)), fabsf(fmaxf(mx[i], 0.f))));
+  const int e8 = mx_exponent(amax, rule);
+  if (e8_out) e8_out[i] = (uint8_t)e8;
+  if (scale_out) scale_out[i] = exp2i(e8 - 127);
+}
+
+__global__ void mxfp4_dequant_kernel(const uint8_t* codes, const uint8_t* scales, int64_t rows,
+                                     int64_t cols, uint16_t* out) {
+  const int64_t n = rows * cols;
+  const float lut[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
+    const int64_t r = i / cols, c = i % cols;
+    const uint32_t byte = codes[r * (cols / 2) + c / 2];
+    const uint32_t code = (c & 1) ? (byte >> 4) : (byte & 15u);
+    const int e8 = scales[r * (cols / 32) + c / 32];
+    float v = lut[code & 7u];
+    if (code & 8u) v = -v;
+    float s = exp2i(e8 - 127 < -149 ? -149 : e8 - 127);
+    out[i] = f32_to_bf16_bits(v * s);
+  }
+}
+
+// ---------------------------------------------------------------- fp8 e4m3fn
+__device__ __forceinline__ uint8_t f32_to_e4m3fn(float v) {
+  const uint32_t sign = (__float_as_uint(v) >> 31) << 7;
+  float a = fabsf(v);  // caller clamps to <= 448
+  uint32_t out;
+  if (a >= 0.015625f) {  // normal range 2^-6 and up
+    uint32_t u = __float_as_uint(a);
+    u += 0x7ffffu + ((u >> 20) & 1u);  // RNE to 3 mantissa bits
+    const int e = (int)((u >> 23) & 0xffu) - 127 + 7;
+    out = ((uint32_t)e << 3) | ((u >> 20) & 7u);
+  } else {
+    out = (uint32_t)rintf(a * 512.f);  // subnormals m * 2^-9 (8 -> min normal)
+  }
+  return (uint8_t)(sign | out);
+}
+
+__global__ void quantize_fp8_kernel(const void* x, mi355q_dtype dt, int64_t rows, int64_t cols,
+                                    int64_t ldx, const float* scale, int64_t ld_scale, int strategy,
+                                    int64_t group_size, int div_bf16, uint8_t* out) {
+  const int64_t total = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < total; i += (int64_t)gridDim.x * NT) {
+    const int64_t r = i / cols, c = i % cols;
+    const int64_t si = scale_index(strategy, r, c, ld_scale, nullptr, group_size, 1, 1);
+    float q = load_elem(x, dt, r * ldx + c) / scale[si];
+    if (div_bf16) q = round_to_bf16(q);
+    q = fminf(fmaxf(q, -448.f), 448.f);
+    out[r * cols + c] = f32_to_e4m3fn(q);
+  }
+}
+
+// ---------------------------------------------------------------- per-token int8
+__global__ __launch_bounds__(NT) void int8_per_token_kernel(const uint16_t* x, int64_t rows,
+                                                            int64_t cols, int64_t ldx, int8_t* codes,
+                                                            uint16_t* scale_out) {
+  __shared__ float smx[NT / 64];
+  const int64_t r = blockIdx.x;
+  const uint16_t* row = x + r * ldx;
+  float mx = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += NT) mx = fmaxf(mx, fabsf(bf16_bits_to_f32(row[c])));
+  mx = warp_max(mx);
+  if ((threadIdx.x & 63) == 0) smx[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = smx[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) mx = fmaxf(mx, smx[w]);
+  float s = round_to_bf16(mx / 127.5f);
+  if (s == 0.f) s = 0.0078125f;
+  if (threadIdx.x == 0) scale_out[r] = f32_to_bf16_bits(s);
+  for (int64_t c = threadIdx.x; c < cols; c += NT) {
+    float q = round_to_bf16(bf16_bits_to_f32(row[c]) / s);
+    q = fminf(fmaxf(q, -128.f), 127.f);
+    codes[r * cols + c] = (int8_t)rintf(q);
+  }
+}
+
+inline unsigned grid_for(int64_t n, int64_t per_block = NT, unsigned cap = 65536u) {
+  int64_t g = (n + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  return (unsigned)(g > cap ? cap : g);
+}
+
+}  // namespace
+}  // namespace mi355q
+
+using namespace mi355q;
+
+extern "C" int mi355q_observe_minmax(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
+                                     int64_t ldx, int strategy, int64_t group_size, int block_h,
+                                     int block_w, float* min_dev, float* max_dev, void* stream) {
+  MQ_CHECK_ARG(x_dev && min_dev && max_dev, "observe_minmax: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "observe_minmax: bad shape");
+  MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F32, "observe_minmax: bad dtype");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (strategy) {
+    case MI355Q_TENSOR:
+      hipLaunchKernelGGL(minmax_init_kernel, dim3(1), dim3(1), 0, st, min_dev, max_dev);
+      hipLaunchKernelGGL(minmax_rows_kernel, dim3((unsigned)rows), dim3(NT), 0, st, x_dev, dtype, rows,
+                         cols, ldx, min_dev, max_dev, 1);
+      hipLaunchKernelGGL(minmax_finish_kernel, dim3(1), dim3(1), 0, st, min_dev, max_dev);
+      break;
+    case MI355Q_CHANNEL:
+    case MI355Q_TOKEN:
+      hipLaunchKernelGGL(minmax_rows_kernel, dim3((unsigned)rows), dim3(NT), 0, st, x_dev, dtype, rows,
+                         cols, ldx, min_dev, max_dev, 0);
+      break;
+    case MI355Q_GROUP: {
+      MQ_CHECK_ARG(group_size > 0, "observe_minmax: group_size must be > 0");
+      MQ_CHECK_ARG(cols % group_size == 0, "observe_minmax: columns (%lld) not divisible by group_size (%lld)",
+                   (long long)cols, (long long)group_size);
+      const bool vec = dtype == MI355Q_BF16 && ldx % 8 == 0 && aligned16(x_dev);
+      const int64_t lpg = group_size / 8;
+      const int64_t chunks = rows * (cols / 8);
+      const unsigned g = grid_for(chunks, NT, 1u << 20);
+      const uint16_t* xb = static_cast<const uint16_t*>(x_dev);
+      if (vec && group_size % 8 == 0 && lpg == 4)
+        hipLaunchKernelGGL(minmax_group_vec_kernel<4>, dim3(g), dim3(NT), 0, st, xb, rows, cols, ldx, min_dev, max_dev);
+      else if (vec && group_size % 8 == 0 && lpg == 8)
+        hipLaunchKernelGGL(minmax_group_vec_kernel<8>, dim3(g), dim3(NT), 0, st, xb, rows, cols, ldx, min_dev, max_dev);
+      else if (vec && group_size % 8 == 0 && lpg == 16)
+        hipLaunchKernelGGL(minmax_group_vec_kernel<16>, dim3(g), dim3(NT), 0, st, xb, rows, cols, ldx, min_dev, max_dev);
+      else if (vec && group_size % 8 == 0 && lpg == 2)
+        hipLaunchKernelGGL(minmax_group_vec_kernel<2>, dim3(g), dim3(NT), 0, st, xb, rows, cols, ldx, min_dev, max_dev);
+      else {
+        const int64_t ng = cols / group_size;
+        hipLaunchKernelGGL(minmax_cells_kernel, dim3(grid_for(rows * ng, NT, 1u << 30)), dim3(NT), 0, st,
+                           x_dev, dtype, rows, cols, ldx, (int64_t)1, group_size, rows, ng, min_dev, max_dev);
+      }
+      break;
+    }
+    case MI355Q_BLOCK: {
+      MQ_CHECK_ARG(block_h > 0 && block_w > 0, "observe_minmax: bad block structure");
+      const int64_t ncr = (rows + block_h - 1) / block_h, ncc = (cols + block_w - 1) / block_w;
+      hipLaunchKernelGGL(minmax_cells_kernel, dim3(grid_for(ncr * ncc, NT, 1u << 30)), dim3(NT), 0, st,
+                         x_dev, dtype, rows, cols, ldx, (int64_t)block_h, (int64_t)block_w, ncr, ncc,
+                         min_dev, max_dev);
+      break;
+    }
+    default:
+      set_error("observe_minmax: unknown strategy %d", strategy);
+      return MI355Q_INVALID_ARGUMENT;
+  }
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_calculate_qparams(const float* min_dev, const float* max_dev, int64_t n, float qmin,
+                                        float qmax, int symmetric, int strict, mi355q_dtype scale_dtype,
+                                        float* scale_out_dev, float* zp_out_dev, void* stream) {
+  MQ_CHECK_ARG(min_dev && max_dev && scale_out_dev && zp_out_dev, "calculate_qparams: null pointer");
+  MQ_CHECK_ARG(qmin < 0.f && qmax > 0.f, "calculate_qparams: range must straddle zero");
+  MQ_CHECK_ARG(!strict || symmetric, "calculate_qparams: strict requires symmetric");
+  if (n <= 0) return MI355Q_OK;
+  hipLaunchKernelGGL(qparams_kernel, dim3(grid_for(n, NT, 1u << 30)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), min_dev, max_dev, n, qmin, qmax, symmetric,
+                     strict, scale_dtype == MI355Q_BF16 ? 1 : 0, scale_out_dev, zp_out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_mx_scales(const float* min_dev, const float* max_dev, int64_t n, int rule,
+                                uint8_t* e8m0_out_dev, float* scale_out_dev, void* stream) {
+  MQ_CHECK_ARG(min_dev && max_dev, "mx_scales: null pointer");
+  MQ_CHECK_ARG(rule == MI355Q_MX_RULE_CT || rule == MI355Q_MX_RULE_OCP, "mx_scales: unknown rule");
+  if (n <= 0) return MI355Q_OK;
+  hipLaunchKernelGGL(mx_scales_kernel, dim3(grid_for(n, NT, 1u << 30)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), min_dev, max_dev, n, rule, e8m0_out_dev,
+                     scale_out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_quantize_int(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
+                                   int64_t ldx, const float* scale_dev, const float* zp_dev,
+                                   int64_t ld_scale, const int32_t* g_idx_dev, int strategy,
+                                   int64_t group_size, int block_h, int block_w, int num_bits,
+                                   mi355q_dtype div_dtype, int8_t* codes_dev, void* stream) {
+  MQ_CHECK_ARG(x_dev && scale_dev && codes_dev, "quantize_int: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "quantize_int: bad shape");
+  MQ_CHECK_ARG(num_bits >= 2 && num_bits <= 8, "quantize_int: num_bits must be in [2, 8]");
+  MQ_CHECK_ARG(strategy != MI355Q_GROUP || group_size > 0 || g_idx_dev, "quantize_int: group_size");
+  MQ_CHECK_ARG(strategy != MI355Q_BLOCK || (block_h > 0 && block_w > 0), "quantize_int: block");
+  const float qmin = -(float)(1 << (num_bits - 1)), qmax = (float)((1 << (num_bits - 1)) - 1);
+  hipLaunchKernelGGL(quantize_int_kernel, dim3(grid_for(rows * cols, NT, 1u << 16)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), x_dev, dtype, rows, cols, ldx, scale_dev,
+                     zp_dev, ld_scale, g_idx_dev, strategy, group_size, block_h, block_w, qmin, qmax,
+                     div_dtype == MI355Q_BF16 ? 1 : 0, codes_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_pack_int4_int32(const int8_t* codes_dev, int64_t rows, int64_t cols,
+                                      int32_t* out_dev, void* stream) {
+  MQ_CHECK_ARG(codes_dev && out_dev, "pack_int4_int32: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && cols % 8 == 0, "pack_int4_int32: cols must be a multiple of 8");
+  MQ_CHECK_ARG((reinterpret_cast<uintptr_t>(codes_dev) & 7) == 0, "pack_int4_int32: codes must be 8-byte aligned");
+  hipLaunchKernelGGL(pack_int4_int32_kernel, dim3(grid_for(rows * cols / 8, NT, 1u << 16)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), codes_dev, rows, cols, out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_pack_int4_int8(const int8_t* codes_dev, int64_t rows, int64_t cols,
+                                     int8_t* out_dev, void* stream) {
+  MQ_CHECK_ARG(codes_dev && out_dev, "pack_int4_int8: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0, "pack_int4_int8: bad shape");
+  MQ_CHECK_ARG(cols % 2 == 0, "Expected even number of columns for int4 packing, got %lld", (long long)cols);
+  hipLaunchKernelGGL(pack_int4_int8_kernel, dim3(grid_for(rows * cols / 2, NT, 1u << 16)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), codes_dev, rows, cols, out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_mxfp4_quantize_pack(const void* x_dev, int64_t rows, int64_t cols, int64_t ldx,
+                                          int rule, uint8_t* codes_dev, uint8_t* scales_dev,
+                                          void* stream) {
+  MQ_CHECK_ARG(x_dev && codes_dev && scales_dev, "mxfp4: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && cols % 32 == 0, "mxfp4: cols must be a positive multiple of 32");
+  MQ_CHECK_ARG(ldx >= cols && ldx % 8 == 0 && aligned16(x_dev), "mxfp4: x must be 16-byte aligned rows");
+  MQ_CHECK_ARG((reinterpret_cast<uintptr_t>(codes_dev) & 3) == 0, "mxfp4: codes must be 4-byte aligned");
+  MQ_CHECK_ARG(rule == MI355Q_MX_RULE_CT || rule == MI355Q_MX_RULE_OCP, "mxfp4: unknown rule");
+  const int64_t chunks = rows * (cols / 8);
+  // enough workgroups for ~8 per CU resident, each lane streaming several chunks
+  unsigned g = grid_for(chunks, NT, 256u * 16u);
+  hipLaunchKernelGGL(mxfp4_quantize_pack_kernel, dim3(g), dim3(NT), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(x_dev), rows, cols, ldx, rule,
+                     reinterpret_cast<uint32_t*>(codes_dev), scales_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_mxfp4_dequantize(const uint8_t* codes_dev, const uint8_t* scales_dev, int64_t rows,
+                                       int64_t cols, void* out_dev, void* stream) {
+  MQ_CHECK_ARG(codes_dev && scales_dev && out_dev, "mxfp4_dequantize: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && cols % 32 == 0, "mxfp4_dequantize: bad shape");
+  hipLaunchKernelGGL(mxfp4_dequant_kernel, dim3(grid_for(rows * cols, NT, 1u << 16)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), codes_dev, scales_dev, rows, cols,
+                     static_cast<uint16_t*>(out_dev));
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_quantize_fp8(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
+                                   int64_t ldx, const float* scale_dev, int64_t ld_scale, int strategy,
+                                   int64_t group_size, mi355q_dtype div_dtype, uint8_t* out_dev,
+                                   void* stream) {
+  MQ_CHECK_ARG(x_dev && scale_dev && out_dev, "quantize_fp8: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "quantize_fp8: bad shape");
+  MQ_CHECK_ARG(strategy == MI355Q_TENSOR || strategy == MI355Q_CHANNEL || strategy == MI355Q_TOKEN ||
+                   (strategy == MI355Q_GROUP && group_size > 0),
+               "quantize_fp8: unsupported strategy");
+  hipLaunchKernelGGL(quantize_fp8_kernel, dim3(grid_for(rows * cols, NT, 1u << 16)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), x_dev, dtype, rows, cols, ldx, scale_dev, ld_scale,
+                     strategy, group_size, div_dtype == MI355Q_BF16 ? 1 : 0, out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_quantize_int8_per_token(const void* x_dev, int64_t rows, int64_t cols, int64_t ldx,
+                                              int8_t* codes_dev, uint16_t* scale_out_dev, void* stream) {
+  MQ_CHECK_ARG(x_dev && codes_dev && scale_out_dev, "int8_per_token: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "int8_per_token: bad shape");
+  hipLaunchKernelGGL(int8_per_token_kernel, dim3((unsigned)rows), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x_dev), rows, cols,
+                     ldx, codes_dev, scale_out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}

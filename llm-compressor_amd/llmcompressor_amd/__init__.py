@@ -1,0 +1,21 @@
+"""MI355X (gfx950) calibration-time quantization for llm-compressor's hot path.
+
+The public functions keep the reference's names and signatures
+(``make_empty_hessian``, ``accumulate_hessian``, ``quantize_weight``, the
+observer registry, ``observe`` / ``update_qparams``); the arithmetic runs in
+hand-written HIP kernels (``libmi355q.so``, C ABI in ``include/mi355q.h``).
+"""
+from .calibration import initialize_module_for_quantization, initialize_observer, observe, update_qparams
+from .gptq import GPTQResult, accumulate_hessian, gptq_quantize, make_empty_hessian, quantize_weight, \
+    symmetrize_hessian
+from .modifiers import GPTQModifier, QuantizationModifier
+from .observers import Observer
+from .quant_args import (ActivationOrdering, QuantizationArgs, QuantizationScheme, QuantizationStrategy,
+                         QuantizationType, preset_name_to_scheme)
+
+__all__ = [
+    "ActivationOrdering", "GPTQModifier", "GPTQResult", "Observer", "QuantizationArgs", "QuantizationModifier",
+    "QuantizationScheme", "QuantizationStrategy", "QuantizationType", "accumulate_hessian", "gptq_quantize",
+    "initialize_module_for_quantization", "initialize_observer", "make_empty_hessian", "observe",
+    "preset_name_to_scheme", "quantize_weight", "symmetrize_hessian", "update_qparams",
+]

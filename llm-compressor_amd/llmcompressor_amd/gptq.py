@@ -1,0 +1,170 @@
+"""GPTQ Hessian accumulation and solve on the GPU (drop-in functions).
+
+Same names, signatures, return values and error behaviour as
+``modifiers/gptq/gptq_quantize.py``:
+
+* ``make_empty_hessian(module, device=None)``                 (``:54-60``)
+* ``accumulate_hessian(inp, module, H, num_samples)``          (``:63-97``)
+* ``quantize_weight(module, quant_args, hessian, blocksize=128, percdamp=0.01)``
+                                                              (``:100-296``)
+
+One documented difference: ``accumulate_hessian`` maintains the upper
+triangle of H (diagonal included) and leaves the strictly-lower part as it
+was (zero for a matrix from ``make_empty_hessian``).  ``quantize_weight``
+reads only the upper triangle, and ``symmetrize_hessian`` restores the full
+symmetric matrix when a caller needs it.
+"""
+from __future__ import annotations
+
+import logging
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationStrategy, QuantizationType
+
+logger = logging.getLogger("llmcompressor_amd")
+
+GPTQ_PRECISION = torch.float32
+
+__all__ = ["make_empty_hessian", "accumulate_hessian", "quantize_weight", "symmetrize_hessian",
+           "GPTQResult", "gptq_quantize"]
+
+
+def make_empty_hessian(module: torch.nn.Module, device: torch.device | None = None) -> torch.Tensor:
+    weight = module.weight
+    num_columns = weight.shape[1]
+    device = device if device is not None else weight.device
+    return torch.zeros((num_columns, num_columns), device=device, dtype=GPTQ_PRECISION)
+
+
+def _is_linear_like(module) -> bool:
+    if isinstance(module, torch.nn.Linear):
+        return True
+    return type(module).__name__ == "Conv1D"  # transformers.Conv1D
+
+
+def accumulate_hessian(inp: torch.Tensor, module: torch.nn.Module, H: torch.Tensor,
+                       num_samples: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """H += 2 * X^T X over the rows of ``inp`` (upper triangle, in place).
+
+    ``num_samples`` grows by the leading dimension after a 2-D input is
+    unsqueezed to 3-D, exactly as the reference counts it.
+    """
+    inp = inp.to(device=H.device)
+    if inp.dim() == 2:
+        inp = inp.unsqueeze(0)
+    num_added = inp.shape[0]
+    if not _is_linear_like(module):
+        raise NotImplementedError(f"GPTQ Hessian for {type(module).__name__} is not provided by this build")
+    x = inp.reshape(-1, inp.shape[-1])
+    num_samples += num_added
+    if x.shape[0] > 0:
+        ops.hessian_syrk_(H, x, alpha=2.0)
+    return H, num_samples
+
+
+def symmetrize_hessian(H: torch.Tensor) -> torch.Tensor:
+    """Mirror the upper triangle onto the lower one (in place)."""
+    return ops.symmetrize_upper_(H)
+
+
+@dataclass
+class GPTQResult:
+    loss: float
+    weight: torch.Tensor            # fake-quantised, original dtype, original column order
+    scale: torch.Tensor             # as the observer produced it
+    zero_point: torch.Tensor
+    g_idx: torch.Tensor | None      # reference g_idx in working order (None if no groups)
+    perm: torch.Tensor | None
+    codes: torch.Tensor             # int8 integer codes, original column order
+    hinv_ok: bool
+
+
+def _qparams_for_sweep(scale: torch.Tensor, zero_point: torch.Tensor, strategy: QuantizationStrategy):
+    s = scale.to(torch.float32)
+    z = zero_point.to(torch.float32)
+    if strategy == QuantizationStrategy.TENSOR:
+        s, z = s.reshape(1, 1), z.reshape(1, 1)
+    elif s.dim() == 1:
+        s, z = s.reshape(-1, 1), z.reshape(-1, 1)
+    return s.contiguous(), z.contiguous()
+
+
+def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: torch.Tensor, observer,
+                  blocksize: int = 128, percdamp: float = 0.01, num_samples: float = 1.0) -> GPTQResult:
+    """The GPTQ solve of ``gptq_quantize.py:100-296`` on the GPU.
+
+    ``hessian`` is the accumulated upper-triangle Hessian; ``num_samples``
+    is divided out inside the kernels (the reference divides before the call,
+    ``modifiers/gptq/base.py:594``).  ``observer`` must already hold the
+    weight statistics (``observe``), as in the reference.
+    """
+    strategy = quant_args.strategy
+    actorder = quant_args.actorder
+    if quant_args.type != QuantizationType.INT:
+        raise NotImplementedError("GPTQ on the GPU supports integer quantization types")
+    if strategy not in (QuantizationStrategy.TENSOR, QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP,
+                        QuantizationStrategy.BLOCK):
+        raise ValueError(f"Quantization strategy is not supported for GPTQ: {strategy}")
+    W = weight
+    rows, cols = W.shape
+    if actorder == ActivationOrdering.GROUP and strategy not in (QuantizationStrategy.GROUP,
+                                                                 QuantizationStrategy.TENSOR_GROUP):
+        logger.warning("ActivationOrdering.GROUP requires a grouped quantization strategy; "
+                       "falling back to actorder=None for this module.")
+        actorder = None
+
+    perm = invperm = None
+    if actorder:
+        perm = torch.argsort(torch.diagonal(hessian), descending=True, stable=True)
+        invperm = torch.argsort(perm)
+    if actorder == ActivationOrdering.GROUP:
+        observer.delete_statistics(check_fused=False)
+        observer(ops.gptq_load_weight(W, perm))   # permuted fp32 weight
+
+    g_idx = None
+    if strategy in (QuantizationStrategy.GROUP, QuantizationStrategy.BLOCK):
+        divisor = quant_args.group_size if strategy != QuantizationStrategy.BLOCK else quant_args.block_structure[1]
+        g_idx = torch.arange(cols, device=W.device, dtype=torch.int) // divisor
+        if actorder == ActivationOrdering.WEIGHT:
+            g_idx = g_idx[perm]
+
+    qp = observer.get_qparams()
+    scale, zero_point = qp["scale"], qp["zero_point"]
+
+    hinv, dead, ok = ops.gptq_hinv(hessian, perm, float(num_samples), percdamp)
+    if not ok:
+        logger.warning("Failed to invert hessian due to numerical instability. Consider increasing "
+                       "GPTQModifier.dampening_frac, increasing the number of calibration samples, or "
+                       "shuffling the calibration dataset. Falling back to round-to-nearest for this module.")
+        hinv = torch.eye(cols, dtype=torch.float32, device=W.device)
+
+    w_work = ops.gptq_load_weight(W, perm, dead)
+    s, z = _qparams_for_sweep(scale, zero_point, strategy)
+    qmin, qmax = quant_args.q_range()
+    bh = quant_args.block_structure[0] if strategy == QuantizationStrategy.BLOCK else 1
+    codes, losses = ops.gptq_sweep_(w_work, hinv, s, z, strategy.value, g_idx, qmin, qmax,
+                                    dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize, block_h=bh)
+    w_out, codes_out = ops.gptq_store_weight(w_work, invperm, W.dtype, codes)
+    loss = torch.sum(losses).item()
+    return GPTQResult(loss=loss, weight=w_out, scale=scale, zero_point=zero_point, g_idx=g_idx, perm=perm,
+                      codes=codes_out, hinv_ok=ok)
+
+
+def quantize_weight(module: torch.nn.Module, quant_args: QuantizationArgs, hessian: torch.Tensor,
+                    blocksize: int = 128, percdamp: float = 0.01):
+    """Drop-in for ``gptq_quantize.quantize_weight``: returns ``(loss, q_param_dict)``."""
+    res = gptq_quantize(module.weight, quant_args, hessian, module.weight_observer, blocksize, percdamp)
+    final_dtype = module.weight.dtype
+    q = {
+        "weight": res.weight.reshape(module.weight.shape),
+        "weight_scale": res.scale.to(dtype=final_dtype),
+        "weight_zero_point": res.zero_point.to(dtype=quant_args.zp_dtype),
+    }
+    actorder = quant_args.actorder
+    if actorder == ActivationOrdering.GROUP and quant_args.strategy in (QuantizationStrategy.GROUP,
+                                                                        QuantizationStrategy.TENSOR_GROUP):
+        q["weight_g_idx"] = res.g_idx[torch.argsort(res.perm)]
+    return res.loss, q

@@ -1,0 +1,174 @@
+"""Min-max observers backed by the gfx950 reduction kernels.
+
+Mirrors ``observers/base.py:29-206`` and ``observers/min_max.py:16-110``:
+the same registry names (``memoryless_minmax``, ``static_minmax``,
+``minmax``, ``strict_symmetric_minmax``), the same statistics
+(``min_vals`` / ``max_vals`` shaped per strategy as
+``observers/helpers.py:63-131`` flattens), weight observers that keep their
+first statistics until ``get_qparams`` deletes them, and ``get_qparams``
+returning ``{"scale", "zero_point", "global_scale"}`` with the scale in the
+observed dtype (bf16 for a bf16 weight).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from .quant_args import QuantizationArgs, QuantizationStrategy, QuantizationType
+
+ACTIVATION_OBS = ("input", "output", "q", "k", "v")
+
+
+class Observer(torch.nn.Module):
+    _registry: dict[str, type] = {}
+    _stats_attrs = ("min_vals", "max_vals")
+
+    def __init__(self, base_name: str, args: QuantizationArgs, **observer_kwargs):
+        super().__init__()
+        self.base_name = base_name
+        self.args = args
+        self.args.observer_kwargs = dict(self.args.observer_kwargs or {})
+        self.args.observer_kwargs.update(observer_kwargs)
+        self._observed_dtype: torch.dtype | None = None
+
+    # -- registry (compressed-tensors RegistryMixin semantics)
+    @classmethod
+    def register(cls, name: str):
+        def deco(sub):
+            cls._registry[name] = sub
+            return sub
+        return deco
+
+    @classmethod
+    def load_from_registry(cls, name: str, **kwargs) -> "Observer":
+        try:
+            sub = cls._registry[name]
+        except KeyError:
+            raise ValueError(f"Unknown observer {name}; registered: {sorted(cls._registry)}") from None
+        return sub(**kwargs)
+
+    @property
+    def has_statistics(self) -> bool:
+        return all(getattr(self, a, None) is not None for a in self._stats_attrs)
+
+    @property
+    def is_weight_obs(self) -> bool:
+        return self.base_name == "weight"
+
+    def delete_statistics(self, check_fused: bool = True) -> None:
+        for a in self._stats_attrs:
+            if hasattr(self, a):
+                delattr(self, a)
+
+    def get_statistics(self) -> dict:
+        assert self.has_statistics, "No statistics available. Call observer(value) first."
+        return {a: getattr(self, a) for a in self._stats_attrs}
+
+    # -- observation
+    def _min_max(self, observed: torch.Tensor):
+        a = self.args
+        s = a.strategy
+        if self.is_weight_obs:
+            if s == QuantizationStrategy.TOKEN:
+                raise ValueError("Token quantization cannot be applied to weights")
+            return ops.observe_minmax(observed, s.value, a.group_size, a.block_structure)
+        # activations: (batch, seq, hidden) -> rows = tokens
+        x2 = observed.reshape(-1, observed.shape[-1])
+        if s == QuantizationStrategy.TENSOR:
+            return ops.observe_minmax(x2, "tensor")
+        if s in (QuantizationStrategy.GROUP, QuantizationStrategy.TENSOR_GROUP):
+            mn, mx = ops.observe_minmax(x2, "group", a.group_size)
+            return mn.amin(dim=0), mx.amax(dim=0)
+        raise ValueError(f"{s.value} quantization cannot be observed for activations here")
+
+    def update_statistics_from_observed(self, mn: torch.Tensor, mx: torch.Tensor) -> None:
+        raise NotImplementedError
+
+    @torch.no_grad()
+    def forward(self, observed: torch.Tensor) -> "Observer":
+        if observed.numel() == 0:
+            return self
+        if self.is_weight_obs and self.has_statistics:
+            return self
+        if not observed.is_floating_point():
+            observed = observed.to(torch.float32)  # integer observations compute in fp32
+        elif observed.dtype not in (torch.bfloat16, torch.float32):
+            raise TypeError(f"observer supports bf16 / fp32 values, got {observed.dtype}")
+        self._observed_dtype = observed.dtype
+        mn, mx = self._min_max(observed)
+        # statistics live in the observed dtype, as torch.amin/amax return them
+        self.update_statistics_from_observed(mn.to(observed.dtype), mx.to(observed.dtype))
+        return self
+
+    # -- qparams
+    def _stats_dtype(self) -> torch.dtype:
+        return self._observed_dtype if self._observed_dtype == torch.bfloat16 else torch.float32
+
+    @torch.no_grad()
+    def get_qparams(self) -> dict:
+        assert self.has_statistics, "No statistics available. Call observer(value) first."
+        a = self.args
+        dt = self._stats_dtype()
+        if a.is_mx:
+            _, scale = ops.mx_scales(self.min_vals, self.max_vals, a.observer_kwargs.get("mx_rule", "ct"))
+            zp = torch.zeros(scale.shape, dtype=a.zp_dtype, device=scale.device)
+            out = {"scale": scale.to(torch.bfloat16), "zero_point": zp, "global_scale": None}
+        elif a.strategy == QuantizationStrategy.TENSOR_GROUP:
+            raise NotImplementedError("tensor_group (NVFP4 global scale) is not provided by this build")
+        else:
+            qmin, qmax = a.q_range()
+            scale, zp = ops.calculate_qparams(self.min_vals, self.max_vals, qmin, qmax, a.symmetric, dt)
+            if a.type == QuantizationType.FLOAT and not a.symmetric:
+                raise NotImplementedError("asymmetric float quantization")
+            scale = scale.to(a.scale_dtype if a.scale_dtype is not None else dt)
+            out = {"scale": scale, "zero_point": zp.to(a.zp_dtype), "global_scale": None}
+        self.delete_statistics()
+        return out
+
+
+@Observer.register("memoryless_minmax")
+class MemorylessMinMaxObserver(Observer):
+    def update_statistics_from_observed(self, mn, mx):
+        self.min_vals, self.max_vals = mn, mx
+
+
+@Observer.register("strict_symmetric_minmax")
+class StrictSymmetricMinMaxObserver(MemorylessMinMaxObserver):
+    """Symmetric int range [-(2^(b-1)-1), 2^(b-1)-1], fp32 scale (``min_max.py:28-55``)."""
+
+    @torch.no_grad()
+    def get_qparams(self):
+        a = self.args
+        if a.type != QuantizationType.INT or not a.symmetric:
+            raise ValueError("strict_symmetric_minmax requires symmetric integer quantization")
+        qmax = 2.0 ** (a.num_bits - 1) - 1
+        sdt = a.scale_dtype if a.scale_dtype is not None else torch.float32
+        scale, _ = ops.calculate_qparams(self.min_vals, self.max_vals, -qmax - 1, qmax, True,
+                                         torch.bfloat16 if sdt == torch.bfloat16 else torch.float32, strict=True)
+        scale = scale.to(sdt)
+        self.delete_statistics()
+        return {"scale": scale, "zero_point": torch.zeros_like(scale, dtype=a.zp_dtype), "global_scale": None}
+
+
+@Observer.register("static_minmax")
+class StaticMinMaxObserver(MemorylessMinMaxObserver):
+    def update_statistics_from_observed(self, mn, mx):
+        if self.has_statistics:
+            mn, mx = torch.min(mn, self.min_vals), torch.max(mx, self.max_vals)
+        self.min_vals, self.max_vals = mn, mx
+
+
+@Observer.register("minmax")
+class MinMaxObserver(Observer):
+    """Moving average of min/max with ``averaging_constant`` (default 0.01)."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.avg_constant = self.args.observer_kwargs.get("averaging_constant", 0.01)
+
+    def update_statistics_from_observed(self, mn, mx):
+        if self.has_statistics and self.avg_constant != 1.0:
+            c = self.avg_constant
+            mn = self.min_vals * (1.0 - c) + mn * c
+            mx = self.max_vals * (1.0 - c) + mx * c
+        self.min_vals, self.max_vals = mn, mx

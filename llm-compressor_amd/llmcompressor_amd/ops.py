@@ -1,0 +1,327 @@
+"""Tensor-level wrappers of the libmi355q kernels.
+
+Each function validates shapes, allocates outputs and workspaces with the
+torch caching allocator on the inputs' device, and launches on torch's
+current stream.  All tensors must live on a ROCm GPU; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib as L
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return L.BF16
+    if t.dtype == torch.float32:
+        return L.F32
+    raise TypeError(f"unsupported dtype {t.dtype} (bf16 or fp32)")
+
+
+def _ws(nbytes: int, device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------- Hessian
+def hessian_syrk_(H: torch.Tensor, x: torch.Tensor, alpha: float = 2.0) -> torch.Tensor:
+    """H[i, j] += alpha * sum_t x[t, i] x[t, j] for i <= j, in place.
+
+    ``x`` is [tokens, d] bf16 (row stride may exceed d); H is fp32 [d, d].
+    """
+    L.require_gpu(H, x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"hessian input must be bf16, got {x.dtype}")
+    if x.dim() != 2 or x.stride(1) != 1:
+        x = x.reshape(-1, x.shape[-1]).contiguous()
+    if x.data_ptr() % 16 or x.stride(0) % 8:
+        x = x.contiguous()
+    n, d = x.shape
+    if H.dtype != torch.float32 or H.shape != (d, d) or H.stride(1) != 1:
+        raise ValueError(f"H must be fp32 [{d}, {d}] row-major, got {tuple(H.shape)} {H.dtype}")
+    lib = L.lib()
+    ws = _ws(lib.mi355q_hessian_workspace_size(n, d), x.device)
+    L.check(lib.mi355q_hessian_syrk_bf16(x.data_ptr(), n, d, x.stride(0), H.data_ptr(), H.stride(0),
+                                         C.c_float(alpha), L.ptr(ws), 0 if ws is None else ws.numel(),
+                                         L.stream_of(x)))
+    return H
+
+
+def hessian_grouped_syrk_(H: torch.Tensor, x: torch.Tensor, rows: torch.Tensor, offsets: list[int],
+                          alpha: float = 2.0) -> torch.Tensor:
+    """Per-group upper-triangle syrk: H[e] += alpha * X_e^T X_e where X_e are
+    the rows ``x[rows[offsets[e]:offsets[e+1]]]``.  H is [E, d, d] fp32."""
+    L.require_gpu(H, x, rows)
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.stride(1) != 1:
+        raise TypeError("grouped hessian input must be a row-major bf16 matrix")
+    E = len(offsets) - 1
+    d = x.shape[1]
+    if H.shape != (E, d, d) or H.dtype != torch.float32 or not H.is_contiguous():
+        raise ValueError(f"H must be contiguous fp32 [{E}, {d}, {d}]")
+    rows = rows.to(torch.int32).contiguous()
+    off = (C.c_int64 * (E + 1))(*[int(o) for o in offsets])
+    lib = L.lib()
+    ws = _ws(lib.mi355q_hessian_grouped_workspace_size(off, E, d), x.device)
+    L.check(lib.mi355q_hessian_grouped_syrk_bf16(x.data_ptr(), x.stride(0), d, rows.data_ptr(), off, E,
+                                                 H.data_ptr(), d * d, C.c_float(alpha), L.ptr(ws),
+                                                 0 if ws is None else ws.numel(), L.stream_of(x)))
+    return H
+
+
+def symmetrize_upper_(H: torch.Tensor) -> torch.Tensor:
+    """Copy the upper triangle onto the lower one, in place."""
+    L.require_gpu(H)
+    d = H.shape[0]
+    L.call("mi355q_symmetrize_upper", H.data_ptr(), d, H.stride(0), L.stream_of(H))
+    return H
+
+
+# ---------------------------------------------------------------- GPTQ pieces
+def gptq_hinv(H: torch.Tensor, perm: torch.Tensor | None, num_samples: float, percdamp: float):
+    """Upper Cholesky factor of inverse(damped H / num_samples).
+
+    Returns (hinv [d, d] fp32, dead [d] int32, positive_definite: bool).
+    Synchronises once to read the status flag.
+    """
+    L.require_gpu(H)
+    d = H.shape[0]
+    dev = H.device
+    hinv = torch.empty((d, d), dtype=torch.float32, device=dev)
+    dead = torch.empty(d, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    lib = L.lib()
+    ws = _ws(lib.mi355q_gptq_hinv_workspace_size(d), dev)
+    p = None if perm is None else perm.to(torch.int32).contiguous()
+    L.check(lib.mi355q_gptq_hinv(H.data_ptr(), H.stride(0), d, L.ptr(p), C.c_float(num_samples),
+                                 C.c_float(percdamp), hinv.data_ptr(), dead.data_ptr(), status.data_ptr(),
+                                 ws.data_ptr(), ws.numel(), L.stream_of(H)))
+    ok = int(status.item()) == 0
+    return hinv, dead, ok
+
+
+def gptq_load_weight(w: torch.Tensor, perm=None, dead=None) -> torch.Tensor:
+    L.require_gpu(w)
+    rows, cols = w.shape
+    out = torch.empty((rows, cols), dtype=torch.float32, device=w.device)
+    p = None if perm is None else perm.to(torch.int32).contiguous()
+    dd = None if dead is None else dead.to(torch.int32).contiguous()
+    L.call("mi355q_gptq_load_weight", w.data_ptr(), _dt(w), rows, cols, w.stride(0), L.ptr(p), L.ptr(dd),
+           out.data_ptr(), L.stream_of(w))
+    return out
+
+
+STRATEGY_CODE = {"tensor": L.TENSOR, "channel": L.CHANNEL, "group": L.GROUP, "tensor_group": L.GROUP,
+                 "block": L.BLOCK, "token": L.TOKEN}
+
+
+def gptq_sweep_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.Tensor, zero_point, strategy: str,
+                g_idx: torch.Tensor | None, qmin: float, qmax: float, dequant_bf16: bool,
+                blocksize: int = 128, block_h: int = 1):
+    """In-place GPTQ column sweep.  Returns (codes int8 [rows, cols], losses fp32 [rows])."""
+    L.require_gpu(w_work, hinv, scale)
+    rows, cols = w_work.shape
+    dev = w_work.device
+    s = scale.to(torch.float32).contiguous()
+    if s.dim() == 1:
+        s = s.reshape(-1, 1)
+    z = None if zero_point is None else zero_point.to(torch.float32).reshape(s.shape).contiguous()
+    gi = None if g_idx is None else g_idx.to(torch.int32).contiguous()
+    codes = torch.empty((rows, cols), dtype=torch.int8, device=dev)
+    losses = torch.zeros(rows, dtype=torch.float32, device=dev)
+    lib = L.lib()
+    ws = _ws(lib.mi355q_gptq_sweep_workspace_size(rows, cols, blocksize), dev)
+    L.check(lib.mi355q_gptq_sweep(w_work.data_ptr(), rows, cols, hinv.data_ptr(), s.data_ptr(), L.ptr(z),
+                                  s.stride(0), L.ptr(gi), STRATEGY_CODE[strategy], block_h, C.c_float(qmin),
+                                  C.c_float(qmax), 1 if dequant_bf16 else 0, blocksize, codes.data_ptr(),
+                                  losses.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_of(w_work)))
+    return codes, losses
+
+
+def gptq_store_weight(w_work: torch.Tensor, invperm, out_dtype: torch.dtype, codes=None):
+    rows, cols = w_work.shape
+    out = torch.empty((rows, cols), dtype=out_dtype, device=w_work.device)
+    ip = None if invperm is None else invperm.to(torch.int32).contiguous()
+    cout = None if codes is None else torch.empty_like(codes)
+    L.call("mi355q_gptq_store_weight", w_work.data_ptr(), rows, cols, L.ptr(ip), out.data_ptr(), _dt(out),
+           out.stride(0), L.ptr(codes), L.ptr(cout), L.stream_of(w_work))
+    return out, cout
+
+
+# ---------------------------------------------------------------- observers
+def observe_minmax(x: torch.Tensor, strategy: str, group_size: int | None = None,
+                   block_structure=None):
+    """Min/max statistics of a 2-D tensor per strategy, as fp32 tensors.
+
+    Shapes: tensor -> [1]; channel/token -> [rows, 1]; group ->
+    [rows, cols / group]; block -> [ceil(rows/bh), ceil(cols/bw)].
+    """
+    L.require_gpu(x)
+    if x.dim() != 2:
+        raise ValueError("observe_minmax expects a 2-D tensor")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    rows, cols = x.shape
+    bh = bw = 1
+    if strategy == "tensor":
+        shape = (1,)
+    elif strategy in ("channel", "token"):
+        shape = (rows, 1)
+    elif strategy in ("group", "tensor_group"):
+        if not group_size or cols % group_size:
+            raise ValueError(f"columns ({cols}) must be divisible by group_size ({group_size})")
+        shape = (rows, cols // group_size)
+    elif strategy == "block":
+        bh, bw = block_structure
+        shape = (-(-rows // bh), -(-cols // bw))
+    else:
+        raise ValueError(f"unknown strategy {strategy}")
+    mn = torch.empty(shape, dtype=torch.float32, device=x.device)
+    mx = torch.empty(shape, dtype=torch.float32, device=x.device)
+    L.call("mi355q_observe_minmax", x.data_ptr(), _dt(x), rows, cols, x.stride(0), STRATEGY_CODE[strategy],
+           group_size or 0, bh, bw, mn.data_ptr(), mx.data_ptr(), L.stream_of(x))
+    return mn, mx
+
+
+def calculate_qparams(mn: torch.Tensor, mx: torch.Tensor, qmin: float, qmax: float, symmetric: bool,
+                      scale_dtype: torch.dtype, strict: bool = False):
+    """Scale / zero-point from min/max statistics (fp32 outputs holding
+    ``scale_dtype`` values and integer zero-points)."""
+    L.require_gpu(mn, mx)
+    mn = mn.to(torch.float32).contiguous()
+    mx = mx.to(torch.float32).contiguous()
+    scale = torch.empty_like(mn)
+    zp = torch.empty_like(mn)
+    L.call("mi355q_calculate_qparams", mn.data_ptr(), mx.data_ptr(), mn.numel(), C.c_float(qmin),
+           C.c_float(qmax), 1 if symmetric else 0, 1 if strict else 0,
+           L.BF16 if scale_dtype == torch.bfloat16 else L.F32, scale.data_ptr(), zp.data_ptr(), L.stream_of(mn))
+    return scale, zp
+
+
+MX_RULES = {"ct": L.MX_RULE_CT, "ocp": L.MX_RULE_OCP}
+
+
+def mx_scales(mn: torch.Tensor, mx: torch.Tensor, rule: str = "ct"):
+    """(e8m0 uint8, 2^(e-127) fp32) per group from min/max statistics."""
+    L.require_gpu(mn, mx)
+    mn = mn.to(torch.float32).contiguous()
+    mx = mx.to(torch.float32).contiguous()
+    e8 = torch.empty(mn.shape, dtype=torch.uint8, device=mn.device)
+    sc = torch.empty_like(mn)
+    L.call("mi355q_mx_scales", mn.data_ptr(), mx.data_ptr(), mn.numel(), MX_RULES[rule], e8.data_ptr(),
+           sc.data_ptr(), L.stream_of(mn))
+    return e8, sc
+
+
+# ---------------------------------------------------------------- quantize / pack
+def quantize_int(x: torch.Tensor, scale: torch.Tensor, zero_point, strategy: str, num_bits: int,
+                 group_size: int | None = None, g_idx=None, block_structure=None,
+                 div_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Integer codes (int8) of ``x`` with CT quantize arithmetic."""
+    L.require_gpu(x, scale)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    rows, cols = x.shape
+    s = scale.to(torch.float32).contiguous()
+    s2 = s.reshape(-1, 1) if s.dim() < 2 else s
+    z = None if zero_point is None else zero_point.to(torch.float32).reshape(s2.shape).contiguous()
+    gi = None if g_idx is None else g_idx.to(torch.int32).contiguous()
+    bh, bw = block_structure if block_structure else (1, 1)
+    if div_dtype is None:
+        div_dtype = torch.promote_types(x.dtype, scale.dtype)
+    out = torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+    L.call("mi355q_quantize_int", x.data_ptr(), _dt(x), rows, cols, x.stride(0), s2.data_ptr(), L.ptr(z),
+           s2.stride(0), L.ptr(gi), STRATEGY_CODE[strategy], group_size or 0, bh, bw, num_bits,
+           L.BF16 if div_dtype == torch.bfloat16 else L.F32, out.data_ptr(), L.stream_of(x))
+    return out
+
+
+def pack_int4_int32(codes: torch.Tensor) -> torch.Tensor:
+    L.require_gpu(codes)
+    codes = codes.contiguous()
+    rows, cols = codes.shape
+    out = torch.empty((rows, cols // 8), dtype=torch.int32, device=codes.device)
+    L.call("mi355q_pack_int4_int32", codes.data_ptr(), rows, cols, out.data_ptr(), L.stream_of(codes))
+    return out
+
+
+def pack_int4_int8(codes: torch.Tensor) -> torch.Tensor:
+    L.require_gpu(codes)
+    if codes.dim() != 2:
+        raise ValueError(f"Expected 2D tensor, but got {codes.dim()}D")
+    rows, cols = codes.shape
+    if cols % 2:
+        raise ValueError(f"Expected even number of columns for int4 packing, but got shape {tuple(codes.shape)}")
+    codes = codes.contiguous()
+    out = torch.empty((rows, cols // 2), dtype=torch.int8, device=codes.device)
+    L.call("mi355q_pack_int4_int8", codes.data_ptr(), rows, cols, out.data_ptr(), L.stream_of(codes))
+    return out
+
+
+def mxfp4_quantize_pack(x: torch.Tensor, rule: str = "ct", out=None):
+    """bf16 [rows, cols] -> (codes uint8 [rows, cols/2], e8m0 uint8 [rows, cols/32])."""
+    L.require_gpu(x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError("MXFP4 quantize expects bf16 input")
+    if x.dim() != 2:
+        x = x.reshape(-1, x.shape[-1])
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    rows, cols = x.shape
+    if cols % 32:
+        raise ValueError(f"MXFP4 needs the last dim divisible by 32, got {cols}")
+    if out is None:
+        codes = torch.empty((rows, cols // 2), dtype=torch.uint8, device=x.device)
+        scales = torch.empty((rows, cols // 32), dtype=torch.uint8, device=x.device)
+    else:
+        codes, scales = out
+    L.call("mi355q_mxfp4_quantize_pack", x.data_ptr(), rows, cols, x.stride(0), MX_RULES[rule],
+           codes.data_ptr(), scales.data_ptr(), L.stream_of(x))
+    return codes, scales
+
+
+def mxfp4_dequantize(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    L.require_gpu(codes, scales)
+    rows, half = codes.shape
+    out = torch.empty((rows, half * 2), dtype=torch.bfloat16, device=codes.device)
+    L.call("mi355q_mxfp4_dequantize", codes.contiguous().data_ptr(), scales.contiguous().data_ptr(), rows,
+           half * 2, out.data_ptr(), L.stream_of(codes))
+    return out
+
+
+def quantize_fp8(x: torch.Tensor, scale: torch.Tensor, strategy: str, group_size: int | None = None,
+                 div_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """float8_e4m3fn codes (as a float8 tensor) with CT quantize arithmetic."""
+    L.require_gpu(x, scale)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    rows, cols = x.shape
+    s = scale.to(torch.float32).contiguous()
+    s2 = s.reshape(-1, 1) if s.dim() < 2 else s
+    if div_dtype is None:
+        div_dtype = torch.promote_types(x.dtype, scale.dtype)
+    out = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
+    L.call("mi355q_quantize_fp8", x.data_ptr(), _dt(x), rows, cols, x.stride(0), s2.data_ptr(), s2.stride(0),
+           STRATEGY_CODE[strategy], group_size or 0, L.BF16 if div_dtype == torch.bfloat16 else L.F32,
+           out.data_ptr(), L.stream_of(x))
+    return out.view(torch.float8_e4m3fn)
+
+
+def quantize_int8_per_token(x: torch.Tensor):
+    """Dynamic per-token int8: (codes int8 [rows, cols], scale bf16 [rows, 1])."""
+    L.require_gpu(x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError("per-token int8 expects bf16 activations")
+    if x.dim() != 2:
+        x = x.reshape(-1, x.shape[-1])
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    rows, cols = x.shape
+    codes = torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+    scale = torch.empty((rows, 1), dtype=torch.bfloat16, device=x.device)
+    L.call("mi355q_quantize_int8_per_token", x.data_ptr(), rows, cols, x.stride(0), codes.data_ptr(),
+           scale.data_ptr(), L.stream_of(x))
+    return codes, scale

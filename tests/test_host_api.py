@@ -1,0 +1,97 @@
+"""Host-side logic of the drop-in API (CPU only, no kernel launches)."""
+import pytest
+import torch
+
+from llmcompressor_amd import GPTQModifier, Observer, QuantizationArgs, preset_name_to_scheme
+from llmcompressor_amd.calibration import initialize_module_for_quantization, initialize_observer
+from llmcompressor_amd.quant_args import ActivationOrdering, QuantizationScheme, QuantizationStrategy
+
+
+def test_quantization_args_defaults_follow_compressed_tensors():
+    assert QuantizationArgs().strategy == QuantizationStrategy.TENSOR
+    assert QuantizationArgs(group_size=128).strategy == QuantizationStrategy.GROUP
+    assert QuantizationArgs(group_size=-1).strategy == QuantizationStrategy.CHANNEL
+    assert QuantizationArgs().zp_dtype == torch.int8
+    assert QuantizationArgs(num_bits=4).q_range() == (-8.0, 7.0)
+    assert QuantizationArgs(num_bits=8, type="float").q_range() == (-448.0, 448.0)
+    assert QuantizationArgs(actorder="static").actorder == ActivationOrdering.WEIGHT
+    assert QuantizationArgs(actorder="dynamic").actorder == ActivationOrdering.GROUP
+    assert QuantizationArgs(actorder=True).actorder == ActivationOrdering.GROUP
+    with pytest.raises(ValueError):
+        QuantizationArgs(strategy="block")
+
+
+def test_presets():
+    w4 = preset_name_to_scheme("W4A16", ["Linear"])
+    assert w4.weights.num_bits == 4 and w4.weights.group_size == 128 and w4.input_activations is None
+    w8 = preset_name_to_scheme("W8A8", ["Linear"])
+    assert w8.weights.strategy == QuantizationStrategy.CHANNEL
+    assert w8.input_activations.strategy == QuantizationStrategy.TOKEN and w8.input_activations.dynamic
+    mx = preset_name_to_scheme("MXFP4", ["Linear"])
+    assert mx.weights.is_mx and mx.input_activations.dynamic
+    with pytest.raises(KeyError):
+        preset_name_to_scheme("NOPE", ["Linear"])
+
+
+def test_observer_registry_names():
+    args = QuantizationArgs()
+    for name in ("memoryless_minmax", "static_minmax", "minmax", "strict_symmetric_minmax"):
+        assert isinstance(Observer.load_from_registry(name, base_name="weight", args=args), Observer)
+    with pytest.raises(ValueError):
+        Observer.load_from_registry("nope", base_name="weight", args=args)
+
+
+def test_initialize_observer_overrides_weight_minmax():
+    """calibration.py:64-71: weight minmax -> memoryless; dynamic args get none (:80)."""
+    lin = torch.nn.Linear(16, 8, bias=False)
+    initialize_module_for_quantization(lin, preset_name_to_scheme("W8A8", ["Linear"]))
+    initialize_observer(lin, "weight")
+    initialize_observer(lin, "input")
+    assert type(lin.weight_observer).__name__ == "MemorylessMinMaxObserver"
+    assert not hasattr(lin, "input_observer")
+    assert lin.weight_scale.shape == (8, 1) and lin.weight_zero_point.dtype == torch.int8
+
+
+def test_qparam_shapes_per_strategy():
+    lin = torch.nn.Linear(64, 6, bias=False)
+    initialize_module_for_quantization(lin, QuantizationScheme(weights=QuantizationArgs(num_bits=4, group_size=16)))
+    assert lin.weight_scale.shape == (6, 4)
+    lin2 = torch.nn.Linear(7, 5, bias=False)
+    initialize_module_for_quantization(lin2, QuantizationScheme(
+        weights=QuantizationArgs(num_bits=8, strategy="block", block_structure=[2, 4])))
+    assert lin2.weight_scale.shape == (3, 2)
+
+
+@pytest.mark.parametrize("modifier_actorder,scheme_actorder,expected", [
+    ("static", None, ActivationOrdering.WEIGHT),
+    ("static", "group", ActivationOrdering.GROUP),
+    ("group", None, ActivationOrdering.GROUP),
+    (None, None, None),
+    ("weight", "weight", ActivationOrdering.WEIGHT),
+])
+def test_actorder_resolution(modifier_actorder, scheme_actorder, expected):
+    """modifiers/gptq/base.py:137-193 truth table."""
+    m = GPTQModifier(actorder=modifier_actorder)
+    s = QuantizationScheme(weights=QuantizationArgs(num_bits=4, group_size=128, actorder=scheme_actorder))
+    m._resolve_actorder(s)
+    assert s.weights.actorder == expected
+
+
+def test_actorder_conflict_raises():
+    m = GPTQModifier(actorder="group")
+    s = QuantizationScheme(weights=QuantizationArgs(num_bits=4, group_size=128, actorder="weight"))
+    with pytest.raises(ValueError, match="Cannot resolve activation ordering"):
+        m._resolve_actorder(s)
+
+
+def test_actorder_group_on_channel_falls_back():
+    m = GPTQModifier(actorder="group")
+    s = QuantizationScheme(weights=QuantizationArgs(num_bits=8, strategy="channel"))
+    m._resolve_actorder(s)
+    assert s.weights.actorder is None
+
+
+def test_cpu_tensors_are_refused():
+    from llmcompressor_amd import ops
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops.observe_minmax(torch.zeros(4, 4), "tensor")

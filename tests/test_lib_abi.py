@@ -1,0 +1,60 @@
+"""The C-ABI library loads, exports every declared symbol, and validates
+arguments on the host (CPU only: no kernel launches)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from llmcompressor_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mi355q.h"
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mi355q_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load_library()
+    names = declared_symbols()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version_and_workspace_queries():
+    lib = _lib.load_library()
+    assert lib.mi355q_version() == 1
+    assert lib.mi355q_hessian_workspace_size(2048, 4096) == 0            # single split, direct update
+    assert lib.mi355q_hessian_workspace_size(131072, 4096) == 8 * 528 * 128 * 128 * 4
+    assert lib.mi355q_gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 128 * 4
+    assert lib.mi355q_gptq_hinv_workspace_size(4096) >= 2 * 4096 * 4096 * 4
+
+
+@pytest.mark.parametrize("call,needle", [
+    (lambda l: l.mi355q_hessian_syrk_bf16(None, 10, 7, 7, None, 7, C.c_float(2.0), None, 0, None), "multiple of 8"),
+    (lambda l: l.mi355q_pack_int4_int8(None, 2, 3, None, None), "null pointer"),
+    (lambda l: l.mi355q_mxfp4_quantize_pack(C.c_void_p(16), 4, 30, 32, 0, C.c_void_p(16), C.c_void_p(16), None),
+     "multiple of 32"),
+    (lambda l: l.mi355q_gptq_sweep(C.c_void_p(16), 4, 4, C.c_void_p(16), C.c_void_p(16), None, 1, None, 7, 1,
+                                   C.c_float(-8), C.c_float(7), 1, 128, C.c_void_p(16), C.c_void_p(16),
+                                   C.c_void_p(16), 1 << 20, None), "not supported for GPTQ"),
+    (lambda l: l.mi355q_calculate_qparams(C.c_void_p(16), C.c_void_p(16), 4, C.c_float(0), C.c_float(7), 1, 0, 0,
+                                          C.c_void_p(16), C.c_void_p(16), None), "straddle zero"),
+])
+def test_invalid_arguments_are_rejected_on_the_host(call, needle):
+    lib = _lib.load_library()
+    assert call(lib) == _lib.INVALID_ARGUMENT
+    assert needle in lib.mi355q_last_error().decode()
+
+
+def test_hessian_grouped_rejects_decreasing_offsets():
+    lib = _lib.load_library()
+    off = (C.c_int64 * 3)(0, 5, 3)
+    rc = lib.mi355q_hessian_grouped_syrk_bf16(C.c_void_p(16), 8, 8, C.c_void_p(16), off, 2, C.c_void_p(16), 64,
+                                              C.c_float(2.0), None, 0, None)
+    assert rc == _lib.INVALID_ARGUMENT and "non-decreasing" in lib.mi355q_last_error().decode()

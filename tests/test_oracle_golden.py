@@ -1,0 +1,203 @@
+"""Pin the CPU oracle against the reference's own known-answer tests and
+against what the mathematics fixes (CPU only)."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fake_quant as ofq
+from oracle import moe as omoe
+from oracle import observers as oobs
+from oracle import pack as opack
+from oracle.qargs import OArgs
+
+GOLD = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+
+
+def _args(d):
+    d = dict(d)
+    if d.get("scale_dtype") == "float8_e4m3fn":
+        d["scale_dtype"] = torch.float8_e4m3fn
+    return OArgs(**d)
+
+
+@pytest.mark.parametrize("case", GOLD["static_weight_quantization"]["cases"],
+                         ids=lambda c: c["args"]["strategy"])
+def test_static_weight_quantization_table(case):
+    """test_lifecycle.py:16-165 - observer stats + fake-quant forward."""
+    args = _args(case["args"])
+    w = torch.arange(24, dtype=torch.bfloat16).reshape(4, 6)
+    obs = oobs.OMinMax("memoryless_minmax", "weight", args)
+    obs(w)
+    assert torch.equal(obs.min_vals.float(), torch.tensor(case["min"], dtype=torch.float32))
+    assert torch.equal(obs.max_vals.float(), torch.tensor(case["max"], dtype=torch.float32))
+    qp = obs.get_qparams()
+    out = ofq.fake_quantize_weight(w, qp["scale"], qp["zero_point"], args, qp["global_scale"])
+    exp = torch.tensor(case["quant"], dtype=torch.bfloat16)
+    # the reference compares the bf16 forward output with allclose at default tolerances
+    assert torch.allclose(out.float(), exp.float())
+    assert torch.nn.functional.mse_loss(out.float(), w.float()) <= case["loss"]
+
+
+def test_static_activation_quantization_table():
+    """test_lifecycle.py:168-273 (int tensor row)."""
+    case = GOLD["static_activation_quantization"]["cases"][0]
+    args = _args(case["args"])
+    x = torch.arange(12, dtype=torch.bfloat16).reshape(1, 2, 6)
+    obs = oobs.OMinMax("memoryless_minmax", "input", args)
+    obs(x)
+    assert torch.equal(obs.min_vals.float(), torch.tensor(case["min"]))
+    assert torch.equal(obs.max_vals.float(), torch.tensor(case["max"]))
+    qp = obs.get_qparams()
+    out = ofq.fake_quantize(x, qp["scale"], qp["zero_point"], args)
+    # the reference converts the 4-decimal table to the output dtype (bf16) first
+    assert torch.allclose(out.float(), torch.tensor(case["quant"]).to(torch.bfloat16).float())
+
+
+@pytest.mark.parametrize("case", GOLD["min_max_observer"]["cases"], ids=lambda c: str(c["symmetric"]))
+def test_min_max_observer_scale(case):
+    """test_min_max.py:8-29."""
+    args = OArgs(num_bits=8, symmetric=case["symmetric"])
+    obs = oobs.OMinMax("memoryless_minmax", "weight", args)
+    qp = obs(torch.tensor(GOLD["min_max_observer"]["input"])).get_qparams()
+    assert round(qp["scale"].item(), 4) == case["scale"]
+    assert round(qp["zero_point"].item(), 4) == case["zero_point"]
+
+
+def test_min_max_value_update():
+    """test_min_max.py:49-86 (moving average, base 'input')."""
+    g = GOLD["min_max_value_update"]
+    obs = oobs.OMinMax("minmax", "input", OArgs(num_bits=8, strategy="tensor"))
+    cmax = cmin = 1
+    for t, emax, emin in zip(g["inputs"], g["expected_running_max_after"], g["expected_running_min_after"]):
+        obs(torch.tensor(t))
+        cmax = max(obs.max_vals[0].item(), cmax)
+        cmin = min(obs.min_vals[0].item(), cmin)
+        assert abs(cmax - emax) < 1e-6 and abs(cmin - emin) < 1e-6
+
+
+@pytest.mark.parametrize("case", GOLD["observer_min_max_vals"]["cases"], ids=lambda c: c["name"])
+def test_observer_min_max_vals(case):
+    """test_observers.py:66-123."""
+    obs = oobs.OMinMax(case["name"], "input", OArgs(strategy="tensor", observer_kwargs=case["kwargs"]))
+    mins, maxs = [], []
+    for o in GOLD["observer_min_max_vals"]["observed"]:
+        obs(torch.tensor(o))
+        mins.append(obs.min_vals)
+        maxs.append(obs.max_vals)
+    assert torch.allclose(torch.stack(mins), torch.tensor(case["min"]))
+    assert torch.allclose(torch.stack(maxs), torch.tensor(case["max"]))
+
+
+def test_strict_symmetric():
+    """test_strict_symmetric.py:13-71."""
+    g = GOLD["strict_symmetric"]
+    args = OArgs(num_bits=8, strategy="channel")
+    obs = oobs.OMinMax("strict_symmetric_minmax", "weight", args)
+    qp = obs(torch.tensor(g["observed"], dtype=torch.float32)).get_qparams()
+    assert qp["scale"].dtype == torch.float32
+    assert qp["scale"].flatten().tolist() == pytest.approx(g["scale"])
+    obs2 = oobs.OMinMax("strict_symmetric_minmax", "weight", args)
+    assert obs2(torch.zeros(2, 3)).get_qparams()["scale"].flatten().tolist() == pytest.approx(g["zeros_scale"])
+
+
+def test_pack_int4_to_int8_table():
+    """test_pack_int4_to_int8.py:25-46."""
+    g = GOLD["pack_int4_to_int8"]
+    out = opack.pack_int4_to_int8(np.array(g["input"], dtype=np.int8))
+    assert np.array_equal(out, np.array(g["expected"], dtype=np.int8))
+    with pytest.raises(ValueError, match=g["odd_error"]):
+        opack.pack_int4_to_int8(np.array(g["odd_input"], dtype=np.int8))
+
+
+def test_linear_experts_routing_counts():
+    """test_linear_experts.py:12-100."""
+    g = GOLD["linear_experts_routing"]
+    idx = torch.tensor(g["top_k_index"])
+    routed = omoe.expert_token_lists(idx, g["num_experts"], False, g["num_tokens"])
+    assert all(len(r) == g["routed_tokens_per_expert"] for r in routed)
+    alls = omoe.expert_token_lists(idx, g["num_experts"], True, g["num_tokens"])
+    assert all(len(r) == g["calibrate_all_tokens_per_expert"] for r in alls)
+
+
+# ---------------------------------------------------------------- math pins
+def _all_finite_bf16():
+    b = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    f = (b.astype(np.uint32) << 16).view(np.float32)
+    return b[np.isfinite(f)]
+
+
+def test_cast_to_fp4_is_nearest_ties_even_brute_force():
+    """cast_to_fp4 == nearest e2m1 grid point, ties to the even mantissa, for every bf16 in [-6, 6]."""
+    bits = _all_finite_bf16()
+    x = torch.from_numpy((bits.astype(np.uint32) << 16).view(np.float32).copy())
+    x = x[(x.abs() <= 6)]
+    got = ofq.cast_to_fp4(x)
+    grid = torch.tensor(ofq.FP4_GRID)
+    a = x.abs()
+    dist = (a.unsqueeze(1) - grid.unsqueeze(0)).abs()
+    best = dist.min(dim=1).values
+    cand = dist == best.unsqueeze(1)
+    # even mantissa: grid indices 0,2,4,6 (0, 1, 2, 4) win ties
+    even = torch.tensor([1, 0, 1, 0, 1, 0, 1, 0], dtype=torch.bool)
+    pick = torch.where((cand & even).any(1), (cand & even).float().argmax(1), cand.float().argmax(1))
+    exp = grid[pick] * torch.sign(x)
+    assert torch.equal(got, exp)
+
+
+def test_mxfp4_numpy_matches_torch_fake_quant_path():
+    """The numpy byte packer and the torch observer + cast_to_fp4 path agree."""
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(64, 256, generator=g) * torch.exp(torch.randn(64, 1, generator=g) * 3)).to(torch.bfloat16)
+    x[0, :32] = 0
+    x[1, :32] = -0.0
+    x[2, 5] = 1e-30
+    bits = x.view(torch.int16).numpy().view(np.uint16)
+    for rule in ("ct", "ocp"):
+        codes, e8 = opack.mxfp4_quantize_pack(bits, rule)
+        args = OArgs(num_bits=4, type="float", strategy="group", group_size=32, is_mx=True)
+        obs = oobs.OMinMax("memoryless_minmax", "weight", args)
+        qp = obs(x).get_qparams(mx_rule=rule)
+        deq = ofq.fake_quantize_weight(x.float(), qp["scale"], None, args)
+        back = opack.mxfp4_unpack(codes, e8)
+        assert np.array_equal(back, deq.numpy()), rule
+        assert np.array_equal(oobs.mx_scale_exponent(
+            torch.max(obs_abs := x.float().abs().reshape(64, 8, 32), dim=2).values, rule).numpy(), e8.astype(np.int32))
+        del obs_abs
+
+
+def test_mx_scale_rules_bound_the_group():
+    """OCP: amax / scale in [4, 8); CT rule: amax / scale in [3.5, 7)."""
+    bits = _all_finite_bf16()
+    bits = bits[(bits & 0x7FFF) != 0]
+    amax = torch.from_numpy((bits.astype(np.uint32) << 16).view(np.float32).copy()).abs()
+    amax = amax[(amax > 2.0 ** -100) & (amax < 2.0 ** 100)]
+    for rule, lo, hi in (("ocp", 4.0, 8.0), ("ct", 3.5, 7.0)):
+        s = oobs.e8m0_to_float(oobs.mx_scale_exponent(amax, rule))
+        r = amax / s
+        assert bool(((r >= lo) & (r < hi)).all()), rule
+
+
+def test_int32_pack_known_vector_and_round_trip():
+    codes = np.array([[-8, -7, -1, 0, 1, 2, 6, 7]], dtype=np.int8)
+    # offset-binary nibbles 0,1,7,8,9,10,14,15 at bits 0,4,...,28
+    exp = np.array([0xFEA98710], dtype=np.uint32).view(np.int32)
+    assert np.array_equal(opack.pack_to_int32(codes), exp.reshape(1, 1))
+    r = np.random.default_rng(0).integers(-8, 8, size=(16, 64)).astype(np.int8)
+    assert np.array_equal(opack.unpack_from_int32(opack.pack_to_int32(r), 64), r)
+
+
+def test_fp8_cast_is_torch_rne():
+    x = torch.tensor([464.0, 448.0, 1.5 * 2 ** -10, -0.0, 2 ** -10])
+    args = OArgs(num_bits=8, type="float")
+    q = ofq.round_to_type(x, args, -448.0, 448.0)
+    assert q.tolist()[:3] == [448.0, 448.0, 2 ** -9]
+    assert torch.signbit(q[3])
+
+
+def test_int_round_half_even_and_clamp():
+    args = OArgs(num_bits=4)
+    q = ofq.quantize(torch.tensor([0.5, 1.5, 2.5, -0.5, 7.6, -9.0]), torch.tensor(1.0), None, args)
+    assert q.tolist() == [0.0, 2.0, 2.0, -0.0, 7.0, -8.0]

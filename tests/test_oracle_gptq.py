@@ -1,0 +1,156 @@
+"""Pin the GPTQ oracle (Hessian, Cholesky chain, sweep) by mathematics (CPU only)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gptq as og
+from oracle.observers import OMinMax
+from oracle.qargs import OArgs
+
+
+def _x(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * torch.exp(torch.randn(shape[-1], generator=g))).to(torch.bfloat16)
+
+
+def test_hessian_closed_form_and_sample_count():
+    x = _x((3, 50, 16), 0)
+    H = og.make_empty_hessian(16)
+    n = torch.zeros(())
+    H, n = og.accumulate_hessian(x, H, n)
+    assert n.item() == 3
+    x2 = _x((7, 16), 1)
+    H, n = og.accumulate_hessian(x2, H, n)          # 2-D input counts as one sample
+    assert n.item() == 4
+    xs = torch.cat([x.reshape(-1, 16), x2]).double()
+    exact = 2.0 * xs.t() @ xs
+    rel = ((H.double() - exact).norm() / exact.norm()).item()
+    assert rel < 1e-6
+    assert torch.equal(H, H.t())
+
+
+def _spd(d, seed, tokens=None):
+    x = _x((tokens or 4 * d, d), seed).float()
+    return x.t() @ x / x.shape[0]
+
+
+def test_cholesky_chain_identity_and_fp64():
+    H = _spd(64, 2)
+    U, ok = og.cholesky_chain(H, 0.01)
+    assert ok
+    assert torch.equal(U, torch.triu(U))
+    Hd = H.double() + 0.01 * torch.mean(torch.diag(H.double())) * torch.eye(64, dtype=torch.float64)
+    I = U.double().t() @ U.double() @ Hd
+    assert (I - torch.eye(64, dtype=torch.float64)).abs().max().item() < 1e-3
+    U64 = torch.linalg.cholesky(torch.linalg.inv(Hd), upper=True)
+    assert ((U.double() - U64).norm() / U64.norm()).item() < 1e-4
+
+
+def test_cholesky_chain_non_pd_falls_back_to_identity():
+    H = _spd(16, 3)
+    H[5, 5] = -50.0
+    U, ok = og.cholesky_chain(H, 0.0)
+    assert not ok and torch.equal(U, torch.eye(16))
+
+
+def _weight(r, c, seed):
+    return (torch.randn(r, c, generator=torch.Generator().manual_seed(seed)) * 0.02).to(torch.bfloat16)
+
+
+def test_diagonal_hessian_is_round_to_nearest():
+    """Diagonal H -> diagonal Hinv -> no cross-column error feedback -> GPTQ == RTN."""
+    W = _weight(12, 64, 4)
+    H = torch.diag(torch.arange(1, 65, dtype=torch.float32))
+    args = OArgs(num_bits=4, strategy="group", group_size=16)
+    _, out, ex = og.quantize_weight(W, args, H, return_codes=True)
+    s = ex["scale_used"].float().repeat_interleave(16, 1)
+    rtn = torch.clamp(torch.round(W.float() / s), -8, 7).to(torch.int32)
+    assert torch.equal(ex["codes"], rtn)
+
+
+def test_blocksize_invariance():
+    W = _weight(16, 48, 5)
+    H = _spd(48, 6)
+    args = OArgs(num_bits=4, strategy="group", group_size=16)
+    outs = [og.quantize_weight(W, args, H, blocksize=b, return_codes=True) for b in (3, 16, 128)]
+    for o in outs[1:]:
+        assert torch.equal(o[2]["codes"], outs[0][2]["codes"])
+        assert abs(o[0] - outs[0][0]) <= 1e-4 * abs(outs[0][0]) + 1e-9
+
+
+def _obq_fp64(W, H, scale, qmin, qmax, percdamp=0.01):
+    """Optimal Brain Quantization with explicit inverse downdates, fp64, column order.
+
+    After quantizing the first remaining column q, the remaining weights move by
+    -(w_q - q) / [H_F^-1]_qq * [H_F^-1]_{q, :} with H_F the Hessian restricted
+    to the not-yet-quantized columns (recomputed by a full inverse each step).
+    """
+    W = W.astype(np.float64).copy()
+    r, c = W.shape
+    Hd = H.astype(np.float64) + percdamp * np.mean(np.diag(H)) * np.eye(c)
+    codes = np.zeros((r, c), dtype=np.int64)
+    for i in range(c):
+        F = list(range(i, c))
+        Hi = np.linalg.inv(Hd[np.ix_(F, F)])
+        w = W[:, i]
+        q = np.clip(np.round(w / scale[:, i]), qmin, qmax)
+        codes[:, i] = q
+        deq = q * scale[:, i]
+        W[:, i + 1:] -= np.outer((w - deq) / Hi[0, 0], Hi[0, 1:])
+    return codes
+
+
+def test_sweep_matches_brute_force_obq_fp64():
+    W = _weight(32, 24, 7)
+    H = _spd(24, 8, tokens=200)
+    args = OArgs(num_bits=4, strategy="channel")
+    _, _, ex = og.quantize_weight(W, args, H, blocksize=8, return_codes=True,
+                                  dequant_in_scale_dtype=False)
+    s = ex["scale_used"].float().expand(32, 24).double().numpy()
+    ref = _obq_fp64(W.float().numpy(), H.numpy(), s, -8, 7)
+    agree = (ex["codes"].numpy() == ref).mean()
+    assert agree >= 0.99 and np.abs(ex["codes"].numpy() - ref).max() <= 1
+
+
+@pytest.mark.parametrize("actorder", [None, "weight", "group"])
+def test_shapes_group_actorder(actorder):
+    """test_gptq_quantize.py:21-60."""
+    W = _weight(6, 8, 9)
+    H = torch.diag(torch.arange(1, 9, dtype=torch.float32))
+    args = OArgs(num_bits=4, strategy="group", group_size=2, actorder=actorder)
+    loss, q = og.quantize_weight(W, args, H)
+    assert loss >= 0
+    assert q["weight"].shape == W.shape
+    assert q["weight_scale"].shape == (6, 4) and q["weight_zero_point"].shape == (6, 4)
+    assert ("weight_g_idx" in q) == (actorder == "group")
+    if actorder == "group":
+        assert q["weight_g_idx"].shape == (8,)
+
+
+@pytest.mark.parametrize("actorder", [None, "weight"])
+def test_shapes_block_strategy(actorder):
+    """test_gptq_quantize.py:63-97."""
+    W = _weight(5, 7, 10)
+    args = OArgs(num_bits=8, strategy="block", block_structure=[2, 4], actorder=actorder)
+    loss, q = og.quantize_weight(W, args, torch.eye(7), blocksize=3)
+    assert loss >= 0 and q["weight"].shape == W.shape
+    assert q["weight_scale"].shape == (3, 2) and "weight_g_idx" not in q
+
+
+def test_channel_actorder_weight():
+    """test_gptq_quantize.py:100-132."""
+    W = _weight(4, 8, 11)
+    args = OArgs(num_bits=4, strategy="channel", actorder="weight")
+    loss, q = og.quantize_weight(W, args, torch.diag(torch.arange(1, 9, dtype=torch.float32)), blocksize=4)
+    assert loss >= 0 and q["weight"].shape == W.shape and q["weight_scale"].shape[0] == 4
+    assert "weight_g_idx" not in q
+
+
+def test_dead_columns_are_zeroed():
+    W = _weight(8, 16, 12)
+    H = _spd(16, 13)
+    H[3, :] = 0
+    H[:, 3] = 0
+    args = OArgs(num_bits=4, strategy="channel")
+    _, q, ex = og.quantize_weight(W, args, H, return_codes=True)
+    assert torch.all(q["weight"][:, 3] == 0) and torch.all(ex["codes"][:, 3] == 0)
