@@ -42,9 +42,21 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
     int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out) {
   __shared__ float h1[MAXB * MAXB];
   const int tid = threadIdx.x;
-  for (int e = tid; e < count * count; e += SW_NT) {
-    const int i = e / count, j = e % count;
-    if (j >= i) h1[i * MAXB + j] = hinv[(i1 + i) * cols + (i1 + j)];
+  if (count == MAXB && (cols & 3) == 0 && (reinterpret_cast<uintptr_t>(hinv) & 15) == 0) {
+    // 16 independent 16-byte loads per thread (lower-triangle chunks skipped)
+#pragma unroll
+    for (int v = 0; v < MAXB * MAXB / 4 / SW_NT; ++v) {
+      const int e = v * SW_NT + tid;
+      const int i = e >> 5, j4 = (e & 31) * 4;
+      if (j4 + 3 >= i)
+        *reinterpret_cast<f32x4_t*>(h1 + i * MAXB + j4) =
+            *reinterpret_cast<const f32x4_t*>(hinv + (i1 + i) * cols + i1 + j4);
+    }
+  } else {
+    for (int e = tid; e < count * count; e += SW_NT) {
+      const int i = e / count, j = e % count;
+      if (j >= i) h1[i * MAXB + j] = hinv[(i1 + i) * cols + (i1 + j)];
+    }
   }
   __syncthreads();
 

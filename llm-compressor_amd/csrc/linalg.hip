@@ -53,8 +53,11 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
   f32x4_t ra[4], rb[4];
+  const bool vec_a = ((reinterpret_cast<uintptr_t>(A) & 15) == 0) && ((g.lda & 3) == 0);
+  const bool vec_b = ((reinterpret_cast<uintptr_t>(B) & 15) == 0) && ((g.ldb & 3) == 0);
   // A / B^T tiles: 128 rows x 32 k -> 1024 float4 (4 per thread)
-  auto load_mk = [&](const float* P, int64_t ld, int64_t rows_lim, int64_t r0, int64_t k0, f32x4_t* r) {
+  auto load_mk = [&](const float* P, int64_t ld, bool vec, int64_t rows_lim, int64_t r0, int64_t k0,
+                     f32x4_t* r) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int idx = v * GNT + tid;
@@ -63,9 +66,13 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
       f32x4_t x = {0.f, 0.f, 0.f, 0.f};
       if (gr < rows_lim) {
         const float* src = P + gr * ld + gk;
+        if (vec && gk + 3 < g.K) {
+          x = *reinterpret_cast<const f32x4_t*>(src);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (gk + e < g.K) x[e] = src[e];
+          for (int e = 0; e < 4; ++e)
+            if (gk + e < g.K) x[e] = src[e];
+        }
       }
       r[v] = x;
     }
@@ -89,9 +96,13 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
       f32x4_t x = {0.f, 0.f, 0.f, 0.f};
       if (gk < g.K) {
         const float* src = B + gk * g.ldb + gn;
+        if (vec_b && gn + 3 < g.N) {
+          x = *reinterpret_cast<const f32x4_t*>(src);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (gn + e < g.N) x[e] = src[e];
+          for (int e = 0; e < 4; ++e)
+            if (gn + e < g.N) x[e] = src[e];
+        }
       }
       r[v] = x;
     }
@@ -107,8 +118,8 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
 
   const int64_t nst = (g.K + GBK - 1) / GBK;
   if (nst > 0) {
-    load_mk(A, g.lda, g.M, m0, 0, ra);
-    if (BT) load_mk(B, g.ldb, g.N, n0, 0, rb); else load_kn(0, rb);
+    load_mk(A, g.lda, vec_a, g.M, m0, 0, ra);
+    if (BT) load_mk(B, g.ldb, vec_b, g.N, n0, 0, rb); else load_kn(0, rb);
     store_mk(lds_a[0], ra);
     if (BT) store_mk(lds_b[0], rb); else store_kn(lds_b[0], rb);
   }
@@ -117,8 +128,8 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
     const int buf = st & 1;
     const bool more = st + 1 < nst;
     if (more) {
-      load_mk(A, g.lda, g.M, m0, (st + 1) * GBK, ra);
-      if (BT) load_mk(B, g.ldb, g.N, n0, (st + 1) * GBK, rb); else load_kn((st + 1) * GBK, rb);
+      load_mk(A, g.lda, vec_a, g.M, m0, (st + 1) * GBK, ra);
+      if (BT) load_mk(B, g.ldb, vec_b, g.N, n0, (st + 1) * GBK, rb); else load_kn((st + 1) * GBK, rb);
     }
     const float* la = lds_a[buf];
     const float* lb = lds_b[buf];
@@ -164,69 +175,194 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
 
 // ---------------------------------------------------------------- Cholesky pieces
 constexpr int NB = 128;        // panel width
-constexpr int PNT = 512;       // threads of the diagonal-block kernel
+constexpr int SB = 32;         // register-resident sub-block of the diagonal kernel
+constexpr int PNT = 256;       // threads of the diagonal-block kernel (4 waves)
 constexpr int LP = NB + 1;     // LDS row stride
+constexpr int LT = 2 * SB + 1; // LDS row stride of the product scratch
+
+__device__ __forceinline__ float rdlane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// acc += sum_k A[m][k] * op(B)[k][n] over a 32 x 32 tile, operands in LDS
+// (A row-major lda; B row-major [k][n] (ldb) or, if bt, [n][k]).  K even.
+__device__ __forceinline__ void lds_mfma_tile(f32x16_t& acc, const float* A, int lda, const float* B, int ldb,
+                                              bool bt, int K, int lane, float sign) {
+  for (int k2 = 0; k2 < K; k2 += 2) {
+    const int k = k2 + (lane >> 5);
+    const float av = sign * A[(lane & 31) * lda + k];
+    const float bv = bt ? B[(lane & 31) * ldb + k] : B[k * ldb + (lane & 31)];
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void tile_load(f32x16_t& acc, const float* C, int ldc, int lane) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = C[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ldc + (lane & 31)];
+}
+__device__ __forceinline__ void tile_store(const f32x16_t& acc, float* C, int ldc, int lane) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) C[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ldc + (lane & 31)] = acc[r];
+}
 
 // Lower Cholesky of the NB x NB diagonal block at (k0, k0) of F (in place,
 // lower triangle) and its inverse into linv (NB x NB, zeros above the
-// diagonal).  nb <= NB is the block size (smaller for the last block).
+// diagonal).  nb <= NB is the block size; rows / columns beyond nb are padded
+// with the identity so the whole NB block factors uniformly.
+//
+// The block is processed in 32-wide steps.  Wave 0 factors and inverts the
+// 32 x 32 diagonal sub-block in registers (lane i holds row i; values of
+// other rows arrive by readlane, so no workgroup barrier is needed inside
+// the step); then all four waves apply the sub-block inverse to the panel
+// below and update the trailing lower triangle with fp32 MFMA.  The block
+// inverse is assembled from the four sub-block inverses by two doubling
+// steps, inv([[A,0],[B,C]]) = [[A^-1,0],[-C^-1 B A^-1, C^-1]].
 __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, int64_t k0, int nb,
                                                         float* linv, int32_t* status) {
   __shared__ float a[NB * LP];
   __shared__ float x[NB * LP];
-  const int tid = threadIdx.x;
-  for (int e = tid; e < NB * NB; e += PNT) {
+  __shared__ float t[2 * SB * LT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // load: 64 independent loads per thread in flight
+#pragma unroll 16
+  for (int v = 0; v < NB * NB / PNT; ++v) {
+    const int e = v * PNT + tid;
     const int i = e / NB, j = e % NB;
-    float v = 0.f;
-    if (i < nb && j <= i) v = F[(k0 + i) * ldf + (k0 + j)];
-    a[i * LP + j] = v;
-    x[i * LP + j] = (i == j) ? 1.f : 0.f;
+    float val = (i == j) ? 1.f : 0.f;
+    if (i < nb && j < nb && j <= i) val = F[(k0 + i) * ldf + (k0 + j)];
+    a[i * LP + j] = val;
+    x[i * LP + j] = 0.f;
   }
   __syncthreads();
+
   bool bad = false;
-  for (int j = 0; j < nb; ++j) {
-    float piv = a[j * LP + j];
-    if (!(piv > 0.f) || !isfinite(piv)) {
-      bad = true;
-      piv = 1.f;
+  for (int kb = 0; kb < NB / SB; ++kb) {
+    const int o = kb * SB;
+    if (wave == 0) {
+      const int row = o + (lane & 31);
+      float r[SB], q[SB];
+#pragma unroll
+      for (int c = 0; c < SB; ++c) {
+        r[c] = a[row * LP + o + c];
+        q[c] = (c == (lane & 31)) ? 1.f : 0.f;
+      }
+      // right-looking Cholesky of the sub-block
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        float piv = rdlane(r[j], j);
+        if (!(piv > 0.f) || !isfinite(piv)) {
+          bad = true;
+          piv = 1.f;
+        }
+        const float ljj = sqrtf(piv);
+        const float inv = 1.f / ljj;
+        r[j] = (lane == j) ? ljj : ((lane > j) ? r[j] * inv : r[j]);
+#pragma unroll
+        for (int c = j + 1; c < SB; ++c) {
+          const float s = rdlane(r[j], c);
+          if (lane >= c) r[c] = fmaf(-r[j], s, r[c]);
+        }
+      }
+      // inverse by row elimination of [L | I]: lane i holds row i of L^-1
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const float ljj = rdlane(r[j], j);
+        if (lane == j) {
+#pragma unroll
+          for (int c = 0; c <= j; ++c) q[c] = q[c] / ljj;
+        }
+#pragma unroll
+        for (int c = 0; c <= j; ++c) {
+          const float s = rdlane(q[c], j);
+          if (lane > j) q[c] = fmaf(-r[j], s, q[c]);
+        }
+      }
+      if (lane < SB) {
+#pragma unroll
+        for (int c = 0; c < SB; ++c) {
+          if (c <= lane) {
+            a[row * LP + o + c] = r[c];
+            x[row * LP + o + c] = q[c];
+          }
+        }
+      }
     }
-    const float ljj = sqrtf(piv);
     __syncthreads();
-    for (int i = j + 1 + tid; i < nb; i += PNT) a[i * LP + j] = a[i * LP + j] / ljj;
-    if (tid == 0) a[j * LP + j] = ljj;
-    __syncthreads();
-    // rank-1 update of the trailing lower triangle: rows i > j, cols j < c <= i
-    const int m = nb - 1 - j;
-    const int cnt = m * (m + 1) / 2;
-    for (int e = tid; e < cnt; e += PNT) {
-      // e -> (ii, cc) with 0 <= cc <= ii < m
-      int ii = (int)((sqrtf(8.f * e + 1.f) - 1.f) * 0.5f);
-      while ((ii + 1) * (ii + 2) / 2 <= e) ++ii;
-      while (ii * (ii + 1) / 2 > e) --ii;
-      const int cc = e - ii * (ii + 1) / 2;
-      const int i = j + 1 + ii, c = j + 1 + cc;
-      a[i * LP + c] = a[i * LP + c] - a[i * LP + j] * a[c * LP + j];
+    // panel below the sub-block: P = A_panel * Xd^T (in place, one 32-row tile per wave)
+    const int ntile = (NB - o - SB) / SB;
+    if (wave < ntile) {
+      f32x16_t acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+      float* ap = a + (o + SB + SB * wave) * LP + o;
+      lds_mfma_tile(acc, ap, LP, x + o * LP + o, LP, true, SB, lane, 1.f);
+      tile_store(acc, ap, LP, lane);
     }
-    __syncthreads();  // updates of step j complete before step j+1 reads its pivot
+    __syncthreads();
+    // trailing lower tiles: A[ti][tj] -= P_ti P_tj^T for tj <= ti
+    const int ntt = ntile * (ntile + 1) / 2;
+    for (int tt = wave; tt < ntt; tt += PNT / 64) {
+      int ti = 0, rem = tt;
+      while (rem > ti) { rem -= ti + 1; ++ti; }
+      const int tj = rem;
+      float* cp = a + (o + SB + SB * ti) * LP + (o + SB + SB * tj);
+      f32x16_t acc;
+      tile_load(acc, cp, LP, lane);
+      lds_mfma_tile(acc, a + (o + SB + SB * ti) * LP + o, LP, a + (o + SB + SB * tj) * LP + o, LP, true, SB,
+                    lane, -1.f);
+      tile_store(acc, cp, LP, lane);
+    }
+    __syncthreads();
   }
-  if (bad && status && tid == 0) *status = MI355Q_NOT_POSITIVE_DEFINITE;
+  if (wave == 0 && lane == 0 && bad && status) *status = MI355Q_NOT_POSITIVE_DEFINITE;
+
+  // block inverse from the four 32 x 32 inverses
+  // level 1: pairs (0,1) and (2,3)
+  if (wave < 2) {
+    const int a0 = 2 * SB * wave, c0 = a0 + SB;
+    f32x16_t acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    lds_mfma_tile(acc, a + c0 * LP + a0, LP, x + a0 * LP + a0, LP, false, SB, lane, 1.f);
+    tile_store(acc, t + SB * wave * LT, LT, lane);
+  }
   __syncthreads();
-  // inverse: X = L^-1 by row elimination of [L | I]
-  for (int j = 0; j < nb; ++j) {
-    const float ljj = a[j * LP + j];
-    for (int c = tid; c <= j; c += PNT) x[j * LP + c] = x[j * LP + c] / ljj;
-    __syncthreads();
-    const int rows = nb - 1 - j, colsn = j + 1;
-    for (int e = tid; e < rows * colsn; e += PNT) {
-      const int i = j + 1 + e / colsn, c = e % colsn;
-      x[i * LP + c] = x[i * LP + c] - a[i * LP + j] * x[j * LP + c];
-    }
-    __syncthreads();
+  if (wave < 2) {
+    const int a0 = 2 * SB * wave, c0 = a0 + SB;
+    f32x16_t acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    lds_mfma_tile(acc, x + c0 * LP + c0, LP, t + SB * wave * LT, LT, false, SB, lane, -1.f);
+    tile_store(acc, x + c0 * LP + a0, LP, lane);
   }
-  for (int e = tid; e < NB * NB; e += PNT) {
+  __syncthreads();
+  // level 2: T = L[64:128, 0:64] X[0:64, 0:64]; X[64:128, 0:64] = -X[64:128, 64:128] T
+  {
+    const int ti = wave >> 1, tj = wave & 1;
+    f32x16_t acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    lds_mfma_tile(acc, a + (2 * SB + SB * ti) * LP, LP, x + SB * tj, LP, false, 2 * SB, lane, 1.f);
+    tile_store(acc, t + SB * ti * LT + SB * tj, LT, lane);
+  }
+  __syncthreads();
+  {
+    const int ti = wave >> 1, tj = wave & 1;
+    f32x16_t acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    lds_mfma_tile(acc, x + (2 * SB + SB * ti) * LP + 2 * SB, LP, t + SB * tj, LT, false, 2 * SB, lane, -1.f);
+    tile_store(acc, x + (2 * SB + SB * ti) * LP + SB * tj, LP, lane);
+  }
+  __syncthreads();
+
+#pragma unroll 16
+  for (int v = 0; v < NB * NB / PNT; ++v) {
+    const int e = v * PNT + tid;
     const int i = e / NB, j = e % NB;
     if (i < nb && j <= i) F[(k0 + i) * ldf + (k0 + j)] = a[i * LP + j];
-    linv[i * NB + j] = (i < nb && j <= i) ? x[i * LP + j] : 0.f;
+    linv[e] = (j <= i) ? x[i * LP + j] : 0.f;
   }
 }
 
