@@ -80,10 +80,14 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
   }
 
   float loss = 0.f;
+  // column i = SW_G * to + go; `to` is a compile-time register slot (outer
+  // loop unrolled), `go` the owner lane (inner loop, runtime), so no
+  // register array is ever indexed dynamically
 #pragma unroll
-  for (int i = 0; i < MAXB; ++i) {
-    if (i >= count) continue;  // count is uniform; keeps the loop fully unrollable
-    const int to = i / SW_G, go = i % SW_G;
+  for (int to = 0; to < SW_T; ++to) {
+  for (int go = 0; go < SW_G; ++go) {
+    const int i = SW_G * to + go;
+    if (i >= count) break;
     const float x = __shfl(w[to], go, SW_G);
     const float sc = __shfl(s[to], go, SW_G);
     const float zz = __shfl(z[to], go, SW_G);
@@ -105,6 +109,7 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
       const int col = SW_G * t + g;
       if (col > i && col < count) w[t] = w[t] - err * h1[i * MAXB + col];
     }
+  }
   }
 
   if (live) {

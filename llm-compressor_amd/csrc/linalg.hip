@@ -247,7 +247,9 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
         r[c] = a[row * LP + o + c];
         q[c] = (c == (lane & 31)) ? 1.f : 0.f;
       }
-      // right-looking Cholesky of the sub-block
+      // right-looking Cholesky of the sub-block.  Entries above the diagonal
+      // (c > lane) are updated too: they are never read into the lower
+      // triangle, which keeps every update unpredicated.
 #pragma unroll
       for (int j = 0; j < SB; ++j) {
         float piv = rdlane(r[j], j);
@@ -257,26 +259,20 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
         }
         const float ljj = sqrtf(piv);
         const float inv = 1.f / ljj;
-        r[j] = (lane == j) ? ljj : ((lane > j) ? r[j] * inv : r[j]);
+        r[j] = (lane == j) ? ljj : r[j] * inv;
 #pragma unroll
-        for (int c = j + 1; c < SB; ++c) {
-          const float s = rdlane(r[j], c);
-          if (lane >= c) r[c] = fmaf(-r[j], s, r[c]);
-        }
+        for (int c = j + 1; c < SB; ++c) r[c] = fmaf(-r[j], rdlane(r[j], c), r[c]);
       }
-      // inverse by row elimination of [L | I]: lane i holds row i of L^-1
+      // inverse by row elimination of [L | I]: lane i holds row i of L^-1;
+      // rows above j are final, so their multiplier is zero
 #pragma unroll
       for (int j = 0; j < SB; ++j) {
-        const float ljj = rdlane(r[j], j);
-        if (lane == j) {
+        const float fac = (lane == j) ? 1.f / rdlane(r[j], j) : 1.f;
 #pragma unroll
-          for (int c = 0; c <= j; ++c) q[c] = q[c] / ljj;
-        }
+        for (int c = 0; c <= j; ++c) q[c] *= fac;
+        const float m = (lane > j) ? r[j] : 0.f;
 #pragma unroll
-        for (int c = 0; c <= j; ++c) {
-          const float s = rdlane(q[c], j);
-          if (lane > j) q[c] = fmaf(-r[j], s, q[c]);
-        }
+        for (int c = 0; c <= j; ++c) q[c] = fmaf(-m, rdlane(q[c], j), q[c]);
       }
       if (lane < SB) {
 #pragma unroll
