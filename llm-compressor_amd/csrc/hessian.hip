@@ -6,17 +6,22 @@
 // contraction runs over tokens, so both MFMA operands need token-contiguous
 // fragments: each thread loads an 8-token x 8-feature block with eight
 // 16-byte loads and transposes it in registers (v_perm) before the LDS
-// store.  bf16 x bf16 products are exact in fp32 and accumulate in fp32.
+// store.  bf16 x bf16 products are exact in fp32 and accumulate in fp32
+// (v_mfma_f32_32x32x16_bf16).
+//
+// Tiles are TM x TM (TM = 256 for d >= 512, else 128) on a 2 x 2 grid of
+// waves; each wave owns a (TM/2)^2 block of 32 x 32 MFMA tiles, so one 16-token
+// step issues (TM/64)^2 MFMAs per TM/16 fragment reads.  The transposed
+// stores map lane -> (feature block, token block) with the token block
+// fastest, which keeps 16 consecutive lanes on distinct LDS banks
+// (row stride 144 B = 9 x 16 B).
 //
 // Work decomposition: a work item is (matrix e, upper tile t, token split s).
 // Token splits are assigned by blockIdx % S, and workgroups are dispatched
 // round-robin over the 8 XCDs, so with S = 8 each XCD streams only its own
-// eighth of X through its L2.  With S > 1 each item writes its 128x128
-// partial (in MFMA fragment order) to the workspace and a second kernel sums
-// the partials in split order and updates H, so results are deterministic.
-#include <stdarg.h>
-#include <stdio.h>
-
+// eighth of X through its L2.  With S > 1 each item writes its partial tile
+// (in MFMA fragment order) to the workspace and a second kernel sums the
+// partials in split order and updates H, so results are deterministic.
 #include <vector>
 
 #include "common.h"
@@ -25,11 +30,9 @@ namespace mi355q {
 
 namespace {
 
-constexpr int BM = 128;          // tile edge (features)
 constexpr int BK = 64;           // tokens per LDS stage
 constexpr int NT = 256;          // threads per workgroup (4 waves, 2x2)
 constexpr int LDS_ROW = BK + 8;  // bf16 elements per feature row, +16 B pad
-constexpr int TILE_FLOATS = BM * BM;
 
 struct Matrix {            // one Hessian being accumulated
   int64_t row_begin;       // first index into rows[] (or first token)
@@ -42,6 +45,11 @@ struct Item {              // grouped work item
   int64_t slot;            // partial slot (>= 0 when S > 1)
 };
 
+struct ReduceItem {        // one tile to finish from S partial slots
+  int e, t, S;
+  int64_t slot0;           // slots slot0 .. slot0 + S - 1
+};
+
 struct SyrkParams {
   const uint16_t* x;
   int64_t ldx;
@@ -50,11 +58,9 @@ struct SyrkParams {
   int nt;                  // tiles per edge
   float alpha;
   const int32_t* rows;     // optional token -> row indirection
-  // single-matrix mode
-  Matrix single;
+  Matrix single;           // single-matrix mode
   int S;
-  // grouped mode (items != nullptr)
-  const Item* items;
+  const Item* items;       // grouped mode (items != nullptr)
   const Matrix* mats;
   float* ws;               // partial tiles
 };
@@ -83,9 +89,9 @@ __device__ __forceinline__ void load_block(const SyrkParams& p, int64_t tok0, in
                                            int64_t row_base, int64_t f, u32x4_t r[8]) {
 #pragma unroll
   for (int tt = 0; tt < 8; ++tt) {
-    int64_t k = tok0 + tt;
+    const int64_t k = tok0 + tt;
     if (k < tok_end && f < p.d) {
-      int64_t row = p.rows ? (int64_t)p.rows[row_base + k] : (row_base + k);
+      const int64_t row = p.rows ? (int64_t)p.rows[row_base + k] : (row_base + k);
       r[tt] = *reinterpret_cast<const u32x4_t*>(p.x + row * p.ldx + f);
     } else {
       r[tt] = u32x4_t{0u, 0u, 0u, 0u};
@@ -108,21 +114,33 @@ __device__ __forceinline__ void store_block(uint16_t* lds, int fb, int kb, const
   }
 }
 
-__global__ __launch_bounds__(NT, 2) void syrk_bf16_kernel(SyrkParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][BM * LDS_ROW];
+template <int TM>
+struct Cfg {
+  static constexpr int W = TM / 2;            // wave tile edge
+  static constexpr int NB = W / 32;           // 32x32 MFMA blocks per wave edge
+  static constexpr int ACC = NB * NB * 16;    // accumulator floats per lane
+  static constexpr int BLK = TM / 128;        // 8x8 load blocks per thread per operand
+  static constexpr int OPLDS = TM * LDS_ROW;  // bf16 elements per operand buffer
+  static constexpr int TILE = TM * TM;
+};
+
+template <int TM>
+__global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkParams p) {
+  using C = Cfg<TM>;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][C::OPLDS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  int e = 0, t, s, S;
+  int t, s, S;
   int64_t slot = -1;
   Matrix mat;
   if (p.items) {
-    Item it = p.items[blockIdx.x];
-    e = it.e; t = it.t; s = it.s; S = it.S; slot = it.slot;
-    mat = p.mats[e];
+    const Item it = p.items[blockIdx.x];
+    t = it.t; s = it.s; S = it.S; slot = it.slot;
+    mat = p.mats[it.e];
   } else {
     S = p.S;
     s = blockIdx.x % S;
@@ -142,79 +160,95 @@ __global__ __launch_bounds__(NT, 2) void syrk_bf16_kernel(SyrkParams p) {
   if (st_end > nst_total) st_end = nst_total;
   const int64_t nst = st_end > st_begin ? st_end - st_begin : 0;
 
-  // loader role
-  const int op = tid >> 7;          // 0: row-tile operand, 1: column-tile operand
-  const int u = tid & 127;
-  const int fb = u & 15, kb = u >> 4;
-  const int64_t fbase = (int64_t)(op ? tj : ti) * BM + 8 * fb;
+  // loader roles: (operand, block u) -> feature block u / 8, token block u % 8
+  int op[C::BLK > 1 ? 2 : 1], fbk[C::BLK > 1 ? 2 : 1], kbk[C::BLK > 1 ? 2 : 1];
+  int64_t fbase[C::BLK > 1 ? 2 : 1];
+  constexpr int NL = C::BLK > 1 ? 2 : 1;
+#pragma unroll
+  for (int b = 0; b < NL; ++b) {
+    const int u = (TM == 128) ? (tid & 127) : tid;
+    op[b] = (TM == 128) ? (tid >> 7) : b;
+    fbk[b] = u >> 3;
+    kbk[b] = u & 7;
+    fbase[b] = (int64_t)(op[b] ? tj : ti) * TM + 8 * fbk[b];
+  }
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[C::NB][C::NB];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < C::NB; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < C::NB; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-  u32x4_t regs[8];
+  u32x4_t regs[NL][8];
   if (nst > 0) {
-    load_block(p, st_begin * BK + 8 * kb, n, mat.row_begin, fbase, regs);
-    store_block(lds[0][op], fb, kb, regs);
+#pragma unroll
+    for (int b = 0; b < NL; ++b)
+      load_block(p, st_begin * BK + 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
+#pragma unroll
+    for (int b = 0; b < NL; ++b) store_block(lds[0][op[b]], fbk[b], kbk[b], regs[b]);
   }
   __syncthreads();
 
   for (int64_t st = 0; st < nst; ++st) {
     const int buf = st & 1;
-    if (st + 1 < nst) load_block(p, (st_begin + st + 1) * BK + 8 * kb, n, mat.row_begin, fbase, regs);
-
+    const bool more = st + 1 < nst;
+    if (more) {
+#pragma unroll
+      for (int b = 0; b < NL; ++b)
+        load_block(p, (st_begin + st + 1) * BK + 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
+    }
     const uint16_t* la = lds[buf][0];
     const uint16_t* lb = lds[buf][1];
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       const int koff = kk * 16 + 8 * (lane >> 5);
-      bf16x8_t fa[2], fbv[2];
+      bf16x8_t fa[C::NB], fbv[C::NB];
 #pragma unroll
-      for (int bm = 0; bm < 2; ++bm)
-        fa[bm] = *reinterpret_cast<const bf16x8_t*>(la + (wm * 64 + bm * 32 + (lane & 31)) * LDS_ROW + koff);
+      for (int bm = 0; bm < C::NB; ++bm)
+        fa[bm] = *reinterpret_cast<const bf16x8_t*>(la + (wm * C::W + bm * 32 + (lane & 31)) * LDS_ROW + koff);
 #pragma unroll
-      for (int bn = 0; bn < 2; ++bn)
-        fbv[bn] = *reinterpret_cast<const bf16x8_t*>(lb + (wn * 64 + bn * 32 + (lane & 31)) * LDS_ROW + koff);
+      for (int bn = 0; bn < C::NB; ++bn)
+        fbv[bn] = *reinterpret_cast<const bf16x8_t*>(lb + (wn * C::W + bn * 32 + (lane & 31)) * LDS_ROW + koff);
 #pragma unroll
-      for (int bm = 0; bm < 2; ++bm)
+      for (int bm = 0; bm < C::NB; ++bm)
 #pragma unroll
-        for (int bn = 0; bn < 2; ++bn)
+        for (int bn = 0; bn < C::NB; ++bn)
           acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm], fbv[bn], acc[bm][bn], 0, 0, 0);
     }
-
-    if (st + 1 < nst) store_block(lds[buf ^ 1][op], fb, kb, regs);
+    if (more) {
+#pragma unroll
+      for (int b = 0; b < NL; ++b) store_block(lds[buf ^ 1][op[b]], fbk[b], kbk[b], regs[b]);
+    }
     __syncthreads();
   }
 
   if (slot >= 0) {
-    float* dst = p.ws + (slot * NT + tid) * 64;
+    float* dst = p.ws + (slot * NT + tid) * C::ACC;
 #pragma unroll
-    for (int bm = 0; bm < 2; ++bm)
+    for (int bm = 0; bm < C::NB; ++bm)
 #pragma unroll
-      for (int bn = 0; bn < 2; ++bn)
+      for (int bn = 0; bn < C::NB; ++bn)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           f32x4_t v = {acc[bm][bn][4 * q], acc[bm][bn][4 * q + 1], acc[bm][bn][4 * q + 2],
                        acc[bm][bn][4 * q + 3]};
-          *reinterpret_cast<f32x4_t*>(dst + (bm * 2 + bn) * 16 + 4 * q) = v;
+          *reinterpret_cast<f32x4_t*>(dst + (bm * C::NB + bn) * 16 + 4 * q) = v;
         }
     return;
   }
 
   // direct update of the upper triangle
-  const int64_t gi0 = (int64_t)ti * BM, gj0 = (int64_t)tj * BM;
+  const int64_t gi0 = (int64_t)ti * TM, gj0 = (int64_t)tj * TM;
 #pragma unroll
-  for (int bm = 0; bm < 2; ++bm)
+  for (int bm = 0; bm < C::NB; ++bm)
 #pragma unroll
-    for (int bn = 0; bn < 2; ++bn)
+    for (int bn = 0; bn < C::NB; ++bn)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int nn = wn * 64 + bn * 32 + (lane & 31);
+        const int m = wm * C::W + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int nn = wn * C::W + bn * 32 + (lane & 31);
         const int64_t gi = gi0 + m, gj = gj0 + nn;
         if (gi < p.d && gj < p.d && gi <= gj) {
           float* hp = mat.h + gi * p.ldh + gj;
@@ -223,59 +257,57 @@ __global__ __launch_bounds__(NT, 2) void syrk_bf16_kernel(SyrkParams p) {
       }
 }
 
-struct ReduceItem {        // one tile to finish from S partial slots
-  int e, t, S;
-  int64_t slot0;           // slots slot0 .. slot0 + S - 1
-};
-
-__global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict__ ws,
-                                                         const ReduceItem* items, int single_S,
-                                                         Matrix single, const Matrix* mats,
+// Sums the S partial slots of a tile in split order and updates H.  Each
+// workgroup finishes one row of 32 x 32 blocks of its wave tiles
+// (blockIdx.y = bm), so a TM = 256 tile is finished by four workgroups.
+template <int TM>
+__global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict__ ws, const ReduceItem* items,
+                                                         int single_S, Matrix single, const Matrix* mats,
                                                          int64_t d, int64_t ldh, int nt, float alpha) {
+  using C = Cfg<TM>;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  const int bm = blockIdx.y;
   int t, S;
   int64_t slot0;
   Matrix mat;
   if (items) {
-    ReduceItem it = items[blockIdx.x];
+    const ReduceItem it = items[blockIdx.x];
     t = it.t; S = it.S; slot0 = it.slot0; mat = mats[it.e];
   } else {
     t = blockIdx.x; S = single_S; slot0 = (int64_t)t * S; mat = single;
   }
   int ti, tj;
   tile_coords(t, nt, ti, tj);
-  float sum[64];
+  float sum[C::NB * 16];
 #pragma unroll
-  for (int r = 0; r < 64; ++r) sum[r] = 0.f;
+  for (int r = 0; r < C::NB * 16; ++r) sum[r] = 0.f;
   for (int s = 0; s < S; ++s) {
-    const float* src = ws + ((slot0 + s) * NT + tid) * 64;
+    const float* src = ws + ((slot0 + s) * NT + tid) * C::ACC + bm * C::NB * 16;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      f32x4_t v = *reinterpret_cast<const f32x4_t*>(src + 4 * q);
+    for (int q = 0; q < C::NB * 4; ++q) {
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(src + 4 * q);
       sum[4 * q] += v[0];
       sum[4 * q + 1] += v[1];
       sum[4 * q + 2] += v[2];
       sum[4 * q + 3] += v[3];
     }
   }
-  const int64_t gi0 = (int64_t)ti * BM, gj0 = (int64_t)tj * BM;
+  const int64_t gi0 = (int64_t)ti * TM, gj0 = (int64_t)tj * TM;
 #pragma unroll
-  for (int bm = 0; bm < 2; ++bm)
+  for (int bn = 0; bn < C::NB; ++bn)
 #pragma unroll
-    for (int bn = 0; bn < 2; ++bn)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int nn = wn * 64 + bn * 32 + (lane & 31);
-        const int64_t gi = gi0 + m, gj = gj0 + nn;
-        if (gi < d && gj < d && gi <= gj) {
-          float* hp = mat.h + gi * ldh + gj;
-          *hp = *hp + alpha * sum[(bm * 2 + bn) * 16 + r];
-        }
+    for (int r = 0; r < 16; ++r) {
+      const int m = wm * C::W + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int nn = wn * C::W + bn * 32 + (lane & 31);
+      const int64_t gi = gi0 + m, gj = gj0 + nn;
+      if (gi < d && gj < d && gi <= gj) {
+        float* hp = mat.h + gi * ldh + gj;
+        *hp = *hp + alpha * sum[bn * 16 + r];
       }
+    }
 }
 
 __global__ void symmetrize_kernel(float* h, int64_t d, int64_t ldh) {
@@ -284,26 +316,48 @@ __global__ void symmetrize_kernel(float* h, int64_t d, int64_t ldh) {
   if (bi > bj) return;
   const int tx = threadIdx.x, ty = threadIdx.y;  // 32 x 8
   for (int k = ty; k < 32; k += 8) {
-    int64_t r = (int64_t)bi * 32 + k, c = (int64_t)bj * 32 + tx;
+    const int64_t r = (int64_t)bi * 32 + k, c = (int64_t)bj * 32 + tx;
     tile[k][tx] = (r < d && c < d) ? h[r * ldh + c] : 0.f;
   }
   __syncthreads();
   for (int k = ty; k < 32; k += 8) {
-    int64_t r = (int64_t)bj * 32 + k, c = (int64_t)bi * 32 + tx;  // lower element (r, c) = upper (c, r)
+    const int64_t r = (int64_t)bj * 32 + k, c = (int64_t)bi * 32 + tx;  // lower (r, c) = upper (c, r)
     if (r < d && c < d && r > c) h[r * ldh + c] = tile[tx][k];
   }
 }
 
 int choose_splits(int64_t n) {
-  int64_t s = n / 2048;
+  const int64_t s = n / 2048;
   if (s >= 8) return 8;
   if (s >= 4) return 4;
   if (s >= 2) return 2;
   return 1;
 }
 
-inline int tiles_per_edge(int64_t d) { return (int)((d + BM - 1) / BM); }
+inline int tile_edge(int64_t d) { return d >= 512 ? 256 : 128; }
+inline int tiles_per_edge(int64_t d) {
+  const int tm = tile_edge(d);
+  return (int)((d + tm - 1) / tm);
+}
 inline int upper_tiles(int nt) { return nt * (nt + 1) / 2; }
+inline size_t tile_floats(int64_t d) { return (size_t)tile_edge(d) * tile_edge(d); }
+
+void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
+  if (tile_edge(d) == 256)
+    hipLaunchKernelGGL(syrk_bf16_kernel<256>, dim3(grid), dim3(NT), 0, st, p);
+  else
+    hipLaunchKernelGGL(syrk_bf16_kernel<128>, dim3(grid), dim3(NT), 0, st, p);
+}
+
+void launch_reduce(const float* ws, const ReduceItem* items, int S, const Matrix& single, const Matrix* mats,
+                   int64_t d, int64_t ldh, int nt, float alpha, unsigned ntiles, hipStream_t st) {
+  if (tile_edge(d) == 256)
+    hipLaunchKernelGGL(syrk_reduce_kernel<256>, dim3(ntiles, Cfg<256>::NB), dim3(NT), 0, st, ws, items, S, single,
+                       mats, d, ldh, nt, alpha);
+  else
+    hipLaunchKernelGGL(syrk_reduce_kernel<128>, dim3(ntiles, Cfg<128>::NB), dim3(NT), 0, st, ws, items, S, single,
+                       mats, d, ldh, nt, alpha);
+}
 
 }  // namespace
 
@@ -315,7 +369,7 @@ extern "C" size_t mi355q_hessian_workspace_size(int64_t n_tokens, int64_t d) {
   if (n_tokens <= 0 || d <= 0) return 0;
   const int S = choose_splits(n_tokens);
   if (S == 1) return 0;
-  return (size_t)upper_tiles(tiles_per_edge(d)) * S * TILE_FLOATS * sizeof(float);
+  return (size_t)upper_tiles(tiles_per_edge(d)) * S * tile_floats(d) * sizeof(float);
 }
 
 extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
@@ -349,11 +403,10 @@ extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int
   p.items = nullptr;
   p.mats = nullptr;
   p.ws = static_cast<float*>(workspace_dev);
-  hipLaunchKernelGGL(syrk_bf16_kernel, dim3((unsigned)T * S), dim3(NT), 0, st, p);
+  launch_syrk(p, d, (unsigned)T * S, st);
   MQ_LAUNCH_CHECK();
   if (S > 1) {
-    hipLaunchKernelGGL(syrk_reduce_kernel, dim3((unsigned)T), dim3(NT), 0, st, p.ws,
-                       (const ReduceItem*)nullptr, S, p.single, (const Matrix*)nullptr, d, ldh, nt, alpha);
+    launch_reduce(p.ws, nullptr, S, p.single, nullptr, d, ldh, nt, alpha, (unsigned)T, st);
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;
@@ -374,12 +427,12 @@ GroupedPlan plan_grouped(const int64_t* offsets, int E, int64_t d, float* h, int
   const int nt = tiles_per_edge(d);
   const int T = upper_tiles(nt);
   for (int e = 0; e < E; ++e) {
-    int64_t n = offsets[e + 1] - offsets[e];
+    const int64_t n = offsets[e + 1] - offsets[e];
     g.mats.push_back(Matrix{offsets[e], n, h ? h + (int64_t)e * h_stride : nullptr});
     if (n <= 0) continue;
     const int S = choose_splits(n);
     for (int t = 0; t < T; ++t) {
-      int64_t slot0 = S > 1 ? g.slots : -1;
+      const int64_t slot0 = S > 1 ? g.slots : -1;
       for (int s = 0; s < S; ++s) g.items.push_back(Item{e, t, s, S, S > 1 ? slot0 + s : -1});
       if (S > 1) {
         g.reduces.push_back(ReduceItem{e, t, S, slot0});
@@ -388,7 +441,7 @@ GroupedPlan plan_grouped(const int64_t* offsets, int E, int64_t d, float* h, int
     }
   }
   auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  size_t off = align((size_t)g.slots * TILE_FLOATS * sizeof(float));
+  size_t off = align((size_t)g.slots * tile_floats(d) * sizeof(float));
   g.off_items = off;
   off = align(off + g.items.size() * sizeof(Item));
   g.off_reduces = off;
@@ -433,29 +486,26 @@ extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, 
                                 g.reduces.size() * sizeof(ReduceItem), hipMemcpyHostToDevice, st));
   MQ_CHECK_HIP(hipMemcpyAsync(ws + g.off_mats, g.mats.data(), g.mats.size() * sizeof(Matrix),
                               hipMemcpyHostToDevice, st));
-  // the host vectors die at return: wait for the copies (pageable memory
-  // is staged synchronously by HIP, but make the ordering explicit)
+  // the host-side plan dies at return: wait for the copies
   MQ_CHECK_HIP(hipStreamSynchronize(st));
 
-  const int nt = tiles_per_edge(d);
   SyrkParams p{};
   p.x = static_cast<const uint16_t*>(x_dev);
   p.ldx = ldx;
   p.d = d;
   p.ldh = d;
-  p.nt = nt;
+  p.nt = tiles_per_edge(d);
   p.alpha = alpha;
   p.rows = rows_dev;
   p.S = 1;
   p.items = reinterpret_cast<const Item*>(ws + g.off_items);
   p.mats = reinterpret_cast<const Matrix*>(ws + g.off_mats);
   p.ws = reinterpret_cast<float*>(ws);
-  hipLaunchKernelGGL(syrk_bf16_kernel, dim3((unsigned)g.items.size()), dim3(NT), 0, st, p);
+  launch_syrk(p, d, (unsigned)g.items.size(), st);
   MQ_LAUNCH_CHECK();
   if (!g.reduces.empty()) {
-    hipLaunchKernelGGL(syrk_reduce_kernel, dim3((unsigned)g.reduces.size()), dim3(NT), 0, st,
-                       p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, Matrix{},
-                       p.mats, d, d, nt, alpha);
+    launch_reduce(p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, Matrix{}, p.mats, d, d,
+                  p.nt, alpha, (unsigned)g.reduces.size(), st);
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;
