@@ -24,16 +24,74 @@ constexpr int SW_NT = SW_G * SW_ROWS;    // 256 threads
 constexpr int MAXB = 128;                // largest supported block size
 constexpr int SW_T = MAXB / SW_G;        // columns per lane
 
-__device__ __forceinline__ int64_t sidx(int strategy, int64_t r, int64_t c, int64_t ld_scale,
-                                        const int32_t* g_idx, int block_h) {
-  switch (strategy) {
-    case MI355Q_TENSOR: return 0;
-    case MI355Q_CHANNEL: return r * ld_scale;
-    case MI355Q_GROUP: return r * ld_scale + g_idx[c];
-    case MI355Q_BLOCK: return (r / block_h) * ld_scale + g_idx[c];
-  }
-  return 0;
+// Per-lane state of the sweep: lane g of a row holds block columns
+// SW_G * t + g, t = 0..SW_T-1.
+struct SweepState {
+  float w[SW_T];   // working values (final once their column is reached)
+  float s[SW_T];   // scale of each column
+  float z[SW_T];   // zero point of each column
+  float q[SW_T];   // dequantised result (owner)
+  float er[SW_T];  // (w - q) / Hinv[i][i] (owner)
+  float df[SW_T];  // w - q (owner), for the loss
+  int cq[SW_T];    // integer code (owner)
+};
+
+// Branch-free bf16 round-to-nearest-even of a finite fp32 value.
+__device__ __forceinline__ float bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
 }
+
+// Broadcast lane `L` of every 16-lane row to the whole row (DPP row_newbcast).
+template <int L>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xF, 0xF, false));
+}
+
+// One column of the sweep: column I = SW_G * TO + GO, owned by lane GO of
+// each row.  Every lane runs the quantisation on its own slot TO (only the
+// owner's result is kept), the owner's error is broadcast within the row, and
+// each lane updates its later columns.
+template <int TO, int GO>
+__device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, int g, int count, float qmin,
+                                           float qmax, bool dq_bf16) {
+  constexpr int I = SW_G * TO + GO;
+  if (I >= count) return;
+  const float dd = h1[I * MAXB + I];
+  const float x = S.w[TO];
+  float qq = x / S.s[TO] + S.z[TO];
+  qq = rintf(fminf(fmaxf(qq, qmin), qmax));
+  float deq = (qq - S.z[TO]) * S.s[TO];
+  if (dq_bf16) deq = bf16_rne(deq);
+  const float diff = x - deq;
+  const float err = diff / dd;
+  const bool own = g == GO;
+  S.q[TO] = own ? deq : S.q[TO];
+  S.cq[TO] = own ? (int)qq : S.cq[TO];
+  S.er[TO] = own ? err : S.er[TO];
+  S.df[TO] = own ? diff : S.df[TO];
+  const float e = row_bcast<GO>(err);
+#pragma unroll
+  for (int t = TO; t < SW_T; ++t) {
+    const int col = SW_G * t + g;
+    const float upd = S.w[t] - e * h1[I * MAXB + col];
+    const bool take = (t > TO || g > GO) && col < count;
+    S.w[t] = take ? upd : S.w[t];
+  }
+}
+
+template <int I>
+struct SweepSteps {
+  static __device__ __forceinline__ void run(SweepState& S, const float* h1, int g, int count, float qmin,
+                                             float qmax, bool dq_bf16) {
+    sweep_step<I / SW_G, I % SW_G>(S, h1, g, count, qmin, qmax, dq_bf16);
+    SweepSteps<I + 1>::run(S, h1, g, count, qmin, qmax, dq_bf16);
+  }
+};
+template <>
+struct SweepSteps<MAXB> {
+  static __device__ __forceinline__ void run(SweepState&, const float*, int, int, float, float, bool) {}
+};
 
 __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
@@ -41,16 +99,31 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
     const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax, int dq_bf16,
     int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out) {
   __shared__ float h1[MAXB * MAXB];
+  __shared__ int gsh[MAXB];
   const int tid = threadIdx.x;
+  const int g = tid & (SW_G - 1);
+  const int64_t r = (int64_t)blockIdx.x * SW_ROWS + (tid / SW_G);
+  const bool live = r < rows;
+  const int64_t rr = live ? r : rows - 1;  // clamped row: every address below is in bounds
+
+  SweepState S;
+  // the row's working values first, so they load while the block of Hinv does
+#pragma unroll
+  for (int t = 0; t < SW_T; ++t) {
+    const int col = min(SW_G * t + g, count - 1);
+    S.w[t] = W[rr * cols + i1 + col];
+  }
   if (count == MAXB && (cols & 3) == 0 && (reinterpret_cast<uintptr_t>(hinv) & 15) == 0) {
-    // 16 independent 16-byte loads per thread (lower-triangle chunks skipped)
+    f32x4_t hv[MAXB * MAXB / 4 / SW_NT];
 #pragma unroll
     for (int v = 0; v < MAXB * MAXB / 4 / SW_NT; ++v) {
       const int e = v * SW_NT + tid;
-      const int i = e >> 5, j4 = (e & 31) * 4;
-      if (j4 + 3 >= i)
-        *reinterpret_cast<f32x4_t*>(h1 + i * MAXB + j4) =
-            *reinterpret_cast<const f32x4_t*>(hinv + (i1 + i) * cols + i1 + j4);
+      hv[v] = *reinterpret_cast<const f32x4_t*>(hinv + (i1 + (e >> 5)) * cols + i1 + (e & 31) * 4);
+    }
+#pragma unroll
+    for (int v = 0; v < MAXB * MAXB / 4 / SW_NT; ++v) {
+      const int e = v * SW_NT + tid;
+      *reinterpret_cast<f32x4_t*>(h1 + (e >> 5) * MAXB + (e & 31) * 4) = hv[v];
     }
   } else {
     for (int e = tid; e < count * count; e += SW_NT) {
@@ -58,69 +131,45 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
       if (j >= i) h1[i * MAXB + j] = hinv[(i1 + i) * cols + (i1 + j)];
     }
   }
+  const bool uses_gidx = strategy == MI355Q_GROUP || strategy == MI355Q_BLOCK;
+  if (tid < MAXB) gsh[tid] = (uses_gidx && tid < count) ? g_idx[i1 + tid] : 0;
   __syncthreads();
 
-  const int g = tid & (SW_G - 1);
-  const int64_t r = (int64_t)blockIdx.x * SW_ROWS + (tid / SW_G);
-  const bool live = r < rows;
+  int64_t sbase = 0;
+  if (strategy == MI355Q_CHANNEL || strategy == MI355Q_GROUP) sbase = rr * ld_scale;
+  if (strategy == MI355Q_BLOCK) sbase = (rr / block_h) * ld_scale;
+#pragma unroll
+  for (int t = 0; t < SW_T; ++t) {
+    const int col = min(SW_G * t + g, count - 1);
+    const int64_t si = sbase + gsh[col];
+    S.s[t] = scale[si];
+    S.z[t] = zp ? zp[si] : 0.f;
+    S.q[t] = 0.f;
+    S.er[t] = 0.f;
+    S.df[t] = 0.f;
+    S.cq[t] = 0;
+  }
 
-  float w[SW_T], s[SW_T], z[SW_T], q[SW_T], er[SW_T];
-  int cq[SW_T];
+  SweepSteps<0>::run(S, h1, g, count, qmin, qmax, dq_bf16 != 0);
+
+  float loss = 0.f;
 #pragma unroll
   for (int t = 0; t < SW_T; ++t) {
     const int col = SW_G * t + g;
-    w[t] = 0.f; s[t] = 1.f; z[t] = 0.f; q[t] = 0.f; er[t] = 0.f; cq[t] = 0;
-    if (live && col < count) {
-      const int64_t c = i1 + col;
-      w[t] = W[r * cols + c];
-      const int64_t si = sidx(strategy, r, c, ld_scale, g_idx, block_h);
-      s[t] = scale[si];
-      z[t] = zp ? zp[si] : 0.f;
+    if (col < count) {
+      const float dd = h1[col * MAXB + col];
+      loss = loss + S.df[t] * S.df[t] / (dd * dd);
     }
   }
-
-  float loss = 0.f;
-  // column i = SW_G * to + go; `to` is a compile-time register slot (outer
-  // loop unrolled), `go` the owner lane (inner loop, runtime), so no
-  // register array is ever indexed dynamically
-#pragma unroll
-  for (int to = 0; to < SW_T; ++to) {
-  for (int go = 0; go < SW_G; ++go) {
-    const int i = SW_G * to + go;
-    if (i >= count) break;
-    const float x = __shfl(w[to], go, SW_G);
-    const float sc = __shfl(s[to], go, SW_G);
-    const float zz = __shfl(z[to], go, SW_G);
-    const float dd = h1[i * MAXB + i];
-    float qq = x / sc + zz;
-    qq = rintf(fminf(fmaxf(qq, qmin), qmax));
-    float deq = (qq - zz) * sc;
-    if (dq_bf16) deq = round_to_bf16(deq);
-    const float diff = x - deq;
-    const float err = diff / dd;
-    if (g == go) {
-      q[to] = deq;
-      cq[to] = (int)qq;
-      er[to] = err;
-      loss = loss + diff * diff / (dd * dd);
-    }
-#pragma unroll
-    for (int t = to; t < SW_T; ++t) {
-      const int col = SW_G * t + g;
-      if (col > i && col < count) w[t] = w[t] - err * h1[i * MAXB + col];
-    }
-  }
-  }
-
   if (live) {
 #pragma unroll
     for (int t = 0; t < SW_T; ++t) {
       const int col = SW_G * t + g;
       if (col < count) {
         const int64_t c = i1 + col;
-        W[r * cols + c] = q[t];
-        codes[r * cols + c] = (int8_t)cq[t];
-        err_out[r * MAXB + col] = er[t];
+        W[r * cols + c] = S.q[t];
+        codes[r * cols + c] = (int8_t)S.cq[t];
+        err_out[r * MAXB + col] = S.er[t];
       }
     }
   }
@@ -129,39 +178,58 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
   if (live && g == 0) losses[r] = losses[r] + loss / 2.f;
 }
 
+// One row per blockIdx.y, four consecutive output columns per thread.
 __global__ void load_weight_kernel(const void* w, mi355q_dtype dt, int64_t rows, int64_t cols, int64_t ldw,
                                    const int32_t* perm, const int32_t* dead, float* out) {
-  const int64_t n = rows * cols;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / cols, j = i % cols;
-    const int64_t src = perm ? perm[j] : j;
-    float v = dt == MI355Q_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(w)[r * ldw + src])
-                                : static_cast<const float*>(w)[r * ldw + src];
-    if (dead && dead[j]) v = 0.f;
-    out[i] = v;
+  const int64_t r = blockIdx.y;
+  for (int64_t j4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; j4 < cols;
+       j4 += (int64_t)gridDim.x * blockDim.x * 4) {
+    f32x4_t v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t j = j4 + e < cols ? j4 + e : cols - 1;
+      const int64_t src = perm ? perm[j] : j;
+      float x = dt == MI355Q_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(w)[r * ldw + src])
+                                  : static_cast<const float*>(w)[r * ldw + src];
+      v[e] = (dead && dead[j]) ? 0.f : x;
+    }
+    float* o = out + r * cols + j4;
+    if ((cols & 3) == 0) {
+      *reinterpret_cast<f32x4_t*>(o) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (j4 + e < cols) o[e] = v[e];
+    }
   }
 }
 
 __global__ void store_weight_kernel(const float* w, int64_t rows, int64_t cols, const int32_t* invperm,
                                     void* out, mi355q_dtype dt, int64_t ld_out, const int8_t* cin,
                                     int8_t* cout) {
-  const int64_t n = rows * cols;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / cols, j = i % cols;
-    const int64_t src = r * cols + (invperm ? invperm[j] : j);
-    const float v = w[src];
-    if (dt == MI355Q_BF16)
-      static_cast<uint16_t*>(out)[r * ld_out + j] = f32_to_bf16_bits(v);
-    else
-      static_cast<float*>(out)[r * ld_out + j] = v;
-    if (cin && cout) cout[i] = cin[src];
+  const int64_t r = blockIdx.y;
+  for (int64_t j4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; j4 < cols;
+       j4 += (int64_t)gridDim.x * blockDim.x * 4) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t j = j4 + e;
+      if (j >= cols) break;
+      const int64_t src = r * cols + (invperm ? invperm[j] : j);
+      const float v = w[src];
+      if (dt == MI355Q_BF16)
+        static_cast<uint16_t*>(out)[r * ld_out + j] = f32_to_bf16_bits(v);
+      else
+        static_cast<float*>(out)[r * ld_out + j] = v;
+      if (cin && cout) cout[r * cols + j] = cin[src];
+    }
   }
 }
 
-inline unsigned grid1d(int64_t n) {
-  int64_t g = (n + 255) / 256;
-  if (g > 65536) g = 65536;
-  return (unsigned)(g < 1 ? 1 : g);
+inline dim3 grid_rows(int64_t rows, int64_t cols) {
+  int64_t gx = (cols / 4 + 255) / 256;
+  if (gx < 1) gx = 1;
+  if (gx > 64) gx = 64;
+  return dim3((unsigned)gx, (unsigned)rows);
 }
 
 }  // namespace
@@ -174,7 +242,8 @@ extern "C" int mi355q_gptq_load_weight(const void* w_dev, mi355q_dtype w_dtype, 
                                        float* w_work_dev, void* stream) {
   MQ_CHECK_ARG(w_dev && w_work_dev, "gptq_load_weight: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && ldw >= cols, "gptq_load_weight: bad shape");
-  hipLaunchKernelGGL(load_weight_kernel, dim3(grid1d(rows * cols)), dim3(256), 0,
+  MQ_CHECK_ARG(rows <= 65535, "gptq_load_weight: at most 65535 rows");
+  hipLaunchKernelGGL(load_weight_kernel, grid_rows(rows, cols), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), w_dev, w_dtype, rows, cols, ldw, perm_dev, dead_dev,
                      w_work_dev);
   MQ_LAUNCH_CHECK();
@@ -239,7 +308,8 @@ extern "C" int mi355q_gptq_store_weight(const float* w_work_dev, int64_t rows, i
   MQ_CHECK_ARG(w_work_dev && w_out_dev, "gptq_store_weight: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && ld_out >= cols, "gptq_store_weight: bad shape");
   MQ_CHECK_ARG(codes_out_dev != codes_in_dev || !codes_in_dev, "gptq_store_weight: codes must not alias");
-  hipLaunchKernelGGL(store_weight_kernel, dim3(grid1d(rows * cols)), dim3(256), 0,
+  MQ_CHECK_ARG(rows <= 65535, "gptq_store_weight: at most 65535 rows");
+  hipLaunchKernelGGL(store_weight_kernel, grid_rows(rows, cols), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), w_work_dev, rows, cols, invperm_dev, w_out_dev,
                      out_dtype, ld_out, codes_in_dev, codes_out_dev);
   MQ_LAUNCH_CHECK();

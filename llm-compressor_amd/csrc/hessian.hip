@@ -84,30 +84,61 @@ __device__ __forceinline__ unsigned perm_hi(unsigned a, unsigned b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);  // hi16(a) | hi16(b) << 16
 }
 
-// Load one 8 (tokens) x 8 (features) block into r[8] (4 dwords each).
-__device__ __forceinline__ void load_block(const SyrkParams& p, int64_t tok0, int64_t tok_end,
-                                           int64_t row_base, int64_t f, u32x4_t r[8]) {
+// Load one 8 (tokens) x 8 (features) block into r[8] (4 dwords each): tokens
+// stage0 + lt0 + 0..7 of the matrix, features f..f+7.  Branch-free:
+// out-of-range tokens / features read a clamped in-range address, and the
+// returned mask (bit tt = token tt valid) zeroes them when the block is
+// stored, so the eight loads issue back to back and nothing waits for them
+// before the MFMAs of the current stage.  Dense X is addressed as a
+// wave-uniform stage base plus a 32-bit lane offset; the gathered layout (G)
+// fetches its eight row indices first.
+template <bool G>
+__device__ __forceinline__ unsigned load_block(const SyrkParams& p, int64_t stage0, int lt0, int64_t tok_end,
+                                               int64_t row_base, int64_t f, u32x4_t r[8]) {
+  const bool fin = f < p.d;
+  const int64_t fc = fin ? f : 0;
+  const int64_t rem = tok_end - stage0;           // >= 1 for a stage in range
+  const int lim = rem < BK ? (int)rem : BK;
+  if (!G) {
+    const char* base = reinterpret_cast<const char*>(p.x + (row_base + stage0) * p.ldx);
 #pragma unroll
-  for (int tt = 0; tt < 8; ++tt) {
-    const int64_t k = tok0 + tt;
-    if (k < tok_end && f < p.d) {
-      const int64_t row = p.rows ? (int64_t)p.rows[row_base + k] : (row_base + k);
-      r[tt] = *reinterpret_cast<const u32x4_t*>(p.x + row * p.ldx + f);
-    } else {
-      r[tt] = u32x4_t{0u, 0u, 0u, 0u};
+    for (int tt = 0; tt < 8; ++tt) {
+      const int lt = lt0 + tt;
+      const int ltc = lt < lim ? lt : lim - 1;
+      const uint32_t off = (uint32_t)(ltc * p.ldx + fc) * 2u;
+      r[tt] = *reinterpret_cast<const u32x4_t*>(base + off);
     }
+  } else {
+    int64_t row[8];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) {
+      const int lt = lt0 + tt;
+      row[tt] = p.rows[row_base + stage0 + (lt < lim ? lt : lim - 1)];
+    }
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) r[tt] = *reinterpret_cast<const u32x4_t*>(p.x + row[tt] * p.ldx + fc);
   }
+  const int nv = lim - lt0;
+  return !fin || nv <= 0 ? 0u : (nv >= 8 ? 0xffu : (1u << nv) - 1u);
 }
 
-// Transpose r (token-major) and store 8 feature rows of 8 tokens to LDS.
-__device__ __forceinline__ void store_block(uint16_t* lds, int fb, int kb, const u32x4_t r[8]) {
+// Transpose r (token-major) and store 8 feature rows of 8 tokens to LDS;
+// tokens whose mask bit is clear are stored as zeros.
+__device__ __forceinline__ void store_block(uint16_t* lds, int fb, int kb, const u32x4_t r[8], unsigned mask) {
+  u32x4_t z[8];
+#pragma unroll
+  for (int tt = 0; tt < 8; ++tt) {
+    const unsigned m = (mask >> tt) & 1u ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) z[tt][j] = r[tt][j] & m;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {     // feature pair (2j, 2j+1)
     u32x4_t lo, hi;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {   // token pair (2q, 2q+1)
-      lo[q] = perm_lo(r[2 * q][j], r[2 * q + 1][j]);
-      hi[q] = perm_hi(r[2 * q][j], r[2 * q + 1][j]);
+      lo[q] = perm_lo(z[2 * q][j], z[2 * q + 1][j]);
+      hi[q] = perm_hi(z[2 * q][j], z[2 * q + 1][j]);
     }
     *reinterpret_cast<u32x4_t*>(lds + (8 * fb + 2 * j) * LDS_ROW + 8 * kb) = lo;
     *reinterpret_cast<u32x4_t*>(lds + (8 * fb + 2 * j + 1) * LDS_ROW + 8 * kb) = hi;
@@ -124,7 +155,7 @@ struct Cfg {
   static constexpr int TILE = TM * TM;
 };
 
-template <int TM>
+template <int TM, bool G>
 __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkParams p) {
   using C = Cfg<TM>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][C::OPLDS];
@@ -182,12 +213,13 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
   u32x4_t regs[NL][8];
+  unsigned vmask[NL];
   if (nst > 0) {
 #pragma unroll
     for (int b = 0; b < NL; ++b)
-      load_block(p, st_begin * BK + 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
+      vmask[b] = load_block<G>(p, st_begin * BK, 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
 #pragma unroll
-    for (int b = 0; b < NL; ++b) store_block(lds[0][op[b]], fbk[b], kbk[b], regs[b]);
+    for (int b = 0; b < NL; ++b) store_block(lds[0][op[b]], fbk[b], kbk[b], regs[b], vmask[b]);
   }
   __syncthreads();
 
@@ -197,7 +229,7 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
     if (more) {
 #pragma unroll
       for (int b = 0; b < NL; ++b)
-        load_block(p, (st_begin + st + 1) * BK + 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
+        vmask[b] = load_block<G>(p, (st_begin + st + 1) * BK, 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
     }
     const uint16_t* la = lds[buf][0];
     const uint16_t* lb = lds[buf][1];
@@ -219,7 +251,7 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
     }
     if (more) {
 #pragma unroll
-      for (int b = 0; b < NL; ++b) store_block(lds[buf ^ 1][op[b]], fbk[b], kbk[b], regs[b]);
+      for (int b = 0; b < NL; ++b) store_block(lds[buf ^ 1][op[b]], fbk[b], kbk[b], regs[b], vmask[b]);
     }
     __syncthreads();
   }
@@ -343,10 +375,14 @@ inline int upper_tiles(int nt) { return nt * (nt + 1) / 2; }
 inline size_t tile_floats(int64_t d) { return (size_t)tile_edge(d) * tile_edge(d); }
 
 void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
-  if (tile_edge(d) == 256)
-    hipLaunchKernelGGL(syrk_bf16_kernel<256>, dim3(grid), dim3(NT), 0, st, p);
-  else
-    hipLaunchKernelGGL(syrk_bf16_kernel<128>, dim3(grid), dim3(NT), 0, st, p);
+  const bool g = p.rows != nullptr;
+  if (tile_edge(d) == 256) {
+    if (g) hipLaunchKernelGGL((syrk_bf16_kernel<256, true>), dim3(grid), dim3(NT), 0, st, p);
+    else   hipLaunchKernelGGL((syrk_bf16_kernel<256, false>), dim3(grid), dim3(NT), 0, st, p);
+  } else {
+    if (g) hipLaunchKernelGGL((syrk_bf16_kernel<128, true>), dim3(grid), dim3(NT), 0, st, p);
+    else   hipLaunchKernelGGL((syrk_bf16_kernel<128, false>), dim3(grid), dim3(NT), 0, st, p);
+  }
 }
 
 void launch_reduce(const float* ws, const ReduceItem* items, int S, const Matrix& single, const Matrix* mats,
@@ -377,6 +413,7 @@ extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int
                                         size_t workspace_bytes, void* stream) {
   MQ_CHECK_ARG(d > 0 && d % 8 == 0, "hessian: d must be a positive multiple of 8 (got %lld)", (long long)d);
   MQ_CHECK_ARG(ldx >= d && ldx % 8 == 0, "hessian: ldx must be >= d and a multiple of 8");
+  MQ_CHECK_ARG(ldx <= (int64_t(1) << 24), "hessian: ldx above 2^24 elements is not supported");
   MQ_CHECK_ARG(ldh >= d, "hessian: ldh must be >= d");
   MQ_CHECK_ARG(n_tokens >= 0, "hessian: negative token count");
   MQ_CHECK_ARG(h_dev != nullptr, "hessian: null H");

@@ -25,6 +25,12 @@ namespace mi355q {
 namespace {
 
 // ---------------------------------------------------------------- GEMM
+// x if keep else +0.0, as a bit mask: a select on a loaded value can be
+// turned back into a branch around the load, which serialises the loads
+__device__ __forceinline__ float keep_if(float x, bool keep) {
+  return __uint_as_float(__float_as_uint(x) & (keep ? 0xffffffffu : 0u));
+}
+
 constexpr int GBM = 128, GBN = 128, GBK = 32, GNT = 256;
 constexpr int LA = GBK + 1;     // LDS row stride for [m][k] tiles
 constexpr int LBN = GBN + 32;   // LDS row stride for [k][n] tiles
@@ -53,37 +59,38 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
   f32x4_t ra[4], rb[4];
-  const bool vec_a = ((reinterpret_cast<uintptr_t>(A) & 15) == 0) && ((g.lda & 3) == 0);
-  const bool vec_b = ((reinterpret_cast<uintptr_t>(B) & 15) == 0) && ((g.ldb & 3) == 0);
+  // Branch-free loads: out-of-range elements read a clamped in-range address
+  // and are zeroed when the tile is stored to LDS (after the MFMAs of the
+  // current stage), so the loads issue back to back and are not waited for
+  // before the MFMAs.
+  const bool vec_a = ((reinterpret_cast<uintptr_t>(A) & 15) == 0) && ((g.lda & 3) == 0) && ((g.K & 3) == 0);
+  const bool vec_bk = ((reinterpret_cast<uintptr_t>(B) & 15) == 0) && ((g.ldb & 3) == 0) && ((g.K & 3) == 0);
+  const bool vec_bn = ((reinterpret_cast<uintptr_t>(B) & 15) == 0) && ((g.ldb & 3) == 0) && ((g.N & 3) == 0);
   // A / B^T tiles: 128 rows x 32 k -> 1024 float4 (4 per thread)
   auto load_mk = [&](const float* P, int64_t ld, bool vec, int64_t rows_lim, int64_t r0, int64_t k0,
                      f32x4_t* r) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int idx = v * GNT + tid;
-      const int row = idx >> 3, quad = idx & 7;
-      const int64_t gr = r0 + row, gk = k0 + 4 * quad;
-      f32x4_t x = {0.f, 0.f, 0.f, 0.f};
-      if (gr < rows_lim) {
-        const float* src = P + gr * ld + gk;
-        if (vec && gk + 3 < g.K) {
-          x = *reinterpret_cast<const f32x4_t*>(src);
-        } else {
+      const int64_t gr = r0 + (idx >> 3), gk = k0 + 4 * (idx & 7);
+      const int64_t grc = gr < rows_lim ? gr : rows_lim - 1;
+      if (vec) {
+        const int64_t gkc = gk < g.K ? gk : g.K - 4;
+        r[v] = *reinterpret_cast<const f32x4_t*>(P + grc * ld + gkc);
+      } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (gk + e < g.K) x[e] = src[e];
-        }
+        for (int e = 0; e < 4; ++e) r[v][e] = P[grc * ld + (gk + e < g.K ? gk + e : g.K - 1)];
       }
-      r[v] = x;
     }
   };
-  auto store_mk = [&](float* L, const f32x4_t* r) {
+  auto store_mk = [&](float* L, const f32x4_t* r, int64_t rows_lim, int64_t r0, int64_t k0) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int idx = v * GNT + tid;
       const int row = idx >> 3, quad = idx & 7;
+      const bool rok = r0 + row < rows_lim;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) L[row * LA + 4 * quad + e] = r[v][e];
+      for (int e = 0; e < 4; ++e) L[row * LA + 4 * quad + e] = keep_if(r[v][e], rok && k0 + 4 * quad + e < g.K);
     }
   };
   // B tile (not transposed): 32 k x 128 n -> 1024 float4
@@ -91,37 +98,36 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int idx = v * GNT + tid;
-      const int krow = idx >> 5, quad = idx & 31;
-      const int64_t gk = k0 + krow, gn = n0 + 4 * quad;
-      f32x4_t x = {0.f, 0.f, 0.f, 0.f};
-      if (gk < g.K) {
-        const float* src = B + gk * g.ldb + gn;
-        if (vec_b && gn + 3 < g.N) {
-          x = *reinterpret_cast<const f32x4_t*>(src);
-        } else {
+      const int64_t gk = k0 + (idx >> 5), gn = n0 + 4 * (idx & 31);
+      const int64_t gkc = gk < g.K ? gk : g.K - 1;
+      if (vec_bn) {
+        const int64_t gnc = gn < g.N ? gn : g.N - 4;
+        r[v] = *reinterpret_cast<const f32x4_t*>(B + gkc * g.ldb + gnc);
+      } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (gn + e < g.N) x[e] = src[e];
-        }
+        for (int e = 0; e < 4; ++e) r[v][e] = B[gkc * g.ldb + (gn + e < g.N ? gn + e : g.N - 1)];
       }
-      r[v] = x;
     }
   };
-  auto store_kn = [&](float* L, const f32x4_t* r) {
+  auto store_kn = [&](float* L, const f32x4_t* r, int64_t k0) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int idx = v * GNT + tid;
       const int krow = idx >> 5, quad = idx & 31;
-      *reinterpret_cast<f32x4_t*>(L + krow * LBN + 4 * quad) = r[v];
+      const bool kok = k0 + krow < g.K;
+      f32x4_t x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = keep_if(r[v][e], kok && n0 + 4 * quad + e < g.N);
+      *reinterpret_cast<f32x4_t*>(L + krow * LBN + 4 * quad) = x;
     }
   };
 
   const int64_t nst = (g.K + GBK - 1) / GBK;
   if (nst > 0) {
     load_mk(A, g.lda, vec_a, g.M, m0, 0, ra);
-    if (BT) load_mk(B, g.ldb, vec_b, g.N, n0, 0, rb); else load_kn(0, rb);
-    store_mk(lds_a[0], ra);
-    if (BT) store_mk(lds_b[0], rb); else store_kn(lds_b[0], rb);
+    if (BT) load_mk(B, g.ldb, vec_bk, g.N, n0, 0, rb); else load_kn(0, rb);
+    store_mk(lds_a[0], ra, g.M, m0, 0);
+    if (BT) store_mk(lds_b[0], rb, g.N, n0, 0); else store_kn(lds_b[0], rb, 0);
   }
   __syncthreads();
   for (int64_t st = 0; st < nst; ++st) {
@@ -129,7 +135,7 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
     const bool more = st + 1 < nst;
     if (more) {
       load_mk(A, g.lda, vec_a, g.M, m0, (st + 1) * GBK, ra);
-      if (BT) load_mk(B, g.ldb, vec_b, g.N, n0, (st + 1) * GBK, rb); else load_kn((st + 1) * GBK, rb);
+      if (BT) load_mk(B, g.ldb, vec_bk, g.N, n0, (st + 1) * GBK, rb); else load_kn((st + 1) * GBK, rb);
     }
     const float* la = lds_a[buf];
     const float* lb = lds_b[buf];
@@ -151,12 +157,26 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
           acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[bm], fb[bn], acc[bm][bn], 0, 0, 0);
     }
     if (more) {
-      store_mk(lds_a[buf ^ 1], ra);
-      if (BT) store_mk(lds_b[buf ^ 1], rb); else store_kn(lds_b[buf ^ 1], rb);
+      store_mk(lds_a[buf ^ 1], ra, g.M, m0, (st + 1) * GBK);
+      if (BT) store_mk(lds_b[buf ^ 1], rb, g.N, n0, (st + 1) * GBK); else store_kn(lds_b[buf ^ 1], rb, (st + 1) * GBK);
     }
     __syncthreads();
   }
 
+  // C is read (clamped, all loads in flight together) before any store
+  float cv[64];
+  if (g.beta != 0.f) {
+#pragma unroll
+    for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+      for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t gm = m0 + wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const int64_t gn = n0 + wn * 64 + bn * 32 + (lane & 31);
+          cv[(bm * 2 + bn) * 16 + r] = C[(gm < g.M ? gm : g.M - 1) * g.ldc + (gn < g.N ? gn : g.N - 1)];
+        }
+  }
 #pragma unroll
   for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
@@ -166,11 +186,131 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
         const int64_t gm = m0 + wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int64_t gn = n0 + wn * 64 + bn * 32 + (lane & 31);
         if (gm < g.M && gn < g.N && (!g.lower_only || gm >= gn)) {
-          float* cp = C + gm * g.ldc + gn;
           const float prod = g.alpha * acc[bm][bn][r];
-          *cp = g.beta == 0.f ? prod : g.beta * *cp + prod;
+          C[gm * g.ldc + gn] = g.beta == 0.f ? prod : g.beta * cv[(bm * 2 + bn) * 16 + r] + prod;
         }
       }
+}
+
+// ---------------------------------------------------------------- K <= 128 GEMM
+// The solve's panel GEMMs all have K = 128 (one panel of columns): the
+// Cholesky panel solve and trailing update, and GPTQ's lazy update.  A
+// workgroup keeps its 128-row tile of A (all of K) in LDS and walks the
+// column tiles n = blockIdx.x, blockIdx.x + gridDim.x, ...; the next B tile
+// and the current C tile are fetched into registers while the MFMAs of the
+// current tile run, so every load after the first overlaps compute.
+constexpr int KT = 128;          // tile edge and largest K
+constexpr int KLA = KT + 2;      // LDS stride of [row][k] tiles: lanes m, k and m, k+1 hit distinct banks
+
+// Whole tiles only: K == 128, M and N multiples of 128, 16-byte aligned rows
+// (other shapes take the general kernel).  Every address is a wave-uniform
+// tile base plus a 32-bit lane offset, with no clamping, so the loads issue
+// back to back from few registers.
+template <bool BT>
+__global__ __launch_bounds__(GNT, 1) void gemm_k128_kernel(GemmArgs g) {
+  __shared__ float la[KT * KLA];
+  __shared__ float lb[BT ? KT * KLA : KT * LBN];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * KT;
+  const int64_t ntiles = g.N / KT;
+  int64_t nt = blockIdx.x;
+  if (nt >= ntiles || (g.lower_only && nt * KT > m0)) return;
+
+  // [row][k] tiles: float4 v covers row 8 v + tid / 32, k 4 (tid % 32)
+  // lane offsets in bytes (32-bit: uniform base + lane offset addressing)
+  const uint32_t off_a = (uint32_t)((tid >> 5) * g.lda + 4 * (tid & 31)) * 4u;
+  const uint32_t off_b = (uint32_t)((tid >> 5) * g.ldb + 4 * (tid & 31)) * 4u;
+  const uint32_t off_c = (uint32_t)((wm * 64 + 4 * (lane >> 5)) * g.ldc + wn * 64 + (lane & 31)) * 4u;
+  auto at = [](const float* base, uint32_t off) {
+    return reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off);
+  };
+  auto load_rows = [&](const float* base, int64_t ld, uint32_t off, f32x4_t* r) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) r[v] = *reinterpret_cast<const f32x4_t*>(at(base + 8 * v * ld, off));
+  };
+  auto store_rk = [&](float* L, const f32x4_t* r) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int row = 8 * v + (tid >> 5), k4 = 4 * (tid & 31);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) L[row * KLA + k4 + e] = r[v][e];
+    }
+  };
+  auto store_kn = [&](const f32x4_t* r) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      *reinterpret_cast<f32x4_t*>(lb + (8 * v + (tid >> 5)) * LBN + 4 * (tid & 31)) = r[v];
+  };
+  auto b_tile = [&](int64_t t) { return BT ? g.B + t * KT * g.ldb : g.B + t * KT; };
+
+  f32x4_t rv[16];
+  load_rows(g.A + m0 * g.lda, g.lda, off_a, rv);
+  store_rk(la, rv);
+  load_rows(b_tile(nt), g.ldb, off_b, rv);
+  if (BT) store_rk(lb, rv); else store_kn(rv);
+  __syncthreads();
+
+  for (;;) {
+    const int64_t n0 = nt * KT;
+    const int64_t nn = nt + gridDim.x;
+    const bool more = nn < ntiles && !(g.lower_only && nn * KT > m0);
+    if (more) load_rows(b_tile(nn), g.ldb, off_b, rv);
+    float* cbase = g.C + m0 * g.ldc + n0;
+    float cv[64];
+    if (g.beta != 0.f) {
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+        for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            cv[(bm * 2 + bn) * 16 + r] = *at(cbase + (bm * 32 + 8 * (r >> 2) + (r & 3)) * g.ldc + bn * 32, off_c);
+    }
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+#pragma unroll 8
+    for (int kk = 0; kk < KT / 2; ++kk) {
+      const int k = 2 * kk + (lane >> 5);
+      float fa[2], fb[2];
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm) fa[bm] = la[(wm * 64 + bm * 32 + (lane & 31)) * KLA + k];
+#pragma unroll
+      for (int bn = 0; bn < 2; ++bn) {
+        const int n = wn * 64 + bn * 32 + (lane & 31);
+        fb[bn] = BT ? lb[n * KLA + k] : lb[k * LBN + n];
+      }
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+        for (int bn = 0; bn < 2; ++bn)
+          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[bm], fb[bn], acc[bm][bn], 0, 0, 0);
+    }
+    const bool diag = g.lower_only && n0 == m0;  // only the diagonal tile straddles gm >= gn
+#pragma unroll
+    for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+      for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int tm = wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const int tn = wn * 64 + bn * 32 + (lane & 31);
+          const float prod = g.alpha * acc[bm][bn][r];
+          const float out = g.beta == 0.f ? prod : g.beta * cv[(bm * 2 + bn) * 16 + r] + prod;
+          if (!diag || tm >= tn)
+            *const_cast<float*>(at(cbase + (bm * 32 + 8 * (r >> 2) + (r & 3)) * g.ldc + bn * 32, off_c)) = out;
+        }
+    if (!more) break;
+    __syncthreads();  // every wave is done reading lb
+    if (BT) store_rk(lb, rv); else store_kn(rv);
+    __syncthreads();
+    nt = nn;
+  }
 }
 
 // ---------------------------------------------------------------- Cholesky pieces
@@ -180,14 +320,18 @@ constexpr int PNT = 256;       // threads of the diagonal-block kernel (4 waves)
 constexpr int LP = NB + 1;     // LDS row stride
 constexpr int LT = 2 * SB + 1; // LDS row stride of the product scratch
 
-__device__ __forceinline__ float rdlane(float v, int l) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+// Value of v in lane l (same l for every lane), through the LDS crossbar.
+__device__ __forceinline__ float bperm(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(l << 2, __float_as_int(v)));
 }
 
 // acc += sum_k A[m][k] * op(B)[k][n] over a 32 x 32 tile, operands in LDS
 // (A row-major lda; B row-major [k][n] (ldb) or, if bt, [n][k]).  K even.
 __device__ __forceinline__ void lds_mfma_tile(f32x16_t& acc, const float* A, int lda, const float* B, int ldb,
                                               bool bt, int K, int lane, float sign) {
+  // K is a literal at every call site: fully unrolled after inlining, so the
+  // LDS reads of later steps are issued ahead of the MFMA chain
+#pragma unroll
   for (int k2 = 0; k2 < K; k2 += 2) {
     const int k = k2 + (lane >> 5);
     const float av = sign * A[(lane & 31) * lda + k];
@@ -221,18 +365,26 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
                                                         float* linv, int32_t* status) {
   __shared__ float a[NB * LP];
   __shared__ float x[NB * LP];
-  __shared__ float t[2 * SB * LT];
+  __shared__ __attribute__((aligned(16))) float t[2 * SB * LT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  // load: 64 independent loads per thread in flight
-#pragma unroll 16
-  for (int v = 0; v < NB * NB / PNT; ++v) {
-    const int e = v * PNT + tid;
-    const int i = e / NB, j = e % NB;
-    float val = (i == j) ? 1.f : 0.f;
-    if (i < nb && j < nb && j <= i) val = F[(k0 + i) * ldf + (k0 + j)];
-    a[i * LP + j] = val;
-    x[i * LP + j] = 0.f;
+  // load: all 64 loads per thread issued before any is consumed; addresses
+  // are clamped into the block so no load needs a branch
+  {
+    float lv[NB * NB / PNT];
+#pragma unroll
+    for (int v = 0; v < NB * NB / PNT; ++v) {
+      const int e = v * PNT + tid;
+      const int i = min(e / NB, nb - 1), j = min(e % NB, nb - 1);
+      lv[v] = F[(k0 + i) * ldf + (k0 + j)];
+    }
+#pragma unroll
+    for (int v = 0; v < NB * NB / PNT; ++v) {
+      const int e = v * PNT + tid;
+      const int i = e / NB, j = e % NB;
+      a[i * LP + j] = (i < nb && j < nb && j <= i) ? lv[v] : ((i == j) ? 1.f : 0.f);
+      x[i * LP + j] = 0.f;
+    }
   }
   __syncthreads();
 
@@ -240,48 +392,58 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
   for (int kb = 0; kb < NB / SB; ++kb) {
     const int o = kb * SB;
     if (wave == 0) {
-      const int row = o + (lane & 31);
-      float r[SB], q[SB];
+      // Lanes 0..31 each hold one row of the sub-block.  LDS operations of
+      // one wave complete in program order, so the column buffer needs no
+      // barrier between its write and the reads that follow.
+      const int li = lane & 31;
+      const int row = o + li;
+      float* cb = t;  // 32-float buffer (t is idle during the factorisation)
+      float r[SB];
 #pragma unroll
-      for (int c = 0; c < SB; ++c) {
-        r[c] = a[row * LP + o + c];
-        q[c] = (c == (lane & 31)) ? 1.f : 0.f;
-      }
-      // right-looking Cholesky of the sub-block.  Entries above the diagonal
-      // (c > lane) are updated too: they are never read into the lower
-      // triangle, which keeps every update unpredicated.
+      for (int c = 0; c < SB; ++c) r[c] = a[row * LP + o + c];
+      // right-looking Cholesky.  Column j's entries reach every lane through
+      // ds_bpermute (a VGPR result, so no SGPR pressure however many are in
+      // flight): L[i][j] L[c][j] = A[i][j] A[c][j] / piv, one FMA each.
+      // Entries above the diagonal (c > row) are updated too and never read
+      // into the lower triangle, which keeps every update unpredicated.
 #pragma unroll
       for (int j = 0; j < SB; ++j) {
-        float piv = rdlane(r[j], j);
+        float piv = bperm(r[j], j);
         if (!(piv > 0.f) || !isfinite(piv)) {
           bad = true;
           piv = 1.f;
         }
         const float ljj = sqrtf(piv);
-        const float inv = 1.f / ljj;
-        r[j] = (lane == j) ? ljj : r[j] * inv;
+        const float tj = r[j] * (1.f / piv);
 #pragma unroll
-        for (int c = j + 1; c < SB; ++c) r[c] = fmaf(-r[j], rdlane(r[j], c), r[c]);
+        for (int c = j + 1; c < SB; ++c) r[c] = fmaf(-tj, bperm(r[j], c), r[c]);
+        r[j] = (li == j) ? ljj : r[j] / ljj;
       }
-      // inverse by row elimination of [L | I]: lane i holds row i of L^-1;
-      // rows above j are final, so their multiplier is zero
+      // store L and the reciprocal diagonal
+      if (lane < SB) {
 #pragma unroll
-      for (int j = 0; j < SB; ++j) {
-        const float fac = (lane == j) ? 1.f / rdlane(r[j], j) : 1.f;
+        for (int c = 0; c < SB; ++c)
+          if (c <= li) a[row * LP + o + c] = r[c];
+        cb[li] = 1.f / r[li];
+      }
+      // inverse: lane c solves L x = e_c by forward substitution (column c
+      // of L^-1); every lane reads the same L entries (LDS broadcast)
+      float xv[SB];
 #pragma unroll
-        for (int c = 0; c <= j; ++c) q[c] *= fac;
-        const float m = (lane > j) ? r[j] : 0.f;
+      for (int i = 0; i < SB; ++i) {
+        float s0 = (i == li) ? 1.f : 0.f, s1 = 0.f;
 #pragma unroll
-        for (int c = 0; c <= j; ++c) q[c] = fmaf(-m, rdlane(q[c], j), q[c]);
+        for (int k = 0; k + 1 < i; k += 2) {
+          s0 = fmaf(-a[(o + i) * LP + o + k], xv[k], s0);
+          s1 = fmaf(-a[(o + i) * LP + o + k + 1], xv[k + 1], s1);
+        }
+        if (i & 1) s0 = fmaf(-a[(o + i) * LP + o + i - 1], xv[i - 1], s0);
+        xv[i] = (s0 + s1) * cb[i];
       }
       if (lane < SB) {
 #pragma unroll
-        for (int c = 0; c < SB; ++c) {
-          if (c <= lane) {
-            a[row * LP + o + c] = r[c];
-            x[row * LP + o + c] = q[c];
-          }
-        }
+        for (int i = 0; i < SB; ++i)
+          if (i >= li) x[(o + i) * LP + o + li] = xv[i];
       }
     }
     __syncthreads();
@@ -451,6 +613,23 @@ HinvLayout hinv_layout(int64_t d) {
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
+  const bool k128 = batch == 1 && g.K == KT && g.M % KT == 0 && g.N % KT == 0 && g.lda % 4 == 0 &&
+                    g.ldb % 4 == 0 && aligned16(g.A) && aligned16(g.B) && (g.lda * 7 + KT) < (1 << 29) &&
+                    (g.ldb * 7 + KT) < (1 << 29) && (g.ldc * 127 + KT) < (1 << 29);
+  if (k128) {
+    // one workgroup per CU: spread the column tiles so ~256 workgroups run
+    const int64_t mt = g.M / KT, ntl = g.N / KT;
+    int64_t p = (256 + mt - 1) / mt;
+    if (p > ntl) p = ntl;
+    if (p < 1) p = 1;
+    dim3 grid((unsigned)p, (unsigned)mt, 1);
+    if (b_trans)
+      hipLaunchKernelGGL(gemm_k128_kernel<true>, grid, dim3(GNT), 0, stream, g);
+    else
+      hipLaunchKernelGGL(gemm_k128_kernel<false>, grid, dim3(GNT), 0, stream, g);
+    MQ_LAUNCH_CHECK();
+    return MI355Q_OK;
+  }
   dim3 grid((unsigned)((g.N + GBN - 1) / GBN), (unsigned)((g.M + GBM - 1) / GBM), (unsigned)batch);
   if (b_trans)
     hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(GNT), 0, stream, g);
