@@ -153,6 +153,21 @@ def main():
                     "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": int(nbytes)}
         del t, out
 
+    # plain elementwise copy of 1 GiB (read 1 GiB, write 1 GiB): measured
+    # copy bandwidth, and the known-size kernel that scales the FETCH_SIZE /
+    # WRITE_SIZE counters
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.mul(src, 1.0, out=dst)
+    e0.record(stream)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    copy_ms = e0.elapsed_time(e1) / 3
+    copy_gbs = 2 * src.numel() * 4 / (copy_ms * 1e-3) / 1e9
+    del src, dst
+
     traffic = None
     tf = ROOT / "profiles" / "hessian_syrk_traffic.json"
     if tf.exists():
@@ -181,6 +196,7 @@ def main():
                     "frac_fp32_mfma_peak": round(syrk_tflops / PEAK_FP32_MFMA_TFLOPS, 3),
                     "frac_bf16_mfma_peak": round(syrk_tflops / PEAK_BF16_TFLOPS, 4)},
         "mxfp4_quantize_pack": mx,
+        "copy_1GiB_GB_s": round(copy_gbs, 1),
         "roofline": {"bound": "mfma", "achieved": round(syrk_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(syrk_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "kernel": "syrk_bf16_kernel + syrk_reduce_kernel (Hessian, 131072 tokens)"},

@@ -273,55 +273,66 @@ __device__ __forceinline__ float exp2i(int k) {  // 2^k for k in [-149, 127]
   return __uint_as_float(1u << (k + 149));
 }
 
-// e2m1 code of v (already divided by the shared scale), CT cast_to_fp4
-// thresholds, sign bit set for strictly negative inputs.
-__device__ __forceinline__ uint32_t e2m1_code(float v) {
-  float a = fminf(fabsf(v), 6.f);
-  uint32_t idx = a <= 0.25f ? 0u : a < 0.75f ? 1u : a <= 1.25f ? 2u : a < 1.75f ? 3u
-               : a <= 2.5f ? 4u : a < 3.5f ? 5u : a <= 5.f ? 6u : 7u;
-  return idx | (v < 0.f ? 8u : 0u);
-}
+constexpr int MX_U = 4;  // chunks per lane, loads issued together
 
-// Each lane handles 8 consecutive elements; 4 lanes form a 32-element group.
 __global__ __launch_bounds__(NT) void mxfp4_quantize_pack_kernel(const uint16_t* __restrict__ x,
                                                                   int64_t rows, int64_t cols,
                                                                   int64_t ldx, int rule,
                                                                   uint32_t* __restrict__ codes,
                                                                   uint8_t* __restrict__ scales) {
-  const int64_t cpr = cols / 8;  // chunks per row
+  // chunk = 8 bf16 (16 B); four consecutive lanes hold one 32-element group.
+  // Workgroup b owns chunks [b NT U, (b+1) NT U); lane t takes chunks
+  // b NT U + u NT + t, so every load instruction is fully coalesced.  A group's
+  // four lanes are live or dead together (cols / 8 is a multiple of 4).
+  const int64_t cpr = cols / 8;
   const int64_t total = rows * cpr;
-  const int64_t stride = (int64_t)gridDim.x * NT;
-  for (int64_t c = (int64_t)blockIdx.x * NT + threadIdx.x; c - (threadIdx.x & 3) < total; c += stride) {
-    const bool live = c < total;
-    int64_t r = 0, k = 0;
-    u32x4_t v = {0u, 0u, 0u, 0u};
-    if (live) {
-      r = c / cpr;
-      k = c - r * cpr;
-      v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + r * ldx + 8 * k));
+  const int64_t c0 = (int64_t)blockIdx.x * NT * MX_U + threadIdx.x;
+  const bool dense = ldx == cols;
+  u32x4_t v[MX_U];
+#pragma unroll
+  for (int u = 0; u < MX_U; ++u) {
+    const int64_t c = c0 + (int64_t)u * NT;
+    const int64_t cc = c < total ? c : total - 1;
+    int64_t off = 8 * cc;
+    if (!dense) {
+      const int64_t r = cc / cpr;
+      off = r * ldx + 8 * (cc - r * cpr);
     }
+    v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + off));
+  }
+#pragma unroll
+  for (int u = 0; u < MX_U; ++u) {
+    const int64_t c = c0 + (int64_t)u * NT;
     uint32_t am = 0;  // max |x| as bf16 bits (order-preserving for non-negative)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      uint32_t lo = v[q] & 0x7fffu, hi = (v[q] >> 16) & 0x7fffu;
+      const uint32_t lo = v[u][q] & 0x7fffu, hi = (v[u][q] >> 16) & 0x7fffu;
       am = max(am, max(lo, hi));
     }
     am = max(am, (uint32_t)__shfl_xor((int)am, 1));
     am = max(am, (uint32_t)__shfl_xor((int)am, 2));
-    if (!live) continue;
     const int e8 = mx_exponent(__uint_as_float(am << 16), rule);
     // e8 in [0, 254]: dividing by 2^(e8-127) is an exact multiply by 2^(127-e8)
     const float inv = exp2i(127 - e8);
+    // gfx950's fp4 conversion rounds to nearest-even on the e2m1 grid and
+    // saturates at 6, which is the cast_to_fp4 rule; it takes the sign from
+    // the sign bit, so -0.0 is turned into +0.0 first (the rule sets the sign
+    // only for v < 0).  The scale operand is 1: x is pre-multiplied by the
+    // exact power of two 1 / 2^(e8 - 127).
     uint32_t word = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float a = __uint_as_float(v[q] << 16) * inv;
-      const float b = __uint_as_float(v[q] & 0xffff0000u) * inv;
-      word |= e2m1_code(a) << (8 * q);
-      word |= e2m1_code(b) << (8 * q + 4);
+    word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, __uint_as_float(v[u][0] << 16) * inv + 0.f,
+                                                   __uint_as_float(v[u][0] & 0xffff0000u) * inv + 0.f, 1.f, 0);
+    word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, __uint_as_float(v[u][1] << 16) * inv + 0.f,
+                                                   __uint_as_float(v[u][1] & 0xffff0000u) * inv + 0.f, 1.f, 1);
+    word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, __uint_as_float(v[u][2] << 16) * inv + 0.f,
+                                                   __uint_as_float(v[u][2] & 0xffff0000u) * inv + 0.f, 1.f, 2);
+    word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, __uint_as_float(v[u][3] << 16) * inv + 0.f,
+                                                   __uint_as_float(v[u][3] & 0xffff0000u) * inv + 0.f, 1.f, 3);
+    if (c < total) {
+      // dense outputs: codes [rows][cols / 8] words, scales [rows][cols / 32]
+      __builtin_nontemporal_store(word, codes + c);
+      if ((threadIdx.x & 3) == 0) scales[c >> 2] = (uint8_t)e8;
     }
-    __builtin_nontemporal_store(word, codes + r * (cols / 8) + k);
-    if ((threadIdx.x & 3) == 0) scales[r * (cols / 32) + k / 4] = (uint8_t)e8;
   }
 }
 
@@ -552,8 +563,8 @@ extern "C" int mi355q_mxfp4_quantize_pack(const void* x_dev, int64_t rows, int64
   MQ_CHECK_ARG((reinterpret_cast<uintptr_t>(codes_dev) & 3) == 0, "mxfp4: codes must be 4-byte aligned");
   MQ_CHECK_ARG(rule == MI355Q_MX_RULE_CT || rule == MI355Q_MX_RULE_OCP, "mxfp4: unknown rule");
   const int64_t chunks = rows * (cols / 8);
-  // enough workgroups for ~8 per CU resident, each lane streaming several chunks
-  unsigned g = grid_for(chunks, NT, 256u * 16u);
+  MQ_CHECK_ARG((chunks + (int64_t)NT * MX_U - 1) / ((int64_t)NT * MX_U) < (int64_t(1) << 31), "mxfp4: too large");
+  const unsigned g = (unsigned)((chunks + (int64_t)NT * MX_U - 1) / ((int64_t)NT * MX_U));
   hipLaunchKernelGGL(mxfp4_quantize_pack_kernel, dim3(g), dim3(NT), 0, reinterpret_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(x_dev), rows, cols, ldx, rule,
                      reinterpret_cast<uint32_t*>(codes_dev), scales_dev);
