@@ -4,17 +4,21 @@
 // d x d matrix) with a syrk that computes and writes only the tiles on or
 // above the diagonal.  X rows are tokens (bf16, feature-contiguous); the
 // contraction runs over tokens, so both MFMA operands need token-contiguous
-// fragments: each thread loads an 8-token x 8-feature block with eight
-// 16-byte loads and transposes it in registers (v_perm) before the LDS
-// store.  bf16 x bf16 products are exact in fp32 and accumulate in fp32
+// fragments.  bf16 x bf16 products are exact in fp32 and accumulate in fp32
 // (v_mfma_f32_32x32x16_bf16).
 //
+// Two tile kernels share the work decomposition below:
+//  * syrk_stream_kernel (dense X, d >= 512): 256 x 256 tiles streamed
+//    global -> LDS by LDS-DMA in token-major layout and read back with the
+//    transposing LDS load (details at the kernel);
+//  * syrk_bf16_kernel (row-gathered X for per-expert Hessians, and d < 512):
+//    each thread loads an 8-token x 8-feature block with eight 16-byte loads
+//    and transposes it in registers (v_perm) before the LDS store; the
+//    transposed stores map lane -> (feature block, token block) with the
+//    token block fastest, which keeps 16 consecutive lanes on distinct LDS
+//    banks (row stride 144 B = 9 x 16 B).
 // Tiles are TM x TM (TM = 256 for d >= 512, else 128) on a 2 x 2 grid of
-// waves; each wave owns a (TM/2)^2 block of 32 x 32 MFMA tiles, so one 16-token
-// step issues (TM/64)^2 MFMAs per TM/16 fragment reads.  The transposed
-// stores map lane -> (feature block, token block) with the token block
-// fastest, which keeps 16 consecutive lanes on distinct LDS banks
-// (row stride 144 B = 9 x 16 B).
+// waves; each wave owns a (TM/2)^2 block of 32 x 32 MFMA tiles.
 //
 // Work decomposition: a work item is (matrix e, upper tile t, token split s).
 // Token splits are assigned by blockIdx % S, and workgroups are dispatched
@@ -65,16 +69,40 @@ struct SyrkParams {
   float* ws;               // partial tiles
 };
 
+// The t-th tile on or above the diagonal, in super-block order: super-blocks
+// of SBK x SBK tiles (I <= J, row-major), tiles inside row-major.  Workgroups
+// of one XCD run consecutive t together, so a round of concurrent tiles
+// touches about 2 SBK feature slices of X instead of all of them, and the
+// slices it streams are shared through that XCD's L2.
 __device__ __forceinline__ void tile_coords(int t, int nt, int& ti, int& tj) {
-  int r = 0;
-  int rowlen = nt;
-  while (t >= rowlen) {
-    t -= rowlen;
-    ++r;
-    --rowlen;
+  constexpr int SBK = 8;
+  const int nb = (nt + SBK - 1) / SBK;
+  for (int I = 0; I < nb; ++I) {
+    const int i0 = I * SBK, i1 = min(nt, i0 + SBK);
+    for (int J = I; J < nb; ++J) {
+      const int j0 = J * SBK, j1 = min(nt, j0 + SBK);
+      const int m = i1 - i0, w = j1 - j0;
+      const int cnt = I == J ? m * (m + 1) / 2 : m * w;
+      if (t < cnt) {
+        if (I == J) {
+          int r = 0, rowlen = m;
+          while (t >= rowlen) {
+            t -= rowlen;
+            ++r;
+            --rowlen;
+          }
+          ti = i0 + r;
+          tj = i0 + r + t;
+        } else {
+          ti = i0 + t / w;
+          tj = j0 + t % w;
+        }
+        return;
+      }
+      t -= cnt;
+    }
   }
-  ti = r;
-  tj = r + t;
+  ti = tj = 0;  // t >= nt (nt + 1) / 2 is never launched
 }
 
 __device__ __forceinline__ unsigned perm_lo(unsigned a, unsigned b) {
@@ -289,6 +317,211 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
       }
 }
 
+// ---------------------------------------------------------------- streaming syrk
+// Dense X, 256 x 256 tiles.  Tiles of X are copied global -> LDS by the
+// gfx950 LDS-DMA load (global_load_lds_dwordx4: no registers, no VALU) in
+// their natural token-major layout, through a ring of NSTG stages of SK
+// tokens, so the loads of stage s + NSTG - 1 are in flight while stage s is
+// multiplied.  The MFMA operands (8 consecutive tokens of one feature per
+// lane) are read with the transposing LDS load ds_read_b64_tr_b16: for lane
+// L = 16 g + 4 q + r it returns element r of the 8-byte rows supplied by
+// lanes 16 g + 4 e + q, e = 0..3.  Each token row (256 features, 512 B) is
+// stored with its 16-byte chunks XOR-swizzled by 4 (row & 3), which keeps
+// both the DMA writes and the transposed reads free of bank conflicts.
+constexpr int SK = 32;           // tokens per stage
+constexpr int NSTG = 4;          // stages in the LDS ring
+constexpr int SROW = 512;        // bytes per token row of a 256-feature operand
+constexpr int SOP = SK * SROW;   // bytes per operand per stage
+
+typedef short v4s16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s16_t lds_v4s16_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __attribute__((aligned(16))) const uint32_t kZeroChunk[4] = {0u, 0u, 0u, 0u};
+
+__device__ __forceinline__ bf16x8_t tr_pair(const char* lds, int off0, int off1) {
+  const v4s16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s16_t*)(lds + off0));
+  const v4s16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s16_t*)(lds + off1));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
+  using C = Cfg<256>;
+  constexpr int TM = 256;
+  __shared__ __attribute__((aligned(1024))) char a0[SOP], a1[SOP], a2[SOP], a3[SOP];
+  __shared__ __attribute__((aligned(1024))) char b0[SOP], b1[SOP], b2[SOP], b3[SOP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int S = p.S;
+  const int s = blockIdx.x % S;
+  const int t = blockIdx.x / S;
+  const Matrix mat = p.single;
+  const int64_t slot = (S > 1) ? (int64_t)t * S + s : -1;
+  int ti, tj;
+  tile_coords(t, p.nt, ti, tj);
+
+  const int64_t n = mat.row_count;
+  const int64_t nst_total = (n + SK - 1) / SK;
+  const int64_t st_per = (nst_total + S - 1) / S;
+  const int64_t st_begin = (int64_t)s * st_per;
+  int64_t st_end = st_begin + st_per;
+  if (st_end > nst_total) st_end = nst_total;
+  const int64_t nst = st_end > st_begin ? st_end - st_begin : 0;
+
+  // DMA roles: wave w copies token rows 8 w .. 8 w + 7 of each operand, two
+  // rows (1 KB) per instruction j; lane L fills LDS position L & 31 of row
+  // 8 w + 2 j + L / 32 with global chunk (L & 31) ^ 4 (row & 3).
+  const int64_t fa0 = (int64_t)ti * TM, fb0 = (int64_t)tj * TM;
+  const bool edge = fa0 + TM > p.d || fb0 + TM > p.d;
+  uint32_t doff[4];    // lane byte offsets from the stage's first token row
+  int drow[4], dchunk[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * wave + 2 * j + (lane >> 5);
+    const int chunk = (lane & 31) ^ (4 * (row & 3));
+    drow[j] = row;
+    dchunk[j] = chunk;
+    doff[j] = (uint32_t)(row * p.ldx + 8 * chunk) * 2u;
+  }
+  // The DMA is issued from inline asm so that the compiler does not treat
+  // every later LDS read as dependent on it (it cannot tell the ring slots
+  // apart and would wait for all DMA in flight); completion is tracked
+  // explicitly with vmcnt before each stage's barrier and after the loop.
+  auto dma = [&](const void* gaddr, char* lds) __attribute__((always_inline)) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(m0) : "memory", "m0");
+  };
+  auto issue = [&](int64_t stage, char* la, char* lb) __attribute__((always_inline)) {
+    const int64_t tok0 = (stage < nst ? stage : nst - 1) + st_begin;
+    const int64_t t0 = tok0 * SK;
+    const bool slow = edge || t0 + SK > n;
+    const char* xa = reinterpret_cast<const char*>(p.x + (mat.row_begin + t0) * p.ldx + fa0);
+    const char* xb = reinterpret_cast<const char*>(p.x + (mat.row_begin + t0) * p.ldx + fb0);
+    if (!slow) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dma(xa + doff[j], la + (4 * wave + j) * 1024);
+        dma(xb + doff[j], lb + (4 * wave + j) * 1024);
+      }
+    } else {
+      // partial stage or edge tile: rows past n and chunks past d read zeros
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool rok = t0 + drow[j] < n;
+        const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
+        const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
+        dma(aok ? (const void*)(xa + doff[j]) : (const void*)kZeroChunk, la + (4 * wave + j) * 1024);
+        dma(bok ? (const void*)(xb + doff[j]) : (const void*)kZeroChunk, lb + (4 * wave + j) * 1024);
+      }
+    }
+  };
+
+  // transposed-read lane offsets: lane 16 g + 4 e + q supplies row
+  // 8 (g >> 1) + e (+ 16 kk + 4 h) and features 16 (g & 1) + 4 q of the
+  // 32-feature block; with the swizzle the 16-byte position of block b of
+  // wave half w is 16 w + 4 (b ^ e) + 2 (g & 1) + (q >> 1)
+  const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+  const int rbase = (8 * (g >> 1) + e) * SROW + 8 * (q & 1);
+  int ra[C::NB], rb[C::NB];
+#pragma unroll
+  for (int b = 0; b < C::NB; ++b) {
+    ra[b] = rbase + 16 * (16 * wm + 4 * (b ^ e) + 2 * (g & 1) + (q >> 1));
+    rb[b] = rbase + 16 * (16 * wn + 4 * (b ^ e) + 2 * (g & 1) + (q >> 1));
+  }
+
+  f32x16_t acc[C::NB][C::NB];
+#pragma unroll
+  for (int x = 0; x < C::NB; ++x)
+#pragma unroll
+    for (int y = 0; y < C::NB; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+
+  // both 16-token steps of a stage: the reads of step 1 are interleaved with
+  // the MFMAs of step 0 (explicit scheduling groups; operands of the two
+  // steps live in separate registers)
+  auto compute = [&](const char* la, const char* lb) __attribute__((always_inline)) {
+    bf16x8_t fa[2][C::NB], fbv[2][C::NB];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int b = 0; b < C::NB; ++b) {
+        fa[kk][b] = tr_pair(la, ra[b] + kk * 16 * SROW, ra[b] + (kk * 16 + 4) * SROW);
+        fbv[kk][b] = tr_pair(lb, rb[b] + kk * 16 * SROW, rb[b] + (kk * 16 + 4) * SROW);
+      }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int x = 0; x < C::NB; ++x)
+#pragma unroll
+        for (int y = 0; y < C::NB; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk][x], fbv[kk][y], acc[x][y], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4 * C::NB, 0);    // step-0 reads
+#pragma unroll
+    for (int i = 0; i < 4 * C::NB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // step-0 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // step-1 read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, C::NB * C::NB, 0);  // step-1 MFMAs
+  };
+  // one stage: own DMA of this stage done (two later stages may be in
+  // flight), barrier (every wave's DMA done, previous slot free), refill the
+  // freed slot three stages ahead, multiply
+  // (a bare s_barrier: __syncthreads would also wait for the DMA still in
+  // flight for later stages)
+  auto stage = [&](int64_t st, const char* la, const char* lb, char* na, char* nb) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    issue(st + 3, na, nb);
+    compute(la, lb);
+  };
+
+  if (nst > 0) {
+    issue(0, a0, b0);
+    issue(1, a1, b1);
+    issue(2, a2, b2);
+    for (int64_t st = 0; st < nst; st += 4) {
+      stage(st, a0, b0, a3, b3);
+      if (st + 1 < nst) stage(st + 1, a1, b1, a0, b0);
+      if (st + 2 < nst) stage(st + 2, a2, b2, a1, b1);
+      if (st + 3 < nst) stage(st + 3, a3, b3, a2, b2);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+
+  if (slot >= 0) {
+    float* dst = p.ws + (slot * NT + tid) * C::ACC;
+#pragma unroll
+    for (int x = 0; x < C::NB; ++x)
+#pragma unroll
+      for (int y = 0; y < C::NB; ++y)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          f32x4_t v = {acc[x][y][4 * r4], acc[x][y][4 * r4 + 1], acc[x][y][4 * r4 + 2], acc[x][y][4 * r4 + 3]};
+          *reinterpret_cast<f32x4_t*>(dst + (x * C::NB + y) * 16 + 4 * r4) = v;
+        }
+    return;
+  }
+  const int64_t gi0 = fa0, gj0 = fb0;
+#pragma unroll
+  for (int x = 0; x < C::NB; ++x)
+#pragma unroll
+    for (int y = 0; y < C::NB; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = wm * C::W + x * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int nn = wn * C::W + y * 32 + (lane & 31);
+        const int64_t gi = gi0 + m, gj = gj0 + nn;
+        if (gi < p.d && gj < p.d && gi <= gj) {
+          float* hp = mat.h + gi * p.ldh + gj;
+          *hp = *hp + p.alpha * acc[x][y][r];
+        }
+      }
+}
+
 // Sums the S partial slots of a tile in split order and updates H.  Each
 // workgroup finishes one row of 32 x 32 blocks of its wave tiles
 // (blockIdx.y = bm), so a TM = 256 tile is finished by four workgroups.
@@ -378,7 +611,7 @@ void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) 
   const bool g = p.rows != nullptr;
   if (tile_edge(d) == 256) {
     if (g) hipLaunchKernelGGL((syrk_bf16_kernel<256, true>), dim3(grid), dim3(NT), 0, st, p);
-    else   hipLaunchKernelGGL((syrk_bf16_kernel<256, false>), dim3(grid), dim3(NT), 0, st, p);
+    else   hipLaunchKernelGGL(syrk_stream_kernel, dim3(grid), dim3(NT), 0, st, p);
   } else {
     if (g) hipLaunchKernelGGL((syrk_bf16_kernel<128, true>), dim3(grid), dim3(NT), 0, st, p);
     else   hipLaunchKernelGGL((syrk_bf16_kernel<128, false>), dim3(grid), dim3(NT), 0, st, p);
