@@ -40,6 +40,11 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--hessian-calls", type=int, default=1,
                    help="split the 64 x 2048 calibration tokens into this many accumulate_hessian calls")
+    p.add_argument("--workload", default="gptq_w4a16",
+                   choices=["gptq_w4a16", "mxfp4", "gptq_w8a8", "moe", "decoder"],
+                   help="gptq_w4a16 (default): the headline line; the others measure the remaining "
+                        "calibration workloads (MXFP4 pack, W8A8 channel + actorder, MoE experts, "
+                        "Llama-3-8B-shaped decoder layer)")
     return p.parse_args()
 
 
@@ -65,6 +70,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the hot path is measured on "
                                    "one GPU's share; the multi-GPU sharding is described, not run)"}))
         sys.exit(2)
+    if a.workload != "gptq_w4a16":
+        OTHER_WORKLOADS[a.workload](a)
+        return
     import torch
 
     from llmcompressor_amd import _lib, gptq, ops
@@ -226,6 +234,246 @@ def cpu_baseline(torch, w_cpu, x_sample):
             "sample": f"Hessian over {x_sample.shape[0]}x{x_sample.shape[1]} tokens x{scale:g} + one full "
                       f"{ROWS}x{COLS} GPTQ solve (oracle, torch-CPU MKL)",
             "hessian_ms_scaled": round(t_h * scale * 1e3, 1), "solve_ms": round(t_s * 1e3, 1)}
+
+
+# ---------------------------------------------------------------- other workloads
+def _setup():
+    import torch
+    from llmcompressor_amd import _lib
+    _lib.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    return torch, dev
+
+
+def _gpu_heavy(torch, dev, rows, cols, seed, nu=4, lognormal=True, chunk=8192):
+    """Student-t(nu) [x lognormal(0,1) per column] bf16 [rows, cols], generated on the GPU."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    c = torch.exp(torch.randn(cols, generator=g, device=dev)) if lognormal else None
+    out = torch.empty(rows, cols, dtype=torch.bfloat16, device=dev)
+    for r0 in range(0, rows, chunk):
+        m = min(chunk, rows - r0)
+        z = torch.randn(m, cols, generator=g, device=dev)
+        chi = torch.zeros(m, cols, device=dev)
+        for _ in range(nu):
+            chi += torch.randn(m, cols, generator=g, device=dev) ** 2
+        t = z / torch.sqrt(chi / nu)
+        if c is not None:
+            t *= c
+        out[r0:r0 + m] = t.to(torch.bfloat16)
+    return out
+
+
+def _timed(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps, out
+
+
+def _line(metric, value, unit, a, ms, workload, extra, higher=False, dtype="bf16 inputs, fp32 accumulate/solve"):
+    line = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": a.steps,
+            "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": higher, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded, generated on the GPU)",
+            "config": {"workload": workload}}
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+def bench_mxfp4(a):
+    """MXFP4 W4A4 quantize + pack: W [4096, 14336] and A [8192, 14336] bf16."""
+    torch, dev = _setup()
+    from llmcompressor_amd import ops
+    res = {}
+    tot_ms = tot_b = 0.0
+    for name, shape, seed in (("W", (4096, 14336), 2), ("A", (8192, 14336), 3)):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        t = (torch.randn(shape, generator=g, device=dev) * 0.015).to(torch.bfloat16) if name == "W" else \
+            _gpu_heavy(torch, dev, shape[0], shape[1], seed, nu=3, lognormal=False)
+        out = (torch.empty(shape[0], shape[1] // 2, dtype=torch.uint8, device=dev),
+               torch.empty(shape[0], shape[1] // 32, dtype=torch.uint8, device=dev))
+        ms, _ = _timed(torch, lambda: ops.mxfp4_quantize_pack(t, out=out), max(a.steps, 20), max(a.warmup, 3))
+        nbytes = t.numel() * 2.53125
+        res[name] = {"ms": round(ms, 5), "GB_s": round(nbytes / ms / 1e6, 1),
+                     "frac_hbm_peak": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4), "bytes": int(nbytes)}
+        tot_ms += ms
+        tot_b += nbytes
+    gbs = tot_b / tot_ms / 1e6
+    _line("MXFP4 quantize+pack GB/s (W 4096x14336 + A 8192x14336)", gbs, "GB/s", a, tot_ms, "mxfp4_w4a4_pack",
+          {"per_tensor": res, "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}},
+          higher=True, dtype="bf16 in, e2m1 + e8m0 out")
+
+
+def bench_w8a8(a):
+    """GPTQ W8A8: int8 channel-symmetric weights, actorder=weight, W [14336, 4096], X 128 x 2048 tokens,
+    plus per-token dynamic int8 quantization of X."""
+    torch, dev = _setup()
+    from llmcompressor_amd import gptq, ops
+    from llmcompressor_amd.observers import Observer
+    from llmcompressor_amd.quant_args import QuantizationArgs
+    rows, cols, batches, seq = 14336, 4096, 128, 2048
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    w = (torch.randn(rows, cols, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x = _gpu_heavy(torch, dev, batches * seq, cols, 5)
+    lin = torch.nn.Linear(cols, rows, bias=False, device=dev, dtype=torch.bfloat16)
+    lin.weight.data = w
+    qa = QuantizationArgs(num_bits=8, type="int", symmetric=True, strategy="channel", actorder="weight")
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    def step():
+        H = gptq.make_empty_hessian(lin)
+        n = torch.zeros((), device=dev)
+        ev[0].record()
+        H, n = gptq.accumulate_hessian(x.view(batches, seq, cols), lin, H, n)
+        ev[1].record()
+        obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+        obs(lin.weight)
+        r = gptq.gptq_quantize(lin.weight, qa, H, obs, num_samples=float(batches))
+        ev[2].record()
+        return r
+
+    ms, res = _timed(torch, step, a.steps, a.warmup)
+    torch.cuda.synchronize()
+    hess_ms, solve_ms = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+    assert int(res.codes.min()) >= -128 and int(res.codes.max()) <= 127
+    act_ms, _ = _timed(torch, lambda: ops.quantize_int8_per_token(x), 5, 2)
+    act_bytes = x.numel() * 2 + x.numel() + x.shape[0] * 2
+    flop = batches * seq * cols * (cols + 1)
+    _line("GPTQ ms/layer (W8A8 int8 channel, actorder=weight, 14336x4096, Hessian over 128x2048 tokens + solve)",
+          ms, "ms/layer", a, ms, "gptq_w8a8_channel_actorder_14336x4096_128x2048tok",
+          {"phases_ms": {"hessian": round(hess_ms, 3), "solve": round(solve_ms, 3)},
+           "hessian": {"tflops": round(flop / hess_ms / 1e9, 1),
+                       "frac_bf16_mfma_peak": round(flop / hess_ms / 1e9 / PEAK_BF16_TFLOPS, 4)},
+           "act_quant_int8_per_token": {"ms": round(act_ms, 4), "GB_s": round(act_bytes / act_ms / 1e6, 1),
+                                        "frac_hbm_peak": round(act_bytes / act_ms / 1e6 / PEAK_HBM_GBS, 4)}})
+
+
+def bench_moe(a):
+    """MoE expert GPTQ W4A16 g128: 128 experts (gate/up 768x2048, down 2048x768), 32768 tokens routed
+    top-8 (Zipf 1.1 prior + Gumbel): grouped per-expert Hessians + 384 solves."""
+    torch, dev = _setup()
+    from llmcompressor_amd import gptq, moe, workloads
+    from llmcompressor_amd.observers import Observer
+    from llmcompressor_amd.quant_args import QuantizationArgs
+    E, hid, inter, tokens, k = 128, 2048, 768, 32768, 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    gate = (torch.randn(E, inter, hid, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    up = (torch.randn(E, inter, hid, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    down = (torch.randn(E, hid, inter, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    hs = _gpu_heavy(torch, dev, tokens, hid, 7)
+    idx, _ = workloads.moe_routing(tokens, E, k)
+    rows, offsets, _ = moe.route_tokens(idx.to(dev), E)
+    counts = [offsets[e + 1] - offsets[e] for e in range(E)]
+    inter_x = moe.expert_intermediate(hs, rows, offsets, gate, up)   # calibration forward (untimed)
+    ident = torch.arange(inter_x.shape[0], device=dev, dtype=torch.int32)
+    qa = QuantizationArgs(num_bits=4, type="int", symmetric=True, strategy="group", group_size=128)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    def solve(wt, H):
+        obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+        obs(wt)
+        return gptq.gptq_quantize(wt, qa, H, obs, num_samples=1.0)
+
+    def step():
+        Hgu = torch.zeros(E, hid, hid, device=dev)
+        Hd = torch.zeros(E, inter, inter, device=dev)
+        ns = torch.zeros(E, device=dev)
+        ev[0].record()
+        moe.accumulate_expert_hessians(hs, rows, offsets, Hgu, ns)
+        moe.accumulate_expert_hessians(inter_x, ident, offsets, Hd, ns.clone())
+        ev[1].record()
+        for e in range(E):
+            solve(gate[e], Hgu[e])
+            solve(up[e], Hgu[e])
+            solve(down[e], Hd[e])
+        ev[2].record()
+
+    ms, _ = _timed(torch, step, a.steps, a.warmup)
+    torch.cuda.synchronize()
+    hess_ms, solve_ms = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+    flop = sum(c * (hid * (hid + 1) + inter * (inter + 1)) for c in counts)
+    _line("MoE GPTQ ms/layer (128 experts W4A16 g128, 32768 tokens top-8: grouped Hessians + 384 solves)",
+          ms, "ms/layer", a, ms, "moe_128x(768x2048,2048x768)_32768tok_top8",
+          {"phases_ms": {"grouped_hessians": round(hess_ms, 3), "solves": round(solve_ms, 3)},
+           "hessian": {"tflops": round(flop / hess_ms / 1e9, 1),
+                       "frac_bf16_mfma_peak": round(flop / hess_ms / 1e9 / PEAK_BF16_TFLOPS, 4)},
+           "tokens_per_expert": {"min": min(counts), "max": max(counts), "mean": sum(counts) / E}})
+
+
+def bench_decoder(a):
+    """Llama-3-8B-shaped decoder layer, sequential GPTQ W4A16 g128 over 256 x 2048 tokens: four Hessians
+    (q/k/v shared, o, gate/up shared, down d=14336) and seven solves."""
+    torch, dev = _setup()
+    from llmcompressor_amd import gptq
+    from llmcompressor_amd.observers import Observer
+    from llmcompressor_amd.quant_args import QuantizationArgs
+    hidden, inter, kv, batches, seq = 4096, 14336, 1024, 256, 2048
+    ntok = batches * seq
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+
+    def w(r, c):
+        return (torch.randn(r, c, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+    W = {"q_proj": w(hidden, hidden), "k_proj": w(kv, hidden), "v_proj": w(kv, hidden),
+         "o_proj": w(hidden, hidden), "gate_proj": w(inter, hidden), "up_proj": w(inter, hidden),
+         "down_proj": w(hidden, inter)}
+    # module inputs the calibration hooks see (generated / computed untimed)
+    x_attn = _gpu_heavy(torch, dev, ntok, hidden, 10)
+    x_o = _gpu_heavy(torch, dev, ntok, hidden, 11)
+    x_mlp = _gpu_heavy(torch, dev, ntok, hidden, 12)
+    x_down = torch.empty(ntok, inter, dtype=torch.bfloat16, device=dev)
+    for r0 in range(0, ntok, 32768):
+        xm = x_mlp[r0:r0 + 32768]
+        x_down[r0:r0 + 32768] = torch.nn.functional.silu(xm @ W["gate_proj"].t()) * (xm @ W["up_proj"].t())
+    qa = QuantizationArgs(num_bits=4, type="int", symmetric=True, strategy="group", group_size=128)
+    lin = {}
+    for name, wt in W.items():
+        m = torch.nn.Linear(wt.shape[1], wt.shape[0], bias=False, device=dev, dtype=torch.bfloat16)
+        m.weight.data = wt
+        lin[name] = m
+    groups = [(("q_proj", "k_proj", "v_proj"), x_attn), (("o_proj",), x_o), (("gate_proj", "up_proj"), x_mlp),
+              (("down_proj",), x_down)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    def step():
+        Hs = []
+        ev[0].record()
+        for names, xin in groups:
+            m = lin[names[0]]
+            H = gptq.make_empty_hessian(m)
+            n = torch.zeros((), device=dev)
+            H, n = gptq.accumulate_hessian(xin.view(batches, seq, -1), m, H, n)
+            Hs.append(H)
+        ev[1].record()
+        for (names, _), H in zip(groups, Hs):
+            for nm in names:
+                obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+                obs(lin[nm].weight)
+                gptq.gptq_quantize(lin[nm].weight, qa, H, obs, num_samples=float(batches))
+        ev[2].record()
+
+    ms, _ = _timed(torch, step, a.steps, a.warmup)
+    torch.cuda.synchronize()
+    hess_ms, solve_ms = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+    flop = 3 * ntok * hidden * (hidden + 1) + ntok * inter * (inter + 1)
+    _line("Decoder-layer GPTQ ms (Llama-3-8B-shaped, W4A16 g128, 256x2048 tokens: 4 Hessians + 7 solves)",
+          ms, "ms/layer", a, ms, "llama3_8b_decoder_layer_w4a16_256x2048tok",
+          {"phases_ms": {"hessians": round(hess_ms, 3), "solves": round(solve_ms, 3)},
+           "hessian": {"tflops": round(flop / hess_ms / 1e9, 1),
+                       "frac_bf16_mfma_peak": round(flop / hess_ms / 1e9 / PEAK_BF16_TFLOPS, 4)}})
+
+
+OTHER_WORKLOADS = {"mxfp4": bench_mxfp4, "gptq_w8a8": bench_w8a8, "moe": bench_moe, "decoder": bench_decoder}
 
 
 if __name__ == "__main__":
