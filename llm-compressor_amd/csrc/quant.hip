@@ -417,6 +417,73 @@ __global__ __launch_bounds__(NT) void int8_per_token_kernel(const uint16_t* x, i
   }
 }
 
+// Vectorised variant (16-byte rows, cols % 8 == 0, cols <= 8 NT CPT): each
+// thread keeps its CPT chunks of 8 elements in registers, so the row is read
+// once; the max |x| is reduced on the bf16 bit patterns (order-preserving for
+// non-negative values), and each chunk is written as 8 int8 codes (8 bytes).
+template <int CPT>
+__global__ __launch_bounds__(NT) void int8_per_token_vec_kernel(const uint16_t* __restrict__ x, int64_t cols,
+                                                                int64_t ldx, int8_t* __restrict__ codes,
+                                                                uint16_t* __restrict__ scale_out) {
+  __shared__ uint32_t smx[NT / 64];
+  const int64_t r = blockIdx.x;
+  const int nch = (int)(cols / 8);
+  const u32x4_t* row = reinterpret_cast<const u32x4_t*>(x + r * ldx);
+  u32x4_t v[CPT];
+  uint32_t am = 0;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + i * NT;
+    v[i] = __builtin_nontemporal_load(row + (c < nch ? c : nch - 1));
+    if (c >= nch) v[i] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) am = max(am, max(v[i][q] & 0x7fffu, (v[i][q] >> 16) & 0x7fffu));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) am = max(am, (uint32_t)__shfl_xor((int)am, o));
+  if ((threadIdx.x & 63) == 0) smx[threadIdx.x >> 6] = am;
+  __syncthreads();
+  am = smx[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) am = max(am, smx[w]);
+  float s = round_to_bf16(__uint_as_float(am << 16) / 127.5f);
+  if (s == 0.f) s = 0.0078125f;
+  if (threadIdx.x == 0) scale_out[r] = f32_to_bf16_bits(s);
+  // x / s by reciprocal and one FMA residual correction (Markstein): the
+  // refined quotient is exact when x / s is representable and within one
+  // fp32 ulp otherwise.  Rounded to bf16 it equals the rounded IEEE quotient:
+  // x / s with 8-bit significands is either a bf16 midpoint exactly or at
+  // least 2^-17 (relative) away from every midpoint.  Scales below 2^-100
+  // (rows of denormal-sized values) take the IEEE division.
+  const bool refine = s >= 0x1p-100f;
+  const float rs = __builtin_amdgcn_rcpf(s);
+  uint32_t* out = reinterpret_cast<uint32_t*>(codes + r * cols);
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + i * NT;
+    if (c < nch) {
+      uint32_t w[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t bits = e & 1 ? (v[i][e >> 1] & 0xffff0000u) : (v[i][e >> 1] << 16);
+        const float xv = __uint_as_float(bits);
+        float q;
+        if (refine) {
+          const float q0 = xv * rs;
+          q = fmaf(fmaf(-q0, s, xv), rs, q0);
+        } else {
+          q = xv / s;
+        }
+        q = round_to_bf16(q);
+        q = fminf(fmaxf(q, -128.f), 127.f);
+        w[e >> 2] |= ((uint32_t)(int32_t)rintf(q) & 0xffu) << (8 * (e & 3));
+      }
+      __builtin_nontemporal_store(w[0], out + 2 * c);
+      __builtin_nontemporal_store(w[1], out + 2 * c + 1);
+    }
+  }
+}
+
 inline unsigned grid_for(int64_t n, int64_t per_block = NT, unsigned cap = 65536u) {
   int64_t g = (n + per_block - 1) / per_block;
   if (g < 1) g = 1;
@@ -603,9 +670,27 @@ extern "C" int mi355q_quantize_int8_per_token(const void* x_dev, int64_t rows, i
                                               int8_t* codes_dev, uint16_t* scale_out_dev, void* stream) {
   MQ_CHECK_ARG(x_dev && codes_dev && scale_out_dev, "int8_per_token: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "int8_per_token: bad shape");
-  hipLaunchKernelGGL(int8_per_token_kernel, dim3((unsigned)rows), dim3(NT), 0,
-                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x_dev), rows, cols,
-                     ldx, codes_dev, scale_out_dev);
+  MQ_CHECK_ARG(rows < (int64_t(1) << 31), "int8_per_token: too many rows");
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uint16_t* x = static_cast<const uint16_t*>(x_dev);
+  const int64_t nch = cols / 8;
+  const bool vec = cols % 8 == 0 && ldx % 8 == 0 && aligned16(x_dev) &&
+                   (reinterpret_cast<uintptr_t>(codes_dev) & 7) == 0;
+  if (vec && nch <= NT)
+    hipLaunchKernelGGL(int8_per_token_vec_kernel<1>, dim3((unsigned)rows), dim3(NT), 0, st, x, cols, ldx, codes_dev,
+                       scale_out_dev);
+  else if (vec && nch <= 2 * NT)
+    hipLaunchKernelGGL(int8_per_token_vec_kernel<2>, dim3((unsigned)rows), dim3(NT), 0, st, x, cols, ldx, codes_dev,
+                       scale_out_dev);
+  else if (vec && nch <= 4 * NT)
+    hipLaunchKernelGGL(int8_per_token_vec_kernel<4>, dim3((unsigned)rows), dim3(NT), 0, st, x, cols, ldx, codes_dev,
+                       scale_out_dev);
+  else if (vec && nch <= 8 * NT)
+    hipLaunchKernelGGL(int8_per_token_vec_kernel<8>, dim3((unsigned)rows), dim3(NT), 0, st, x, cols, ldx, codes_dev,
+                       scale_out_dev);
+  else
+    hipLaunchKernelGGL(int8_per_token_kernel, dim3((unsigned)rows), dim3(NT), 0, st, x, rows, cols, ldx, codes_dev,
+                       scale_out_dev);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
 }

@@ -206,10 +206,35 @@ def test_fp8_exact_all_bf16(dev):
         assert torch.equal(q.view(torch.uint8), oq.view(torch.uint8)), scale
 
 
-def test_int8_per_token_exact(dev):
-    say("int8 per token")
-    x = workloads.heavy_tailed_activations((333, 1024), seed=8)
+@pytest.mark.parametrize("cols", [1024, 4096, 14336, 1000])
+def test_int8_per_token_exact(dev, cols):
+    say(f"int8 per token cols={cols}")
+    x = workloads.heavy_tailed_activations((333, cols), seed=8)
     x[5] = 0
+    codes, scale = ops.quantize_int8_per_token(x.to(dev))
+    oa = OArgs(num_bits=8, strategy="token")
+    mn, mx = x.amin(dim=1, keepdim=True), x.amax(dim=1, keepdim=True)
+    os_, oz = oobs.calculate_qparams(mn, mx, oa)
+    oc = ofq.quantize(x, os_, None, oa)
+    assert torch.equal(scale.cpu(), os_)
+    assert torch.equal(codes.cpu().float(), oc.float())
+
+
+def test_int8_per_token_quotients_all_bf16(dev):
+    """Every finite bf16 value divided by 257 different row scales."""
+    say("int8 per token, all bf16 quotients")
+    b = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    f = (b.astype(np.uint32) << 16).view(np.float32)
+    vals = torch.from_numpy(f[np.isfinite(f)].copy()).reshape(8, -1)   # 8 rows of 8160 values
+    g = torch.Generator().manual_seed(11)
+    amax = torch.cat([torch.tensor([1.0, 127.5, 3.0e38, 1e-30, 0.0078125 * 127.5]),
+                      torch.exp(torch.randn(252, generator=g) * 8.0)])
+    x = vals.unsqueeze(0).repeat(amax.numel(), 1, 1)
+    lim = amax.view(-1, 1, 1)
+    x = torch.maximum(torch.minimum(x, lim), -lim)
+    x[:, :, 0] = lim[:, :, 0]
+    x = x.reshape(-1, vals.shape[1])
+    x = x.to(torch.bfloat16)
     codes, scale = ops.quantize_int8_per_token(x.to(dev))
     oa = OArgs(num_bits=8, strategy="token")
     mn, mx = x.amin(dim=1, keepdim=True), x.amax(dim=1, keepdim=True)
