@@ -361,7 +361,6 @@ def bench_moe(a):
     top-8 (Zipf 1.1 prior + Gumbel): grouped per-expert Hessians + 384 solves."""
     torch, dev = _setup()
     from llmcompressor_amd import gptq, moe, workloads
-    from llmcompressor_amd.observers import Observer
     from llmcompressor_amd.quant_args import QuantizationArgs
     E, hid, inter, tokens, k = 128, 2048, 768, 32768, 8
     g = torch.Generator(device=dev)
@@ -378,11 +377,6 @@ def bench_moe(a):
     qa = QuantizationArgs(num_bits=4, type="int", symmetric=True, strategy="group", group_size=128)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
 
-    def solve(wt, H):
-        obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
-        obs(wt)
-        return gptq.gptq_quantize(wt, qa, H, obs, num_samples=1.0)
-
     def step():
         Hgu = torch.zeros(E, hid, hid, device=dev)
         Hd = torch.zeros(E, inter, inter, device=dev)
@@ -391,10 +385,10 @@ def bench_moe(a):
         moe.accumulate_expert_hessians(hs, rows, offsets, Hgu, ns)
         moe.accumulate_expert_hessians(inter_x, ident, offsets, Hd, ns.clone())
         ev[1].record()
-        for e in range(E):
-            solve(gate[e], Hgu[e])
-            solve(up[e], Hgu[e])
-            solve(down[e], Hd[e])
+        # all experts of one projection solved together (one launch per step)
+        gptq.gptq_quantize_batched(gate, qa, Hgu, num_samples=ns)
+        gptq.gptq_quantize_batched(up, qa, Hgu, num_samples=ns)
+        gptq.gptq_quantize_batched(down, qa, Hd, num_samples=ns)
         ev[2].record()
 
     ms, _ = _timed(torch, step, a.steps, a.warmup)

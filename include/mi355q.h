@@ -88,7 +88,7 @@ int mi355q_symmetrize_upper(float* h_dev, int64_t d, int64_t ldh, void* stream);
 /* ------------------------------------------------------------------ GPTQ
  * mi355q_gptq_hinv: from the accumulated upper-triangle Hessian (optionally
  * permuted by perm_dev, may be NULL), computes
- *   H' = H * inv_num_samples (modifiers/gptq/base.py:594),
+ *   H' = H / num_samples (modifiers/gptq/base.py:594),
  *   dead columns: diag(H') == 0 -> H'_ii = 1, dead_dev[i] = 1
  *     (modifiers/gptq/gptq_quantize.py:35-38),
  *   H' += percdamp * mean(diag(H')) * I  (:182-184),
@@ -100,15 +100,34 @@ int mi355q_symmetrize_upper(float* h_dev, int64_t d, int64_t ldh, void* stream);
  */
 size_t mi355q_gptq_hinv_workspace_size(int64_t d);
 int mi355q_gptq_hinv(const float* h_dev, int64_t ldh, int64_t d, const int32_t* perm_dev,
-                     float inv_num_samples, float percdamp, float* hinv_dev,
+                     float num_samples, float percdamp, float* hinv_dev,
                      int32_t* dead_dev, int32_t* status_dev, void* workspace_dev,
                      size_t workspace_bytes, void* stream);
+
+/* Batched variants.  The reference solves the Hessians of same-shaped modules
+ * (the experts of an MoE layer, modeling/moe/linear_experts.py:244-277) one
+ * module at a time in compress_module_list (modifiers/gptq/base.py:578-601);
+ * these run `batch` independent solves per launch.  Matrix b reads
+ * h + b * stride_h and perm + b * stride_perm (stride 0: shared perm),
+ * num_samples_dev[b], and writes hinv + b * stride_hinv, dead + b * d and
+ * status_dev[b].  Workspace: batch * mi355q_gptq_hinv_workspace_size(d). */
+int mi355q_gptq_hinv_batched(const float* h_dev, int64_t ldh, int64_t stride_h, int64_t d,
+                             int64_t batch, const int32_t* perm_dev, int64_t stride_perm,
+                             const float* num_samples_dev, float percdamp, float* hinv_dev,
+                             int64_t stride_hinv, int32_t* dead_dev, int32_t* status_dev,
+                             void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /* mi355q_gptq_load_weight: w_work[r][j] = dead[j] ? 0 : float(w[r][perm[j]])
  * (fp32 working copy, :121,126,142,178).  perm_dev / dead_dev may be NULL. */
 int mi355q_gptq_load_weight(const void* w_dev, mi355q_dtype w_dtype, int64_t rows, int64_t cols,
                             int64_t ldw, const int32_t* perm_dev, const int32_t* dead_dev,
                             float* w_work_dev, void* stream);
+/* batched: matrix b reads w + b * stride_w (elements), perm + b * stride_perm,
+ * dead + b * cols, and writes w_work + b * rows * cols */
+int mi355q_gptq_load_weight_batched(const void* w_dev, mi355q_dtype w_dtype, int64_t rows, int64_t cols,
+                                    int64_t ldw, int64_t stride_w, int64_t batch,
+                                    const int32_t* perm_dev, int64_t stride_perm,
+                                    const int32_t* dead_dev, float* w_work_dev, void* stream);
 
 /* mi355q_gptq_sweep: the blocked column sweep of :199-277 over the fp32
  * working copy, in place.  Column j is quantised with
@@ -131,6 +150,17 @@ int mi355q_gptq_sweep(float* w_work_dev, int64_t rows, int64_t cols, const float
                       const int32_t* g_idx_dev, int strategy, int block_h, float qmin, float qmax,
                       int dequant_bf16, int64_t blocksize, int8_t* codes_dev, float* losses_dev,
                       void* workspace_dev, size_t workspace_bytes, void* stream);
+/* batched: matrix b uses w_work + b * rows * cols, hinv + b * stride_hinv,
+ * scale / zp + b * stride_scale, g_idx + b * stride_gidx (0: shared),
+ * codes + b * rows * cols, losses + b * rows.
+ * Workspace: batch * mi355q_gptq_sweep_workspace_size(rows, cols, blocksize). */
+int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
+                              const float* hinv_dev, int64_t stride_hinv, const float* scale_dev,
+                              const float* zp_dev, int64_t ld_scale, int64_t stride_scale,
+                              const int32_t* g_idx_dev, int64_t stride_gidx, int strategy, int block_h,
+                              float qmin, float qmax, int dequant_bf16, int64_t blocksize,
+                              int8_t* codes_dev, float* losses_dev, void* workspace_dev,
+                              size_t workspace_bytes, void* stream);
 
 /* mi355q_gptq_store_weight: w_out[r][j] = w_work[r][invperm[j]] converted
  * to out_dtype (:279-284); codes are permuted the same way when
@@ -139,6 +169,12 @@ int mi355q_gptq_store_weight(const float* w_work_dev, int64_t rows, int64_t cols
                              const int32_t* invperm_dev, void* w_out_dev, mi355q_dtype out_dtype,
                              int64_t ld_out, const int8_t* codes_in_dev, int8_t* codes_out_dev,
                              void* stream);
+/* batched: matrix b reads w_work + b * rows * cols, invperm + b * stride_perm,
+ * codes_in + b * rows * cols, writes w_out + b * stride_out, codes_out + b * rows * cols */
+int mi355q_gptq_store_weight_batched(const float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
+                                     const int32_t* invperm_dev, int64_t stride_perm, void* w_out_dev,
+                                     mi355q_dtype out_dtype, int64_t ld_out, int64_t stride_out,
+                                     const int8_t* codes_in_dev, int8_t* codes_out_dev, void* stream);
 
 /* ------------------------------------------------------------------ observers
  * Min/max statistics per strategy (observers/min_max.py:106-110 over

@@ -93,13 +93,30 @@ struct SweepSteps<MAXB> {
   static __device__ __forceinline__ void run(SweepState&, const float*, int, int, float, float, bool) {}
 };
 
+// Element strides between the matrices of a batch (blockIdx.y); zero for a
+// shared operand.
+struct SweepBatch {
+  int64_t w, hinv, scale, gidx, codes, losses, err;
+};
+
 __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
     int count, const float* __restrict__ scale, const float* __restrict__ zp, int64_t ld_scale,
     const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax, int dq_bf16,
-    int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out) {
+    int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, SweepBatch sb) {
   __shared__ float h1[MAXB * MAXB];
   __shared__ int gsh[MAXB];
+  {
+    const int64_t b = blockIdx.y;
+    W += b * sb.w;
+    hinv += b * sb.hinv;
+    scale += b * sb.scale;
+    if (zp) zp += b * sb.scale;
+    if (g_idx) g_idx += b * sb.gidx;
+    codes += b * sb.codes;
+    losses += b * sb.losses;
+    err_out += b * sb.err;
+  }
   const int tid = threadIdx.x;
   const int g = tid & (SW_G - 1);
   const int64_t r = (int64_t)blockIdx.x * SW_ROWS + (tid / SW_G);
@@ -179,8 +196,16 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
 }
 
 // One row per blockIdx.y, four consecutive output columns per thread.
+// (matrix blockIdx.z of a batch: w + z sw elements, perm + z sp, dead + z cols,
+// out + z rows cols)
 __global__ void load_weight_kernel(const void* w, mi355q_dtype dt, int64_t rows, int64_t cols, int64_t ldw,
-                                   const int32_t* perm, const int32_t* dead, float* out) {
+                                   const int32_t* perm, const int32_t* dead, float* out, int64_t sw, int64_t sp) {
+  const int64_t z = blockIdx.z;
+  w = dt == MI355Q_BF16 ? (const void*)(static_cast<const uint16_t*>(w) + z * sw)
+                        : (const void*)(static_cast<const float*>(w) + z * sw);
+  if (perm) perm += z * sp;
+  if (dead) dead += z * cols;
+  out += z * rows * cols;
   const int64_t r = blockIdx.y;
   for (int64_t j4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; j4 < cols;
        j4 += (int64_t)gridDim.x * blockDim.x * 4) {
@@ -204,9 +229,16 @@ __global__ void load_weight_kernel(const void* w, mi355q_dtype dt, int64_t rows,
   }
 }
 
+// (matrix blockIdx.z: w, cin, cout + z rows cols; invperm + z sp; out + z so)
 __global__ void store_weight_kernel(const float* w, int64_t rows, int64_t cols, const int32_t* invperm,
                                     void* out, mi355q_dtype dt, int64_t ld_out, const int8_t* cin,
-                                    int8_t* cout) {
+                                    int8_t* cout, int64_t sp, int64_t so) {
+  const int64_t z = blockIdx.z;
+  w += z * rows * cols;
+  if (invperm) invperm += z * sp;
+  out = dt == MI355Q_BF16 ? (void*)(static_cast<uint16_t*>(out) + z * so) : (void*)(static_cast<float*>(out) + z * so);
+  if (cin) cin += z * rows * cols;
+  if (cout) cout += z * rows * cols;
   const int64_t r = blockIdx.y;
   for (int64_t j4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; j4 < cols;
        j4 += (int64_t)gridDim.x * blockDim.x * 4) {
@@ -225,11 +257,11 @@ __global__ void store_weight_kernel(const float* w, int64_t rows, int64_t cols, 
   }
 }
 
-inline dim3 grid_rows(int64_t rows, int64_t cols) {
+inline dim3 grid_rows(int64_t rows, int64_t cols, int64_t batch = 1) {
   int64_t gx = (cols / 4 + 255) / 256;
   if (gx < 1) gx = 1;
   if (gx > 64) gx = 64;
-  return dim3((unsigned)gx, (unsigned)rows);
+  return dim3((unsigned)gx, (unsigned)rows, (unsigned)batch);
 }
 
 }  // namespace
@@ -237,17 +269,26 @@ inline dim3 grid_rows(int64_t rows, int64_t cols) {
 
 using namespace mi355q;
 
+extern "C" int mi355q_gptq_load_weight_batched(const void* w_dev, mi355q_dtype w_dtype, int64_t rows,
+                                               int64_t cols, int64_t ldw, int64_t stride_w, int64_t batch,
+                                               const int32_t* perm_dev, int64_t stride_perm,
+                                               const int32_t* dead_dev, float* w_work_dev, void* stream) {
+  MQ_CHECK_ARG(w_dev && w_work_dev, "gptq_load_weight: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && ldw >= cols && batch > 0, "gptq_load_weight: bad shape");
+  MQ_CHECK_ARG(rows <= 65535 && batch <= 65535, "gptq_load_weight: at most 65535 rows and matrices");
+  MQ_CHECK_ARG(batch == 1 || stride_w >= rows * ldw, "gptq_load_weight: matrices overlap");
+  hipLaunchKernelGGL(load_weight_kernel, grid_rows(rows, cols, batch), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), w_dev, w_dtype, rows, cols, ldw, perm_dev, dead_dev,
+                     w_work_dev, stride_w, stride_perm);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
 extern "C" int mi355q_gptq_load_weight(const void* w_dev, mi355q_dtype w_dtype, int64_t rows, int64_t cols,
                                        int64_t ldw, const int32_t* perm_dev, const int32_t* dead_dev,
                                        float* w_work_dev, void* stream) {
-  MQ_CHECK_ARG(w_dev && w_work_dev, "gptq_load_weight: null pointer");
-  MQ_CHECK_ARG(rows > 0 && cols > 0 && ldw >= cols, "gptq_load_weight: bad shape");
-  MQ_CHECK_ARG(rows <= 65535, "gptq_load_weight: at most 65535 rows");
-  hipLaunchKernelGGL(load_weight_kernel, grid_rows(rows, cols), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), w_dev, w_dtype, rows, cols, ldw, perm_dev, dead_dev,
-                     w_work_dev);
-  MQ_LAUNCH_CHECK();
-  return MI355Q_OK;
+  return mi355q_gptq_load_weight_batched(w_dev, w_dtype, rows, cols, ldw, 0, 1, perm_dev, 0, dead_dev,
+                                         w_work_dev, stream);
 }
 
 extern "C" size_t mi355q_gptq_sweep_workspace_size(int64_t rows, int64_t cols, int64_t blocksize) {
@@ -256,13 +297,15 @@ extern "C" size_t mi355q_gptq_sweep_workspace_size(int64_t rows, int64_t cols, i
   return rows > 0 ? (size_t)rows * MAXB * sizeof(float) : 0;
 }
 
-extern "C" int mi355q_gptq_sweep(float* w_work_dev, int64_t rows, int64_t cols, const float* hinv_dev,
-                                 const float* scale_dev, const float* zp_dev, int64_t ld_scale,
-                                 const int32_t* g_idx_dev, int strategy, int block_h, float qmin, float qmax,
-                                 int dequant_bf16, int64_t blocksize, int8_t* codes_dev, float* losses_dev,
-                                 void* workspace_dev, size_t workspace_bytes, void* stream) {
+extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
+                                         const float* hinv_dev, int64_t stride_hinv, const float* scale_dev,
+                                         const float* zp_dev, int64_t ld_scale, int64_t stride_scale,
+                                         const int32_t* g_idx_dev, int64_t stride_gidx, int strategy, int block_h,
+                                         float qmin, float qmax, int dequant_bf16, int64_t blocksize,
+                                         int8_t* codes_dev, float* losses_dev, void* workspace_dev,
+                                         size_t workspace_bytes, void* stream) {
   MQ_CHECK_ARG(w_work_dev && hinv_dev && scale_dev && codes_dev && losses_dev, "gptq_sweep: null pointer");
-  MQ_CHECK_ARG(rows > 0 && cols > 0, "gptq_sweep: bad shape");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && batch > 0 && batch <= 65535, "gptq_sweep: bad shape");
   MQ_CHECK_ARG(blocksize > 0, "gptq_sweep: blocksize must be positive");
   MQ_CHECK_ARG(strategy == MI355Q_TENSOR || strategy == MI355Q_CHANNEL || strategy == MI355Q_GROUP ||
                    strategy == MI355Q_BLOCK,
@@ -271,10 +314,12 @@ extern "C" int mi355q_gptq_sweep(float* w_work_dev, int64_t rows, int64_t cols, 
                "gptq_sweep: group/block strategies need g_idx");
   MQ_CHECK_ARG(strategy != MI355Q_BLOCK || block_h > 0, "gptq_sweep: block_h must be positive");
   MQ_CHECK_ARG(qmin < qmax && qmin >= -128.f && qmax <= 127.f, "gptq_sweep: integer range must fit int8");
-  const size_t need = mi355q_gptq_sweep_workspace_size(rows, cols, blocksize);
+  MQ_CHECK_ARG(batch == 1 || stride_hinv >= cols * cols, "gptq_sweep: Hinv matrices overlap");
+  const size_t need = mi355q_gptq_sweep_workspace_size(rows, cols, blocksize) * (size_t)batch;
   MQ_CHECK_ARG(workspace_dev && workspace_bytes >= need, "gptq_sweep: workspace too small");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* err = static_cast<float*>(workspace_dev);
+  SweepBatch sb{rows * cols, stride_hinv, stride_scale, stride_gidx, rows * cols, rows, rows * MAXB};
   // the sweep kernel holds at most MAXB columns; larger reference block
   // sizes give the same result up to fp32 rounding of the lazy update, so
   // they are processed in MAXB-wide sub-blocks
@@ -283,21 +328,48 @@ extern "C" int mi355q_gptq_sweep(float* w_work_dev, int64_t rows, int64_t cols, 
   for (int64_t i1 = 0; i1 < cols; i1 += B) {
     const int64_t i2 = (i1 + B < cols) ? i1 + B : cols;
     const int count = (int)(i2 - i1);
-    hipLaunchKernelGGL(sweep_block_kernel, dim3(nwg), dim3(SW_NT), 0, st, w_work_dev, rows, cols, hinv_dev, i1,
-                       count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin, qmax,
-                       dequant_bf16, codes_dev, losses_dev, err);
+    hipLaunchKernelGGL(sweep_block_kernel, dim3(nwg, (unsigned)batch), dim3(SW_NT), 0, st, w_work_dev, rows, cols,
+                       hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
+                       qmax, dequant_bf16, codes_dev, losses_dev, err, sb);
     MQ_LAUNCH_CHECK();
     if (i2 < cols) {
       GemmArgs g{};
-      g.A = err; g.lda = MAXB;
-      g.B = hinv_dev + i1 * cols + i2; g.ldb = cols;
-      g.C = w_work_dev + i2; g.ldc = cols;
+      g.A = err; g.lda = MAXB; g.strideA = rows * MAXB;
+      g.B = hinv_dev + i1 * cols + i2; g.ldb = cols; g.strideB = stride_hinv;
+      g.C = w_work_dev + i2; g.ldc = cols; g.strideC = rows * cols;
       g.M = rows; g.N = cols - i2; g.K = count;
       g.alpha = -1.f; g.beta = 1.f;
-      int rc = gemm_f32(g, false, 1, st);
+      int rc = gemm_f32(g, false, (int)batch, st);
       if (rc) return rc;
     }
   }
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_gptq_sweep(float* w_work_dev, int64_t rows, int64_t cols, const float* hinv_dev,
+                                 const float* scale_dev, const float* zp_dev, int64_t ld_scale,
+                                 const int32_t* g_idx_dev, int strategy, int block_h, float qmin, float qmax,
+                                 int dequant_bf16, int64_t blocksize, int8_t* codes_dev, float* losses_dev,
+                                 void* workspace_dev, size_t workspace_bytes, void* stream) {
+  return mi355q_gptq_sweep_batched(w_work_dev, rows, cols, 1, hinv_dev, 0, scale_dev, zp_dev, ld_scale, 0,
+                                   g_idx_dev, 0, strategy, block_h, qmin, qmax, dequant_bf16, blocksize,
+                                   codes_dev, losses_dev, workspace_dev, workspace_bytes, stream);
+}
+
+extern "C" int mi355q_gptq_store_weight_batched(const float* w_work_dev, int64_t rows, int64_t cols,
+                                                int64_t batch, const int32_t* invperm_dev, int64_t stride_perm,
+                                                void* w_out_dev, mi355q_dtype out_dtype, int64_t ld_out,
+                                                int64_t stride_out, const int8_t* codes_in_dev,
+                                                int8_t* codes_out_dev, void* stream) {
+  MQ_CHECK_ARG(w_work_dev && w_out_dev, "gptq_store_weight: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && ld_out >= cols && batch > 0, "gptq_store_weight: bad shape");
+  MQ_CHECK_ARG(codes_out_dev != codes_in_dev || !codes_in_dev, "gptq_store_weight: codes must not alias");
+  MQ_CHECK_ARG(rows <= 65535 && batch <= 65535, "gptq_store_weight: at most 65535 rows and matrices");
+  MQ_CHECK_ARG(batch == 1 || stride_out >= rows * ld_out, "gptq_store_weight: matrices overlap");
+  hipLaunchKernelGGL(store_weight_kernel, grid_rows(rows, cols, batch), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), w_work_dev, rows, cols, invperm_dev, w_out_dev,
+                     out_dtype, ld_out, codes_in_dev, codes_out_dev, stride_perm, stride_out);
+  MQ_LAUNCH_CHECK();
   return MI355Q_OK;
 }
 
@@ -305,13 +377,6 @@ extern "C" int mi355q_gptq_store_weight(const float* w_work_dev, int64_t rows, i
                                         const int32_t* invperm_dev, void* w_out_dev, mi355q_dtype out_dtype,
                                         int64_t ld_out, const int8_t* codes_in_dev, int8_t* codes_out_dev,
                                         void* stream) {
-  MQ_CHECK_ARG(w_work_dev && w_out_dev, "gptq_store_weight: null pointer");
-  MQ_CHECK_ARG(rows > 0 && cols > 0 && ld_out >= cols, "gptq_store_weight: bad shape");
-  MQ_CHECK_ARG(codes_out_dev != codes_in_dev || !codes_in_dev, "gptq_store_weight: codes must not alias");
-  MQ_CHECK_ARG(rows <= 65535, "gptq_store_weight: at most 65535 rows");
-  hipLaunchKernelGGL(store_weight_kernel, grid_rows(rows, cols), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), w_work_dev, rows, cols, invperm_dev, w_out_dev,
-                     out_dtype, ld_out, codes_in_dev, codes_out_dev);
-  MQ_LAUNCH_CHECK();
-  return MI355Q_OK;
+  return mi355q_gptq_store_weight_batched(w_work_dev, rows, cols, 1, invperm_dev, 0, w_out_dev, out_dtype,
+                                          ld_out, 0, codes_in_dev, codes_out_dev, stream);
 }

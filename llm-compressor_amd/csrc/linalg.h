@@ -11,12 +11,17 @@ struct GemmArgs {
   float* C;        // [M x N] row-major (ldc)
   int64_t lda, ldb, ldc;
   int64_t strideA, strideB, strideC;  // batch strides (elements)
+  // optional second batch level: batch index z = b1 + inner * b2 with
+  // b1 < inner; element offsets b1 * stride + b2 * stride2 (inner = 0: one level)
+  int64_t inner;
+  int64_t strideA2, strideB2, strideC2;
   int64_t M, N, K;
   float alpha, beta;  // C = beta * C + alpha * (A op(B)); beta == 0 never reads C
   int lower_only;     // only C elements with row >= col (tiles fully above skipped)
 };
 
-// Launches the batched GEMM on `stream`; returns a status code.
+// Launches the batched GEMM (batch = total number of products) on `stream`;
+// returns a status code.
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream);
 
 }  // namespace mi355q

@@ -42,10 +42,11 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
 
   const int64_t m0 = (int64_t)blockIdx.y * GBM, n0 = (int64_t)blockIdx.x * GBN;
   if (g.lower_only && m0 + GBM - 1 < n0) return;
-  const int bz = blockIdx.z;
-  const float* A = g.A + bz * g.strideA;
-  const float* B = g.B + bz * g.strideB;
-  float* C = g.C + bz * g.strideC;
+  const int64_t bz = blockIdx.z;
+  const int64_t b1 = g.inner > 0 ? bz % g.inner : bz, b2 = g.inner > 0 ? bz / g.inner : 0;
+  const float* A = g.A + b1 * g.strideA + b2 * g.strideA2;
+  const float* B = g.B + b1 * g.strideB + b2 * g.strideB2;
+  float* C = g.C + b1 * g.strideC + b2 * g.strideC2;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -210,6 +211,13 @@ template <bool BT>
 __global__ __launch_bounds__(GNT, 1) void gemm_k128_kernel(GemmArgs g) {
   __shared__ float la[KT * KLA];
   __shared__ float lb[BT ? KT * KLA : KT * LBN];
+  {
+    const int64_t bz = blockIdx.z;
+    const int64_t b1 = g.inner > 0 ? bz % g.inner : bz, b2 = g.inner > 0 ? bz / g.inner : 0;
+    g.A += b1 * g.strideA + b2 * g.strideA2;
+    g.B += b1 * g.strideB + b2 * g.strideB2;
+    g.C += b1 * g.strideC + b2 * g.strideC2;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t m0 = (int64_t)blockIdx.y * KT;
@@ -362,11 +370,15 @@ __device__ __forceinline__ void tile_store(const f32x16_t& acc, float* C, int ld
 // inverse is assembled from the four sub-block inverses by two doubling
 // steps, inv([[A,0],[B,C]]) = [[A^-1,0],[-C^-1 B A^-1, C^-1]].
 __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, int64_t k0, int nb,
-                                                        float* linv, int32_t* status) {
+                                                        float* linv, int32_t* status, int64_t wsf) {
   __shared__ float a[NB * LP];
   __shared__ float x[NB * LP];
   __shared__ __attribute__((aligned(16))) float t[2 * SB * LT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // matrix blockIdx.x of a batch: workspaces wsf floats apart
+  F += (int64_t)blockIdx.x * wsf;
+  linv += (int64_t)blockIdx.x * wsf;
+  status += blockIdx.x;
 
   // load: all 64 loads per thread issued before any is consumed; addresses
   // are clamped into the block so no load needs a branch
@@ -525,11 +537,19 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
 }
 
 // diag'[j] = H[p(j)][p(j)] / n with 0 -> 1 (dead), damp = percdamp * mean(diag')
-__global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t ldh, int64_t d,
-                                                         const int32_t* perm, float num_samples,
-                                                         float percdamp, int32_t* dead, float* damp_out,
-                                                         int32_t* status) {
+// (one workgroup per matrix of a batch)
+__global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t ldh, int64_t sh, int64_t d,
+                                                         const int32_t* perm, int64_t sp, const float* ns_arr,
+                                                         float ns0, float percdamp, int32_t* dead,
+                                                         float* damp_out, int64_t wsf, int32_t* status) {
   __shared__ float part[1024 / 64];
+  const int64_t bm = blockIdx.x;
+  H += bm * sh;
+  if (perm) perm += bm * sp;
+  if (dead) dead += bm * d;
+  damp_out += bm * wsf;
+  if (status) status += bm;
+  const float num_samples = ns_arr ? ns_arr[bm] : ns0;
   float s = 0.f;
   for (int64_t j = threadIdx.x; j < d; j += 1024) {
     const int64_t pj = perm ? perm[j] : j;
@@ -551,8 +571,15 @@ __global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t
 }
 
 // F (lower) = flip(permute(H / n)) with dead / damping rules on the diagonal.
-__global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t d, const int32_t* perm,
-                                    float num_samples, const float* damp, float* F) {
+__global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t sh, int64_t d, const int32_t* perm,
+                                    int64_t sp, const float* ns_arr, float ns0, const float* damp, float* F,
+                                    int64_t wsf) {
+  const int64_t bm = blockIdx.z;
+  H += bm * sh;
+  if (perm) perm += bm * sp;
+  damp += bm * wsf;
+  F += bm * wsf;
+  const float num_samples = ns_arr ? ns_arr[bm] : ns0;
   const int64_t a = (int64_t)blockIdx.y * 16 + threadIdx.y;
   const int64_t b = (int64_t)blockIdx.x * 64 + threadIdx.x;
   if (a >= d || b > a) return;
@@ -568,20 +595,25 @@ __global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t d, cons
 }
 
 // hinv[a][b] = X[d-1-a][d-1-b] (a <= b), zero below the diagonal.
-__global__ void flip_out_kernel(const float* X, int64_t d, float* hinv) {
+__global__ void flip_out_kernel(const float* X, int64_t d, float* hinv, int64_t wsf, int64_t shinv) {
+  X += (int64_t)blockIdx.z * wsf;
+  hinv += (int64_t)blockIdx.z * shinv;
   const int64_t a = (int64_t)blockIdx.y * 16 + threadIdx.y;
   const int64_t b = (int64_t)blockIdx.x * 64 + threadIdx.x;
   if (a >= d || b >= d) return;
   hinv[a * d + b] = (a <= b) ? X[(d - 1 - a) * d + (d - 1 - b)] : 0.f;
 }
 
-__global__ void fill_kernel(float* p, int64_t n, float v) {
+__global__ void fill_kernel(float* p, int64_t n, float v, int64_t wsf) {
+  p += (int64_t)blockIdx.y * wsf;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     p[i] = v;
 }
 
 // Place diagonal-block inverses into X.
-__global__ void place_diag_inv_kernel(const float* linv, int64_t d, float* X) {
+__global__ void place_diag_inv_kernel(const float* linv, int64_t d, float* X, int64_t wsf) {
+  linv += (int64_t)blockIdx.y * wsf;
+  X += (int64_t)blockIdx.y * wsf;
   const int blk = blockIdx.x;
   const int64_t k0 = (int64_t)blk * NB;
   for (int e = threadIdx.x; e < NB * NB; e += blockDim.x) {
@@ -613,16 +645,19 @@ HinvLayout hinv_layout(int64_t d) {
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
-  const bool k128 = batch == 1 && g.K == KT && g.M % KT == 0 && g.N % KT == 0 && g.lda % 4 == 0 &&
-                    g.ldb % 4 == 0 && aligned16(g.A) && aligned16(g.B) && (g.lda * 7 + KT) < (1 << 29) &&
-                    (g.ldb * 7 + KT) < (1 << 29) && (g.ldc * 127 + KT) < (1 << 29);
+  MQ_CHECK_ARG(batch <= 65535, "gemm: batch too large");
+  // whole-tile K = 128 products (every batch member 16-byte aligned)
+  const bool strides16 = g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 && g.strideB2 % 4 == 0;
+  const bool k128 = g.K == KT && g.M % KT == 0 && g.N % KT == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                    aligned16(g.A) && aligned16(g.B) && (batch == 1 || strides16) &&
+                    (g.lda * 7 + KT) < (1 << 29) && (g.ldb * 7 + KT) < (1 << 29) && (g.ldc * 127 + KT) < (1 << 29);
   if (k128) {
     // one workgroup per CU: spread the column tiles so ~256 workgroups run
     const int64_t mt = g.M / KT, ntl = g.N / KT;
-    int64_t p = (256 + mt - 1) / mt;
+    int64_t p = (256 + mt * batch - 1) / (mt * batch);
     if (p > ntl) p = ntl;
     if (p < 1) p = 1;
-    dim3 grid((unsigned)p, (unsigned)mt, 1);
+    dim3 grid((unsigned)p, (unsigned)mt, (unsigned)batch);
     if (b_trans)
       hipLaunchKernelGGL(gemm_k128_kernel<true>, grid, dim3(GNT), 0, stream, g);
     else
@@ -645,29 +680,30 @@ using namespace mi355q;
 
 extern "C" size_t mi355q_gptq_hinv_workspace_size(int64_t d) { return d > 0 ? hinv_layout(d).total : 0; }
 
-extern "C" int mi355q_gptq_hinv(const float* h_dev, int64_t ldh, int64_t d, const int32_t* perm_dev,
-                                float num_samples, float percdamp, float* hinv_dev, int32_t* dead_dev,
-                                int32_t* status_dev, void* workspace_dev, size_t workspace_bytes,
-                                void* stream) {
-  MQ_CHECK_ARG(h_dev && hinv_dev && status_dev, "gptq_hinv: null pointer");
-  MQ_CHECK_ARG(d > 0 && ldh >= d, "gptq_hinv: bad shape");
-  MQ_CHECK_ARG(num_samples > 0.f, "gptq_hinv: num_samples must be positive");
+namespace mi355q {
+namespace {
+
+// The hinv pipeline for `batch` matrices of order d: matrix b reads
+// H + b sh (and perm + b sp), writes hinv + b shinv, dead + b d, status[b],
+// and uses workspace bytes [b L.total, (b + 1) L.total).
+int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t batch, const int32_t* perm_dev,
+              int64_t sp, const float* ns_dev, float ns0, float percdamp, float* hinv_dev, int64_t shinv,
+              int32_t* dead_dev, int32_t* status_dev, char* ws, hipStream_t st) {
   const HinvLayout L = hinv_layout(d);
-  MQ_CHECK_ARG(workspace_dev && workspace_bytes >= L.total, "gptq_hinv: workspace too small (%zu < %zu)",
-               workspace_bytes, L.total);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace_dev);
+  const int64_t wsf = (int64_t)(L.total / sizeof(float));
   float* F = reinterpret_cast<float*>(ws + L.F);
   float* X = reinterpret_cast<float*>(ws + L.X);
   float* T = reinterpret_cast<float*>(ws + L.T);
   float* linv = reinterpret_cast<float*>(ws + L.linv);
   float* damp = reinterpret_cast<float*>(ws + L.damp);
+  const unsigned nb_ = (unsigned)batch;
 
-  hipLaunchKernelGGL(diag_damp_kernel, dim3(1), dim3(1024), 0, st, h_dev, ldh, d, perm_dev, num_samples,
-                     percdamp, dead_dev, damp, status_dev);
+  hipLaunchKernelGGL(diag_damp_kernel, dim3(nb_), dim3(1024), 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0,
+                     percdamp, dead_dev, damp, wsf, status_dev);
   MQ_LAUNCH_CHECK();
-  dim3 fb(64, 16), fg((unsigned)((d + 63) / 64), (unsigned)((d + 15) / 16));
-  hipLaunchKernelGGL(prepare_flip_kernel, fg, fb, 0, st, h_dev, ldh, d, perm_dev, num_samples, damp, F);
+  dim3 fb(64, 16), fg((unsigned)((d + 63) / 64), (unsigned)((d + 15) / 16), nb_);
+  hipLaunchKernelGGL(prepare_flip_kernel, fg, fb, 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0, damp, F,
+                     wsf);
   MQ_LAUNCH_CHECK();
 
   // blocked right-looking Cholesky on F (lower)
@@ -675,35 +711,35 @@ extern "C" int mi355q_gptq_hinv(const float* h_dev, int64_t ldh, int64_t d, cons
   for (int64_t kb = 0; kb < nblk; ++kb) {
     const int64_t k0 = kb * NB;
     const int nb = (int)((d - k0) < NB ? (d - k0) : NB);
-    hipLaunchKernelGGL(potf2_inv_kernel, dim3(1), dim3(PNT), 0, st, F, d, k0, nb, linv + kb * NB * NB,
-                       status_dev);
+    hipLaunchKernelGGL(potf2_inv_kernel, dim3(nb_), dim3(PNT), 0, st, F, d, k0, nb, linv + kb * NB * NB,
+                       status_dev, wsf);
     MQ_LAUNCH_CHECK();
     const int64_t rest = d - k0 - nb;
     if (rest <= 0) break;
     // panel: F[k0+nb:, k0:k0+nb] = F[...] * linv^T (in place, one workgroup per row tile)
     GemmArgs p{};
-    p.A = F + (k0 + nb) * d + k0; p.lda = d;
-    p.B = linv + kb * NB * NB; p.ldb = NB;
-    p.C = F + (k0 + nb) * d + k0; p.ldc = d;
+    p.A = F + (k0 + nb) * d + k0; p.lda = d; p.strideA = wsf;
+    p.B = linv + kb * NB * NB; p.ldb = NB; p.strideB = wsf;
+    p.C = F + (k0 + nb) * d + k0; p.ldc = d; p.strideC = wsf;
     p.M = rest; p.N = nb; p.K = nb; p.alpha = 1.f; p.beta = 0.f;
-    int rc = gemm_f32(p, true, 1, st);
+    int rc = gemm_f32(p, true, (int)batch, st);
     if (rc) return rc;
     // trailing: F[k0+nb:, k0+nb:] -= P P^T (lower)
     GemmArgs s{};
-    s.A = F + (k0 + nb) * d + k0; s.lda = d;
-    s.B = F + (k0 + nb) * d + k0; s.ldb = d;
-    s.C = F + (k0 + nb) * d + (k0 + nb); s.ldc = d;
+    s.A = F + (k0 + nb) * d + k0; s.lda = d; s.strideA = wsf;
+    s.B = F + (k0 + nb) * d + k0; s.ldb = d; s.strideB = wsf;
+    s.C = F + (k0 + nb) * d + (k0 + nb); s.ldc = d; s.strideC = wsf;
     s.M = rest; s.N = rest; s.K = nb; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
-    rc = gemm_f32(s, true, 1, st);
+    rc = gemm_f32(s, true, (int)batch, st);
     if (rc) return rc;
   }
 
   // triangular inverse X = L^-1 by recursive doubling over NB blocks; the
   // doubling reads whole s x s blocks of X, so everything above the
   // diagonal blocks must be zero
-  hipLaunchKernelGGL(fill_kernel, dim3(2048), dim3(256), 0, st, X, d * d, 0.f);
+  hipLaunchKernelGGL(fill_kernel, dim3(2048, nb_), dim3(256), 0, st, X, d * d, 0.f, wsf);
   MQ_LAUNCH_CHECK();
-  hipLaunchKernelGGL(place_diag_inv_kernel, dim3((unsigned)nblk), dim3(256), 0, st, linv, d, X);
+  hipLaunchKernelGGL(place_diag_inv_kernel, dim3((unsigned)nblk, nb_), dim3(256), 0, st, linv, d, X, wsf);
   MQ_LAUNCH_CHECK();
   for (int64_t s = NB; s < d; s *= 2) {
     // pairs (a0 = p*2s, c0 = a0 + s); full pairs batched, ragged tail alone
@@ -722,23 +758,59 @@ extern "C" int mi355q_gptq_hinv(const float* h_dev, int64_t ldh, int64_t d, cons
       const int64_t stride_diag = 2 * s * (d + 1);
       // T = L[c0:c0+s2, a0:a0+s] * X[a0:a0+s, a0:a0+s]
       GemmArgs t1{};
-      t1.A = F + c0 * d + a0; t1.lda = d; t1.strideA = stride_diag;
-      t1.B = X + a0 * d + a0; t1.ldb = d; t1.strideB = stride_diag;
-      t1.C = T; t1.ldc = s; t1.strideC = s2 * s;
+      t1.A = F + c0 * d + a0; t1.lda = d; t1.strideA = stride_diag; t1.strideA2 = wsf;
+      t1.B = X + a0 * d + a0; t1.ldb = d; t1.strideB = stride_diag; t1.strideB2 = wsf;
+      t1.C = T; t1.ldc = s; t1.strideC = s2 * s; t1.strideC2 = wsf;
+      t1.inner = npairs;
       t1.M = s2; t1.N = s; t1.K = s; t1.alpha = 1.f; t1.beta = 0.f;
-      int rc = gemm_f32(t1, false, (int)npairs, st);
+      int rc = gemm_f32(t1, false, (int)(npairs * batch), st);
       if (rc) return rc;
       // X[c0:c0+s2, a0:a0+s] = -X[c0:c0+s2, c0:c0+s2] * T
       GemmArgs t2{};
-      t2.A = X + c0 * d + c0; t2.lda = d; t2.strideA = stride_diag;
-      t2.B = T; t2.ldb = s; t2.strideB = s2 * s;
-      t2.C = X + c0 * d + a0; t2.ldc = d; t2.strideC = stride_diag;
+      t2.A = X + c0 * d + c0; t2.lda = d; t2.strideA = stride_diag; t2.strideA2 = wsf;
+      t2.B = T; t2.ldb = s; t2.strideB = s2 * s; t2.strideB2 = wsf;
+      t2.C = X + c0 * d + a0; t2.ldc = d; t2.strideC = stride_diag; t2.strideC2 = wsf;
+      t2.inner = npairs;
       t2.M = s2; t2.N = s; t2.K = s2; t2.alpha = -1.f; t2.beta = 0.f;
-      rc = gemm_f32(t2, false, (int)npairs, st);
+      rc = gemm_f32(t2, false, (int)(npairs * batch), st);
       if (rc) return rc;
     }
   }
-  hipLaunchKernelGGL(flip_out_kernel, fg, fb, 0, st, X, d, hinv_dev);
+  hipLaunchKernelGGL(flip_out_kernel, fg, fb, 0, st, X, d, hinv_dev, wsf, shinv);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
+}
+
+}  // namespace
+}  // namespace mi355q
+
+extern "C" int mi355q_gptq_hinv(const float* h_dev, int64_t ldh, int64_t d, const int32_t* perm_dev,
+                                float num_samples, float percdamp, float* hinv_dev, int32_t* dead_dev,
+                                int32_t* status_dev, void* workspace_dev, size_t workspace_bytes,
+                                void* stream) {
+  MQ_CHECK_ARG(h_dev && hinv_dev && status_dev, "gptq_hinv: null pointer");
+  MQ_CHECK_ARG(d > 0 && ldh >= d, "gptq_hinv: bad shape");
+  MQ_CHECK_ARG(num_samples > 0.f, "gptq_hinv: num_samples must be positive");
+  const HinvLayout L = hinv_layout(d);
+  MQ_CHECK_ARG(workspace_dev && workspace_bytes >= L.total, "gptq_hinv: workspace too small (%zu < %zu)",
+               workspace_bytes, L.total);
+  return hinv_impl(h_dev, ldh, 0, d, 1, perm_dev, 0, nullptr, num_samples, percdamp, hinv_dev, 0, dead_dev,
+                   status_dev, static_cast<char*>(workspace_dev), reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int mi355q_gptq_hinv_batched(const float* h_dev, int64_t ldh, int64_t stride_h, int64_t d,
+                                        int64_t batch, const int32_t* perm_dev, int64_t stride_perm,
+                                        const float* num_samples_dev, float percdamp, float* hinv_dev,
+                                        int64_t stride_hinv, int32_t* dead_dev, int32_t* status_dev,
+                                        void* workspace_dev, size_t workspace_bytes, void* stream) {
+  MQ_CHECK_ARG(h_dev && hinv_dev && status_dev && num_samples_dev, "gptq_hinv_batched: null pointer");
+  MQ_CHECK_ARG(d > 0 && ldh >= d && batch > 0 && batch <= 65535, "gptq_hinv_batched: bad shape");
+  MQ_CHECK_ARG(stride_h >= ldh * d && stride_hinv >= d * d, "gptq_hinv_batched: matrices overlap");
+  MQ_CHECK_ARG(!perm_dev || stride_perm >= 0, "gptq_hinv_batched: bad perm stride");
+  const HinvLayout L = hinv_layout(d);
+  MQ_CHECK_ARG(workspace_dev && workspace_bytes >= L.total * (size_t)batch,
+               "gptq_hinv_batched: workspace too small (%zu < %zu)", workspace_bytes, L.total * (size_t)batch);
+  return hinv_impl(h_dev, ldh, stride_h, d, batch, perm_dev, stride_perm, num_samples_dev, 0.f, percdamp,
+                   hinv_dev, stride_hinv, dead_dev, status_dev, static_cast<char*>(workspace_dev),
+                   reinterpret_cast<hipStream_t>(stream));
 }

@@ -35,6 +35,14 @@ SIGNATURES = {
     "mi355q_gptq_sweep": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _f32, _f32, _i32,
                                  _i64, _vp, _vp, _vp, _sz, _vp]),
     "mi355q_gptq_store_weight": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _vp]),
+    "mi355q_gptq_hinv_batched": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _f32, _vp, _i64, _vp, _vp,
+                                        _vp, _sz, _vp]),
+    "mi355q_gptq_load_weight_batched": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
+                                               _vp]),
+    "mi355q_gptq_sweep_batched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i32,
+                                         _i32, _f32, _f32, _i32, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "mi355q_gptq_store_weight_batched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _i64, _i64, _vp,
+                                                _vp, _vp]),
     "mi355q_observe_minmax": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
     "mi355q_calculate_qparams": (_i32, [_vp, _vp, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "mi355q_mx_scales": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp]),

@@ -29,7 +29,7 @@ logger = logging.getLogger("llmcompressor_amd")
 GPTQ_PRECISION = torch.float32
 
 __all__ = ["make_empty_hessian", "accumulate_hessian", "quantize_weight", "symmetrize_hessian",
-           "GPTQResult", "gptq_quantize"]
+           "GPTQResult", "gptq_quantize", "gptq_quantize_batched"]
 
 
 def make_empty_hessian(module: torch.nn.Module, device: torch.device | None = None) -> torch.Tensor:
@@ -151,6 +151,94 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
     loss = torch.sum(losses).item()
     return GPTQResult(loss=loss, weight=w_out, scale=scale, zero_point=zero_point, g_idx=g_idx, perm=perm,
                       codes=codes_out, hinv_ok=ok)
+
+
+def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, hessians: torch.Tensor,
+                          num_samples=1.0, blocksize: int = 128, percdamp: float = 0.01,
+                          observer: str = "memoryless_minmax") -> list[GPTQResult]:
+    """``gptq_quantize`` for B same-shaped modules at once (the experts of an
+    MoE layer): weights [B, rows, cols], hessians [B, cols, cols] (upper
+    triangles), num_samples a number or [B].  Each module gets exactly the
+    result of its own ``gptq_quantize`` call (same kernels, one launch per
+    step for the whole batch, one host synchronisation for the status flags
+    and one for the losses).  The weight observer named ``observer`` is run
+    here on the stacked weights (its statistics are per row for channel and
+    group strategies).
+    """
+    from .observers import Observer
+
+    strategy = quant_args.strategy
+    actorder = quant_args.actorder
+    if quant_args.type != QuantizationType.INT:
+        raise NotImplementedError("GPTQ on the GPU supports integer quantization types")
+    if strategy not in (QuantizationStrategy.TENSOR, QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP,
+                        QuantizationStrategy.BLOCK):
+        raise ValueError(f"Quantization strategy is not supported for GPTQ: {strategy}")
+    B, rows, cols = weights.shape
+    if hessians.shape != (B, cols, cols):
+        raise ValueError(f"hessians must be [{B}, {cols}, {cols}], got {tuple(hessians.shape)}")
+    if actorder == ActivationOrdering.GROUP and strategy != QuantizationStrategy.GROUP:
+        logger.warning("ActivationOrdering.GROUP requires a grouped quantization strategy; "
+                       "falling back to actorder=None for this module.")
+        actorder = None
+    dev = weights.device
+    ns = torch.as_tensor(num_samples, dtype=torch.float32, device=dev).expand(B).contiguous()
+
+    perm = invperm = None
+    if actorder:
+        perm = torch.argsort(torch.diagonal(hessians, dim1=1, dim2=2), dim=1, descending=True, stable=True)
+        invperm = torch.argsort(perm, dim=1)
+    src = ops.gptq_load_weight_batched(weights, perm) if actorder == ActivationOrdering.GROUP else weights
+
+    def observe(x):
+        obs = Observer.load_from_registry(observer, base_name="weight", args=quant_args)
+        obs(x)
+        qp = obs.get_qparams()
+        return qp["scale"], qp["zero_point"]
+
+    stackable = strategy in (QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP) or (
+        strategy == QuantizationStrategy.BLOCK and rows % quant_args.block_structure[0] == 0)
+    if stackable:
+        sc, zp = observe(src.reshape(B * rows, cols))
+        scale, zero_point = sc.reshape(B, -1, sc.shape[-1]), zp.reshape(B, -1, zp.shape[-1])
+    else:
+        qps = [observe(src[b]) for b in range(B)]
+        scale = torch.stack([q[0] for q in qps]).reshape(B, 1, 1) if strategy == QuantizationStrategy.TENSOR \
+            else torch.stack([q[0] for q in qps])
+        zero_point = torch.stack([q[1] for q in qps]).reshape(scale.shape)
+
+    g_idx = None
+    if strategy in (QuantizationStrategy.GROUP, QuantizationStrategy.BLOCK):
+        divisor = quant_args.group_size if strategy != QuantizationStrategy.BLOCK else quant_args.block_structure[1]
+        g_idx = torch.arange(cols, device=dev, dtype=torch.int) // divisor
+        if actorder == ActivationOrdering.WEIGHT:
+            g_idx = g_idx[perm]
+
+    hinv, dead, ok = ops.gptq_hinv_batched(hessians, perm, ns, percdamp)
+    for b in torch.nonzero(~ok).flatten().tolist():
+        logger.warning("Failed to invert hessian due to numerical instability. Consider increasing "
+                       "GPTQModifier.dampening_frac, increasing the number of calibration samples, or "
+                       "shuffling the calibration dataset. Falling back to round-to-nearest for this module.")
+        hinv[b] = torch.eye(cols, dtype=torch.float32, device=dev)
+
+    w_work = ops.gptq_load_weight_batched(weights, perm, dead)
+    qmin, qmax = quant_args.q_range()
+    bh = quant_args.block_structure[0] if strategy == QuantizationStrategy.BLOCK else 1
+    codes, losses = ops.gptq_sweep_batched_(w_work, hinv, scale.to(torch.float32), zero_point.to(torch.float32),
+                                            strategy.value, g_idx, qmin, qmax,
+                                            dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize,
+                                            block_h=bh)
+    w_out, codes_out = ops.gptq_store_weight_batched(w_work, invperm, weights.dtype, codes)
+    loss = torch.sum(losses, dim=1).cpu()
+    out = []
+    for b in range(B):
+        sb, zb = scale[b], zero_point[b]
+        if strategy == QuantizationStrategy.TENSOR:
+            sb, zb = sb.reshape(-1), zb.reshape(-1)
+        out.append(GPTQResult(loss=float(loss[b]), weight=w_out[b], scale=sb, zero_point=zb,
+                              g_idx=None if g_idx is None else (g_idx[b] if g_idx.dim() == 2 else g_idx),
+                              perm=None if perm is None else perm[b], codes=codes_out[b], hinv_ok=bool(ok[b])))
+    return out
 
 
 def quantize_weight(module: torch.nn.Module, quant_args: QuantizationArgs, hessian: torch.Tensor,

@@ -151,6 +151,73 @@ def gptq_store_weight(w_work: torch.Tensor, invperm, out_dtype: torch.dtype, cod
     return out, cout
 
 
+# ---------------------------------------------------------------- batched GPTQ
+def gptq_hinv_batched(H: torch.Tensor, perm: torch.Tensor | None, num_samples: torch.Tensor, percdamp: float):
+    """``gptq_hinv`` for a stack H [B, d, d] of same-order Hessians (perm [B, d]
+    or None, num_samples [B]).  Returns (hinv [B, d, d], dead [B, d], ok
+    [B] bool tensor on the host); synchronises once."""
+    L.require_gpu(H)
+    B, d, _ = H.shape
+    dev = H.device
+    hinv = torch.empty((B, d, d), dtype=torch.float32, device=dev)
+    dead = torch.empty((B, d), dtype=torch.int32, device=dev)
+    status = torch.zeros(B, dtype=torch.int32, device=dev)
+    ns = num_samples.to(device=dev, dtype=torch.float32).reshape(B).contiguous()
+    lib = L.lib()
+    ws = _ws(lib.mi355q_gptq_hinv_workspace_size(d) * B, dev)
+    p = None if perm is None else perm.to(torch.int32).reshape(B, d).contiguous()
+    L.check(lib.mi355q_gptq_hinv_batched(H.data_ptr(), H.stride(1), H.stride(0), d, B, L.ptr(p),
+                                         0 if p is None else d, ns.data_ptr(), C.c_float(percdamp),
+                                         hinv.data_ptr(), d * d, dead.data_ptr(), status.data_ptr(),
+                                         ws.data_ptr(), ws.numel(), L.stream_of(H)))
+    return hinv, dead, status.cpu() == 0
+
+
+def gptq_load_weight_batched(w: torch.Tensor, perm=None, dead=None) -> torch.Tensor:
+    L.require_gpu(w)
+    B, rows, cols = w.shape
+    out = torch.empty((B, rows, cols), dtype=torch.float32, device=w.device)
+    p = None if perm is None else perm.to(torch.int32).reshape(B, cols).contiguous()
+    dd = None if dead is None else dead.to(torch.int32).reshape(B, cols).contiguous()
+    L.call("mi355q_gptq_load_weight_batched", w.data_ptr(), _dt(w), rows, cols, w.stride(1), w.stride(0), B,
+           L.ptr(p), 0 if p is None else cols, L.ptr(dd), out.data_ptr(), L.stream_of(w))
+    return out
+
+
+def gptq_sweep_batched_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.Tensor, zero_point, strategy: str,
+                        g_idx: torch.Tensor | None, qmin: float, qmax: float, dequant_bf16: bool,
+                        blocksize: int = 128, block_h: int = 1):
+    """``gptq_sweep_`` over a batch: w_work [B, rows, cols], hinv [B, cols, cols],
+    scale / zero_point [B, rows or 1, groups], g_idx [B, cols] or [cols] (shared)."""
+    L.require_gpu(w_work, hinv, scale)
+    B, rows, cols = w_work.shape
+    dev = w_work.device
+    s = scale.to(torch.float32).reshape(B, -1, scale.shape[-1] if scale.dim() == 3 else 1).contiguous()
+    z = None if zero_point is None else zero_point.to(torch.float32).reshape(s.shape).contiguous()
+    gi = None if g_idx is None else g_idx.to(torch.int32).contiguous()
+    codes = torch.empty((B, rows, cols), dtype=torch.int8, device=dev)
+    losses = torch.zeros((B, rows), dtype=torch.float32, device=dev)
+    lib = L.lib()
+    ws = _ws(lib.mi355q_gptq_sweep_workspace_size(rows, cols, blocksize) * B, dev)
+    L.check(lib.mi355q_gptq_sweep_batched(
+        w_work.data_ptr(), rows, cols, B, hinv.data_ptr(), hinv.stride(0), s.data_ptr(), L.ptr(z), s.stride(1),
+        s.stride(0), L.ptr(gi), 0 if gi is None or gi.dim() == 1 else gi.stride(0), STRATEGY_CODE[strategy],
+        block_h, C.c_float(qmin), C.c_float(qmax), 1 if dequant_bf16 else 0, blocksize, codes.data_ptr(),
+        losses.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_of(w_work)))
+    return codes, losses
+
+
+def gptq_store_weight_batched(w_work: torch.Tensor, invperm, out_dtype: torch.dtype, codes=None):
+    B, rows, cols = w_work.shape
+    out = torch.empty((B, rows, cols), dtype=out_dtype, device=w_work.device)
+    ip = None if invperm is None else invperm.to(torch.int32).reshape(B, cols).contiguous()
+    cout = None if codes is None else torch.empty_like(codes)
+    L.call("mi355q_gptq_store_weight_batched", w_work.data_ptr(), rows, cols, B, L.ptr(ip),
+           0 if ip is None else cols, out.data_ptr(), _dt(out), out.stride(1), out.stride(0), L.ptr(codes),
+           L.ptr(cout), L.stream_of(w_work))
+    return out, cout
+
+
 # ---------------------------------------------------------------- observers
 def observe_minmax(x: torch.Tensor, strategy: str, group_size: int | None = None,
                    block_structure=None):

@@ -290,6 +290,33 @@ GPTQ_CASES = [
 ]
 
 
+@pytest.mark.parametrize("case", GPTQ_CASES, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+def test_gptq_batched_equals_single(dev, case):
+    """The batched solve (one launch per step for all experts) gives each
+    module exactly what its own solve gives, including a non-PD member."""
+    say(f"gptq batched {case}")
+    B, rows, d = 3, 200, 384
+    qa = QuantizationArgs(type="int", **case)
+    Ws, Hs = [], []
+    for b in range(B):
+        Ws.append(workloads.gptq_weight(rows, d, seed=20 + b))
+        Hs.append(torch.triu(_spd_from_tokens(d, 1024, seed=30 + b)) * (b + 1))
+    Hs[2][7, 7] = -1e3        # not positive definite: RTN fallback for this member only
+    W = torch.stack(Ws).to(dev)
+    H = torch.stack(Hs).to(dev)
+    ns = torch.tensor([1.0, 2.0, 3.0])
+    res = gptq.gptq_quantize_batched(W, qa, H.clone(), num_samples=ns)
+    for b in range(B):
+        obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+        obs(W[b])
+        single = gptq.gptq_quantize(W[b], qa, H[b].clone(), obs, num_samples=float(ns[b]))
+        assert res[b].hinv_ok == single.hinv_ok == (b != 2)
+        assert torch.equal(res[b].codes, single.codes)
+        assert torch.equal(res[b].weight, single.weight)
+        assert torch.equal(res[b].scale.reshape(single.scale.shape), single.scale)
+        assert abs(res[b].loss - single.loss) <= 1e-5 * abs(single.loss) + 1e-12
+
+
 def _layer_err(W, Q, X):
     Xf = X.reshape(-1, X.shape[-1]).float()
     return (Xf @ (W.float() - Q.float()).t()).norm().item()
