@@ -18,6 +18,10 @@ struct GemmArgs {
   int64_t M, N, K;
   float alpha, beta;  // C = beta * C + alpha * (A op(B)); beta == 0 never reads C
   int lower_only;     // only C elements with row >= col (tiles fully above skipped)
+  // triangular operands (general kernel): A lower (A[i][k] = 0 for k > i) or
+  // B lower (B[k][j] = 0 for k < j) limits each tile's K range to where the
+  // operand can be nonzero
+  int a_lower, b_lower;
 };
 
 // Launches the batched GEMM (batch = total number of products) on `stream`;

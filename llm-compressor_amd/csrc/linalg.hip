@@ -123,20 +123,24 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
     }
   };
 
-  const int64_t nst = (g.K + GBK - 1) / GBK;
+  // K range of this tile: all of K, or where a triangular operand can be nonzero
+  const int64_t kbeg = g.b_lower ? (n0 / GBK) * GBK : 0;
+  const int64_t kend = g.a_lower ? (m0 + GBM < g.K ? m0 + GBM : g.K) : g.K;
+  const int64_t nst = kend > kbeg ? (kend - kbeg + GBK - 1) / GBK : 0;
   if (nst > 0) {
-    load_mk(A, g.lda, vec_a, g.M, m0, 0, ra);
-    if (BT) load_mk(B, g.ldb, vec_bk, g.N, n0, 0, rb); else load_kn(0, rb);
-    store_mk(lds_a[0], ra, g.M, m0, 0);
-    if (BT) store_mk(lds_b[0], rb, g.N, n0, 0); else store_kn(lds_b[0], rb, 0);
+    load_mk(A, g.lda, vec_a, g.M, m0, kbeg, ra);
+    if (BT) load_mk(B, g.ldb, vec_bk, g.N, n0, kbeg, rb); else load_kn(kbeg, rb);
+    store_mk(lds_a[0], ra, g.M, m0, kbeg);
+    if (BT) store_mk(lds_b[0], rb, g.N, n0, kbeg); else store_kn(lds_b[0], rb, kbeg);
   }
   __syncthreads();
   for (int64_t st = 0; st < nst; ++st) {
     const int buf = st & 1;
     const bool more = st + 1 < nst;
+    const int64_t kn = kbeg + (st + 1) * GBK;
     if (more) {
-      load_mk(A, g.lda, vec_a, g.M, m0, (st + 1) * GBK, ra);
-      if (BT) load_mk(B, g.ldb, vec_bk, g.N, n0, (st + 1) * GBK, rb); else load_kn((st + 1) * GBK, rb);
+      load_mk(A, g.lda, vec_a, g.M, m0, kn, ra);
+      if (BT) load_mk(B, g.ldb, vec_bk, g.N, n0, kn, rb); else load_kn(kn, rb);
     }
     const float* la = lds_a[buf];
     const float* lb = lds_b[buf];
@@ -158,8 +162,8 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
           acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[bm], fb[bn], acc[bm][bn], 0, 0, 0);
     }
     if (more) {
-      store_mk(lds_a[buf ^ 1], ra, g.M, m0, (st + 1) * GBK);
-      if (BT) store_mk(lds_b[buf ^ 1], rb, g.N, n0, (st + 1) * GBK); else store_kn(lds_b[buf ^ 1], rb, (st + 1) * GBK);
+      store_mk(lds_a[buf ^ 1], ra, g.M, m0, kn);
+      if (BT) store_mk(lds_b[buf ^ 1], rb, g.N, n0, kn); else store_kn(lds_b[buf ^ 1], rb, kn);
     }
     __syncthreads();
   }
@@ -648,7 +652,7 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   MQ_CHECK_ARG(batch <= 65535, "gemm: batch too large");
   // whole-tile K = 128 products (every batch member 16-byte aligned)
   const bool strides16 = g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 && g.strideB2 % 4 == 0;
-  const bool k128 = g.K == KT && g.M % KT == 0 && g.N % KT == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+  const bool k128 = !g.a_lower && !g.b_lower && g.K == KT && g.M % KT == 0 && g.N % KT == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                     aligned16(g.A) && aligned16(g.B) && (batch == 1 || strides16) &&
                     (g.lda * 7 + KT) < (1 << 29) && (g.ldb * 7 + KT) < (1 << 29) && (g.ldc * 127 + KT) < (1 << 29);
   if (k128) {
@@ -761,7 +765,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       t1.A = F + c0 * d + a0; t1.lda = d; t1.strideA = stride_diag; t1.strideA2 = wsf;
       t1.B = X + a0 * d + a0; t1.ldb = d; t1.strideB = stride_diag; t1.strideB2 = wsf;
       t1.C = T; t1.ldc = s; t1.strideC = s2 * s; t1.strideC2 = wsf;
-      t1.inner = npairs;
+      t1.inner = npairs; t1.b_lower = 1;  // X11 is lower triangular
       t1.M = s2; t1.N = s; t1.K = s; t1.alpha = 1.f; t1.beta = 0.f;
       int rc = gemm_f32(t1, false, (int)(npairs * batch), st);
       if (rc) return rc;
@@ -770,7 +774,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       t2.A = X + c0 * d + c0; t2.lda = d; t2.strideA = stride_diag; t2.strideA2 = wsf;
       t2.B = T; t2.ldb = s; t2.strideB = s2 * s; t2.strideB2 = wsf;
       t2.C = X + c0 * d + a0; t2.ldc = d; t2.strideC = stride_diag; t2.strideC2 = wsf;
-      t2.inner = npairs;
+      t2.inner = npairs; t2.a_lower = 1;  // X22 is lower triangular
       t2.M = s2; t2.N = s; t2.K = s2; t2.alpha = -1.f; t2.beta = 0.f;
       rc = gemm_f32(t2, false, (int)(npairs * batch), st);
       if (rc) return rc;
