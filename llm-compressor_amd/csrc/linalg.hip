@@ -19,6 +19,10 @@
 //   flip:     hinv[a][b] = X[d-1-a][d-1-b] for a <= b, 0 below
 #include "linalg.h"
 
+#include <rocblas/rocblas.h>
+
+#include <mutex>
+
 #pragma clang fp contract(off)
 
 namespace mi355q {
@@ -205,7 +209,7 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
 // and the current C tile are fetched into registers while the MFMAs of the
 // current tile run, so every load after the first overlaps compute.
 constexpr int KT = 128;          // tile edge and largest K
-constexpr int KLA = KT + 2;      // LDS stride of [row][k] tiles: lanes m, k and m, k+1 hit distinct banks
+constexpr int KLA = KT + 1;      // LDS stride of [row][k] tiles (odd: 32 consecutive rows hit 32 banks)
 
 // Whole tiles only: K == 128, M and N multiples of 128, 16-byte aligned rows
 // (other shapes take the general kernel).  Every address is a wave-uniform
@@ -286,22 +290,37 @@ __global__ __launch_bounds__(GNT, 1) void gemm_k128_kernel(GemmArgs g) {
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+    // operands of step kk + 1 are read while the MFMAs of step kk run
+    // (explicit double buffer + scheduling groups: the default schedule
+    // waits for each step's LDS reads right before its MFMAs)
+    {
+      const float* pa = la + (wm * 64 + (lane & 31)) * KLA + (lane >> 5);
+      const float* pb = BT ? lb + (wn * 64 + (lane & 31)) * KLA + (lane >> 5)
+                           : lb + (lane >> 5) * LBN + wn * 64 + (lane & 31);
+      auto rd = [&](int kk, float* fa, float* fb) __attribute__((always_inline)) {
+        fa[0] = pa[2 * kk];
+        fa[1] = pa[32 * KLA + 2 * kk];
+        fb[0] = BT ? pb[2 * kk] : pb[2 * kk * LBN];
+        fb[1] = BT ? pb[32 * KLA + 2 * kk] : pb[2 * kk * LBN + 32];
+      };
+      float f[2][4];
+      rd(0, f[0], f[0] + 2);
 #pragma unroll 8
-    for (int kk = 0; kk < KT / 2; ++kk) {
-      const int k = 2 * kk + (lane >> 5);
-      float fa[2], fb[2];
+      for (int kk = 0; kk < KT / 2; ++kk) {
+        float* cur = f[kk & 1];
+        float* nxt = f[(kk + 1) & 1];
+        if (kk + 1 < KT / 2) rd(kk + 1, nxt, nxt + 2);
 #pragma unroll
-      for (int bm = 0; bm < 2; ++bm) fa[bm] = la[(wm * 64 + bm * 32 + (lane & 31)) * KLA + k];
+        for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-      for (int bn = 0; bn < 2; ++bn) {
-        const int n = wn * 64 + bn * 32 + (lane & 31);
-        fb[bn] = BT ? lb[n * KLA + k] : lb[k * LBN + n];
+          for (int bn = 0; bn < 2; ++bn)
+            acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[bm], cur[2 + bn], acc[bm][bn], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of step kk
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one read of step kk + 1
+        }
       }
-#pragma unroll
-      for (int bm = 0; bm < 2; ++bm)
-#pragma unroll
-        for (int bn = 0; bn < 2; ++bn)
-          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[bm], fb[bn], acc[bm][bn], 0, 0, 0);
     }
     const bool diag = g.lower_only && n0 == m0;  // only the diagonal tile straddles gm >= gn
 #pragma unroll
@@ -647,8 +666,51 @@ HinvLayout hinv_layout(int64_t d) {
 
 }  // namespace
 
+// Large-K products (K >= 256, not lower-only) are plain GEMMs that rocBLAS
+// runs near the fp32 MFMA peak; one handle per device, its stream set under
+// a lock for each call (rocBLAS keeps its own workspace).
+namespace {
+std::mutex g_blas_mu;
+rocblas_handle g_blas[64] = {};
+
+int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
+  int dev = 0;
+  MQ_CHECK_HIP(hipGetDevice(&dev));
+  MQ_CHECK_ARG(dev >= 0 && dev < 64, "gemm: device index out of range");
+  std::lock_guard<std::mutex> lock(g_blas_mu);
+  if (!g_blas[dev] && rocblas_create_handle(&g_blas[dev]) != rocblas_status_success) {
+    g_blas[dev] = nullptr;
+    set_error("rocblas_create_handle failed");
+    return MI355Q_HIP_ERROR;
+  }
+  rocblas_handle h = g_blas[dev];
+  if (rocblas_set_stream(h, stream) != rocblas_status_success) {
+    set_error("rocblas_set_stream failed");
+    return MI355Q_HIP_ERROR;
+  }
+  // row-major C = alpha A op(B) + beta C  <=>  column-major C^T = alpha op(B)^T A^T + beta C^T
+  const int64_t inner = g.inner > 0 ? g.inner : batch;
+  const int64_t outer = batch / inner;
+  for (int64_t b2 = 0; b2 < outer; ++b2) {
+    const rocblas_status rs = rocblas_sgemm_strided_batched(
+        h, b_trans ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none,
+        (rocblas_int)g.N, (rocblas_int)g.M, (rocblas_int)g.K, &g.alpha, g.B + b2 * g.strideB2, (rocblas_int)g.ldb,
+        g.strideB, g.A + b2 * g.strideA2, (rocblas_int)g.lda, g.strideA, &g.beta, g.C + b2 * g.strideC2,
+        (rocblas_int)g.ldc, g.strideC, (rocblas_int)inner);
+    if (rs != rocblas_status_success) {
+      set_error("rocblas_sgemm_strided_batched failed: %s", rocblas_status_to_string(rs));
+      return MI355Q_HIP_ERROR;
+    }
+  }
+  return MI355Q_OK;
+}
+}  // namespace
+
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
+  if (g.K >= 256 && !g.lower_only && g.M < (1ll << 31) && g.N < (1ll << 31) && g.K < (1ll << 31) &&
+      (g.inner == 0 || batch % g.inner == 0))
+    return gemm_rocblas(g, b_trans, batch, stream);
   MQ_CHECK_ARG(batch <= 65535, "gemm: batch too large");
   // whole-tile K = 128 products (every batch member 16-byte aligned)
   const bool strides16 = g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 && g.strideB2 % 4 == 0;
