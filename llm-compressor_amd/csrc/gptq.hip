@@ -23,6 +23,7 @@ constexpr int SW_ROWS = 16;              // rows per workgroup
 constexpr int SW_NT = SW_G * SW_ROWS;    // 256 threads
 constexpr int MAXB = 128;                // largest supported block size
 constexpr int SW_T = MAXB / SW_G;        // columns per lane
+constexpr int SUPER = 1024;              // columns per lazy-update super-block
 
 // Per-lane state of the sweep: lane g of a row holds block columns
 // SW_G * t + g, t = 0..SW_T-1.
@@ -103,7 +104,8 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
     int count, const float* __restrict__ scale, const float* __restrict__ zp, int64_t ld_scale,
     const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax, int dq_bf16,
-    int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, SweepBatch sb) {
+    int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, int err_col,
+    SweepBatch sb) {
   __shared__ float h1[MAXB * MAXB];
   __shared__ int gsh[MAXB];
   {
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
         const int64_t c = i1 + col;
         W[r * cols + c] = S.q[t];
         codes[r * cols + c] = (int8_t)S.cq[t];
-        err_out[r * MAXB + col] = S.er[t];
+        err_out[r * SUPER + err_col + col] = S.er[t];
       }
     }
   }
@@ -294,7 +296,7 @@ extern "C" int mi355q_gptq_load_weight(const void* w_dev, mi355q_dtype w_dtype, 
 extern "C" size_t mi355q_gptq_sweep_workspace_size(int64_t rows, int64_t cols, int64_t blocksize) {
   (void)cols;
   (void)blocksize;
-  return rows > 0 ? (size_t)rows * MAXB * sizeof(float) : 0;
+  return rows > 0 ? (size_t)rows * SUPER * sizeof(float) : 0;
 }
 
 extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
@@ -319,25 +321,46 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
   MQ_CHECK_ARG(workspace_dev && workspace_bytes >= need, "gptq_sweep: workspace too small");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* err = static_cast<float*>(workspace_dev);
-  SweepBatch sb{rows * cols, stride_hinv, stride_scale, stride_gidx, rows * cols, rows, rows * MAXB};
+  SweepBatch sb{rows * cols, stride_hinv, stride_scale, stride_gidx, rows * cols, rows, rows * SUPER};
   // the sweep kernel holds at most MAXB columns; larger reference block
   // sizes give the same result up to fp32 rounding of the lazy update, so
-  // they are processed in MAXB-wide sub-blocks
+  // they are processed in MAXB-wide sub-blocks.
+  //
+  // Lazy updates are two-level: inside a super-block of SUPER columns each
+  // block's errors update the rest of the super-block (K = block size, as in
+  // the reference); the columns past the super-block receive the errors of
+  // all its blocks in one GEMM with K up to SUPER.  The far columns thus get
+  // Sum_b Err_b Hinv[b, far] rounded once instead of once per block, an fp32
+  // rounding-order difference of the same kind as a GEMM's summation order.
   const int64_t B = blocksize < MAXB ? blocksize : MAXB;
+  const int64_t sup = (SUPER / B) * B;  // whole blocks per super-block: block boundaries as in the reference
   const unsigned nwg = (unsigned)((rows + SW_ROWS - 1) / SW_ROWS);
-  for (int64_t i1 = 0; i1 < cols; i1 += B) {
-    const int64_t i2 = (i1 + B < cols) ? i1 + B : cols;
-    const int count = (int)(i2 - i1);
-    hipLaunchKernelGGL(sweep_block_kernel, dim3(nwg, (unsigned)batch), dim3(SW_NT), 0, st, w_work_dev, rows, cols,
-                       hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
-                       qmax, dequant_bf16, codes_dev, losses_dev, err, sb);
-    MQ_LAUNCH_CHECK();
-    if (i2 < cols) {
+  for (int64_t s0 = 0; s0 < cols; s0 += sup) {
+    const int64_t s1 = s0 + sup < cols ? s0 + sup : cols;
+    for (int64_t i1 = s0; i1 < s1; i1 += B) {
+      const int64_t i2 = (i1 + B < s1) ? i1 + B : s1;
+      const int count = (int)(i2 - i1);
+      hipLaunchKernelGGL(sweep_block_kernel, dim3(nwg, (unsigned)batch), dim3(SW_NT), 0, st, w_work_dev, rows,
+                         cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
+                         qmax, dequant_bf16, codes_dev, losses_dev, err, (int)(i1 - s0), sb);
+      MQ_LAUNCH_CHECK();
+      if (i2 < s1) {
+        GemmArgs g{};
+        g.A = err + (i1 - s0); g.lda = SUPER; g.strideA = rows * SUPER;
+        g.B = hinv_dev + i1 * cols + i2; g.ldb = cols; g.strideB = stride_hinv;
+        g.C = w_work_dev + i2; g.ldc = cols; g.strideC = rows * cols;
+        g.M = rows; g.N = s1 - i2; g.K = count;
+        g.alpha = -1.f; g.beta = 1.f;
+        int rc = gemm_f32(g, false, (int)batch, st);
+        if (rc) return rc;
+      }
+    }
+    if (s1 < cols) {
       GemmArgs g{};
-      g.A = err; g.lda = MAXB; g.strideA = rows * MAXB;
-      g.B = hinv_dev + i1 * cols + i2; g.ldb = cols; g.strideB = stride_hinv;
-      g.C = w_work_dev + i2; g.ldc = cols; g.strideC = rows * cols;
-      g.M = rows; g.N = cols - i2; g.K = count;
+      g.A = err; g.lda = SUPER; g.strideA = rows * SUPER;
+      g.B = hinv_dev + s0 * cols + s1; g.ldb = cols; g.strideB = stride_hinv;
+      g.C = w_work_dev + s1; g.ldc = cols; g.strideC = rows * cols;
+      g.M = rows; g.N = cols - s1; g.K = s1 - s0;
       g.alpha = -1.f; g.beta = 1.f;
       int rc = gemm_f32(g, false, (int)batch, st);
       if (rc) return rc;
