@@ -704,6 +704,33 @@ int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream)
   }
   return MI355Q_OK;
 }
+
+// Lower triangle of row-major C (n x n) += alpha P P^T with P (n x k) row-major:
+// rocBLAS ssyrk on the column-major view (upper triangle of C^T = C).
+int syrk_rocblas(float* C, int64_t ldc, const float* P, int64_t ldp, int64_t n, int64_t k, float alpha, float beta,
+                 hipStream_t stream) {
+  int dev = 0;
+  MQ_CHECK_HIP(hipGetDevice(&dev));
+  MQ_CHECK_ARG(dev >= 0 && dev < 64, "syrk: device index out of range");
+  std::lock_guard<std::mutex> lock(g_blas_mu);
+  if (!g_blas[dev] && rocblas_create_handle(&g_blas[dev]) != rocblas_status_success) {
+    g_blas[dev] = nullptr;
+    set_error("rocblas_create_handle failed");
+    return MI355Q_HIP_ERROR;
+  }
+  rocblas_handle h = g_blas[dev];
+  if (rocblas_set_stream(h, stream) != rocblas_status_success) {
+    set_error("rocblas_set_stream failed");
+    return MI355Q_HIP_ERROR;
+  }
+  const rocblas_status rs = rocblas_ssyrk(h, rocblas_fill_upper, rocblas_operation_transpose, (rocblas_int)n,
+                                          (rocblas_int)k, &alpha, P, (rocblas_int)ldp, &beta, C, (rocblas_int)ldc);
+  if (rs != rocblas_status_success) {
+    set_error("rocblas_ssyrk failed: %s", rocblas_status_to_string(rs));
+    return MI355Q_HIP_ERROR;
+  }
+  return MI355Q_OK;
+}
 }  // namespace
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
@@ -772,32 +799,59 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
                      wsf);
   MQ_LAUNCH_CHECK();
 
-  // blocked right-looking Cholesky on F (lower)
+  // blocked right-looking Cholesky on F (lower), two levels: inside an outer
+  // panel of OUTB blocks each 128-column block updates only the panel's
+  // remaining columns (K = 128); the trailing matrix past the panel takes
+  // one rank-(OUTB * 128) update, a syrk with K up to 512
+  constexpr int64_t OUTB = 4;
   const int64_t nblk = (d + NB - 1) / NB;
-  for (int64_t kb = 0; kb < nblk; ++kb) {
-    const int64_t k0 = kb * NB;
-    const int nb = (int)((d - k0) < NB ? (d - k0) : NB);
-    hipLaunchKernelGGL(potf2_inv_kernel, dim3(nb_), dim3(PNT), 0, st, F, d, k0, nb, linv + kb * NB * NB,
-                       status_dev, wsf);
-    MQ_LAUNCH_CHECK();
-    const int64_t rest = d - k0 - nb;
-    if (rest <= 0) break;
-    // panel: F[k0+nb:, k0:k0+nb] = F[...] * linv^T (in place, one workgroup per row tile)
-    GemmArgs p{};
-    p.A = F + (k0 + nb) * d + k0; p.lda = d; p.strideA = wsf;
-    p.B = linv + kb * NB * NB; p.ldb = NB; p.strideB = wsf;
-    p.C = F + (k0 + nb) * d + k0; p.ldc = d; p.strideC = wsf;
-    p.M = rest; p.N = nb; p.K = nb; p.alpha = 1.f; p.beta = 0.f;
-    int rc = gemm_f32(p, true, (int)batch, st);
-    if (rc) return rc;
-    // trailing: F[k0+nb:, k0+nb:] -= P P^T (lower)
-    GemmArgs s{};
-    s.A = F + (k0 + nb) * d + k0; s.lda = d; s.strideA = wsf;
-    s.B = F + (k0 + nb) * d + k0; s.ldb = d; s.strideB = wsf;
-    s.C = F + (k0 + nb) * d + (k0 + nb); s.ldc = d; s.strideC = wsf;
-    s.M = rest; s.N = rest; s.K = nb; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
-    rc = gemm_f32(s, true, (int)batch, st);
-    if (rc) return rc;
+  for (int64_t ob = 0; ob < nblk; ob += OUTB) {
+    const int64_t oe = ob + OUTB < nblk ? ob + OUTB : nblk;
+    const int64_t c0 = ob * NB, c_end = oe * NB < d ? oe * NB : d;
+    for (int64_t kb = ob; kb < oe; ++kb) {
+      const int64_t k0 = kb * NB;
+      const int nb = (int)((d - k0) < NB ? (d - k0) : NB);
+      hipLaunchKernelGGL(potf2_inv_kernel, dim3(nb_), dim3(PNT), 0, st, F, d, k0, nb, linv + kb * NB * NB,
+                         status_dev, wsf);
+      MQ_LAUNCH_CHECK();
+      const int64_t rest = d - k0 - nb;
+      if (rest <= 0) break;
+      // panel: F[k0+nb:, k0:k0+nb] = F[...] * linv^T (in place, one workgroup per row tile)
+      GemmArgs p{};
+      p.A = F + (k0 + nb) * d + k0; p.lda = d; p.strideA = wsf;
+      p.B = linv + kb * NB * NB; p.ldb = NB; p.strideB = wsf;
+      p.C = F + (k0 + nb) * d + k0; p.ldc = d; p.strideC = wsf;
+      p.M = rest; p.N = nb; p.K = nb; p.alpha = 1.f; p.beta = 0.f;
+      int rc = gemm_f32(p, true, (int)batch, st);
+      if (rc) return rc;
+      // inside the outer panel: F[k0+nb:, k0+nb:c_end] -= P P[:c_end-k0-nb]^T (lower)
+      const int64_t nin = c_end - (k0 + nb);
+      if (nin > 0) {
+        GemmArgs s{};
+        s.A = F + (k0 + nb) * d + k0; s.lda = d; s.strideA = wsf;
+        s.B = F + (k0 + nb) * d + k0; s.ldb = d; s.strideB = wsf;
+        s.C = F + (k0 + nb) * d + (k0 + nb); s.ldc = d; s.strideC = wsf;
+        s.M = rest; s.N = nin; s.K = nb; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
+        rc = gemm_f32(s, true, (int)batch, st);
+        if (rc) return rc;
+      }
+    }
+    // past the outer panel: F[c_end:, c_end:] -= P P^T (lower), P = F[c_end:, c0:c_end]
+    const int64_t rest2 = d - c_end, kk = c_end - c0;
+    if (rest2 > 0) {
+      if (batch == 1 && kk >= 256) {
+        int rc = syrk_rocblas(F + c_end * d + c_end, d, F + c_end * d + c0, d, rest2, kk, -1.f, 1.f, st);
+        if (rc) return rc;
+      } else {
+        GemmArgs s{};
+        s.A = F + c_end * d + c0; s.lda = d; s.strideA = wsf;
+        s.B = F + c_end * d + c0; s.ldb = d; s.strideB = wsf;
+        s.C = F + c_end * d + c_end; s.ldc = d; s.strideC = wsf;
+        s.M = rest2; s.N = rest2; s.K = kk; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
+        int rc = gemm_f32(s, true, (int)batch, st);
+        if (rc) return rc;
+      }
+    }
   }
 
   // triangular inverse X = L^-1 by recursive doubling over NB blocks; the
