@@ -424,61 +424,62 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
   __syncthreads();
 
   bool bad = false;
+#pragma unroll 1
   for (int kb = 0; kb < NB / SB; ++kb) {
     const int o = kb * SB;
     if (wave == 0) {
-      // Lanes 0..31 each hold one row of the sub-block.  LDS operations of
-      // one wave complete in program order, so the column buffer needs no
-      // barrier between its write and the reads that follow.
+      // Lanes 0..31 hold the rows of the sub-block (row role), lanes 32..63
+      // the columns of its inverse (column role): v = row li of A, or column
+      // li of X = L^-1, initially e_li.  Right-looking Cholesky and the
+      // inverse's row elimination (X[j][:] /= L[j][j]; X[i][:] -= L[i][j]
+      // X[j][:], i > j) advance together, and with col = A[:, j] before
+      // scaling both take the same form:
+      //   m = v[j] / piv;  v[k] -= m col[k] (k > j);  v[j] /= L[j][j]
+      // (a row's diagonal becomes L[j][j] itself).  Column j reaches every
+      // lane through one LDS write and eight broadcast reads (a wave's LDS
+      // operations complete in program order, so no barrier is needed).
+      // Entries above the diagonal are updated too and never stored, which
+      // keeps every update unpredicated.
       const int li = lane & 31;
-      const int row = o + li;
-      float* cb = t;  // 32-float buffer (t is idle during the factorisation)
-      float r[SB];
+      const bool row_role = lane < SB;
+      float* cb = t;  // column buffer: cb[0..31] = column j (t is idle during the factorisation)
+      float v[SB];
 #pragma unroll
-      for (int c = 0; c < SB; ++c) r[c] = a[row * LP + o + c];
-      // right-looking Cholesky.  Column j's entries reach every lane through
-      // ds_bpermute (a VGPR result, so no SGPR pressure however many are in
-      // flight): L[i][j] L[c][j] = A[i][j] A[c][j] / piv, one FMA each.
-      // Entries above the diagonal (c > row) are updated too and never read
-      // into the lower triangle, which keeps every update unpredicated.
+      for (int c = 0; c < SB; ++c) v[c] = row_role ? a[(o + li) * LP + o + c] : ((c == li) ? 1.f : 0.f);
 #pragma unroll
       for (int j = 0; j < SB; ++j) {
-        float piv = bperm(r[j], j);
+        // every lane stores (column-role lanes into a scratch slot): no
+        // divergent branch around the LDS write that the reads could sink into
+        cb[lane] = v[j];
+        float col[SB];
+#pragma unroll
+        for (int q = 0; q < SB / 4; ++q) {
+          const f32x4_t w = *reinterpret_cast<const f32x4_t*>(cb + 4 * q);
+          col[4 * q] = w[0];
+          col[4 * q + 1] = w[1];
+          col[4 * q + 2] = w[2];
+          col[4 * q + 3] = w[3];
+        }
+        float piv = col[j];
         if (!(piv > 0.f) || !isfinite(piv)) {
           bad = true;
           piv = 1.f;
         }
         const float ljj = sqrtf(piv);
-        const float tj = r[j] * (1.f / piv);
+        const float m = v[j] * (1.f / piv);
 #pragma unroll
-        for (int c = j + 1; c < SB; ++c) r[c] = fmaf(-tj, bperm(r[j], c), r[c]);
-        r[j] = (li == j) ? ljj : r[j] / ljj;
+        for (int k = j + 1; k < SB; ++k) v[k] = fmaf(-m, col[k], v[k]);
+        v[j] = (row_role && li == j) ? ljj : v[j] / ljj;
       }
-      // store L and the reciprocal diagonal
-      if (lane < SB) {
+      // store row li of L (row role) and column li of L^-1 (column role)
+      if (row_role) {
 #pragma unroll
         for (int c = 0; c < SB; ++c)
-          if (c <= li) a[row * LP + o + c] = r[c];
-        cb[li] = 1.f / r[li];
-      }
-      // inverse: lane c solves L x = e_c by forward substitution (column c
-      // of L^-1); every lane reads the same L entries (LDS broadcast)
-      float xv[SB];
-#pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        float s0 = (i == li) ? 1.f : 0.f, s1 = 0.f;
-#pragma unroll
-        for (int k = 0; k + 1 < i; k += 2) {
-          s0 = fmaf(-a[(o + i) * LP + o + k], xv[k], s0);
-          s1 = fmaf(-a[(o + i) * LP + o + k + 1], xv[k + 1], s1);
-        }
-        if (i & 1) s0 = fmaf(-a[(o + i) * LP + o + i - 1], xv[i - 1], s0);
-        xv[i] = (s0 + s1) * cb[i];
-      }
-      if (lane < SB) {
+          if (c <= li) a[(o + li) * LP + o + c] = v[c];
+      } else {
 #pragma unroll
         for (int i = 0; i < SB; ++i)
-          if (i >= li) x[(o + i) * LP + o + li] = xv[i];
+          if (i >= li) x[(o + i) * LP + o + li] = v[i];
       }
     }
     __syncthreads();
