@@ -24,6 +24,12 @@ constexpr int SW_NT = SW_G * SW_ROWS;    // 256 threads
 constexpr int MAXB = 128;                // largest supported block size
 constexpr int SW_T = MAXB / SW_G;        // columns per lane
 constexpr int SUPER = 1024;              // columns per lazy-update super-block
+constexpr int HPK = MAXB * (MAXB + 1) / 2;  // packed upper triangle of a Hinv block
+
+// Row i of the block's upper triangle starts at hrow(i) in the packed LDS copy
+// (element (i, j), j >= i, at hrow(i) + j - i): 33 KB instead of 64 KB, so four
+// workgroups fit in a CU's LDS.
+__host__ __device__ constexpr int hrow(int i) { return i * MAXB - i * (i - 1) / 2; }
 
 // Per-lane state of the sweep: lane g of a row holds block columns
 // SW_G * t + g, t = 0..SW_T-1.
@@ -58,7 +64,7 @@ __device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, int g
                                            float qmax, bool dq_bf16) {
   constexpr int I = SW_G * TO + GO;
   if (I >= count) return;
-  const float dd = h1[I * MAXB + I];
+  const float dd = h1[hrow(I)];
   const float x = S.w[TO];
   float qq = x / S.s[TO] + S.z[TO];
   qq = rintf(fminf(fmaxf(qq, qmin), qmax));
@@ -75,7 +81,8 @@ __device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, int g
 #pragma unroll
   for (int t = TO; t < SW_T; ++t) {
     const int col = SW_G * t + g;
-    const float upd = S.w[t] - e * h1[I * MAXB + col];
+    // (col < I reads a neighbouring entry, in bounds, and is never taken)
+    const float upd = S.w[t] - e * h1[hrow(I) - I + col];
     const bool take = (t > TO || g > GO) && col < count;
     S.w[t] = take ? upd : S.w[t];
   }
@@ -106,7 +113,7 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
     const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax, int dq_bf16,
     int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, int err_col,
     SweepBatch sb) {
-  __shared__ float h1[MAXB * MAXB];
+  __shared__ float h1[HPK];
   __shared__ int gsh[MAXB];
   {
     const int64_t b = blockIdx.y;
@@ -142,12 +149,15 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
 #pragma unroll
     for (int v = 0; v < MAXB * MAXB / 4 / SW_NT; ++v) {
       const int e = v * SW_NT + tid;
-      *reinterpret_cast<f32x4_t*>(h1 + (e >> 5) * MAXB + (e & 31) * 4) = hv[v];
+      const int i = e >> 5, j0 = (e & 31) * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (j0 + q >= i) h1[hrow(i) + j0 + q - i] = hv[v][q];
     }
   } else {
     for (int e = tid; e < count * count; e += SW_NT) {
       const int i = e / count, j = e % count;
-      if (j >= i) h1[i * MAXB + j] = hinv[(i1 + i) * cols + (i1 + j)];
+      if (j >= i) h1[hrow(i) + j - i] = hinv[(i1 + i) * cols + (i1 + j)];
     }
   }
   const bool uses_gidx = strategy == MI355Q_GROUP || strategy == MI355Q_BLOCK;
@@ -176,7 +186,7 @@ __global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
   for (int t = 0; t < SW_T; ++t) {
     const int col = SW_G * t + g;
     if (col < count) {
-      const float dd = h1[col * MAXB + col];
+      const float dd = h1[hrow(col)];
       loss = loss + S.df[t] * S.df[t] / (dd * dd);
     }
   }

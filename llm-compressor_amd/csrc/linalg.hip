@@ -736,9 +736,23 @@ int syrk_rocblas(float* C, int64_t ldc, const float* P, int64_t ldp, int64_t n, 
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
+  // (one strided-batched library call: a single level of batching)
   if (g.K >= 256 && !g.lower_only && g.M < (1ll << 31) && g.N < (1ll << 31) && g.K < (1ll << 31) &&
-      (g.inner == 0 || batch % g.inner == 0))
+      (g.inner == 0 || g.inner == batch))
     return gemm_rocblas(g, b_trans, batch, stream);
+  // large-K lower-only products: K = 128 slices on the whole-tile kernel
+  if (g.lower_only && g.K > KT && g.K % KT == 0 && g.M % KT == 0 && g.N % KT == 0) {
+    GemmArgs s = g;
+    s.K = KT;
+    for (int64_t k0 = 0; k0 < g.K; k0 += KT) {
+      s.A = g.A + k0;
+      s.B = b_trans ? g.B + k0 : g.B + k0 * g.ldb;
+      s.beta = k0 == 0 ? g.beta : 1.f;
+      const int rc = gemm_f32(s, b_trans, batch, stream);
+      if (rc) return rc;
+    }
+    return MI355Q_OK;
+  }
   MQ_CHECK_ARG(batch <= 65535, "gemm: batch too large");
   // whole-tile K = 128 products (every batch member 16-byte aligned)
   const bool strides16 = g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 && g.strideB2 % 4 == 0;
