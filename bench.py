@@ -385,9 +385,11 @@ def bench_moe(a):
         moe.accumulate_expert_hessians(hs, rows, offsets, Hgu, ns)
         moe.accumulate_expert_hessians(inter_x, ident, offsets, Hd, ns.clone())
         ev[1].record()
-        # all experts of one projection solved together (one launch per step)
-        gptq.gptq_quantize_batched(gate, qa, Hgu, num_samples=ns)
-        gptq.gptq_quantize_batched(up, qa, Hgu, num_samples=ns)
+        # all experts of one projection solved together (one launch per step);
+        # gate and up share their input, hence their Hessian and its Cholesky chain
+        pgu = gptq.prepare_hessians_batched(Hgu, qa, ns)
+        gptq.gptq_quantize_batched(gate, qa, Hgu, num_samples=ns, prepared=pgu)
+        gptq.gptq_quantize_batched(up, qa, Hgu, num_samples=ns, prepared=pgu)
         gptq.gptq_quantize_batched(down, qa, Hd, num_samples=ns)
         ev[2].record()
 
@@ -450,10 +452,11 @@ def bench_decoder(a):
             Hs.append(H)
         ev[1].record()
         for (names, _), H in zip(groups, Hs):
+            prep = gptq.prepare_hessian(H, qa, float(batches))   # shared by modules with the same input
             for nm in names:
                 obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
                 obs(lin[nm].weight)
-                gptq.gptq_quantize(lin[nm].weight, qa, H, obs, num_samples=float(batches))
+                gptq.gptq_quantize(lin[nm].weight, qa, H, obs, num_samples=float(batches), prepared=prep)
         ev[2].record()
 
     ms, _ = _timed(torch, step, a.steps, a.warmup)

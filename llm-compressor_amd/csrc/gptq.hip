@@ -107,7 +107,7 @@ struct SweepBatch {
   int64_t w, hinv, scale, gidx, codes, losses, err;
 };
 
-__global__ __launch_bounds__(SW_NT) void sweep_block_kernel(
+__global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
     int count, const float* __restrict__ scale, const float* __restrict__ zp, int64_t ld_scale,
     const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax, int dq_bf16,

@@ -689,15 +689,20 @@ int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream)
     set_error("rocblas_set_stream failed");
     return MI355Q_HIP_ERROR;
   }
-  // row-major C = alpha A op(B) + beta C  <=>  column-major C^T = alpha op(B)^T A^T + beta C^T
-  const int64_t inner = g.inner > 0 ? g.inner : batch;
-  const int64_t outer = batch / inner;
-  for (int64_t b2 = 0; b2 < outer; ++b2) {
+  // row-major C = alpha A op(B) + beta C  <=>  column-major C^T = alpha op(B)^T A^T + beta C^T.
+  // Two batch levels: one strided-batched call per index of the shorter level.
+  const int64_t n1 = g.inner > 0 ? g.inner : batch, n2 = batch / n1;
+  const bool loop1 = n1 < n2;  // loop over level 1, batch over level 2
+  const int64_t nloop = loop1 ? n1 : n2, nbat = loop1 ? n2 : n1;
+  const int64_t sa = loop1 ? g.strideA2 : g.strideA, sb = loop1 ? g.strideB2 : g.strideB,
+                sc = loop1 ? g.strideC2 : g.strideC;
+  for (int64_t l = 0; l < nloop; ++l) {
+    const int64_t oa = l * (loop1 ? g.strideA : g.strideA2), ob = l * (loop1 ? g.strideB : g.strideB2),
+                  oc = l * (loop1 ? g.strideC : g.strideC2);
     const rocblas_status rs = rocblas_sgemm_strided_batched(
         h, b_trans ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none,
-        (rocblas_int)g.N, (rocblas_int)g.M, (rocblas_int)g.K, &g.alpha, g.B + b2 * g.strideB2, (rocblas_int)g.ldb,
-        g.strideB, g.A + b2 * g.strideA2, (rocblas_int)g.lda, g.strideA, &g.beta, g.C + b2 * g.strideC2,
-        (rocblas_int)g.ldc, g.strideC, (rocblas_int)inner);
+        (rocblas_int)g.N, (rocblas_int)g.M, (rocblas_int)g.K, &g.alpha, g.B + ob, (rocblas_int)g.ldb, sb,
+        g.A + oa, (rocblas_int)g.lda, sa, &g.beta, g.C + oc, (rocblas_int)g.ldc, sc, (rocblas_int)nbat);
     if (rs != rocblas_status_success) {
       set_error("rocblas_sgemm_strided_batched failed: %s", rocblas_status_to_string(rs));
       return MI355Q_HIP_ERROR;
@@ -709,7 +714,7 @@ int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream)
 // Lower triangle of row-major C (n x n) += alpha P P^T with P (n x k) row-major:
 // rocBLAS ssyrk on the column-major view (upper triangle of C^T = C).
 int syrk_rocblas(float* C, int64_t ldc, const float* P, int64_t ldp, int64_t n, int64_t k, float alpha, float beta,
-                 hipStream_t stream) {
+                 int64_t batch, int64_t stride, hipStream_t stream) {
   int dev = 0;
   MQ_CHECK_HIP(hipGetDevice(&dev));
   MQ_CHECK_ARG(dev >= 0 && dev < 64, "syrk: device index out of range");
@@ -724,8 +729,12 @@ int syrk_rocblas(float* C, int64_t ldc, const float* P, int64_t ldp, int64_t n, 
     set_error("rocblas_set_stream failed");
     return MI355Q_HIP_ERROR;
   }
-  const rocblas_status rs = rocblas_ssyrk(h, rocblas_fill_upper, rocblas_operation_transpose, (rocblas_int)n,
-                                          (rocblas_int)k, &alpha, P, (rocblas_int)ldp, &beta, C, (rocblas_int)ldc);
+  const rocblas_status rs =
+      batch == 1 ? rocblas_ssyrk(h, rocblas_fill_upper, rocblas_operation_transpose, (rocblas_int)n, (rocblas_int)k,
+                                 &alpha, P, (rocblas_int)ldp, &beta, C, (rocblas_int)ldc)
+                 : rocblas_ssyrk_strided_batched(h, rocblas_fill_upper, rocblas_operation_transpose, (rocblas_int)n,
+                                                 (rocblas_int)k, &alpha, P, (rocblas_int)ldp, stride, &beta, C,
+                                                 (rocblas_int)ldc, stride, (rocblas_int)batch);
   if (rs != rocblas_status_success) {
     set_error("rocblas_ssyrk failed: %s", rocblas_status_to_string(rs));
     return MI355Q_HIP_ERROR;
@@ -736,9 +745,9 @@ int syrk_rocblas(float* C, int64_t ldc, const float* P, int64_t ldp, int64_t n, 
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
-  // (one strided-batched library call: a single level of batching)
+  // (at most 8 strided-batched library calls: the shorter batch level is looped)
   if (g.K >= 256 && !g.lower_only && g.M < (1ll << 31) && g.N < (1ll << 31) && g.K < (1ll << 31) &&
-      (g.inner == 0 || g.inner == batch))
+      (g.inner == 0 || (batch % g.inner == 0 && (g.inner <= 8 || batch / g.inner <= 8))))
     return gemm_rocblas(g, b_trans, batch, stream);
   // large-K lower-only products: K = 128 slices on the whole-tile kernel
   if (g.lower_only && g.K > KT && g.K % KT == 0 && g.M % KT == 0 && g.N % KT == 0) {
@@ -817,7 +826,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
   // blocked right-looking Cholesky on F (lower), two levels: inside an outer
   // panel of OUTB blocks each 128-column block updates only the panel's
   // remaining columns (K = 128); the trailing matrix past the panel takes
-  // one rank-(OUTB * 128) update, a syrk with K up to 512
+  // one rank-(OUTB * 128) update, a syrk with K up to 512 (rocBLAS)
   constexpr int64_t OUTB = 4;
   const int64_t nblk = (d + NB - 1) / NB;
   for (int64_t ob = 0; ob < nblk; ob += OUTB) {
@@ -854,8 +863,8 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
     // past the outer panel: F[c_end:, c_end:] -= P P^T (lower), P = F[c_end:, c0:c_end]
     const int64_t rest2 = d - c_end, kk = c_end - c0;
     if (rest2 > 0) {
-      if (batch == 1 && kk >= 256) {
-        int rc = syrk_rocblas(F + c_end * d + c_end, d, F + c_end * d + c0, d, rest2, kk, -1.f, 1.f, st);
+      if (kk >= 256) {
+        int rc = syrk_rocblas(F + c_end * d + c_end, d, F + c_end * d + c0, d, rest2, kk, -1.f, 1.f, batch, wsf, st);
         if (rc) return rc;
       } else {
         GemmArgs s{};

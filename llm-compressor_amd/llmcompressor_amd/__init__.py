@@ -6,8 +6,8 @@ observer registry, ``observe`` / ``update_qparams``); the arithmetic runs in
 hand-written HIP kernels (``libmi355q.so``, C ABI in ``include/mi355q.h``).
 """
 from .calibration import initialize_module_for_quantization, initialize_observer, observe, update_qparams
-from .gptq import GPTQResult, accumulate_hessian, gptq_quantize, make_empty_hessian, quantize_weight, \
-    symmetrize_hessian
+from .gptq import GPTQResult, PreparedHessian, accumulate_hessian, gptq_quantize, gptq_quantize_batched, \
+    make_empty_hessian, prepare_hessian, prepare_hessians_batched, quantize_weight, symmetrize_hessian
 from .modifiers import GPTQModifier, QuantizationModifier
 from .observers import Observer
 from .quant_args import (ActivationOrdering, QuantizationArgs, QuantizationScheme, QuantizationStrategy,
@@ -16,6 +16,7 @@ from .quant_args import (ActivationOrdering, QuantizationArgs, QuantizationSchem
 __all__ = [
     "ActivationOrdering", "GPTQModifier", "GPTQResult", "Observer", "QuantizationArgs", "QuantizationModifier",
     "QuantizationScheme", "QuantizationStrategy", "QuantizationType", "accumulate_hessian", "gptq_quantize",
-    "initialize_module_for_quantization", "initialize_observer", "make_empty_hessian", "observe",
-    "preset_name_to_scheme", "quantize_weight", "symmetrize_hessian", "update_qparams",
+    "gptq_quantize_batched", "initialize_module_for_quantization", "initialize_observer", "make_empty_hessian",
+    "observe", "prepare_hessian", "prepare_hessians_batched", "PreparedHessian", "preset_name_to_scheme",
+    "quantize_weight", "symmetrize_hessian", "update_qparams",
 ]

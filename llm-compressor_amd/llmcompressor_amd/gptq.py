@@ -29,7 +29,8 @@ logger = logging.getLogger("llmcompressor_amd")
 GPTQ_PRECISION = torch.float32
 
 __all__ = ["make_empty_hessian", "accumulate_hessian", "quantize_weight", "symmetrize_hessian",
-           "GPTQResult", "gptq_quantize", "gptq_quantize_batched"]
+           "GPTQResult", "gptq_quantize", "gptq_quantize_batched", "PreparedHessian", "prepare_hessian",
+           "prepare_hessians_batched"]
 
 
 def make_empty_hessian(module: torch.nn.Module, device: torch.device | None = None) -> torch.Tensor:
@@ -92,17 +93,82 @@ def _qparams_for_sweep(scale: torch.Tensor, zero_point: torch.Tensor, strategy: 
     return s.contiguous(), z.contiguous()
 
 
+@dataclass
+class PreparedHessian:
+    """The weight-independent part of the solve for one Hessian (or a stack):
+    activation-order permutation, dead columns and the upper Cholesky factor of
+    the damped inverse, with the RTN fallback already applied.  Modules whose
+    inputs are the same tensor (q/k/v, gate/up) share it."""
+    actorder: ActivationOrdering | None
+    perm: torch.Tensor | None
+    invperm: torch.Tensor | None
+    hinv: torch.Tensor
+    dead: torch.Tensor
+    ok: torch.Tensor | bool
+
+
+def _effective_actorder(quant_args: QuantizationArgs):
+    actorder = quant_args.actorder
+    if actorder == ActivationOrdering.GROUP and quant_args.strategy not in (QuantizationStrategy.GROUP,
+                                                                            QuantizationStrategy.TENSOR_GROUP):
+        logger.warning("ActivationOrdering.GROUP requires a grouped quantization strategy; "
+                       "falling back to actorder=None for this module.")
+        actorder = None
+    return actorder
+
+
+def _hinv_fallback_warning():
+    logger.warning("Failed to invert hessian due to numerical instability. Consider increasing "
+                   "GPTQModifier.dampening_frac, increasing the number of calibration samples, or "
+                   "shuffling the calibration dataset. Falling back to round-to-nearest for this module.")
+
+
+def prepare_hessian(hessian: torch.Tensor, quant_args: QuantizationArgs, num_samples: float = 1.0,
+                    percdamp: float = 0.01) -> PreparedHessian:
+    """Permutation, dead columns and Hinv for one upper-triangle Hessian
+    (``gptq_quantize.py:130-196``)."""
+    actorder = _effective_actorder(quant_args)
+    perm = invperm = None
+    if actorder:
+        perm = torch.argsort(torch.diagonal(hessian), descending=True, stable=True)
+        invperm = torch.argsort(perm)
+    hinv, dead, ok = ops.gptq_hinv(hessian, perm, float(num_samples), percdamp)
+    if not ok:
+        _hinv_fallback_warning()
+        hinv = torch.eye(hessian.shape[0], dtype=torch.float32, device=hessian.device)
+    return PreparedHessian(actorder, perm, invperm, hinv, dead, ok)
+
+
+def prepare_hessians_batched(hessians: torch.Tensor, quant_args: QuantizationArgs, num_samples=1.0,
+                             percdamp: float = 0.01) -> PreparedHessian:
+    """``prepare_hessian`` for a stack [B, d, d] (one launch per step)."""
+    actorder = _effective_actorder(quant_args)
+    B, d, _ = hessians.shape
+    ns = torch.as_tensor(num_samples, dtype=torch.float32, device=hessians.device).expand(B).contiguous()
+    perm = invperm = None
+    if actorder:
+        perm = torch.argsort(torch.diagonal(hessians, dim1=1, dim2=2), dim=1, descending=True, stable=True)
+        invperm = torch.argsort(perm, dim=1)
+    hinv, dead, ok = ops.gptq_hinv_batched(hessians, perm, ns, percdamp)
+    for b in torch.nonzero(~ok).flatten().tolist():
+        _hinv_fallback_warning()
+        hinv[b] = torch.eye(d, dtype=torch.float32, device=hessians.device)
+    return PreparedHessian(actorder, perm, invperm, hinv, dead, ok)
+
+
 def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: torch.Tensor, observer,
-                  blocksize: int = 128, percdamp: float = 0.01, num_samples: float = 1.0) -> GPTQResult:
+                  blocksize: int = 128, percdamp: float = 0.01, num_samples: float = 1.0,
+                  prepared: PreparedHessian | None = None) -> GPTQResult:
     """The GPTQ solve of ``gptq_quantize.py:100-296`` on the GPU.
 
     ``hessian`` is the accumulated upper-triangle Hessian; ``num_samples``
     is divided out inside the kernels (the reference divides before the call,
     ``modifiers/gptq/base.py:594``).  ``observer`` must already hold the
-    weight statistics (``observe``), as in the reference.
+    weight statistics (``observe``), as in the reference.  ``prepared`` (from
+    ``prepare_hessian`` on the same Hessian and quantization args) skips the
+    Cholesky chain for modules that share their input.
     """
     strategy = quant_args.strategy
-    actorder = quant_args.actorder
     if quant_args.type != QuantizationType.INT:
         raise NotImplementedError("GPTQ on the GPU supports integer quantization types")
     if strategy not in (QuantizationStrategy.TENSOR, QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP,
@@ -110,16 +176,8 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
         raise ValueError(f"Quantization strategy is not supported for GPTQ: {strategy}")
     W = weight
     rows, cols = W.shape
-    if actorder == ActivationOrdering.GROUP and strategy not in (QuantizationStrategy.GROUP,
-                                                                 QuantizationStrategy.TENSOR_GROUP):
-        logger.warning("ActivationOrdering.GROUP requires a grouped quantization strategy; "
-                       "falling back to actorder=None for this module.")
-        actorder = None
-
-    perm = invperm = None
-    if actorder:
-        perm = torch.argsort(torch.diagonal(hessian), descending=True, stable=True)
-        invperm = torch.argsort(perm)
+    prep = prepared if prepared is not None else prepare_hessian(hessian, quant_args, num_samples, percdamp)
+    actorder, perm, invperm = prep.actorder, prep.perm, prep.invperm
     if actorder == ActivationOrdering.GROUP:
         observer.delete_statistics(check_fused=False)
         observer(ops.gptq_load_weight(W, perm))   # permuted fp32 weight
@@ -134,13 +192,7 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
     qp = observer.get_qparams()
     scale, zero_point = qp["scale"], qp["zero_point"]
 
-    hinv, dead, ok = ops.gptq_hinv(hessian, perm, float(num_samples), percdamp)
-    if not ok:
-        logger.warning("Failed to invert hessian due to numerical instability. Consider increasing "
-                       "GPTQModifier.dampening_frac, increasing the number of calibration samples, or "
-                       "shuffling the calibration dataset. Falling back to round-to-nearest for this module.")
-        hinv = torch.eye(cols, dtype=torch.float32, device=W.device)
-
+    hinv, dead, ok = prep.hinv, prep.dead, prep.ok
     w_work = ops.gptq_load_weight(W, perm, dead)
     s, z = _qparams_for_sweep(scale, zero_point, strategy)
     qmin, qmax = quant_args.q_range()
@@ -155,7 +207,8 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
 
 def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, hessians: torch.Tensor,
                           num_samples=1.0, blocksize: int = 128, percdamp: float = 0.01,
-                          observer: str = "memoryless_minmax") -> list[GPTQResult]:
+                          observer: str = "memoryless_minmax",
+                          prepared: PreparedHessian | None = None) -> list[GPTQResult]:
     """``gptq_quantize`` for B same-shaped modules at once (the experts of an
     MoE layer): weights [B, rows, cols], hessians [B, cols, cols] (upper
     triangles), num_samples a number or [B].  Each module gets exactly the
@@ -163,12 +216,12 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
     step for the whole batch, one host synchronisation for the status flags
     and one for the losses).  The weight observer named ``observer`` is run
     here on the stacked weights (its statistics are per row for channel and
-    group strategies).
+    group strategies).  ``prepared`` (``prepare_hessians_batched`` on the same
+    stack and args) is shared by projections with the same input (gate, up).
     """
     from .observers import Observer
 
     strategy = quant_args.strategy
-    actorder = quant_args.actorder
     if quant_args.type != QuantizationType.INT:
         raise NotImplementedError("GPTQ on the GPU supports integer quantization types")
     if strategy not in (QuantizationStrategy.TENSOR, QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP,
@@ -177,17 +230,10 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
     B, rows, cols = weights.shape
     if hessians.shape != (B, cols, cols):
         raise ValueError(f"hessians must be [{B}, {cols}, {cols}], got {tuple(hessians.shape)}")
-    if actorder == ActivationOrdering.GROUP and strategy != QuantizationStrategy.GROUP:
-        logger.warning("ActivationOrdering.GROUP requires a grouped quantization strategy; "
-                       "falling back to actorder=None for this module.")
-        actorder = None
     dev = weights.device
-    ns = torch.as_tensor(num_samples, dtype=torch.float32, device=dev).expand(B).contiguous()
-
-    perm = invperm = None
-    if actorder:
-        perm = torch.argsort(torch.diagonal(hessians, dim1=1, dim2=2), dim=1, descending=True, stable=True)
-        invperm = torch.argsort(perm, dim=1)
+    prep = prepared if prepared is not None else prepare_hessians_batched(hessians, quant_args, num_samples,
+                                                                          percdamp)
+    actorder, perm, invperm = prep.actorder, prep.perm, prep.invperm
     src = ops.gptq_load_weight_batched(weights, perm) if actorder == ActivationOrdering.GROUP else weights
 
     def observe(x):
@@ -214,13 +260,7 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
         if actorder == ActivationOrdering.WEIGHT:
             g_idx = g_idx[perm]
 
-    hinv, dead, ok = ops.gptq_hinv_batched(hessians, perm, ns, percdamp)
-    for b in torch.nonzero(~ok).flatten().tolist():
-        logger.warning("Failed to invert hessian due to numerical instability. Consider increasing "
-                       "GPTQModifier.dampening_frac, increasing the number of calibration samples, or "
-                       "shuffling the calibration dataset. Falling back to round-to-nearest for this module.")
-        hinv[b] = torch.eye(cols, dtype=torch.float32, device=dev)
-
+    hinv, dead, ok = prep.hinv, prep.dead, prep.ok
     w_work = ops.gptq_load_weight_batched(weights, perm, dead)
     qmin, qmax = quant_args.q_range()
     bh = quant_args.block_structure[0] if strategy == QuantizationStrategy.BLOCK else 1

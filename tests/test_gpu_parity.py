@@ -317,6 +317,26 @@ def test_gptq_batched_equals_single(dev, case):
         assert abs(res[b].loss - single.loss) <= 1e-5 * abs(single.loss) + 1e-12
 
 
+def test_gptq_prepared_hessian_shared(dev):
+    """Modules with the same input (q/k/v, gate/up) may share the Cholesky
+    chain: a prepared Hessian gives exactly the results of separate solves."""
+    say("gptq shared prepared Hessian")
+    d = 384
+    qa = QuantizationArgs(type="int", num_bits=4, strategy="group", group_size=128, actorder="weight")
+    H = torch.triu(_spd_from_tokens(d, 1024, seed=41)).to(dev)
+    prep = gptq.prepare_hessian(H, qa, 2.0)
+    for seed, rows in ((50, 128), (51, 200)):
+        W = workloads.gptq_weight(rows, d, seed=seed).to(dev)
+        outs = []
+        for p in (prep, None):
+            obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+            obs(W)
+            outs.append(gptq.gptq_quantize(W, qa, H.clone(), obs, num_samples=2.0, prepared=p))
+        assert torch.equal(outs[0].codes, outs[1].codes)
+        assert torch.equal(outs[0].weight, outs[1].weight)
+        assert torch.equal(outs[0].g_idx, outs[1].g_idx)
+
+
 def _layer_err(W, Q, X):
     Xf = X.reshape(-1, X.shape[-1]).float()
     return (Xf @ (W.float() - Q.float()).t()).norm().item()
