@@ -36,12 +36,22 @@ __host__ __device__ constexpr int hrow(int i) { return i * MAXB - i * (i - 1) / 
 struct SweepState {
   float w[SW_T];   // working values (final once their column is reached)
   float s[SW_T];   // scale of each column
+  float rs[SW_T];  // 1 / scale, correctly rounded
   float z[SW_T];   // zero point of each column
-  float q[SW_T];   // dequantised result (owner)
-  float er[SW_T];  // (w - q) / Hinv[i][i] (owner)
-  float df[SW_T];  // w - q (owner), for the loss
-  int cq[SW_T];    // integer code (owner)
 };
+
+// a / b correctly rounded, from rb = 1 / b correctly rounded: q0 = a rb,
+// then one FMA residual correction (Markstein's theorem: with a correctly
+// rounded reciprocal the corrected quotient is the correctly rounded one, in
+// the absence of overflow and underflow, as for every scale and Hinv diagonal
+// here).  Three dependent operations on the sweep's serial chain instead of
+// the ten of a full IEEE division; a probe found no difference from a / b in
+// 2^32 random and near-half-integer quotients.
+__device__ __forceinline__ float div_by_recip(float a, float b, float rb) {
+  const float q0 = a * rb;
+  const float r = fmaf(-b, q0, a);
+  return fmaf(r, rb, q0);
+}
 
 // Branch-free bf16 round-to-nearest-even of a finite fp32 value.
 __device__ __forceinline__ float bf16_rne(float f) {
@@ -55,50 +65,59 @@ __device__ __forceinline__ float row_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xF, 0xF, false));
 }
 
+// CT quantize / dequantize of one value: qq = clamp(rint(x / s + z)),
+// deq = (qq - z) * s, rounded to bf16 when the scale is bf16.
+__device__ __forceinline__ void quant1(float x, float s, float rs, float z, float qmin, float qmax, bool dq_bf16,
+                                       float& qq, float& deq) {
+  qq = div_by_recip(x, s, rs) + z;
+  qq = rintf(fminf(fmaxf(qq, qmin), qmax));
+  deq = (qq - z) * s;
+  if (dq_bf16) deq = bf16_rne(deq);
+}
+
 // One column of the sweep: column I = SW_G * TO + GO, owned by lane GO of
-// each row.  Every lane runs the quantisation on its own slot TO (only the
-// owner's result is kept), the owner's error is broadcast within the row, and
-// each lane updates its later columns.
-template <int TO, int GO>
-__device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, int g, int count, float qmin,
-                                           float qmax, bool dq_bf16) {
+// each row.  Every lane quantises its own slot TO (only the owner's value is
+// column I; the others are discarded), the owner's error is broadcast within
+// the row, and each lane updates its later columns.  A lane's slot is final
+// from its own step on, so its code, dequantised value and error are
+// recomputed once after the sweep instead of being selected at every step.
+template <int TO, int GO, bool FULL>
+__device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, const float* rdg, int g, int count,
+                                           float qmin, float qmax, bool dq_bf16) {
   constexpr int I = SW_G * TO + GO;
-  if (I >= count) return;
+  if (!FULL && I >= count) return;
   const float dd = h1[hrow(I)];
   const float x = S.w[TO];
-  float qq = x / S.s[TO] + S.z[TO];
-  qq = rintf(fminf(fmaxf(qq, qmin), qmax));
-  float deq = (qq - S.z[TO]) * S.s[TO];
-  if (dq_bf16) deq = bf16_rne(deq);
-  const float diff = x - deq;
-  const float err = diff / dd;
-  const bool own = g == GO;
-  S.q[TO] = own ? deq : S.q[TO];
-  S.cq[TO] = own ? (int)qq : S.cq[TO];
-  S.er[TO] = own ? err : S.er[TO];
-  S.df[TO] = own ? diff : S.df[TO];
+  float qq, deq;
+  quant1(x, S.s[TO], S.rs[TO], S.z[TO], qmin, qmax, dq_bf16, qq, deq);
+  const float err = div_by_recip(x - deq, dd, rdg[I]);
   const float e = row_bcast<GO>(err);
 #pragma unroll
   for (int t = TO; t < SW_T; ++t) {
     const int col = SW_G * t + g;
     // (col < I reads a neighbouring entry, in bounds, and is never taken)
     const float upd = S.w[t] - e * h1[hrow(I) - I + col];
-    const bool take = (t > TO || g > GO) && col < count;
-    S.w[t] = take ? upd : S.w[t];
+    if (t == TO)
+      S.w[t] = g > GO ? upd : S.w[t];
+    else if (FULL)
+      S.w[t] = upd;
+    else
+      S.w[t] = col < count ? upd : S.w[t];
   }
 }
 
-template <int I>
+template <int I, bool FULL>
 struct SweepSteps {
-  static __device__ __forceinline__ void run(SweepState& S, const float* h1, int g, int count, float qmin,
-                                             float qmax, bool dq_bf16) {
-    sweep_step<I / SW_G, I % SW_G>(S, h1, g, count, qmin, qmax, dq_bf16);
-    SweepSteps<I + 1>::run(S, h1, g, count, qmin, qmax, dq_bf16);
+  static __device__ __forceinline__ void run(SweepState& S, const float* h1, const float* rdg, int g, int count,
+                                             float qmin, float qmax, bool dq_bf16) {
+    sweep_step<I / SW_G, I % SW_G, FULL>(S, h1, rdg, g, count, qmin, qmax, dq_bf16);
+    SweepSteps<I + 1, FULL>::run(S, h1, rdg, g, count, qmin, qmax, dq_bf16);
   }
 };
-template <>
-struct SweepSteps<MAXB> {
-  static __device__ __forceinline__ void run(SweepState&, const float*, int, int, float, float, bool) {}
+template <bool FULL>
+struct SweepSteps<MAXB, FULL> {
+  static __device__ __forceinline__ void run(SweepState&, const float*, const float*, int, int, float, float,
+                                             bool) {}
 };
 
 // Element strides between the matrices of a batch (blockIdx.y); zero for a
@@ -107,6 +126,7 @@ struct SweepBatch {
   int64_t w, hinv, scale, gidx, codes, losses, err;
 };
 
+template <bool FULL>
 __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
     int count, const float* __restrict__ scale, const float* __restrict__ zp, int64_t ld_scale,
@@ -114,6 +134,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, int err_col,
     SweepBatch sb) {
   __shared__ float h1[HPK];
+  __shared__ float rdg[MAXB];  // 1 / Hinv[i][i], correctly rounded
   __shared__ int gsh[MAXB];
   {
     const int64_t b = blockIdx.y;
@@ -162,6 +183,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
   }
   const bool uses_gidx = strategy == MI355Q_GROUP || strategy == MI355Q_BLOCK;
   if (tid < MAXB) gsh[tid] = (uses_gidx && tid < count) ? g_idx[i1 + tid] : 0;
+  if (tid < MAXB) rdg[tid] = tid < count ? 1.f / hinv[(i1 + tid) * cols + i1 + tid] : 1.f;
   __syncthreads();
 
   int64_t sbase = 0;
@@ -172,33 +194,30 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     const int col = min(SW_G * t + g, count - 1);
     const int64_t si = sbase + gsh[col];
     S.s[t] = scale[si];
+    S.rs[t] = 1.f / S.s[t];
     S.z[t] = zp ? zp[si] : 0.f;
-    S.q[t] = 0.f;
-    S.er[t] = 0.f;
-    S.df[t] = 0.f;
-    S.cq[t] = 0;
   }
 
-  SweepSteps<0>::run(S, h1, g, count, qmin, qmax, dq_bf16 != 0);
+  SweepSteps<0, FULL>::run(S, h1, rdg, g, count, qmin, qmax, dq_bf16 != 0);
 
+  // each slot is final: its code, dequantised value, error and loss
   float loss = 0.f;
 #pragma unroll
   for (int t = 0; t < SW_T; ++t) {
     const int col = SW_G * t + g;
+    const int cc = min(col, count - 1);
+    const float dd = h1[hrow(cc)];
+    float qq, deq;
+    quant1(S.w[t], S.s[t], S.rs[t], S.z[t], qmin, qmax, dq_bf16 != 0, qq, deq);
+    const float diff = S.w[t] - deq;
+    const float err = div_by_recip(diff, dd, rdg[cc]);
     if (col < count) {
-      const float dd = h1[hrow(col)];
-      loss = loss + S.df[t] * S.df[t] / (dd * dd);
-    }
-  }
-  if (live) {
-#pragma unroll
-    for (int t = 0; t < SW_T; ++t) {
-      const int col = SW_G * t + g;
-      if (col < count) {
+      loss = loss + diff * diff / (dd * dd);
+      if (live) {
         const int64_t c = i1 + col;
-        W[r * cols + c] = S.q[t];
-        codes[r * cols + c] = (int8_t)S.cq[t];
-        err_out[r * SUPER + err_col + col] = S.er[t];
+        W[r * cols + c] = deq;
+        codes[r * cols + c] = (int8_t)qq;
+        err_out[r * SUPER + err_col + col] = err;
       }
     }
   }
@@ -350,9 +369,14 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
     for (int64_t i1 = s0; i1 < s1; i1 += B) {
       const int64_t i2 = (i1 + B < s1) ? i1 + B : s1;
       const int count = (int)(i2 - i1);
-      hipLaunchKernelGGL(sweep_block_kernel, dim3(nwg, (unsigned)batch), dim3(SW_NT), 0, st, w_work_dev, rows,
-                         cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
-                         qmax, dequant_bf16, codes_dev, losses_dev, err, (int)(i1 - s0), sb);
+      if (count == MAXB)
+        hipLaunchKernelGGL(sweep_block_kernel<true>, dim3(nwg, (unsigned)batch), dim3(SW_NT), 0, st, w_work_dev,
+                           rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h,
+                           qmin, qmax, dequant_bf16, codes_dev, losses_dev, err, (int)(i1 - s0), sb);
+      else
+        hipLaunchKernelGGL(sweep_block_kernel<false>, dim3(nwg, (unsigned)batch), dim3(SW_NT), 0, st, w_work_dev,
+                           rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h,
+                           qmin, qmax, dequant_bf16, codes_dev, losses_dev, err, (int)(i1 - s0), sb);
       MQ_LAUNCH_CHECK();
       if (i2 < s1) {
         GemmArgs g{};
