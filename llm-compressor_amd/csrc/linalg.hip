@@ -344,6 +344,108 @@ __global__ __launch_bounds__(GNT, 1) void gemm_k128_kernel(GemmArgs g) {
   }
 }
 
+// Skinny K = 128 products (few 128 x 128 tiles: the Cholesky panel solves
+// and updates at d = 4096 have N = 128 and at most 31 row tiles) leave most
+// CUs idle on the big-tile kernel, and each of its tiles is a long MFMA
+// chain.  This variant computes one 64 x 64 tile per workgroup (each wave a
+// 32 x 32 quadrant, K = 128 as 64 MFMA steps on two accumulators), so the
+// same product spreads over four times as many CUs with a quarter of the
+// chain per wave.  Whole tiles only: M and N multiples of 64, 16-byte
+// aligned rows.
+constexpr int ST = 64;           // tile edge
+constexpr int SLB = ST + 32;     // LDS stride of [k][n] B tiles
+
+template <bool BT>
+__global__ __launch_bounds__(GNT, 2) void gemm_k128_small_kernel(GemmArgs g) {
+  __shared__ float la[ST * KLA];
+  __shared__ float lb[BT ? ST * KLA : KT * SLB];
+  {
+    const int64_t bz = blockIdx.z;
+    const int64_t b1 = g.inner > 0 ? bz % g.inner : bz, b2 = g.inner > 0 ? bz / g.inner : 0;
+    g.A += b1 * g.strideA + b2 * g.strideA2;
+    g.B += b1 * g.strideB + b2 * g.strideB2;
+    g.C += b1 * g.strideC + b2 * g.strideC2;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * ST, n0 = (int64_t)blockIdx.x * ST;
+  if (g.lower_only && n0 > m0) return;
+
+  // A (and B^T) tiles [row][k]: float4 v covers row 8 v + tid / 32, k 4 (tid % 32);
+  // B tiles [k][n]: float4 v covers k 16 v + tid / 16, n 4 (tid % 16)
+  auto at = [](const float* base, uint32_t off) {
+    return reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off);
+  };
+  f32x4_t ra[8], rb[8];
+  {
+    const uint32_t off_a = (uint32_t)((tid >> 5) * g.lda + 4 * (tid & 31)) * 4u;
+    const float* pa = g.A + m0 * g.lda;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) ra[v] = *reinterpret_cast<const f32x4_t*>(at(pa + 8 * v * g.lda, off_a));
+    if (BT) {
+      const uint32_t off_b = (uint32_t)((tid >> 5) * g.ldb + 4 * (tid & 31)) * 4u;
+      const float* pb = g.B + n0 * g.ldb;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) rb[v] = *reinterpret_cast<const f32x4_t*>(at(pb + 8 * v * g.ldb, off_b));
+    } else {
+      const uint32_t off_b = (uint32_t)((tid >> 4) * g.ldb + 4 * (tid & 15)) * 4u;
+      const float* pb = g.B + n0;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) rb[v] = *reinterpret_cast<const f32x4_t*>(at(pb + 16 * v * g.ldb, off_b));
+    }
+  }
+  // C quadrant of this wave, fetched while the tiles are staged
+  const uint32_t off_c = (uint32_t)((wm * 32 + 4 * (lane >> 5)) * g.ldc + wn * 32 + (lane & 31)) * 4u;
+  float* cbase = g.C + m0 * g.ldc + n0;
+  float cv[16];
+  if (g.beta != 0.f) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cv[r] = *at(cbase + (8 * (r >> 2) + (r & 3)) * g.ldc, off_c);
+  }
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const int row = 8 * v + (tid >> 5), k4 = 4 * (tid & 31);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) la[row * KLA + k4 + e] = ra[v][e];
+  }
+  if (BT) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int row = 8 * v + (tid >> 5), k4 = 4 * (tid & 31);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lb[row * KLA + k4 + e] = rb[v][e];
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      *reinterpret_cast<f32x4_t*>(lb + (16 * v + (tid >> 4)) * SLB + 4 * (tid & 15)) = rb[v];
+  }
+  __syncthreads();
+
+  f32x16_t acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
+  const float* pa = la + (wm * 32 + (lane & 31)) * KLA + (lane >> 5);
+  const float* pb = BT ? lb + (wn * 32 + (lane & 31)) * KLA + (lane >> 5) : lb + (lane >> 5) * SLB + wn * 32 + (lane & 31);
+#pragma unroll
+  for (int kk = 0; kk < KT / 2; kk += 2) {
+    const float a0 = pa[2 * kk], a1 = pa[2 * kk + 2];
+    const float b0 = BT ? pb[2 * kk] : pb[2 * kk * SLB];
+    const float b1 = BT ? pb[2 * kk + 2] : pb[(2 * kk + 2) * SLB];
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc1, 0, 0, 0);
+  }
+  const bool diag = g.lower_only && n0 == m0;  // only the diagonal tile straddles gm >= gn
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int tm = wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    const int tn = wn * 32 + (lane & 31);
+    const float prod = g.alpha * (acc0[r] + acc1[r]);
+    const float out = g.beta == 0.f ? prod : g.beta * cv[r] + prod;
+    if (!diag || tm >= tn) *const_cast<float*>(at(cbase + (8 * (r >> 2) + (r & 3)) * g.ldc, off_c)) = out;
+  }
+}
+
 // ---------------------------------------------------------------- Cholesky pieces
 constexpr int NB = 128;        // panel width
 constexpr int SB = 32;         // register-resident sub-block of the diagonal kernel
@@ -351,48 +453,59 @@ constexpr int PNT = 256;       // threads of the diagonal-block kernel (4 waves)
 constexpr int LP = NB + 1;     // LDS row stride
 constexpr int LT = 2 * SB + 1; // LDS row stride of the product scratch
 
-// Value of v in lane l (same l for every lane), through the LDS crossbar.
-__device__ __forceinline__ float bperm(float v, int l) {
-  return __int_as_float(__builtin_amdgcn_ds_bpermute(l << 2, __float_as_int(v)));
-}
-
-// acc += sum_k A[m][k] * op(B)[k][n] over a 32 x 32 tile, operands in LDS
-// (A row-major lda; B row-major [k][n] (ldb) or, if bt, [n][k]).  K even.
-__device__ __forceinline__ void lds_mfma_tile(f32x16_t& acc, const float* A, int lda, const float* B, int ldb,
-                                              bool bt, int K, int lane, float sign) {
-  // K is a literal at every call site: fully unrolled after inlining, so the
-  // LDS reads of later steps are issued ahead of the MFMA chain
+// 16 x 16 fp32 MFMA tile, operands in LDS: acc += sign * sum_{k in [kb, ke)}
+// A[m][k] op(B)[k][n], A row-major (lda), B row-major [k][n] (ldb) or, if bt,
+// [n][k].  kb and ke are multiples of 16.  acc[q] is row 4 (lane / 16) + q,
+// column lane % 16; the A operand of lane l is row l % 16, k offset l / 16.
+// The K ranges follow the triangles: with a lower-triangular operand only
+// the k that can be nonzero are visited.
+__device__ __forceinline__ void mfma16_tile(f32x4_t& acc, const float* A, int lda, const float* B, int ldb,
+                                            bool bt, int kb, int ke, int lane, float sign) {
+  const int r = lane & 15, kq = lane >> 4;
+#pragma unroll 2
+  for (int k0 = kb; k0 < ke; k0 += 16) {
+    float av[4], bv[4];
 #pragma unroll
-  for (int k2 = 0; k2 < K; k2 += 2) {
-    const int k = k2 + (lane >> 5);
-    const float av = sign * A[(lane & 31) * lda + k];
-    const float bv = bt ? B[(lane & 31) * ldb + k] : B[k * ldb + (lane & 31)];
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+    for (int s = 0; s < 4; ++s) {
+      const int k = k0 + 4 * s + kq;
+      av[s] = sign * A[r * lda + k];
+      bv[s] = bt ? B[r * ldb + k] : B[k * ldb + r];
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc, 0, 0, 0);
   }
 }
 
-__device__ __forceinline__ void tile_load(f32x16_t& acc, const float* C, int ldc, int lane) {
+__device__ __forceinline__ f32x4_t tile16_load(const float* C, int ldc, int lane) {
+  f32x4_t acc;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = C[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ldc + (lane & 31)];
+  for (int q = 0; q < 4; ++q) acc[q] = C[(4 * (lane >> 4) + q) * ldc + (lane & 15)];
+  return acc;
 }
-__device__ __forceinline__ void tile_store(const f32x16_t& acc, float* C, int ldc, int lane) {
+__device__ __forceinline__ void tile16_store(const f32x4_t& acc, float* C, int ldc, int lane) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) C[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ldc + (lane & 31)] = acc[r];
+  for (int q = 0; q < 4; ++q) C[(4 * (lane >> 4) + q) * ldc + (lane & 15)] = acc[q];
+}
+__device__ __forceinline__ f32x4_t zero4() {
+  f32x4_t z;
+  z[0] = z[1] = z[2] = z[3] = 0.f;
+  return z;
 }
 
-// Lower Cholesky of the NB x NB diagonal block at (k0, k0) of F (in place,
-// lower triangle) and its inverse into linv (NB x NB, zeros above the
-// diagonal).  nb <= NB is the block size; rows / columns beyond nb are padded
-// with the identity so the whole NB block factors uniformly.
+// Inverse X = L^-1 of the lower Cholesky factor of the NB x NB diagonal
+// block at (k0, k0) of F, into linv (NB x NB, zeros above the diagonal).
+// nb <= NB is the block size; rows / columns beyond nb are padded with the
+// identity so the whole NB block factors uniformly.  L itself is not
+// written back: the blocked Cholesky only consumes L^-1 (panel solves and
+// the triangular inverse) and the off-diagonal panels.
 //
-// The block is processed in 32-wide steps.  Wave 0 factors and inverts the
-// 32 x 32 diagonal sub-block in registers (lane i holds row i; values of
-// other rows arrive by readlane, so no workgroup barrier is needed inside
-// the step); then all four waves apply the sub-block inverse to the panel
-// below and update the trailing lower triangle with fp32 MFMA.  The block
-// inverse is assembled from the four sub-block inverses by two doubling
-// steps, inv([[A,0],[B,C]]) = [[A^-1,0],[-C^-1 B A^-1, C^-1]].
-__global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, int64_t k0, int nb,
+// The block is processed in 32-wide steps.  Wave 0 factors the 32 x 32
+// diagonal sub-block in registers and inverts it on the way; then all four
+// waves apply the sub-block inverse to the panel below and update the
+// trailing lower triangle with fp32 MFMA (16 x 16 tiles).  The block inverse
+// is assembled from the four sub-block inverses by two doubling steps,
+// inv([[A,0],[B,C]]) = [[A^-1,0],[-C^-1 B A^-1, C^-1]].
+__global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t ldf, int64_t k0, int nb,
                                                         float* linv, int32_t* status, int64_t wsf) {
   __shared__ float a[NB * LP];
   __shared__ float x[NB * LP];
@@ -403,9 +516,22 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
   linv += (int64_t)blockIdx.x * wsf;
   status += blockIdx.x;
 
-  // load: all 64 loads per thread issued before any is consumed; addresses
-  // are clamped into the block so no load needs a branch
-  {
+  // load the lower triangle (zeros above): thread tid covers columns
+  // 4 (tid % 32) .. + 3 of rows 8 v + tid / 32
+  if (nb == NB && (ldf & 3) == 0) {
+    const int i0 = tid >> 5, j = 4 * (tid & 31);
+    const float* src = F + (k0 + i0) * ldf + k0 + j;
+    f32x4_t lv[NB * NB / (4 * PNT)];
+#pragma unroll
+    for (int v = 0; v < NB * NB / (4 * PNT); ++v) lv[v] = *reinterpret_cast<const f32x4_t*>(src + 8 * v * ldf);
+#pragma unroll
+    for (int v = 0; v < NB * NB / (4 * PNT); ++v) {
+      const int i = 8 * v + i0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) a[i * LP + j + c] = (j + c <= i) ? lv[v][c] : 0.f;
+    }
+  } else {
+    // ragged block: addresses clamped into the block, identity padding
     float lv[NB * NB / PNT];
 #pragma unroll
     for (int v = 0; v < NB * NB / PNT; ++v) {
@@ -418,12 +544,13 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
       const int e = v * PNT + tid;
       const int i = e / NB, j = e % NB;
       a[i * LP + j] = (i < nb && j < nb && j <= i) ? lv[v] : ((i == j) ? 1.f : 0.f);
-      x[i * LP + j] = 0.f;
     }
   }
   __syncthreads();
 
-  bool bad = false;
+  // pivot checks, off the dependency chain: min over the pivots and a
+  // running sum of (piv - piv), NaN once any pivot is inf or NaN
+  float pmin = 1.f, pnan = 0.f;
 #pragma unroll 1
   for (int kb = 0; kb < NB / SB; ++kb) {
     const int o = kb * SB;
@@ -435,11 +562,16 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
       // X[j][:], i > j) advance together, and with col = A[:, j] before
       // scaling both take the same form:
       //   m = v[j] / piv;  v[k] -= m col[k] (k > j);  v[j] /= L[j][j]
-      // (a row's diagonal becomes L[j][j] itself).  Column j reaches every
-      // lane through one LDS write and eight broadcast reads (a wave's LDS
-      // operations complete in program order, so no barrier is needed).
-      // Entries above the diagonal are updated too and never stored, which
-      // keeps every update unpredicated.
+      // Column j reaches every lane through one LDS write and broadcast
+      // reads (a wave's LDS operations complete in program order, so no
+      // barrier is needed).  Entries above the diagonal are updated too and
+      // never used, which keeps every update unpredicated.
+      //
+      // The column loop is latency-bound (one wave, 128 sequential steps), so
+      // its dependency chain is kept short: rl = 1 / L[j][j] straight from the
+      // hardware reciprocal square root (within 1 ulp), and the column is
+      // scaled by the reciprocal, as LAPACK's potf2 scales it (dscal by
+      // 1 / ajj).
       const int li = lane & 31;
       const bool row_role = lane < SB;
       float* cb = t;  // column buffer: cb[0..31] = column j (t is idle during the factorisation)
@@ -451,112 +583,117 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(float* F, int64_t ldf, i
         // every lane stores (column-role lanes into a scratch slot): no
         // divergent branch around the LDS write that the reads could sink into
         cb[lane] = v[j];
+        // only col[j..SB-1] is used: read the aligned quads that cover it
         float col[SB];
 #pragma unroll
-        for (int q = 0; q < SB / 4; ++q) {
+        for (int q = j / 4; q < SB / 4; ++q) {
           const f32x4_t w = *reinterpret_cast<const f32x4_t*>(cb + 4 * q);
           col[4 * q] = w[0];
           col[4 * q + 1] = w[1];
           col[4 * q + 2] = w[2];
           col[4 * q + 3] = w[3];
         }
-        float piv = col[j];
-        if (!(piv > 0.f) || !isfinite(piv)) {
-          bad = true;
-          piv = 1.f;
-        }
-        const float ljj = sqrtf(piv);
-        const float m = v[j] * (1.f / piv);
+        const float piv = col[j];
+        pmin = fminf(pmin, piv);
+        pnan += piv - piv;
+        const float rl = __builtin_amdgcn_rsqf(piv);
+        const float sj = v[j] * rl;
+        const float m = sj * rl;
 #pragma unroll
         for (int k = j + 1; k < SB; ++k) v[k] = fmaf(-m, col[k], v[k]);
-        v[j] = (row_role && li == j) ? ljj : v[j] / ljj;
+        v[j] = sj;
       }
-      // store row li of L (row role) and column li of L^-1 (column role)
-      if (row_role) {
+      // column li of the sub-block inverse, zeros above the diagonal included
+      if (!row_role) {
 #pragma unroll
-        for (int c = 0; c < SB; ++c)
-          if (c <= li) a[(o + li) * LP + o + c] = v[c];
-      } else {
-#pragma unroll
-        for (int i = 0; i < SB; ++i)
-          if (i >= li) x[(o + i) * LP + o + li] = v[i];
+        for (int i = 0; i < SB; ++i) x[(o + i) * LP + o + li] = v[i];
       }
     }
     __syncthreads();
-    // panel below the sub-block: P = A_panel * Xd^T (in place, one 32-row tile per wave)
-    const int ntile = (NB - o - SB) / SB;
-    if (wave < ntile) {
-      f32x16_t acc;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-      float* ap = a + (o + SB + SB * wave) * LP + o;
-      lds_mfma_tile(acc, ap, LP, x + o * LP + o, LP, true, SB, lane, 1.f);
-      tile_store(acc, ap, LP, lane);
+    // panel below the sub-block: P = A_panel Xd^T in place, 16 rows per unit
+    // (both column tiles of a unit in one wave, read before written);
+    // Xd^T is upper triangular, so column tile c needs k < 16 (c + 1)
+    const int R = NB - o - SB;
+    for (int u = wave; u < R / 16; u += PNT / 64) {
+      float* ap = a + (o + SB + 16 * u) * LP + o;
+      f32x4_t acc0 = zero4(), acc1 = zero4();
+      mfma16_tile(acc0, ap, LP, x + o * LP + o, LP, true, 0, 16, lane, 1.f);
+      mfma16_tile(acc1, ap, LP, x + (o + 16) * LP + o, LP, true, 0, 32, lane, 1.f);
+      tile16_store(acc0, ap, LP, lane);
+      tile16_store(acc1, ap + 16, LP, lane);
     }
     __syncthreads();
     // trailing lower tiles: A[ti][tj] -= P_ti P_tj^T for tj <= ti
-    const int ntt = ntile * (ntile + 1) / 2;
+    const int nt = R / 16, ntt = nt * (nt + 1) / 2, rb = o + SB;
     for (int tt = wave; tt < ntt; tt += PNT / 64) {
       int ti = 0, rem = tt;
       while (rem > ti) { rem -= ti + 1; ++ti; }
       const int tj = rem;
-      float* cp = a + (o + SB + SB * ti) * LP + (o + SB + SB * tj);
-      f32x16_t acc;
-      tile_load(acc, cp, LP, lane);
-      lds_mfma_tile(acc, a + (o + SB + SB * ti) * LP + o, LP, a + (o + SB + SB * tj) * LP + o, LP, true, SB,
-                    lane, -1.f);
-      tile_store(acc, cp, LP, lane);
+      float* cp = a + (rb + 16 * ti) * LP + rb + 16 * tj;
+      f32x4_t acc = tile16_load(cp, LP, lane);
+      mfma16_tile(acc, a + (rb + 16 * ti) * LP + o, LP, a + (rb + 16 * tj) * LP + o, LP, true, 0, SB, lane, -1.f);
+      tile16_store(acc, cp, LP, lane);
     }
     __syncthreads();
   }
-  if (wave == 0 && lane == 0 && bad && status) *status = MI355Q_NOT_POSITIVE_DEFINITE;
+  if (wave == 0 && lane == 0 && status && !(pmin > 0.f && pnan == 0.f)) *status = MI355Q_NOT_POSITIVE_DEFINITE;
 
   // block inverse from the four 32 x 32 inverses
-  // level 1: pairs (0,1) and (2,3)
-  if (wave < 2) {
-    const int a0 = 2 * SB * wave, c0 = a0 + SB;
-    f32x16_t acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    lds_mfma_tile(acc, a + c0 * LP + a0, LP, x + a0 * LP + a0, LP, false, SB, lane, 1.f);
-    tile_store(acc, t + SB * wave * LT, LT, lane);
-  }
-  __syncthreads();
-  if (wave < 2) {
-    const int a0 = 2 * SB * wave, c0 = a0 + SB;
-    f32x16_t acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    lds_mfma_tile(acc, x + c0 * LP + c0, LP, t + SB * wave * LT, LT, false, SB, lane, -1.f);
-    tile_store(acc, x + c0 * LP + a0, LP, lane);
-  }
-  __syncthreads();
-  // level 2: T = L[64:128, 0:64] X[0:64, 0:64]; X[64:128, 0:64] = -X[64:128, 64:128] T
+  // level 1, pairs p = 0, 1 (a0 = 64 p, c0 = a0 + 32): T_p = L[c0][a0] X[a0][a0]
   {
-    const int ti = wave >> 1, tj = wave & 1;
-    f32x16_t acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    lds_mfma_tile(acc, a + (2 * SB + SB * ti) * LP, LP, x + SB * tj, LP, false, 2 * SB, lane, 1.f);
-    tile_store(acc, t + SB * ti * LT + SB * tj, LT, lane);
+    const int p = wave >> 1, tr = wave & 1, a0 = 2 * SB * p, c0 = a0 + SB;
+    const float* A = a + (c0 + 16 * tr) * LP + a0;
+    f32x4_t acc0 = zero4(), acc1 = zero4();
+    mfma16_tile(acc0, A, LP, x + a0 * LP + a0, LP, false, 0, SB, lane, 1.f);
+    mfma16_tile(acc1, A, LP, x + a0 * LP + a0 + 16, LP, false, 16, SB, lane, 1.f);
+    tile16_store(acc0, t + (SB * p + 16 * tr) * LT, LT, lane);
+    tile16_store(acc1, t + (SB * p + 16 * tr) * LT + 16, LT, lane);
   }
   __syncthreads();
+  // X[c0][a0] = -X[c0][c0] T_p
   {
-    const int ti = wave >> 1, tj = wave & 1;
-    f32x16_t acc;
+    const int p = wave >> 1, tc = wave & 1, a0 = 2 * SB * p, c0 = a0 + SB;
+    f32x4_t acc0 = zero4(), acc1 = zero4();
+    mfma16_tile(acc0, x + c0 * LP + c0, LP, t + SB * p * LT + 16 * tc, LT, false, 0, 16, lane, -1.f);
+    mfma16_tile(acc1, x + (c0 + 16) * LP + c0, LP, t + SB * p * LT + 16 * tc, LT, false, 0, SB, lane, -1.f);
+    tile16_store(acc0, x + c0 * LP + a0 + 16 * tc, LP, lane);
+    tile16_store(acc1, x + (c0 + 16) * LP + a0 + 16 * tc, LP, lane);
+  }
+  __syncthreads();
+  // level 2: T = L[64:128][0:64] X[0:64][0:64], one 16-row strip per wave
+  {
+    const float* A = a + (2 * SB + 16 * wave) * LP;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    lds_mfma_tile(acc, x + (2 * SB + SB * ti) * LP + 2 * SB, LP, t + SB * tj, LT, false, 2 * SB, lane, -1.f);
-    tile_store(acc, x + (2 * SB + SB * ti) * LP + SB * tj, LP, lane);
+    for (int tc = 0; tc < 4; ++tc) {
+      f32x4_t acc = zero4();
+      mfma16_tile(acc, A, LP, x + 16 * tc, LP, false, 16 * tc, 2 * SB, lane, 1.f);
+      tile16_store(acc, t + 16 * wave * LT + 16 * tc, LT, lane);
+    }
+  }
+  __syncthreads();
+  // X[64:128][0:64] = -X[64:128][64:128] T, one 16-column strip per wave
+  {
+#pragma unroll
+    for (int tr = 0; tr < 4; ++tr) {
+      f32x4_t acc = zero4();
+      mfma16_tile(acc, x + (2 * SB + 16 * tr) * LP + 2 * SB, LP, t + 16 * wave, LT, false, 0, 16 * (tr + 1), lane,
+                  -1.f);
+      tile16_store(acc, x + (2 * SB + 16 * tr) * LP + 16 * wave, LP, lane);
+    }
   }
   __syncthreads();
 
-#pragma unroll 16
-  for (int v = 0; v < NB * NB / PNT; ++v) {
-    const int e = v * PNT + tid;
-    const int i = e / NB, j = e % NB;
-    if (i < nb && j <= i) F[(k0 + i) * ldf + (k0 + j)] = a[i * LP + j];
-    linv[e] = (j <= i) ? x[i * LP + j] : 0.f;
+  // store L^-1, zeros above the diagonal: rows 8 v + tid / 32, columns 4 (tid % 32) .. + 3
+  {
+    const int i0 = tid >> 5, j = 4 * (tid & 31);
+#pragma unroll
+    for (int v = 0; v < NB * NB / (4 * PNT); ++v) {
+      const int i = 8 * v + i0;
+      f32x4_t o4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o4[c] = (j + c <= i) ? x[i * LP + j + c] : 0.f;
+      *reinterpret_cast<f32x4_t*>(linv + i * NB + j) = o4;
+    }
   }
 }
 
@@ -768,6 +905,22 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   const bool k128 = !g.a_lower && !g.b_lower && g.K == KT && g.M % KT == 0 && g.N % KT == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                     aligned16(g.A) && aligned16(g.B) && (batch == 1 || strides16) &&
                     (g.lda * 7 + KT) < (1 << 29) && (g.ldb * 7 + KT) < (1 << 29) && (g.ldc * 127 + KT) < (1 << 29);
+  // the same products in 64 x 64 tiles when 128 x 128 tiles would leave
+  // most CUs idle (fewer than two tiles per CU)
+  const bool k128s = !g.a_lower && !g.b_lower && g.K == KT && g.M % ST == 0 && g.N % ST == 0 && g.lda % 4 == 0 &&
+                     g.ldb % 4 == 0 && aligned16(g.A) && aligned16(g.B) && (batch == 1 || strides16) &&
+                     (g.lda * 63 + KT) < (1 << 29) && (g.ldb * 127 + KT) < (1 << 29) && (g.ldc * 63 + ST) < (1 << 29) &&
+                     g.M / ST <= 65535 && g.N / ST <= 65535;
+  const int64_t big_tiles = (g.M / KT) * (g.N / KT) * batch / (g.lower_only ? 2 : 1);
+  if (k128s && (!k128 || big_tiles < 512)) {
+    dim3 grid((unsigned)(g.N / ST), (unsigned)(g.M / ST), (unsigned)batch);
+    if (b_trans)
+      hipLaunchKernelGGL(gemm_k128_small_kernel<true>, grid, dim3(GNT), 0, stream, g);
+    else
+      hipLaunchKernelGGL(gemm_k128_small_kernel<false>, grid, dim3(GNT), 0, stream, g);
+    MQ_LAUNCH_CHECK();
+    return MI355Q_OK;
+  }
   if (k128) {
     // one workgroup per CU: spread the column tiles so ~256 workgroups run
     const int64_t mt = g.M / KT, ntl = g.N / KT;
