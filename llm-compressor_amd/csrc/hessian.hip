@@ -64,6 +64,9 @@ struct SyrkParams {
   const int32_t* rows;     // optional token -> row indirection
   Matrix single;           // single-matrix mode
   int S;
+  // dense tail: tiles t >= tail_start run as tail_f parts per split (see
+  // plan_dense); tail_start = number of tiles when there is no tail
+  int tail_start, tail_f;
   const Item* items;       // grouped mode (items != nullptr)
   const Matrix* mats;
   float* ws;               // partial tiles
@@ -356,20 +359,42 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave >> 1, wn = wave & 1;
 
+  // work item: tile t, token split s (and, for tail tiles, part `part` of
+  // tail_f equal pieces of that split), partial slot
   const int S = p.S;
-  const int s = blockIdx.x % S;
-  const int t = blockIdx.x / S;
+  const int64_t nfull = (int64_t)p.tail_start * S;
+  int t, s, part = 0, nparts = 1;
+  int64_t slot;
+  if ((int64_t)blockIdx.x < nfull) {
+    s = blockIdx.x % S;
+    t = blockIdx.x / S;
+    slot = (S > 1) ? (int64_t)t * S + s : -1;
+  } else {
+    const int b = (int)(blockIdx.x - nfull);
+    s = b % S;
+    const int j = b / S;
+    t = p.tail_start + j / p.tail_f;
+    part = j % p.tail_f;
+    nparts = p.tail_f;
+    slot = nfull + ((int64_t)(t - p.tail_start) * S + s) * p.tail_f + part;
+  }
   const Matrix mat = p.single;
-  const int64_t slot = (S > 1) ? (int64_t)t * S + s : -1;
   int ti, tj;
   tile_coords(t, p.nt, ti, tj);
 
   const int64_t n = mat.row_count;
   const int64_t nst_total = (n + SK - 1) / SK;
   const int64_t st_per = (nst_total + S - 1) / S;
-  const int64_t st_begin = (int64_t)s * st_per;
+  int64_t st_begin = (int64_t)s * st_per;
   int64_t st_end = st_begin + st_per;
   if (st_end > nst_total) st_end = nst_total;
+  if (nparts > 1 && st_end > st_begin) {
+    const int64_t per = (st_end - st_begin + nparts - 1) / nparts;
+    const int64_t b2 = st_begin + part * per;
+    const int64_t e2 = b2 + per < st_end ? b2 + per : st_end;
+    st_begin = b2;
+    st_end = e2;
+  }
   const int64_t nst = st_end > st_begin ? st_end - st_begin : 0;
 
   // DMA roles: wave w copies token rows 8 w .. 8 w + 7 of each operand, two
@@ -527,8 +552,9 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
 // (blockIdx.y = bm), so a TM = 256 tile is finished by four workgroups.
 template <int TM>
 __global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict__ ws, const ReduceItem* items,
-                                                         int single_S, Matrix single, const Matrix* mats,
-                                                         int64_t d, int64_t ldh, int nt, float alpha) {
+                                                         int single_S, int tail_start, int64_t tail_base,
+                                                         Matrix single, const Matrix* mats, int64_t d,
+                                                         int64_t ldh, int nt, float alpha) {
   using C = Cfg<TM>;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -542,7 +568,8 @@ __global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict
     const ReduceItem it = items[blockIdx.x];
     t = it.t; S = it.S; slot0 = it.slot0; mat = mats[it.e];
   } else {
-    t = blockIdx.x; S = single_S; slot0 = (int64_t)t * S; mat = single;
+    t = blockIdx.x; S = single_S; mat = single;
+    slot0 = t < tail_start ? (int64_t)t * S : tail_base + (int64_t)(t - tail_start) * S;
   }
   int ti, tj;
   tile_coords(t, nt, ti, tj);
@@ -591,6 +618,29 @@ __global__ void symmetrize_kernel(float* h, int64_t d, int64_t ldh) {
   }
 }
 
+// Dense tail: sums the tail_f part slots of each (tail tile, split) group,
+// in part order, into one slot (group g: slots src0 + g f .. + f - 1 ->
+// slot dst0 + g), so the reduction sees S slots per tile for every tile.
+// blockIdx.y picks a quarter of the slot.
+__global__ __launch_bounds__(NT) void syrk_tail_sum_kernel(float* ws, int64_t slot_floats, int64_t src0,
+                                                           int64_t dst0, int f) {
+  const int64_t g = blockIdx.x;
+  const int64_t q = slot_floats / 4;
+  const float* src = ws + (src0 + g * f) * slot_floats + blockIdx.y * q;
+  float* dst = ws + (dst0 + g) * slot_floats + blockIdx.y * q;
+  for (int64_t i = 4 * (int64_t)threadIdx.x; i < q; i += 4 * NT) {
+    f32x4_t acc = *reinterpret_cast<const f32x4_t*>(src + i);
+    for (int part = 1; part < f; ++part) {
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(src + part * slot_floats + i);
+      acc[0] += v[0];
+      acc[1] += v[1];
+      acc[2] += v[2];
+      acc[3] += v[3];
+    }
+    *reinterpret_cast<f32x4_t*>(dst + i) = acc;
+  }
+}
+
 int choose_splits(int64_t n) {
   const int64_t s = n / 2048;
   if (s >= 8) return 8;
@@ -607,6 +657,40 @@ inline int tiles_per_edge(int64_t d) {
 inline int upper_tiles(int nt) { return nt * (nt + 1) / 2; }
 inline size_t tile_floats(int64_t d) { return (size_t)tile_edge(d) * tile_edge(d); }
 
+// Dense work plan.  With S = 8 token splits, split s runs on XCD s (work
+// items are dispatched round-robin over the 8 XCDs), so each XCD takes T
+// items of equal length on its 32 CUs (one workgroup per CU): T / 32 full
+// rounds and a last round with only T % 32 items.  The last rem = T % 32
+// tiles are therefore cut into f = min(4, 32 / rem) parts per split, so the
+// last round takes 1 / f of a full one (d = 4096: T = 136, rem = 8, f = 4,
+// 4.25 rounds instead of 5).  Their f part slots per split are summed into
+// one slot per split before the reduction.
+constexpr int kCusPerXcd = 32;
+struct DensePlan {
+  int S = 1, T = 0, tail_start = 0, tail_f = 1;
+  int64_t grid = 0, slots = 0;
+  int64_t tail_src0 = 0, tail_dst0 = 0, tail_groups = 0;
+};
+DensePlan plan_dense(int64_t n, int64_t d) {
+  DensePlan pl;
+  pl.S = choose_splits(n);
+  pl.T = upper_tiles(tiles_per_edge(d));
+  pl.tail_start = pl.T;
+  const int rem = pl.T % kCusPerXcd;
+  if (pl.S == 8 && tile_edge(d) == 256 && rem > 0 && rem <= kCusPerXcd / 2) {
+    pl.tail_f = kCusPerXcd / rem < 4 ? kCusPerXcd / rem : 4;
+    pl.tail_start = pl.T - rem;
+  }
+  const int64_t nfull = (int64_t)pl.tail_start * pl.S;
+  const int64_t ntail = (int64_t)(pl.T - pl.tail_start) * pl.S;
+  pl.grid = nfull + ntail * pl.tail_f;
+  pl.tail_src0 = nfull;
+  pl.tail_dst0 = nfull + ntail * pl.tail_f;
+  pl.tail_groups = ntail;
+  pl.slots = pl.S > 1 ? (pl.tail_f > 1 ? pl.tail_dst0 + ntail : (int64_t)pl.T * pl.S) : 0;
+  return pl;
+}
+
 void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
   const bool g = p.rows != nullptr;
   if (tile_edge(d) == 256) {
@@ -618,14 +702,15 @@ void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) 
   }
 }
 
-void launch_reduce(const float* ws, const ReduceItem* items, int S, const Matrix& single, const Matrix* mats,
-                   int64_t d, int64_t ldh, int nt, float alpha, unsigned ntiles, hipStream_t st) {
+void launch_reduce(const float* ws, const ReduceItem* items, int S, int tail_start, int64_t tail_base,
+                   const Matrix& single, const Matrix* mats, int64_t d, int64_t ldh, int nt, float alpha,
+                   unsigned ntiles, hipStream_t st) {
   if (tile_edge(d) == 256)
-    hipLaunchKernelGGL(syrk_reduce_kernel<256>, dim3(ntiles, Cfg<256>::NB), dim3(NT), 0, st, ws, items, S, single,
-                       mats, d, ldh, nt, alpha);
+    hipLaunchKernelGGL(syrk_reduce_kernel<256>, dim3(ntiles, Cfg<256>::NB), dim3(NT), 0, st, ws, items, S,
+                       tail_start, tail_base, single, mats, d, ldh, nt, alpha);
   else
-    hipLaunchKernelGGL(syrk_reduce_kernel<128>, dim3(ntiles, Cfg<128>::NB), dim3(NT), 0, st, ws, items, S, single,
-                       mats, d, ldh, nt, alpha);
+    hipLaunchKernelGGL(syrk_reduce_kernel<128>, dim3(ntiles, Cfg<128>::NB), dim3(NT), 0, st, ws, items, S,
+                       tail_start, tail_base, single, mats, d, ldh, nt, alpha);
 }
 
 }  // namespace
@@ -636,9 +721,7 @@ using namespace mi355q;
 
 extern "C" size_t mi355q_hessian_workspace_size(int64_t n_tokens, int64_t d) {
   if (n_tokens <= 0 || d <= 0) return 0;
-  const int S = choose_splits(n_tokens);
-  if (S == 1) return 0;
-  return (size_t)upper_tiles(tiles_per_edge(d)) * S * tile_floats(d) * sizeof(float);
+  return (size_t)plan_dense(n_tokens, d).slots * tile_floats(d) * sizeof(float);
 }
 
 extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
@@ -653,8 +736,8 @@ extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int
   if (n_tokens == 0) return MI355Q_OK;
   MQ_CHECK_ARG(x_dev != nullptr && aligned16(x_dev), "hessian: x must be non-null and 16-byte aligned");
   const int nt = tiles_per_edge(d);
-  const int T = upper_tiles(nt);
-  const int S = choose_splits(n_tokens);
+  const DensePlan pl = plan_dense(n_tokens, d);
+  const int T = pl.T, S = pl.S;
   const size_t need = mi355q_hessian_workspace_size(n_tokens, d);
   MQ_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace_dev != nullptr),
                "hessian: workspace too small (%zu < %zu)", workspace_bytes, need);
@@ -670,13 +753,21 @@ extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int
   p.rows = nullptr;
   p.single = Matrix{0, n_tokens, h_dev};
   p.S = S;
+  p.tail_start = pl.tail_start;
+  p.tail_f = pl.tail_f;
   p.items = nullptr;
   p.mats = nullptr;
   p.ws = static_cast<float*>(workspace_dev);
-  launch_syrk(p, d, (unsigned)T * S, st);
+  launch_syrk(p, d, (unsigned)pl.grid, st);
   MQ_LAUNCH_CHECK();
   if (S > 1) {
-    launch_reduce(p.ws, nullptr, S, p.single, nullptr, d, ldh, nt, alpha, (unsigned)T, st);
+    if (pl.tail_f > 1) {
+      hipLaunchKernelGGL(syrk_tail_sum_kernel, dim3((unsigned)pl.tail_groups, 4), dim3(NT), 0, st, p.ws,
+                         (int64_t)tile_floats(d), pl.tail_src0, pl.tail_dst0, pl.tail_f);
+      MQ_LAUNCH_CHECK();
+    }
+    launch_reduce(p.ws, nullptr, S, pl.tail_start, pl.tail_dst0, p.single, nullptr, d, ldh, nt, alpha,
+                  (unsigned)T, st);
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;
@@ -768,13 +859,15 @@ extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, 
   p.alpha = alpha;
   p.rows = rows_dev;
   p.S = 1;
+  p.tail_start = 0;
+  p.tail_f = 1;
   p.items = reinterpret_cast<const Item*>(ws + g.off_items);
   p.mats = reinterpret_cast<const Matrix*>(ws + g.off_mats);
   p.ws = reinterpret_cast<float*>(ws);
   launch_syrk(p, d, (unsigned)g.items.size(), st);
   MQ_LAUNCH_CHECK();
   if (!g.reduces.empty()) {
-    launch_reduce(p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, Matrix{}, p.mats, d, d,
+    launch_reduce(p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, 0, 0, Matrix{}, p.mats, d, d,
                   p.nt, alpha, (unsigned)g.reduces.size(), st);
     MQ_LAUNCH_CHECK();
   }

@@ -33,7 +33,10 @@ def rel_fro(a, b):
 
 
 # ---------------------------------------------------------------- Hessian
-@pytest.mark.parametrize("n,d", [(300, 64), (2048, 256), (5000, 384), (16384, 512), (4100, 1000)])
+# (16384, 512): every tile split into parts; (16500, 2304) and (16384, 4096):
+# full tiles plus split tail tiles
+@pytest.mark.parametrize("n,d", [(300, 64), (2048, 256), (5000, 384), (16384, 512), (4100, 1000), (16500, 2304),
+                                 (16384, 4096)])
 def test_hessian_syrk_parity(dev, n, d):
     say(f"hessian syrk n={n} d={d}")
     x = workloads.heavy_tailed_activations((n, d), seed=n + d)

@@ -30,8 +30,9 @@ def test_version_and_workspace_queries():
     lib = _lib.load_library()
     assert lib.mi355q_version() == 1
     assert lib.mi355q_hessian_workspace_size(2048, 4096) == 0            # single split, direct update
-    # 256 x 256 tiles for d >= 512: 136 upper tiles x 8 token splits
-    assert lib.mi355q_hessian_workspace_size(131072, 4096) == 8 * 136 * 256 * 256 * 4
+    # d = 4096: 136 tiles, 8 splits; the last 8 tiles run as 4 parts per split
+    # (128 * 8 + 8 * 8 * 4 part slots + 8 * 8 summed slots)
+    assert lib.mi355q_hessian_workspace_size(131072, 4096) == (128 * 8 + 8 * 8 * 4 + 8 * 8) * 256 * 256 * 4
     assert lib.mi355q_hessian_workspace_size(131072, 384) == 8 * 6 * 128 * 128 * 4
     assert lib.mi355q_gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 1024 * 4   # errors of one 1024-column super-block
     assert lib.mi355q_gptq_hinv_workspace_size(4096) >= 2 * 4096 * 4096 * 4
