@@ -415,32 +415,49 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   // The DMA is issued from inline asm so that the compiler does not treat
   // every later LDS read as dependent on it (it cannot tell the ring slots
   // apart and would wait for all DMA in flight); completion is tracked
-  // explicitly with vmcnt before each stage's barrier and after the loop.
-  auto dma = [&](const void* gaddr, char* lds) __attribute__((always_inline)) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds));
+  // explicitly with vmcnt before each barrier and after the loop.  Whole
+  // stages use the scalar-base form (stage base in SGPRs + the lane's 32-bit
+  // offset); partial stages and edge tiles redirect lanes past n or d to a
+  // zero chunk with per-lane 64-bit addresses.  M0 (the LDS destination of
+  // the wave's 1 KB) is formed in scalar registers.
+  auto lds_u32 = [](const char* ptr) { return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)ptr); };
+  const uint32_t wave_lds = (uint32_t)wave * 4096u;
+  const uint32_t sa[4] = {lds_u32(a0) + wave_lds, lds_u32(a1) + wave_lds, lds_u32(a2) + wave_lds,
+                          lds_u32(a3) + wave_lds};
+  const uint32_t sb[4] = {lds_u32(b0) + wave_lds, lds_u32(b1) + wave_lds, lds_u32(b2) + wave_lds,
+                          lds_u32(b3) + wave_lds};
+  auto dma_s = [&](uint32_t off, const char* base, uint32_t m0) __attribute__((always_inline)) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
+                 : "memory", "m0");
+  };
+  auto dma_v = [&](const void* gaddr, uint32_t m0) __attribute__((always_inline)) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(m0) : "memory", "m0");
   };
-  auto issue = [&](int64_t stage, char* la, char* lb) __attribute__((always_inline)) {
-    const int64_t tok0 = (stage < nst ? stage : nst - 1) + st_begin;
-    const int64_t t0 = tok0 * SK;
-    const bool slow = edge || t0 + SK > n;
-    const char* xa = reinterpret_cast<const char*>(p.x + (mat.row_begin + t0) * p.ldx + fa0);
-    const char* xb = reinterpret_cast<const char*>(p.x + (mat.row_begin + t0) * p.ldx + fb0);
-    if (!slow) {
+  const char* xbase = reinterpret_cast<const char*>(p.x + (mat.row_begin + st_begin * SK) * p.ldx);
+  const int64_t sbytes = (int64_t)SK * p.ldx * 2;  // bytes per stage
+  // stages [0, nwhole) hold SK tokens
+  const int64_t nwhole = (n - st_begin * SK) / SK;
+  auto issue = [&](int64_t stage, int slot) __attribute__((always_inline)) {
+    const int64_t sc = stage < nst ? stage : nst - 1;
+    const char* xs = xbase + sc * sbytes;
+    const char* xa = xs + fa0 * 2;
+    const char* xb = xs + fb0 * 2;
+    if (!edge && sc < nwhole) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        dma(xa + doff[j], la + (4 * wave + j) * 1024);
-        dma(xb + doff[j], lb + (4 * wave + j) * 1024);
+        dma_s(doff[j], xa, sa[slot] + 1024u * j);
+        dma_s(doff[j], xb, sb[slot] + 1024u * j);
       }
     } else {
       // partial stage or edge tile: rows past n and chunks past d read zeros
+      const int64_t t0 = (st_begin + sc) * SK;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bool rok = t0 + drow[j] < n;
         const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
         const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
-        dma(aok ? (const void*)(xa + doff[j]) : (const void*)kZeroChunk, la + (4 * wave + j) * 1024);
-        dma(bok ? (const void*)(xb + doff[j]) : (const void*)kZeroChunk, lb + (4 * wave + j) * 1024);
+        dma_v(aok ? (const void*)(xa + doff[j]) : (const void*)kZeroChunk, sa[slot] + 1024u * j);
+        dma_v(bok ? (const void*)(xb + doff[j]) : (const void*)kZeroChunk, sb[slot] + 1024u * j);
       }
     }
   };
@@ -466,53 +483,64 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
 
-  // both 16-token steps of a stage: the reads of step 1 are interleaved with
-  // the MFMAs of step 0 (explicit scheduling groups; operands of the two
-  // steps live in separate registers)
-  auto compute = [&](const char* la, const char* lb) __attribute__((always_inline)) {
-    bf16x8_t fa[2][C::NB], fbv[2][C::NB];
+  // Software pipeline over half-stages (16-token steps): the MFMAs of one
+  // step run while the operands of the next step are read, including across
+  // the stage boundary, so the barrier that publishes stage st + 1 sits in
+  // the middle of stage st (between its two steps) and the MFMA pipe does not
+  // drain at stage boundaries.  F0 / F1 hold the operands of step 0 / step 1.
+  bf16x8_t fa0r[C::NB], fb0r[C::NB], fa1r[C::NB], fb1r[C::NB];
+  auto read_op = [&](const char* la, const char* lb, int kk, int i, bf16x8_t* fa, bf16x8_t* fb)
+      __attribute__((always_inline)) {
+    // operand i of a step: A fragments 0..NB-1, then B fragments
+    if (i < C::NB)
+      fa[i] = tr_pair(la, ra[i] + kk * 16 * SROW, ra[i] + (kk * 16 + 4) * SROW);
+    else
+      fb[i - C::NB] = tr_pair(lb, rb[i - C::NB] + kk * 16 * SROW, rb[i - C::NB] + (kk * 16 + 4) * SROW);
+  };
+  // MFMAs of one step (operands fa, fb) interleaved with the 2 NB fragment
+  // reads of the next step: two tr reads per MFMA for the first NB MFMAs
+  auto half = [&](const bf16x8_t* fa, const bf16x8_t* fb, const char* la, const char* lb, int kk, bf16x8_t* na,
+                  bf16x8_t* nb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int i = 0; i < 2 * C::NB; ++i) read_op(la, lb, kk, i, na, nb);
 #pragma unroll
-      for (int b = 0; b < C::NB; ++b) {
-        fa[kk][b] = tr_pair(la, ra[b] + kk * 16 * SROW, ra[b] + (kk * 16 + 4) * SROW);
-        fbv[kk][b] = tr_pair(lb, rb[b] + kk * 16 * SROW, rb[b] + (kk * 16 + 4) * SROW);
-      }
+    for (int x = 0; x < C::NB; ++x)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int x = 0; x < C::NB; ++x)
-#pragma unroll
-        for (int y = 0; y < C::NB; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk][x], fbv[kk][y], acc[x][y], 0, 0, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4 * C::NB, 0);    // step-0 reads
+      for (int y = 0; y < C::NB; ++y)
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[x], fb[y], acc[x][y], 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4 * C::NB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // step-0 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // step-1 read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one tr read of the next step
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, C::NB * C::NB, 0);  // step-1 MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x008, C::NB * C::NB - 4 * C::NB, 0);
   };
-  // one stage: own DMA of this stage done (two later stages may be in
-  // flight), barrier (every wave's DMA done, previous slot free), refill the
-  // freed slot three stages ahead, multiply
-  // (a bare s_barrier: __syncthreads would also wait for the DMA still in
-  // flight for later stages)
-  auto stage = [&](int64_t st, const char* la, const char* lb, char* na, char* nb) __attribute__((always_inline)) {
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-    issue(st + 3, na, nb);
-    compute(la, lb);
+  // stage st (slot st % 4 = cur, next slot nx): step-0 MFMAs with the step-1
+  // reads of stage st; barrier publishing stage st + 1 (this wave's DMA of
+  // stage st + 1 done: only stage st + 2 may be in flight) and freeing slot
+  // st - 1, which takes stage st + 3; step-1 MFMAs with the step-0 reads of
+  // stage st + 1.  (A bare s_barrier: __syncthreads would also wait for the
+  // DMA of stage st + 2.)
+  auto stage = [&](int64_t st, int cur, const char* la, const char* lb, const char* lan, const char* lbn)
+      __attribute__((always_inline)) {
+    half(fa0r, fb0r, la, lb, 1, fa1r, fb1r);
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    issue(st + 3, (cur + 3) & 3);
+    half(fa1r, fb1r, lan, lbn, 0, fa0r, fb0r);
   };
 
   if (nst > 0) {
-    issue(0, a0, b0);
-    issue(1, a1, b1);
-    issue(2, a2, b2);
+    issue(0, 0);
+    issue(1, 1);
+    issue(2, 2);
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 2 * C::NB; ++i) read_op(a0, b0, 0, i, fa0r, fb0r);
     for (int64_t st = 0; st < nst; st += 4) {
-      stage(st, a0, b0, a3, b3);
-      if (st + 1 < nst) stage(st + 1, a1, b1, a0, b0);
-      if (st + 2 < nst) stage(st + 2, a2, b2, a1, b1);
-      if (st + 3 < nst) stage(st + 3, a3, b3, a2, b2);
+      stage(st, 0, a0, b0, a1, b1);
+      if (st + 1 < nst) stage(st + 1, 1, a1, b1, a2, b2);
+      if (st + 2 < nst) stage(st + 2, 2, a2, b2, a3, b3);
+      if (st + 3 < nst) stage(st + 3, 3, a3, b3, a0, b0);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
