@@ -515,18 +515,64 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
     }
     __builtin_amdgcn_sched_group_barrier(0x008, C::NB * C::NB - 4 * C::NB, 0);
   };
-  // stage st (slot st % 4 = cur, next slot nx): step-0 MFMAs with the step-1
-  // reads of stage st; barrier publishing stage st + 1 (this wave's DMA of
-  // stage st + 1 done: only stage st + 2 may be in flight) and freeing slot
-  // st - 1, which takes stage st + 3; step-1 MFMAs with the step-0 reads of
-  // stage st + 1.  (A bare s_barrier: __syncthreads would also wait for the
-  // DMA of stage st + 2.)
+  // Per-lane global addresses of the 8 DMAs of a stage (A0, B0, A1, B1, ...):
+  // whole stages from the stage base; partial stages and edge tiles send the
+  // lanes past n or d to the zero chunk.
+  auto dma_addrs = [&](int64_t stage, const void** ad) __attribute__((always_inline)) {
+    const int64_t sc = stage < nst ? stage : nst - 1;
+    const char* xs = xbase + sc * sbytes;
+    const char* xa = xs + fa0 * 2;
+    const char* xb = xs + fb0 * 2;
+    if (!edge && sc < nwhole) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ad[2 * j] = xa + doff[j];
+        ad[2 * j + 1] = xb + doff[j];
+      }
+    } else {
+      const int64_t t0 = (st_begin + sc) * SK;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool rok = t0 + drow[j] < n;
+        const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
+        const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
+        ad[2 * j] = aok ? (const void*)(xa + doff[j]) : (const void*)kZeroChunk;
+        ad[2 * j + 1] = bok ? (const void*)(xb + doff[j]) : (const void*)kZeroChunk;
+      }
+    }
+  };
+  // Step MFMAs with the next step's reads and one DMA after every two MFMAs.
+  // A burst of DMAs right after the barrier stalls the issuing wave until the
+  // load path drains them (and its MFMAs with it); one DMA per 64 MFMA cycles
+  // keeps the path under half load.  A scheduling barrier after each group
+  // keeps the interleave in source order.
+  auto half_dma = [&](const bf16x8_t* fa, const bf16x8_t* fb, const char* la, const char* lb, int kk, bf16x8_t* na,
+                      bf16x8_t* nb, const void* const* ad, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2 * C::NB; ++i) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int m = 2 * i + h, x = m / C::NB, y = m % C::NB;
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[x], fb[y], acc[x][y], 0, 0, 0);
+      }
+      read_op(la, lb, kk, i, na, nb);
+      dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // stage st (slot st % 4 = cur): step-0 MFMAs with the step-1 reads of stage
+  // st; barrier publishing stage st + 1 (this wave's DMA of stage st + 1 done:
+  // only stage st + 2 may be in flight) and freeing slot st - 1, which takes
+  // stage st + 3; step-1 MFMAs with the step-0 reads of stage st + 1 and the
+  // DMA of stage st + 3.  (A bare s_barrier: __syncthreads would also wait
+  // for the DMA of stage st + 2.)
   auto stage = [&](int64_t st, int cur, const char* la, const char* lb, const char* lan, const char* lbn)
       __attribute__((always_inline)) {
+    const void* ad[8];
+    dma_addrs(st + 3, ad);
     half(fa0r, fb0r, la, lb, 1, fa1r, fb1r);
     asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-    issue(st + 3, (cur + 3) & 3);
-    half(fa1r, fb1r, lan, lbn, 0, fa0r, fb0r);
+    half_dma(fa1r, fb1r, lan, lbn, 0, fa0r, fb0r, ad, (cur + 3) & 3);
   };
 
   if (nst > 0) {
