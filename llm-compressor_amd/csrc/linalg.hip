@@ -811,10 +811,12 @@ namespace {
 std::mutex g_blas_mu;
 rocblas_handle g_blas[64] = {};
 
-int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
+// Runs f(handle) under the lock with this device's handle bound to `stream`.
+template <class F>
+int with_blas(hipStream_t stream, F&& f) {
   int dev = 0;
   MQ_CHECK_HIP(hipGetDevice(&dev));
-  MQ_CHECK_ARG(dev >= 0 && dev < 64, "gemm: device index out of range");
+  MQ_CHECK_ARG(dev >= 0 && dev < 64, "rocblas: device index out of range");
   std::lock_guard<std::mutex> lock(g_blas_mu);
   if (!g_blas[dev] && rocblas_create_handle(&g_blas[dev]) != rocblas_status_success) {
     g_blas[dev] = nullptr;
@@ -826,8 +828,20 @@ int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream)
     set_error("rocblas_set_stream failed");
     return MI355Q_HIP_ERROR;
   }
-  // row-major C = alpha A op(B) + beta C  <=>  column-major C^T = alpha op(B)^T A^T + beta C^T.
-  // Two batch levels: one strided-batched call per index of the shorter level.
+  return f(h);
+}
+
+int blas_status(rocblas_status rs, const char* what) {
+  if (rs == rocblas_status_success) return MI355Q_OK;
+  set_error("%s failed: %s", what, rocblas_status_to_string(rs));
+  return MI355Q_HIP_ERROR;
+}
+
+// Two batch levels (GemmArgs::inner): one strided-batched library call per
+// index of the shorter level, batching over the longer one.  f(nbat, oa, ob,
+// oc, sa, sb, sc) issues one call.
+template <class F>
+int blas_batches(const GemmArgs& g, int batch, F&& f) {
   const int64_t n1 = g.inner > 0 ? g.inner : batch, n2 = batch / n1;
   const bool loop1 = n1 < n2;  // loop over level 1, batch over level 2
   const int64_t nloop = loop1 ? n1 : n2, nbat = loop1 ? n2 : n1;
@@ -836,48 +850,40 @@ int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream)
   for (int64_t l = 0; l < nloop; ++l) {
     const int64_t oa = l * (loop1 ? g.strideA : g.strideA2), ob = l * (loop1 ? g.strideB : g.strideB2),
                   oc = l * (loop1 ? g.strideC : g.strideC2);
-    const rocblas_status rs = rocblas_sgemm_strided_batched(
-        h, b_trans ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none,
-        (rocblas_int)g.N, (rocblas_int)g.M, (rocblas_int)g.K, &g.alpha, g.B + ob, (rocblas_int)g.ldb, sb,
-        g.A + oa, (rocblas_int)g.lda, sa, &g.beta, g.C + oc, (rocblas_int)g.ldc, sc, (rocblas_int)nbat);
-    if (rs != rocblas_status_success) {
-      set_error("rocblas_sgemm_strided_batched failed: %s", rocblas_status_to_string(rs));
-      return MI355Q_HIP_ERROR;
-    }
+    const int rc = f(nbat, oa, ob, oc, sa, sb, sc);
+    if (rc) return rc;
   }
   return MI355Q_OK;
 }
 
-// Lower triangle of row-major C (n x n) += alpha P P^T with P (n x k) row-major:
-// rocBLAS ssyrk on the column-major view (upper triangle of C^T = C).
+// row-major C = alpha A op(B) + beta C  <=>  column-major C^T = alpha op(B)^T A^T + beta C^T
+int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
+  return with_blas(stream, [&](rocblas_handle h) {
+    return blas_batches(g, batch, [&](int64_t nbat, int64_t oa, int64_t ob, int64_t oc, int64_t sa, int64_t sb,
+                                      int64_t sc) {
+      return blas_status(
+          rocblas_sgemm_strided_batched(h, b_trans ? rocblas_operation_transpose : rocblas_operation_none,
+                                        rocblas_operation_none, (rocblas_int)g.N, (rocblas_int)g.M, (rocblas_int)g.K,
+                                        &g.alpha, g.B + ob, (rocblas_int)g.ldb, sb, g.A + oa, (rocblas_int)g.lda, sa,
+                                        &g.beta, g.C + oc, (rocblas_int)g.ldc, sc, (rocblas_int)nbat),
+          "rocblas_sgemm_strided_batched");
+    });
+  });
+}
+
 int syrk_rocblas(float* C, int64_t ldc, const float* P, int64_t ldp, int64_t n, int64_t k, float alpha, float beta,
                  int64_t batch, int64_t stride, hipStream_t stream) {
-  int dev = 0;
-  MQ_CHECK_HIP(hipGetDevice(&dev));
-  MQ_CHECK_ARG(dev >= 0 && dev < 64, "syrk: device index out of range");
-  std::lock_guard<std::mutex> lock(g_blas_mu);
-  if (!g_blas[dev] && rocblas_create_handle(&g_blas[dev]) != rocblas_status_success) {
-    g_blas[dev] = nullptr;
-    set_error("rocblas_create_handle failed");
-    return MI355Q_HIP_ERROR;
-  }
-  rocblas_handle h = g_blas[dev];
-  if (rocblas_set_stream(h, stream) != rocblas_status_success) {
-    set_error("rocblas_set_stream failed");
-    return MI355Q_HIP_ERROR;
-  }
-  const rocblas_status rs =
-      batch == 1 ? rocblas_ssyrk(h, rocblas_fill_upper, rocblas_operation_transpose, (rocblas_int)n, (rocblas_int)k,
-                                 &alpha, P, (rocblas_int)ldp, &beta, C, (rocblas_int)ldc)
-                 : rocblas_ssyrk_strided_batched(h, rocblas_fill_upper, rocblas_operation_transpose, (rocblas_int)n,
-                                                 (rocblas_int)k, &alpha, P, (rocblas_int)ldp, stride, &beta, C,
-                                                 (rocblas_int)ldc, stride, (rocblas_int)batch);
-  if (rs != rocblas_status_success) {
-    set_error("rocblas_ssyrk failed: %s", rocblas_status_to_string(rs));
-    return MI355Q_HIP_ERROR;
-  }
-  return MI355Q_OK;
+  return with_blas(stream, [&](rocblas_handle h) {
+    return blas_status(
+        batch == 1 ? rocblas_ssyrk(h, rocblas_fill_upper, rocblas_operation_transpose, (rocblas_int)n, (rocblas_int)k,
+                                   &alpha, P, (rocblas_int)ldp, &beta, C, (rocblas_int)ldc)
+                   : rocblas_ssyrk_strided_batched(h, rocblas_fill_upper, rocblas_operation_transpose,
+                                                   (rocblas_int)n, (rocblas_int)k, &alpha, P, (rocblas_int)ldp,
+                                                   stride, &beta, C, (rocblas_int)ldc, stride, (rocblas_int)batch),
+        "rocblas_ssyrk");
+  });
 }
+
 }  // namespace
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
@@ -1053,24 +1059,38 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       if (npairs == 0) continue;
       const int64_t c0 = a0 + s;
       const int64_t stride_diag = 2 * s * (d + 1);
-      // T = L[c0:c0+s2, a0:a0+s] * X[a0:a0+s, a0:a0+s]
-      GemmArgs t1{};
-      t1.A = F + c0 * d + a0; t1.lda = d; t1.strideA = stride_diag; t1.strideA2 = wsf;
-      t1.B = X + a0 * d + a0; t1.ldb = d; t1.strideB = stride_diag; t1.strideB2 = wsf;
-      t1.C = T; t1.ldc = s; t1.strideC = s2 * s; t1.strideC2 = wsf;
-      t1.inner = npairs; t1.b_lower = 1;  // X11 is lower triangular
-      t1.M = s2; t1.N = s; t1.K = s; t1.alpha = 1.f; t1.beta = 0.f;
-      int rc = gemm_f32(t1, false, (int)(npairs * batch), st);
-      if (rc) return rc;
-      // X[c0:c0+s2, a0:a0+s] = -X[c0:c0+s2, c0:c0+s2] * T
-      GemmArgs t2{};
-      t2.A = X + c0 * d + c0; t2.lda = d; t2.strideA = stride_diag; t2.strideA2 = wsf;
-      t2.B = T; t2.ldb = s; t2.strideB = s2 * s; t2.strideB2 = wsf;
-      t2.C = X + c0 * d + a0; t2.ldc = d; t2.strideC = stride_diag; t2.strideC2 = wsf;
-      t2.inner = npairs; t2.a_lower = 1;  // X22 is lower triangular
-      t2.M = s2; t2.N = s; t2.K = s2; t2.alpha = -1.f; t2.beta = 0.f;
-      rc = gemm_f32(t2, false, (int)(npairs * batch), st);
-      if (rc) return rc;
+      // Large levels (library GEMMs, which do not skip the zero triangle)
+      // run as `parts` strips, each with only the K range where the
+      // triangular operand can be nonzero: 5/8 of the multiply-adds at 4
+      // strips.  Smaller levels use the triangular K ranges of the MFMA
+      // kernel directly.
+      const int64_t parts = (s >= 1024 && s % 4 == 0 && s2 % 4 == 0) ? 4 : 1;
+      // T = L[c0:c0+s2, a0:a0+s] * X[a0:a0+s, a0:a0+s], column strip j of T
+      // needs rows k >= j w of the lower-triangular X11
+      for (int64_t j = 0; j < parts; ++j) {
+        const int64_t w = s / parts, k0 = j * w;
+        GemmArgs t1{};
+        t1.A = F + c0 * d + a0 + k0; t1.lda = d; t1.strideA = stride_diag; t1.strideA2 = wsf;
+        t1.B = X + (a0 + k0) * d + a0 + k0; t1.ldb = d; t1.strideB = stride_diag; t1.strideB2 = wsf;
+        t1.C = T + k0; t1.ldc = s; t1.strideC = s2 * s; t1.strideC2 = wsf;
+        t1.inner = npairs; t1.b_lower = 1;  // X11 is lower triangular
+        t1.M = s2; t1.N = w; t1.K = s - k0; t1.alpha = 1.f; t1.beta = 0.f;
+        const int rc = gemm_f32(t1, false, (int)(npairs * batch), st);
+        if (rc) return rc;
+      }
+      // X[c0:c0+s2, a0:a0+s] = -X[c0:c0+s2, c0:c0+s2] * T, row strip i of
+      // the result needs columns k < (i + 1) w of the lower-triangular X22
+      for (int64_t i = 0; i < parts; ++i) {
+        const int64_t w = s2 / parts, r0 = i * w;
+        GemmArgs t2{};
+        t2.A = X + (c0 + r0) * d + c0; t2.lda = d; t2.strideA = stride_diag; t2.strideA2 = wsf;
+        t2.B = T; t2.ldb = s; t2.strideB = s2 * s; t2.strideB2 = wsf;
+        t2.C = X + (c0 + r0) * d + a0; t2.ldc = d; t2.strideC = stride_diag; t2.strideC2 = wsf;
+        t2.inner = npairs; t2.a_lower = parts == 1 ? 1 : 0;  // X22 is lower triangular
+        t2.M = w; t2.N = s; t2.K = parts == 1 ? s2 : r0 + w; t2.alpha = -1.f; t2.beta = 0.f;
+        const int rc = gemm_f32(t2, false, (int)(npairs * batch), st);
+        if (rc) return rc;
+      }
     }
   }
   hipLaunchKernelGGL(flip_out_kernel, fg, fb, 0, st, X, d, hinv_dev, wsf, shinv);
