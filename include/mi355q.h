@@ -117,6 +117,14 @@ int mi355q_gptq_hinv_batched(const float* h_dev, int64_t ldh, int64_t stride_h, 
                              int64_t stride_hinv, int32_t* dead_dev, int32_t* status_dev,
                              void* workspace_dev, size_t workspace_bytes, void* stream);
 
+/* mi355q_gptq_hinv_fallback: hinv + b * stride_hinv = identity for every b
+ * with status_dev[b] != 0 -- the reference's non-positive-definite branch
+ * (gptq_quantize.py:189-196: LinAlgError -> Hinv = eye, round-to-nearest)
+ * applied on the device, so the solve runs on without reading the flag on
+ * the host.  batch <= 65535. */
+int mi355q_gptq_hinv_fallback(float* hinv_dev, int64_t d, int64_t stride_hinv, int64_t batch,
+                              const int32_t* status_dev, void* stream);
+
 /* mi355q_gptq_load_weight: w_work[r][j] = dead[j] ? 0 : float(w[r][perm[j]])
  * (fp32 working copy, :121,126,142,178).  perm_dev / dead_dev may be NULL. */
 int mi355q_gptq_load_weight(const void* w_dev, mi355q_dtype w_dtype, int64_t rows, int64_t cols,

@@ -302,22 +302,27 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
     return;
   }
 
-  // direct update of the upper triangle
-  const int64_t gi0 = (int64_t)ti * TM, gj0 = (int64_t)tj * TM;
+  // direct update of the upper triangle, one 32 x 32 block at a time (the
+  // scheduling barrier keeps the blocks' loads from being hoisted together,
+  // which would need more registers than the accumulators leave free)
+  const bool diag = ti == tj;
 #pragma unroll
   for (int bm = 0; bm < C::NB; ++bm)
 #pragma unroll
-    for (int bn = 0; bn < C::NB; ++bn)
+    for (int bn = 0; bn < C::NB; ++bn) {
+      const int mb = wm * C::W + bm * 32, nb = wn * C::W + bn * 32;
+      const int64_t gib = (int64_t)ti * TM + mb, gjb = (int64_t)tj * TM + nb;
+      float* hb = mat.h + gib * p.ldh + gjb;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = wm * C::W + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int nn = wn * C::W + bn * 32 + (lane & 31);
-        const int64_t gi = gi0 + m, gj = gj0 + nn;
-        if (gi < p.d && gj < p.d && gi <= gj) {
-          float* hp = mat.h + gi * p.ldh + gj;
+        const int mi = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), nj = lane & 31;
+        if (gib + mi < p.d && gjb + nj < p.d && (!diag || mb + mi <= nb + nj)) {
+          float* hp = hb + (int64_t)mi * p.ldh + nj;
           *hp = *hp + p.alpha * acc[bm][bn][r];
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
 // ---------------------------------------------------------------- streaming syrk
@@ -591,33 +596,19 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  if (slot >= 0) {
-    float* dst = p.ws + (slot * NT + tid) * C::ACC;
-#pragma unroll
-    for (int x = 0; x < C::NB; ++x)
-#pragma unroll
-      for (int y = 0; y < C::NB; ++y)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          f32x4_t v = {acc[x][y][4 * r4], acc[x][y][4 * r4 + 1], acc[x][y][4 * r4 + 2], acc[x][y][4 * r4 + 3]};
-          *reinterpret_cast<f32x4_t*>(dst + (x * C::NB + y) * 16 + 4 * r4) = v;
-        }
-    return;
-  }
-  const int64_t gi0 = fa0, gj0 = fb0;
+  // partial slot in MFMA fragment order (single-split calls, which update H
+  // directly, take syrk_bf16_kernel: the direct update's registers next to
+  // 256 live accumulators would spill here)
+  if (slot < 0) return;
+  float* dst = p.ws + (slot * NT + tid) * C::ACC;
 #pragma unroll
   for (int x = 0; x < C::NB; ++x)
 #pragma unroll
     for (int y = 0; y < C::NB; ++y)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = wm * C::W + x * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int nn = wn * C::W + y * 32 + (lane & 31);
-        const int64_t gi = gi0 + m, gj = gj0 + nn;
-        if (gi < p.d && gj < p.d && gi <= gj) {
-          float* hp = mat.h + gi * p.ldh + gj;
-          *hp = *hp + p.alpha * acc[x][y][r];
-        }
+      for (int r4 = 0; r4 < 4; ++r4) {
+        f32x4_t v = {acc[x][y][4 * r4], acc[x][y][4 * r4 + 1], acc[x][y][4 * r4 + 2], acc[x][y][4 * r4 + 3]};
+        *reinterpret_cast<f32x4_t*>(dst + (x * C::NB + y) * 16 + 4 * r4) = v;
       }
 }
 
@@ -768,8 +759,9 @@ DensePlan plan_dense(int64_t n, int64_t d) {
 void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
   const bool g = p.rows != nullptr;
   if (tile_edge(d) == 256) {
-    if (g) hipLaunchKernelGGL((syrk_bf16_kernel<256, true>), dim3(grid), dim3(NT), 0, st, p);
-    else   hipLaunchKernelGGL(syrk_stream_kernel, dim3(grid), dim3(NT), 0, st, p);
+    if (g)             hipLaunchKernelGGL((syrk_bf16_kernel<256, true>), dim3(grid), dim3(NT), 0, st, p);
+    else if (p.S == 1) hipLaunchKernelGGL((syrk_bf16_kernel<256, false>), dim3(grid), dim3(NT), 0, st, p);
+    else               hipLaunchKernelGGL(syrk_stream_kernel, dim3(grid), dim3(NT), 0, st, p);
   } else {
     if (g) hipLaunchKernelGGL((syrk_bf16_kernel<128, true>), dim3(grid), dim3(NT), 0, st, p);
     else   hipLaunchKernelGGL((syrk_bf16_kernel<128, false>), dim3(grid), dim3(NT), 0, st, p);

@@ -783,6 +783,16 @@ __global__ void place_diag_inv_kernel(const float* linv, int64_t d, float* X, in
   }
 }
 
+// hinv of matrix b = identity where status[b] != 0 (blockIdx.y = b); every
+// thread reads the flag, so a positive-definite matrix costs one load
+__global__ void identity_on_failure_kernel(float* hinv, int64_t d, int64_t stride, const int32_t* status) {
+  const int64_t b = blockIdx.y;
+  if (status[b] == 0) return;
+  float* h = hinv + b * stride;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < d * d; i += (int64_t)gridDim.x * blockDim.x)
+    h[i] = (i / d == i % d) ? 1.f : 0.f;
+}
+
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct HinvLayout {
@@ -1130,4 +1140,17 @@ extern "C" int mi355q_gptq_hinv_batched(const float* h_dev, int64_t ldh, int64_t
   return hinv_impl(h_dev, ldh, stride_h, d, batch, perm_dev, stride_perm, num_samples_dev, 0.f, percdamp,
                    hinv_dev, stride_hinv, dead_dev, status_dev, static_cast<char*>(workspace_dev),
                    reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int mi355q_gptq_hinv_fallback(float* hinv_dev, int64_t d, int64_t stride_hinv, int64_t batch,
+                                         const int32_t* status_dev, void* stream) {
+  MQ_CHECK_ARG(d > 0 && batch > 0 && batch <= 65535, "hinv fallback: bad d or batch");
+  MQ_CHECK_ARG(stride_hinv >= d * d || batch == 1, "hinv fallback: stride_hinv below d * d");
+  MQ_CHECK_ARG(hinv_dev != nullptr && status_dev != nullptr, "hinv fallback: null pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t blocks = (d * d + 255) / 256;
+  hipLaunchKernelGGL(identity_on_failure_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024), (unsigned)batch),
+                     dim3(256), 0, st, hinv_dev, d, stride_hinv, status_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
 }

@@ -37,6 +37,7 @@ SIGNATURES = {
     "mi355q_gptq_store_weight": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _vp]),
     "mi355q_gptq_hinv_batched": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _f32, _vp, _i64, _vp, _vp,
                                         _vp, _sz, _vp]),
+    "mi355q_gptq_hinv_fallback": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "mi355q_gptq_load_weight_batched": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
                                                _vp]),
     "mi355q_gptq_sweep_batched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i32,

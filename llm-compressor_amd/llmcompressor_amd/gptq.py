@@ -97,14 +97,24 @@ def _qparams_for_sweep(scale: torch.Tensor, zero_point: torch.Tensor, strategy: 
 class PreparedHessian:
     """The weight-independent part of the solve for one Hessian (or a stack):
     activation-order permutation, dead columns and the upper Cholesky factor of
-    the damped inverse, with the RTN fallback already applied.  Modules whose
+    the damped inverse, with the RTN fallback already applied on the device
+    (hinv = identity where the Hessian is not positive definite).  ``status``
+    is the device flag (int32 [1] or [B], 0 = positive definite); it is read
+    on the host only after the solve's final synchronisation.  Modules whose
     inputs are the same tensor (q/k/v, gate/up) share it."""
     actorder: ActivationOrdering | None
     perm: torch.Tensor | None
     invperm: torch.Tensor | None
     hinv: torch.Tensor
     dead: torch.Tensor
-    ok: torch.Tensor | bool
+    status: torch.Tensor
+
+    @property
+    def ok(self):
+        """Positive definite: a bool (single) or a host bool tensor [B]
+        (synchronises)."""
+        ok = self.status.cpu() == 0
+        return bool(ok[0]) if ok.numel() == 1 and self.hinv.dim() == 2 else ok
 
 
 def _effective_actorder(quant_args: QuantizationArgs):
@@ -132,11 +142,8 @@ def prepare_hessian(hessian: torch.Tensor, quant_args: QuantizationArgs, num_sam
     if actorder:
         perm = torch.argsort(torch.diagonal(hessian), descending=True, stable=True)
         invperm = torch.argsort(perm)
-    hinv, dead, ok = ops.gptq_hinv(hessian, perm, float(num_samples), percdamp)
-    if not ok:
-        _hinv_fallback_warning()
-        hinv = torch.eye(hessian.shape[0], dtype=torch.float32, device=hessian.device)
-    return PreparedHessian(actorder, perm, invperm, hinv, dead, ok)
+    hinv, dead, status = ops.gptq_hinv_rtn(hessian, perm, float(num_samples), percdamp)
+    return PreparedHessian(actorder, perm, invperm, hinv, dead, status)
 
 
 def prepare_hessians_batched(hessians: torch.Tensor, quant_args: QuantizationArgs, num_samples=1.0,
@@ -149,11 +156,8 @@ def prepare_hessians_batched(hessians: torch.Tensor, quant_args: QuantizationArg
     if actorder:
         perm = torch.argsort(torch.diagonal(hessians, dim1=1, dim2=2), dim=1, descending=True, stable=True)
         invperm = torch.argsort(perm, dim=1)
-    hinv, dead, ok = ops.gptq_hinv_batched(hessians, perm, ns, percdamp)
-    for b in torch.nonzero(~ok).flatten().tolist():
-        _hinv_fallback_warning()
-        hinv[b] = torch.eye(d, dtype=torch.float32, device=hessians.device)
-    return PreparedHessian(actorder, perm, invperm, hinv, dead, ok)
+    hinv, dead, status = ops.gptq_hinv_batched(hessians, perm, ns, percdamp, sync=False)
+    return PreparedHessian(actorder, perm, invperm, hinv, dead, status)
 
 
 def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: torch.Tensor, observer,
@@ -192,7 +196,7 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
     qp = observer.get_qparams()
     scale, zero_point = qp["scale"], qp["zero_point"]
 
-    hinv, dead, ok = prep.hinv, prep.dead, prep.ok
+    hinv, dead = prep.hinv, prep.dead
     w_work = ops.gptq_load_weight(W, perm, dead)
     s, z = _qparams_for_sweep(scale, zero_point, strategy)
     qmin, qmax = quant_args.q_range()
@@ -200,9 +204,12 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
     codes, losses = ops.gptq_sweep_(w_work, hinv, s, z, strategy.value, g_idx, qmin, qmax,
                                     dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize, block_h=bh)
     w_out, codes_out = ops.gptq_store_weight(w_work, invperm, W.dtype, codes)
-    loss = torch.sum(losses).item()
-    return GPTQResult(loss=loss, weight=w_out, scale=scale, zero_point=zero_point, g_idx=g_idx, perm=perm,
-                      codes=codes_out, hinv_ok=ok)
+    loss_ok = torch.stack([torch.sum(losses), (prep.status[0] == 0).float()]).cpu()  # the one sync
+    ok = bool(loss_ok[1])
+    if not ok:
+        _hinv_fallback_warning()
+    return GPTQResult(loss=float(loss_ok[0]), weight=w_out, scale=scale, zero_point=zero_point, g_idx=g_idx,
+                      perm=perm, codes=codes_out, hinv_ok=ok)
 
 
 def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, hessians: torch.Tensor,
@@ -260,7 +267,7 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
         if actorder == ActivationOrdering.WEIGHT:
             g_idx = g_idx[perm]
 
-    hinv, dead, ok = prep.hinv, prep.dead, prep.ok
+    hinv, dead = prep.hinv, prep.dead
     w_work = ops.gptq_load_weight_batched(weights, perm, dead)
     qmin, qmax = quant_args.q_range()
     bh = quant_args.block_structure[0] if strategy == QuantizationStrategy.BLOCK else 1
@@ -269,7 +276,10 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
                                             dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize,
                                             block_h=bh)
     w_out, codes_out = ops.gptq_store_weight_batched(w_work, invperm, weights.dtype, codes)
-    loss = torch.sum(losses, dim=1).cpu()
+    loss_ok = torch.stack([torch.sum(losses, dim=1), (prep.status == 0).float()]).cpu()  # the one sync
+    loss, ok = loss_ok[0], loss_ok[1] > 0
+    for _ in range(int((~ok).sum())):
+        _hinv_fallback_warning()
     out = []
     for b in range(B):
         sb, zb = scale[b], zero_point[b]

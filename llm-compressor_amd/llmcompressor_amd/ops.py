@@ -103,6 +103,27 @@ def gptq_hinv(H: torch.Tensor, perm: torch.Tensor | None, num_samples: float, pe
     return hinv, dead, ok
 
 
+def gptq_hinv_rtn(H: torch.Tensor, perm: torch.Tensor | None, num_samples: float, percdamp: float):
+    """``gptq_hinv`` without a host synchronisation: a Hessian that is not
+    positive definite gets hinv = identity on the device (the reference's
+    round-to-nearest fallback).  Returns (hinv, dead, status [1] int32 on the
+    device, 0 = positive definite)."""
+    L.require_gpu(H)
+    d = H.shape[0]
+    dev = H.device
+    hinv = torch.empty((d, d), dtype=torch.float32, device=dev)
+    dead = torch.empty(d, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    lib = L.lib()
+    ws = _ws(lib.mi355q_gptq_hinv_workspace_size(d), dev)
+    p = None if perm is None else perm.to(torch.int32).contiguous()
+    L.check(lib.mi355q_gptq_hinv(H.data_ptr(), H.stride(0), d, L.ptr(p), C.c_float(num_samples),
+                                 C.c_float(percdamp), hinv.data_ptr(), dead.data_ptr(), status.data_ptr(),
+                                 ws.data_ptr(), ws.numel(), L.stream_of(H)))
+    L.call("mi355q_gptq_hinv_fallback", hinv.data_ptr(), d, d * d, 1, status.data_ptr(), L.stream_of(H))
+    return hinv, dead, status
+
+
 def gptq_load_weight(w: torch.Tensor, perm=None, dead=None) -> torch.Tensor:
     L.require_gpu(w)
     rows, cols = w.shape
@@ -152,10 +173,14 @@ def gptq_store_weight(w_work: torch.Tensor, invperm, out_dtype: torch.dtype, cod
 
 
 # ---------------------------------------------------------------- batched GPTQ
-def gptq_hinv_batched(H: torch.Tensor, perm: torch.Tensor | None, num_samples: torch.Tensor, percdamp: float):
+def gptq_hinv_batched(H: torch.Tensor, perm: torch.Tensor | None, num_samples: torch.Tensor, percdamp: float,
+                      sync: bool = True):
     """``gptq_hinv`` for a stack H [B, d, d] of same-order Hessians (perm [B, d]
     or None, num_samples [B]).  Returns (hinv [B, d, d], dead [B, d], ok
-    [B] bool tensor on the host); synchronises once."""
+    [B] bool tensor on the host); synchronises once.  With ``sync=False``:
+    no synchronisation, members that are not positive definite get
+    hinv = identity on the device, and the third value is the status [B]
+    int32 device tensor (0 = positive definite)."""
     L.require_gpu(H)
     B, d, _ = H.shape
     dev = H.device
@@ -170,6 +195,9 @@ def gptq_hinv_batched(H: torch.Tensor, perm: torch.Tensor | None, num_samples: t
                                          0 if p is None else d, ns.data_ptr(), C.c_float(percdamp),
                                          hinv.data_ptr(), d * d, dead.data_ptr(), status.data_ptr(),
                                          ws.data_ptr(), ws.numel(), L.stream_of(H)))
+    if not sync:
+        L.call("mi355q_gptq_hinv_fallback", hinv.data_ptr(), d, d * d, B, status.data_ptr(), L.stream_of(H))
+        return hinv, dead, status
     return hinv, dead, status.cpu() == 0
 
 

@@ -282,6 +282,31 @@ def test_gptq_hinv_non_pd_reports_status(dev):
     assert not ok
 
 
+def test_gptq_non_pd_falls_back_to_rtn_on_device(dev):
+    """A Hessian that is not positive definite gets Hinv = identity on the
+    device (no host synchronisation before the sweep), so the solve is
+    round-to-nearest, as the reference's LinAlgError branch
+    (gptq_quantize.py:189-196)."""
+    say("gptq non-PD -> RTN on the device")
+    d, rows = 256, 64
+    qa = QuantizationArgs(type="int", num_bits=4, strategy="group", group_size=128)
+    H = torch.triu(_spd_from_tokens(d, 1024, seed=61))
+    H[5, 5] = -1e3
+    prep = gptq.prepare_hessian(H.to(dev), qa, 1.0)
+    assert torch.equal(prep.hinv.cpu(), torch.eye(d))
+    assert prep.ok is False
+    W = workloads.gptq_weight(rows, d, seed=62).to(dev)
+    obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+    obs(W)
+    res = gptq.gptq_quantize(W, qa, H.to(dev), obs, prepared=prep)
+    assert res.hinv_ok is False
+    s = res.scale.float().repeat_interleave(128, dim=1)
+    rtn = torch.clamp(torch.round(W.float() / s), -8, 7)
+    assert torch.equal(res.codes.float().cpu(), rtn.cpu())
+    ok_prep = gptq.prepare_hessian(torch.triu(_spd_from_tokens(d, 1024, seed=63)).to(dev), qa, 1.0)
+    assert ok_prep.ok is True
+
+
 GPTQ_CASES = [
     dict(num_bits=4, strategy="group", group_size=128),
     dict(num_bits=4, strategy="group", group_size=128, symmetric=False),
