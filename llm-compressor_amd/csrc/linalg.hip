@@ -351,14 +351,14 @@ __global__ __launch_bounds__(GNT, 1) void gemm_k128_kernel(GemmArgs g) {
 // 32 x 32 quadrant, K = 128 as 64 MFMA steps on two accumulators), so the
 // same product spreads over four times as many CUs with a quarter of the
 // chain per wave.  Whole tiles only: M and N multiples of 64, 16-byte
-// aligned rows.
+// aligned rows.  Both operands sit in LDS as [row][k] (B transposed on the
+// way in when it arrives as [k][n]): 66 KB, two workgroups per CU.
 constexpr int ST = 64;           // tile edge
-constexpr int SLB = ST + 32;     // LDS stride of [k][n] B tiles
 
 template <bool BT>
 __global__ __launch_bounds__(GNT, 2) void gemm_k128_small_kernel(GemmArgs g) {
   __shared__ float la[ST * KLA];
-  __shared__ float lb[BT ? ST * KLA : KT * SLB];
+  __shared__ float lb[ST * KLA];
   {
     const int64_t bz = blockIdx.z;
     const int64_t b1 = g.inner > 0 ? bz % g.inner : bz, b2 = g.inner > 0 ? bz / g.inner : 0;
@@ -416,9 +416,13 @@ __global__ __launch_bounds__(GNT, 2) void gemm_k128_small_kernel(GemmArgs g) {
       for (int e = 0; e < 4; ++e) lb[row * KLA + k4 + e] = rb[v][e];
     }
   } else {
+    // [k][n] float4 -> [n][k]: lanes of a wave hit banks 4 (n / 4) + k % 4, all distinct
 #pragma unroll
-    for (int v = 0; v < 8; ++v)
-      *reinterpret_cast<f32x4_t*>(lb + (16 * v + (tid >> 4)) * SLB + 4 * (tid & 15)) = rb[v];
+    for (int v = 0; v < 8; ++v) {
+      const int k = 16 * v + (tid >> 4), n4 = 4 * (tid & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lb[(n4 + e) * KLA + k] = rb[v][e];
+    }
   }
   __syncthreads();
 
@@ -426,12 +430,11 @@ __global__ __launch_bounds__(GNT, 2) void gemm_k128_small_kernel(GemmArgs g) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
   const float* pa = la + (wm * 32 + (lane & 31)) * KLA + (lane >> 5);
-  const float* pb = BT ? lb + (wn * 32 + (lane & 31)) * KLA + (lane >> 5) : lb + (lane >> 5) * SLB + wn * 32 + (lane & 31);
+  const float* pb = lb + (wn * 32 + (lane & 31)) * KLA + (lane >> 5);
 #pragma unroll
   for (int kk = 0; kk < KT / 2; kk += 2) {
     const float a0 = pa[2 * kk], a1 = pa[2 * kk + 2];
-    const float b0 = BT ? pb[2 * kk] : pb[2 * kk * SLB];
-    const float b1 = BT ? pb[2 * kk + 2] : pb[(2 * kk + 2) * SLB];
+    const float b0 = pb[2 * kk], b1 = pb[2 * kk + 2];
     acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc0, 0, 0, 0);
     acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc1, 0, 0, 0);
   }
