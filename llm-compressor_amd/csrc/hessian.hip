@@ -17,8 +17,11 @@
 //    transposed stores map lane -> (feature block, token block) with the
 //    token block fastest, which keeps 16 consecutive lanes on distinct LDS
 //    banks (row stride 144 B = 9 x 16 B).
-// Tiles are TM x TM (TM = 256 for d >= 512, else 128) on a 2 x 2 grid of
-// waves; each wave owns a (TM/2)^2 block of 32 x 32 MFMA tiles.
+// Tiles are TM x TM (TM = 256 for d >= 512, else 128).  syrk_bf16_kernel runs
+// them on a 2 x 2 grid of waves, each owning a (TM/2)^2 block of 32 x 32 MFMA
+// tiles; the streaming kernel on a 2 x 4 grid of 8 waves (two per SIMD, so
+// one wave's waits are covered by the other's MFMAs), each owning 128 x 64.
+// Partial tiles are written in the 2 x 2 layout's fragment order either way.
 //
 // Work decomposition: a work item is (matrix e, upper tile t, token split s).
 // Token splits are assigned by blockIdx % S, and workgroups are dispatched
@@ -340,6 +343,7 @@ constexpr int SK = 32;           // tokens per stage
 constexpr int NSTG = 4;          // stages in the LDS ring
 constexpr int SROW = 512;        // bytes per token row of a 256-feature operand
 constexpr int SOP = SK * SROW;   // bytes per operand per stage
+constexpr int SNT = 512;         // threads of the streaming kernel: 8 waves, 2 per SIMD
 
 typedef short v4s16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s16_t lds_v4s16_t;
@@ -353,7 +357,8 @@ __device__ __forceinline__ bf16x8_t tr_pair(const char* lds, int off0, int off1)
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-__global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
+__global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
+  constexpr int MB = 4, NBN = 2;  // 32 x 32 MFMA blocks per wave: 128 rows x 64 columns
   using C = Cfg<256>;
   constexpr int TM = 256;
   __shared__ __attribute__((aligned(1024))) char a0[SOP], a1[SOP], a2[SOP], a3[SOP];
@@ -362,7 +367,7 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
 
   // work item: tile t, token split s (and, for tail tiles, part `part` of
   // tail_f equal pieces of that split), partial slot
@@ -402,16 +407,16 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   }
   const int64_t nst = st_end > st_begin ? st_end - st_begin : 0;
 
-  // DMA roles: wave w copies token rows 8 w .. 8 w + 7 of each operand, two
+  // DMA roles: wave w copies token rows 4 w .. 4 w + 3 of each operand, two
   // rows (1 KB) per instruction j; lane L fills LDS position L & 31 of row
-  // 8 w + 2 j + L / 32 with global chunk (L & 31) ^ 4 (row & 3).
+  // 4 w + 2 j + L / 32 with global chunk (L & 31) ^ 4 (row & 3).
   const int64_t fa0 = (int64_t)ti * TM, fb0 = (int64_t)tj * TM;
   const bool edge = fa0 + TM > p.d || fb0 + TM > p.d;
-  uint32_t doff[4];    // lane byte offsets from the stage's first token row
-  int drow[4], dchunk[4];
+  uint32_t doff[2];    // lane byte offsets from the stage's first token row
+  int drow[2], dchunk[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = 8 * wave + 2 * j + (lane >> 5);
+  for (int j = 0; j < 2; ++j) {
+    const int row = 4 * wave + 2 * j + (lane >> 5);
     const int chunk = (lane & 31) ^ (4 * (row & 3));
     drow[j] = row;
     dchunk[j] = chunk;
@@ -426,7 +431,7 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   // zero chunk with per-lane 64-bit addresses.  M0 (the LDS destination of
   // the wave's 1 KB) is formed in scalar registers.
   auto lds_u32 = [](const char* ptr) { return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)ptr); };
-  const uint32_t wave_lds = (uint32_t)wave * 4096u;
+  const uint32_t wave_lds = (uint32_t)wave * 2048u;
   const uint32_t sa[4] = {lds_u32(a0) + wave_lds, lds_u32(a1) + wave_lds, lds_u32(a2) + wave_lds,
                           lds_u32(a3) + wave_lds};
   const uint32_t sb[4] = {lds_u32(b0) + wave_lds, lds_u32(b1) + wave_lds, lds_u32(b2) + wave_lds,
@@ -449,7 +454,7 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
     const char* xb = xs + fb0 * 2;
     if (!edge && sc < nwhole) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         dma_s(doff[j], xa, sa[slot] + 1024u * j);
         dma_s(doff[j], xb, sb[slot] + 1024u * j);
       }
@@ -457,7 +462,7 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
       // partial stage or edge tile: rows past n and chunks past d read zeros
       const int64_t t0 = (st_begin + sc) * SK;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         const bool rok = t0 + drow[j] < n;
         const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
         const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
@@ -469,22 +474,21 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
 
   // transposed-read lane offsets: lane 16 g + 4 e + q supplies row
   // 8 (g >> 1) + e (+ 16 kk + 4 h) and features 16 (g & 1) + 4 q of the
-  // 32-feature block; with the swizzle the 16-byte position of block b of
-  // wave half w is 16 w + 4 (b ^ e) + 2 (g & 1) + (q >> 1)
+  // 32-feature block; with the swizzle the 16-byte position of 32-feature
+  // block B of the row is 4 (B ^ e) + 2 (g & 1) + (q >> 1)
   const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
   const int rbase = (8 * (g >> 1) + e) * SROW + 8 * (q & 1);
-  int ra[C::NB], rb[C::NB];
+  int ra[MB], rb[NBN];
 #pragma unroll
-  for (int b = 0; b < C::NB; ++b) {
-    ra[b] = rbase + 16 * (16 * wm + 4 * (b ^ e) + 2 * (g & 1) + (q >> 1));
-    rb[b] = rbase + 16 * (16 * wn + 4 * (b ^ e) + 2 * (g & 1) + (q >> 1));
-  }
+  for (int b = 0; b < MB; ++b) ra[b] = rbase + 16 * (4 * ((MB * wm + b) ^ e) + 2 * (g & 1) + (q >> 1));
+#pragma unroll
+  for (int b = 0; b < NBN; ++b) rb[b] = rbase + 16 * (4 * ((NBN * wn + b) ^ e) + 2 * (g & 1) + (q >> 1));
 
-  f32x16_t acc[C::NB][C::NB];
+  f32x16_t acc[MB][NBN];
 #pragma unroll
-  for (int x = 0; x < C::NB; ++x)
+  for (int x = 0; x < MB; ++x)
 #pragma unroll
-    for (int y = 0; y < C::NB; ++y)
+    for (int y = 0; y < NBN; ++y)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
 
@@ -493,32 +497,32 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   // the stage boundary, so the barrier that publishes stage st + 1 sits in
   // the middle of stage st (between its two steps) and the MFMA pipe does not
   // drain at stage boundaries.  F0 / F1 hold the operands of step 0 / step 1.
-  bf16x8_t fa0r[C::NB], fb0r[C::NB], fa1r[C::NB], fb1r[C::NB];
+  bf16x8_t fa0r[MB], fb0r[NBN], fa1r[MB], fb1r[NBN];
   auto read_op = [&](const char* la, const char* lb, int kk, int i, bf16x8_t* fa, bf16x8_t* fb)
       __attribute__((always_inline)) {
-    // operand i of a step: A fragments 0..NB-1, then B fragments
-    if (i < C::NB)
+    // operand i of a step: A fragments 0..MB-1, then B fragments
+    if (i < MB)
       fa[i] = tr_pair(la, ra[i] + kk * 16 * SROW, ra[i] + (kk * 16 + 4) * SROW);
     else
-      fb[i - C::NB] = tr_pair(lb, rb[i - C::NB] + kk * 16 * SROW, rb[i - C::NB] + (kk * 16 + 4) * SROW);
+      fb[i - MB] = tr_pair(lb, rb[i - MB] + kk * 16 * SROW, rb[i - MB] + (kk * 16 + 4) * SROW);
   };
   // MFMAs of one step (operands fa, fb) interleaved with the 2 NB fragment
   // reads of the next step: two tr reads per MFMA for the first NB MFMAs
   auto half = [&](const bf16x8_t* fa, const bf16x8_t* fb, const char* la, const char* lb, int kk, bf16x8_t* na,
                   bf16x8_t* nb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2 * C::NB; ++i) read_op(la, lb, kk, i, na, nb);
+    for (int i = 0; i < MB + NBN; ++i) read_op(la, lb, kk, i, na, nb);
 #pragma unroll
-    for (int x = 0; x < C::NB; ++x)
+    for (int x = 0; x < MB; ++x)
 #pragma unroll
-      for (int y = 0; y < C::NB; ++y)
+      for (int y = 0; y < NBN; ++y)
         acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[x], fb[y], acc[x][y], 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4 * C::NB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one tr read of the next step
+    for (int i = 0; i < 6; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, C::NB * C::NB - 4 * C::NB, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   };
   // Per-lane global addresses of the 8 DMAs of a stage (A0, B0, A1, B1, ...):
   // whole stages from the stage base; partial stages and edge tiles send the
@@ -530,14 +534,14 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
     const char* xb = xs + fb0 * 2;
     if (!edge && sc < nwhole) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         ad[2 * j] = xa + doff[j];
         ad[2 * j + 1] = xb + doff[j];
       }
     } else {
       const int64_t t0 = (st_begin + sc) * SK;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         const bool rok = t0 + drow[j] < n;
         const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
         const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
@@ -554,14 +558,11 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   auto half_dma = [&](const bf16x8_t* fa, const bf16x8_t* fb, const char* la, const char* lb, int kk, bf16x8_t* na,
                       bf16x8_t* nb, const void* const* ad, int slot) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2 * C::NB; ++i) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int m = 2 * i + h, x = m / C::NB, y = m % C::NB;
-        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[x], fb[y], acc[x][y], 0, 0, 0);
-      }
-      read_op(la, lb, kk, i, na, nb);
-      dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
+    for (int i = 0; i < MB * NBN; ++i) {
+      const int x = i / NBN, y = i % NBN;
+      acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[x], fb[y], acc[x][y], 0, 0, 0);
+      if (i < MB + NBN) read_op(la, lb, kk, i, na, nb);
+      if (i < 4) dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -573,10 +574,10 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   // for the DMA of stage st + 2.)
   auto stage = [&](int64_t st, int cur, const char* la, const char* lb, const char* lan, const char* lbn)
       __attribute__((always_inline)) {
-    const void* ad[8];
+    const void* ad[4];
     dma_addrs(st + 3, ad);
     half(fa0r, fb0r, la, lb, 1, fa1r, fb1r);
-    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
     half_dma(fa1r, fb1r, lan, lbn, 0, fa0r, fb0r, ad, (cur + 3) & 3);
   };
 
@@ -584,9 +585,9 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
     issue(0, 0);
     issue(1, 1);
     issue(2, 2);
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 2 * C::NB; ++i) read_op(a0, b0, 0, i, fa0r, fb0r);
+    for (int i = 0; i < MB + NBN; ++i) read_op(a0, b0, 0, i, fa0r, fb0r);
     for (int64_t st = 0; st < nst; st += 4) {
       stage(st, 0, a0, b0, a1, b1);
       if (st + 1 < nst) stage(st + 1, 1, a1, b1, a2, b2);
@@ -600,15 +601,18 @@ __global__ __launch_bounds__(NT, 1) void syrk_stream_kernel(SyrkParams p) {
   // directly, take syrk_bf16_kernel: the direct update's registers next to
   // 256 live accumulators would spill here)
   if (slot < 0) return;
-  float* dst = p.ws + (slot * NT + tid) * C::ACC;
+  // slot in the fragment order of the 2 x 2 layout (the reduction's): wave
+  // (wm, wn >> 1), block (x, 2 (wn & 1) + y)
+  const int tid4 = (wm * 2 + (wn >> 1)) * 64 + lane;
+  float* dst = p.ws + (slot * NT + tid4) * C::ACC;
 #pragma unroll
-  for (int x = 0; x < C::NB; ++x)
+  for (int x = 0; x < MB; ++x)
 #pragma unroll
-    for (int y = 0; y < C::NB; ++y)
+    for (int y = 0; y < NBN; ++y)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         f32x4_t v = {acc[x][y][4 * r4], acc[x][y][4 * r4 + 1], acc[x][y][4 * r4 + 2], acc[x][y][4 * r4 + 3]};
-        *reinterpret_cast<f32x4_t*>(dst + (x * C::NB + y) * 16 + 4 * r4) = v;
+        *reinterpret_cast<f32x4_t*>(dst + (x * C::NB + 2 * (wn & 1) + y) * 16 + 4 * r4) = v;
       }
 }
 
@@ -761,7 +765,7 @@ void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) 
   if (tile_edge(d) == 256) {
     if (g)             hipLaunchKernelGGL((syrk_bf16_kernel<256, true>), dim3(grid), dim3(NT), 0, st, p);
     else if (p.S == 1) hipLaunchKernelGGL((syrk_bf16_kernel<256, false>), dim3(grid), dim3(NT), 0, st, p);
-    else               hipLaunchKernelGGL(syrk_stream_kernel, dim3(grid), dim3(NT), 0, st, p);
+    else               hipLaunchKernelGGL(syrk_stream_kernel, dim3(grid), dim3(SNT), 0, st, p);
   } else {
     if (g) hipLaunchKernelGGL((syrk_bf16_kernel<128, true>), dim3(grid), dim3(NT), 0, st, p);
     else   hipLaunchKernelGGL((syrk_bf16_kernel<128, false>), dim3(grid), dim3(NT), 0, st, p);
