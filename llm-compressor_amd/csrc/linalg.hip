@@ -503,16 +503,21 @@ __device__ __forceinline__ f32x4_t zero4() {
 // the triangular inverse) and the off-diagonal panels.
 //
 // The block is processed in 32-wide steps.  Wave 0 factors the 32 x 32
-// diagonal sub-block in registers and inverts it on the way; then all four
-// waves apply the sub-block inverse to the panel below and update the
-// trailing lower triangle with fp32 MFMA (16 x 16 tiles).  The block inverse
-// is assembled from the four sub-block inverses by two doubling steps,
-// inv([[A,0],[B,C]]) = [[A^-1,0],[-C^-1 B A^-1, C^-1]].
+// diagonal sub-block in registers and inverts it on the way; all four waves
+// apply the sub-block inverse to the panel below, and the trailing lower
+// triangle is updated with fp32 MFMA (16 x 16 tiles), the next diagonal
+// sub-block first so that its factorisation overlaps the rest.  The block
+// inverse is assembled from the four sub-block inverses by two doubling
+// steps, inv([[A,0],[B,C]]) = [[A^-1,0],[-C^-1 B A^-1, C^-1]], partly under
+// the last factorisations.
 __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t ldf, int64_t k0, int nb,
                                                         float* linv, int32_t* status, int64_t wsf) {
   __shared__ float a[NB * LP];
   __shared__ float x[NB * LP];
-  __shared__ __attribute__((aligned(16))) float t[2 * SB * LT];
+  // product scratch: rows 0..63 the first level-2 product (and, earlier, the
+  // pair (0, 1) in rows 32..63), rows 64..95 the pair (2, 3)
+  __shared__ __attribute__((aligned(16))) float t[3 * SB * LT];
+  __shared__ __attribute__((aligned(16))) float cb[2 * SB];  // column broadcast of the factorisation
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // matrix blockIdx.x of a batch: workspaces wsf floats apart
   F += (int64_t)blockIdx.x * wsf;
@@ -554,65 +559,118 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
   // pivot checks, off the dependency chain: min over the pivots and a
   // running sum of (piv - piv), NaN once any pivot is inf or NaN
   float pmin = 1.f, pnan = 0.f;
+
+  // Factor + invert the 32 x 32 diagonal sub-block at o (wave 0 only).
+  // Lanes 0..31 hold the rows of the sub-block (row role), lanes 32..63 the
+  // columns of its inverse (column role): v = row li of A, or column li of
+  // X = L^-1, initially e_li.  Right-looking Cholesky and the inverse's row
+  // elimination (X[j][:] /= L[j][j]; X[i][:] -= L[i][j] X[j][:], i > j)
+  // advance together, and with col = A[:, j] before scaling both take the
+  // same form:
+  //   m = v[j] / piv;  v[k] -= m col[k] (k > j);  v[j] /= L[j][j]
+  // Column j reaches every lane through one LDS write and broadcast reads (a
+  // wave's LDS operations complete in program order, so no barrier is
+  // needed).  Entries above the diagonal are updated too and never used,
+  // which keeps every update unpredicated.
+  //
+  // The column loop is latency-bound (one wave, 128 sequential steps per
+  // block), so its dependency chain is kept short: rl = 1 / L[j][j] straight
+  // from the hardware reciprocal square root (within 1 ulp), and the column
+  // is scaled by the reciprocal, as LAPACK's potf2 scales it (dscal by
+  // 1 / ajj).
+  auto factor = [&](int o) __attribute__((always_inline)) {
+    const int li = lane & 31;
+    const bool row_role = lane < SB;
+    float v[SB];
+#pragma unroll
+    for (int c = 0; c < SB; ++c) v[c] = row_role ? a[(o + li) * LP + o + c] : ((c == li) ? 1.f : 0.f);
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      // every lane stores (column-role lanes into a scratch slot): no
+      // divergent branch around the LDS write that the reads could sink into
+      cb[lane] = v[j];
+      // only col[j..SB-1] is used: read the aligned quads that cover it
+      float col[SB];
+#pragma unroll
+      for (int q = j / 4; q < SB / 4; ++q) {
+        const f32x4_t w = *reinterpret_cast<const f32x4_t*>(cb + 4 * q);
+        col[4 * q] = w[0];
+        col[4 * q + 1] = w[1];
+        col[4 * q + 2] = w[2];
+        col[4 * q + 3] = w[3];
+      }
+      const float piv = col[j];
+      pmin = fminf(pmin, piv);
+      pnan += piv - piv;
+      const float rl = __builtin_amdgcn_rsqf(piv);
+      const float sj = v[j] * rl;
+      const float m = sj * rl;
+#pragma unroll
+      for (int k = j + 1; k < SB; ++k) v[k] = fmaf(-m, col[k], v[k]);
+      v[j] = sj;
+    }
+    // column li of the sub-block inverse, zeros above the diagonal included
+    if (!row_role) {
+#pragma unroll
+      for (int i = 0; i < SB; ++i) x[(o + i) * LP + o + li] = v[i];
+    }
+  };
+  // trailing tile tt (16 x 16, lower triangle of the region below / right of
+  // sub-block o, enumerated row by row): A[ti][tj] -= P_ti P_tj^T
+  auto trailing_tile = [&](int o, int tt) __attribute__((always_inline)) {
+    const int rb = o + SB;
+    int ti = 0, rem = tt;
+    while (rem > ti) { rem -= ti + 1; ++ti; }
+    const int tj = rem;
+    float* cp = a + (rb + 16 * ti) * LP + rb + 16 * tj;
+    f32x4_t acc = tile16_load(cp, LP, lane);
+    mfma16_tile(acc, a + (rb + 16 * ti) * LP + o, LP, a + (rb + 16 * tj) * LP + o, LP, true, 0, SB, lane, -1.f);
+    tile16_store(acc, cp, LP, lane);
+  };
+  // one wave: X[c0][a0] = -X[c0][c0] L[c0][a0] X[a0][a0] for the 32-wide pair
+  // (a0, c0 = a0 + 32), through T (32 x 32 at tp); the wave's own LDS writes
+  // and reads stay in program order
+  auto pair_one_wave = [&](int a0, float* tp) __attribute__((always_inline)) {
+    const int c0 = a0 + SB;
+#pragma unroll
+    for (int tr = 0; tr < 2; ++tr) {
+      const float* A = a + (c0 + 16 * tr) * LP + a0;
+      f32x4_t acc0 = zero4(), acc1 = zero4();
+      mfma16_tile(acc0, A, LP, x + a0 * LP + a0, LP, false, 0, SB, lane, 1.f);
+      mfma16_tile(acc1, A, LP, x + a0 * LP + a0 + 16, LP, false, 16, SB, lane, 1.f);
+      tile16_store(acc0, tp + 16 * tr * LT, LT, lane);
+      tile16_store(acc1, tp + 16 * tr * LT + 16, LT, lane);
+    }
+#pragma unroll
+    for (int tc = 0; tc < 2; ++tc) {
+      f32x4_t acc0 = zero4(), acc1 = zero4();
+      mfma16_tile(acc0, x + c0 * LP + c0, LP, tp + 16 * tc, LT, false, 0, 16, lane, -1.f);
+      mfma16_tile(acc1, x + (c0 + 16) * LP + c0, LP, tp + 16 * tc, LT, false, 0, SB, lane, -1.f);
+      tile16_store(acc0, x + c0 * LP + a0 + 16 * tc, LP, lane);
+      tile16_store(acc1, x + (c0 + 16) * LP + a0 + 16 * tc, LP, lane);
+    }
+  };
+  // level-2 first product, row strip r: T2[16 r..][0:64] = L[64 + 16 r..][0:64] X[0:64][0:64]
+  auto level2_strip = [&](int r) __attribute__((always_inline)) {
+    const float* A = a + (2 * SB + 16 * r) * LP;
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc) {
+      f32x4_t acc = zero4();
+      mfma16_tile(acc, A, LP, x + 16 * tc, LP, false, 16 * tc, 2 * SB, lane, 1.f);
+      tile16_store(acc, t + 16 * r * LT + 16 * tc, LT, lane);
+    }
+  };
+
+  // Lookahead: after the panel of sub-block kb, the three 16 x 16 trailing
+  // tiles that form the next diagonal sub-block are updated first; then
+  // wave 0 factors sub-block kb + 1 while waves 1..3 finish the trailing
+  // update of kb and the inverse products whose inputs are complete (the
+  // pair (0, 1) during factor 2, the first level-2 product during factor 3).
+  if (wave == 0) factor(0);
+  __syncthreads();
 #pragma unroll 1
   for (int kb = 0; kb < NB / SB; ++kb) {
     const int o = kb * SB;
-    if (wave == 0) {
-      // Lanes 0..31 hold the rows of the sub-block (row role), lanes 32..63
-      // the columns of its inverse (column role): v = row li of A, or column
-      // li of X = L^-1, initially e_li.  Right-looking Cholesky and the
-      // inverse's row elimination (X[j][:] /= L[j][j]; X[i][:] -= L[i][j]
-      // X[j][:], i > j) advance together, and with col = A[:, j] before
-      // scaling both take the same form:
-      //   m = v[j] / piv;  v[k] -= m col[k] (k > j);  v[j] /= L[j][j]
-      // Column j reaches every lane through one LDS write and broadcast
-      // reads (a wave's LDS operations complete in program order, so no
-      // barrier is needed).  Entries above the diagonal are updated too and
-      // never used, which keeps every update unpredicated.
-      //
-      // The column loop is latency-bound (one wave, 128 sequential steps), so
-      // its dependency chain is kept short: rl = 1 / L[j][j] straight from the
-      // hardware reciprocal square root (within 1 ulp), and the column is
-      // scaled by the reciprocal, as LAPACK's potf2 scales it (dscal by
-      // 1 / ajj).
-      const int li = lane & 31;
-      const bool row_role = lane < SB;
-      float* cb = t;  // column buffer: cb[0..31] = column j (t is idle during the factorisation)
-      float v[SB];
-#pragma unroll
-      for (int c = 0; c < SB; ++c) v[c] = row_role ? a[(o + li) * LP + o + c] : ((c == li) ? 1.f : 0.f);
-#pragma unroll
-      for (int j = 0; j < SB; ++j) {
-        // every lane stores (column-role lanes into a scratch slot): no
-        // divergent branch around the LDS write that the reads could sink into
-        cb[lane] = v[j];
-        // only col[j..SB-1] is used: read the aligned quads that cover it
-        float col[SB];
-#pragma unroll
-        for (int q = j / 4; q < SB / 4; ++q) {
-          const f32x4_t w = *reinterpret_cast<const f32x4_t*>(cb + 4 * q);
-          col[4 * q] = w[0];
-          col[4 * q + 1] = w[1];
-          col[4 * q + 2] = w[2];
-          col[4 * q + 3] = w[3];
-        }
-        const float piv = col[j];
-        pmin = fminf(pmin, piv);
-        pnan += piv - piv;
-        const float rl = __builtin_amdgcn_rsqf(piv);
-        const float sj = v[j] * rl;
-        const float m = sj * rl;
-#pragma unroll
-        for (int k = j + 1; k < SB; ++k) v[k] = fmaf(-m, col[k], v[k]);
-        v[j] = sj;
-      }
-      // column li of the sub-block inverse, zeros above the diagonal included
-      if (!row_role) {
-#pragma unroll
-        for (int i = 0; i < SB; ++i) x[(o + i) * LP + o + li] = v[i];
-      }
-    }
-    __syncthreads();
     // panel below the sub-block: P = A_panel Xd^T in place, 16 rows per unit
     // (both column tiles of a unit in one wave, read before written);
     // Xd^T is upper triangular, so column tile c needs k < 16 (c + 1)
@@ -626,55 +684,46 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
       tile16_store(acc1, ap + 16, LP, lane);
     }
     __syncthreads();
-    // trailing lower tiles: A[ti][tj] -= P_ti P_tj^T for tj <= ti
-    const int nt = R / 16, ntt = nt * (nt + 1) / 2, rb = o + SB;
-    for (int tt = wave; tt < ntt; tt += PNT / 64) {
-      int ti = 0, rem = tt;
-      while (rem > ti) { rem -= ti + 1; ++ti; }
-      const int tj = rem;
-      float* cp = a + (rb + 16 * ti) * LP + rb + 16 * tj;
-      f32x4_t acc = tile16_load(cp, LP, lane);
-      mfma16_tile(acc, a + (rb + 16 * ti) * LP + o, LP, a + (rb + 16 * tj) * LP + o, LP, true, 0, SB, lane, -1.f);
-      tile16_store(acc, cp, LP, lane);
+    if (kb + 1 == NB / SB) break;
+    // the next diagonal sub-block: trailing tiles 0, 1, 2
+    if (wave < 3) trailing_tile(o, wave);
+    __syncthreads();
+    const int nt = R / 16, ntt = nt * (nt + 1) / 2;
+    if (wave == 0) {
+      factor(o + SB);
+    } else if (kb == 1 && wave == 3) {
+      pair_one_wave(0, t + 2 * SB * LT - SB * LT);  // T of pair (0, 1) in rows 32..63 of t
+    } else {
+      const int nw = kb == 1 ? 2 : 3;             // waves 1..nw share the remaining tiles
+      for (int tt = 3 + (wave - 1); tt < ntt; tt += nw) trailing_tile(o, tt);
+      if (kb == 2) {
+        // first level-2 product, row strips 0..3 over waves 1..3
+        level2_strip(wave - 1);
+        if (wave == 1) level2_strip(3);
+      }
     }
     __syncthreads();
   }
   if (wave == 0 && lane == 0 && status && !(pmin > 0.f && pnan == 0.f)) *status = MI355Q_NOT_POSITIVE_DEFINITE;
 
-  // block inverse from the four 32 x 32 inverses
-  // level 1, pairs p = 0, 1 (a0 = 64 p, c0 = a0 + 32): T_p = L[c0][a0] X[a0][a0]
+  // pair (2, 3): T_1 = L[96:128][64:96] X[64:96][64:96]; X[96:128][64:96] = -X[96:128][96:128] T_1
   {
-    const int p = wave >> 1, tr = wave & 1, a0 = 2 * SB * p, c0 = a0 + SB;
-    const float* A = a + (c0 + 16 * tr) * LP + a0;
-    f32x4_t acc0 = zero4(), acc1 = zero4();
-    mfma16_tile(acc0, A, LP, x + a0 * LP + a0, LP, false, 0, SB, lane, 1.f);
-    mfma16_tile(acc1, A, LP, x + a0 * LP + a0 + 16, LP, false, 16, SB, lane, 1.f);
-    tile16_store(acc0, t + (SB * p + 16 * tr) * LT, LT, lane);
-    tile16_store(acc1, t + (SB * p + 16 * tr) * LT + 16, LT, lane);
+    const int tr = wave >> 1, tc = wave & 1;
+    f32x4_t acc = zero4();
+    mfma16_tile(acc, a + (3 * SB + 16 * tr) * LP + 2 * SB, LP, x + 2 * SB * LP + 2 * SB + 16 * tc, LP, false,
+                16 * tc, SB, lane, 1.f);
+    tile16_store(acc, t + (2 * SB + 16 * tr) * LT + 16 * tc, LT, lane);
   }
   __syncthreads();
-  // X[c0][a0] = -X[c0][c0] T_p
   {
-    const int p = wave >> 1, tc = wave & 1, a0 = 2 * SB * p, c0 = a0 + SB;
-    f32x4_t acc0 = zero4(), acc1 = zero4();
-    mfma16_tile(acc0, x + c0 * LP + c0, LP, t + SB * p * LT + 16 * tc, LT, false, 0, 16, lane, -1.f);
-    mfma16_tile(acc1, x + (c0 + 16) * LP + c0, LP, t + SB * p * LT + 16 * tc, LT, false, 0, SB, lane, -1.f);
-    tile16_store(acc0, x + c0 * LP + a0 + 16 * tc, LP, lane);
-    tile16_store(acc1, x + (c0 + 16) * LP + a0 + 16 * tc, LP, lane);
+    const int tr = wave >> 1, tc = wave & 1;
+    f32x4_t acc = zero4();
+    mfma16_tile(acc, x + (3 * SB + 16 * tr) * LP + 3 * SB, LP, t + 2 * SB * LT + 16 * tc, LT, false, 0,
+                16 * (tr + 1), lane, -1.f);
+    tile16_store(acc, x + (3 * SB + 16 * tr) * LP + 2 * SB + 16 * tc, LP, lane);
   }
   __syncthreads();
-  // level 2: T = L[64:128][0:64] X[0:64][0:64], one 16-row strip per wave
-  {
-    const float* A = a + (2 * SB + 16 * wave) * LP;
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc) {
-      f32x4_t acc = zero4();
-      mfma16_tile(acc, A, LP, x + 16 * tc, LP, false, 16 * tc, 2 * SB, lane, 1.f);
-      tile16_store(acc, t + 16 * wave * LT + 16 * tc, LT, lane);
-    }
-  }
-  __syncthreads();
-  // X[64:128][0:64] = -X[64:128][64:128] T, one 16-column strip per wave
+  // X[64:128][0:64] = -X[64:128][64:128] T2, one 16-column strip per wave
   {
 #pragma unroll
     for (int tr = 0; tr < 4; ++tr) {
