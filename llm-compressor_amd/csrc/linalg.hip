@@ -661,6 +661,19 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
     }
   };
 
+  // rows r0 .. r0 + 63 of L^-1 to linv, zeros above the diagonal, by `nthr`
+  // threads (thread index q): float4 v covers row r0 + v nthr / 32 + q / 32,
+  // columns 4 (q % 32) .. + 3
+  auto store_rows = [&](int r0, int q, int nthr) __attribute__((always_inline)) {
+    const int j = 4 * (q & 31);
+    for (int i = r0 + (q >> 5); i < r0 + 2 * SB; i += nthr / 32) {
+      f32x4_t o4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o4[c] = (j + c <= i) ? x[i * LP + j + c] : 0.f;
+      *reinterpret_cast<f32x4_t*>(linv + i * NB + j) = o4;
+    }
+  };
+
   // Lookahead: after the panel of sub-block kb, the three 16 x 16 trailing
   // tiles that form the next diagonal sub-block are updated first; then
   // wave 0 factors sub-block kb + 1 while waves 1..3 finish the trailing
@@ -697,9 +710,11 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
       const int nw = kb == 1 ? 2 : 3;             // waves 1..nw share the remaining tiles
       for (int tt = 3 + (wave - 1); tt < ntt; tt += nw) trailing_tile(o, tt);
       if (kb == 2) {
-        // first level-2 product, row strips 0..3 over waves 1..3
+        // first level-2 product, row strips 0..3 over waves 1..3; waves 2
+        // and 3 then store rows 0..63 of L^-1, final since the pair (0, 1)
         level2_strip(wave - 1);
         if (wave == 1) level2_strip(3);
+        else store_rows(0, tid - 128, 128);
       }
     }
     __syncthreads();
@@ -723,30 +738,31 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
     tile16_store(acc, x + (3 * SB + 16 * tr) * LP + 2 * SB + 16 * tc, LP, lane);
   }
   __syncthreads();
-  // X[64:128][0:64] = -X[64:128][64:128] T2, one 16-column strip per wave
+  // X[64:128][0:64] = -X[64:128][64:128] T2, one 16-column strip per wave:
+  // row tile tr needs k < 16 (tr + 1); the B values of a k step are shared
+  // by the row tiles and the four accumulators interleave
   {
+    const int r = lane & 15, kq = lane >> 4;
+    f32x4_t acc[4];
 #pragma unroll
-    for (int tr = 0; tr < 4; ++tr) {
-      f32x4_t acc = zero4();
-      mfma16_tile(acc, x + (2 * SB + 16 * tr) * LP + 2 * SB, LP, t + 16 * wave, LT, false, 0, 16 * (tr + 1), lane,
-                  -1.f);
-      tile16_store(acc, x + (2 * SB + 16 * tr) * LP + 16 * wave, LP, lane);
+    for (int tr = 0; tr < 4; ++tr) acc[tr] = zero4();
+#pragma unroll
+    for (int k4 = 0; k4 < 16; ++k4) {
+      const int k = 4 * k4 + kq;
+      const float bv = t[k * LT + 16 * wave + r];
+#pragma unroll
+      for (int tr = k4 / 4; tr < 4; ++tr) {
+        const float av = -x[(2 * SB + 16 * tr + r) * LP + 2 * SB + k];
+        acc[tr] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[tr], 0, 0, 0);
+      }
     }
+#pragma unroll
+    for (int tr = 0; tr < 4; ++tr) tile16_store(acc[tr], x + (2 * SB + 16 * tr) * LP + 16 * wave, LP, lane);
   }
   __syncthreads();
 
-  // store L^-1, zeros above the diagonal: rows 8 v + tid / 32, columns 4 (tid % 32) .. + 3
-  {
-    const int i0 = tid >> 5, j = 4 * (tid & 31);
-#pragma unroll
-    for (int v = 0; v < NB * NB / (4 * PNT); ++v) {
-      const int i = 8 * v + i0;
-      f32x4_t o4;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) o4[c] = (j + c <= i) ? x[i * LP + j + c] : 0.f;
-      *reinterpret_cast<f32x4_t*>(linv + i * NB + j) = o4;
-    }
-  }
+  // rows 64..127 of L^-1 (rows 0..63 went out during the last factorisation)
+  store_rows(2 * SB, tid, PNT);
 }
 
 // diag'[j] = H[p(j)][p(j)] / n with 0 -> 1 (dead), damp = percdamp * mean(diag')
