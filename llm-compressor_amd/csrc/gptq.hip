@@ -66,13 +66,18 @@ __device__ __forceinline__ float row_bcast(float v) {
 }
 
 // CT quantize / dequantize of one value: qq = clamp(rint(x / s + z)),
-// deq = (qq - z) * s, rounded to bf16 when the scale is bf16.
-__device__ __forceinline__ void quant1(float x, float s, float rs, float z, float qmin, float qmax, bool dq_bf16,
-                                       float& qq, float& deq) {
-  qq = div_by_recip(x, s, rs) + z;
+// deq = (qq - z) * s, rounded to bf16 when the scale is bf16 (BF16).  ZP:
+// a zero point (asymmetric); without one, z = 0 and the additions drop out
+// (x + 0 = x, and the sign of a zero quotient changes neither the code nor
+// the error).
+template <bool BF16, bool ZP>
+__device__ __forceinline__ void quant1(float x, float s, float rs, float z, float qmin, float qmax, float& qq,
+                                       float& deq) {
+  qq = div_by_recip(x, s, rs);
+  if (ZP) qq = qq + z;
   qq = rintf(fminf(fmaxf(qq, qmin), qmax));
-  deq = (qq - z) * s;
-  if (dq_bf16) deq = bf16_rne(deq);
+  deq = (ZP ? qq - z : qq) * s;
+  if (BF16) deq = bf16_rne(deq);
 }
 
 // One column of the sweep: column I = SW_G * TO + GO, owned by lane GO of
@@ -81,15 +86,15 @@ __device__ __forceinline__ void quant1(float x, float s, float rs, float z, floa
 // the row, and each lane updates its later columns.  A lane's slot is final
 // from its own step on, so its code, dequantised value and error are
 // recomputed once after the sweep instead of being selected at every step.
-template <int TO, int GO, bool FULL>
+template <int TO, int GO, bool FULL, bool BF16, bool ZP>
 __device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, const float* rdg, int g, int count,
-                                           float qmin, float qmax, bool dq_bf16) {
+                                           float qmin, float qmax) {
   constexpr int I = SW_G * TO + GO;
   if (!FULL && I >= count) return;
   const float dd = h1[hrow(I)];
   const float x = S.w[TO];
   float qq, deq;
-  quant1(x, S.s[TO], S.rs[TO], S.z[TO], qmin, qmax, dq_bf16, qq, deq);
+  quant1<BF16, ZP>(x, S.s[TO], S.rs[TO], S.z[TO], qmin, qmax, qq, deq);
   const float err = div_by_recip(x - deq, dd, rdg[I]);
   const float e = row_bcast<GO>(err);
 #pragma unroll
@@ -106,18 +111,17 @@ __device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, const
   }
 }
 
-template <int I, bool FULL>
+template <int I, bool FULL, bool BF16, bool ZP>
 struct SweepSteps {
   static __device__ __forceinline__ void run(SweepState& S, const float* h1, const float* rdg, int g, int count,
-                                             float qmin, float qmax, bool dq_bf16) {
-    sweep_step<I / SW_G, I % SW_G, FULL>(S, h1, rdg, g, count, qmin, qmax, dq_bf16);
-    SweepSteps<I + 1, FULL>::run(S, h1, rdg, g, count, qmin, qmax, dq_bf16);
+                                             float qmin, float qmax) {
+    sweep_step<I / SW_G, I % SW_G, FULL, BF16, ZP>(S, h1, rdg, g, count, qmin, qmax);
+    SweepSteps<I + 1, FULL, BF16, ZP>::run(S, h1, rdg, g, count, qmin, qmax);
   }
 };
-template <bool FULL>
-struct SweepSteps<MAXB, FULL> {
-  static __device__ __forceinline__ void run(SweepState&, const float*, const float*, int, int, float, float,
-                                             bool) {}
+template <bool FULL, bool BF16, bool ZP>
+struct SweepSteps<MAXB, FULL, BF16, ZP> {
+  static __device__ __forceinline__ void run(SweepState&, const float*, const float*, int, int, float, float) {}
 };
 
 // Element strides between the matrices of a batch (blockIdx.y); zero for a
@@ -126,11 +130,12 @@ struct SweepBatch {
   int64_t w, hinv, scale, gidx, codes, losses, err;
 };
 
-template <bool FULL>
+// FULL: a whole MAXB-column block; BF16: dequantise in bf16; ZP: zero points
+template <bool FULL, bool BF16, bool ZP>
 __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
     int count, const float* __restrict__ scale, const float* __restrict__ zp, int64_t ld_scale,
-    const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax, int dq_bf16,
+    const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax,
     int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, int err_col,
     SweepBatch sb) {
   __shared__ float h1[HPK];
@@ -195,10 +200,10 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     const int64_t si = sbase + gsh[col];
     S.s[t] = scale[si];
     S.rs[t] = 1.f / S.s[t];
-    S.z[t] = zp ? zp[si] : 0.f;
+    S.z[t] = ZP ? zp[si] : 0.f;
   }
 
-  SweepSteps<0, FULL>::run(S, h1, rdg, g, count, qmin, qmax, dq_bf16 != 0);
+  SweepSteps<0, FULL, BF16, ZP>::run(S, h1, rdg, g, count, qmin, qmax);
 
   // each slot is final: its code, dequantised value, error and loss
   float loss = 0.f;
@@ -208,7 +213,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     const int cc = min(col, count - 1);
     const float dd = h1[hrow(cc)];
     float qq, deq;
-    quant1(S.w[t], S.s[t], S.rs[t], S.z[t], qmin, qmax, dq_bf16 != 0, qq, deq);
+    quant1<BF16, ZP>(S.w[t], S.s[t], S.rs[t], S.z[t], qmin, qmax, qq, deq);
     const float diff = S.w[t] - deq;
     const float err = div_by_recip(diff, dd, rdg[cc]);
     if (col < count) {
@@ -295,6 +300,19 @@ inline dim3 grid_rows(int64_t rows, int64_t cols, int64_t batch = 1) {
   return dim3((unsigned)gx, (unsigned)rows, (unsigned)batch);
 }
 
+// the kernel variant for (whole block, bf16 dequantisation, zero points)
+template <class... A>
+void launch_sweep(bool full, bool bf16, bool zp, dim3 grid, hipStream_t st, A... args) {
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(SW_NT), 0, st, args...); };
+  if (full) {
+    if (bf16) zp ? go(sweep_block_kernel<true, true, true>) : go(sweep_block_kernel<true, true, false>);
+    else      zp ? go(sweep_block_kernel<true, false, true>) : go(sweep_block_kernel<true, false, false>);
+  } else {
+    if (bf16) zp ? go(sweep_block_kernel<false, true, true>) : go(sweep_block_kernel<false, true, false>);
+    else      zp ? go(sweep_block_kernel<false, false, true>) : go(sweep_block_kernel<false, false, false>);
+  }
+}
+
 }  // namespace
 }  // namespace mi355q
 
@@ -369,14 +387,9 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
     for (int64_t i1 = s0; i1 < s1; i1 += B) {
       const int64_t i2 = (i1 + B < s1) ? i1 + B : s1;
       const int count = (int)(i2 - i1);
-      if (count == MAXB)
-        hipLaunchKernelGGL(sweep_block_kernel<true>, dim3(nwg, (unsigned)batch), dim3(SW_NT), 0, st, w_work_dev,
-                           rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h,
-                           qmin, qmax, dequant_bf16, codes_dev, losses_dev, err, (int)(i1 - s0), sb);
-      else
-        hipLaunchKernelGGL(sweep_block_kernel<false>, dim3(nwg, (unsigned)batch), dim3(SW_NT), 0, st, w_work_dev,
-                           rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h,
-                           qmin, qmax, dequant_bf16, codes_dev, losses_dev, err, (int)(i1 - s0), sb);
+      launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, dim3(nwg, (unsigned)batch), st, w_work_dev,
+                   rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
+                   qmax, codes_dev, losses_dev, err, (int)(i1 - s0), sb);
       MQ_LAUNCH_CHECK();
       if (i2 < s1) {
         GemmArgs g{};

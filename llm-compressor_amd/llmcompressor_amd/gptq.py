@@ -199,6 +199,8 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
     hinv, dead = prep.hinv, prep.dead
     w_work = ops.gptq_load_weight(W, perm, dead)
     s, z = _qparams_for_sweep(scale, zero_point, strategy)
+    if quant_args.symmetric:
+        z = None  # zero points are 0: the sweep's variant without them
     qmin, qmax = quant_args.q_range()
     bh = quant_args.block_structure[0] if strategy == QuantizationStrategy.BLOCK else 1
     codes, losses = ops.gptq_sweep_(w_work, hinv, s, z, strategy.value, g_idx, qmin, qmax,
@@ -271,7 +273,8 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
     w_work = ops.gptq_load_weight_batched(weights, perm, dead)
     qmin, qmax = quant_args.q_range()
     bh = quant_args.block_structure[0] if strategy == QuantizationStrategy.BLOCK else 1
-    codes, losses = ops.gptq_sweep_batched_(w_work, hinv, scale.to(torch.float32), zero_point.to(torch.float32),
+    codes, losses = ops.gptq_sweep_batched_(w_work, hinv, scale.to(torch.float32),
+                                            None if quant_args.symmetric else zero_point.to(torch.float32),
                                             strategy.value, g_idx, qmin, qmax,
                                             dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize,
                                             block_h=bh)
