@@ -159,12 +159,19 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
   const int64_t rr = live ? r : rows - 1;  // clamped row: every address below is in bounds
 
   SweepState S;
-  // the row's working values first, so they load while the block of Hinv does
+  // every global load is issued before the first LDS store: the row's
+  // working values, this thread's diagonal element and group index, then
+  // the block of Hinv (the diagonal and g_idx loads would otherwise wait
+  // behind the block's stores, a second memory round trip)
 #pragma unroll
   for (int t = 0; t < SW_T; ++t) {
     const int col = min(SW_G * t + g, count - 1);
     S.w[t] = W[rr * cols + i1 + col];
   }
+  const bool uses_gidx = strategy == MI355Q_GROUP || strategy == MI355Q_BLOCK;
+  const int dcol = tid < count ? tid : count - 1;
+  const float diag = hinv[(i1 + dcol) * cols + i1 + dcol];
+  const int gval = uses_gidx ? g_idx[i1 + dcol] : 0;
   if (count == MAXB && (cols & 3) == 0 && (reinterpret_cast<uintptr_t>(hinv) & 15) == 0) {
     f32x4_t hv[MAXB * MAXB / 4 / SW_NT];
 #pragma unroll
@@ -186,9 +193,8 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
       if (j >= i) h1[hrow(i) + j - i] = hinv[(i1 + i) * cols + (i1 + j)];
     }
   }
-  const bool uses_gidx = strategy == MI355Q_GROUP || strategy == MI355Q_BLOCK;
-  if (tid < MAXB) gsh[tid] = (uses_gidx && tid < count) ? g_idx[i1 + tid] : 0;
-  if (tid < MAXB) rdg[tid] = tid < count ? 1.f / hinv[(i1 + tid) * cols + i1 + tid] : 1.f;
+  if (tid < MAXB) gsh[tid] = tid < count ? gval : 0;
+  if (tid < MAXB) rdg[tid] = tid < count ? 1.f / diag : 1.f;
   __syncthreads();
 
   int64_t sbase = 0;
