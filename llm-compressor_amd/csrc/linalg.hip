@@ -949,19 +949,6 @@ int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream)
   });
 }
 
-int syrk_rocblas(float* C, int64_t ldc, const float* P, int64_t ldp, int64_t n, int64_t k, float alpha, float beta,
-                 int64_t batch, int64_t stride, hipStream_t stream) {
-  return with_blas(stream, [&](rocblas_handle h) {
-    return blas_status(
-        batch == 1 ? rocblas_ssyrk(h, rocblas_fill_upper, rocblas_operation_transpose, (rocblas_int)n, (rocblas_int)k,
-                                   &alpha, P, (rocblas_int)ldp, &beta, C, (rocblas_int)ldc)
-                   : rocblas_ssyrk_strided_batched(h, rocblas_fill_upper, rocblas_operation_transpose,
-                                                   (rocblas_int)n, (rocblas_int)k, &alpha, P, (rocblas_int)ldp,
-                                                   stride, &beta, C, (rocblas_int)ldc, stride, (rocblas_int)batch),
-        "rocblas_ssyrk");
-  });
-}
-
 }  // namespace
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
@@ -1101,8 +1088,22 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
     const int64_t rest2 = d - c_end, kk = c_end - c0;
     if (rest2 > 0) {
       if (kk >= 256) {
-        int rc = syrk_rocblas(F + c_end * d + c_end, d, F + c_end * d + c0, d, rest2, kk, -1.f, 1.f, batch, wsf, st);
-        if (rc) return rc;
+        // row strips of 512: strip [r0, r1) takes columns [0, r1) in one
+        // library GEMM (K = kk), the lower triangle plus the upper half of its
+        // diagonal block, which nothing reads (the diagonal-block kernel
+        // masks it).  1.14x the triangle's multiply-adds at the library's
+        // GEMM rate, instead of its syrk at about a third of that rate.
+        constexpr int64_t SW = 512;
+        for (int64_t r0 = 0; r0 < rest2; r0 += SW) {
+          const int64_t r1 = r0 + SW < rest2 ? r0 + SW : rest2;
+          GemmArgs s{};
+          s.A = F + (c_end + r0) * d + c0; s.lda = d; s.strideA = wsf;
+          s.B = F + c_end * d + c0; s.ldb = d; s.strideB = wsf;
+          s.C = F + (c_end + r0) * d + c_end; s.ldc = d; s.strideC = wsf;
+          s.M = r1 - r0; s.N = r1; s.K = kk; s.alpha = -1.f; s.beta = 1.f;
+          int rc = gemm_f32(s, true, (int)batch, st);
+          if (rc) return rc;
+        }
       } else {
         GemmArgs s{};
         s.A = F + c_end * d + c0; s.lda = d; s.strideA = wsf;
