@@ -24,6 +24,7 @@ constexpr int SW_NT = SW_G * SW_ROWS;    // 256 threads
 constexpr int MAXB = 128;                // largest supported block size
 constexpr int SW_T = MAXB / SW_G;        // columns per lane
 constexpr int SUPER = 1024;              // columns per lazy-update super-block
+constexpr int MID = 512;                 // columns per lazy-update mid-block
 constexpr int HPK = MAXB * (MAXB + 1) / 2;  // packed upper triangle of a Hinv block
 
 // Row i of the block's upper triangle starts at hrow(i) in the packed LDS copy
@@ -136,8 +137,8 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
     int count, const float* __restrict__ scale, const float* __restrict__ zp, int64_t ld_scale,
     const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax,
-    int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, int err_col,
-    SweepBatch sb) {
+    int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, int64_t lde,
+    int err_col, SweepBatch sb) {
   __shared__ float h1[HPK];
   __shared__ float rdg[MAXB];  // 1 / Hinv[i][i], correctly rounded
   __shared__ int gsh[MAXB];
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
         const int64_t c = i1 + col;
         W[r * cols + c] = deq;
         codes[r * cols + c] = (int8_t)qq;
-        err_out[r * SUPER + err_col + col] = err;
+        err_out[r * lde + err_col + col] = err;
       }
     }
   }
@@ -346,10 +347,18 @@ extern "C" int mi355q_gptq_load_weight(const void* w_dev, mi355q_dtype w_dtype, 
                                          w_work_dev, stream);
 }
 
+namespace {
+// columns of the error buffer: one super-block of whole blocks, or all columns
+int64_t err_cols(int64_t cols, int64_t blocksize) {
+  const int64_t B = blocksize < MAXB ? blocksize : MAXB;
+  const int64_t sup = (SUPER / B) * B;
+  return sup < cols ? sup : cols;
+}
+}  // namespace
+
 extern "C" size_t mi355q_gptq_sweep_workspace_size(int64_t rows, int64_t cols, int64_t blocksize) {
-  (void)cols;
-  (void)blocksize;
-  return rows > 0 ? (size_t)rows * SUPER * sizeof(float) : 0;
+  if (rows <= 0 || cols <= 0 || blocksize <= 0) return 0;
+  return (size_t)rows * err_cols(cols, blocksize) * sizeof(float);
 }
 
 extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
@@ -374,48 +383,58 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
   MQ_CHECK_ARG(workspace_dev && workspace_bytes >= need, "gptq_sweep: workspace too small");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* err = static_cast<float*>(workspace_dev);
-  SweepBatch sb{rows * cols, stride_hinv, stride_scale, stride_gidx, rows * cols, rows, rows * SUPER};
+  const int64_t lde = err_cols(cols, blocksize);
+  SweepBatch sb{rows * cols, stride_hinv, stride_scale, stride_gidx, rows * cols, rows, rows * lde};
   // the sweep kernel holds at most MAXB columns; larger reference block
   // sizes give the same result up to fp32 rounding of the lazy update, so
   // they are processed in MAXB-wide sub-blocks.
   //
-  // Lazy updates are two-level: inside a super-block of SUPER columns each
-  // block's errors update the rest of the super-block (K = block size, as in
-  // the reference); the columns past the super-block receive the errors of
-  // all its blocks in one GEMM with K up to SUPER.  The far columns thus get
-  // Sum_b Err_b Hinv[b, far] rounded once instead of once per block, an fp32
-  // rounding-order difference of the same kind as a GEMM's summation order.
+  // Lazy updates are three-level: inside a mid-block of MID columns each
+  // block's errors update the rest of the mid-block (K = block size, as in
+  // the reference); the rest of the super-block (SUPER columns) receives a
+  // mid-block's errors in one GEMM (K up to MID), and the columns past the
+  // super-block all its errors in one GEMM (K up to SUPER).  The far columns
+  // thus get Sum_b Err_b Hinv[b, far] rounded once per mid- or super-block
+  // instead of once per block, an fp32 rounding-order difference of the same
+  // kind as a GEMM's summation order; most of the multiply-adds run at the
+  // library GEMM's large-K rate instead of the K = 128 kernel's.
   const int64_t B = blocksize < MAXB ? blocksize : MAXB;
-  const int64_t sup = (SUPER / B) * B;  // whole blocks per super-block: block boundaries as in the reference
+  // whole blocks per mid- and super-block: block boundaries as in the reference
+  const int64_t sup = (SUPER / B) * B, mid = (MID / B) * B;
   const unsigned nwg = (unsigned)((rows + SW_ROWS - 1) / SW_ROWS);
+  // W[:, c0:c1] -= Err[:, k0:k1] Hinv[k0:k1, c0:c1] (errors of super-block s0)
+  auto lazy = [&](int64_t k0, int64_t k1, int64_t s0, int64_t c0, int64_t c1) {
+    GemmArgs g{};
+    g.A = err + (k0 - s0); g.lda = lde; g.strideA = rows * lde;
+    g.B = hinv_dev + k0 * cols + c0; g.ldb = cols; g.strideB = stride_hinv;
+    g.C = w_work_dev + c0; g.ldc = cols; g.strideC = rows * cols;
+    g.M = rows; g.N = c1 - c0; g.K = k1 - k0;
+    g.alpha = -1.f; g.beta = 1.f;
+    return gemm_f32(g, false, (int)batch, st);
+  };
   for (int64_t s0 = 0; s0 < cols; s0 += sup) {
     const int64_t s1 = s0 + sup < cols ? s0 + sup : cols;
-    for (int64_t i1 = s0; i1 < s1; i1 += B) {
-      const int64_t i2 = (i1 + B < s1) ? i1 + B : s1;
-      const int count = (int)(i2 - i1);
-      launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, dim3(nwg, (unsigned)batch), st, w_work_dev,
-                   rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
-                   qmax, codes_dev, losses_dev, err, (int)(i1 - s0), sb);
-      MQ_LAUNCH_CHECK();
-      if (i2 < s1) {
-        GemmArgs g{};
-        g.A = err + (i1 - s0); g.lda = SUPER; g.strideA = rows * SUPER;
-        g.B = hinv_dev + i1 * cols + i2; g.ldb = cols; g.strideB = stride_hinv;
-        g.C = w_work_dev + i2; g.ldc = cols; g.strideC = rows * cols;
-        g.M = rows; g.N = s1 - i2; g.K = count;
-        g.alpha = -1.f; g.beta = 1.f;
-        int rc = gemm_f32(g, false, (int)batch, st);
+    for (int64_t m0 = s0; m0 < s1; m0 += mid) {
+      const int64_t m1 = m0 + mid < s1 ? m0 + mid : s1;
+      for (int64_t i1 = m0; i1 < m1; i1 += B) {
+        const int64_t i2 = (i1 + B < m1) ? i1 + B : m1;
+        const int count = (int)(i2 - i1);
+        launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, dim3(nwg, (unsigned)batch), st,
+                     w_work_dev, rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy,
+                     block_h, qmin, qmax, codes_dev, losses_dev, err, lde, (int)(i1 - s0), sb);
+        MQ_LAUNCH_CHECK();
+        if (i2 < m1) {
+          const int rc = lazy(i1, i2, s0, i2, m1);
+          if (rc) return rc;
+        }
+      }
+      if (m1 < s1) {
+        const int rc = lazy(m0, m1, s0, m1, s1);
         if (rc) return rc;
       }
     }
     if (s1 < cols) {
-      GemmArgs g{};
-      g.A = err; g.lda = SUPER; g.strideA = rows * SUPER;
-      g.B = hinv_dev + s0 * cols + s1; g.ldb = cols; g.strideB = stride_hinv;
-      g.C = w_work_dev + s1; g.ldc = cols; g.strideC = rows * cols;
-      g.M = rows; g.N = cols - s1; g.K = s1 - s0;
-      g.alpha = -1.f; g.beta = 1.f;
-      int rc = gemm_f32(g, false, (int)batch, st);
+      const int rc = lazy(s0, s1, s0, s1, cols);
       if (rc) return rc;
     }
   }

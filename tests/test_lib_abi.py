@@ -35,6 +35,7 @@ def test_version_and_workspace_queries():
     assert lib.mi355q_hessian_workspace_size(131072, 4096) == (128 * 8 + 8 * 8 * 4 + 8 * 8) * 256 * 256 * 4
     assert lib.mi355q_hessian_workspace_size(131072, 384) == 8 * 6 * 128 * 128 * 4
     assert lib.mi355q_gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 1024 * 4   # errors of one 1024-column super-block
+    assert lib.mi355q_gptq_sweep_workspace_size(768, 768, 128) == 768 * 768 * 4       # fewer columns than a super-block
     assert lib.mi355q_gptq_hinv_workspace_size(4096) >= 2 * 4096 * 4096 * 4
 
 
