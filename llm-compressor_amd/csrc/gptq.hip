@@ -250,9 +250,29 @@ __global__ void load_weight_kernel(const void* w, mi355q_dtype dt, int64_t rows,
   if (dead) dead += z * cols;
   out += z * rows * cols;
   const int64_t r = blockIdx.y;
+  // whole rows of bf16 without a permutation: 8-byte loads of four values
+  const bool vec = !perm && dt == MI355Q_BF16 && (cols & 3) == 0 && (ldw & 3) == 0 &&
+                   (reinterpret_cast<uintptr_t>(w) & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(dead) & 15) == 0;
   for (int64_t j4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; j4 < cols;
        j4 += (int64_t)gridDim.x * blockDim.x * 4) {
     f32x4_t v;
+    if (vec) {
+      const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(w) + r * ldw + j4);
+      v[0] = __uint_as_float(u.x << 16);
+      v[1] = __uint_as_float(u.x & 0xffff0000u);
+      v[2] = __uint_as_float(u.y << 16);
+      v[3] = __uint_as_float(u.y & 0xffff0000u);
+      if (dead) {
+        const int4 dd = *reinterpret_cast<const int4*>(dead + j4);
+        if (dd.x) v[0] = 0.f;
+        if (dd.y) v[1] = 0.f;
+        if (dd.z) v[2] = 0.f;
+        if (dd.w) v[3] = 0.f;
+      }
+      *reinterpret_cast<f32x4_t*>(out + r * cols + j4) = v;
+      continue;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int64_t j = j4 + e < cols ? j4 + e : cols - 1;
@@ -283,8 +303,22 @@ __global__ void store_weight_kernel(const float* w, int64_t rows, int64_t cols, 
   if (cin) cin += z * rows * cols;
   if (cout) cout += z * rows * cols;
   const int64_t r = blockIdx.y;
+  // whole rows to bf16 without a permutation: 16-byte loads, 8-byte stores
+  const bool vec = !invperm && dt == MI355Q_BF16 && (cols & 3) == 0 && (ld_out & 3) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 7) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(cin) & 3) == 0 && (reinterpret_cast<uintptr_t>(cout) & 3) == 0;
   for (int64_t j4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; j4 < cols;
        j4 += (int64_t)gridDim.x * blockDim.x * 4) {
+    if (vec) {
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(w + r * cols + j4);
+      uint2 u;
+      u.x = f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+      u.y = f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + r * ld_out + j4) = u;
+      if (cin && cout)
+        *reinterpret_cast<uint32_t*>(cout + r * cols + j4) = *reinterpret_cast<const uint32_t*>(cin + r * cols + j4);
+      continue;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int64_t j = j4 + e;

@@ -802,7 +802,7 @@ __global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t
 // F (lower) = flip(permute(H / n)) with dead / damping rules on the diagonal.
 __global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t sh, int64_t d, const int32_t* perm,
                                     int64_t sp, const float* ns_arr, float ns0, const float* damp, float* F,
-                                    int64_t wsf) {
+                                    int64_t wsf, int vec) {
   const int64_t bm = blockIdx.z;
   H += bm * sh;
   if (perm) perm += bm * sp;
@@ -810,6 +810,27 @@ __global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t sh, int
   F += bm * wsf;
   const float num_samples = ns_arr ? ns_arr[bm] : ns0;
   const int64_t a = (int64_t)blockIdx.y * 16 + threadIdx.y;
+  if (vec) {
+    // (no permutation, d, ldh and the batch stride multiples of 4, H 16-byte
+    // aligned: checked on the host, which sizes the grid for it) four columns per thread: F[a][b4 + e] = H[d-1-a][d-1-b4-e], one
+    // 16-byte load of H's row read backwards (no permutation)
+    const int64_t b4 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * 4;
+    if (a >= d || b4 > a) return;
+    const int64_t ia = d - 1 - a;
+    const f32x4_t h = *reinterpret_cast<const f32x4_t*>(H + ia * ldh + d - 4 - b4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t b = b4 + e;
+      if (b > a) break;
+      float v = h[3 - e] / num_samples;
+      if (a == b) {
+        if (v == 0.f) v = 1.f;
+        v = v + damp[0];
+      }
+      F[a * d + b] = v;
+    }
+    return;
+  }
   const int64_t b = (int64_t)blockIdx.x * 64 + threadIdx.x;
   if (a >= d || b > a) return;
   const int64_t ia = d - 1 - a, ib = d - 1 - b;
@@ -824,10 +845,25 @@ __global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t sh, int
 }
 
 // hinv[a][b] = X[d-1-a][d-1-b] (a <= b), zero below the diagonal.
-__global__ void flip_out_kernel(const float* X, int64_t d, float* hinv, int64_t wsf, int64_t shinv) {
+__global__ void flip_out_kernel(const float* X, int64_t d, float* hinv, int64_t wsf, int64_t shinv, int vec) {
   X += (int64_t)blockIdx.z * wsf;
   hinv += (int64_t)blockIdx.z * shinv;
   const int64_t a = (int64_t)blockIdx.y * 16 + threadIdx.y;
+  if (vec) {
+    // (d and shinv multiples of 4, hinv 16-byte aligned: checked on the host)
+    // four columns per thread: one 16-byte load of X's row read backwards,
+    // one 16-byte store (the load is skipped where all four are below)
+    const int64_t b4 = ((int64_t)blockIdx.x * 64 + threadIdx.x) * 4;
+    if (a >= d || b4 >= d) return;
+    f32x4_t o = {0.f, 0.f, 0.f, 0.f};
+    if (b4 + 3 >= a) {
+      const f32x4_t x = *reinterpret_cast<const f32x4_t*>(X + (d - 1 - a) * d + d - 4 - b4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (a <= b4 + e) ? x[3 - e] : 0.f;
+    }
+    *reinterpret_cast<f32x4_t*>(hinv + a * d + b4) = o;
+    return;
+  }
   const int64_t b = (int64_t)blockIdx.x * 64 + threadIdx.x;
   if (a >= d || b >= d) return;
   hinv[a * d + b] = (a <= b) ? X[(d - 1 - a) * d + (d - 1 - b)] : 0.f;
@@ -835,8 +871,14 @@ __global__ void flip_out_kernel(const float* X, int64_t d, float* hinv, int64_t 
 
 __global__ void fill_kernel(float* p, int64_t n, float v, int64_t wsf) {
   p += (int64_t)blockIdx.y * wsf;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = v;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {  // 16-byte stores, then the tail
+    const f32x4_t v4 = {v, v, v, v};
+    for (int64_t i4 = i; 4 * i4 + 3 < n; i4 += stride) *reinterpret_cast<f32x4_t*>(p + 4 * i4) = v4;
+    i = (n & ~(int64_t)3) + i;
+  }
+  for (; i < n; i += stride) p[i] = v;
 }
 
 // Place diagonal-block inverses into X.
@@ -1042,9 +1084,17 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
   hipLaunchKernelGGL(diag_damp_kernel, dim3(nb_), dim3(1024), 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0,
                      percdamp, dead_dev, damp, wsf, status_dev);
   MQ_LAUNCH_CHECK();
-  dim3 fb(64, 16), fg((unsigned)((d + 63) / 64), (unsigned)((d + 15) / 16), nb_);
-  hipLaunchKernelGGL(prepare_flip_kernel, fg, fb, 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0, damp, F,
-                     wsf);
+  // 64 x 16 threads; the vectorised paths take four columns per thread, so a
+  // block row covers 256 columns instead of 64
+  const bool vin = !perm_dev && (d & 3) == 0 && (ldh & 3) == 0 && (nb_ == 1 || (sh & 3) == 0) && aligned16(h_dev);
+  const bool vout = (d & 3) == 0 && (nb_ == 1 || (shinv & 3) == 0) && aligned16(hinv_dev);
+  auto grid_for = [&](bool vec) {
+    const int64_t cpb = vec ? 256 : 64;
+    return dim3((unsigned)((d + cpb - 1) / cpb), (unsigned)((d + 15) / 16), nb_);
+  };
+  const dim3 fb(64, 16);
+  hipLaunchKernelGGL(prepare_flip_kernel, grid_for(vin), fb, 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0, damp, F,
+                     wsf, vin ? 1 : 0);
   MQ_LAUNCH_CHECK();
 
   // blocked right-looking Cholesky on F (lower), two levels: inside an outer
@@ -1172,7 +1222,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       }
     }
   }
-  hipLaunchKernelGGL(flip_out_kernel, fg, fb, 0, st, X, d, hinv_dev, wsf, shinv);
+  hipLaunchKernelGGL(flip_out_kernel, grid_for(vout), fb, 0, st, X, d, hinv_dev, wsf, shinv, vout ? 1 : 0);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
 }
