@@ -1138,12 +1138,13 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
     const int64_t rest2 = d - c_end, kk = c_end - c0;
     if (rest2 > 0) {
       if (kk >= 256) {
-        // row strips of 512: strip [r0, r1) takes columns [0, r1) in one
+        // row strips of 1024: strip [r0, r1) takes columns [0, r1) in one
         // library GEMM (K = kk), the lower triangle plus the upper half of its
         // diagonal block, which nothing reads (the diagonal-block kernel
-        // masks it).  1.14x the triangle's multiply-adds at the library's
-        // GEMM rate, instead of its syrk at about a third of that rate.
-        constexpr int64_t SW = 512;
+        // masks it).  About 1.3x the triangle's multiply-adds at the
+        // library's GEMM rate, instead of its syrk at about a third of that
+        // rate (512-row strips get smaller library tiles and are slower).
+        constexpr int64_t SW = 1024;
         for (int64_t r0 = 0; r0 < rest2; r0 += SW) {
           const int64_t r1 = r0 + SW < rest2 ? r0 + SW : rest2;
           GemmArgs s{};
