@@ -70,6 +70,16 @@ int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int
                              float* h_dev, int64_t ldh, float alpha,
                              void* workspace_dev, size_t workspace_bytes, void* stream);
 
+/* H[i][j] = beta * H[i][j] + alpha * sum_t x[t][i] * x[t][j] (i <= j), the
+ * scaling of H a rounded multiply of its own; with n_tokens == 0 only the
+ * scaling runs.  Workspace as mi355q_hessian_syrk_bf16.
+ * Replaces: modifiers/pruning/sparsegpt/sgpt_sparsify.py:48-53 (the running
+ * mean H *= n / (n + added); H += (sqrt(2 / n') X)^T (sqrt(2 / n') X), i.e.
+ * beta = n / n', alpha = 2 / n'). */
+int mi355q_hessian_syrk_scaled_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
+                                    float* h_dev, int64_t ldh, float alpha, float beta,
+                                    void* workspace_dev, size_t workspace_bytes, void* stream);
+
 /* Grouped (MoE) variant: expert e accumulates the rows
  * x[rows_dev[k]] for k in [offsets_host[e], offsets_host[e+1]) into
  * h_dev + e * h_stride (each d x d, leading dimension d, upper triangle).
@@ -184,6 +194,38 @@ int mi355q_gptq_store_weight_batched(const float* w_work_dev, int64_t rows, int6
                                      const int32_t* invperm_dev, int64_t stride_perm, void* w_out_dev,
                                      mi355q_dtype out_dtype, int64_t ld_out, int64_t stride_out,
                                      const int8_t* codes_in_dev, int8_t* codes_out_dev, void* stream);
+
+/* ------------------------------------------------------------------ SparseGPT
+ * The solve of modifiers/pruning/sparsegpt/sgpt_sparsify.py:58-213 on a
+ * working copy from mi355q_gptq_load_weight (dead columns zeroed) and the
+ * upper factor from mi355q_gptq_hinv / _hinv_fallback (the same chain as
+ * :97-117, num_samples = 1 since the running-mean Hessian is normalised).
+ *
+ * mi355q_sparsegpt_base_mask: mask[i] = (w_work[i] == 0), count = number of
+ * such entries (device uint32; the caller reads it for the reference's
+ * "target sparsity is lower than the sparsity of the base model" check,
+ * :122-135).
+ *
+ * mi355q_sparsegpt_sweep: blocked sweep (:137-206) in place on w_work (fp32
+ * [rows, cols]); losses [rows] fp32 accumulate sum_blocks sum (w - q)^2 /
+ * d^2 / 2 (zero it first).  prune_n == 0: unstructured, per block every
+ * entry whose w^2 / Hinv[c][c]^2 is at or below the k-th smallest of the
+ * block, k = int(rows * count * sparsity) (:150-165).  prune_n > 0: N:M
+ * groups of prune_m <= 16 columns from each block's start, the prune_n
+ * smallest per row pruned, lower column first on equal values (:166-186).
+ * mask_dev != NULL: preserve_sparsity_mask with the mask from
+ * mi355q_sparsegpt_base_mask (in N:M mode it is updated in place, as the
+ * reference's view of it is).  blocksize <= 128 (MI355Q_UNSUPPORTED above);
+ * arguments the reference rejects by raising (k out of range, a group
+ * narrower than prune_n, mismatched preserved-mask windows) give
+ * MI355Q_INVALID_ARGUMENT. */
+int mi355q_sparsegpt_base_mask(const float* w_work_dev, int64_t rows, int64_t cols, uint8_t* mask_dev,
+                               uint32_t* count_dev, void* stream);
+size_t mi355q_sparsegpt_workspace_size(int64_t rows, int64_t cols, int64_t blocksize);
+int mi355q_sparsegpt_sweep(float* w_work_dev, int64_t rows, int64_t cols, const float* hinv_dev,
+                           double sparsity, int prune_n, int prune_m, int64_t blocksize,
+                           uint8_t* mask_dev, float* losses_dev, void* workspace_dev,
+                           size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ observers
  * Min/max statistics per strategy (observers/min_max.py:106-110 over

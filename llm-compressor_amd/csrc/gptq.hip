@@ -11,26 +11,14 @@
 // in-place subtract).  Hinv's diagonal block sits in LDS.  After each block
 // the lazy update W[:, i2:] -= Err @ Hinv[i1:i2, i2:] runs as an fp32 MFMA
 // GEMM whose output is rounded once and then subtracted, as in the reference.
-#include "linalg.h"
+#include "sweep.h"
 
 #pragma clang fp contract(off)
 
 namespace mi355q {
 namespace {
 
-constexpr int SW_G = 16;                 // lanes per row
-constexpr int SW_ROWS = 16;              // rows per workgroup
-constexpr int SW_NT = SW_G * SW_ROWS;    // 256 threads
-constexpr int MAXB = 128;                // largest supported block size
-constexpr int SW_T = MAXB / SW_G;        // columns per lane
-constexpr int SUPER = 1024;              // columns per lazy-update super-block
-constexpr int MID = 512;                 // columns per lazy-update mid-block
-constexpr int HPK = MAXB * (MAXB + 1) / 2;  // packed upper triangle of a Hinv block
-
-// Row i of the block's upper triangle starts at hrow(i) in the packed LDS copy
-// (element (i, j), j >= i, at hrow(i) + j - i): 33 KB instead of 64 KB, so four
-// workgroups fit in a CU's LDS.
-__host__ __device__ constexpr int hrow(int i) { return i * MAXB - i * (i - 1) / 2; }
+using namespace sweep;
 
 // Per-lane state of the sweep: lane g of a row holds block columns
 // SW_G * t + g, t = 0..SW_T-1.
@@ -41,29 +29,10 @@ struct SweepState {
   float z[SW_T];   // zero point of each column
 };
 
-// a / b correctly rounded, from rb = 1 / b correctly rounded: q0 = a rb,
-// then one FMA residual correction (Markstein's theorem: with a correctly
-// rounded reciprocal the corrected quotient is the correctly rounded one, in
-// the absence of overflow and underflow, as for every scale and Hinv diagonal
-// here).  Three dependent operations on the sweep's serial chain instead of
-// the ten of a full IEEE division; a probe found no difference from a / b in
-// 2^32 random and near-half-integer quotients.
-__device__ __forceinline__ float div_by_recip(float a, float b, float rb) {
-  const float q0 = a * rb;
-  const float r = fmaf(-b, q0, a);
-  return fmaf(r, rb, q0);
-}
-
 // Branch-free bf16 round-to-nearest-even of a finite fp32 value.
 __device__ __forceinline__ float bf16_rne(float f) {
   const uint32_t u = __float_as_uint(f);
   return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
-}
-
-// Broadcast lane `L` of every 16-lane row to the whole row (DPP row_newbcast).
-template <int L>
-__device__ __forceinline__ float row_bcast(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xF, 0xF, false));
 }
 
 // CT quantize / dequantize of one value: qq = clamp(rint(x / s + z)),
@@ -173,27 +142,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
   const int dcol = tid < count ? tid : count - 1;
   const float diag = hinv[(i1 + dcol) * cols + i1 + dcol];
   const int gval = uses_gidx ? g_idx[i1 + dcol] : 0;
-  if (count == MAXB && (cols & 3) == 0 && (reinterpret_cast<uintptr_t>(hinv) & 15) == 0) {
-    f32x4_t hv[MAXB * MAXB / 4 / SW_NT];
-#pragma unroll
-    for (int v = 0; v < MAXB * MAXB / 4 / SW_NT; ++v) {
-      const int e = v * SW_NT + tid;
-      hv[v] = *reinterpret_cast<const f32x4_t*>(hinv + (i1 + (e >> 5)) * cols + i1 + (e & 31) * 4);
-    }
-#pragma unroll
-    for (int v = 0; v < MAXB * MAXB / 4 / SW_NT; ++v) {
-      const int e = v * SW_NT + tid;
-      const int i = e >> 5, j0 = (e & 31) * 4;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (j0 + q >= i) h1[hrow(i) + j0 + q - i] = hv[v][q];
-    }
-  } else {
-    for (int e = tid; e < count * count; e += SW_NT) {
-      const int i = e / count, j = e % count;
-      if (j >= i) h1[hrow(i) + j - i] = hinv[(i1 + i) * cols + (i1 + j)];
-    }
-  }
+  load_hinv_block(h1, hinv, cols, i1, count, tid);
   if (tid < MAXB) gsh[tid] = tid < count ? gval : 0;
   if (tid < MAXB) rdg[tid] = tid < count ? 1.f / diag : 1.f;
   __syncthreads();
@@ -358,6 +307,7 @@ void launch_sweep(bool full, bool bf16, bool zp, dim3 grid, hipStream_t st, A...
 }  // namespace mi355q
 
 using namespace mi355q;
+using namespace mi355q::sweep;
 
 extern "C" int mi355q_gptq_load_weight_batched(const void* w_dev, mi355q_dtype w_dtype, int64_t rows,
                                                int64_t cols, int64_t ldw, int64_t stride_w, int64_t batch,
@@ -380,15 +330,6 @@ extern "C" int mi355q_gptq_load_weight(const void* w_dev, mi355q_dtype w_dtype, 
   return mi355q_gptq_load_weight_batched(w_dev, w_dtype, rows, cols, ldw, 0, 1, perm_dev, 0, dead_dev,
                                          w_work_dev, stream);
 }
-
-namespace {
-// columns of the error buffer: one super-block of whole blocks, or all columns
-int64_t err_cols(int64_t cols, int64_t blocksize) {
-  const int64_t B = blocksize < MAXB ? blocksize : MAXB;
-  const int64_t sup = (SUPER / B) * B;
-  return sup < cols ? sup : cols;
-}
-}  // namespace
 
 extern "C" size_t mi355q_gptq_sweep_workspace_size(int64_t rows, int64_t cols, int64_t blocksize) {
   if (rows <= 0 || cols <= 0 || blocksize <= 0) return 0;
@@ -421,58 +362,21 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
   SweepBatch sb{rows * cols, stride_hinv, stride_scale, stride_gidx, rows * cols, rows, rows * lde};
   // the sweep kernel holds at most MAXB columns; larger reference block
   // sizes give the same result up to fp32 rounding of the lazy update, so
-  // they are processed in MAXB-wide sub-blocks.
-  //
-  // Lazy updates are three-level: inside a mid-block of MID columns each
-  // block's errors update the rest of the mid-block (K = block size, as in
-  // the reference); the rest of the super-block (SUPER columns) receives a
-  // mid-block's errors in one GEMM (K up to MID), and the columns past the
-  // super-block all its errors in one GEMM (K up to SUPER).  The far columns
-  // thus get Sum_b Err_b Hinv[b, far] rounded once per mid- or super-block
-  // instead of once per block, an fp32 rounding-order difference of the same
-  // kind as a GEMM's summation order; most of the multiply-adds run at the
-  // library GEMM's large-K rate instead of the K = 128 kernel's.
+  // they are processed in MAXB-wide sub-blocks
   const int64_t B = blocksize < MAXB ? blocksize : MAXB;
-  // whole blocks per mid- and super-block: block boundaries as in the reference
-  const int64_t sup = (SUPER / B) * B, mid = (MID / B) * B;
   const unsigned nwg = (unsigned)((rows + SW_ROWS - 1) / SW_ROWS);
-  // W[:, c0:c1] -= Err[:, k0:k1] Hinv[k0:k1, c0:c1] (errors of super-block s0)
-  auto lazy = [&](int64_t k0, int64_t k1, int64_t s0, int64_t c0, int64_t c1) {
-    GemmArgs g{};
-    g.A = err + (k0 - s0); g.lda = lde; g.strideA = rows * lde;
-    g.B = hinv_dev + k0 * cols + c0; g.ldb = cols; g.strideB = stride_hinv;
-    g.C = w_work_dev + c0; g.ldc = cols; g.strideC = rows * cols;
-    g.M = rows; g.N = c1 - c0; g.K = k1 - k0;
-    g.alpha = -1.f; g.beta = 1.f;
-    return gemm_f32(g, false, (int)batch, st);
+  auto block = [&](int64_t i1, int64_t i2, int64_t s0) {
+    const int count = (int)(i2 - i1);
+    launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, dim3(nwg, (unsigned)batch), st, w_work_dev,
+                 rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
+                 qmax, codes_dev, losses_dev, err, lde, (int)(i1 - s0), sb);
+    MQ_LAUNCH_CHECK();
+    return MI355Q_OK;
   };
-  for (int64_t s0 = 0; s0 < cols; s0 += sup) {
-    const int64_t s1 = s0 + sup < cols ? s0 + sup : cols;
-    for (int64_t m0 = s0; m0 < s1; m0 += mid) {
-      const int64_t m1 = m0 + mid < s1 ? m0 + mid : s1;
-      for (int64_t i1 = m0; i1 < m1; i1 += B) {
-        const int64_t i2 = (i1 + B < m1) ? i1 + B : m1;
-        const int count = (int)(i2 - i1);
-        launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, dim3(nwg, (unsigned)batch), st,
-                     w_work_dev, rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy,
-                     block_h, qmin, qmax, codes_dev, losses_dev, err, lde, (int)(i1 - s0), sb);
-        MQ_LAUNCH_CHECK();
-        if (i2 < m1) {
-          const int rc = lazy(i1, i2, s0, i2, m1);
-          if (rc) return rc;
-        }
-      }
-      if (m1 < s1) {
-        const int rc = lazy(m0, m1, s0, m1, s1);
-        if (rc) return rc;
-      }
-    }
-    if (s1 < cols) {
-      const int rc = lazy(s0, s1, s0, s1, cols);
-      if (rc) return rc;
-    }
-  }
-  return MI355Q_OK;
+  auto lazy = [&](int64_t k0, int64_t k1, int64_t s0, int64_t c0, int64_t c1) {
+    return lazy_update(w_work_dev, rows, cols, batch, hinv_dev, stride_hinv, err, lde, k0, k1, s0, c0, c1, st);
+  };
+  return blocked_schedule(cols, B, block, lazy);
 }
 
 extern "C" int mi355q_gptq_sweep(float* w_work_dev, int64_t rows, int64_t cols, const float* hinv_dev,

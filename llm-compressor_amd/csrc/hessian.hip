@@ -64,6 +64,7 @@ struct SyrkParams {
   int64_t ldh;
   int nt;                  // tiles per edge
   float alpha;
+  float beta;              // H = beta * H + alpha * X^T X (beta == 1: H += ...)
   const int32_t* rows;     // optional token -> row indirection
   Matrix single;           // single-matrix mode
   int S;
@@ -80,6 +81,10 @@ struct SyrkParams {
 // of one XCD run consecutive t together, so a round of concurrent tiles
 // touches about 2 SBK feature slices of X instead of all of them, and the
 // slices it streams are shared through that XCD's L2.
+// beta * h as its own rounded multiply (the reference scales H before adding
+// the product); beta == 1 leaves h as it is
+__device__ __forceinline__ float scaled(float h, float beta) { return beta == 1.f ? h : h * beta; }
+
 __device__ __forceinline__ void tile_coords(int t, int nt, int& ti, int& tj) {
   constexpr int SBK = 8;
   const int nb = (nt + SBK - 1) / SBK;
@@ -321,7 +326,7 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
         const int mi = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), nj = lane & 31;
         if (gib + mi < p.d && gjb + nj < p.d && (!diag || mb + mi <= nb + nj)) {
           float* hp = hb + (int64_t)mi * p.ldh + nj;
-          *hp = *hp + p.alpha * acc[bm][bn][r];
+          *hp = scaled(*hp, p.beta) + p.alpha * acc[bm][bn][r];
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -623,7 +628,7 @@ template <int TM>
 __global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict__ ws, const ReduceItem* items,
                                                          int single_S, int tail_start, int64_t tail_base,
                                                          Matrix single, const Matrix* mats, int64_t d,
-                                                         int64_t ldh, int nt, float alpha) {
+                                                         int64_t ldh, int nt, float alpha, float beta) {
   using C = Cfg<TM>;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -666,7 +671,7 @@ __global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict
       const int64_t gi = gi0 + m, gj = gj0 + nn;
       if (gi < d && gj < d && gi <= gj) {
         float* hp = mat.h + gi * ldh + gj;
-        *hp = *hp + alpha * sum[bn * 16 + r];
+        *hp = scaled(*hp, beta) + alpha * sum[bn * 16 + r];
       }
     }
 }
@@ -774,13 +779,20 @@ void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) 
 
 void launch_reduce(const float* ws, const ReduceItem* items, int S, int tail_start, int64_t tail_base,
                    const Matrix& single, const Matrix* mats, int64_t d, int64_t ldh, int nt, float alpha,
-                   unsigned ntiles, hipStream_t st) {
+                   float beta, unsigned ntiles, hipStream_t st) {
   if (tile_edge(d) == 256)
     hipLaunchKernelGGL(syrk_reduce_kernel<256>, dim3(ntiles, Cfg<256>::NB), dim3(NT), 0, st, ws, items, S,
-                       tail_start, tail_base, single, mats, d, ldh, nt, alpha);
+                       tail_start, tail_base, single, mats, d, ldh, nt, alpha, beta);
   else
     hipLaunchKernelGGL(syrk_reduce_kernel<128>, dim3(ntiles, Cfg<128>::NB), dim3(NT), 0, st, ws, items, S,
-                       tail_start, tail_base, single, mats, d, ldh, nt, alpha);
+                       tail_start, tail_base, single, mats, d, ldh, nt, alpha, beta);
+}
+
+// H[i][j] *= beta on the upper triangle (a call without tokens)
+__global__ void scale_upper_kernel(float* h, int64_t d, int64_t ldh, float beta) {
+  const int64_t i = blockIdx.y;
+  for (int64_t j = i + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < d; j += (int64_t)gridDim.x * blockDim.x)
+    h[i * ldh + j] = h[i * ldh + j] * beta;
 }
 
 }  // namespace
@@ -794,16 +806,23 @@ extern "C" size_t mi355q_hessian_workspace_size(int64_t n_tokens, int64_t d) {
   return (size_t)plan_dense(n_tokens, d).slots * tile_floats(d) * sizeof(float);
 }
 
-extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
-                                        float* h_dev, int64_t ldh, float alpha, void* workspace_dev,
-                                        size_t workspace_bytes, void* stream) {
+extern "C" int mi355q_hessian_syrk_scaled_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
+                                               float* h_dev, int64_t ldh, float alpha, float beta,
+                                               void* workspace_dev, size_t workspace_bytes, void* stream) {
   MQ_CHECK_ARG(d > 0 && d % 8 == 0, "hessian: d must be a positive multiple of 8 (got %lld)", (long long)d);
   MQ_CHECK_ARG(ldx >= d && ldx % 8 == 0, "hessian: ldx must be >= d and a multiple of 8");
   MQ_CHECK_ARG(ldx <= (int64_t(1) << 24), "hessian: ldx above 2^24 elements is not supported");
   MQ_CHECK_ARG(ldh >= d, "hessian: ldh must be >= d");
   MQ_CHECK_ARG(n_tokens >= 0, "hessian: negative token count");
   MQ_CHECK_ARG(h_dev != nullptr, "hessian: null H");
-  if (n_tokens == 0) return MI355Q_OK;
+  if (n_tokens == 0) {
+    if (beta != 1.f) {
+      hipLaunchKernelGGL(scale_upper_kernel, dim3((unsigned)((d + 255) / 256), (unsigned)d), dim3(256), 0,
+                         reinterpret_cast<hipStream_t>(stream), h_dev, d, ldh, beta);
+      MQ_LAUNCH_CHECK();
+    }
+    return MI355Q_OK;
+  }
   MQ_CHECK_ARG(x_dev != nullptr && aligned16(x_dev), "hessian: x must be non-null and 16-byte aligned");
   const int nt = tiles_per_edge(d);
   const DensePlan pl = plan_dense(n_tokens, d);
@@ -820,6 +839,7 @@ extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int
   p.ldh = ldh;
   p.nt = nt;
   p.alpha = alpha;
+  p.beta = beta;
   p.rows = nullptr;
   p.single = Matrix{0, n_tokens, h_dev};
   p.S = S;
@@ -836,11 +856,18 @@ extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int
                          (int64_t)tile_floats(d), pl.tail_src0, pl.tail_dst0, pl.tail_f);
       MQ_LAUNCH_CHECK();
     }
-    launch_reduce(p.ws, nullptr, S, pl.tail_start, pl.tail_dst0, p.single, nullptr, d, ldh, nt, alpha,
+    launch_reduce(p.ws, nullptr, S, pl.tail_start, pl.tail_dst0, p.single, nullptr, d, ldh, nt, alpha, beta,
                   (unsigned)T, st);
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;
+}
+
+extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
+                                        float* h_dev, int64_t ldh, float alpha, void* workspace_dev,
+                                        size_t workspace_bytes, void* stream) {
+  return mi355q_hessian_syrk_scaled_bf16(x_dev, n_tokens, d, ldx, h_dev, ldh, alpha, 1.f, workspace_dev,
+                                         workspace_bytes, stream);
 }
 
 namespace {
@@ -927,6 +954,7 @@ extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, 
   p.ldh = d;
   p.nt = tiles_per_edge(d);
   p.alpha = alpha;
+  p.beta = 1.f;
   p.rows = rows_dev;
   p.S = 1;
   p.tail_start = 0;
@@ -938,7 +966,7 @@ extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, 
   MQ_LAUNCH_CHECK();
   if (!g.reduces.empty()) {
     launch_reduce(p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, 0, 0, Matrix{}, p.mats, d, d,
-                  p.nt, alpha, (unsigned)g.reduces.size(), st);
+                  p.nt, alpha, 1.f, (unsigned)g.reduces.size(), st);
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;

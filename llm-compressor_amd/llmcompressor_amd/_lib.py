@@ -17,7 +17,7 @@ BF16, F32 = 0, 1
 TENSOR, CHANNEL, GROUP, BLOCK, TOKEN = 0, 1, 2, 3, 4
 MX_RULE_CT, MX_RULE_OCP = 0, 1
 
-_vp, _i64, _i32, _f32, _sz = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_size_t
+_vp, _i64, _i32, _f32, _f64, _sz = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double, C.c_size_t
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -25,6 +25,7 @@ SIGNATURES = {
     "mi355q_version": (_i32, []),
     "mi355q_hessian_workspace_size": (_sz, [_i64, _i64]),
     "mi355q_hessian_syrk_bf16": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _f32, _vp, _sz, _vp]),
+    "mi355q_hessian_syrk_scaled_bf16": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _f32, _f32, _vp, _sz, _vp]),
     "mi355q_hessian_grouped_workspace_size": (_sz, [_vp, _i32, _i64]),
     "mi355q_hessian_grouped_syrk_bf16": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _f32, _vp, _sz, _vp]),
     "mi355q_symmetrize_upper": (_i32, [_vp, _i64, _i64, _vp]),
@@ -44,6 +45,9 @@ SIGNATURES = {
                                          _i32, _f32, _f32, _i32, _i64, _vp, _vp, _vp, _sz, _vp]),
     "mi355q_gptq_store_weight_batched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _i64, _i64, _vp,
                                                 _vp, _vp]),
+    "mi355q_sparsegpt_base_mask": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "mi355q_sparsegpt_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "mi355q_sparsegpt_sweep": (_i32, [_vp, _i64, _i64, _vp, _f64, _i32, _i32, _i64, _vp, _vp, _vp, _sz, _vp]),
     "mi355q_observe_minmax": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
     "mi355q_calculate_qparams": (_i32, [_vp, _vp, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "mi355q_mx_scales": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp]),

@@ -13,7 +13,11 @@ These mirror the reference's modifiers at the level the hot path needs
   -> ``quantize_weight`` on H / num_samples (``base.py:578-601``), writing
   ``weight`` / ``weight_scale`` / ``weight_zero_point`` / ``weight_g_idx``;
 * ``QuantizationModifier``: RTN - observe + update_qparams of weights
-  (``quantization/base.py:85-96``).
+  (``quantization/base.py:85-96``);
+* ``SparseGPTModifier`` (``modifiers/pruning/sparsegpt/base.py:24-173``,
+  ``sgpt_base.py:20-252``): per target layer a sparsity, a forward hook per
+  prunable submodule accumulating the running-mean Hessian, and
+  ``sparsify_weight`` at the epoch end.
 
 ``GPTQModifier.apply(model, batches)`` runs one calibration pass over the
 batches (the basic pipeline: every target sees its inputs in one pass) and
@@ -28,6 +32,7 @@ import time
 import torch
 
 from .calibration import initialize_module_for_quantization, initialize_observer, observe, update_qparams
+from . import sparsegpt as sgpt
 from .gptq import accumulate_hessian, gptq_quantize, make_empty_hessian
 from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationScheme, preset_name_to_scheme
 
@@ -197,5 +202,128 @@ class GPTQModifier(QuantizationModifier):
                 model(b)
         self.on_calibration_end()
         self.on_sequential_epoch_end(list(self._modules))
+        self.on_finalize()
+        return model
+
+
+class SparseGPTModifier:
+    """One-shot SparseGPT (``modifiers/pruning/sparsegpt/base.py:24-173``).
+
+    ``targets`` name the layers that carry a sparsity (a float for all, or
+    one per layer in model order); every ``nn.Linear`` / Conv1D inside a target
+    layer (the layer itself included) that ``ignore`` does not match is pruned
+    with its layer's sparsity (``sgpt_base.py:103-172``).  ``mask_structure``
+    is ``"N:M"`` (``"0:0"``: unstructured).  OWL layer sparsities
+    (``sparsity_profile="owl"``) are not provided by this build.
+    """
+
+    def __init__(self, sparsity=None, sparsity_profile: str | None = None, mask_structure: str = "0:0",
+                 owl_m: int | None = None, owl_lmbda: float | None = None, targets=("Linear",), ignore=(),
+                 block_size: int = 128, dampening_frac: float | None = 0.01, preserve_sparsity_mask: bool = False,
+                 offload_hessians: bool = False):
+        if sparsity_profile is not None:
+            sparsity_profile = sparsity_profile.lower()
+            if sparsity_profile not in ["owl"]:
+                raise ValueError("Please choose profile from ['owl']")
+        owl_args = (owl_m is not None, owl_lmbda is not None, sparsity_profile == "owl")
+        if any(owl_args) and not all(owl_args):
+            raise ValueError('Must provide all of `profile="owl"`, `owl_m` and `owl_lmbda` or none')
+        if sparsity_profile == "owl":
+            raise NotImplementedError("OWL layer-wise sparsities are not provided by this build")
+        self.sparsity = sparsity
+        self.mask_structure = mask_structure
+        self.targets = [targets] if isinstance(targets, str) else list(targets)
+        self.ignore = list(ignore)
+        self.block_size = block_size
+        self.dampening_frac = dampening_frac
+        self.preserve_sparsity_mask = preserve_sparsity_mask
+        self.offload_hessians = offload_hessians
+        n, m = mask_structure.split(":")
+        self._prune_n, self._prune_m = int(n), int(m)
+        self._hessians: dict = {}
+        self._num_samples: dict = {}
+        self._module_names: dict = {}
+        self._module_sparsities: dict = {}
+        self._hooks = []
+        self.timings: dict[str, float] = {}
+
+    def on_initialize(self, model):
+        self._target_layers = {name: m for name, m in model.named_modules()
+                               if name and _matches(name, m, self.targets)}
+        if isinstance(self.sparsity, (list, dict)) and len(self._target_layers) != len(self.sparsity):
+            raise ValueError(f"SparseGPTModifier was initialized with {len(self.sparsity)} sparsities values, "
+                             f"but model has {len(self._target_layers)} target layers")
+        return True
+
+    def on_calibration_start(self, model):
+        for index, (layer_name, layer) in enumerate(self._target_layers.items()):
+            layer_sparsity = self.sparsity[index] if isinstance(self.sparsity, list) else self.sparsity
+            for sub, module in layer.named_modules():
+                if not (isinstance(module, torch.nn.Linear) or type(module).__name__ == "Conv1D"):
+                    continue
+                name = f"{layer_name}.{sub}" if sub else layer_name
+                if _matches(name, module, self.ignore) or module in self._module_names:
+                    continue
+                if name.endswith("lm_head"):
+                    logger.warning("`lm_head` was previously auto-ignored by SparseGPT and Wanda modifiers and is "
+                                   "not advised. Please add `re:.*lm_head` to your ignore list if this was "
+                                   "unintentional")
+                self._module_names[module] = name
+                self._module_sparsities[module] = layer_sparsity
+                self._hooks.append(module.register_forward_hook(self.calibrate_module))
+
+    def calibrate_module(self, module, args, _output):
+        inp = args[0]
+        if module not in self._num_samples:
+            dev = module.weight.device
+            self._hessians[module] = sgpt.make_empty_hessian(module, device="cpu" if self.offload_hessians else dev)
+            self._num_samples[module] = 0
+        H = self._hessians[module]
+        if self.offload_hessians:
+            H = H.to(module.weight.device)
+        H, self._num_samples[module] = sgpt.accumulate_hessian(inp, module, H, self._num_samples[module])
+        self._hessians[module] = H.to("cpu") if self.offload_hessians else H
+
+    def compress_modules(self):
+        for module in list(self._num_samples):
+            name = self._module_names[module]
+            if self.offload_hessians:
+                self._hessians[module] = self._hessians[module].to(module.weight.device)
+            t0 = time.perf_counter()
+            with torch.no_grad():
+                loss, w = sgpt.sparsify_weight(module=module, hessians_dict=self._hessians,
+                                               sparsity=self._module_sparsities[module], prune_n=self._prune_n,
+                                               prune_m=self._prune_m, block_size=self.block_size,
+                                               dampening_frac=self.dampening_frac,
+                                               preserve_sparsity_mask=self.preserve_sparsity_mask)
+                module.weight.data.copy_(w)
+            self.timings[name] = time.perf_counter() - t0
+            logger.info("Sparsified %s using %d samples, loss %.4f", name, self._num_samples[module], loss)
+            del self._num_samples[module]
+
+    def on_sequential_epoch_end(self):
+        self.compress_modules()
+
+    def on_calibration_end(self):
+        for h in self._hooks:
+            h.remove()
+        self._hooks = []
+
+    def on_finalize(self):
+        if self._num_samples:
+            raise ValueError(f"Failed to compress {len(self._num_samples)} modules")
+        self._hessians, self._num_samples = {}, {}
+        self._module_names, self._module_sparsities = {}, {}
+        return True
+
+    def apply(self, model, batches):
+        """Initialize, hook, run the calibration batches, prune."""
+        self.on_initialize(model)
+        self.on_calibration_start(model)
+        with torch.no_grad():
+            for b in batches:
+                model(b)
+        self.on_calibration_end()
+        self.on_sequential_epoch_end()
         self.on_finalize()
         return model

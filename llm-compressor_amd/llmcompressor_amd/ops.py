@@ -28,8 +28,9 @@ def _ws(nbytes: int, device) -> torch.Tensor | None:
 
 
 # ---------------------------------------------------------------- Hessian
-def hessian_syrk_(H: torch.Tensor, x: torch.Tensor, alpha: float = 2.0) -> torch.Tensor:
-    """H[i, j] += alpha * sum_t x[t, i] x[t, j] for i <= j, in place.
+def hessian_syrk_(H: torch.Tensor, x: torch.Tensor, alpha: float = 2.0, beta: float = 1.0) -> torch.Tensor:
+    """H[i, j] = beta * H[i, j] + alpha * sum_t x[t, i] x[t, j] for i <= j, in
+    place (beta == 1: H += ...).
 
     ``x`` is [tokens, d] bf16 (row stride may exceed d); H is fp32 [d, d].
     """
@@ -45,9 +46,14 @@ def hessian_syrk_(H: torch.Tensor, x: torch.Tensor, alpha: float = 2.0) -> torch
         raise ValueError(f"H must be fp32 [{d}, {d}] row-major, got {tuple(H.shape)} {H.dtype}")
     lib = L.lib()
     ws = _ws(lib.mi355q_hessian_workspace_size(n, d), x.device)
-    L.check(lib.mi355q_hessian_syrk_bf16(x.data_ptr(), n, d, x.stride(0), H.data_ptr(), H.stride(0),
-                                         C.c_float(alpha), L.ptr(ws), 0 if ws is None else ws.numel(),
-                                         L.stream_of(x)))
+    if beta == 1.0:
+        L.check(lib.mi355q_hessian_syrk_bf16(x.data_ptr(), n, d, x.stride(0), H.data_ptr(), H.stride(0),
+                                             C.c_float(alpha), L.ptr(ws), 0 if ws is None else ws.numel(),
+                                             L.stream_of(x)))
+    else:
+        L.check(lib.mi355q_hessian_syrk_scaled_bf16(x.data_ptr(), n, d, x.stride(0), H.data_ptr(), H.stride(0),
+                                                    C.c_float(alpha), C.c_float(beta), L.ptr(ws),
+                                                    0 if ws is None else ws.numel(), L.stream_of(x)))
     return H
 
 
@@ -420,3 +426,35 @@ def quantize_int8_per_token(x: torch.Tensor):
     L.call("mi355q_quantize_int8_per_token", x.data_ptr(), rows, cols, x.stride(0), codes.data_ptr(),
            scale.data_ptr(), L.stream_of(x))
     return codes, scale
+
+
+# ---------------------------------------------------------------- SparseGPT
+def sparsegpt_base_mask(w_work: torch.Tensor):
+    """(mask uint8 [rows, cols] = w_work == 0, count int32 [1] on the device)."""
+    L.require_gpu(w_work)
+    rows, cols = w_work.shape
+    mask = torch.empty((rows, cols), dtype=torch.uint8, device=w_work.device)
+    count = torch.empty(1, dtype=torch.int32, device=w_work.device)
+    L.call("mi355q_sparsegpt_base_mask", w_work.data_ptr(), rows, cols, mask.data_ptr(), count.data_ptr(),
+           L.stream_of(w_work))
+    return mask, count
+
+
+def sparsegpt_sweep_(w_work: torch.Tensor, hinv: torch.Tensor, sparsity: float, prune_n: int, prune_m: int,
+                     blocksize: int = 128, mask: torch.Tensor | None = None) -> torch.Tensor:
+    """In-place SparseGPT sweep of w_work (fp32 [rows, cols]) with the upper
+    factor hinv.  ``mask`` (uint8, from ``sparsegpt_base_mask``) preserves the
+    entries it holds.  Returns the per-row losses fp32 [rows]."""
+    L.require_gpu(w_work, hinv, mask)
+    rows, cols = w_work.shape
+    if hinv.shape != (cols, cols) or hinv.dtype != torch.float32 or not hinv.is_contiguous():
+        raise ValueError(f"hinv must be a contiguous fp32 [{cols}, {cols}] matrix")
+    if mask is not None and (mask.shape != (rows, cols) or mask.dtype != torch.uint8 or not mask.is_contiguous()):
+        raise ValueError("mask must be a contiguous uint8 matrix shaped like w_work")
+    losses = torch.zeros(rows, dtype=torch.float32, device=w_work.device)
+    lib = L.lib()
+    ws = _ws(lib.mi355q_sparsegpt_workspace_size(rows, cols, blocksize), w_work.device)
+    L.check(lib.mi355q_sparsegpt_sweep(w_work.data_ptr(), rows, cols, hinv.data_ptr(), C.c_double(sparsity),
+                                       int(prune_n), int(prune_m), blocksize, L.ptr(mask), losses.data_ptr(),
+                                       ws.data_ptr(), ws.numel(), L.stream_of(w_work)))
+    return losses

@@ -95,3 +95,38 @@ def test_cpu_tensors_are_refused():
     from llmcompressor_amd import ops
     with pytest.raises(RuntimeError, match="GPU only"):
         ops.observe_minmax(torch.zeros(4, 4), "tensor")
+
+
+def test_sparsegpt_host_checks_raise_as_reference():
+    """sgpt_sparsify.py:160,185,181-182: the sort index past the block
+    (IndexError), a topk wider than its group (RuntimeError), a preserved-mask
+    window of another width (RuntimeError) - raised before any kernel runs."""
+    from llmcompressor_amd.sparsegpt import _check_blocks
+    with pytest.raises(IndexError):
+        _check_blocks(8, 64, 1.0, 0, 0, 32, False)
+    _check_blocks(8, 64, 0.999, 0, 0, 32, False)
+    with pytest.raises(RuntimeError):
+        _check_blocks(8, 64, 0.5, 3, 2, 32, False)
+    with pytest.raises(RuntimeError):
+        _check_blocks(8, 62, 0.5, 3, 4, 32, False)          # last group 2 wide, n = 3
+    _check_blocks(8, 62, 0.5, 2, 4, 32, False)
+    with pytest.raises(RuntimeError):
+        _check_blocks(8, 64, 0.5, 1, 3, 32, True)           # block 32 ends in a 2-wide group, mask window 3
+    with pytest.raises(NotImplementedError):
+        _check_blocks(8, 512, 0.5, 0, 0, 256, False)
+
+
+def test_sparsegpt_modifier_validation():
+    from llmcompressor_amd import SparseGPTModifier
+    m = SparseGPTModifier(sparsity=0.5, mask_structure="2:4")
+    assert (m._prune_n, m._prune_m) == (2, 4)
+    assert (SparseGPTModifier(sparsity=0.5)._prune_n, SparseGPTModifier(sparsity=0.5)._prune_m) == (0, 0)
+    with pytest.raises(ValueError):
+        SparseGPTModifier(sparsity=0.5, owl_m=5)
+    with pytest.raises(ValueError):
+        SparseGPTModifier(sparsity=0.5, sparsity_profile="bad")
+    model = torch.nn.Sequential(torch.nn.Linear(8, 8), torch.nn.ReLU(), torch.nn.Linear(8, 8))
+    for sp, targets in (([0.5, 0.2], "__ALL__"), ([0.2, 0.1, 0.3], ["0", "2"]), ([0.3, 0.4], ["re:.*1$"])):
+        with pytest.raises(ValueError):
+            SparseGPTModifier(sparsity=sp, targets=targets).on_initialize(model)
+    assert SparseGPTModifier(sparsity=[0.5, 0.2], targets=["0", "2"]).on_initialize(model)

@@ -37,6 +37,8 @@ def test_version_and_workspace_queries():
     assert lib.mi355q_gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 1024 * 4   # errors of one 1024-column super-block
     assert lib.mi355q_gptq_sweep_workspace_size(768, 768, 128) == 768 * 768 * 4       # fewer columns than a super-block
     assert lib.mi355q_gptq_hinv_workspace_size(4096) >= 2 * 4096 * 4096 * 4
+    # SparseGPT: the super-block error buffer plus the radix-select words
+    assert lib.mi355q_sparsegpt_workspace_size(4096, 4096, 128) == 4096 * 1024 * 4 + 4100 * 4
 
 
 @pytest.mark.parametrize("call,needle", [
@@ -49,6 +51,13 @@ def test_version_and_workspace_queries():
                                    C.c_void_p(16), 1 << 20, None), "not supported for GPTQ"),
     (lambda l: l.mi355q_calculate_qparams(C.c_void_p(16), C.c_void_p(16), 4, C.c_float(0), C.c_float(7), 1, 0, 0,
                                           C.c_void_p(16), C.c_void_p(16), None), "straddle zero"),
+    (lambda l: l.mi355q_sparsegpt_sweep(C.c_void_p(16), 4, 64, C.c_void_p(16), C.c_double(1.0), 0, 0, 32, None,
+                                        C.c_void_p(16), C.c_void_p(16), 1 << 20, None), "out of bounds"),
+    (lambda l: l.mi355q_sparsegpt_sweep(C.c_void_p(16), 4, 64, C.c_void_p(16), C.c_double(0.5), 3, 2, 32, None,
+                                        C.c_void_p(16), C.c_void_p(16), 1 << 20, None), "out of range"),
+    (lambda l: l.mi355q_sparsegpt_sweep(C.c_void_p(16), 4, 64, C.c_void_p(16), C.c_double(0.5), 1, 3, 32,
+                                        C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), 1 << 20, None),
+     "broadcast"),
 ])
 def test_invalid_arguments_are_rejected_on_the_host(call, needle):
     lib = _lib.load_library()
@@ -62,3 +71,13 @@ def test_hessian_grouped_rejects_decreasing_offsets():
     rc = lib.mi355q_hessian_grouped_syrk_bf16(C.c_void_p(16), 8, 8, C.c_void_p(16), off, 2, C.c_void_p(16), 64,
                                               C.c_float(2.0), None, 0, None)
     assert rc == _lib.INVALID_ARGUMENT and "non-decreasing" in lib.mi355q_last_error().decode()
+
+
+def test_sparsegpt_limits_are_reported_unsupported():
+    lib = _lib.load_library()
+    rc = lib.mi355q_sparsegpt_sweep(C.c_void_p(16), 4, 512, C.c_void_p(16), C.c_double(0.5), 0, 0, 256, None,
+                                    C.c_void_p(16), C.c_void_p(16), 1 << 24, None)
+    assert rc == _lib.UNSUPPORTED and "block sizes" in lib.mi355q_last_error().decode()
+    rc = lib.mi355q_sparsegpt_sweep(C.c_void_p(16), 4, 512, C.c_void_p(16), C.c_double(0.5), 16, 32, 128, None,
+                                    C.c_void_p(16), C.c_void_p(16), 1 << 24, None)
+    assert rc == _lib.UNSUPPORTED and "wider than 16" in lib.mi355q_last_error().decode()
