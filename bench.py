@@ -41,10 +41,10 @@ def parse():
     p.add_argument("--hessian-calls", type=int, default=1,
                    help="split the 64 x 2048 calibration tokens into this many accumulate_hessian calls")
     p.add_argument("--workload", default="gptq_w4a16",
-                   choices=["gptq_w4a16", "mxfp4", "gptq_w8a8", "moe", "decoder"],
+                   choices=["gptq_w4a16", "mxfp4", "gptq_w8a8", "moe", "decoder", "sparsegpt"],
                    help="gptq_w4a16 (default): the headline line; the others measure the remaining "
                         "calibration workloads (MXFP4 pack, W8A8 channel + actorder, MoE experts, "
-                        "Llama-3-8B-shaped decoder layer)")
+                        "Llama-3-8B-shaped decoder layer, SparseGPT 50 %% / 2:4 on a 4096x4096 layer)")
     return p.parse_args()
 
 
@@ -470,7 +470,48 @@ def bench_decoder(a):
                        "frac_bf16_mfma_peak": round(flop / hess_ms / 1e9 / PEAK_BF16_TFLOPS, 4)}})
 
 
-OTHER_WORKLOADS = {"mxfp4": bench_mxfp4, "gptq_w8a8": bench_w8a8, "moe": bench_moe, "decoder": bench_decoder}
+def bench_sparsegpt(a):
+    """SparseGPT on a 4096 x 4096 layer: running-mean Hessian over 64 x 2048 tokens, then the 50 %
+    unstructured solve (the step); the 2:4 solve on the same Hessian is timed beside it."""
+    torch, dev = _setup()
+    from llmcompressor_amd import sparsegpt
+    rows = cols = 4096
+    batches, seq = 64, 2048
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    w = (torch.randn(rows, cols, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x = _gpu_heavy(torch, dev, batches * seq, cols, 1)
+    lin = torch.nn.Linear(cols, rows, bias=False, device=dev, dtype=torch.bfloat16)
+    lin.weight.data = w
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    def step():
+        H = sparsegpt.make_empty_hessian(lin)
+        ev[0].record()
+        H, n = sparsegpt.accumulate_hessian(x.view(batches, seq, cols), lin, H, 0)
+        ev[1].record()
+        r = sparsegpt.sparsegpt_prune(lin.weight, H, 0.5)
+        ev[2].record()
+        return r, H
+
+    ms, (res, H) = _timed(torch, step, a.steps, a.warmup)
+    torch.cuda.synchronize()
+    hess_ms, solve_ms = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+    nm_ms, res24 = _timed(torch, lambda: sparsegpt.sparsegpt_prune(lin.weight, H, 0.5, 2, 4), a.steps, a.warmup)
+    z = float((res.weight == 0).float().mean())
+    z24 = float((res24.weight == 0).float().mean())
+    assert 0.5 <= z < 0.51 and 0.5 <= z24 < 0.51
+    flop = batches * seq * cols * (cols + 1)
+    _line("SparseGPT ms/layer (50 % unstructured, 4096x4096, Hessian over 64x2048 tokens + solve)",
+          ms, "ms/layer", a, ms, "sparsegpt_50pct_4096x4096_64x2048tok",
+          {"phases_ms": {"hessian": round(hess_ms, 3), "solve": round(solve_ms, 3)},
+           "solve_2of4_ms": round(nm_ms, 3), "sparsity": {"unstructured": round(z, 6), "2of4": round(z24, 6)},
+           "hessian": {"tflops": round(flop / hess_ms / 1e9, 1),
+                       "frac_bf16_mfma_peak": round(flop / hess_ms / 1e9 / PEAK_BF16_TFLOPS, 4)}})
+
+
+OTHER_WORKLOADS = {"mxfp4": bench_mxfp4, "gptq_w8a8": bench_w8a8, "moe": bench_moe, "decoder": bench_decoder,
+                   "sparsegpt": bench_sparsegpt}
 
 
 if __name__ == "__main__":

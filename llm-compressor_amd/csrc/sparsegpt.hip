@@ -8,12 +8,12 @@
 // Unstructured masks (:150-165): per block the threshold is the k-th smallest
 // (k = int(numel * sparsity)) of tmp = W1^2 / diag(Hinv1)^2 over every row
 // of the block.  tmp >= 0, so its fp32 bit patterns order like its values and
-// a three-pass radix select finds the exact k-th key: pass 0 counts bits
-// 30..20 into 2048 bins, pass 1 bits 19..10 of the keys in the selected bin,
-// pass 2 bits 9..0 of the keys left; a one-workgroup kernel turns the three
-// histograms into the threshold key and clears them for the next block.  The
-// sweep recomputes tmp from the block's starting values and prunes
-// tmp <= threshold (every value tied with the k-th as well, as the reference).
+// a three-pass radix select finds the exact k-th key: pass 0 counts the
+// exponent (bits 30..23, 256 bins), pass 1 bits 22..12 of the keys in the
+// selected bin (2048 bins), pass 2 bits 11..0 of the keys left (4096 bins).
+// The sweep kernel reads the threshold key off the three histograms, prunes
+// tmp <= threshold (every value tied with the k-th as well, as the
+// reference), and clears the other of two histogram sets for the next block.
 //
 // N:M masks (:166-186): at every m-th column of a block the n smallest tmp of
 // each row's next m columns (their values at that moment) are pruned.  The
@@ -45,45 +45,50 @@ namespace {
 
 using namespace sweep;
 
-// Select workspace (uint32 words): three histograms, the base-mask count,
-// the threshold key and the extend flag.
-constexpr int H0 = 0, H1 = 2048, H2 = 3072, HCNT = 4096, HKEY = 4097, HEXT = 4098, SEL_WORDS = 4100;
+// Select workspace: two sets of histograms (block b uses set b % 2), each
+// three histograms and the base-mask count (uint32 words).
+constexpr int NB0 = 256, NB1 = 2048, NB2 = 4096;
+constexpr int H0 = 0, H1 = NB0, H2 = NB0 + NB1, HCNT = NB0 + NB1 + NB2, SET_WORDS = HCNT + 64;
+constexpr int SEL_WORDS = 2 * SET_WORDS;
 constexpr int SEL_NT = 256;
-constexpr int SEL_ROWS = 32;   // rows per select workgroup (two per pass of 256 threads)
+constexpr int SEL_ROWS = 16;  // rows per select workgroup: 2 rows x 128 columns per round
+constexpr int SEL_IT = SEL_ROWS / 2;
 
 // The bin holding the k-th (0-based) counted key: the smallest b whose
 // cumulative count exceeds k, and k minus the count of the bins before b.
-// All SEL_NT threads call it; sh holds SEL_NT + 2 words of LDS.
-__device__ void find_bin(const unsigned* h, int nb, unsigned k, unsigned* sh, unsigned& bin, unsigned& rem) {
-  const int tid = threadIdx.x;
+// All 256 threads of the workgroup call it; sh holds 8 words of LDS.
+__device__ void find_bin(const unsigned* __restrict__ h, int nb, unsigned k, unsigned* sh, unsigned& bin,
+                         unsigned& rem) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = nb / SEL_NT;
   unsigned v = 0;
   for (int j = 0; j < per; ++j) v += h[tid * per + j];
-  sh[tid] = v;
-  __syncthreads();
-  for (int off = 1; off < SEL_NT; off <<= 1) {
-    const unsigned t = tid >= off ? sh[tid - off] : 0u;
-    __syncthreads();
-    sh[tid] += t;
-    __syncthreads();
+  unsigned x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned y = __shfl_up(x, off);
+    if (lane >= off) x += y;
   }
-  const unsigned ex = sh[tid] - v;
+  if (lane == 63) sh[wave] = x;
   __syncthreads();
-  if (ex <= k && k < ex + v) {
+  unsigned incl = x;
+  for (int w = 0; w < wave; ++w) incl += sh[w];
+  const unsigned ex = incl - v;
+  if (ex <= k && k < incl) {
     unsigned acc = ex;
     for (int j = 0; j < per; ++j) {
       const unsigned c = h[tid * per + j];
       if (k < acc + c) {
-        sh[SEL_NT] = (unsigned)(tid * per + j);
-        sh[SEL_NT + 1] = k - acc;
+        sh[4] = (unsigned)(tid * per + j);
+        sh[5] = k - acc;
         break;
       }
       acc += c;
     }
   }
   __syncthreads();
-  bin = sh[SEL_NT];
-  rem = sh[SEL_NT + 1];
+  bin = sh[4];
+  rem = sh[5];
   __syncthreads();
 }
 
@@ -96,69 +101,58 @@ __device__ __forceinline__ float saliency(float w, float dd2, bool masked) { ret
 // a non-finite weight still lands in a bin)
 __device__ __forceinline__ unsigned skey(float tmp) { return __float_as_uint(tmp) & 0x7fffffffu; }
 
-// One radix pass over the block's keys (see the file comment).
+// One radix pass over the block's keys into the histograms of set hs.
 __global__ __launch_bounds__(SEL_NT) void sgpt_select_kernel(const float* __restrict__ W, int64_t rows, int64_t cols,
                                                              const float* __restrict__ hinv, int64_t i1, int count,
                                                              const uint8_t* __restrict__ mask,
-                                                             unsigned* __restrict__ sel, int pass, unsigned k) {
-  __shared__ unsigned lh[2048];
+                                                             unsigned* __restrict__ hs, int pass, unsigned k) {
+  __shared__ unsigned lh[NB2];
   __shared__ float dd2[MAXB];
-  __shared__ unsigned sh[SEL_NT + 2];
+  __shared__ unsigned sh[8];
   const int tid = threadIdx.x;
-  for (int b = tid; b < 2048; b += SEL_NT) lh[b] = 0u;
+  const int nb = pass == 0 ? NB0 : pass == 1 ? NB1 : NB2;
+  for (int b = tid; b < nb; b += SEL_NT) lh[b] = 0u;
   if (tid < count) {
     const float d = hinv[(i1 + tid) * cols + i1 + tid];
     dd2[tid] = d * d;
   }
   unsigned b0 = 0, b1 = 0, rem = k;
-  if (pass >= 1) find_bin(sel + H0, 2048, k, sh, b0, rem);
-  if (pass >= 2) find_bin(sel + H1, 1024, rem, sh, b1, rem);
+  if (pass >= 1) find_bin(hs + H0, NB0, k, sh, b0, rem);
+  if (pass >= 2) find_bin(hs + H1, NB1, rem, sh, b1, rem);
   __syncthreads();
   const int c = tid & (MAXB - 1);
+  const int64_t r0 = (int64_t)blockIdx.x * SEL_ROWS + (tid >> 7);
+  float w[SEL_IT];
+  bool mk[SEL_IT];
+#pragma unroll
+  for (int it = 0; it < SEL_IT; ++it) {   // every load issued before the first use
+    const int64_t r = r0 + 2 * it;
+    const bool ok = c < count && r < rows;
+    const int64_t idx = (ok ? r : 0) * cols + i1 + (ok ? c : 0);
+    w[it] = W[idx];
+    mk[it] = ok && mask && mask[idx];
+  }
   unsigned nmask = 0;
-  if (c < count) {
-    const int64_t r0 = (int64_t)blockIdx.x * SEL_ROWS + (tid >> 7);
-    for (int it = 0; it < SEL_ROWS / 2; ++it) {
-      const int64_t r = r0 + 2 * it;
-      if (r >= rows) break;
-      const int64_t idx = r * cols + i1 + c;
-      const bool mk = mask && mask[idx];
-      nmask += mk;
-      const unsigned key = skey(saliency(W[idx], dd2[c], mk));
-      if (pass == 0)
-        atomicAdd(&lh[key >> 20], 1u);
-      else if (pass == 1) {
-        if ((key >> 20) == b0) atomicAdd(&lh[(key >> 10) & 1023u], 1u);
-      } else if ((key >> 10) == ((b0 << 10) | b1)) {
-        atomicAdd(&lh[key & 1023u], 1u);
-      }
+#pragma unroll
+  for (int it = 0; it < SEL_IT; ++it) {
+    if (!(c < count && r0 + 2 * it < rows)) continue;
+    nmask += mk[it];
+    const unsigned key = skey(saliency(w[it], dd2[c], mk[it]));
+    if (pass == 0)
+      atomicAdd(&lh[key >> 23], 1u);
+    else if (pass == 1) {
+      if ((key >> 23) == b0) atomicAdd(&lh[(key >> 12) & (NB1 - 1)], 1u);
+    } else if ((key >> 12) == ((b0 << 11) | b1)) {
+      atomicAdd(&lh[key & (NB2 - 1)], 1u);
     }
   }
   __syncthreads();
-  const int nb = pass == 0 ? 2048 : 1024;
-  unsigned* out = sel + (pass == 0 ? H0 : pass == 1 ? H1 : H2);
+  unsigned* out = hs + (pass == 0 ? H0 : pass == 1 ? H1 : H2);
   for (int b = tid; b < nb; b += SEL_NT)
     if (lh[b]) atomicAdd(&out[b], lh[b]);
   if (pass == 0 && mask) {
     for (int o = 32; o > 0; o >>= 1) nmask += __shfl_xor(nmask, o);
-    if ((tid & 63) == 0 && nmask) atomicAdd(&sel[HCNT], nmask);
-  }
-}
-
-// Threshold key and extend flag of the block from the three histograms,
-// then the histograms and the count cleared for the next block.
-__global__ __launch_bounds__(SEL_NT) void sgpt_threshold_kernel(unsigned* __restrict__ sel, unsigned k) {
-  __shared__ unsigned sh[SEL_NT + 2];
-  unsigned b0, b1, b2, rem;
-  find_bin(sel + H0, 2048, k, sh, b0, rem);
-  find_bin(sel + H1, 1024, rem, sh, b1, rem);
-  find_bin(sel + H2, 1024, rem, sh, b2, rem);
-  const unsigned cnt = sel[HCNT];
-  __syncthreads();
-  for (int b = threadIdx.x; b < HCNT + 1; b += SEL_NT) sel[b] = 0u;
-  if (threadIdx.x == 0) {
-    sel[HKEY] = (b0 << 20) | (b1 << 10) | b2;
-    sel[HEXT] = k > cnt ? 1u : 0u;
+    if ((tid & 63) == 0 && nmask) atomicAdd(&hs[HCNT], nmask);
   }
 }
 
@@ -239,6 +233,11 @@ __device__ __forceinline__ void prune_step(PruneState& S, const float* h1, const
     else
       S.w[t] = upd;
   }
+  // The updated values are materialised here: without this the compiler sinks
+  // each slot's updates past the N:M and mask branches into one chain at the
+  // slot's next use, keeping every earlier step's error alive (and spilled).
+#pragma unroll
+  for (int t = TO; t < SW_T; ++t) asm volatile("" : "+v"(S.w[t]));
 }
 
 template <int I, bool NM, bool PRESERVE>
@@ -264,13 +263,15 @@ template <bool NM, bool PRESERVE>
 __global__ __launch_bounds__(SW_NT, 4) void sgpt_sweep_kernel(float* __restrict__ W, int64_t rows, int64_t cols,
                                                               const float* __restrict__ hinv, int64_t i1, int count,
                                                               uint8_t* __restrict__ mask,
-                                                              const unsigned* __restrict__ sel, int n, int m,
-                                                              float* __restrict__ losses,
+                                                              const unsigned* __restrict__ hs,
+                                                              unsigned* __restrict__ hs_next, unsigned k, int n,
+                                                              int m, float* __restrict__ losses,
                                                               float* __restrict__ err_out, int64_t lde,
                                                               int err_col) {
   __shared__ float h1[HPK];
   __shared__ float rdg[MAXB];  // 1 / Hinv[i][i], correctly rounded
   __shared__ float dd2[MAXB];  // Hinv[i][i]^2
+  __shared__ unsigned sh[8];
   const int tid = threadIdx.x;
   const int g = tid & (SW_G - 1);
   const int64_t r = (int64_t)blockIdx.x * SW_ROWS + (tid / SW_G);
@@ -302,8 +303,17 @@ __global__ __launch_bounds__(SW_NT, 4) void sgpt_sweep_kernel(float* __restrict_
   __syncthreads();
 
   if (!NM) {
-    const unsigned thresh = sel[HKEY];
-    if (!PRESERVE || sel[HEXT]) {
+    // the block's threshold key from the three histograms; the other set is
+    // cleared for the next block (its last reader, the previous block's
+    // sweep, has finished)
+    unsigned b0, b1, b2, rem;
+    find_bin(hs + H0, NB0, k, sh, b0, rem);
+    find_bin(hs + H1, NB1, rem, sh, b1, rem);
+    find_bin(hs + H2, NB2, rem, sh, b2, rem);
+    const unsigned thresh = (b0 << 23) | (b1 << 12) | b2;
+    if (blockIdx.x == 0)
+      for (int i = tid; i < SET_WORDS; i += SW_NT) hs_next[i] = 0u;
+    if (!PRESERVE || k > hs[HCNT]) {
 #pragma unroll
       for (int t = 0; t < SW_T; ++t) {
         const int col = min(SW_G * t + g, count - 1);
@@ -441,6 +451,7 @@ extern "C" int mi355q_sparsegpt_sweep(float* w_work_dev, int64_t rows, int64_t c
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* err = static_cast<float*>(workspace_dev);
   unsigned* sel = reinterpret_cast<unsigned*>(static_cast<char*>(workspace_dev) + sel_offset(rows, cols, blocksize));
+  int nblock = 0;  // blocks swept so far: block b counts into set b % 2
   const int64_t lde = err_cols(cols, blocksize);
   if (!nm) {
     hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, sel, SEL_WORDS);
@@ -450,18 +461,19 @@ extern "C" int mi355q_sparsegpt_sweep(float* w_work_dev, int64_t rows, int64_t c
   const unsigned nsel = (unsigned)((rows + SEL_ROWS - 1) / SEL_ROWS);
   auto block = [&](int64_t i1, int64_t i2, int64_t s0) {
     const int count = (int)(i2 - i1);
+    unsigned* hs = sel + (nblock & 1) * SET_WORDS;
+    unsigned* hs_next = sel + ((nblock + 1) & 1) * SET_WORDS;
+    ++nblock;
+    const unsigned k = nm ? 0u : (unsigned)kth(rows * count, sparsity);
     if (!nm) {
-      const unsigned k = (unsigned)kth(rows * count, sparsity);
       for (int pass = 0; pass < 3; ++pass) {
         hipLaunchKernelGGL(sgpt_select_kernel, dim3(nsel), dim3(SEL_NT), 0, st, w_work_dev, rows, cols, hinv_dev,
-                           i1, count, mask_dev, sel, pass, k);
+                           i1, count, mask_dev, hs, pass, k);
         MQ_LAUNCH_CHECK();
       }
-      hipLaunchKernelGGL(sgpt_threshold_kernel, dim3(1), dim3(SEL_NT), 0, st, sel, k);
-      MQ_LAUNCH_CHECK();
     }
     launch_prune(nm, preserve, dim3(nwg), st, w_work_dev, rows, cols, hinv_dev, i1, count, mask_dev,
-                 (const unsigned*)sel, prune_n, prune_m, losses_dev, err, lde, (int)(i1 - s0));
+                 (const unsigned*)hs, hs_next, k, prune_n, prune_m, losses_dev, err, lde, (int)(i1 - s0));
     MQ_LAUNCH_CHECK();
     return MI355Q_OK;
   };

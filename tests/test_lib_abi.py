@@ -38,7 +38,7 @@ def test_version_and_workspace_queries():
     assert lib.mi355q_gptq_sweep_workspace_size(768, 768, 128) == 768 * 768 * 4       # fewer columns than a super-block
     assert lib.mi355q_gptq_hinv_workspace_size(4096) >= 2 * 4096 * 4096 * 4
     # SparseGPT: the super-block error buffer plus the radix-select words
-    assert lib.mi355q_sparsegpt_workspace_size(4096, 4096, 128) == 4096 * 1024 * 4 + 4100 * 4
+    assert lib.mi355q_sparsegpt_workspace_size(4096, 4096, 128) == 4096 * 1024 * 4 + 2 * (256 + 2048 + 4096 + 64) * 4
 
 
 @pytest.mark.parametrize("call,needle", [
