@@ -277,6 +277,14 @@ int mi355q_quantize_int(const void* x_dev, mi355q_dtype dtype, int64_t rows, int
 int mi355q_pack_int4_int32(const int8_t* codes_dev, int64_t rows, int64_t cols,
                            int32_t* out_dev, void* stream);
 
+/* The same layout for num_bits in {2, 4, 8}: 32 / num_bits codes per word,
+ * element e at bits num_bits * e, offset-binary (q + 2^(num_bits-1)); out is
+ * [rows, ceil(cols * num_bits / 32)] and positions past a row's end are 0.
+ * Replaces CT pack_to_int32 for pack-quantized W4 / W8 checkpoints (the
+ * compressor call at transformers/compression/compressed_tensors_utils.py:191). */
+int mi355q_pack_int32(const int8_t* codes_dev, int64_t rows, int64_t cols, int num_bits,
+                      int32_t* out_dev, void* stream);
+
 /* utils/pack_int4_to_int8.py:13-28: out[r][k] = (c[r][2k+1] & 15) << 4 |
  * (c[r][2k] & 15).  cols must be even. */
 int mi355q_pack_int4_int8(const int8_t* codes_dev, int64_t rows, int64_t cols,

@@ -237,6 +237,24 @@ __global__ void pack_int4_int32_kernel(const int8_t* codes, int64_t rows, int64_
   }
 }
 
+// General form: 32 / bits codes per word, element e of a word at bits
+// bits * e, offset-binary (q + 2^(bits-1)); words past the row's end read 0.
+__global__ void pack_int32_kernel(const int8_t* codes, int64_t rows, int64_t cols, int bits, int64_t wpr,
+                                  int32_t* out) {
+  const int pf = 32 / bits;
+  const uint32_t off = 1u << (bits - 1), mask = (1u << bits) - 1u;
+  const int64_t words = rows * wpr;
+  for (int64_t w = (int64_t)blockIdx.x * NT + threadIdx.x; w < words; w += (int64_t)gridDim.x * NT) {
+    const int64_t r = w / wpr, k = w % wpr;
+    uint32_t acc = 0;
+    for (int e = 0; e < pf; ++e) {
+      const int64_t c = k * pf + e;
+      if (c < cols) acc |= (((uint32_t)((int)codes[r * cols + c] + (int)off)) & mask) << (bits * e);
+    }
+    out[w] = (int32_t)acc;
+  }
+}
+
 __global__ void pack_int4_int8_kernel(const int8_t* codes, int64_t rows, int64_t cols, int8_t* out) {
   const int64_t n = rows * (cols / 2);
   for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
@@ -606,6 +624,18 @@ extern "C" int mi355q_pack_int4_int32(const int8_t* codes_dev, int64_t rows, int
   MQ_CHECK_ARG((reinterpret_cast<uintptr_t>(codes_dev) & 7) == 0, "pack_int4_int32: codes must be 8-byte aligned");
   hipLaunchKernelGGL(pack_int4_int32_kernel, dim3(grid_for(rows * cols / 8, NT, 1u << 16)), dim3(NT), 0,
                      reinterpret_cast<hipStream_t>(stream), codes_dev, rows, cols, out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_pack_int32(const int8_t* codes_dev, int64_t rows, int64_t cols, int num_bits,
+                                 int32_t* out_dev, void* stream) {
+  MQ_CHECK_ARG(codes_dev && out_dev, "pack_int32: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0, "pack_int32: bad shape");
+  MQ_CHECK_ARG(num_bits == 2 || num_bits == 4 || num_bits == 8, "pack_int32: num_bits must be 2, 4 or 8");
+  const int64_t wpr = (cols + 32 / num_bits - 1) / (32 / num_bits);
+  hipLaunchKernelGGL(pack_int32_kernel, dim3(grid_for(rows * wpr, NT, 1u << 16)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), codes_dev, rows, cols, num_bits, wpr, out_dev);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
 }

@@ -55,6 +55,7 @@ SIGNATURES = {
                                    _i32, _i32, _vp, _vp]),
     "mi355q_pack_int4_int32": (_i32, [_vp, _i64, _i64, _vp, _vp]),
     "mi355q_pack_int4_int8": (_i32, [_vp, _i64, _i64, _vp, _vp]),
+    "mi355q_pack_int32": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp]),
     "mi355q_mxfp4_quantize_pack": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
     "mi355q_mxfp4_dequantize": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "mi355q_quantize_fp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _i64, _i32, _vp, _vp]),

@@ -349,6 +349,17 @@ def pack_int4_int32(codes: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def pack_int32(codes: torch.Tensor, num_bits: int) -> torch.Tensor:
+    """CT pack_to_int32 layout for 2-, 4- or 8-bit codes (rows padded with 0)."""
+    L.require_gpu(codes)
+    codes = codes.contiguous()
+    rows, cols = codes.shape
+    pf = 32 // num_bits
+    out = torch.empty((rows, -(-cols // pf)), dtype=torch.int32, device=codes.device)
+    L.call("mi355q_pack_int32", codes.data_ptr(), rows, cols, int(num_bits), out.data_ptr(), L.stream_of(codes))
+    return out
+
+
 def pack_int4_int8(codes: torch.Tensor) -> torch.Tensor:
     L.require_gpu(codes)
     if codes.dim() != 2:

@@ -40,9 +40,9 @@ def pack_int4_to_int8(t: np.ndarray) -> np.ndarray:
 def pack_to_int32(codes: np.ndarray, num_bits: int = 4) -> np.ndarray:
     rows, cols = codes.shape
     per = 32 // num_bits
-    if cols % per:
-        codes = np.pad(codes, ((0, 0), (0, per - cols % per)))
     v = (codes.astype(np.int32) + (1 << (num_bits - 1))).astype(np.uint32) & ((1 << num_bits) - 1)
+    if cols % per:   # padded after the offset: unused positions hold 0
+        v = np.pad(v, ((0, 0), (0, per - cols % per)))
     v = v.reshape(rows, -1, per)
     shifts = (np.arange(per, dtype=np.uint32) * num_bits)
     return np.bitwise_or.reduce(v << shifts, axis=2).astype(np.uint32).view(np.int32)
