@@ -41,10 +41,11 @@ def parse():
     p.add_argument("--hessian-calls", type=int, default=1,
                    help="split the 64 x 2048 calibration tokens into this many accumulate_hessian calls")
     p.add_argument("--workload", default="gptq_w4a16",
-                   choices=["gptq_w4a16", "mxfp4", "gptq_w8a8", "moe", "decoder", "sparsegpt"],
+                   choices=["gptq_w4a16", "mxfp4", "gptq_w8a8", "moe", "decoder", "sparsegpt", "mse_observer"],
                    help="gptq_w4a16 (default): the headline line; the others measure the remaining "
                         "calibration workloads (MXFP4 pack, W8A8 channel + actorder, MoE experts, "
-                        "Llama-3-8B-shaped decoder layer, SparseGPT 50 %% / 2:4 on a 4096x4096 layer)")
+                        "Llama-3-8B-shaped decoder layer, SparseGPT 50 %% / 2:4 on a 4096x4096 layer, "
+                        "MSE weight observer on 4096x4096 and 14336x4096)")
     return p.parse_args()
 
 
@@ -510,8 +511,35 @@ def bench_sparsegpt(a):
                        "frac_bf16_mfma_peak": round(flop / hess_ms / 1e9 / PEAK_BF16_TFLOPS, 4)}})
 
 
+def bench_mse_observer(a):
+    """memoryless_mse weight observer (20 shrink candidates, norm 2.4): W 4096x4096 int4 group 128 (the step)
+    and W 14336x4096 int8 channel, bf16; the min-max observer beside them."""
+    torch, dev = _setup()
+    from llmcompressor_amd.observers import Observer
+    from llmcompressor_amd.quant_args import QuantizationArgs
+    res = {}
+    for name, shape, kw in (("w4_g128_4096x4096", (4096, 4096), dict(num_bits=4, strategy="group", group_size=128)),
+                            ("w8_channel_14336x4096", (14336, 4096), dict(num_bits=8, strategy="channel"))):
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        w = (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+        def run(obs_name):
+            o = Observer.load_from_registry(obs_name, base_name="weight", args=QuantizationArgs(observer=obs_name, **kw))
+            return o(w).get_qparams()
+
+        ms, _ = _timed(torch, lambda: run("memoryless_mse"), max(a.steps, 10), max(a.warmup, 2))
+        mm_ms, _ = _timed(torch, lambda: run("memoryless_minmax"), max(a.steps, 10), max(a.warmup, 2))
+        evals = w.numel() * 20
+        res[name] = {"ms": round(ms, 4), "minmax_ms": round(mm_ms, 4),
+                     "candidate_evals_per_s": round(evals / ms * 1e3 / 1e9, 2), "unit_evals": "1e9/s"}
+    ms = res["w4_g128_4096x4096"]["ms"]
+    _line("MSE weight observer ms (memoryless_mse, W 4096x4096 bf16, int4 group 128, 20 shrink candidates)", ms,
+          "ms", a, ms, "mse_observer_w4_g128_4096x4096", {"per_shape": res}, dtype="bf16 in, fp32 error sums")
+
+
 OTHER_WORKLOADS = {"mxfp4": bench_mxfp4, "gptq_w8a8": bench_w8a8, "moe": bench_moe, "decoder": bench_decoder,
-                   "sparsegpt": bench_sparsegpt}
+                   "sparsegpt": bench_sparsegpt, "mse_observer": bench_mse_observer}
 
 
 if __name__ == "__main__":

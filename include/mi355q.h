@@ -257,6 +257,27 @@ int mi355q_calculate_qparams(const float* min_dev, const float* max_dev, int64_t
 int mi355q_mx_scales(const float* min_dev, const float* max_dev, int64_t n, int rule,
                      uint8_t* e8m0_out_dev, float* scale_out_dev, void* stream);
 
+/* MSE observer grid search (observers/mse_quant.py:48-130,244-273; the
+ * memoryless_mse / mse observers of observers/mse.py:12-98).  x [rows, cols]
+ * (bf16 or fp32, leading dimension ldx) is split into cells of cell_rows x
+ * cell_cols (clipped at the edges, row-major; a group is 1 x group_size, a
+ * channel 1 x cols, the tensor rows x cols, a block its block shape); min_dev /
+ * max_dev hold each cell's min / max.  For candidate i < total_steps
+ * (= int(maxshrink * grid)) the min / max are scaled by p = 1 - i / grid,
+ * qparams computed as calculate_qparams does in the observed dtype, and the
+ * error is sum |fake_quantize(x) - x|^norm in that dtype (for bf16 with the
+ * exponent rounded to bf16, as torch's pow does); each cell keeps its
+ * first best candidate over the steps before the first run of `patience`
+ * steps without an improvement in any cell.  Writes the chosen min / max
+ * (float values of the observed dtype) to min_out / max_out.  Integer types. */
+size_t mi355q_observe_mse_workspace_size(int64_t rows, int64_t cols, int64_t cell_rows, int64_t cell_cols,
+                                         int total_steps);
+int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
+                       int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric,
+                       int total_steps, int patience, double grid, float norm, const float* min_dev,
+                       const float* max_dev, float* min_out_dev, float* max_out_dev, void* workspace_dev,
+                       size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ quantize / pack
  * Integer quantize of a whole weight with the scale indexing of
  * mi355q_gptq_sweep (g_idx may be NULL: column / group_size):

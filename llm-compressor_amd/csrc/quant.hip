@@ -172,14 +172,13 @@ __global__ void minmax_cells_kernel(const void* x, mi355q_dtype dt, int64_t rows
 // ---------------------------------------------------------------- qparams
 __device__ __forceinline__ float rnd(float v, bool bf16) { return bf16 ? round_to_bf16(v) : v; }
 
-__global__ void qparams_kernel(const float* mn_in, const float* mx_in, int64_t n, float qmin, float qmax,
-                               int symmetric, int strict, int bf16_scale, float* scale_out,
-                               float* zp_out) {
-  const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
-  if (i >= n) return;
-  const bool b = bf16_scale != 0;
-  float mn = fminf(mn_in[i], 0.f), mx = fmaxf(mx_in[i], 0.f);
-  float scale, zp = 0.f;
+// CT calculate_qparams of one (min, max) pair in the statistics dtype (b:
+// bf16, every operation rounded to it) or fp32.
+__device__ __forceinline__ void qparams_one(float mn, float mx, float qmin, float qmax, bool symmetric, bool strict,
+                                            bool b, float& scale, float& zp) {
+  mn = fminf(mn, 0.f);
+  mx = fmaxf(mx, 0.f);
+  zp = 0.f;
   if (strict) {
     float mvp = fmaxf(fabsf(mn), fabsf(mx));
     scale = fmaxf(mvp / qmax, 1e-8f);
@@ -194,8 +193,284 @@ __global__ void qparams_kernel(const float* mn_in, const float* mx_in, int64_t n
     zp = rintf(zp);
   }
   if (!strict && scale == 0.f) scale = b ? 0.0078125f : 1.1920928955078125e-07f;
+}
+
+__global__ void qparams_kernel(const float* mn_in, const float* mx_in, int64_t n, float qmin, float qmax,
+                               int symmetric, int strict, int bf16_scale, float* scale_out,
+                               float* zp_out) {
+  const int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (i >= n) return;
+  float scale, zp;
+  qparams_one(mn_in[i], mx_in[i], qmin, qmax, symmetric != 0, strict != 0, bf16_scale != 0, scale, zp);
   scale_out[i] = scale;
   zp_out[i] = zp;
+}
+
+// ---------------------------------------------------------------- MSE observer
+// observers/mse_quant.py:48-130,244-273.  A matrix is split into cells of
+// cell_rows x cell_cols (clipped at the edges, row-major) - a group, a channel,
+// a block or the whole tensor.  Candidate i < T shrinks the cell's min / max by
+// p = 1 - i / grid; its error is sum |fq(x) - x|^norm with every operation in
+// the observed dtype (bf16: rounded after each op, the sum accumulated in fp32
+// and rounded once).  The first candidate with the smallest error wins, over
+// the steps before the first run of `patience` steps in which no cell
+// improved.
+struct MseArgs {
+  const void* x;
+  int64_t rows, cols, ldx;
+  int64_t ch, cw, ncr, ncc;
+  float qmin, qmax;
+  int T;
+  double grid;
+  float norm;
+  const float* mn;
+  const float* mx;
+};
+
+// bf16 rounding (hardware round-to-nearest-even) when the observed dtype is bf16
+template <bool B>
+__device__ __forceinline__ float rb(float v) { return B ? (float)(__bf16)v : v; }
+
+// torch's pow(tensor, scalar) in the tensor's dtype: 2 as a product, 3 as two
+// products (each rounded to bf16 for a bf16 tensor), 0.5 as a square root;
+// otherwise pow with the exponent first cast to the tensor's dtype (a bf16
+// tensor raises to bf16(norm), e.g. 2.40625 for 2.4).  The caller rounds the
+// result to the dtype.
+template <bool B>
+__device__ __forceinline__ float pow_norm(float a, float norm) {
+  if (norm == 2.f) return a * a;
+  if (norm == 3.f) return B ? rb<true>(a * a) * a : a * a * a;
+  if (norm == 0.5f) return sqrtf(a);
+  return powf(a, B ? rb<true>(norm) : norm);
+}
+
+// A bf16 error |fq(x) - x| takes one of 2^15 non-negative bf16 values, so its
+// rounded power is read from a table of all of them (bf16 bits, 64 KB, held
+// in LDS) built once per call with pow_norm.
+constexpr int POW_TAB = 1 << 15;
+
+__global__ void mse_pow_table_kernel(float norm, uint16_t* tab) {
+  const int i = blockIdx.x * NT + threadIdx.x;
+  if (i < POW_TAB) tab[i] = f32_to_bf16_bits(pow_norm<true>(__uint_as_float((uint32_t)i << 16), norm));
+}
+
+__device__ __forceinline__ float shrink_p(int i, double grid) { return (float)(1.0 - (double)i / grid); }
+
+// |fq(x) - x|^norm of one value with CT fake_quantize (per-token scale s,
+// zero point z; rs = 1 / s correctly rounded), each step in the observed
+// dtype.  bf16: the quotient from the reciprocal with one FMA residual step
+// (the correctly rounded fp32 quotient, then rounded to bf16 as torch does)
+// and the power from the LDS table.
+template <bool B, bool ZP>
+__device__ __forceinline__ float mse_term(float v, float s, float rs, float z, float qmin, float qmax, float norm,
+                                          const uint16_t* tab) {
+  float t;
+  if (B) {
+    const float q0 = v * rs;
+    t = rb<true>(fmaf(fmaf(-s, q0, v), rs, q0));
+  } else {
+    t = v / s;
+  }
+  if (ZP) t = rb<B>(t + z);
+  t = rintf(fminf(fmaxf(t, qmin), qmax));
+  if (ZP) t = rb<B>(t - z);
+  const float d = fabsf(rb<B>(rb<B>(t * s) - v));
+  if (B) return __uint_as_float((uint32_t)tab[__float_as_uint(d) >> 16] << 16);
+  return pow_norm<false>(d, norm);
+}
+
+__device__ __forceinline__ void cell_geom(const MseArgs& a, int64_t cell, int64_t& r0, int64_t& c0, int64_t& cwe,
+                                          int64_t& n) {
+  const int64_t cr = cell / a.ncc, cq = cell % a.ncc;
+  r0 = cr * a.ch;
+  c0 = cq * a.cw;
+  cwe = min(a.cw, a.cols - c0);
+  n = cwe * min(a.ch, a.rows - r0);
+}
+
+template <bool B>
+__device__ __forceinline__ void load_pow_table(uint16_t* tab, const uint16_t* table) {
+  if (B) {
+    for (int i = threadIdx.x; i < POW_TAB / 8; i += NT)
+      reinterpret_cast<uint4*>(tab)[i] = reinterpret_cast<const uint4*>(table)[i];
+    __syncthreads();
+  }
+}
+
+// Cells of at most 8 * LG <= 512 values: LG lanes per cell, 8 values per
+// lane; workgroups loop over the cells (the table is loaded once each).
+template <bool B, bool ZP>
+__global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log2, const uint16_t* table,
+                                                           float* err) {
+  __shared__ uint16_t tab[B ? POW_TAB : 8];
+  load_pow_table<B>(tab, table);
+  const int LG = 1 << lg_log2, per_wg = NT >> lg_log2;
+  const int64_t ncells = a.ncr * a.ncc;
+  const int l = threadIdx.x & (LG - 1);
+  for (int64_t base = (int64_t)blockIdx.x * per_wg; base < ncells; base += (int64_t)gridDim.x * per_wg) {
+    const int64_t cell_raw = base + (threadIdx.x >> lg_log2);
+    const bool live = cell_raw < ncells;
+    const int64_t cell = live ? cell_raw : ncells - 1;
+    int64_t r0, c0, cwe, n;
+    cell_geom(a, cell, r0, c0, cwe, n);
+    float v[8];
+    bool ok[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int64_t e = l + (int64_t)k * LG;
+      ok[k] = e < n;
+      const int64_t ee = ok[k] ? e : 0;
+      v[k] = load_elem(a.x, B ? MI355Q_BF16 : MI355Q_F32, (r0 + ee / cwe) * a.ldx + c0 + ee % cwe);
+    }
+    const float mn = a.mn[cell], mx = a.mx[cell];
+    for (int i = 0; i < a.T; ++i) {
+      const float p = shrink_p(i, a.grid);
+      float s, z;
+      qparams_one(rb<B>(mn * p), rb<B>(mx * p), a.qmin, a.qmax, !ZP, false, B, s, z);
+      const float rs = 1.f / s;
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (ok[k]) acc += mse_term<B, ZP>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab);
+      for (int o = 1; o < LG; o <<= 1) acc += __shfl_xor(acc, o, LG);
+      if (live && l == 0) err[cell * a.T + i] = rb<B>(acc);
+    }
+  }
+}
+
+// Larger cells: chunks of 16 * NT values, one fp32 partial sum per chunk and
+// candidate (summed in chunk order by mse_flags_kernel); workgroups loop over
+// the (cell, chunk) items.
+template <bool B, bool ZP>
+__global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nchunk, const uint16_t* table,
+                                                           float* part) {
+  __shared__ uint16_t tab[B ? POW_TAB : 8];
+  __shared__ float red[NT / 64];
+  load_pow_table<B>(tab, table);
+  const int tid = threadIdx.x;
+  const int64_t nitems = a.ncr * a.ncc * nchunk;
+  for (int64_t item = blockIdx.x; item < nitems; item += gridDim.x) {
+    const int64_t cell = item / nchunk, chunk = item % nchunk;
+    int64_t r0, c0, cwe, n;
+    cell_geom(a, cell, r0, c0, cwe, n);
+    float v[16];
+    bool ok[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int64_t e = chunk * (16 * NT) + (int64_t)k * NT + tid;
+      ok[k] = e < n;
+      const int64_t ee = ok[k] ? e : 0;
+      v[k] = load_elem(a.x, B ? MI355Q_BF16 : MI355Q_F32, (r0 + ee / cwe) * a.ldx + c0 + ee % cwe);
+    }
+    const float mn = a.mn[cell], mx = a.mx[cell];
+    for (int i = 0; i < a.T; ++i) {
+      const float p = shrink_p(i, a.grid);
+      float s, z;
+      qparams_one(rb<B>(mn * p), rb<B>(mx * p), a.qmin, a.qmax, !ZP, false, B, s, z);
+      const float rs = 1.f / s;
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (ok[k]) acc += mse_term<B, ZP>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab);
+      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+      if ((tid & 63) == 0) red[tid >> 6] = acc;
+      __syncthreads();
+      if (tid == 0) part[(cell * nchunk + chunk) * a.T + i] = ((red[0] + red[1]) + red[2]) + red[3];
+      __syncthreads();
+    }
+  }
+}
+
+// Per cell: the errors (from the chunk partials when nchunk > 0) and, for
+// every step, whether any cell improved its best error at it.
+template <bool B>
+__global__ void mse_flags_kernel(const float* part, int64_t nchunk, float* err, int64_t ncells, int T, int* any) {
+  const int64_t cell_raw = (int64_t)blockIdx.x * NT + threadIdx.x;
+  const bool live = cell_raw < ncells;
+  const int64_t cell = live ? cell_raw : ncells - 1;
+  float best = B ? 3.3895313892515355e38f : 3.4028234663852886e38f;
+  for (int i = 0; i < T; ++i) {
+    float e;
+    if (nchunk > 0) {
+      float acc = 0.f;
+      for (int64_t c = 0; c < nchunk; ++c) acc += part[(cell * nchunk + c) * T + i];
+      e = rb<B>(acc);
+      if (live) err[cell * T + i] = e;
+    } else {
+      e = err[cell * T + i];
+    }
+    const bool imp = live && e < best;
+    if (imp) best = e;
+    if (__any(imp) && (threadIdx.x & 63) == 0) any[i] = 1;
+  }
+}
+
+// The steps the reference evaluates end at the first run of `patience`
+// steps without an improvement anywhere; each cell takes its first best
+// candidate among them.
+template <bool B>
+__global__ void mse_select_kernel(const float* err, const int* any, int64_t ncells, int T, int patience,
+                                  double grid, const float* mn, const float* mx, float* mn_out, float* mx_out) {
+  const int64_t cell = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (cell >= ncells) return;
+  int last = T - 1, cnt = 0;
+  for (int i = 0; i < T; ++i) {
+    if (any[i]) {
+      cnt = 0;
+    } else if (++cnt >= patience) {
+      last = i;
+      break;
+    }
+  }
+  float best = B ? 3.3895313892515355e38f : 3.4028234663852886e38f;
+  int bi = -1;
+  for (int i = 0; i <= last; ++i) {
+    const float e = err[cell * T + i];
+    if (e < best) {
+      best = e;
+      bi = i;
+    }
+  }
+  if (bi >= 0) {
+    const float p = shrink_p(bi, grid);
+    mn_out[cell] = rb<B>(mn[cell] * p);
+    mx_out[cell] = rb<B>(mx[cell] * p);
+  } else {
+    mn_out[cell] = mn[cell];
+    mx_out[cell] = mx[cell];
+  }
+}
+
+__global__ void fill_i32_kernel(int* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+struct MsePlan {
+  int64_t ncells, nchunk;
+  int lg_log2;        // small path: log2 lanes per cell; -1: large path
+  size_t off_part, off_any, off_tab, total;
+};
+
+MsePlan plan_mse(int64_t rows, int64_t cols, int64_t ch, int64_t cw, int T) {
+  MsePlan pl{};
+  pl.ncells = ((rows + ch - 1) / ch) * ((cols + cw - 1) / cw);
+  const int64_t nmax = min(ch, rows) * min(cw, cols);
+  pl.lg_log2 = -1;
+  for (int lg = 0; lg <= 6; ++lg)
+    if (8 * (int64_t(1) << lg) >= nmax) {
+      pl.lg_log2 = lg;
+      break;
+    }
+  pl.nchunk = pl.lg_log2 >= 0 ? 0 : (nmax + 16 * NT - 1) / (16 * NT);
+  auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  size_t off = align((size_t)pl.ncells * T * sizeof(float));
+  pl.off_part = off;
+  off = align(off + (size_t)pl.ncells * pl.nchunk * T * sizeof(float));
+  pl.off_any = off;
+  off = align(off + (size_t)T * sizeof(int));
+  pl.off_tab = off;
+  pl.total = align(off + (size_t)POW_TAB * sizeof(uint16_t));
+  return pl;
 }
 
 // ---------------------------------------------------------------- int quantize
@@ -582,6 +857,79 @@ extern "C" int mi355q_calculate_qparams(const float* min_dev, const float* max_d
   hipLaunchKernelGGL(qparams_kernel, dim3(grid_for(n, NT, 1u << 30)), dim3(NT), 0,
                      reinterpret_cast<hipStream_t>(stream), min_dev, max_dev, n, qmin, qmax, symmetric,
                      strict, scale_dtype == MI355Q_BF16 ? 1 : 0, scale_out_dev, zp_out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" size_t mi355q_observe_mse_workspace_size(int64_t rows, int64_t cols, int64_t cell_rows,
+                                                   int64_t cell_cols, int total_steps) {
+  if (rows <= 0 || cols <= 0 || cell_rows <= 0 || cell_cols <= 0 || total_steps <= 0) return 0;
+  return plan_mse(rows, cols, cell_rows, cell_cols, total_steps).total;
+}
+
+extern "C" int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
+                                  int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric,
+                                  int total_steps, int patience, double grid, float norm, const float* min_dev,
+                                  const float* max_dev, float* min_out_dev, float* max_out_dev,
+                                  void* workspace_dev, size_t workspace_bytes, void* stream) {
+  MQ_CHECK_ARG(x_dev && min_dev && max_dev && min_out_dev && max_out_dev, "observe_mse: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "observe_mse: bad shape");
+  MQ_CHECK_ARG(cell_rows > 0 && cell_cols > 0, "observe_mse: bad cell shape");
+  MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F32, "observe_mse: dtype must be bf16 or fp32");
+  MQ_CHECK_ARG(qmin < 0.f && qmax > 0.f, "observe_mse: range must straddle zero");
+  MQ_CHECK_ARG(total_steps >= 0 && grid != 0.0, "observe_mse: bad search grid");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t ncells = ((rows + cell_rows - 1) / cell_rows) * ((cols + cell_cols - 1) / cell_cols);
+  if (total_steps == 0) {
+    MQ_CHECK_HIP(hipMemcpyAsync(min_out_dev, min_dev, ncells * sizeof(float), hipMemcpyDeviceToDevice, st));
+    MQ_CHECK_HIP(hipMemcpyAsync(max_out_dev, max_dev, ncells * sizeof(float), hipMemcpyDeviceToDevice, st));
+    return MI355Q_OK;
+  }
+  const MsePlan pl = plan_mse(rows, cols, cell_rows, cell_cols, total_steps);
+  MQ_CHECK_ARG(workspace_dev && workspace_bytes >= pl.total, "observe_mse: workspace too small (%zu < %zu)",
+               workspace_bytes, pl.total);
+  char* ws = static_cast<char*>(workspace_dev);
+  float* err = reinterpret_cast<float*>(ws);
+  float* part = reinterpret_cast<float*>(ws + pl.off_part);
+  int* any = reinterpret_cast<int*>(ws + pl.off_any);
+  uint16_t* tab = reinterpret_cast<uint16_t*>(ws + pl.off_tab);
+  MseArgs a{x_dev, rows, cols, ldx, cell_rows, cell_cols, (rows + cell_rows - 1) / cell_rows,
+            (cols + cell_cols - 1) / cell_cols, qmin, qmax, total_steps, grid, norm, min_dev, max_dev};
+  const bool b = dtype == MI355Q_BF16, zp = symmetric == 0;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(NT), 0, st, any, total_steps);
+  MQ_LAUNCH_CHECK();
+  if (b) {
+    hipLaunchKernelGGL(mse_pow_table_kernel, dim3(POW_TAB / NT), dim3(NT), 0, st, norm, tab);
+    MQ_LAUNCH_CHECK();
+  }
+  constexpr int64_t kMaxWg = 1024;  // persistent workgroups (each loads the power table once)
+  if (pl.lg_log2 >= 0) {
+    const int64_t per_wg = NT >> pl.lg_log2;
+    const dim3 g((unsigned)min((ncells + per_wg - 1) / per_wg, kMaxWg));
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.lg_log2, tab, err); };
+    if (b) {
+      if (zp) go(mse_err_small_kernel<true, true>); else go(mse_err_small_kernel<true, false>);
+    } else {
+      if (zp) go(mse_err_small_kernel<false, true>); else go(mse_err_small_kernel<false, false>);
+    }
+  } else {
+    const dim3 g((unsigned)min(ncells * pl.nchunk, kMaxWg));
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.nchunk, tab, part); };
+    if (b) {
+      if (zp) go(mse_err_large_kernel<true, true>); else go(mse_err_large_kernel<true, false>);
+    } else {
+      if (zp) go(mse_err_large_kernel<false, true>); else go(mse_err_large_kernel<false, false>);
+    }
+  }
+  MQ_LAUNCH_CHECK();
+  const dim3 gc((unsigned)((ncells + NT - 1) / NT));
+  if (b) hipLaunchKernelGGL(mse_flags_kernel<true>, gc, dim3(NT), 0, st, part, pl.nchunk, err, ncells, total_steps, any);
+  else   hipLaunchKernelGGL(mse_flags_kernel<false>, gc, dim3(NT), 0, st, part, pl.nchunk, err, ncells, total_steps, any);
+  MQ_LAUNCH_CHECK();
+  if (b) hipLaunchKernelGGL(mse_select_kernel<true>, gc, dim3(NT), 0, st, err, any, ncells, total_steps, patience,
+                            grid, min_dev, max_dev, min_out_dev, max_out_dev);
+  else   hipLaunchKernelGGL(mse_select_kernel<false>, gc, dim3(NT), 0, st, err, any, ncells, total_steps, patience,
+                            grid, min_dev, max_dev, min_out_dev, max_out_dev);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
 }

@@ -1,4 +1,4 @@
-"""Min-max observers backed by the gfx950 reduction kernels.
+"""Min-max and MSE observers backed by the gfx950 kernels.
 
 Mirrors ``observers/base.py:29-206`` and ``observers/min_max.py:16-110``:
 the same registry names (``memoryless_minmax``, ``static_minmax``,
@@ -7,7 +7,9 @@ the same registry names (``memoryless_minmax``, ``static_minmax``,
 ``observers/helpers.py:63-131`` flattens), weight observers that keep their
 first statistics until ``get_qparams`` deletes them, and ``get_qparams``
 returning ``{"scale", "zero_point", "global_scale"}`` with the scale in the
-observed dtype (bf16 for a bf16 weight).
+observed dtype (bf16 for a bf16 weight).  ``memoryless_mse`` / ``mse``
+(``observers/mse.py:12-98``) shrink those min / max by the grid search of
+``observers/mse_quant.py:19-273`` in one kernel pass over the values.
 """
 from __future__ import annotations
 
@@ -171,4 +173,75 @@ class MinMaxObserver(Observer):
             c = self.avg_constant
             mn = self.min_vals * (1.0 - c) + mn * c
             mx = self.max_vals * (1.0 - c) + mx * c
+        self.min_vals, self.max_vals = mn, mx
+
+
+class _MSEObserver(Observer):
+    """Grid-searched min / max (``observers/mse.py:12-49``): ``maxshrink``
+    (0.20), ``patience`` (5), ``grid`` (100), ``norm`` (2.4) and ``chunk_size``
+    (5; only validated: the search is one kernel pass) from observer_kwargs."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        kw = self.args.observer_kwargs
+        self.maxshrink = kw.get("maxshrink", 0.20)
+        self.patience = kw.get("patience", 5)
+        self.grid = kw.get("grid", 100.0)
+        self.norm = kw.get("norm", 2.4)
+        self.chunk_size = kw.get("chunk_size", 5)
+        if self.chunk_size <= 0:
+            raise ValueError(f"chunk_size must be positive, got {self.chunk_size}")
+
+    def _cells(self, observed: torch.Tensor):
+        """(2-D values, cell rows, cell cols) of the strategy's groups."""
+        a, s = self.args, self.args.strategy
+        if self.is_weight_obs:
+            rows, cols = observed.shape
+            cell = {QuantizationStrategy.TENSOR: (rows, cols), QuantizationStrategy.CHANNEL: (1, cols),
+                    QuantizationStrategy.GROUP: (1, a.group_size)}.get(s)
+            if s == QuantizationStrategy.BLOCK:
+                cell = tuple(a.block_structure)
+            if cell is None:
+                raise ValueError(f"{s.value} quantization cannot be observed for weights here")
+            return observed, cell[0], cell[1]
+        x2 = observed.reshape(-1, observed.shape[-1])
+        if s == QuantizationStrategy.TENSOR:
+            return x2, x2.shape[0], x2.shape[1]
+        if s == QuantizationStrategy.GROUP:
+            return x2, x2.shape[0], a.group_size
+        raise ValueError(f"{s.value} quantization cannot be observed for activations here")
+
+    def _min_max(self, observed: torch.Tensor):
+        a = self.args
+        if a.type != QuantizationType.INT or a.is_mx:
+            raise NotImplementedError("MSE observers for float types are not provided by this build")
+        mn, mx = super()._min_max(observed)
+        x2, ch, cw = self._cells(observed)
+        qmin, qmax = a.q_range()
+        mn2, mx2 = ops.observe_mse(x2, ch, cw, mn.reshape(-1), mx.reshape(-1), qmin, qmax, a.symmetric,
+                                   int(self.maxshrink * self.grid), self.patience, self.grid, self.norm)
+        return mn2.reshape(mn.shape), mx2.reshape(mx.shape)
+
+
+@Observer.register("memoryless_mse")
+class MemorylessMSEObserver(_MSEObserver):
+    def update_statistics_from_observed(self, mn, mx):
+        self.min_vals, self.max_vals = mn, mx
+
+
+@Observer.register("mse")
+class MovingAverageMSEObserver(_MSEObserver):
+    """The grid search's min / max, interpolated into the running statistics
+    with ``averaging_constant`` (0.01) after the first observation
+    (``observers/mse.py:51-98``, ``helpers.py:219-221``)."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.avg_constant = self.args.observer_kwargs.get("averaging_constant", 0.01)
+
+    def update_statistics_from_observed(self, mn, mx):
+        if self.has_statistics and self.avg_constant != 1.0:
+            c = self.avg_constant
+            mn = (self.min_vals * (1.0 - c)) + (mn * c)
+            mx = (self.max_vals * (1.0 - c)) + (mx * c)
         self.min_vals, self.max_vals = mn, mx

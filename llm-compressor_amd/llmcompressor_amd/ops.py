@@ -349,6 +349,26 @@ def pack_int4_int32(codes: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def observe_mse(x: torch.Tensor, cell_rows: int, cell_cols: int, mn: torch.Tensor, mx: torch.Tensor, qmin: float,
+                qmax: float, symmetric: bool, total_steps: int, patience: int, grid: float, norm: float):
+    """MSE grid search over the cells of x (see ``mi355q_observe_mse``): returns
+    the chosen (min, max) per cell as fp32 tensors shaped like ``mn``."""
+    L.require_gpu(x, mn, mx)
+    if x.dim() != 2 or x.stride(1) != 1:
+        x = x.reshape(-1, x.shape[-1]).contiguous()
+    rows, cols = x.shape
+    mn32, mx32 = mn.to(torch.float32).contiguous(), mx.to(torch.float32).contiguous()
+    out_mn, out_mx = torch.empty_like(mn32), torch.empty_like(mx32)
+    lib = L.lib()
+    ws = _ws(lib.mi355q_observe_mse_workspace_size(rows, cols, cell_rows, cell_cols, total_steps), x.device)
+    L.check(lib.mi355q_observe_mse(x.data_ptr(), _dt(x), rows, cols, x.stride(0), cell_rows, cell_cols,
+                                   C.c_float(qmin), C.c_float(qmax), 1 if symmetric else 0, int(total_steps),
+                                   int(patience), C.c_double(grid), C.c_float(norm), mn32.data_ptr(), mx32.data_ptr(),
+                                   out_mn.data_ptr(), out_mx.data_ptr(), L.ptr(ws), 0 if ws is None else ws.numel(),
+                                   L.stream_of(x)))
+    return out_mn, out_mx
+
+
 def pack_int32(codes: torch.Tensor, num_bits: int) -> torch.Tensor:
     """CT pack_to_int32 layout for 2-, 4- or 8-bit codes (rows padded with 0)."""
     L.require_gpu(codes)

@@ -19,6 +19,12 @@ Zero scales are replaced by the scale dtype's epsilon (CT ``_get_dtype_eps``);
 only exact zeros are affected, which the tests above do not reach: parity
 unpinned for that corner.
 
+MSE observers (``mse_grid_search``, ``observers/mse_quant.py:19-130,244-273``,
+eager path, and ``observers/mse.py:12-98``) are pinned by the known-answer table
+of ``tests/llmcompressor/observers/test_mse.py:9-43`` (eight strategy /
+symmetry cases, loss to 1e-10) and by the brute-force argmin over the same
+candidates.
+
 MXFP4 shared scale (``mx_scale_exponent``) is parity unpinned: no reference
 test covers it and CT is absent.  Two rules are provided:
 
@@ -227,3 +233,66 @@ def global_scale_from_stats(stats):
         gabs = torch.max(gabs, -mn.min())
         gabs = torch.max(gabs, mx.max())
     return generate_gparam(-gabs.reshape(1), gabs.reshape(1))
+
+
+# ---------------------------------------------------------------- MSE observers
+def mse_grid_search(observed: torch.Tensor, args: OArgs, maxshrink: float = 0.20, patience: int = 5,
+                    grid: float = 100.0, norm: float = 2.4, return_steps: bool = False):
+    """``observers/mse_quant.py:48-130`` (eager): min / max of each group (dims
+    0 and -1 reduced) shrunk by p = 1 - i / grid for i < int(maxshrink * grid);
+    per group the first pair with the smallest error sum |q - x|^norm (in the
+    observed dtype), stopping once ``patience`` consecutive steps improve no
+    group.  ``return_steps`` also returns the number of steps evaluated."""
+    from dataclasses import replace
+
+    from .fake_quant import fake_quantize
+
+    min_val = torch.amin(observed, dim=(0, -1))
+    max_val = torch.amax(observed, dim=(0, -1))
+    best_error = torch.full_like(min_val, torch.finfo(min_val.dtype).max)
+    best_min, best_max = min_val.clone(), max_val.clone()
+    total_steps = int(maxshrink * grid)
+    token_args = replace(args, strategy="token")
+    no_improve, steps = 0, 0
+    for i in range(total_steps):
+        steps += 1
+        p = 1 - i / grid
+        smin, smax = min_val * p, max_val * p
+        scale, zp = calculate_qparams(smin, smax, args)
+        q = fake_quantize(observed, scale.unsqueeze(-1), zp.unsqueeze(-1), token_args).to(observed.dtype)
+        err = torch.sum((q - observed).abs().pow(norm), dim=(0, -1))
+        improved = err < best_error
+        if torch.any(improved):
+            best_error[improved] = err[improved]
+            best_min[improved] = smin[improved]
+            best_max[improved] = smax[improved]
+            no_improve = 0
+        else:
+            no_improve += 1
+            if no_improve >= patience:
+                break
+    return (best_min, best_max, steps) if return_steps else (best_min, best_max)
+
+
+class OMSE(OMinMax):
+    """``memoryless_mse`` / ``mse`` (``observers/mse.py:12-98``): the grid
+    search's min / max as statistics; ``mse`` interpolates later observations
+    into them (``helpers.py:219-221``, ``averaging_constant``)."""
+
+    def __init__(self, kind: str, base_name: str, args: OArgs):
+        super().__init__(kind, base_name, args)
+        kw = args.observer_kwargs or {}
+        self.maxshrink, self.patience = kw.get("maxshrink", 0.20), kw.get("patience", 5)
+        self.grid, self.norm = kw.get("grid", 100.0), kw.get("norm", 2.4)
+
+    def __call__(self, observed: torch.Tensor):
+        if observed.numel() == 0 or (self.base_name == "weight" and self.has_statistics):
+            return self
+        flat = flatten_weight(observed, self.args) if self.base_name == "weight" else \
+            flatten_activation(observed, self.args)
+        mn, mx = mse_grid_search(flat, self.args, self.maxshrink, self.patience, self.grid, self.norm)
+        if self.kind == "mse" and self.has_statistics and self.avg != 1.0:
+            mn = self.min_vals * (1.0 - self.avg) + mn * self.avg
+            mx = self.max_vals * (1.0 - self.avg) + mx * self.avg
+        self.min_vals, self.max_vals = mn, mx
+        return self

@@ -201,3 +201,61 @@ def test_int_round_half_even_and_clamp():
     args = OArgs(num_bits=4)
     q = ofq.quantize(torch.tensor([0.5, 1.5, 2.5, -0.5, 7.6, -9.0]), torch.tensor(1.0), None, args)
     assert q.tolist() == [0.0, 2.0, 2.0, -0.0, 7.0, -8.0]
+
+
+@pytest.mark.parametrize("case", GOLD["mse_observer"]["cases"], ids=lambda c: f"{c['strategy']}-{c['symmetric']}")
+def test_mse_observer_known_losses(case):
+    """test_mse.py:9-43: the MSE observer's qparams give the table's loss."""
+    from oracle.fake_quant import fake_quantize_weight
+    from oracle.observers import OMSE
+    g = GOLD["mse_observer"]
+    st = case["strategy"]
+    a = OArgs(num_bits=g["num_bits"], strategy=st, symmetric=case["symmetric"],
+              group_size=g["group_size_for_group"] if st == "group" else None,
+              block_structure=g["block_structure_for_block"] if st == "block" else None, observer="mse")
+    t = torch.arange(24).reshape((6, 4)) / 24
+    qp = OMSE("mse", "weight", a)(t).get_qparams()
+    q = fake_quantize_weight(t, qp["scale"], qp["zero_point"], a)
+    loss = (torch.sum((t - q).abs().pow(2)) / t.numel()).item()
+    assert loss == pytest.approx(case["exp_loss"], abs=g["abs_tol"])
+
+
+def _mse_candidates_fp64(w, a, p_list, norm):
+    """Error of every shrink candidate per group, evaluated in fp64 from the
+    weight QDQ path (the lifecycle-pinned one), independent of the search."""
+    flat = oobs.flatten_weight(w, a)
+    mn, mx = torch.amin(flat, dim=(0, -1)), torch.amax(flat, dim=(0, -1))
+    errs = []
+    for p in p_list:
+        s, z = oobs.calculate_qparams(mn * p, mx * p, a)
+        q = ofq.fake_quantize_weight(w, s, z, a)
+        d = (q.double() - w.double()).abs().pow(norm)
+        errs.append(oobs.flatten_weight(d, a).sum(dim=(0, -1)))
+    return torch.stack(errs)  # [candidates, *groups]
+
+
+@pytest.mark.parametrize("symmetric", [True, False])
+def test_mse_search_picks_the_smallest_candidate(symmetric):
+    w = (torch.randn(16, 256, generator=torch.Generator().manual_seed(7)) * 0.02).to(torch.bfloat16)
+    w[3, 5] = 0.3   # an outlier group, where shrinking pays
+    a = OArgs(num_bits=4, strategy="group", group_size=32, symmetric=symmetric)
+    mn, mx, steps = oobs.mse_grid_search(oobs.flatten_weight(w, a), a, return_steps=True)
+    ps = [1 - i / 100.0 for i in range(steps)]
+    errs = _mse_candidates_fp64(w, a, ps, 2.4)
+    flat = oobs.flatten_weight(w, a)
+    mn0, mx0 = torch.amin(flat, dim=(0, -1)), torch.amax(flat, dim=(0, -1))
+    chosen = torch.stack([(mn0 * p == mn) & (mx0 * p == mx) for p in ps]).float().argmax(0)
+    got = errs.gather(0, chosen.unsqueeze(0))[0]
+    # bf16 sums decide the search: within their resolution of the true minimum
+    assert torch.all(got <= errs.min(0).values * 1.01 + 1e-30)
+
+
+def test_mse_search_stops_after_patience_without_improvement():
+    """A constant group: shrinking only moves the clamped code further away,
+    so step 0 is best, the search stops after 1 + patience steps and keeps
+    min / max."""
+    a = OArgs(num_bits=8, strategy="channel", symmetric=True)
+    w = torch.full((4, 64), 0.25)
+    mn, mx, steps = oobs.mse_grid_search(oobs.flatten_weight(w, a), a, patience=5, return_steps=True)
+    assert steps == 6 and torch.equal(mx, torch.full((4, 1), 0.25)) and torch.equal(mn, mx)
+    assert oobs.mse_grid_search(oobs.flatten_weight(w, a), a, maxshrink=0.0, return_steps=True)[2] == 0
