@@ -278,6 +278,25 @@ int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int6
                        const float* max_dev, float* min_out_dev, float* max_out_dev, void* workspace_dev,
                        size_t workspace_bytes, void* stream);
 
+/* The imatrix observer's search (observers/imatrix.py:289-440): as
+ * mi355q_observe_mse with total_steps = max(1, int(maxshrink * grid)) + 1,
+ * the error |fq(x) - x|^norm computed and summed in fp32 (fq in the observed
+ * dtype) and weighted by importance_dev[column] (fp32 [cols], normalised E[x^2];
+ * NULL: uniform), and no early stop when patience is 0. */
+int mi355q_observe_imatrix_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
+                               int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric,
+                               int total_steps, int patience, double grid, float norm,
+                               const float* importance_dev, const float* min_dev, const float* max_dev,
+                               float* min_out_dev, float* max_out_dev, void* workspace_dev,
+                               size_t workspace_bytes, void* stream);
+
+/* sum_dev[c] += sum_r x[r][c]^2 in fp32 (fixed summation order): the imatrix
+ * observer's per-input-channel accumulation (observers/imatrix.py:92-121).
+ * Workspace from mi355q_column_sumsq_workspace_size. */
+size_t mi355q_column_sumsq_workspace_size(int64_t rows, int64_t cols);
+int mi355q_column_sumsq(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
+                        float* sum_dev, void* workspace_dev, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ quantize / pack
  * Integer quantize of a whole weight with the scale indexing of
  * mi355q_gptq_sweep (g_idx may be NULL: column / group_size):

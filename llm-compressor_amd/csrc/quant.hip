@@ -225,6 +225,7 @@ struct MseArgs {
   float norm;
   const float* mn;
   const float* mx;
+  const float* imp;  // weighted (imatrix) mode: per-column importance, or NULL
 };
 
 // bf16 rounding (hardware round-to-nearest-even) when the observed dtype is bf16
@@ -261,9 +262,11 @@ __device__ __forceinline__ float shrink_p(int i, double grid) { return (float)(1
 // dtype.  bf16: the quotient from the reciprocal with one FMA residual step
 // (the correctly rounded fp32 quotient, then rounded to bf16 as torch does)
 // and the power from the LDS table.
-template <bool B, bool ZP>
+// IM (imatrix observer): |fq(x) - x| and its power in fp32 (fq in the
+// observed dtype), times the column's importance w.
+template <bool B, bool ZP, bool IM>
 __device__ __forceinline__ float mse_term(float v, float s, float rs, float z, float qmin, float qmax, float norm,
-                                          const uint16_t* tab) {
+                                          const uint16_t* tab, float w) {
   float t;
   if (B) {
     const float q0 = v * rs;
@@ -274,6 +277,7 @@ __device__ __forceinline__ float mse_term(float v, float s, float rs, float z, f
   if (ZP) t = rb<B>(t + z);
   t = rintf(fminf(fmaxf(t, qmin), qmax));
   if (ZP) t = rb<B>(t - z);
+  if (IM) return pow_norm<false>(fabsf(rb<B>(t * s) - v), norm) * w;
   const float d = fabsf(rb<B>(rb<B>(t * s) - v));
   if (B) return __uint_as_float((uint32_t)tab[__float_as_uint(d) >> 16] << 16);
   return pow_norm<false>(d, norm);
@@ -299,11 +303,12 @@ __device__ __forceinline__ void load_pow_table(uint16_t* tab, const uint16_t* ta
 
 // Cells of at most 8 * LG <= 512 values: LG lanes per cell, 8 values per
 // lane; workgroups loop over the cells (the table is loaded once each).
-template <bool B, bool ZP>
+template <bool B, bool ZP, bool IM>
 __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log2, const uint16_t* table,
                                                            float* err) {
-  __shared__ uint16_t tab[B ? POW_TAB : 8];
-  load_pow_table<B>(tab, table);
+  constexpr bool TAB = B && !IM;
+  __shared__ uint16_t tab[TAB ? POW_TAB : 8];
+  load_pow_table<TAB>(tab, table);
   const int LG = 1 << lg_log2, per_wg = NT >> lg_log2;
   const int64_t ncells = a.ncr * a.ncc;
   const int l = threadIdx.x & (LG - 1);
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log
     const int64_t cell = live ? cell_raw : ncells - 1;
     int64_t r0, c0, cwe, n;
     cell_geom(a, cell, r0, c0, cwe, n);
-    float v[8];
+    float v[8], w[8];
     bool ok[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -321,6 +326,7 @@ __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log
       ok[k] = e < n;
       const int64_t ee = ok[k] ? e : 0;
       v[k] = load_elem(a.x, B ? MI355Q_BF16 : MI355Q_F32, (r0 + ee / cwe) * a.ldx + c0 + ee % cwe);
+      w[k] = (IM && a.imp) ? a.imp[c0 + ee % cwe] : 1.f;
     }
     const float mn = a.mn[cell], mx = a.mx[cell];
     for (int i = 0; i < a.T; ++i) {
@@ -331,9 +337,9 @@ __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (ok[k]) acc += mse_term<B, ZP>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab);
+        if (ok[k]) acc += mse_term<B, ZP, IM>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab, w[k]);
       for (int o = 1; o < LG; o <<= 1) acc += __shfl_xor(acc, o, LG);
-      if (live && l == 0) err[cell * a.T + i] = rb<B>(acc);
+      if (live && l == 0) err[cell * a.T + i] = IM ? acc : rb<B>(acc);
     }
   }
 }
@@ -341,19 +347,20 @@ __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log
 // Larger cells: chunks of 16 * NT values, one fp32 partial sum per chunk and
 // candidate (summed in chunk order by mse_flags_kernel); workgroups loop over
 // the (cell, chunk) items.
-template <bool B, bool ZP>
+template <bool B, bool ZP, bool IM>
 __global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nchunk, const uint16_t* table,
                                                            float* part) {
-  __shared__ uint16_t tab[B ? POW_TAB : 8];
+  constexpr bool TAB = B && !IM;
+  __shared__ uint16_t tab[TAB ? POW_TAB : 8];
   __shared__ float red[NT / 64];
-  load_pow_table<B>(tab, table);
+  load_pow_table<TAB>(tab, table);
   const int tid = threadIdx.x;
   const int64_t nitems = a.ncr * a.ncc * nchunk;
   for (int64_t item = blockIdx.x; item < nitems; item += gridDim.x) {
     const int64_t cell = item / nchunk, chunk = item % nchunk;
     int64_t r0, c0, cwe, n;
     cell_geom(a, cell, r0, c0, cwe, n);
-    float v[16];
+    float v[16], w[16];
     bool ok[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -361,6 +368,7 @@ __global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nc
       ok[k] = e < n;
       const int64_t ee = ok[k] ? e : 0;
       v[k] = load_elem(a.x, B ? MI355Q_BF16 : MI355Q_F32, (r0 + ee / cwe) * a.ldx + c0 + ee % cwe);
+      w[k] = (IM && a.imp) ? a.imp[c0 + ee % cwe] : 1.f;
     }
     const float mn = a.mn[cell], mx = a.mx[cell];
     for (int i = 0; i < a.T; ++i) {
@@ -371,7 +379,7 @@ __global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nc
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < 16; ++k)
-        if (ok[k]) acc += mse_term<B, ZP>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab);
+        if (ok[k]) acc += mse_term<B, ZP, IM>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab, w[k]);
       for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
       if ((tid & 63) == 0) red[tid >> 6] = acc;
       __syncthreads();
@@ -383,18 +391,20 @@ __global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nc
 
 // Per cell: the errors (from the chunk partials when nchunk > 0) and, for
 // every step, whether any cell improved its best error at it.
-template <bool B>
-__global__ void mse_flags_kernel(const float* part, int64_t nchunk, float* err, int64_t ncells, int T, int* any) {
+// round_sum: the error sums are rounded to bf16 (the uniform MSE observer on
+// bf16 values); best0: the largest value of the error dtype.
+__global__ void mse_flags_kernel(const float* part, int64_t nchunk, float* err, int64_t ncells, int T, int* any,
+                                 int round_sum, float best0) {
   const int64_t cell_raw = (int64_t)blockIdx.x * NT + threadIdx.x;
   const bool live = cell_raw < ncells;
   const int64_t cell = live ? cell_raw : ncells - 1;
-  float best = B ? 3.3895313892515355e38f : 3.4028234663852886e38f;
+  float best = best0;
   for (int i = 0; i < T; ++i) {
     float e;
     if (nchunk > 0) {
       float acc = 0.f;
       for (int64_t c = 0; c < nchunk; ++c) acc += part[(cell * nchunk + c) * T + i];
-      e = rb<B>(acc);
+      e = round_sum ? rb<true>(acc) : acc;
       if (live) err[cell * T + i] = e;
     } else {
       e = err[cell * T + i];
@@ -406,23 +416,27 @@ __global__ void mse_flags_kernel(const float* part, int64_t nchunk, float* err, 
 }
 
 // The steps the reference evaluates end at the first run of `patience`
-// steps without an improvement anywhere; each cell takes its first best
+// steps without an improvement anywhere (never when stop_zero_never and
+// patience == 0, as the imatrix observer); each cell takes its first best
 // candidate among them.
 template <bool B>
 __global__ void mse_select_kernel(const float* err, const int* any, int64_t ncells, int T, int patience,
-                                  double grid, const float* mn, const float* mx, float* mn_out, float* mx_out) {
+                                  int stop_zero_never, float best0, double grid, const float* mn, const float* mx,
+                                  float* mn_out, float* mx_out) {
   const int64_t cell = (int64_t)blockIdx.x * NT + threadIdx.x;
   if (cell >= ncells) return;
   int last = T - 1, cnt = 0;
-  for (int i = 0; i < T; ++i) {
-    if (any[i]) {
-      cnt = 0;
-    } else if (++cnt >= patience) {
-      last = i;
-      break;
+  if (!(stop_zero_never && patience == 0)) {
+    for (int i = 0; i < T; ++i) {
+      if (any[i]) {
+        cnt = 0;
+      } else if (++cnt >= patience) {
+        last = i;
+        break;
+      }
     }
   }
-  float best = B ? 3.3895313892515355e38f : 3.4028234663852886e38f;
+  float best = best0;
   int bi = -1;
   for (int i = 0; i <= last; ++i) {
     const float e = err[cell * T + i];
@@ -867,11 +881,15 @@ extern "C" size_t mi355q_observe_mse_workspace_size(int64_t rows, int64_t cols, 
   return plan_mse(rows, cols, cell_rows, cell_cols, total_steps).total;
 }
 
-extern "C" int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
-                                  int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric,
-                                  int total_steps, int patience, double grid, float norm, const float* min_dev,
-                                  const float* max_dev, float* min_out_dev, float* max_out_dev,
-                                  void* workspace_dev, size_t workspace_bytes, void* stream) {
+namespace mi355q {
+namespace {
+// Both MSE observers: im = the imatrix observer's mode (fp32 error sums,
+// weighted by imp when given, patience 0 = no early stop).
+int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
+                     int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric, int total_steps,
+                     int patience, double grid, float norm, bool im, const float* imp, const float* min_dev,
+                     const float* max_dev, float* min_out_dev, float* max_out_dev, void* workspace_dev,
+                     size_t workspace_bytes, void* stream) {
   MQ_CHECK_ARG(x_dev && min_dev && max_dev && min_out_dev && max_out_dev, "observe_mse: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "observe_mse: bad shape");
   MQ_CHECK_ARG(cell_rows > 0 && cell_cols > 0, "observe_mse: bad cell shape");
@@ -894,42 +912,127 @@ extern "C" int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t
   int* any = reinterpret_cast<int*>(ws + pl.off_any);
   uint16_t* tab = reinterpret_cast<uint16_t*>(ws + pl.off_tab);
   MseArgs a{x_dev, rows, cols, ldx, cell_rows, cell_cols, (rows + cell_rows - 1) / cell_rows,
-            (cols + cell_cols - 1) / cell_cols, qmin, qmax, total_steps, grid, norm, min_dev, max_dev};
+            (cols + cell_cols - 1) / cell_cols, qmin, qmax, total_steps, grid, norm, min_dev, max_dev,
+            im ? imp : nullptr};
   const bool b = dtype == MI355Q_BF16, zp = symmetric == 0;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(NT), 0, st, any, total_steps);
   MQ_LAUNCH_CHECK();
-  if (b) {
+  if (b && !im) {
     hipLaunchKernelGGL(mse_pow_table_kernel, dim3(POW_TAB / NT), dim3(NT), 0, st, norm, tab);
     MQ_LAUNCH_CHECK();
   }
   constexpr int64_t kMaxWg = 1024;  // persistent workgroups (each loads the power table once)
+  // kernel variant for (bf16, zero points, imatrix mode)
+  auto pick = [&](auto k000, auto k001, auto k010, auto k011, auto k100, auto k101, auto k110, auto k111,
+                  auto&& go) {
+    if (b) {
+      if (zp) im ? go(k111) : go(k110); else im ? go(k101) : go(k100);
+    } else {
+      if (zp) im ? go(k011) : go(k010); else im ? go(k001) : go(k000);
+    }
+  };
   if (pl.lg_log2 >= 0) {
     const int64_t per_wg = NT >> pl.lg_log2;
     const dim3 g((unsigned)min((ncells + per_wg - 1) / per_wg, kMaxWg));
-    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.lg_log2, tab, err); };
-    if (b) {
-      if (zp) go(mse_err_small_kernel<true, true>); else go(mse_err_small_kernel<true, false>);
-    } else {
-      if (zp) go(mse_err_small_kernel<false, true>); else go(mse_err_small_kernel<false, false>);
-    }
+    pick(mse_err_small_kernel<false, false, false>, mse_err_small_kernel<false, false, true>,
+         mse_err_small_kernel<false, true, false>, mse_err_small_kernel<false, true, true>,
+         mse_err_small_kernel<true, false, false>, mse_err_small_kernel<true, false, true>,
+         mse_err_small_kernel<true, true, false>, mse_err_small_kernel<true, true, true>,
+         [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.lg_log2, tab, err); });
   } else {
     const dim3 g((unsigned)min(ncells * pl.nchunk, kMaxWg));
-    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.nchunk, tab, part); };
-    if (b) {
-      if (zp) go(mse_err_large_kernel<true, true>); else go(mse_err_large_kernel<true, false>);
-    } else {
-      if (zp) go(mse_err_large_kernel<false, true>); else go(mse_err_large_kernel<false, false>);
-    }
+    pick(mse_err_large_kernel<false, false, false>, mse_err_large_kernel<false, false, true>,
+         mse_err_large_kernel<false, true, false>, mse_err_large_kernel<false, true, true>,
+         mse_err_large_kernel<true, false, false>, mse_err_large_kernel<true, false, true>,
+         mse_err_large_kernel<true, true, false>, mse_err_large_kernel<true, true, true>,
+         [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.nchunk, tab, part); });
   }
   MQ_LAUNCH_CHECK();
+  const bool round_sum = b && !im;
+  const float best0 = round_sum ? 3.3895313892515355e38f : 3.4028234663852886e38f;
   const dim3 gc((unsigned)((ncells + NT - 1) / NT));
-  if (b) hipLaunchKernelGGL(mse_flags_kernel<true>, gc, dim3(NT), 0, st, part, pl.nchunk, err, ncells, total_steps, any);
-  else   hipLaunchKernelGGL(mse_flags_kernel<false>, gc, dim3(NT), 0, st, part, pl.nchunk, err, ncells, total_steps, any);
+  hipLaunchKernelGGL(mse_flags_kernel, gc, dim3(NT), 0, st, part, pl.nchunk, err, ncells, total_steps, any,
+                     round_sum ? 1 : 0, best0);
   MQ_LAUNCH_CHECK();
   if (b) hipLaunchKernelGGL(mse_select_kernel<true>, gc, dim3(NT), 0, st, err, any, ncells, total_steps, patience,
-                            grid, min_dev, max_dev, min_out_dev, max_out_dev);
+                            im ? 1 : 0, best0, grid, min_dev, max_dev, min_out_dev, max_out_dev);
   else   hipLaunchKernelGGL(mse_select_kernel<false>, gc, dim3(NT), 0, st, err, any, ncells, total_steps, patience,
-                            grid, min_dev, max_dev, min_out_dev, max_out_dev);
+                            im ? 1 : 0, best0, grid, min_dev, max_dev, min_out_dev, max_out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+// Column sums of squares over a row range, one partial per (row chunk,
+// column); the partials are added in chunk order into the output.
+constexpr int SQ_ROWS = 512;  // rows per chunk
+
+__global__ void column_sumsq_part_kernel(const void* x, mi355q_dtype dt, int64_t rows, int64_t cols, int64_t ldx,
+                                         float* part) {
+  const int64_t c = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (c >= cols) return;
+  const int64_t r0 = (int64_t)blockIdx.y * SQ_ROWS, r1 = min(r0 + SQ_ROWS, rows);
+  float acc = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float v = load_elem(x, dt, r * ldx + c);
+    acc += v * v;
+  }
+  part[(int64_t)blockIdx.y * cols + c] = acc;
+}
+
+__global__ void column_sumsq_add_kernel(const float* part, int64_t nchunk, int64_t cols, float* out) {
+  const int64_t c = (int64_t)blockIdx.x * NT + threadIdx.x;
+  if (c >= cols) return;
+  float acc = 0.f;
+  for (int64_t k = 0; k < nchunk; ++k) acc += part[k * cols + c];
+  out[c] = out[c] + acc;
+}
+}  // namespace
+}  // namespace mi355q
+
+extern "C" int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
+                                  int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric,
+                                  int total_steps, int patience, double grid, float norm, const float* min_dev,
+                                  const float* max_dev, float* min_out_dev, float* max_out_dev,
+                                  void* workspace_dev, size_t workspace_bytes, void* stream) {
+  return observe_mse_impl(x_dev, dtype, rows, cols, ldx, cell_rows, cell_cols, qmin, qmax, symmetric, total_steps,
+                          patience, grid, norm, false, nullptr, min_dev, max_dev, min_out_dev, max_out_dev,
+                          workspace_dev, workspace_bytes, stream);
+}
+
+extern "C" int mi355q_observe_imatrix_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
+                                          int64_t ldx, int64_t cell_rows, int64_t cell_cols, float qmin, float qmax,
+                                          int symmetric, int total_steps, int patience, double grid, float norm,
+                                          const float* importance_dev, const float* min_dev, const float* max_dev,
+                                          float* min_out_dev, float* max_out_dev, void* workspace_dev,
+                                          size_t workspace_bytes, void* stream) {
+  return observe_mse_impl(x_dev, dtype, rows, cols, ldx, cell_rows, cell_cols, qmin, qmax, symmetric, total_steps,
+                          patience, grid, norm, true, importance_dev, min_dev, max_dev, min_out_dev, max_out_dev,
+                          workspace_dev, workspace_bytes, stream);
+}
+
+extern "C" size_t mi355q_column_sumsq_workspace_size(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)((rows + SQ_ROWS - 1) / SQ_ROWS) * cols * sizeof(float);
+}
+
+extern "C" int mi355q_column_sumsq(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
+                                   float* sum_dev, void* workspace_dev, size_t workspace_bytes, void* stream) {
+  MQ_CHECK_ARG(sum_dev, "column_sumsq: null output");
+  MQ_CHECK_ARG(rows >= 0 && cols > 0 && ldx >= cols, "column_sumsq: bad shape");
+  MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F32, "column_sumsq: dtype must be bf16 or fp32");
+  if (rows == 0) return MI355Q_OK;
+  MQ_CHECK_ARG(x_dev, "column_sumsq: null input");
+  const int64_t nchunk = (rows + SQ_ROWS - 1) / SQ_ROWS;
+  MQ_CHECK_ARG(nchunk <= 65535, "column_sumsq: at most 65535 * 512 rows");
+  MQ_CHECK_ARG(workspace_dev && workspace_bytes >= mi355q_column_sumsq_workspace_size(rows, cols),
+               "column_sumsq: workspace too small");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace_dev);
+  hipLaunchKernelGGL(column_sumsq_part_kernel, dim3((unsigned)((cols + NT - 1) / NT), (unsigned)nchunk), dim3(NT), 0,
+                     st, x_dev, dtype, rows, cols, ldx, part);
+  MQ_LAUNCH_CHECK();
+  hipLaunchKernelGGL(column_sumsq_add_kernel, dim3((unsigned)((cols + NT - 1) / NT)), dim3(NT), 0, st, part, nchunk,
+                     cols, sum_dev);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
 }

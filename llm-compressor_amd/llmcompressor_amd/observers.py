@@ -9,11 +9,16 @@ first statistics until ``get_qparams`` deletes them, and ``get_qparams``
 returning ``{"scale", "zero_point", "global_scale"}`` with the scale in the
 observed dtype (bf16 for a bf16 weight).  ``memoryless_mse`` / ``mse``
 (``observers/mse.py:12-98``) shrink those min / max by the grid search of
-``observers/mse_quant.py:19-273`` in one kernel pass over the values.
+``observers/mse_quant.py:19-273`` in one kernel pass over the values;
+``imatrix_mse`` (``observers/imatrix.py:23-283``) weights that search by the
+per-input-channel E[x^2] its forward pre-hook collects.
 """
 from __future__ import annotations
 
 import torch
+
+import logging
+import math
 
 from . import ops
 from .quant_args import QuantizationArgs, QuantizationStrategy, QuantizationType
@@ -244,4 +249,129 @@ class MovingAverageMSEObserver(_MSEObserver):
             c = self.avg_constant
             mn = (self.min_vals * (1.0 - c)) + (mn * c)
             mx = (self.max_vals * (1.0 - c)) + (mx * c)
+        self.min_vals, self.max_vals = mn, mx
+
+
+_logger = logging.getLogger("llmcompressor_amd")
+_logged_once: set[str] = set()
+
+
+def _warn_once(msg: str) -> None:
+    if msg not in _logged_once:
+        _logged_once.add(msg)
+        _logger.warning(msg)
+
+
+@Observer.register("imatrix_mse")
+class IMatrixMSEObserver(_MSEObserver):
+    """MSE observer weighted by per-input-channel importance E[x^2]
+    (``observers/imatrix.py:23-283``): ``attach(module)`` installs a forward
+    pre-hook accumulating sum x^2 and the token count on the module (or takes
+    accumulators a previous pass left there), ``detach`` removes it.  Defaults
+    maxshrink 0.95, patience 5 (0: no early stop), grid 20, norm 3; ``strict``
+    raises where the reference would otherwise fall back to uniform MSE."""
+
+    def __init__(self, *args, **kwargs):
+        Observer.__init__(self, *args, **kwargs)
+        kw = self.args.observer_kwargs
+        self.maxshrink = kw.get("maxshrink", 0.95)
+        self.patience = kw.get("patience", 5)
+        self.grid = kw.get("grid", 20)
+        self.norm = kw.get("norm", 3.0)
+        self.strict = kw.get("strict", False)
+        self.chunk_size = kw.get("chunk_size", 0)
+        self._imatrix_sum = None
+        self._imatrix_count = torch.tensor(0, dtype=torch.int64)
+        if self.grid <= 0:
+            raise ValueError(f"grid must be > 0, got {self.grid}")
+        if self.patience < 0:
+            raise ValueError(f"patience must be >= 0, got {self.patience}")
+        if self.chunk_size < 0:
+            raise ValueError(f"chunk_size must be >= 0, got {self.chunk_size}")
+        if not (0 <= self.maxshrink <= 1):
+            raise ValueError(f"maxshrink must be in [0, 1], got {self.maxshrink}")
+        if not isinstance(self.norm, (int, float)) or not math.isfinite(self.norm) or self.norm <= 0:
+            raise ValueError(f"norm must be a finite positive number, got {self.norm}")
+
+    # -- hook lifecycle (imatrix.py:68-138)
+    def attach(self, module: torch.nn.Module) -> None:
+        if hasattr(module, "_imatrix_sum"):
+            self._imatrix_sum, self._imatrix_count = module._imatrix_sum, module._imatrix_count
+            del module._imatrix_sum
+            del module._imatrix_count
+            return
+        if not hasattr(module, "in_features"):
+            return
+        module._imatrix_sum = torch.zeros(module.in_features, dtype=torch.float32)
+        module._imatrix_count = torch.tensor(0, dtype=torch.int64)
+
+        def _hook(mod, args):
+            if isinstance(args, tuple):
+                if len(args) == 0:
+                    return
+                x = args[0]
+            else:
+                x = args
+            if isinstance(x, tuple):
+                x = x[0]
+            if x is None or not isinstance(x, torch.Tensor):
+                return
+            x = x.detach()
+            mod._imatrix_sum = mod._imatrix_sum.to(x.device)
+            mod._imatrix_count = mod._imatrix_count.to(x.device)
+            ops.column_sumsq_(x.reshape(-1, x.shape[-1]), mod._imatrix_sum)
+            mod._imatrix_count += math.prod(x.shape[:-1])
+
+        module._imatrix_hook = module.register_forward_pre_hook(_hook)
+
+    def detach(self, module: torch.nn.Module) -> None:
+        if hasattr(module, "_imatrix_hook"):
+            module._imatrix_hook.remove()
+            del module._imatrix_hook
+
+    # -- importance (imatrix.py:157-283)
+    def _fallback(self, msg: str, exc=ValueError):
+        if self.strict:
+            raise exc(f"imatrix_mse: {msg}")
+        _warn_once(f"imatrix_mse: {msg}. Falling back to uniform MSE.")
+        return None
+
+    def _importance(self, observed: torch.Tensor):
+        a = self.args
+        if not self.is_weight_obs:
+            return self._fallback("only supported for weight observers", NotImplementedError)
+        if a.strategy == QuantizationStrategy.TENSOR:
+            return self._fallback("TENSOR strategy not supported", NotImplementedError)
+        if self._imatrix_sum is None or int(self._imatrix_count) == 0:
+            return self._fallback("no importance data available")
+        imp = self._imatrix_sum.to(observed.device) / self._imatrix_count.to(observed.device).float()
+        if not torch.isfinite(imp).all():
+            return self._fallback("contains non-finite values")
+        if (imp < 0).any():
+            return self._fallback("contains negative values")
+        if torch.all(imp == 0):
+            return self._fallback("all zeros")
+        if a.strategy not in (QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP,
+                              QuantizationStrategy.TENSOR_GROUP):
+            return self._fallback(f"unsupported strategy {a.strategy}", NotImplementedError)
+        expected = observed.shape[-1]
+        if imp.numel() != expected:
+            return self._fallback(f"size mismatch: expected {expected}, got {imp.numel()}")
+        imp = imp.to(torch.float32)
+        return imp / (imp.mean() + torch.finfo(torch.float32).tiny)
+
+    def _min_max(self, observed: torch.Tensor):
+        a = self.args
+        if a.type != QuantizationType.INT or a.is_mx:
+            raise NotImplementedError("MSE observers for float types are not provided by this build")
+        imp = self._importance(observed)
+        mn, mx = Observer._min_max(self, observed)
+        x2, ch, cw = self._cells(observed)
+        qmin, qmax = a.q_range()
+        steps = max(1, int(self.maxshrink * self.grid)) + 1
+        mn2, mx2 = ops.observe_mse(x2, ch, cw, mn.reshape(-1), mx.reshape(-1), qmin, qmax, a.symmetric, steps,
+                                   self.patience, self.grid, self.norm, importance=imp, imatrix=True)
+        return mn2.reshape(mn.shape), mx2.reshape(mx.shape)
+
+    def update_statistics_from_observed(self, mn, mx):
         self.min_vals, self.max_vals = mn, mx

@@ -350,10 +350,13 @@ def pack_int4_int32(codes: torch.Tensor) -> torch.Tensor:
 
 
 def observe_mse(x: torch.Tensor, cell_rows: int, cell_cols: int, mn: torch.Tensor, mx: torch.Tensor, qmin: float,
-                qmax: float, symmetric: bool, total_steps: int, patience: int, grid: float, norm: float):
-    """MSE grid search over the cells of x (see ``mi355q_observe_mse``): returns
-    the chosen (min, max) per cell as fp32 tensors shaped like ``mn``."""
-    L.require_gpu(x, mn, mx)
+                qmax: float, symmetric: bool, total_steps: int, patience: int, grid: float, norm: float,
+                importance: torch.Tensor | None = None, imatrix: bool = False):
+    """MSE grid search over the cells of x (``mi355q_observe_mse``, or with
+    ``imatrix`` ``mi355q_observe_imatrix_mse`` weighted by ``importance``
+    [cols]): returns the chosen (min, max) per cell as fp32 tensors shaped
+    like ``mn``."""
+    L.require_gpu(x, mn, mx, importance)
     if x.dim() != 2 or x.stride(1) != 1:
         x = x.reshape(-1, x.shape[-1]).contiguous()
     rows, cols = x.shape
@@ -361,12 +364,35 @@ def observe_mse(x: torch.Tensor, cell_rows: int, cell_cols: int, mn: torch.Tenso
     out_mn, out_mx = torch.empty_like(mn32), torch.empty_like(mx32)
     lib = L.lib()
     ws = _ws(lib.mi355q_observe_mse_workspace_size(rows, cols, cell_rows, cell_cols, total_steps), x.device)
-    L.check(lib.mi355q_observe_mse(x.data_ptr(), _dt(x), rows, cols, x.stride(0), cell_rows, cell_cols,
-                                   C.c_float(qmin), C.c_float(qmax), 1 if symmetric else 0, int(total_steps),
-                                   int(patience), C.c_double(grid), C.c_float(norm), mn32.data_ptr(), mx32.data_ptr(),
-                                   out_mn.data_ptr(), out_mx.data_ptr(), L.ptr(ws), 0 if ws is None else ws.numel(),
-                                   L.stream_of(x)))
+    common = (x.data_ptr(), _dt(x), rows, cols, x.stride(0), cell_rows, cell_cols, C.c_float(qmin), C.c_float(qmax),
+              1 if symmetric else 0, int(total_steps), int(patience), C.c_double(grid), C.c_float(norm))
+    tail = (mn32.data_ptr(), mx32.data_ptr(), out_mn.data_ptr(), out_mx.data_ptr(), L.ptr(ws),
+            0 if ws is None else ws.numel(), L.stream_of(x))
+    if imatrix:
+        imp = None if importance is None else importance.to(torch.float32).contiguous()
+        if imp is not None and imp.numel() != cols:
+            raise ValueError(f"importance must have {cols} entries, got {imp.numel()}")
+        L.check(lib.mi355q_observe_imatrix_mse(*common, L.ptr(imp), *tail))
+    else:
+        L.check(lib.mi355q_observe_mse(*common, *tail))
     return out_mn, out_mx
+
+
+def column_sumsq_(x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[c] += sum over rows of x[:, c]^2 (fp32 accumulation), in place."""
+    L.require_gpu(x, out)
+    if x.dim() != 2 or x.stride(1) != 1:
+        x = x.reshape(-1, x.shape[-1]).contiguous()
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.to(torch.float32)
+    rows, cols = x.shape
+    if out.dtype != torch.float32 or out.numel() != cols or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous fp32 vector of {cols}")
+    lib = L.lib()
+    ws = _ws(lib.mi355q_column_sumsq_workspace_size(rows, cols), x.device)
+    L.check(lib.mi355q_column_sumsq(x.data_ptr() if rows else None, _dt(x), rows, cols, x.stride(0), out.data_ptr(),
+                                    L.ptr(ws), 0 if ws is None else ws.numel(), L.stream_of(x)))
+    return out
 
 
 def pack_int32(codes: torch.Tensor, num_bits: int) -> torch.Tensor:

@@ -296,3 +296,69 @@ class OMSE(OMinMax):
             mx = self.max_vals * (1.0 - self.avg) + mx * self.avg
         self.min_vals, self.max_vals = mn, mx
         return self
+
+
+# ---------------------------------------------------------------- imatrix MSE observer
+def imatrix_grid_search(observed: torch.Tensor, args: OArgs, maxshrink: float = 0.95, patience: int = 5,
+                        grid: float = 20, norm: float = 3.0, importance: torch.Tensor | None = None):
+    """``observers/imatrix.py:289-440`` (unchunked): as ``mse_grid_search``
+    but max(1, int(maxshrink * grid)) + 1 steps, the error |q - x|^norm in
+    fp32 (q fake-quantised in the observed dtype) weighted by ``importance``
+    (broadcast like ``observed``), summed in fp32, and no early stop when
+    patience is 0."""
+    from dataclasses import replace
+
+    from .fake_quant import fake_quantize
+
+    min_val = torch.amin(observed, dim=(0, -1))
+    max_val = torch.amax(observed, dim=(0, -1))
+    best_error = torch.full(min_val.shape, torch.finfo(torch.float32).max, dtype=torch.float32)
+    best_min, best_max = min_val.clone(), max_val.clone()
+    observed_f = observed.float()
+    token_args = replace(args, strategy="token")
+    no_improve = 0
+    for i in range(max(1, int(maxshrink * grid)) + 1):
+        p = 1 - i / grid
+        smin, smax = p * min_val, p * max_val
+        scale, zp = calculate_qparams(smin, smax, args)
+        q = fake_quantize(observed, scale.unsqueeze(-1), zp.unsqueeze(-1), token_args).float()
+        q = (q - observed_f).abs().pow(norm)
+        if importance is not None:
+            q = q * importance.to(torch.float32)
+        err = q.sum(dim=(0, -1), dtype=torch.float32)
+        improved = err < best_error
+        if torch.any(improved):
+            best_error[improved] = err[improved]
+            best_min[improved] = smin[improved]
+            best_max[improved] = smax[improved]
+            no_improve = 0
+        else:
+            no_improve += 1
+            if patience > 0 and no_improve >= patience:
+                break
+    return best_min, best_max
+
+
+def imatrix_importance(imatrix_sum: torch.Tensor, count: int, observed: torch.Tensor, args: OArgs,
+                       base_name: str = "weight"):
+    """``observers/imatrix.py:157-283`` (non-strict): E[x^2] = sum / count,
+    normalised by its mean, broadcast over the weight's rows and flattened
+    like the weight; None (uniform MSE) for non-weight observers, TENSOR and
+    unsupported strategies, missing, non-finite, negative, all-zero or
+    mis-sized data."""
+    if base_name != "weight" or args.strategy == "tensor" or imatrix_sum is None or count == 0:
+        return None
+    imp = imatrix_sum / torch.tensor(count).float()
+    if not torch.isfinite(imp).all() or (imp < 0).any() or torch.all(imp == 0):
+        return None
+    if args.strategy == "channel":
+        expected = observed.shape[-1]
+    elif args.strategy in ("group", "tensor_group"):
+        expected = observed.shape[2] * observed.shape[3]
+    else:
+        return None
+    if imp.numel() != expected:
+        return None
+    imp = imp.to(torch.float32)
+    imp = imp / (imp.mean() + torch.finfo(torch.float32).tiny)
+    return flatten_weight(imp.unsqueeze(0).expand(observed.shape[1], -1), args)

@@ -90,3 +90,75 @@ def test_mse_activation_moving_average(dev, strategy):
     mn, mx = obs.min_vals.cpu().float(), obs.max_vals.cpu().float()
     assert torch.allclose(mn.reshape(-1), ora.min_vals.float().reshape(-1), rtol=1e-2)
     assert torch.allclose(mx.reshape(-1), ora.max_vals.float().reshape(-1), rtol=1e-2)
+
+
+# ---------------------------------------------------------------- imatrix_mse
+def _imatrix_obs(strategy="channel", group_size=None, **kw):
+    args = QuantizationArgs(num_bits=4, symmetric=kw.pop("symmetric", True), strategy=strategy,
+                            group_size=group_size, observer="imatrix_mse", observer_kwargs=kw)
+    return Observer.load_from_registry("imatrix_mse", base_name="weight", args=args)
+
+
+def test_imatrix_uniform_importance_matches_memoryless_mse(dev):
+    """test_imatrix.py:175-212 on the GPU."""
+    say("imatrix uniform == memoryless_mse")
+    torch.manual_seed(123)
+    lin = torch.nn.Linear(8, 4).to(dev)
+    lin._imatrix_sum = torch.ones(8)
+    lin._imatrix_count = torch.tensor(1, dtype=torch.int64)
+    oi = _imatrix_obs(norm=2.4, maxshrink=0.20)
+    oi.attach(lin)
+    ou = Observer.load_from_registry("memoryless_mse", base_name="weight", args=QuantizationArgs(
+        num_bits=4, symmetric=True, strategy="channel", observer="memoryless_mse", observer_kwargs={"grid": 20}))
+    qi = oi(lin.weight.detach()).get_qparams()
+    qu = ou(lin.weight.detach()).get_qparams()
+    assert torch.allclose(qi["scale"], qu["scale"]) and torch.equal(qi["zero_point"], qu["zero_point"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("case", [dict(strategy="channel"), dict(strategy="group", group_size=128),
+                                  dict(strategy="group", group_size=32, symmetric=False)],
+                         ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+def test_imatrix_matches_oracle(dev, case, dtype):
+    say(f"imatrix {case} {dtype}")
+    g = torch.Generator().manual_seed(5)
+    w = (torch.randn(192, 1024, generator=g) * 0.02).to(dtype)
+    s2 = torch.exp(2 * torch.randn(1024, generator=g))        # skewed E[x^2]
+    obs = _imatrix_obs(**dict(case))
+    obs._imatrix_sum, obs._imatrix_count = s2.clone().to(dev), torch.tensor(3, dtype=torch.int64)
+    obs(w.to(dev))
+    mn, mx = obs.min_vals.cpu(), obs.max_vals.cpu()
+    a = OArgs(num_bits=4, observer="imatrix_mse", **case)
+    flat = oobs.flatten_weight(w, a)
+    imp = oobs.imatrix_importance(s2, 3, flat, a)
+    omn, omx = oobs.imatrix_grid_search(flat, a, importance=imp)
+    agree = ((mn == omn.reshape(mn.shape)) & (mx == omx.reshape(mx.shape))).float().mean().item()
+    say(f"  agreement {agree:.5f}")
+    assert agree >= 0.99
+
+
+def test_imatrix_hook_accumulates_and_hands_over(dev, caplog):
+    say("imatrix hook")
+    lin = torch.nn.Linear(256, 64).to(dev).to(torch.bfloat16)
+    obs = _imatrix_obs()
+    obs.attach(lin)
+    xs = [(torch.randn(2, 50, 256, generator=torch.Generator().manual_seed(s)) * 3).to(torch.bfloat16)
+          for s in (1, 2)]
+    with torch.no_grad():
+        for x in xs:
+            lin(x.to(dev))
+    exp = sum(x.float().pow(2).sum(dim=(0, 1)) for x in xs)
+    assert int(lin._imatrix_count) == 200
+    assert torch.allclose(lin._imatrix_sum.cpu(), exp, rtol=1e-5)
+    obs.detach(lin)
+    second = _imatrix_obs()
+    second.attach(lin)                          # takes the accumulators
+    assert not hasattr(lin, "_imatrix_sum") and int(second._imatrix_count) == 200
+    qp = second(lin.weight.detach()).get_qparams()
+    assert torch.isfinite(qp["scale"]).all()
+    bare = _imatrix_obs()
+    with caplog.at_level("WARNING", logger="llmcompressor_amd"):
+        bare(lin.weight.detach()).get_qparams()
+    assert "no importance data available" in caplog.text
+    with pytest.raises(ValueError):
+        _imatrix_obs(strict=True)(lin.weight.detach())

@@ -259,3 +259,59 @@ def test_mse_search_stops_after_patience_without_improvement():
     mn, mx, steps = oobs.mse_grid_search(oobs.flatten_weight(w, a), a, patience=5, return_steps=True)
     assert steps == 6 and torch.equal(mx, torch.full((4, 1), 0.25)) and torch.equal(mn, mx)
     assert oobs.mse_grid_search(oobs.flatten_weight(w, a), a, maxshrink=0.0, return_steps=True)[2] == 0
+
+
+def _imatrix_case(seed=123):
+    torch.manual_seed(seed)
+    return torch.nn.Linear(8, 4).weight.detach().clone()
+
+
+def test_imatrix_uniform_importance_matches_memoryless_mse():
+    """test_imatrix.py:175-212: all-ones importance, norm 2.4, maxshrink 0.2,
+    grid 20 gives the memoryless_mse qparams (fp32 weights)."""
+    w = _imatrix_case()
+    a = OArgs(num_bits=4, strategy="channel")
+    flat = oobs.flatten_weight(w, a)
+    imp = oobs.imatrix_importance(torch.ones(8), 1, flat, a)
+    mi, xi = oobs.imatrix_grid_search(flat, a, maxshrink=0.20, norm=2.4, importance=imp)
+    mu, xu = oobs.mse_grid_search(flat, a, grid=20)
+    si, zi = oobs.calculate_qparams(mi, xi, a)
+    su, zu = oobs.calculate_qparams(mu, xu, a)
+    assert torch.allclose(si, su) and torch.equal(zi, zu)
+
+
+def test_imatrix_importance_changes_and_weights_the_choice():
+    """test_imatrix.py:150-173, and the chosen candidate minimises the
+    importance-weighted fp64 error over the candidates."""
+    w = _imatrix_case()
+    a = OArgs(num_bits=4, strategy="channel")
+    flat = oobs.flatten_weight(w, a)
+    imp = oobs.imatrix_importance(torch.tensor([1000.0] * 4 + [0.01] * 4), 1, flat, a)
+    mw, xw = oobs.imatrix_grid_search(flat, a, importance=imp)
+    mu, xu = oobs.imatrix_grid_search(flat, a, importance=None)
+    assert not torch.allclose(oobs.calculate_qparams(mw, xw, a)[0], oobs.calculate_qparams(mu, xu, a)[0])
+    mn0, mx0 = torch.amin(flat, dim=(0, -1)), torch.amax(flat, dim=(0, -1))
+    errs = []
+    for i in range(20):
+        p = 1 - i / 20
+        s, z = oobs.calculate_qparams(p * mn0, p * mx0, a)
+        q = ofq.fake_quantize_weight(w, s, z, a)
+        errs.append(((q.double() - w.double()).abs().pow(3) * imp.reshape(w.shape).double()).sum(-1))
+    errs = torch.stack(errs)
+    s_w = oobs.calculate_qparams(mw, xw, a)
+    qw = ofq.fake_quantize_weight(w, s_w[0], s_w[1], a)
+    got = ((qw.double() - w.double()).abs().pow(3) * imp.reshape(w.shape).double()).sum(-1)
+    assert torch.all(got <= errs.min(0).values * (1 + 1e-5))
+
+
+def test_imatrix_importance_validation():
+    w = _imatrix_case()
+    a = OArgs(num_bits=4, strategy="channel")
+    flat = oobs.flatten_weight(w, a)
+    assert oobs.imatrix_importance(None, 0, flat, a) is None
+    for bad in (torch.full((8,), float("nan")), -torch.ones(8), torch.zeros(8), torch.ones(7)):
+        assert oobs.imatrix_importance(bad, 1, flat, a) is None
+    assert oobs.imatrix_importance(torch.ones(8), 1, flat, OArgs(num_bits=4, strategy="tensor")) is None
+    assert oobs.imatrix_importance(torch.ones(8), 1, flat, a, base_name="input") is None
+    imp = oobs.imatrix_importance(torch.arange(1.0, 9.0), 2, flat, a)
+    assert torch.allclose(imp[0, 0, 0], torch.arange(1.0, 9.0) / 4.5)
