@@ -41,11 +41,13 @@ def parse():
     p.add_argument("--hessian-calls", type=int, default=1,
                    help="split the 64 x 2048 calibration tokens into this many accumulate_hessian calls")
     p.add_argument("--workload", default="gptq_w4a16",
-                   choices=["gptq_w4a16", "mxfp4", "gptq_w8a8", "moe", "decoder", "sparsegpt", "mse_observer"],
+                   choices=["gptq_w4a16", "mxfp4", "gptq_w8a8", "moe", "decoder", "sparsegpt", "mse_observer",
+                            "pipeline"],
                    help="gptq_w4a16 (default): the headline line; the others measure the remaining "
                         "calibration workloads (MXFP4 pack, W8A8 channel + actorder, MoE experts, "
                         "Llama-3-8B-shaped decoder layer, SparseGPT 50 %% / 2:4 on a 4096x4096 layer, "
-                        "MSE weight observer on 4096x4096 and 14336x4096)")
+                        "MSE weight observer on 4096x4096 and 14336x4096, sequential pipeline over two "
+                        "Llama-3-8B-shaped layers)")
     return p.parse_args()
 
 
@@ -538,8 +540,71 @@ def bench_mse_observer(a):
           "ms", a, ms, "mse_observer_w4_g128_4096x4096", {"per_shape": res}, dtype="bf16 in, fp32 error sums")
 
 
+def bench_pipeline(a):
+    """Sequential pipeline, GPTQ W4A16 g128 over two Llama-3-8B-shaped MLP+projection layers (q/k/v/o 4096,
+    gate/up/down 14336), 64 x 2048 calibration tokens in 8 batches: activation cache on the GPU vs offloaded
+    to pinned host memory with prefetch."""
+    torch, dev = _setup()
+    import copy
+
+    import torch.nn.functional as F
+
+    from llmcompressor_amd import GPTQModifier
+    from llmcompressor_amd.pipeline import sequential_calibrate
+
+    hidden, inter, nb, bs, seq = 4096, 14336, 8, 8, 2048
+
+    class Layer(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            L = lambda i, o: torch.nn.Linear(i, o, bias=False)  # noqa: E731
+            self.q, self.k, self.v, self.o = L(hidden, hidden), L(hidden, 1024), L(hidden, 1024), L(hidden, hidden)
+            self.gate, self.up, self.down = L(hidden, inter), L(hidden, inter), L(inter, hidden)
+
+        def forward(self, x):
+            a = self.q(x) + F.pad(self.k(x) * self.v(x), (0, hidden - 1024))
+            h = x + self.o(torch.tanh(a))
+            return h + self.down(F.silu(self.gate(h)) * self.up(h))
+
+    class Model(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layers = torch.nn.ModuleList(Layer() for _ in range(2))
+
+        def forward(self, x):
+            for layer in self.layers:
+                x = layer(x)
+            return x
+
+    torch.manual_seed(9)
+    base = Model().to(dev).to(torch.bfloat16)
+    for p_ in base.parameters():
+        p_.data.mul_(0.5)
+    xs = [_gpu_heavy(torch, dev, bs * seq, hidden, 10 + b).view(bs, seq, hidden) for b in range(nb)]
+    res = {}
+    for name, off, pre in (("gpu_cache", None, False), ("host_offload_prefetch", "cpu", True)):
+        times = []
+        for it in range(1 + max(1, a.steps // 2)):   # the first run warms the libraries up
+            m = copy.deepcopy(base)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            sequential_calibrate(m, m.layers, xs, GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=()),
+                                 offload_device=off, prefetch=pre)
+            torch.cuda.synchronize()
+            if it:
+                times.append((time.perf_counter() - t0) * 1e3)
+        res[name] = round(min(times), 2)
+    act_bytes = nb * bs * seq * hidden * 2
+    _line("Sequential pipeline ms (GPTQ W4A16 g128, 2 Llama-3-8B-shaped layers, 64x2048 tokens, host-offloaded "
+          "activation cache with prefetch)", res["host_offload_prefetch"], "ms", a, res["host_offload_prefetch"],
+          "sequential_pipeline_2_layers_64x2048tok",
+          {"ms_gpu_cache": res["gpu_cache"], "activation_bytes_per_layer_pass": act_bytes,
+           "offload_overhead_ms": round(res["host_offload_prefetch"] - res["gpu_cache"], 2)})
+
+
 OTHER_WORKLOADS = {"mxfp4": bench_mxfp4, "gptq_w8a8": bench_w8a8, "moe": bench_moe, "decoder": bench_decoder,
-                   "sparsegpt": bench_sparsegpt, "mse_observer": bench_mse_observer}
+                   "sparsegpt": bench_sparsegpt, "mse_observer": bench_mse_observer,
+                   "pipeline": bench_pipeline}
 
 
 if __name__ == "__main__":

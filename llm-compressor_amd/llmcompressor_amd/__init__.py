@@ -8,7 +8,7 @@ hand-written HIP kernels (``libmi355q.so``, C ABI in ``include/mi355q.h``).
 from .calibration import initialize_module_for_quantization, initialize_observer, observe, update_qparams
 from .gptq import GPTQResult, PreparedHessian, accumulate_hessian, gptq_quantize, gptq_quantize_batched, \
     make_empty_hessian, prepare_hessian, prepare_hessians_batched, quantize_weight, symmetrize_hessian
-from . import save, sparsegpt
+from . import pipeline, save, sparsegpt
 from .modifiers import GPTQModifier, QuantizationModifier, SparseGPTModifier
 from .observers import Observer
 from .quant_args import (ActivationOrdering, QuantizationArgs, QuantizationScheme, QuantizationStrategy,
@@ -16,7 +16,7 @@ from .quant_args import (ActivationOrdering, QuantizationArgs, QuantizationSchem
 
 __all__ = [
     "ActivationOrdering", "GPTQModifier", "GPTQResult", "Observer", "QuantizationArgs", "QuantizationModifier",
-    "QuantizationScheme", "QuantizationStrategy", "QuantizationType", "SparseGPTModifier", "save", "sparsegpt", "accumulate_hessian", "gptq_quantize",
+    "QuantizationScheme", "QuantizationStrategy", "QuantizationType", "SparseGPTModifier", "pipeline", "save", "sparsegpt", "accumulate_hessian", "gptq_quantize",
     "gptq_quantize_batched", "initialize_module_for_quantization", "initialize_observer", "make_empty_hessian",
     "observe", "prepare_hessian", "prepare_hessians_batched", "PreparedHessian", "preset_name_to_scheme",
     "quantize_weight", "symmetrize_hessian", "update_qparams",

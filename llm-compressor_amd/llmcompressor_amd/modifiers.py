@@ -137,6 +137,8 @@ class GPTQModifier(QuantizationModifier):
             w.actorder = None
 
     def calibrate_module(self, module, args, _output):
+        if getattr(self, "_hooks_disabled", False):   # a propagation pass of the sequential pipeline
+            return
         inp = args[0]
         if module not in self._num_samples:
             dev = module.weight.device
@@ -273,6 +275,8 @@ class SparseGPTModifier:
                 self._hooks.append(module.register_forward_hook(self.calibrate_module))
 
     def calibrate_module(self, module, args, _output):
+        if getattr(self, "_hooks_disabled", False):   # a propagation pass of the sequential pipeline
+            return
         inp = args[0]
         if module not in self._num_samples:
             dev = module.weight.device
