@@ -195,13 +195,18 @@ def sequential_calibrate(model: torch.nn.Module, layers, batches, modifier, prop
         catch.inputs = (args, kwargs)
         raise _StopForward
 
+    if not layers:
+        raise ValueError("sequential_calibrate needs at least one layer")
     h = layers[0].register_forward_pre_hook(catch, with_kwargs=True)
     try:
         for b, x in enumerate(batches):
+            catch.inputs = None
             try:
                 model(x) if not isinstance(x, dict) else model(**x)
             except _StopForward:
                 pass
+            if catch.inputs is None:
+                raise RuntimeError("the model's forward did not reach the first of the given layers")
             args, kwargs = catch.inputs
             cache.update(b, {"args": args, "kwargs": kwargs})
     finally:
