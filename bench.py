@@ -42,12 +42,13 @@ def parse():
                    help="split the 64 x 2048 calibration tokens into this many accumulate_hessian calls")
     p.add_argument("--workload", default="gptq_w4a16",
                    choices=["gptq_w4a16", "mxfp4", "gptq_w8a8", "moe", "decoder", "sparsegpt", "mse_observer",
-                            "pipeline"],
+                            "pipeline", "torch_reference"],
                    help="gptq_w4a16 (default): the headline line; the others measure the remaining "
                         "calibration workloads (MXFP4 pack, W8A8 channel + actorder, MoE experts, "
                         "Llama-3-8B-shaped decoder layer, SparseGPT 50 %% / 2:4 on a 4096x4096 layer, "
                         "MSE weight observer on 4096x4096 and 14336x4096, sequential pipeline over two "
-                        "Llama-3-8B-shaped layers)")
+                        "Llama-3-8B-shaped layers); torch_reference times the reference's algorithm as "
+                        "plain torch ops on the same GPU beside this library on the headline layer")
     return p.parse_args()
 
 
@@ -142,6 +143,21 @@ def main():
     syrk_flop = n_tok * COLS * (COLS + 1)  # upper triangle incl. diagonal, 2 flop / MAC
     syrk_tflops = syrk_flop / (syrk_ms * 1e-3) / 1e12
 
+    # vendor GEMM on the same product: torch.mm (hipBLASLt) of X^T X as the
+    # full 4096 x 4096 square with a bf16 result (twice the multiply-adds of
+    # the triangle, half the output precision)
+    xt = xf.t().contiguous()
+    for _ in range(2):
+        torch.mm(xt, xf)
+    e0.record(stream)
+    for _ in range(reps):
+        torch.mm(xt, xf)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    mm_ms = e0.elapsed_time(e1) / reps
+    mm_tflops = 2 * n_tok * COLS * COLS / (mm_ms * 1e-3) / 1e12
+    del xt
+
     # MXFP4 quantize + pack (config: W 4096 x 14336, A 8192 x 14336)
     mx = {}
     for name, shape in (("W", (4096, 14336)), ("A", (8192, 14336))):
@@ -205,12 +221,13 @@ def main():
         "phases_ms": {"hessian": round(hess_ms, 3), "solve": round(solve_ms, 3)},
         "hessian": {"kernel_ms": round(syrk_ms, 4), "tflops": round(syrk_tflops, 1),
                     "frac_fp32_mfma_peak": round(syrk_tflops / PEAK_FP32_MFMA_TFLOPS, 3),
-                    "frac_bf16_mfma_peak": round(syrk_tflops / PEAK_BF16_TFLOPS, 4)},
+                    "frac_bf16_mfma_peak": round(syrk_tflops / PEAK_BF16_TFLOPS, 4),
+                    "vendor_gemm_full_square_bf16_out": {"ms": round(mm_ms, 4), "tflops": round(mm_tflops, 1)}},
         "mxfp4_quantize_pack": mx,
         "copy_1GiB_GB_s": round(copy_gbs, 1),
         "roofline": {"bound": "mfma", "achieved": round(syrk_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(syrk_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "syrk_stream_kernel + syrk_tail_sum_kernel + syrk_reduce_kernel (one Hessian call, 131072 tokens)"},
+                     "kernel": "syrk_stream_kernel + syrk_stream_reduce_kernel (one Hessian call, 131072 tokens)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -602,9 +619,116 @@ def bench_pipeline(a):
            "offload_overhead_ms": round(res["host_offload_prefetch"] - res["gpu_cache"], 2)})
 
 
+def _torch_gptq_w4a16(torch, w, x, num_samples, group, blocksize=128, percdamp=0.01):
+    """The reference's own algorithm as torch ops on the GPU, the way it runs
+    on a ROCm device today (timing comparator only): fp32 GEMM Hessian
+    (modifiers/gptq/gptq_quantize.py:22-32, 63-97; base.py:594), memoryless
+    min-max group scales in the weight dtype (observers/min_max.py:16-25,
+    observers/base.py:99-123), damping and the three-call Cholesky chain
+    (gptq_quantize.py:181-196), and the per-column loop with its lazy block
+    update (:199-277), each column a channel-wise fake quantize with the
+    dequantised value in the scale's dtype.  Returns (hessian_ms, solve_ms,
+    Q fp32, scale bf16)."""
+    import math
+
+    sync = torch.cuda.synchronize
+    sync()
+    t0 = time.perf_counter()
+    H = torch.zeros(w.shape[1], w.shape[1], dtype=torch.float32, device=w.device)
+    inp = x.reshape(-1, x.shape[-1]).t().to(torch.float32)
+    inp = math.sqrt(2) * inp
+    H += inp.matmul(inp.t())
+    del inp
+    H = H / num_samples
+    sync()
+    t1 = time.perf_counter()
+    rows, cols = w.shape
+    g = w.view(rows, cols // group, group)
+    mn = torch.clamp(torch.amin(g, dim=-1), max=0)
+    mx = torch.clamp(torch.amax(g, dim=-1), min=0)
+    scale = torch.clamp(torch.maximum(mn.abs(), mx.abs()) / 7.5, min=torch.finfo(torch.float32).eps)
+    W = w.clone().to(torch.float32)
+    g_idx = torch.arange(cols, device=w.device, dtype=torch.int) // group
+    dead = torch.diag(H) == 0
+    H[dead, dead] = 1
+    W[:, dead] = 0
+    damp = percdamp * torch.mean(torch.diag(H))
+    diag = torch.arange(cols, device=w.device)
+    H[diag, diag] += damp
+    H = torch.linalg.cholesky(H)
+    H = torch.cholesky_inverse(H)
+    Hinv = torch.linalg.cholesky(H, upper=True)
+    losses = torch.zeros(rows, device=w.device)
+    for i1 in range(0, cols, blocksize):
+        i2 = min(i1 + blocksize, cols)
+        W1 = W[:, i1:i2].clone()
+        Q1 = torch.zeros_like(W1)
+        Err1 = torch.zeros_like(W1)
+        losses1 = torch.zeros_like(W1)
+        Hinv1 = Hinv[i1:i2, i1:i2]
+        for i in range(i2 - i1):
+            wc = W1[:, i]
+            d = Hinv1[i, i]
+            s = scale[:, g_idx[i1 + i]]
+            q = (torch.round(torch.clamp(wc / s, -8, 7)).to(s.dtype) * s).to(torch.float32)
+            Q1[:, i] = q
+            losses1[:, i] = (wc - q) ** 2 / d ** 2
+            err1 = (wc - q) / d
+            W1[:, i:] -= err1.unsqueeze(1).matmul(Hinv1[i, i:].unsqueeze(0))
+            Err1[:, i] = err1
+        W[:, i1:i2] = Q1
+        losses += torch.sum(losses1, 1) / 2
+        W[:, i2:] -= Err1.matmul(Hinv[i1:i2, i2:])
+    torch.sum(losses).item()
+    sync()
+    t2 = time.perf_counter()
+    return (t1 - t0) * 1e3, (t2 - t1) * 1e3, W, scale
+
+
+def bench_torch_reference(a):
+    """The headline layer (W4A16 g128, 4096 x 4096, 64 x 2048 tokens) through
+    the reference's algorithm as plain torch ops on the same GPU, beside this
+    library's step on the same inputs; the integer codes of the two are
+    compared.  One timed pass of the torch path after a warm-up on a
+    256-column slice (library initialisation)."""
+    torch, dev = _setup()
+    from llmcompressor_amd import gptq
+    from llmcompressor_amd.observers import Observer
+    from llmcompressor_amd.quant_args import QuantizationArgs
+
+    w, x = gen_inputs(torch, dev)
+    _torch_gptq_w4a16(torch, w[:256, :256].contiguous(), x[:2, :, :256].contiguous(), 2, GROUP)
+    h_ms, s_ms, Q, scale = _torch_gptq_w4a16(torch, w, x, BATCHES, GROUP)
+    ref_codes = torch.round(Q / scale.float().repeat_interleave(GROUP, dim=1)).to(torch.int32)
+    del Q
+
+    lin = torch.nn.Linear(COLS, ROWS, bias=False, device=dev, dtype=torch.bfloat16)
+    lin.weight.data = w
+    qa = QuantizationArgs(num_bits=4, type="int", symmetric=True, strategy="group", group_size=GROUP)
+
+    def step():
+        H = gptq.make_empty_hessian(lin)
+        H, n = gptq.accumulate_hessian(x, lin, H, torch.zeros((), device=dev))
+        obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+        obs(lin.weight)
+        return gptq.gptq_quantize(lin.weight, qa, H, obs, num_samples=float(BATCHES))
+
+    ms, res = _timed(torch, step, a.steps, a.warmup)
+    same = (res.codes.to(torch.int32) == ref_codes)
+    diff = (res.codes.to(torch.int32) - ref_codes).abs()
+    ref_ms = h_ms + s_ms
+    _line("GPTQ ms/layer of the reference's algorithm as torch ops on this GPU (W4A16 g128, 4096x4096, "
+          "64x2048 tokens)", ref_ms, "ms/layer", a, ref_ms, "torch_reference_gptq_w4a16_g128_4096x4096",
+          {"phases_ms": {"hessian": round(h_ms, 2), "solve": round(s_ms, 2)},
+           "mi355q_ms_per_layer": round(ms, 3), "speedup": round(ref_ms / ms, 1),
+           "scale_equal": bool(torch.equal(res.scale, scale)),
+           "code_agreement": round(float(same.float().mean()), 6), "max_code_diff": int(diff.max())},
+          dtype="fp32 (torch reference path)")
+
+
 OTHER_WORKLOADS = {"mxfp4": bench_mxfp4, "gptq_w8a8": bench_w8a8, "moe": bench_moe, "decoder": bench_decoder,
                    "sparsegpt": bench_sparsegpt, "mse_observer": bench_mse_observer,
-                   "pipeline": bench_pipeline}
+                   "pipeline": bench_pipeline, "torch_reference": bench_torch_reference}
 
 
 if __name__ == "__main__":

@@ -29,11 +29,9 @@ struct SweepState {
   float z[SW_T];   // zero point of each column
 };
 
-// Branch-free bf16 round-to-nearest-even of a finite fp32 value.
-__device__ __forceinline__ float bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
-}
+// bf16 round-to-nearest-even of a finite fp32 value (the gfx950 conversion
+// instruction: two operations on the sweep's serial chain instead of four).
+__device__ __forceinline__ float bf16_rne(float f) { return (float)(__bf16)f; }
 
 // CT quantize / dequantize of one value: qq = clamp(rint(x / s + z)),
 // deq = (qq - z) * s, rounded to bf16 when the scale is bf16 (BF16).  ZP:

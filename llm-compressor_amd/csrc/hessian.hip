@@ -21,14 +21,16 @@
 // them on a 2 x 2 grid of waves, each owning a (TM/2)^2 block of 32 x 32 MFMA
 // tiles; the streaming kernel on a 2 x 4 grid of 8 waves (two per SIMD, so
 // one wave's waits are covered by the other's MFMAs), each owning 128 x 64.
-// Partial tiles are written in the 2 x 2 layout's fragment order either way.
+// syrk_bf16_kernel writes partial tiles in its fragment order (one 16-float
+// run per thread and block); the streaming kernel in 1 KB chunks of one
+// float4 per lane, which its own reduction reads back coalesced.
 //
 // Work decomposition: a work item is (matrix e, upper tile t, token split s).
 // Token splits are assigned by blockIdx % S, and workgroups are dispatched
 // round-robin over the 8 XCDs, so with S = 8 each XCD streams only its own
 // eighth of X through its L2.  With S > 1 each item writes its partial tile
-// (in MFMA fragment order) to the workspace and a second kernel sums the
-// partials in split order and updates H, so results are deterministic.
+// to the workspace and a second kernel sums the partials in split order and
+// updates H, so results are deterministic.
 #include <vector>
 
 #include "common.h"
@@ -602,14 +604,14 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  // partial slot in MFMA fragment order (single-split calls, which update H
-  // directly, take syrk_bf16_kernel: the direct update's registers next to
-  // 256 live accumulators would spill here)
+  // partial slot (single-split calls, which update H directly, take
+  // syrk_bf16_kernel: the direct update's registers next to 256 live
+  // accumulators would spill here).  Slot layout: 256 chunks of 64 lanes x
+  // 4 floats, chunk ((wave MB + x) NBN + y) 4 + r4 holding accumulator
+  // registers 4 r4 .. 4 r4 + 3 of block (x, y), so every store and every
+  // load of the reduction moves 1 KB of consecutive bytes.
   if (slot < 0) return;
-  // slot in the fragment order of the 2 x 2 layout (the reduction's): wave
-  // (wm, wn >> 1), block (x, 2 (wn & 1) + y)
-  const int tid4 = (wm * 2 + (wn >> 1)) * 64 + lane;
-  float* dst = p.ws + (slot * NT + tid4) * C::ACC;
+  float* dst = p.ws + slot * C::TILE + 4 * lane;
 #pragma unroll
   for (int x = 0; x < MB; ++x)
 #pragma unroll
@@ -617,8 +619,88 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         f32x4_t v = {acc[x][y][4 * r4], acc[x][y][4 * r4 + 1], acc[x][y][4 * r4 + 2], acc[x][y][4 * r4 + 3]};
-        *reinterpret_cast<f32x4_t*>(dst + (x * C::NB + 2 * (wn & 1) + y) * 16 + 4 * r4) = v;
+        *reinterpret_cast<f32x4_t*>(dst + (((wave * MB + x) * NBN + y) * 4 + r4) * 256) = v;
       }
+}
+
+// Finishes the streaming kernel's tiles: for each tile the S split slots
+// are summed in split order (a tail tile's split being first the sum of its
+// tail_f part slots, in part order) and H is updated.  Workgroup
+// (t, blockIdx.y) takes chunks 16 blockIdx.y .. + 15 of tile t, four per
+// wave, one float4 per lane of each slot's chunk; all loads of a wave are
+// issued before its first sum, and all H reads before its first store.
+constexpr int RED_CPW = 4;  // chunks per wave of the streaming reduction
+__global__ __launch_bounds__(NT) void syrk_stream_reduce_kernel(const float* __restrict__ ws, int S,
+                                                                int tail_start, int tail_f, Matrix single,
+                                                                int64_t d, int64_t ldh, int nt, float alpha,
+                                                                float beta) {
+  constexpr int TM = 256, TILE = TM * TM, MB = 4, NBN = 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x;
+  int ti, tj;
+  tile_coords(t, nt, ti, tj);
+  const int ch0 = (NT / 64) * RED_CPW * blockIdx.y + RED_CPW * wave;
+  const float* src = ws + ch0 * 256 + 4 * lane;
+  f32x4_t tot[RED_CPW];
+#pragma unroll
+  for (int c = 0; c < RED_CPW; ++c) tot[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (t < tail_start) {
+    f32x4_t v[8][RED_CPW];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (s < S)
+#pragma unroll
+        for (int c = 0; c < RED_CPW; ++c)
+          v[s][c] = *reinterpret_cast<const f32x4_t*>(src + ((int64_t)t * S + s) * TILE + c * 256);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (s < S)
+#pragma unroll
+        for (int c = 0; c < RED_CPW; ++c)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) tot[c][q] += v[s][c][q];
+  } else {
+    const int64_t base = (int64_t)tail_start * S + (int64_t)(t - tail_start) * S * tail_f;
+    for (int s = 0; s < S; ++s) {
+      f32x4_t v[4][RED_CPW];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp)
+        if (pp < tail_f)
+#pragma unroll
+          for (int c = 0; c < RED_CPW; ++c)
+            v[pp][c] = *reinterpret_cast<const f32x4_t*>(src + (base + (int64_t)s * tail_f + pp) * TILE + c * 256);
+#pragma unroll
+      for (int c = 0; c < RED_CPW; ++c) {
+        f32x4_t ps = v[0][c];
+#pragma unroll
+        for (int pp = 1; pp < 4; ++pp)
+          if (pp < tail_f)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ps[q] += v[pp][c][q];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tot[c][q] += ps[q];
+      }
+    }
+  }
+  // chunk -> wave (wm, wn) of the 2 x 4 layout, block (x, y), registers 4 r4 + q
+  int64_t gi[RED_CPW], gj[RED_CPW];
+  float h[RED_CPW][4];
+#pragma unroll
+  for (int c = 0; c < RED_CPW; ++c) {
+    const int ch = ch0 + c;
+    const int w = ch >> 5, x = (ch >> 3) & (MB - 1), y = (ch >> 2) & (NBN - 1), r4 = ch & 3;
+    gi[c] = (int64_t)ti * TM + (w >> 2) * 128 + x * 32 + 8 * r4 + 4 * (lane >> 5);
+    gj[c] = (int64_t)tj * TM + (w & 3) * 64 + y * 32 + (lane & 31);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      h[c][q] = (gi[c] + q < d && gj[c] < d && gi[c] + q <= gj[c]) ? single.h[(gi[c] + q) * ldh + gj[c]] : 0.f;
+  }
+#pragma unroll
+  for (int c = 0; c < RED_CPW; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (gi[c] + q < d && gj[c] < d && gi[c] + q <= gj[c])
+        single.h[(gi[c] + q) * ldh + gj[c]] = scaled(h[c][q], beta) + alpha * tot[c][q];
 }
 
 // Sums the S partial slots of a tile in split order and updates H.  Each
@@ -626,9 +708,9 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
 // (blockIdx.y = bm), so a TM = 256 tile is finished by four workgroups.
 template <int TM>
 __global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict__ ws, const ReduceItem* items,
-                                                         int single_S, int tail_start, int64_t tail_base,
-                                                         Matrix single, const Matrix* mats, int64_t d,
-                                                         int64_t ldh, int nt, float alpha, float beta) {
+                                                         int single_S, Matrix single, const Matrix* mats,
+                                                         int64_t d, int64_t ldh, int nt, float alpha,
+                                                         float beta) {
   using C = Cfg<TM>;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -643,7 +725,7 @@ __global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict
     t = it.t; S = it.S; slot0 = it.slot0; mat = mats[it.e];
   } else {
     t = blockIdx.x; S = single_S; mat = single;
-    slot0 = t < tail_start ? (int64_t)t * S : tail_base + (int64_t)(t - tail_start) * S;
+    slot0 = (int64_t)t * S;
   }
   int ti, tj;
   tile_coords(t, nt, ti, tj);
@@ -692,29 +774,6 @@ __global__ void symmetrize_kernel(float* h, int64_t d, int64_t ldh) {
   }
 }
 
-// Dense tail: sums the tail_f part slots of each (tail tile, split) group,
-// in part order, into one slot (group g: slots src0 + g f .. + f - 1 ->
-// slot dst0 + g), so the reduction sees S slots per tile for every tile.
-// blockIdx.y picks a quarter of the slot.
-__global__ __launch_bounds__(NT) void syrk_tail_sum_kernel(float* ws, int64_t slot_floats, int64_t src0,
-                                                           int64_t dst0, int f) {
-  const int64_t g = blockIdx.x;
-  const int64_t q = slot_floats / 4;
-  const float* src = ws + (src0 + g * f) * slot_floats + blockIdx.y * q;
-  float* dst = ws + (dst0 + g) * slot_floats + blockIdx.y * q;
-  for (int64_t i = 4 * (int64_t)threadIdx.x; i < q; i += 4 * NT) {
-    f32x4_t acc = *reinterpret_cast<const f32x4_t*>(src + i);
-    for (int part = 1; part < f; ++part) {
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(src + part * slot_floats + i);
-      acc[0] += v[0];
-      acc[1] += v[1];
-      acc[2] += v[2];
-      acc[3] += v[3];
-    }
-    *reinterpret_cast<f32x4_t*>(dst + i) = acc;
-  }
-}
-
 int choose_splits(int64_t n) {
   const int64_t s = n / 2048;
   if (s >= 8) return 8;
@@ -737,13 +796,12 @@ inline size_t tile_floats(int64_t d) { return (size_t)tile_edge(d) * tile_edge(d
 // rounds and a last round with only T % 32 items.  The last rem = T % 32
 // tiles are therefore cut into f = min(4, 32 / rem) parts per split, so the
 // last round takes 1 / f of a full one (d = 4096: T = 136, rem = 8, f = 4,
-// 4.25 rounds instead of 5).  Their f part slots per split are summed into
-// one slot per split before the reduction.
+// 4.25 rounds instead of 5).  The reduction sums their f part slots per
+// split, in part order, before adding the split.
 constexpr int kCusPerXcd = 32;
 struct DensePlan {
   int S = 1, T = 0, tail_start = 0, tail_f = 1;
   int64_t grid = 0, slots = 0;
-  int64_t tail_src0 = 0, tail_dst0 = 0, tail_groups = 0;
 };
 DensePlan plan_dense(int64_t n, int64_t d) {
   DensePlan pl;
@@ -758,10 +816,7 @@ DensePlan plan_dense(int64_t n, int64_t d) {
   const int64_t nfull = (int64_t)pl.tail_start * pl.S;
   const int64_t ntail = (int64_t)(pl.T - pl.tail_start) * pl.S;
   pl.grid = nfull + ntail * pl.tail_f;
-  pl.tail_src0 = nfull;
-  pl.tail_dst0 = nfull + ntail * pl.tail_f;
-  pl.tail_groups = ntail;
-  pl.slots = pl.S > 1 ? (pl.tail_f > 1 ? pl.tail_dst0 + ntail : (int64_t)pl.T * pl.S) : 0;
+  pl.slots = pl.S > 1 ? pl.grid : 0;
   return pl;
 }
 
@@ -777,15 +832,15 @@ void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) 
   }
 }
 
-void launch_reduce(const float* ws, const ReduceItem* items, int S, int tail_start, int64_t tail_base,
-                   const Matrix& single, const Matrix* mats, int64_t d, int64_t ldh, int nt, float alpha,
-                   float beta, unsigned ntiles, hipStream_t st) {
+// reduction of syrk_bf16_kernel partials (2 x 2 fragment order)
+void launch_reduce(const float* ws, const ReduceItem* items, int S, const Matrix& single, const Matrix* mats,
+                   int64_t d, int64_t ldh, int nt, float alpha, float beta, unsigned ntiles, hipStream_t st) {
   if (tile_edge(d) == 256)
     hipLaunchKernelGGL(syrk_reduce_kernel<256>, dim3(ntiles, Cfg<256>::NB), dim3(NT), 0, st, ws, items, S,
-                       tail_start, tail_base, single, mats, d, ldh, nt, alpha, beta);
+                       single, mats, d, ldh, nt, alpha, beta);
   else
     hipLaunchKernelGGL(syrk_reduce_kernel<128>, dim3(ntiles, Cfg<128>::NB), dim3(NT), 0, st, ws, items, S,
-                       tail_start, tail_base, single, mats, d, ldh, nt, alpha, beta);
+                       single, mats, d, ldh, nt, alpha, beta);
 }
 
 // H[i][j] *= beta on the upper triangle (a call without tokens)
@@ -851,13 +906,11 @@ extern "C" int mi355q_hessian_syrk_scaled_bf16(const void* x_dev, int64_t n_toke
   launch_syrk(p, d, (unsigned)pl.grid, st);
   MQ_LAUNCH_CHECK();
   if (S > 1) {
-    if (pl.tail_f > 1) {
-      hipLaunchKernelGGL(syrk_tail_sum_kernel, dim3((unsigned)pl.tail_groups, 4), dim3(NT), 0, st, p.ws,
-                         (int64_t)tile_floats(d), pl.tail_src0, pl.tail_dst0, pl.tail_f);
-      MQ_LAUNCH_CHECK();
-    }
-    launch_reduce(p.ws, nullptr, S, pl.tail_start, pl.tail_dst0, p.single, nullptr, d, ldh, nt, alpha, beta,
-                  (unsigned)T, st);
+    if (tile_edge(d) == 256)  // the streaming kernel's slots
+      hipLaunchKernelGGL(syrk_stream_reduce_kernel, dim3((unsigned)T, 256 / ((NT / 64) * RED_CPW)), dim3(NT), 0,
+                         st, p.ws, S, pl.tail_start, pl.tail_f, p.single, d, ldh, nt, alpha, beta);
+    else
+      launch_reduce(p.ws, nullptr, S, p.single, nullptr, d, ldh, nt, alpha, beta, (unsigned)T, st);
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;
@@ -965,7 +1018,7 @@ extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, 
   launch_syrk(p, d, (unsigned)g.items.size(), st);
   MQ_LAUNCH_CHECK();
   if (!g.reduces.empty()) {
-    launch_reduce(p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, 0, 0, Matrix{}, p.mats, d, d,
+    launch_reduce(p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, Matrix{}, p.mats, d, d,
                   p.nt, alpha, 1.f, (unsigned)g.reduces.size(), st);
     MQ_LAUNCH_CHECK();
   }

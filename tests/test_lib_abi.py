@@ -31,8 +31,8 @@ def test_version_and_workspace_queries():
     assert lib.mi355q_version() == 1
     assert lib.mi355q_hessian_workspace_size(2048, 4096) == 0            # single split, direct update
     # d = 4096: 136 tiles, 8 splits; the last 8 tiles run as 4 parts per split
-    # (128 * 8 + 8 * 8 * 4 part slots + 8 * 8 summed slots)
-    assert lib.mi355q_hessian_workspace_size(131072, 4096) == (128 * 8 + 8 * 8 * 4 + 8 * 8) * 256 * 256 * 4
+    # (128 * 8 split slots + 8 * 8 * 4 part slots, summed by the reduction)
+    assert lib.mi355q_hessian_workspace_size(131072, 4096) == (128 * 8 + 8 * 8 * 4) * 256 * 256 * 4
     assert lib.mi355q_hessian_workspace_size(131072, 384) == 8 * 6 * 128 * 128 * 4
     assert lib.mi355q_gptq_sweep_workspace_size(4096, 4096, 128) == 4096 * 1024 * 4   # errors of one 1024-column super-block
     assert lib.mi355q_gptq_sweep_workspace_size(768, 768, 128) == 768 * 768 * 4       # fewer columns than a super-block
