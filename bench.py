@@ -126,22 +126,15 @@ def main():
     sc = res.scale.float().repeat_interleave(GROUP, dim=1)
     assert torch.equal((codes.float() * sc).to(torch.bfloat16), res.weight)
 
-    # Hessian kernel alone (syrk + split reduction), HIP events on its stream
-    H = torch.zeros(COLS, COLS, device=dev)
-    xf = x.reshape(-1, COLS)
-    for _ in range(2):
-        ops.hessian_syrk_(H, xf)
-    reps = 5
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        ops.hessian_syrk_(H, xf)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    syrk_ms = e0.elapsed_time(e1) / reps
+    # the dominant kernel: the Hessian call (stream + reduction kernels) of
+    # each timed step, HIP events on the kernels' stream around it
     n_tok = BATCHES * SEQ
     syrk_flop = n_tok * COLS * (COLS + 1)  # upper triangle incl. diagonal, 2 flop / MAC
+    syrk_ms = hess_ms
     syrk_tflops = syrk_flop / (syrk_ms * 1e-3) / 1e12
+    xf = x.reshape(-1, COLS)
+    reps = 5
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     # vendor GEMM on the same product: torch.mm (hipBLASLt) of X^T X as the
     # full 4096 x 4096 square with a bf16 result (twice the multiply-adds of
@@ -219,7 +212,7 @@ def main():
                    "tokens": n_tok, "group_size": GROUP, "blocksize": 128, "damp": 0.01, "actorder": None,
                    "hessian_calls": a.hessian_calls},
         "phases_ms": {"hessian": round(hess_ms, 3), "solve": round(solve_ms, 3)},
-        "hessian": {"kernel_ms": round(syrk_ms, 4), "tflops": round(syrk_tflops, 1),
+        "hessian": {"ms": round(syrk_ms, 4), "tflops": round(syrk_tflops, 1),
                     "frac_fp32_mfma_peak": round(syrk_tflops / PEAK_FP32_MFMA_TFLOPS, 3),
                     "frac_bf16_mfma_peak": round(syrk_tflops / PEAK_BF16_TFLOPS, 4),
                     "vendor_gemm_full_square_bf16_out": {"ms": round(mm_ms, 4), "tflops": round(mm_tflops, 1)}},
@@ -227,7 +220,8 @@ def main():
         "copy_1GiB_GB_s": round(copy_gbs, 1),
         "roofline": {"bound": "mfma", "achieved": round(syrk_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(syrk_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "syrk_stream_kernel + syrk_stream_reduce_kernel (one Hessian call, 131072 tokens)"},
+                     "kernel": "syrk_stream_kernel + syrk_stream_reduce_kernel (the Hessian call of each timed step, "
+                               "131072 tokens)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -685,6 +679,25 @@ def _torch_gptq_w4a16(torch, w, x, num_samples, group, blocksize=128, percdamp=0
     return (t1 - t0) * 1e3, (t2 - t1) * 1e3, W, scale
 
 
+def _torch_mxfp4(torch, t):
+    """MXFP4 quantize + pack as torch ops (the compressed-tensors path the
+    reference calls: group absmax, e8m0 exponent of the bf16-rounded absmax,
+    division by the power-of-two scale, the e2m1 thresholds of
+    ``cast_to_fp4``, two codes per byte)."""
+    rows, cols = t.shape
+    g = t.view(rows, cols // 32, 32)
+    amax = torch.amax(torch.abs(g), dim=-1)
+    bits = ((amax.view(torch.int16).to(torch.int32) & 0xFFFF) + 32) & 0xFF80
+    e8 = torch.clamp(((bits >> 7) & 0xFF) - 2, 0, 254)
+    e8 = torch.where(bits == 0, torch.zeros_like(e8), e8)
+    v = g.to(torch.float32) / torch.pow(2.0, (e8 - 127).to(torch.float32))[..., None]
+    a = torch.abs(v)
+    idx = sum((a > th).to(torch.uint8) for th in (0.25, 1.25, 2.5, 5.0)) + \
+        sum((a >= th).to(torch.uint8) for th in (0.75, 1.75, 3.5))
+    code = (idx | ((v < 0).to(torch.uint8) << 3)).view(rows, cols)
+    return code[:, 0::2] | (code[:, 1::2] << 4), e8.to(torch.uint8)
+
+
 def bench_torch_reference(a):
     """The headline layer (W4A16 g128, 4096 x 4096, 64 x 2048 tokens) through
     the reference's algorithm as plain torch ops on the same GPU, beside this
@@ -714,6 +727,18 @@ def bench_torch_reference(a):
         return gptq.gptq_quantize(lin.weight, qa, H, obs, num_samples=float(BATCHES))
 
     ms, res = _timed(torch, step, a.steps, a.warmup)
+
+    # MXFP4 quantize + pack of W 4096 x 14336 (the MXFP4 configuration's weight)
+    from llmcompressor_amd import ops
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    t = (torch.randn((4096, 14336), generator=gen, device=dev) * 0.015).to(torch.bfloat16)
+    mx_ref_ms, (p_ref, e_ref) = _timed(torch, lambda: _torch_mxfp4(torch, t), 3, 1)
+    mx_ms, (p_us, e_us) = _timed(torch, lambda: ops.mxfp4_quantize_pack(t), 20, 3)
+    mx = {"torch_ms": round(mx_ref_ms, 4), "mi355q_ms": round(mx_ms, 4), "speedup": round(mx_ref_ms / mx_ms, 1),
+          "bit_equal": bool(torch.equal(p_ref, p_us) and torch.equal(e_ref, e_us))}
+    del t
+
     same = (res.codes.to(torch.int32) == ref_codes)
     diff = (res.codes.to(torch.int32) - ref_codes).abs()
     ref_ms = h_ms + s_ms
@@ -722,7 +747,8 @@ def bench_torch_reference(a):
           {"phases_ms": {"hessian": round(h_ms, 2), "solve": round(s_ms, 2)},
            "mi355q_ms_per_layer": round(ms, 3), "speedup": round(ref_ms / ms, 1),
            "scale_equal": bool(torch.equal(res.scale, scale)),
-           "code_agreement": round(float(same.float().mean()), 6), "max_code_diff": int(diff.max())},
+           "code_agreement": round(float(same.float().mean()), 6), "max_code_diff": int(diff.max()),
+           "mxfp4_quantize_pack_4096x14336": mx},
           dtype="fp32 (torch reference path)")
 
 

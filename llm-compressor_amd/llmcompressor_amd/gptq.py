@@ -220,10 +220,12 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
                           prepared: PreparedHessian | None = None) -> list[GPTQResult]:
     """``gptq_quantize`` for B same-shaped modules at once (the experts of an
     MoE layer): weights [B, rows, cols], hessians [B, cols, cols] (upper
-    triangles), num_samples a number or [B].  Each module gets exactly the
-    result of its own ``gptq_quantize`` call (same kernels, one launch per
-    step for the whole batch, one host synchronisation for the status flags
-    and one for the losses).  The weight observer named ``observer`` is run
+    triangles), num_samples a number or [B].  Each module gets the result of
+    its own ``gptq_quantize`` call (one launch per step for the whole batch,
+    one host synchronisation for the status flags and one for the losses):
+    bit for bit while the batch's lazy-update products take the same GEMM
+    tile kernel as a single module's, which depends on the total row count;
+    otherwise they differ by fp32 summation order.  The weight observer named ``observer`` is run
     here on the stacked weights (its statistics are per row for channel and
     group strategies).  ``prepared`` (``prepare_hessians_batched`` on the same
     stack and args) is shared by projections with the same input (gate, up).
