@@ -14,7 +14,9 @@ masks, position embeddings) for all layers, as decoder stacks call them.
 Offloading copies tensors into pinned host memory on a copy stream of its own
 (default priority) once their producer has run; fetching copies them back on
 that stream, and the consumer's stream waits on an event, so the prefetch of
-batch b + 1 overlaps the layer's work on batch b.
+batch b + 1 overlaps the layer's work on batch b, and the first batch of a
+pass is fetched while the previous step (the layer's compression, or the end
+of the previous pass) still runs.
 """
 from __future__ import annotations
 
@@ -125,14 +127,21 @@ class IntermediatesCache:
         for b in range(len(self.batches)):
             yield self.fetch(b, input_names)
 
-    def iter_prefetch(self, input_names=None) -> Iterator[dict[str, Any]]:
-        """As ``iter``, with batch b + 1's copies issued before batch b is used."""
+    def iter_prefetch(self, input_names=None, first=None) -> Iterator[dict[str, Any]]:
+        """As ``iter``, with batch b + 1's copies issued before batch b is used;
+        ``first``: batch 0 as already started by ``prefetch(0)``."""
         n = len(self.batches)
-        nxt = None
+        nxt = first
         for b in range(n):
             cur = nxt if nxt is not None else self._start(b, input_names)
             nxt = self._start(b + 1, input_names) if b + 1 < n else None
             yield self._ready(cur)
+
+    def prefetch(self, batch_index: int, input_names=None):
+        """Starts the copies of one batch back to the device (for a later
+        ``iter_prefetch(first=...)``); the batch must not be updated before
+        it is consumed."""
+        return self._start(batch_index, input_names)
 
     def _start(self, b, input_names):
         d = self.batches[b]
@@ -214,24 +223,41 @@ def sequential_calibrate(model: torch.nn.Module, layers, batches, modifier, prop
 
     modifier.on_initialize(model)
     modifier.on_calibration_start(model)
-    batches_of = cache.iter_prefetch if prefetch else cache.iter
+
+    def batches_of(first):
+        return cache.iter_prefetch(first=first) if prefetch else cache.iter()
 
     def run(layer, b, inputs):
         out = layer(*inputs["args"], **inputs["kwargs"])
         return _first_output(out)
 
-    for layer in layers:
+    # With prefetch, the first batch of each pass is copied back while the
+    # previous step still runs: the propagation pass's (unchanged inputs)
+    # during the layer's compression, the next layer's as soon as this pass
+    # has replaced it.
+    pending = None
+    for li, layer in enumerate(layers):
+        ahead = prefetch and li + 1 < len(layers) and len(cache) > 0  # a next layer to prefetch for
+        nxt = None
         # each batch's entry is replaced as soon as it has been consumed (the
         # prefetch has already issued the next batch's copies)
-        for b, inputs in enumerate(batches_of()):
+        for b, inputs in enumerate(batches_of(pending)):
             out = run(layer, b, inputs)
             if not propagate_error:
                 cache.update(b, {"args": (out,) + tuple(inputs["args"][1:])})
-        _compress(modifier, layer)
+                if b == 0 and ahead:
+                    nxt = cache.prefetch(0)
         if propagate_error:
+            pending = cache.prefetch(0) if prefetch and len(cache) > 0 else None
+            _compress(modifier, layer)
             with _hooks_disabled(modifier):
-                for b, inputs in enumerate(batches_of()):
+                for b, inputs in enumerate(batches_of(pending)):
                     cache.update(b, {"args": (run(layer, b, inputs),) + tuple(inputs["args"][1:])})
+                    if b == 0 and ahead:
+                        nxt = cache.prefetch(0)
+        else:
+            _compress(modifier, layer)
+        pending = nxt
     modifier.on_calibration_end()
     modifier.on_finalize()
     return cache
