@@ -13,7 +13,9 @@ masks, position embeddings) for all layers, as decoder stacks call them.
 
 Offloading copies tensors into pinned host memory on a copy stream of its own
 (default priority) once their producer has run; fetching copies them back on
-that stream, and the consumer's stream waits on an event, so the prefetch of
+a second copy stream (so a fetch never queues behind unrelated offloads, and
+the two directions of the link run at once), and the consumer's stream waits
+on an event, so the prefetch of
 batch b + 1 overlaps the layer's work on batch b, and the first batch of a
 pass is fetched while the previous step (the layer's compression, or the end
 of the previous pass) still runs.
@@ -45,19 +47,20 @@ class IntermediatesCache:
     def __init__(self, num_batches: int, offload_device: str | None = "cpu"):
         self.batches: list[dict[str, Any]] = [{} for _ in range(num_batches)]
         self.offload_device = offload_device
-        self._copy_stream = None
+        self._streams = {}
 
-    def _stream(self, device):
-        if self._copy_stream is None:
-            self._copy_stream = torch.cuda.Stream(device=device)
-        return self._copy_stream
+    def _stream(self, device, direction: str):
+        """The copy stream for "d2h" (offload) or "h2d" (fetch)."""
+        if direction not in self._streams:
+            self._streams[direction] = torch.cuda.Stream(device=device)
+        return self._streams[direction]
 
     # -- offload / onload of nested values
     def _offload(self, v):
         if isinstance(v, torch.Tensor):
             if self.offload_device is None or v.device.type != "cuda":
                 return v
-            cs = self._stream(v.device)
+            cs = self._stream(v.device, "d2h")
             cs.wait_stream(torch.cuda.current_stream(v.device))
             host = torch.empty(v.shape, dtype=v.dtype, pin_memory=True)
             with torch.cuda.stream(cs):
@@ -77,7 +80,7 @@ class IntermediatesCache:
     def _onload_async(self, v):
         """Start the copies back; returns the value with _Pending leaves."""
         if isinstance(v, _Offloaded):
-            cs = self._stream(v.device)
+            cs = self._stream(v.device, "h2d")
             with torch.cuda.stream(cs):
                 cs.wait_event(v.event)
                 dev = torch.empty(v.host.shape, dtype=v.host.dtype, device=v.device)
