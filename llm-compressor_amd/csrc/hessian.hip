@@ -774,12 +774,16 @@ __global__ void symmetrize_kernel(float* h, int64_t d, int64_t ldh) {
   }
 }
 
-int choose_splits(int64_t n) {
+// Token splits of a T-tile matrix over n tokens: up to 8 (at least 2048
+// tokens each), one per XCD, while the tiles alone would leave CUs idle;
+// with more than two rounds of tiles per CU, at most 2 (each split slot
+// costs a 256 KiB partial written and read back: at d = 14336 and 16384
+// tokens, 8 splits move 6.7 GB for 3.4 TFLOP of work).
+int choose_splits(int64_t n, int T) {
   const int64_t s = n / 2048;
-  if (s >= 8) return 8;
-  if (s >= 4) return 4;
-  if (s >= 2) return 2;
-  return 1;
+  int S = s >= 8 ? 8 : s >= 4 ? 4 : s >= 2 ? 2 : 1;
+  if (T > 512 && S > 2) S = 2;
+  return S;
 }
 
 inline int tile_edge(int64_t d) { return d >= 512 ? 256 : 128; }
@@ -805,8 +809,8 @@ struct DensePlan {
 };
 DensePlan plan_dense(int64_t n, int64_t d) {
   DensePlan pl;
-  pl.S = choose_splits(n);
   pl.T = upper_tiles(tiles_per_edge(d));
+  pl.S = choose_splits(n, pl.T);
   pl.tail_start = pl.T;
   const int rem = pl.T % kCusPerXcd;
   if (pl.S == 8 && tile_edge(d) == 256 && rem > 0 && rem <= kCusPerXcd / 2) {
@@ -941,7 +945,7 @@ GroupedPlan plan_grouped(const int64_t* offsets, int E, int64_t d, float* h, int
     const int64_t n = offsets[e + 1] - offsets[e];
     g.mats.push_back(Matrix{offsets[e], n, h ? h + (int64_t)e * h_stride : nullptr});
     if (n <= 0) continue;
-    const int S = choose_splits(n);
+    const int S = choose_splits(n, T);
     for (int t = 0; t < T; ++t) {
       const int64_t slot0 = S > 1 ? g.slots : -1;
       for (int s = 0; s < S; ++s) g.items.push_back(Item{e, t, s, S, S > 1 ? slot0 + s : -1});

@@ -56,6 +56,22 @@ def test_hessian_syrk_parity(dev, n, d):
     assert torch.equal(H2.cpu(), got)  # deterministic
 
 
+def test_hessian_syrk_many_tiles(dev):
+    """d = 8192 (528 tiles, so at most two token splits): upper triangle
+    against an fp64 product on the GPU."""
+    n, d = 16384, 8192
+    say(f"hessian syrk n={n} d={d} (fp64 GPU reference)")
+    x = workloads.heavy_tailed_activations((n, d), seed=5).to(dev)
+    H = torch.zeros(d, d, device=dev)
+    ops.hessian_syrk_(H, x, alpha=2.0)
+    xd = x.double()
+    ref = 2.0 * (xd.t().contiguous() @ xd)
+    up = torch.triu(torch.ones(d, d, dtype=torch.bool, device=dev))
+    r = ((H.double() - ref)[up].norm() / ref[up].norm()).item()
+    assert r <= HESS_TOL, r
+    assert torch.count_nonzero(torch.tril(H, -1)) == 0
+
+
 def test_hessian_dropin_counts_and_strided_input(dev):
     say("accumulate_hessian drop-in")
     lin = torch.nn.Linear(128, 16, bias=False).to(dev)
