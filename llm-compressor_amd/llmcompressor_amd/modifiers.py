@@ -33,7 +33,7 @@ import torch
 
 from .calibration import initialize_module_for_quantization, initialize_observer, observe, update_qparams
 from . import sparsegpt as sgpt
-from .gptq import accumulate_hessian, gptq_quantize, make_empty_hessian
+from .gptq import _effective_actorder, accumulate_hessian, gptq_quantize, make_empty_hessian, prepare_hessian
 from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationScheme, preset_name_to_scheme
 
 logger = logging.getLogger("llmcompressor_amd")
@@ -109,14 +109,26 @@ class QuantizationModifier:
 class GPTQModifier(QuantizationModifier):
     def __init__(self, scheme=None, targets=("Linear",), ignore=("lm_head",), config_groups=None,
                  block_size: int = 128, dampening_frac: float | None = 0.01, actorder="static",
-                 offload_hessians: bool = False):
+                 offload_hessians: bool = False, share_hessians: bool = True):
         super().__init__(scheme, targets, ignore, config_groups)
         self.block_size = block_size
         self.dampening_frac = dampening_frac
         self.actorder = actorder
         self.offload_hessians = offload_hessians
+        # Modules fed the very same input tensor (q/k/v, gate/up) accumulate
+        # one Hessian and share one Cholesky chain: the reference computes the
+        # same matrices once per module, with the same results.  A group is
+        # formed in the first batch (a module joins the module that has just
+        # accumulated that tensor as its only input) and must see one tensor
+        # per forward afterwards; otherwise an error asks for
+        # share_hessians=False.
+        self.share_hessians = share_hessians
         self._hessians: dict = {}
         self._num_samples: dict = {}
+        self._leader: dict = {}     # member module -> the module whose Hessian it shares
+        self._calls: dict = {}      # accumulating module -> inputs accumulated
+        self._held: dict = {}       # accumulating module -> its last input (kept alive so its
+        self._last = None           # address cannot be reused); module of the last accumulation
         self._hooks = []
         self.timings: dict[str, float] = {}
 
@@ -136,10 +148,36 @@ class GPTQModifier(QuantizationModifier):
         if w.actorder == ActivationOrdering.GROUP and w.strategy.value not in ("group", "tensor_group"):
             w.actorder = None
 
+    @staticmethod
+    def _same_tensor(a, b) -> bool:
+        return b is not None and (a is b or (a.data_ptr() == b.data_ptr() and a.shape == b.shape
+                                             and a.stride() == b.stride() and a.dtype == b.dtype
+                                             and a._version == b._version))
+
+    def _shared(self, module, inp) -> bool:
+        """True when ``module``'s Hessian is a group's that already holds ``inp``."""
+        leader = self._leader.get(module)
+        if leader is not None:
+            if not self._same_tensor(inp, self._held.get(leader)):
+                raise RuntimeError(f"GPTQModifier: {self._modules.get(module)} shared its input with "
+                                   f"{self._modules.get(leader)} in the first calibration batch but not in a "
+                                   "later one; pass share_hessians=False")
+            return True
+        if module in self._num_samples or self._last is None:
+            return False
+        cand = self._last
+        if self._calls.get(cand) == 1 and self._same_tensor(inp, self._held.get(cand)):
+            self._leader[module] = cand
+            self._num_samples[module] = None    # read from the leader at compression
+            return True
+        return False
+
     def calibrate_module(self, module, args, _output):
         if getattr(self, "_hooks_disabled", False):   # a propagation pass of the sequential pipeline
             return
         inp = args[0]
+        if self.share_hessians and self._shared(module, inp):
+            return
         if module not in self._num_samples:
             dev = module.weight.device
             self._hessians[module] = make_empty_hessian(module, device="cpu" if self.offload_hessians else dev)
@@ -149,6 +187,10 @@ class GPTQModifier(QuantizationModifier):
             H = H.to(module.weight.device)
         H, self._num_samples[module] = accumulate_hessian(inp, module, H, self._num_samples[module])
         self._hessians[module] = H.to("cpu") if self.offload_hessians else H
+        if self.share_hessians:
+            self._calls[module] = self._calls.get(module, 0) + 1
+            self._held[module] = inp
+            self._last = module
 
     def on_calibration_start(self, model):
         for m in self._modules:
@@ -164,26 +206,44 @@ class GPTQModifier(QuantizationModifier):
         self.compress_modules()
 
     def compress_modules(self):
-        for module in list(self._num_samples):
-            name = self._modules[module]
-            n = float(self._num_samples.pop(module).item())
-            H = self._hessians.pop(module).to(module.weight.device)
-            qa = module.quantization_scheme.weights
-            t0 = time.perf_counter()
-            with torch.no_grad():
-                res = gptq_quantize(module.weight, qa, H, module.weight_observer, self.block_size,
-                                    self.dampening_frac, num_samples=n)
-            self.timings[name] = time.perf_counter() - t0
-            logger.info("Quantized %s using %d samples, loss %.4f", name, int(n), res.loss)
-            with torch.no_grad():
-                module.weight.data.copy_(res.weight)
-                update = {"weight_scale": res.scale.to(module.weight.dtype),
-                          "weight_zero_point": res.zero_point.to(qa.zp_dtype)}
-                if qa.actorder == ActivationOrdering.GROUP:
-                    update["weight_g_idx"] = res.g_idx[torch.argsort(res.perm)]
-                for k, v in update.items():
-                    setattr(module, k, torch.nn.Parameter(v, requires_grad=False))
-            module.gptq_codes = res.codes
+        groups: dict = {}
+        for module in self._num_samples:
+            groups.setdefault(self._leader.get(module, module), []).append(module)
+        self._leader, self._calls, self._held, self._last = {}, {}, {}, None
+        for leader, members in groups.items():
+            n = float(self._num_samples[leader].item())
+            H = self._hessians.pop(leader).to(leader.weight.device)
+            prepared: dict = {}
+            for module in members:
+                del self._num_samples[module]
+                self._compress_one(module, H, n, prepared if len(members) > 1 else None)
+
+    def _compress_one(self, module, H, n, prepared):
+        """GPTQ of one module; ``prepared`` caches the Cholesky chain of a
+        shared Hessian per activation ordering."""
+        name = self._modules[module]
+        qa = module.quantization_scheme.weights
+        t0 = time.perf_counter()
+        prep = None
+        if prepared is not None:
+            key = _effective_actorder(qa)
+            if key not in prepared:
+                prepared[key] = prepare_hessian(H, qa, n, self.dampening_frac)
+            prep = prepared[key]
+        with torch.no_grad():
+            res = gptq_quantize(module.weight, qa, H, module.weight_observer, self.block_size,
+                                self.dampening_frac, num_samples=n, prepared=prep)
+        self.timings[name] = time.perf_counter() - t0
+        logger.info("Quantized %s using %d samples, loss %.4f", name, int(n), res.loss)
+        with torch.no_grad():
+            module.weight.data.copy_(res.weight)
+            update = {"weight_scale": res.scale.to(module.weight.dtype),
+                      "weight_zero_point": res.zero_point.to(qa.zp_dtype)}
+            if qa.actorder == ActivationOrdering.GROUP:
+                update["weight_g_idx"] = res.g_idx[torch.argsort(res.perm)]
+            for k, v in update.items():
+                setattr(module, k, torch.nn.Parameter(v, requires_grad=False))
+        module.gptq_codes = res.codes
 
     def on_calibration_end(self):
         for h in self._hooks:

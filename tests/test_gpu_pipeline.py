@@ -137,3 +137,41 @@ def test_sparsegpt_through_the_pipeline(dev):
     for name, p in model.named_parameters():
         z = (p.reshape(p.shape[0], -1, 4) == 0).sum(-1)
         assert torch.all(z >= 2), name
+
+
+def test_shared_hessians_change_nothing(dev):
+    """gate and up read the same tensor: one Hessian and one Cholesky chain
+    for both give exactly the weights of separate ones."""
+    say("shared Hessians vs separate")
+    model, batches = _setup(dev)
+    ref = copy.deepcopy(model)
+    GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), share_hessians=False).apply(ref, batches)
+    mod = _gptq()
+    mod.apply(model, batches)
+    _assert_same(_weights(model), _weights(ref))
+
+
+class _TwoReaders(torch.nn.Module):
+    """a and b read the same tensor in the first forward only."""
+
+    def __init__(self):
+        super().__init__()
+        self.a = torch.nn.Linear(256, 256, bias=False)
+        self.b = torch.nn.Linear(256, 256, bias=False)
+        self.calls = 0
+
+    def forward(self, x):
+        y = self.a(x) + self.b(x if self.calls == 0 else x.clone())
+        self.calls += 1
+        return y
+
+
+def test_shared_hessians_divergence_raises(dev):
+    say("shared Hessians: inputs that stop being shared")
+    torch.manual_seed(1)
+    batches = [workloads.heavy_tailed_activations((2, 64, 256), seed=40 + s).to(dev) for s in range(2)]
+    model = _TwoReaders().to(dev).to(torch.bfloat16)
+    ref = copy.deepcopy(model)
+    with pytest.raises(RuntimeError, match="share_hessians=False"):
+        _gptq().apply(model, batches)
+    GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), share_hessians=False).apply(ref, batches)
