@@ -106,7 +106,61 @@ class QuantizationModifier:
         return model
 
 
-class GPTQModifier(QuantizationModifier):
+class _SharedHessians:
+    """Modules fed the very same input tensor (q/k/v, gate/up) accumulate one
+    Hessian: the reference computes the same matrix once per module, with the
+    same result.  A group is formed in the first batch (a module joins the
+    module that has just accumulated that tensor as its only input) and must
+    see one tensor per forward afterwards; otherwise an error asks for
+    share_hessians=False.  The last accumulated input of each group is kept
+    alive, so its address cannot be reused by another tensor."""
+
+    def _init_sharing(self, share: bool):
+        self.share_hessians = share
+        self._leader: dict = {}     # member module -> the module whose Hessian it shares
+        self._calls: dict = {}      # accumulating module -> inputs accumulated
+        self._held: dict = {}       # accumulating module -> its last input
+        self._last = None           # module of the last accumulation
+
+    @staticmethod
+    def _same_tensor(a, b) -> bool:
+        return b is not None and (a is b or (a.data_ptr() == b.data_ptr() and a.shape == b.shape
+                                             and a.stride() == b.stride() and a.dtype == b.dtype
+                                             and a._version == b._version))
+
+    def _shared(self, module, inp, name) -> bool:
+        """True when ``module``'s Hessian is a group's that already holds ``inp``."""
+        leader = self._leader.get(module)
+        if leader is not None:
+            if not self._same_tensor(inp, self._held.get(leader)):
+                raise RuntimeError(f"{type(self).__name__}: {name(module)} shared its input with {name(leader)} "
+                                   "in the first calibration batch but not in a later one; pass "
+                                   "share_hessians=False")
+            return True
+        if module in self._num_samples or self._last is None:
+            return False
+        cand = self._last
+        if self._calls.get(cand) == 1 and self._same_tensor(inp, self._held.get(cand)):
+            self._leader[module] = cand
+            self._num_samples[module] = None    # read from the leader at compression
+            return True
+        return False
+
+    def _note_accumulated(self, module, inp):
+        self._calls[module] = self._calls.get(module, 0) + 1
+        self._held[module] = inp
+        self._last = module
+
+    def _take_groups(self) -> dict:
+        """{accumulating module: [it and the modules sharing its Hessian]}; resets the bookkeeping."""
+        groups: dict = {}
+        for module in self._num_samples:
+            groups.setdefault(self._leader.get(module, module), []).append(module)
+        self._init_sharing(self.share_hessians)
+        return groups
+
+
+class GPTQModifier(QuantizationModifier, _SharedHessians):
     def __init__(self, scheme=None, targets=("Linear",), ignore=("lm_head",), config_groups=None,
                  block_size: int = 128, dampening_frac: float | None = 0.01, actorder="static",
                  offload_hessians: bool = False, share_hessians: bool = True):
@@ -115,20 +169,11 @@ class GPTQModifier(QuantizationModifier):
         self.dampening_frac = dampening_frac
         self.actorder = actorder
         self.offload_hessians = offload_hessians
-        # Modules fed the very same input tensor (q/k/v, gate/up) accumulate
-        # one Hessian and share one Cholesky chain: the reference computes the
-        # same matrices once per module, with the same results.  A group is
-        # formed in the first batch (a module joins the module that has just
-        # accumulated that tensor as its only input) and must see one tensor
-        # per forward afterwards; otherwise an error asks for
-        # share_hessians=False.
-        self.share_hessians = share_hessians
+        # modules sharing an input also share one Cholesky chain per
+        # activation ordering at compression
+        self._init_sharing(share_hessians)
         self._hessians: dict = {}
         self._num_samples: dict = {}
-        self._leader: dict = {}     # member module -> the module whose Hessian it shares
-        self._calls: dict = {}      # accumulating module -> inputs accumulated
-        self._held: dict = {}       # accumulating module -> its last input (kept alive so its
-        self._last = None           # address cannot be reused); module of the last accumulation
         self._hooks = []
         self.timings: dict[str, float] = {}
 
@@ -148,35 +193,11 @@ class GPTQModifier(QuantizationModifier):
         if w.actorder == ActivationOrdering.GROUP and w.strategy.value not in ("group", "tensor_group"):
             w.actorder = None
 
-    @staticmethod
-    def _same_tensor(a, b) -> bool:
-        return b is not None and (a is b or (a.data_ptr() == b.data_ptr() and a.shape == b.shape
-                                             and a.stride() == b.stride() and a.dtype == b.dtype
-                                             and a._version == b._version))
-
-    def _shared(self, module, inp) -> bool:
-        """True when ``module``'s Hessian is a group's that already holds ``inp``."""
-        leader = self._leader.get(module)
-        if leader is not None:
-            if not self._same_tensor(inp, self._held.get(leader)):
-                raise RuntimeError(f"GPTQModifier: {self._modules.get(module)} shared its input with "
-                                   f"{self._modules.get(leader)} in the first calibration batch but not in a "
-                                   "later one; pass share_hessians=False")
-            return True
-        if module in self._num_samples or self._last is None:
-            return False
-        cand = self._last
-        if self._calls.get(cand) == 1 and self._same_tensor(inp, self._held.get(cand)):
-            self._leader[module] = cand
-            self._num_samples[module] = None    # read from the leader at compression
-            return True
-        return False
-
     def calibrate_module(self, module, args, _output):
         if getattr(self, "_hooks_disabled", False):   # a propagation pass of the sequential pipeline
             return
         inp = args[0]
-        if self.share_hessians and self._shared(module, inp):
+        if self.share_hessians and self._shared(module, inp, self._modules.get):
             return
         if module not in self._num_samples:
             dev = module.weight.device
@@ -188,9 +209,7 @@ class GPTQModifier(QuantizationModifier):
         H, self._num_samples[module] = accumulate_hessian(inp, module, H, self._num_samples[module])
         self._hessians[module] = H.to("cpu") if self.offload_hessians else H
         if self.share_hessians:
-            self._calls[module] = self._calls.get(module, 0) + 1
-            self._held[module] = inp
-            self._last = module
+            self._note_accumulated(module, inp)
 
     def on_calibration_start(self, model):
         for m in self._modules:
@@ -206,11 +225,7 @@ class GPTQModifier(QuantizationModifier):
         self.compress_modules()
 
     def compress_modules(self):
-        groups: dict = {}
-        for module in self._num_samples:
-            groups.setdefault(self._leader.get(module, module), []).append(module)
-        self._leader, self._calls, self._held, self._last = {}, {}, {}, None
-        for leader, members in groups.items():
+        for leader, members in self._take_groups().items():
             n = float(self._num_samples[leader].item())
             H = self._hessians.pop(leader).to(leader.weight.device)
             prepared: dict = {}
@@ -268,7 +283,7 @@ class GPTQModifier(QuantizationModifier):
         return model
 
 
-class SparseGPTModifier:
+class SparseGPTModifier(_SharedHessians):
     """One-shot SparseGPT (``modifiers/pruning/sparsegpt/base.py:24-173``).
 
     ``targets`` name the layers that carry a sparsity (a float for all, or
@@ -277,12 +292,15 @@ class SparseGPTModifier:
     with its layer's sparsity (``sgpt_base.py:103-172``).  ``mask_structure``
     is ``"N:M"`` (``"0:0"``: unstructured).  OWL layer sparsities
     (``sparsity_profile="owl"``) are not provided by this build.
+    ``share_hessians``: modules fed the same tensor accumulate one Hessian
+    (as ``GPTQModifier``).
     """
 
     def __init__(self, sparsity=None, sparsity_profile: str | None = None, mask_structure: str = "0:0",
                  owl_m: int | None = None, owl_lmbda: float | None = None, targets=("Linear",), ignore=(),
                  block_size: int = 128, dampening_frac: float | None = 0.01, preserve_sparsity_mask: bool = False,
-                 offload_hessians: bool = False):
+                 offload_hessians: bool = False, share_hessians: bool = True):
+        self._init_sharing(share_hessians)
         if sparsity_profile is not None:
             sparsity_profile = sparsity_profile.lower()
             if sparsity_profile not in ["owl"]:
@@ -338,6 +356,8 @@ class SparseGPTModifier:
         if getattr(self, "_hooks_disabled", False):   # a propagation pass of the sequential pipeline
             return
         inp = args[0]
+        if self.share_hessians and self._shared(module, inp, self._module_names.get):
+            return
         if module not in self._num_samples:
             dev = module.weight.device
             self._hessians[module] = sgpt.make_empty_hessian(module, device="cpu" if self.offload_hessians else dev)
@@ -347,23 +367,27 @@ class SparseGPTModifier:
             H = H.to(module.weight.device)
         H, self._num_samples[module] = sgpt.accumulate_hessian(inp, module, H, self._num_samples[module])
         self._hessians[module] = H.to("cpu") if self.offload_hessians else H
+        if self.share_hessians:
+            self._note_accumulated(module, inp)
 
     def compress_modules(self):
-        for module in list(self._num_samples):
-            name = self._module_names[module]
-            if self.offload_hessians:
-                self._hessians[module] = self._hessians[module].to(module.weight.device)
-            t0 = time.perf_counter()
-            with torch.no_grad():
-                loss, w = sgpt.sparsify_weight(module=module, hessians_dict=self._hessians,
-                                               sparsity=self._module_sparsities[module], prune_n=self._prune_n,
-                                               prune_m=self._prune_m, block_size=self.block_size,
-                                               dampening_frac=self.dampening_frac,
-                                               preserve_sparsity_mask=self.preserve_sparsity_mask)
-                module.weight.data.copy_(w)
-            self.timings[name] = time.perf_counter() - t0
-            logger.info("Sparsified %s using %d samples, loss %.4f", name, self._num_samples[module], loss)
-            del self._num_samples[module]
+        for leader, members in self._take_groups().items():
+            n = self._num_samples[leader]
+            H = self._hessians.pop(leader).to(leader.weight.device)
+            for module in members:
+                name = self._module_names[module]
+                self._hessians[module] = H     # sparsify_weight reads and removes the module's entry
+                t0 = time.perf_counter()
+                with torch.no_grad():
+                    loss, w = sgpt.sparsify_weight(module=module, hessians_dict=self._hessians,
+                                                   sparsity=self._module_sparsities[module], prune_n=self._prune_n,
+                                                   prune_m=self._prune_m, block_size=self.block_size,
+                                                   dampening_frac=self.dampening_frac,
+                                                   preserve_sparsity_mask=self.preserve_sparsity_mask)
+                    module.weight.data.copy_(w)
+                self.timings[name] = time.perf_counter() - t0
+                logger.info("Sparsified %s using %d samples, loss %.4f", name, n, loss)
+                del self._num_samples[module]
 
     def on_sequential_epoch_end(self):
         self.compress_modules()

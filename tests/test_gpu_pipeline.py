@@ -139,6 +139,16 @@ def test_sparsegpt_through_the_pipeline(dev):
         assert torch.all(z >= 2), name
 
 
+def test_sparsegpt_shared_hessians_change_nothing(dev):
+    say("SparseGPT: shared Hessians vs separate, through the pipeline")
+    model, batches = _setup(dev)
+    ref = copy.deepcopy(model)
+    sequential_calibrate(ref, ref.layers, batches,
+                         SparseGPTModifier(sparsity=0.5, targets=["Linear"], share_hessians=False))
+    sequential_calibrate(model, model.layers, batches, SparseGPTModifier(sparsity=0.5, targets=["Linear"]))
+    _assert_same(_weights(model), _weights(ref))
+
+
 def test_shared_hessians_change_nothing(dev):
     """gate and up read the same tensor: one Hessian and one Cholesky chain
     for both give exactly the weights of separate ones."""
