@@ -110,17 +110,20 @@ class _SharedHessians:
     """Modules fed the very same input tensor (q/k/v, gate/up) accumulate one
     Hessian: the reference computes the same matrix once per module, with the
     same result.  A group is formed in the first batch (a module joins the
-    module that has just accumulated that tensor as its only input) and must
-    see one tensor per forward afterwards; otherwise an error asks for
-    share_hessians=False.  The last accumulated input of each group is kept
-    alive, so its address cannot be reused by another tensor."""
+    module that has just accumulated that tensor as its only input); in every
+    later forward each member must see the tensor its group's first module
+    accumulated, or an error asks for share_hessians=False.  References kept
+    to inputs (so their addresses cannot be reused while compared): the last
+    accumulated input, and a group's current input until all its members
+    have seen it."""
 
     def _init_sharing(self, share: bool):
         self.share_hessians = share
         self._leader: dict = {}     # member module -> the module whose Hessian it shares
+        self._members: dict = {}    # accumulating module -> number of members
         self._calls: dict = {}      # accumulating module -> inputs accumulated
-        self._held: dict = {}       # accumulating module -> its last input
-        self._last = None           # module of the last accumulation
+        self._pending: dict = {}    # accumulating module -> [its input, members still to see it]
+        self._last = None           # (module, input) of the last accumulation
 
     @staticmethod
     def _same_tensor(a, b) -> bool:
@@ -128,28 +131,39 @@ class _SharedHessians:
                                              and a.stride() == b.stride() and a.dtype == b.dtype
                                              and a._version == b._version))
 
+    def _diverged(self, module, leader, name):
+        raise RuntimeError(f"{type(self).__name__}: {name(module)} shared its input with {name(leader)} in the "
+                           "first calibration batch but not in a later one; pass share_hessians=False")
+
     def _shared(self, module, inp, name) -> bool:
         """True when ``module``'s Hessian is a group's that already holds ``inp``."""
         leader = self._leader.get(module)
         if leader is not None:
-            if not self._same_tensor(inp, self._held.get(leader)):
-                raise RuntimeError(f"{type(self).__name__}: {name(module)} shared its input with {name(leader)} "
-                                   "in the first calibration batch but not in a later one; pass "
-                                   "share_hessians=False")
+            pend = self._pending.get(leader)
+            if pend is None or not self._same_tensor(inp, pend[0]):
+                self._diverged(module, leader, name)
+            pend[1] -= 1
+            if pend[1] == 0:
+                del self._pending[leader]
             return True
         if module in self._num_samples or self._last is None:
             return False
-        cand = self._last
-        if self._calls.get(cand) == 1 and self._same_tensor(inp, self._held.get(cand)):
+        cand, held = self._last
+        if self._calls.get(cand) == 1 and self._same_tensor(inp, held):
             self._leader[module] = cand
+            self._members[cand] = self._members.get(cand, 0) + 1
             self._num_samples[module] = None    # read from the leader at compression
             return True
         return False
 
-    def _note_accumulated(self, module, inp):
+    def _note_accumulated(self, module, inp, name):
+        pend = self._pending.get(module)
+        if pend is not None:      # a member did not see the previous input of its group
+            self._diverged(next(m for m, l in self._leader.items() if l is module), module, name)
         self._calls[module] = self._calls.get(module, 0) + 1
-        self._held[module] = inp
-        self._last = module
+        if self._calls[module] > 1 and self._members.get(module):
+            self._pending[module] = [inp, self._members[module]]
+        self._last = (module, inp)
 
     def _take_groups(self) -> dict:
         """{accumulating module: [it and the modules sharing its Hessian]}; resets the bookkeeping."""
@@ -209,7 +223,7 @@ class GPTQModifier(QuantizationModifier, _SharedHessians):
         H, self._num_samples[module] = accumulate_hessian(inp, module, H, self._num_samples[module])
         self._hessians[module] = H.to("cpu") if self.offload_hessians else H
         if self.share_hessians:
-            self._note_accumulated(module, inp)
+            self._note_accumulated(module, inp, self._modules.get)
 
     def on_calibration_start(self, model):
         for m in self._modules:
@@ -368,7 +382,7 @@ class SparseGPTModifier(_SharedHessians):
         H, self._num_samples[module] = sgpt.accumulate_hessian(inp, module, H, self._num_samples[module])
         self._hessians[module] = H.to("cpu") if self.offload_hessians else H
         if self.share_hessians:
-            self._note_accumulated(module, inp)
+            self._note_accumulated(module, inp, self._module_names.get)
 
     def compress_modules(self):
         for leader, members in self._take_groups().items():

@@ -176,6 +176,29 @@ class _TwoReaders(torch.nn.Module):
         return y
 
 
+class _Skipper(torch.nn.Module):
+    """a and b read the same tensor; b is skipped in the second forward."""
+
+    def __init__(self):
+        super().__init__()
+        self.a = torch.nn.Linear(256, 256, bias=False)
+        self.b = torch.nn.Linear(256, 256, bias=False)
+        self.calls = 0
+
+    def forward(self, x):
+        y = self.a(x) if self.calls == 1 else self.a(x) + self.b(x)
+        self.calls += 1
+        return y
+
+
+def test_shared_hessians_member_skipping_a_forward_raises(dev):
+    say("shared Hessians: a member that misses a forward")
+    batches = [workloads.heavy_tailed_activations((2, 64, 256), seed=50 + s).to(dev) for s in range(3)]
+    model = _Skipper().to(dev).to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="share_hessians=False"):
+        _gptq().apply(model, batches)
+
+
 def test_shared_hessians_divergence_raises(dev):
     say("shared Hessians: inputs that stop being shared")
     torch.manual_seed(1)
