@@ -728,6 +728,82 @@ __global__ __launch_bounds__(NT) void int8_per_token_kernel(const uint16_t* x, i
 // thread keeps its CPT chunks of 8 elements in registers, so the row is read
 // once; the max |x| is reduced on the bf16 bit patterns (order-preserving for
 // non-negative values), and each chunk is written as 8 int8 codes (8 bytes).
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+
+// Eight bf16 values (one 16-byte chunk) -> eight int8 codes of x / s:
+// the quotient by reciprocal and one FMA residual correction (Markstein):
+// the refined quotient is exact when x / s is representable and within one
+// fp32 ulp otherwise.  Rounded to bf16 it equals the rounded IEEE quotient:
+// x / s with 8-bit significands is either a bf16 midpoint exactly or at
+// least 2^-17 (relative) away from every midpoint.  Scales below 2^-100
+// (rows of denormal-sized values, refine false) take the IEEE division.
+__device__ __forceinline__ void int8_chunk(const u32x4_t& v, float s, float rs, bool refine, uint32_t w[2]) {
+  w[0] = w[1] = 0u;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t bits = e & 1 ? (v[e >> 1] & 0xffff0000u) : (v[e >> 1] << 16);
+    const float xv = __uint_as_float(bits);
+    float q;
+    if (refine) {
+      const float q0 = xv * rs;
+      q = fmaf(fmaf(-q0, s, xv), rs, q0);
+    } else {
+      q = xv / s;
+    }
+    q = round_to_bf16(q);
+    q = fminf(fmaxf(q, -128.f), 127.f);
+    w[e >> 2] |= ((uint32_t)(int32_t)rintf(q) & 0xffu) << (8 * (e & 3));
+  }
+}
+
+// Per-token scale of one row from its absmax bit pattern: bf16(amax / 127.5),
+// 2^-7 for an all-zero row.
+__device__ __forceinline__ float int8_token_scale(uint32_t am) {
+  float s = round_to_bf16(__uint_as_float(am << 16) / 127.5f);
+  return s == 0.f ? 0.0078125f : s;
+}
+
+// One wave per row (rows of at most 64 CPL 16-byte chunks): every lane keeps
+// CPL chunks in flight, the absmax reduction stays inside the wave, and a
+// workgroup of NT threads finishes NT / 64 rows.
+template <int CPL>
+__global__ __launch_bounds__(NT) void int8_per_token_wave_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                                 int64_t cols, int64_t ldx,
+                                                                 int8_t* __restrict__ codes,
+                                                                 uint16_t* __restrict__ scale_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int nch = (int)(cols / 8);
+  const u32x4_t* row = reinterpret_cast<const u32x4_t*>(x + r * ldx);
+  u32x4_t v[CPL];
+  uint32_t am = 0;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = __builtin_nontemporal_load(row + (c < nch ? c : nch - 1));
+    if (c >= nch) v[i] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) am = max(am, max(v[i][q] & 0x7fffu, (v[i][q] >> 16) & 0x7fffu));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) am = max(am, (uint32_t)__shfl_xor((int)am, o));
+  const float s = int8_token_scale(am);
+  if (lane == 0) scale_out[r] = f32_to_bf16_bits(s);
+  const bool refine = s >= 0x1p-100f;
+  const float rs = __builtin_amdgcn_rcpf(s);
+  uint32_t* out = reinterpret_cast<uint32_t*>(codes + r * cols);
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      uint32_t w[2];
+      int8_chunk(v[i], s, rs, refine, w);
+      __builtin_nontemporal_store(u32x2_t{w[0], w[1]}, reinterpret_cast<u32x2_t*>(out) + c);
+    }
+  }
+}
+
 template <int CPT>
 __global__ __launch_bounds__(NT) void int8_per_token_vec_kernel(const uint16_t* __restrict__ x, int64_t cols,
                                                                 int64_t ldx, int8_t* __restrict__ codes,
@@ -753,15 +829,8 @@ __global__ __launch_bounds__(NT) void int8_per_token_vec_kernel(const uint16_t* 
   am = smx[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) am = max(am, smx[w]);
-  float s = round_to_bf16(__uint_as_float(am << 16) / 127.5f);
-  if (s == 0.f) s = 0.0078125f;
+  const float s = int8_token_scale(am);
   if (threadIdx.x == 0) scale_out[r] = f32_to_bf16_bits(s);
-  // x / s by reciprocal and one FMA residual correction (Markstein): the
-  // refined quotient is exact when x / s is representable and within one
-  // fp32 ulp otherwise.  Rounded to bf16 it equals the rounded IEEE quotient:
-  // x / s with 8-bit significands is either a bf16 midpoint exactly or at
-  // least 2^-17 (relative) away from every midpoint.  Scales below 2^-100
-  // (rows of denormal-sized values) take the IEEE division.
   const bool refine = s >= 0x1p-100f;
   const float rs = __builtin_amdgcn_rcpf(s);
   uint32_t* out = reinterpret_cast<uint32_t*>(codes + r * cols);
@@ -769,24 +838,9 @@ __global__ __launch_bounds__(NT) void int8_per_token_vec_kernel(const uint16_t* 
   for (int i = 0; i < CPT; ++i) {
     const int c = threadIdx.x + i * NT;
     if (c < nch) {
-      uint32_t w[2] = {0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t bits = e & 1 ? (v[i][e >> 1] & 0xffff0000u) : (v[i][e >> 1] << 16);
-        const float xv = __uint_as_float(bits);
-        float q;
-        if (refine) {
-          const float q0 = xv * rs;
-          q = fmaf(fmaf(-q0, s, xv), rs, q0);
-        } else {
-          q = xv / s;
-        }
-        q = round_to_bf16(q);
-        q = fminf(fmaxf(q, -128.f), 127.f);
-        w[e >> 2] |= ((uint32_t)(int32_t)rintf(q) & 0xffu) << (8 * (e & 3));
-      }
-      __builtin_nontemporal_store(w[0], out + 2 * c);
-      __builtin_nontemporal_store(w[1], out + 2 * c + 1);
+      uint32_t w[2];
+      int8_chunk(v[i], s, rs, refine, w);
+      __builtin_nontemporal_store(u32x2_t{w[0], w[1]}, reinterpret_cast<u32x2_t*>(out) + c);
     }
   }
 }
@@ -1157,7 +1211,14 @@ extern "C" int mi355q_quantize_int8_per_token(const void* x_dev, int64_t rows, i
   const int64_t nch = cols / 8;
   const bool vec = cols % 8 == 0 && ldx % 8 == 0 && aligned16(x_dev) &&
                    (reinterpret_cast<uintptr_t>(codes_dev) & 7) == 0;
-  if (vec && nch <= NT)
+  const unsigned wave_grid = (unsigned)((rows + NT / 64 - 1) / (NT / 64));
+  if (vec && nch <= 64 * 4)
+    hipLaunchKernelGGL(int8_per_token_wave_kernel<4>, dim3(wave_grid), dim3(NT), 0, st, x, rows, cols, ldx,
+                       codes_dev, scale_out_dev);
+  else if (vec && nch <= 64 * 8)
+    hipLaunchKernelGGL(int8_per_token_wave_kernel<8>, dim3(wave_grid), dim3(NT), 0, st, x, rows, cols, ldx,
+                       codes_dev, scale_out_dev);
+  else if (vec && nch <= NT)
     hipLaunchKernelGGL(int8_per_token_vec_kernel<1>, dim3((unsigned)rows), dim3(NT), 0, st, x, cols, ldx, codes_dev,
                        scale_out_dev);
   else if (vec && nch <= 2 * NT)
