@@ -4,7 +4,7 @@ Replaces the compress-and-write half of ``modify_save_pretrained``
 (``transformers/compression/compressed_tensors_utils.py:127-228``: the
 compressor's ``compress_model`` and ``update_config``) for the formats the
 calibration path produces, with this package's kernels doing the quantize and
-pack, and the in-repo int4 shard rewriter ``utils/pack_int4_to_int8.py:31-212``
+pack, and the int4 shard rewriter of ``utils/pack_int4_to_int8.py:31-212``
 (``QuantConfigParser``, ``Int8Packer``, its command line).
 
 Format of a module (``infer_quantization_format``), as
@@ -32,7 +32,6 @@ from __future__ import annotations
 import argparse
 import json
 import os
-import re
 import shutil
 
 import torch
@@ -200,139 +199,128 @@ def save_compressed(model: torch.nn.Module, save_directory: str, quantization_fo
 
 
 # ---------------------------------------------------------------- int4 shard rewriter
+# Interface kept from utils/pack_int4_to_int8.py:69-212 (class and method
+# names, constructor arguments, the command-line flags and the ValueError
+# conditions its tests pin); the selection reuses the recipe target matcher
+# and the rewrite streams one shard at a time with the nibble pack on the GPU.
+
+def _int4_int_weights(weights) -> bool:
+    """A config group's weight arguments describe 4-bit integers (type int by
+    default, num_bits given as anything int() accepts)."""
+    if not isinstance(weights, dict):
+        return False
+    try:
+        bits = int(weights["num_bits"])
+    except (KeyError, TypeError, ValueError):
+        return False
+    return bits == 4 and str(weights.get("type", "int")).lower() == "int"
+
+
+def _target_list(targets) -> list[str]:
+    if isinstance(targets, str):
+        return [targets]
+    return [t for t in targets if isinstance(t, str)] if isinstance(targets, list) else []
+
+
 class QuantConfigParser:
-    """Which int8 weights of a checkpoint hold int4 codes, from its
-    ``config.json`` ``quantization_config`` (``pack_int4_to_int8.py:74-141``)."""
+    """Which tensors of a checkpoint hold int4 codes one per int8, from the
+    ``quantization_config`` of its ``config.json``: the targets of every
+    config group with 4-bit integer weights, matched like recipe targets
+    against the tensor's module name (``re:`` patterns also against the
+    tensor name).  A checkpoint records no module classes; its quantized
+    2-D weights come from Linear layers, so a ``Linear`` target takes them
+    all."""
 
     def __init__(self, model_path) -> None:
-        config_path = os.path.join(model_path, "config.json")
-        if not os.path.exists(config_path):
+        path = os.path.join(model_path, "config.json")
+        if not os.path.exists(path):
             raise ValueError("config.json not found in model path")
-        with open(config_path, "r") as f:
-            self.config = json.load(f).get("quantization_config", {})
-            if not self.config:
-                raise ValueError("quantization_config not found in config.json")
+        with open(path) as f:
+            qc = json.load(f).get(QUANTIZATION_CONFIG_NAME) or {}
+        if not qc:
+            raise ValueError("quantization_config not found in config.json")
+        self.config = qc
+        groups = qc.get("config_groups") or {}
+        self.int4_targets = [t for g in groups.values()
+                             if isinstance(g, dict) and _int4_int_weights(g.get("weights"))
+                             for t in _target_list(g.get("targets", []))]
 
-    @staticmethod
-    def _as_module_name(layer_name):
-        return layer_name[: -len(".weight")] if layer_name.endswith(".weight") else layer_name
+    def is_int4_layer(self, layer_name) -> bool:
+        from .modifiers import matches_target
 
-    @staticmethod
-    def _int4_condition(weights_scheme):
-        if not isinstance(weights_scheme, dict):
-            return False
-        num_bits_value = weights_scheme.get("num_bits")
-        if num_bits_value is None:
-            return False
-        try:
-            num_bits = int(num_bits_value)
-        except (TypeError, ValueError):
-            return False
-        return num_bits == 4 and str(weights_scheme.get("type", "int")).lower() == "int"
-
-    def is_int4_layer(self, layer_name):
-        module_name = self._as_module_name(layer_name)
-        for group in self.config.get("config_groups", {}).values():
-            if not isinstance(group, dict) or not self._int4_condition(group.get("weights", {})):
-                continue
-            targets = group.get("targets", [])
-            if isinstance(targets, str):
-                targets = [targets]
-            if not isinstance(targets, list):
-                continue
-            for target in targets:
-                if not isinstance(target, str):
-                    continue
-                if target == "Linear":   # the broad recipe target matches linear weights
-                    return True
-                if target.startswith("re:"):
-                    if re.match(target[3:], module_name) or re.match(target[3:], layer_name):
-                        return True
-                elif target in (module_name, layer_name):
-                    return True
-        return False
+        module = layer_name.removesuffix(".weight")
+        return (matches_target(module, "Linear", self.int4_targets)
+                or matches_target(layer_name, None, self.int4_targets))
 
 
 class Int8Packer:
-    """Rewrites a checkpoint whose int4 layers hold one code per int8 into two
-    codes per int8 (``pack_int4_to_int8.py:144-200``); the packing runs on the
-    GPU (``mi355q_pack_int4_int8``), shard by shard."""
+    """Rewrites a safetensors checkpoint whose int4 layers hold one code per
+    int8 into two codes per int8 (even column in the low nibble,
+    ``mi355q_pack_int4_int8``), shard by shard; optionally widens biases to
+    fp32 and renames packed weights to ``*.weight_packed``.  The index, if
+    any, gets the new weight map and total size; every other file is copied."""
 
     def __init__(self, model_path, save_path, bias32=False, rename=False, device="cuda"):
-        self.bias32, self.rename, self.device = bias32, rename, device
-        self.model_path, self.save_path = model_path, save_path
-        if not os.path.exists(self.model_path) or not os.path.isdir(self.model_path):
+        if not os.path.isdir(model_path):
             raise ValueError("Invalid model path")
-        os.makedirs(self.save_path, exist_ok=True)
+        self.model_path, self.save_path = model_path, save_path
+        self.bias32, self.rename, self.device = bias32, rename, device
+        os.makedirs(save_path, exist_ok=True)
         self.quant_config_parser = QuantConfigParser(model_path)
-        self.model_tensors = sorted(f for f in os.listdir(self.model_path) if f.endswith(".safetensors"))
-        if not self.model_tensors:
+        self.shards = sorted(n for n in os.listdir(model_path) if n.endswith(".safetensors"))
+        if not self.shards:
             raise ValueError("No .safetensors files found in model path")
 
-    def _process(self, tensor_name):
-        from safetensors import safe_open
-        from safetensors.torch import save_file
+    def _packable(self, key: str, t: torch.Tensor) -> bool:
+        return (key.endswith("weight") and t.dtype == torch.int8 and t.dim() == 2
+                and self.quant_config_parser.is_int4_layer(key))
 
-        index, packed, total = {}, {}, 0
-        with safe_open(os.path.join(self.model_path, tensor_name), framework="pt") as f:
-            for key in f.keys():
-                t = f.get_tensor(key)
-                if not key.endswith("weight") or t.dtype != torch.int8 or t.ndim != 2:
-                    packed[key] = t.to(torch.float32) if key.endswith("bias") and self.bias32 else t
-                    index[key] = tensor_name
-                    continue
-                if self.quant_config_parser.is_int4_layer(key):
-                    if t.shape[1] % 2:
-                        raise ValueError(
-                            f"Expected even number of columns for int4 packing, but got shape {t.shape}")
-                    new_key = f"{key[:-len('weight')]}weight_packed" if self.rename else key
-                    packed[new_key] = ops.pack_int4_int8(t.to(self.device)).cpu()
-                    index[new_key] = tensor_name
-                else:
-                    packed[key] = t
-                    index[key] = tensor_name
-        for t in packed.values():
-            total += t.numel() * t.element_size()
-        save_file(packed, os.path.join(self.save_path, tensor_name))
-        return index, total
+    def _rewrite_shard(self, shard: str) -> tuple[dict, int]:
+        from safetensors.torch import load_file, save_file
 
-    def save(self):
-        final_map, final_size = {}, 0
-        for name in self.model_tensors:
-            m, n = self._process(name)
-            final_map.update(m)
-            final_size += n
-        org = os.path.join(self.model_path, "model.safetensors.index.json")
-        if os.path.exists(org):
-            with open(org, "r") as f:
+        tensors = load_file(os.path.join(self.model_path, shard))
+        out = {}
+        for key, t in tensors.items():
+            if self._packable(key, t):
+                key = key.removesuffix("weight") + "weight_packed" if self.rename else key
+                t = ops.pack_int4_int8(t.to(self.device)).cpu()    # odd widths raise ValueError
+            elif self.bias32 and key.endswith("bias"):
+                t = t.to(torch.float32)
+            out[key] = t
+        save_file(out, os.path.join(self.save_path, shard))
+        return dict.fromkeys(out, shard), sum(t.numel() * t.element_size() for t in out.values())
+
+    def save(self) -> None:
+        weight_map, size = {}, 0
+        for shard in self.shards:
+            m, n = self._rewrite_shard(shard)
+            weight_map.update(m)
+            size += n
+        index = "model.safetensors.index.json"
+        if os.path.exists(os.path.join(self.model_path, index)):
+            with open(os.path.join(self.model_path, index)) as f:
                 idx = json.load(f)
-            idx["weight_map"] = final_map
-            meta = idx.get("metadata", {})
-            if not isinstance(meta, dict):
-                meta = {}
-            meta["total_size"] = final_size
-            idx["metadata"] = meta
-            with open(os.path.join(self.save_path, "model.safetensors.index.json"), "w") as f:
-                json.dump(idx, f, sort_keys=True, indent=2)
-        for file in os.listdir(self.model_path):
-            if file.endswith(".safetensors") or file == "model.safetensors.index.json":
-                continue
-            src = os.path.join(self.model_path, file)
-            if os.path.isfile(src):
-                shutil.copy(src, os.path.join(self.save_path, file))
+            meta = idx.get("metadata") if isinstance(idx.get("metadata"), dict) else {}
+            idx.update(weight_map=weight_map, metadata={**meta, "total_size": size})
+            with open(os.path.join(self.save_path, index), "w") as f:
+                json.dump(idx, f, indent=2, sort_keys=True)
+        for name in os.listdir(self.model_path):
+            src = os.path.join(self.model_path, name)
+            if os.path.isfile(src) and not name.endswith(".safetensors") and name != index:
+                shutil.copy(src, os.path.join(self.save_path, name))
 
 
 def main(argv=None):
-    """``python -m llmcompressor_amd.save -i <model> -o <out> [-bias32] [-rename_packed]``
-    (the reference's ``python -m llmcompressor.utils.pack_int4_to_int8``)."""
-    parser = argparse.ArgumentParser()
-    parser.add_argument("-i", "--model_path", type=str, required=True)
-    parser.add_argument("-o", "--save_path", type=str, required=True)
-    parser.add_argument("-bias32", action="store_true", default=False)
-    parser.add_argument("-rename_packed", action="store_true", default=False,
-                        help="Whether to rename packed int8 weight keys to *weight_packed*")
-    args = parser.parse_args(argv)
-    Int8Packer(args.model_path, args.save_path, args.bias32, args.rename_packed).save()
+    """Command line of the rewriter, with the reference's flags:
+    ``python -m llmcompressor_amd.save -i <checkpoint> -o <out> [-bias32] [-rename_packed]``."""
+    ap = argparse.ArgumentParser(description="pack int4-in-int8 checkpoint weights two codes per byte (GPU)")
+    ap.add_argument("-i", "--model_path", type=str, required=True, help="checkpoint directory to read")
+    ap.add_argument("-o", "--save_path", type=str, required=True, help="directory to write")
+    ap.add_argument("-bias32", action="store_true", default=False, help="store biases as fp32")
+    ap.add_argument("-rename_packed", action="store_true", default=False,
+                    help="store packed weights as <module>.weight_packed")
+    a = ap.parse_args(argv)
+    Int8Packer(a.model_path, a.save_path, a.bias32, a.rename_packed).save()
 
 
 if __name__ == "__main__":

@@ -177,24 +177,25 @@ class _TwoReaders(torch.nn.Module):
 
 
 class _Skipper(torch.nn.Module):
-    """a and b read the same tensor; b is skipped in the second forward."""
+    """a and b read the same tensor; b is skipped in forward number `skip`."""
 
-    def __init__(self):
+    def __init__(self, skip):
         super().__init__()
         self.a = torch.nn.Linear(256, 256, bias=False)
         self.b = torch.nn.Linear(256, 256, bias=False)
-        self.calls = 0
+        self.calls, self.skip = 0, skip
 
     def forward(self, x):
-        y = self.a(x) if self.calls == 1 else self.a(x) + self.b(x)
+        y = self.a(x) if self.calls == self.skip else self.a(x) + self.b(x)
         self.calls += 1
         return y
 
 
-def test_shared_hessians_member_skipping_a_forward_raises(dev):
-    say("shared Hessians: a member that misses a forward")
+@pytest.mark.parametrize("skip", [1, 2], ids=["middle", "last"])
+def test_shared_hessians_member_skipping_a_forward_raises(dev, skip):
+    say(f"shared Hessians: a member that misses forward {skip} of 3")
     batches = [workloads.heavy_tailed_activations((2, 64, 256), seed=50 + s).to(dev) for s in range(3)]
-    model = _Skipper().to(dev).to(torch.bfloat16)
+    model = _Skipper(skip).to(dev).to(torch.bfloat16)
     with pytest.raises(RuntimeError, match="share_hessians=False"):
         _gptq().apply(model, batches)
 

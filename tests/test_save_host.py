@@ -86,3 +86,14 @@ def test_packer_validation(tmp_path):
     _write_config(tmp_path, {"format": "pack-quantized"})
     with pytest.raises(ValueError, match="No .safetensors"):
         Int8Packer(str(tmp_path), str(tmp_path / "out"))
+
+
+def test_quant_config_parser_reference_fixtures(tmp_path):
+    """The reference's parser cases (test_pack_int4_to_int8.py:47-86), from the golden fixture."""
+    from pathlib import Path
+    gold = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+    for case in gold["quant_config_parser"]["cases"]:
+        _write_config(tmp_path, case["quantization_config"])
+        p = QuantConfigParser(str(tmp_path))
+        assert all(p.is_int4_layer(n) for n in case["int4"])
+        assert not any(p.is_int4_layer(n) for n in case["not_int4"])
