@@ -104,7 +104,7 @@ def main():
         obs(lin.weight)
         res = gptq.gptq_quantize(lin.weight, qa, H, obs, num_samples=float(BATCHES))
         if ev: ev[2].record(stream)
-        return res
+        return res, H
 
     for _ in range(a.warmup):
         step()
@@ -113,7 +113,7 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
-        res = step(evs[i])
+        res, H_last = step(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / a.steps
@@ -193,9 +193,9 @@ def main():
     if tf.exists():
         traffic = json.loads(tf.read_text()).get("bytes_per_launch")
 
-    cpu = None
+    cpu = parity = None
     if not a.no_cpu_baseline:
-        cpu = cpu_baseline(torch, w.cpu(), x[:4].cpu())
+        cpu, parity = cpu_baseline(torch, w.cpu(), x[:4].cpu(), H_last.cpu(), res)
 
     line = {
         "metric": "GPTQ ms/layer (W4A16 g128, 4096x4096, Hessian over 64x2048 tokens + solve)",
@@ -223,15 +223,38 @@ def main():
                      "kernel": "syrk_stream_kernel + syrk_stream_reduce_kernel (the Hessian call of each timed step, "
                                "131072 tokens)"},
         "cpu_baseline": cpu,
+        "parity": parity,
     }
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(torch, w_cpu, x_sample):
+def _host_info(torch):
+    """CPU model (lscpu) and the BLAS / LAPACK backends torch was built with."""
+    import re
+    import subprocess
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        m = re.search(r"Model name:\s*(.+)", out)
+        model = m.group(1).strip() if m else None
+    except (OSError, subprocess.SubprocessError):
+        pass
+    cfg = torch.__config__.show()
+    blas = re.search(r"BLAS_INFO=(\w+)", cfg)
+    lapack = re.search(r"LAPACK_INFO=(\w+)", cfg)
+    return {"cpu_model": model, "blas": blas.group(1) if blas else None,
+            "lapack": lapack.group(1) if lapack else None}
+
+
+def cpu_baseline(torch, w_cpu, x_sample, h_gpu, res):
     """The oracle (torch-CPU restatement of the reference) on the host cores.
 
-    Sample: Hessian over 4 x 2048 tokens (scaled to the layer's 64 x 2048)
-    plus one full 4096 x 4096 oracle solve."""
+    Sample: the Hessian over 4 x 2048 tokens (scaled to the layer's 64 x 2048)
+    plus one full 4096 x 4096 oracle solve.  The solve runs on the GPU's own
+    Hessian of the timed step (upper triangle mirrored, / num_samples), so its
+    integer codes compare with the GPU's: code agreement, the largest code
+    difference, and the layer output error ||X (W - Q)|| of both on 2048 of
+    the tokens."""
     from oracle import gptq as og
     from oracle.qargs import OArgs
 
@@ -241,13 +264,29 @@ def cpu_baseline(torch, w_cpu, x_sample):
     H, n = og.accumulate_hessian(x_sample, og.make_empty_hessian(COLS), torch.zeros(()))
     t_h = time.perf_counter() - t0
     scale = (BATCHES * SEQ) / (x_sample.shape[0] * x_sample.shape[1])
+    Hf = torch.triu(h_gpu) + torch.triu(h_gpu, 1).t()
     t0 = time.perf_counter()
-    og.quantize_weight(w_cpu, OArgs(num_bits=4, strategy="group", group_size=GROUP), og.normalise_hessian(H, n))
+    _, out_o, ex = og.quantize_weight(w_cpu, OArgs(num_bits=4, strategy="group", group_size=GROUP),
+                                      Hf / float(BATCHES), return_codes=True)
     t_s = time.perf_counter() - t0
-    return {"value": round((t_h * scale + t_s) * 1e3, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
-            "sample": f"Hessian over {x_sample.shape[0]}x{x_sample.shape[1]} tokens x{scale:g} + one full "
-                      f"{ROWS}x{COLS} GPTQ solve (oracle, torch-CPU MKL)",
-            "hessian_ms_scaled": round(t_h * scale * 1e3, 1), "solve_ms": round(t_s * 1e3, 1)}
+    cpu = {"value": round((t_h * scale + t_s) * 1e3, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
+           "sample": f"Hessian over {x_sample.shape[0]}x{x_sample.shape[1]} tokens x{scale:g} + one full "
+                     f"{ROWS}x{COLS} GPTQ solve (oracle, torch-CPU) on the GPU's Hessian",
+           "hessian_ms_scaled": round(t_h * scale * 1e3, 1), "solve_ms": round(t_s * 1e3, 1), **_host_info(torch)}
+    a, b = res.codes.cpu().to(torch.int32), ex["codes"]
+    d = (a - b).abs()
+    nz = d != 0
+    first = torch.where(nz.any(1), d.gather(1, nz.int().argmax(1, keepdim=True))[:, 0], torch.zeros_like(d[:, 0]))
+    xs = x_sample[0].reshape(-1, COLS).float()
+    e_gpu = (xs @ (w_cpu.float() - res.weight.cpu().float()).t()).norm().item()
+    e_ora = (xs @ (w_cpu.float() - out_o["weight"].float()).t()).norm().item()
+    parity = {"vs": "oracle solve on the GPU's Hessian", "code_agreement": round(1.0 - nz.float().mean().item(), 7),
+              "mismatches": int(nz.sum()), "rows_diverged": int(nz.any(1).sum()), "max_code_diff": int(d.max()),
+              "first_divergence_max": int(first.max()), "codes_beyond_1": int((d > 1).sum()),
+              "layer_err_gpu": round(e_gpu, 4), "layer_err_oracle": round(e_ora, 4),
+              "layer_err_ratio": round(e_gpu / e_ora, 6),
+              "scales_equal": bool(torch.equal(res.scale.cpu(), out_o["weight_scale"].reshape(res.scale.shape)))}
+    return cpu, parity
 
 
 # ---------------------------------------------------------------- other workloads

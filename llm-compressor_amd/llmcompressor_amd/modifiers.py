@@ -401,7 +401,7 @@ class SparseGPTModifier(_SharedHessians):
             self._note_accumulated(module, inp, self._module_names.get)
 
     def compress_modules(self):
-        for leader, members in self._take_groups(self._modules.get).items():
+        for leader, members in self._take_groups(self._module_names.get).items():
             n = self._num_samples[leader]
             H = self._hessians.pop(leader).to(leader.weight.device)
             for module in members:

@@ -87,6 +87,14 @@ def symmetrize_upper_(H: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------- GPTQ pieces
+def _row_major_square(H: torch.Tensor) -> torch.Tensor:
+    """H as a row-major fp32 square matrix (rows may be padded): the kernels
+    read H[i][j] at i * ldh + j."""
+    if H.dim() != 2 or H.shape[0] != H.shape[1] or H.dtype != torch.float32:
+        raise ValueError(f"H must be a square fp32 matrix, got {tuple(H.shape)} {H.dtype}")
+    return H if H.stride(1) == 1 and H.stride(0) >= H.shape[1] else H.contiguous()
+
+
 def gptq_hinv(H: torch.Tensor, perm: torch.Tensor | None, num_samples: float, percdamp: float):
     """Upper Cholesky factor of inverse(damped H / num_samples).
 
@@ -94,6 +102,7 @@ def gptq_hinv(H: torch.Tensor, perm: torch.Tensor | None, num_samples: float, pe
     Synchronises once to read the status flag.
     """
     L.require_gpu(H)
+    H = _row_major_square(H)
     d = H.shape[0]
     dev = H.device
     hinv = torch.empty((d, d), dtype=torch.float32, device=dev)
@@ -115,6 +124,7 @@ def gptq_hinv_rtn(H: torch.Tensor, perm: torch.Tensor | None, num_samples: float
     round-to-nearest fallback).  Returns (hinv, dead, status [1] int32 on the
     device, 0 = positive definite)."""
     L.require_gpu(H)
+    H = _row_major_square(H)
     d = H.shape[0]
     dev = H.device
     hinv = torch.empty((d, d), dtype=torch.float32, device=dev)
@@ -152,6 +162,9 @@ def gptq_sweep_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.Tensor, z
     L.require_gpu(w_work, hinv, scale)
     rows, cols = w_work.shape
     dev = w_work.device
+    if hinv.shape != (cols, cols) or hinv.dtype != torch.float32:
+        raise ValueError(f"hinv must be fp32 [{cols}, {cols}], got {tuple(hinv.shape)} {hinv.dtype}")
+    hinv = hinv.contiguous()   # row-major (torch.linalg.cholesky(upper=True) returns a transposed view)
     s = scale.to(torch.float32).contiguous()
     if s.dim() == 1:
         s = s.reshape(-1, 1)
@@ -188,6 +201,10 @@ def gptq_hinv_batched(H: torch.Tensor, perm: torch.Tensor | None, num_samples: t
     hinv = identity on the device, and the third value is the status [B]
     int32 device tensor (0 = positive definite)."""
     L.require_gpu(H)
+    if H.dim() != 3 or H.shape[1] != H.shape[2] or H.dtype != torch.float32:
+        raise ValueError(f"H must be a stack of square fp32 matrices, got {tuple(H.shape)} {H.dtype}")
+    if H.stride(2) != 1 or H.stride(1) < H.shape[2] or H.stride(0) < H.stride(1) * H.shape[1]:
+        H = H.contiguous()
     B, d, _ = H.shape
     dev = H.device
     hinv = torch.empty((B, d, d), dtype=torch.float32, device=dev)
@@ -226,6 +243,10 @@ def gptq_sweep_batched_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.T
     L.require_gpu(w_work, hinv, scale)
     B, rows, cols = w_work.shape
     dev = w_work.device
+    if hinv.shape != (B, cols, cols) or hinv.dtype != torch.float32:
+        raise ValueError(f"hinv must be fp32 [{B}, {cols}, {cols}], got {tuple(hinv.shape)} {hinv.dtype}")
+    if hinv.stride(2) != 1 or hinv.stride(1) != cols:
+        hinv = hinv.contiguous()   # row-major matrices, any batch stride
     s = scale.to(torch.float32).reshape(B, -1, scale.shape[-1] if scale.dim() == 3 else 1).contiguous()
     z = None if zero_point is None else zero_point.to(torch.float32).reshape(s.shape).contiguous()
     gi = None if g_idx is None else g_idx.to(torch.int32).contiguous()

@@ -1,0 +1,116 @@
+"""How far GPTQ integer codes move under fp32 rounding changes that leave the
+algorithm unchanged, measured with the CPU oracle alone (no GPU).
+
+GPTQ feeds each column's rounding error into the later columns of its row,
+so a value that sits within an ulp of a rounding boundary flips by one code
+when any fp32 operation order changes, and the rest of that row then
+diverges; later codes of such a row can differ by more than one.  This
+script quantizes one 4096 x 4096 W4A16-g128 layer (Hessian from 4 x 2048
+heavy-tailed tokens, the shapes of the full-width GPU parity test) with the
+oracle, then again with one of these changes, and reports the code spread:
+
+* ``ref_1_thread``: the oracle itself with torch (MKL) on 1 thread instead
+  of all cores (LAPACK / BLAS blocking and summation order change);
+* ``flip_chain``: the Cholesky chain as chol(J H J) -> L^-1 flipped back
+  (the GPU path's operation order);
+* ``fp64_chain``: the reference's three-call chain in fp64, rounded to fp32;
+* ``ref_order_blocked``: the reference's operation order (cholesky ->
+  cholesky_inverse -> cholesky(upper)) on a right-looking blocked Cholesky
+  with 128-column panels.
+
+Usage: ``python tests/gptq_code_spread.py [seeds...]`` (about a minute per
+seed on 8 cores).
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path[:0] = [str(ROOT), str(ROOT / "llm-compressor_amd")]
+
+from llmcompressor_amd import workloads  # noqa: E402  (CPU generators only)
+from oracle import gptq as og  # noqa: E402
+from oracle.qargs import OArgs  # noqa: E402
+
+
+def _damped(H, p):
+    H = H.clone()
+    i = torch.arange(H.shape[0])
+    H[i, i] += p * torch.mean(torch.diag(H))
+    return H
+
+
+def flip_chain(H, p):
+    J = torch.arange(H.shape[0] - 1, -1, -1)
+    L = torch.linalg.cholesky(_damped(H, p)[J][:, J])
+    return torch.linalg.solve_triangular(L, torch.eye(H.shape[0]), upper=False)[J][:, J], True
+
+
+def fp64_chain(H, p):
+    L = torch.linalg.cholesky(_damped(H.double(), p))
+    return torch.linalg.cholesky(torch.cholesky_inverse(L), upper=True).float(), True
+
+
+def _blocked_cholesky(A, nb=128):
+    A = A.clone()
+    d = A.shape[0]
+    for k in range(0, d, nb):
+        e = min(k + nb, d)
+        A[k:e, k:e] = torch.linalg.cholesky(A[k:e, k:e])
+        if e < d:
+            A[e:, k:e] = torch.linalg.solve_triangular(A[k:e, k:e], A[e:, k:e].t(), upper=False).t()
+            P = A[e:, k:e]
+            A[e:, e:] -= P @ P.t()
+    return torch.tril(A)
+
+
+def ref_order_blocked(H, p):
+    L = _blocked_cholesky(_damped(H, p))
+    Li = torch.linalg.solve_triangular(L, torch.eye(H.shape[0]), upper=False)
+    Hi = Li.t() @ Li
+    Hi = torch.triu(Hi) + torch.triu(Hi, 1).t()
+    return _blocked_cholesky(Hi).t().contiguous(), True
+
+
+def codes(W, H, chain=None):
+    orig = og.cholesky_chain
+    og.cholesky_chain = chain or orig
+    try:
+        return og.quantize_weight(W, OArgs(num_bits=4, strategy="group", group_size=128), H, return_codes=True)[2]["codes"]
+    finally:
+        og.cholesky_chain = orig
+
+
+def spread(a, b):
+    d = (a - b).abs()
+    nz = d != 0
+    return {"mismatches": int(nz.sum()), "rows_diverged": int(nz.any(1).sum()), "max_diff": int(d.max()),
+            "beyond_1": int((d > 1).sum())}
+
+
+def main(seeds):
+    cores = torch.get_num_threads()
+    out = {}
+    for seed in seeds:
+        W = workloads.gptq_weight(4096, 4096, seed=10 * seed)
+        X = workloads.heavy_tailed_activations((4, 2048, 4096), seed=10 * seed + 1)
+        H, n = og.accumulate_hessian(X, og.make_empty_hessian(4096), torch.zeros(()))
+        H = og.normalise_hessian(H, n)
+        base = codes(W, H)
+        torch.set_num_threads(1)
+        row = {"ref_1_thread": spread(codes(W, H), base)}
+        torch.set_num_threads(cores)
+        for name, ch in (("flip_chain", flip_chain), ("fp64_chain", fp64_chain),
+                         ("ref_order_blocked", ref_order_blocked)):
+            row[name] = spread(codes(W, H, ch), base)
+        out[seed] = row
+        print(json.dumps({"seed": seed, **row}), flush=True)
+    return out
+
+
+if __name__ == "__main__":
+    main([int(s) for s in sys.argv[1:]] or [0, 1, 2, 3])
