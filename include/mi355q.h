@@ -37,7 +37,7 @@ typedef enum {
   MI355Q_HIP_ERROR = 4
 } mi355q_status;
 
-typedef enum { MI355Q_BF16 = 0, MI355Q_F32 = 1 } mi355q_dtype;
+typedef enum { MI355Q_BF16 = 0, MI355Q_F32 = 1, MI355Q_F16 = 2 } mi355q_dtype;
 
 /* Quantization strategy, as compressed-tensors QuantizationStrategy. */
 typedef enum {
@@ -80,6 +80,19 @@ int mi355q_hessian_syrk_scaled_bf16(const void* x_dev, int64_t n_tokens, int64_t
                                     float* h_dev, int64_t ldh, float alpha, float beta,
                                     void* workspace_dev, size_t workspace_bytes, void* stream);
 
+/* The same for calibration activations of any floating type the reference
+ * accepts (it casts the input to fp32, modifiers/gptq/gptq_quantize.py:93,
+ * modifiers/pruning/sparsegpt/sgpt_sparsify.py:51): bf16 and fp16 take the
+ * 16-bit MFMA kernels above (products exact in fp32), fp32 an fp32 MFMA
+ * product over the upper tiles (no workspace).  H = beta * H + alpha * X^T X
+ * on the upper triangle, as mi355q_hessian_syrk_scaled_bf16.  x is [n_tokens,
+ * d] row-major (ldx); for the 16-bit types d % 8 == 0, ldx % 8 == 0 and x
+ * 16-byte aligned.  Workspace: mi355q_hessian_syrk_workspace_size. */
+size_t mi355q_hessian_syrk_workspace_size(int64_t n_tokens, int64_t d, mi355q_dtype dtype);
+int mi355q_hessian_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_tokens, int64_t d, int64_t ldx,
+                        float* h_dev, int64_t ldh, float alpha, float beta, void* workspace_dev,
+                        size_t workspace_bytes, void* stream);
+
 /* Grouped (MoE) variant: expert e accumulates the rows
  * x[rows_dev[k]] for k in [offsets_host[e], offsets_host[e+1]) into
  * h_dev + e * h_stride (each d x d, leading dimension d, upper triangle).
@@ -91,6 +104,12 @@ int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, int64_t d,
                                      const int32_t* rows_dev, const int64_t* offsets_host,
                                      int n_experts, float* h_dev, int64_t h_stride, float alpha,
                                      void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/* mi355q_hessian_grouped_syrk_bf16 for bf16 or fp16 hidden states (dtype). */
+int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype, int64_t ldx, int64_t d,
+                                const int32_t* rows_dev, const int64_t* offsets_host, int n_experts,
+                                float* h_dev, int64_t h_stride, float alpha, void* workspace_dev,
+                                size_t workspace_bytes, void* stream);
 
 /* Mirror the upper triangle into the lower one (full symmetric matrix). */
 int mi355q_symmetrize_upper(float* h_dev, int64_t d, int64_t ldh, void* stream);

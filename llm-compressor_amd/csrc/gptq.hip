@@ -313,6 +313,7 @@ extern "C" int mi355q_gptq_load_weight_batched(const void* w_dev, mi355q_dtype w
                                                const int32_t* dead_dev, float* w_work_dev, void* stream) {
   MQ_CHECK_ARG(w_dev && w_work_dev, "gptq_load_weight: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && ldw >= cols && batch > 0, "gptq_load_weight: bad shape");
+  MQ_CHECK_ARG(w_dtype == MI355Q_BF16 || w_dtype == MI355Q_F32, "gptq_load_weight: dtype must be bf16 or fp32");
   MQ_CHECK_ARG(rows <= 65535 && batch <= 65535, "gptq_load_weight: at most 65535 rows and matrices");
   MQ_CHECK_ARG(batch == 1 || stride_w >= rows * ldw, "gptq_load_weight: matrices overlap");
   hipLaunchKernelGGL(load_weight_kernel, grid_rows(rows, cols, batch), dim3(256), 0,
@@ -394,6 +395,7 @@ extern "C" int mi355q_gptq_store_weight_batched(const float* w_work_dev, int64_t
                                                 int8_t* codes_out_dev, void* stream) {
   MQ_CHECK_ARG(w_work_dev && w_out_dev, "gptq_store_weight: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && ld_out >= cols && batch > 0, "gptq_store_weight: bad shape");
+  MQ_CHECK_ARG(out_dtype == MI355Q_BF16 || out_dtype == MI355Q_F32, "gptq_store_weight: dtype must be bf16 or fp32");
   MQ_CHECK_ARG(codes_out_dev != codes_in_dev || !codes_in_dev, "gptq_store_weight: codes must not alias");
   MQ_CHECK_ARG(rows <= 65535 && batch <= 65535, "gptq_store_weight: at most 65535 rows and matrices");
   MQ_CHECK_ARG(batch == 1 || stride_out >= rows * ld_out, "gptq_store_weight: matrices overlap");

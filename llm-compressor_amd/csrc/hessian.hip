@@ -34,6 +34,7 @@
 #include <vector>
 
 #include "common.h"
+#include "linalg.h"
 
 namespace mi355q {
 
@@ -125,6 +126,18 @@ __device__ __forceinline__ unsigned perm_hi(unsigned a, unsigned b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);  // hi16(a) | hi16(b) << 16
 }
 
+// 32 x 32 x 16 MFMA on 16-bit operands: bf16, or fp16 (F16) -- both form
+// exact products in fp32; the operand bits move through the same registers.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+template <bool F16>
+__device__ __forceinline__ f32x16_t mfma16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
 // Load one 8 (tokens) x 8 (features) block into r[8] (4 dwords each): tokens
 // stage0 + lt0 + 0..7 of the matrix, features f..f+7.  Branch-free:
 // out-of-range tokens / features read a clamped in-range address, and the
@@ -196,7 +209,7 @@ struct Cfg {
   static constexpr int TILE = TM * TM;
 };
 
-template <int TM, bool G>
+template <int TM, bool G, bool F16 = false>
 __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkParams p) {
   using C = Cfg<TM>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][C::OPLDS];
@@ -288,7 +301,7 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
       for (int bm = 0; bm < C::NB; ++bm)
 #pragma unroll
         for (int bn = 0; bn < C::NB; ++bn)
-          acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm], fbv[bn], acc[bm][bn], 0, 0, 0);
+          acc[bm][bn] = mfma16<F16>(fa[bm], fbv[bn], acc[bm][bn]);
     }
     if (more) {
 #pragma unroll
@@ -364,6 +377,7 @@ __device__ __forceinline__ bf16x8_t tr_pair(const char* lds, int off0, int off1)
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+template <bool F16 = false>
 __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   constexpr int MB = 4, NBN = 2;  // 32 x 32 MFMA blocks per wave: 128 rows x 64 columns
   using C = Cfg<256>;
@@ -523,7 +537,7 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     for (int x = 0; x < MB; ++x)
 #pragma unroll
       for (int y = 0; y < NBN; ++y)
-        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[x], fb[y], acc[x][y], 0, 0, 0);
+        acc[x][y] = mfma16<F16>(fa[x], fb[y], acc[x][y]);
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -567,7 +581,7 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
 #pragma unroll
     for (int i = 0; i < MB * NBN; ++i) {
       const int x = i / NBN, y = i % NBN;
-      acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[x], fb[y], acc[x][y], 0, 0, 0);
+      acc[x][y] = mfma16<F16>(fa[x], fb[y], acc[x][y]);
       if (i < MB + NBN) read_op(la, lb, kk, i, na, nb);
       if (i < 4) dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
       __builtin_amdgcn_sched_barrier(0);
@@ -824,16 +838,21 @@ DensePlan plan_dense(int64_t n, int64_t d) {
   return pl;
 }
 
-void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
+template <bool F16>
+void launch_syrk_t(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
   const bool g = p.rows != nullptr;
   if (tile_edge(d) == 256) {
-    if (g)             hipLaunchKernelGGL((syrk_bf16_kernel<256, true>), dim3(grid), dim3(NT), 0, st, p);
-    else if (p.S == 1) hipLaunchKernelGGL((syrk_bf16_kernel<256, false>), dim3(grid), dim3(NT), 0, st, p);
-    else               hipLaunchKernelGGL(syrk_stream_kernel, dim3(grid), dim3(SNT), 0, st, p);
+    if (g)             hipLaunchKernelGGL((syrk_bf16_kernel<256, true, F16>), dim3(grid), dim3(NT), 0, st, p);
+    else if (p.S == 1) hipLaunchKernelGGL((syrk_bf16_kernel<256, false, F16>), dim3(grid), dim3(NT), 0, st, p);
+    else               hipLaunchKernelGGL(syrk_stream_kernel<F16>, dim3(grid), dim3(SNT), 0, st, p);
   } else {
-    if (g) hipLaunchKernelGGL((syrk_bf16_kernel<128, true>), dim3(grid), dim3(NT), 0, st, p);
-    else   hipLaunchKernelGGL((syrk_bf16_kernel<128, false>), dim3(grid), dim3(NT), 0, st, p);
+    if (g) hipLaunchKernelGGL((syrk_bf16_kernel<128, true, F16>), dim3(grid), dim3(NT), 0, st, p);
+    else   hipLaunchKernelGGL((syrk_bf16_kernel<128, false, F16>), dim3(grid), dim3(NT), 0, st, p);
   }
+}
+
+void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st, bool f16) {
+  if (f16) launch_syrk_t<true>(p, d, grid, st); else launch_syrk_t<false>(p, d, grid, st);
 }
 
 // reduction of syrk_bf16_kernel partials (2 x 2 fragment order)
@@ -865,9 +884,10 @@ extern "C" size_t mi355q_hessian_workspace_size(int64_t n_tokens, int64_t d) {
   return (size_t)plan_dense(n_tokens, d).slots * tile_floats(d) * sizeof(float);
 }
 
-extern "C" int mi355q_hessian_syrk_scaled_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
-                                               float* h_dev, int64_t ldh, float alpha, float beta,
-                                               void* workspace_dev, size_t workspace_bytes, void* stream) {
+namespace {
+// H = beta H + alpha X^T X (upper) for 16-bit X: bf16, or fp16 (f16)
+int hessian16_impl(const void* x_dev, bool f16, int64_t n_tokens, int64_t d, int64_t ldx, float* h_dev,
+                   int64_t ldh, float alpha, float beta, void* workspace_dev, size_t workspace_bytes, void* stream) {
   MQ_CHECK_ARG(d > 0 && d % 8 == 0, "hessian: d must be a positive multiple of 8 (got %lld)", (long long)d);
   MQ_CHECK_ARG(ldx >= d && ldx % 8 == 0, "hessian: ldx must be >= d and a multiple of 8");
   MQ_CHECK_ARG(ldx <= (int64_t(1) << 24), "hessian: ldx above 2^24 elements is not supported");
@@ -907,7 +927,7 @@ extern "C" int mi355q_hessian_syrk_scaled_bf16(const void* x_dev, int64_t n_toke
   p.items = nullptr;
   p.mats = nullptr;
   p.ws = static_cast<float*>(workspace_dev);
-  launch_syrk(p, d, (unsigned)pl.grid, st);
+  launch_syrk(p, d, (unsigned)pl.grid, st, f16);
   MQ_LAUNCH_CHECK();
   if (S > 1) {
     if (tile_edge(d) == 256)  // the streaming kernel's slots
@@ -918,6 +938,40 @@ extern "C" int mi355q_hessian_syrk_scaled_bf16(const void* x_dev, int64_t n_toke
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;
+}
+}  // namespace
+
+extern "C" int mi355q_hessian_syrk_scaled_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
+                                               float* h_dev, int64_t ldh, float alpha, float beta,
+                                               void* workspace_dev, size_t workspace_bytes, void* stream) {
+  return hessian16_impl(x_dev, false, n_tokens, d, ldx, h_dev, ldh, alpha, beta, workspace_dev, workspace_bytes,
+                        stream);
+}
+
+extern "C" size_t mi355q_hessian_syrk_workspace_size(int64_t n_tokens, int64_t d, mi355q_dtype dtype) {
+  return dtype == MI355Q_F32 ? 0 : mi355q_hessian_workspace_size(n_tokens, d);
+}
+
+extern "C" int mi355q_hessian_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_tokens, int64_t d, int64_t ldx,
+                                   float* h_dev, int64_t ldh, float alpha, float beta, void* workspace_dev,
+                                   size_t workspace_bytes, void* stream) {
+  if (dtype == MI355Q_BF16 || dtype == MI355Q_F16)
+    return hessian16_impl(x_dev, dtype == MI355Q_F16, n_tokens, d, ldx, h_dev, ldh, alpha, beta, workspace_dev,
+                          workspace_bytes, stream);
+  MQ_CHECK_ARG(dtype == MI355Q_F32, "hessian: dtype must be bf16, fp16 or fp32");
+  MQ_CHECK_ARG(d > 0 && ldx >= d && ldh >= d && n_tokens >= 0, "hessian: bad shape");
+  MQ_CHECK_ARG(h_dev != nullptr, "hessian: null H");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (n_tokens == 0) {
+    if (beta != 1.f) {
+      hipLaunchKernelGGL(scale_upper_kernel, dim3((unsigned)((d + 255) / 256), (unsigned)d), dim3(256), 0, st, h_dev,
+                         d, ldh, beta);
+      MQ_LAUNCH_CHECK();
+    }
+    return MI355Q_OK;
+  }
+  MQ_CHECK_ARG(x_dev != nullptr, "hessian: null x");
+  return syrk_f32_upper(static_cast<const float*>(x_dev), n_tokens, d, ldx, h_dev, ldh, alpha, beta, st);
 }
 
 extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int64_t d, int64_t ldx,
@@ -979,6 +1033,15 @@ extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, 
                                                 int n_experts, float* h_dev, int64_t h_stride,
                                                 float alpha, void* workspace_dev,
                                                 size_t workspace_bytes, void* stream) {
+  return mi355q_hessian_grouped_syrk(x_dev, MI355Q_BF16, ldx, d, rows_dev, offsets_host, n_experts, h_dev,
+                                     h_stride, alpha, workspace_dev, workspace_bytes, stream);
+}
+
+extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype, int64_t ldx, int64_t d,
+                                           const int32_t* rows_dev, const int64_t* offsets_host, int n_experts,
+                                           float* h_dev, int64_t h_stride, float alpha, void* workspace_dev,
+                                           size_t workspace_bytes, void* stream) {
+  MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F16, "grouped hessian: dtype must be bf16 or fp16");
   MQ_CHECK_ARG(d > 0 && d % 8 == 0, "grouped hessian: d must be a positive multiple of 8");
   MQ_CHECK_ARG(ldx >= d && ldx % 8 == 0, "grouped hessian: ldx must be >= d and a multiple of 8");
   MQ_CHECK_ARG(n_experts > 0 && offsets_host != nullptr, "grouped hessian: bad expert table");
@@ -1019,7 +1082,7 @@ extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, 
   p.items = reinterpret_cast<const Item*>(ws + g.off_items);
   p.mats = reinterpret_cast<const Matrix*>(ws + g.off_mats);
   p.ws = reinterpret_cast<float*>(ws);
-  launch_syrk(p, d, (unsigned)g.items.size(), st);
+  launch_syrk(p, d, (unsigned)g.items.size(), st, dtype == MI355Q_F16);
   MQ_LAUNCH_CHECK();
   if (!g.reduces.empty()) {
     launch_reduce(p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, Matrix{}, p.mats, d, d,

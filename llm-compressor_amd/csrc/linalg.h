@@ -18,6 +18,8 @@ struct GemmArgs {
   int64_t M, N, K;
   float alpha, beta;  // C = beta * C + alpha * (A op(B)); beta == 0 never reads C
   int lower_only;     // only C elements with row >= col (tiles fully above skipped)
+  int upper_only;     // only C elements with row <= col (tiles fully below skipped)
+  int a_trans;        // A stored as [K x M] row-major (lda); general kernel only
   // triangular operands (general kernel): A lower (A[i][k] = 0 for k > i) or
   // B lower (B[k][j] = 0 for k < j) limits each tile's K range to where the
   // operand can be nonzero
@@ -27,5 +29,11 @@ struct GemmArgs {
 // Launches the batched GEMM (batch = total number of products) on `stream`;
 // returns a status code.
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream);
+
+// H[i][j] = beta * H[i][j] + alpha * sum_t x[t][i] x[t][j] for i <= j, x
+// [n, d] fp32 row-major (ldx): the fp32 MFMA product of the general kernel
+// with A = x transposed, upper tiles only.
+int syrk_f32_upper(const float* x, int64_t n, int64_t d, int64_t ldx, float* h, int64_t ldh, float alpha,
+                   float beta, hipStream_t stream);
 
 }  // namespace mi355q

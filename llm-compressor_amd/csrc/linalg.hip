@@ -39,13 +39,16 @@ constexpr int GBM = 128, GBN = 128, GBK = 32, GNT = 256;
 constexpr int LA = GBK + 1;     // LDS row stride for [m][k] tiles
 constexpr int LBN = GBN + 32;   // LDS row stride for [k][n] tiles
 
-template <bool BT>
+// AT: A is stored transposed, [K x M] row-major (lda): A[m][k] = A_mem[k][m]
+// (the Hessian X^T X of token-major X); it is staged like a non-transposed B.
+template <bool BT, bool AT = false>
 __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
-  __shared__ float lds_a[2][GBM * LA];
+  __shared__ float lds_a[2][AT ? GBK * LBN : GBM * LA];
   __shared__ float lds_b[2][BT ? GBN * LA : GBK * LBN];
 
   const int64_t m0 = (int64_t)blockIdx.y * GBM, n0 = (int64_t)blockIdx.x * GBN;
   if (g.lower_only && m0 + GBM - 1 < n0) return;
+  if (g.upper_only && m0 > n0 + GBN - 1) return;
   const int64_t bz = blockIdx.z;
   const int64_t b1 = g.inner > 0 ? bz % g.inner : bz, b2 = g.inner > 0 ? bz / g.inner : 0;
   const float* A = g.A + b1 * g.strideA + b2 * g.strideA2;
@@ -98,23 +101,25 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
       for (int e = 0; e < 4; ++e) L[row * LA + 4 * quad + e] = keep_if(r[v][e], rok && k0 + 4 * quad + e < g.K);
     }
   };
-  // B tile (not transposed): 32 k x 128 n -> 1024 float4
-  auto load_kn = [&](int64_t k0, f32x4_t* r) {
+  // [k][n] tiles (B not transposed, or A transposed): 32 k x 128 columns
+  // c0.. of P (ld, `cols` columns) -> 1024 float4
+  const bool vec_am = AT && ((reinterpret_cast<uintptr_t>(A) & 15) == 0) && ((g.lda & 3) == 0) && ((g.M & 3) == 0);
+  auto load_kn_of = [&](const float* P, int64_t ld, bool vec, int64_t cols, int64_t c0, int64_t k0, f32x4_t* r) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int idx = v * GNT + tid;
-      const int64_t gk = k0 + (idx >> 5), gn = n0 + 4 * (idx & 31);
+      const int64_t gk = k0 + (idx >> 5), gn = c0 + 4 * (idx & 31);
       const int64_t gkc = gk < g.K ? gk : g.K - 1;
-      if (vec_bn) {
-        const int64_t gnc = gn < g.N ? gn : g.N - 4;
-        r[v] = *reinterpret_cast<const f32x4_t*>(B + gkc * g.ldb + gnc);
+      if (vec) {
+        const int64_t gnc = gn < cols ? gn : cols - 4;
+        r[v] = *reinterpret_cast<const f32x4_t*>(P + gkc * ld + gnc);
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[v][e] = B[gkc * g.ldb + (gn + e < g.N ? gn + e : g.N - 1)];
+        for (int e = 0; e < 4; ++e) r[v][e] = P[gkc * ld + (gn + e < cols ? gn + e : cols - 1)];
       }
     }
   };
-  auto store_kn = [&](float* L, const f32x4_t* r, int64_t k0) {
+  auto store_kn_of = [&](float* L, const f32x4_t* r, int64_t cols, int64_t c0, int64_t k0) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int idx = v * GNT + tid;
@@ -122,9 +127,17 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
       const bool kok = k0 + krow < g.K;
       f32x4_t x;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = keep_if(r[v][e], kok && n0 + 4 * quad + e < g.N);
+      for (int e = 0; e < 4; ++e) x[e] = keep_if(r[v][e], kok && c0 + 4 * quad + e < cols);
       *reinterpret_cast<f32x4_t*>(L + krow * LBN + 4 * quad) = x;
     }
+  };
+  auto load_kn = [&](int64_t k0, f32x4_t* r) { load_kn_of(B, g.ldb, vec_bn, g.N, n0, k0, r); };
+  auto store_kn = [&](float* L, const f32x4_t* r, int64_t k0) { store_kn_of(L, r, g.N, n0, k0); };
+  auto load_a = [&](int64_t k0, f32x4_t* r) {
+    if (AT) load_kn_of(A, g.lda, vec_am, g.M, m0, k0, r); else load_mk(A, g.lda, vec_a, g.M, m0, k0, r);
+  };
+  auto store_a = [&](float* L, const f32x4_t* r, int64_t k0) {
+    if (AT) store_kn_of(L, r, g.M, m0, k0); else store_mk(L, r, g.M, m0, k0);
   };
 
   // K range of this tile: all of K, or where a triangular operand can be nonzero
@@ -132,9 +145,9 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
   const int64_t kend = g.a_lower ? (m0 + GBM < g.K ? m0 + GBM : g.K) : g.K;
   const int64_t nst = kend > kbeg ? (kend - kbeg + GBK - 1) / GBK : 0;
   if (nst > 0) {
-    load_mk(A, g.lda, vec_a, g.M, m0, kbeg, ra);
+    load_a(kbeg, ra);
     if (BT) load_mk(B, g.ldb, vec_bk, g.N, n0, kbeg, rb); else load_kn(kbeg, rb);
-    store_mk(lds_a[0], ra, g.M, m0, kbeg);
+    store_a(lds_a[0], ra, kbeg);
     if (BT) store_mk(lds_b[0], rb, g.N, n0, kbeg); else store_kn(lds_b[0], rb, kbeg);
   }
   __syncthreads();
@@ -143,7 +156,7 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
     const bool more = st + 1 < nst;
     const int64_t kn = kbeg + (st + 1) * GBK;
     if (more) {
-      load_mk(A, g.lda, vec_a, g.M, m0, kn, ra);
+      load_a(kn, ra);
       if (BT) load_mk(B, g.ldb, vec_bk, g.N, n0, kn, rb); else load_kn(kn, rb);
     }
     const float* la = lds_a[buf];
@@ -153,7 +166,10 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
       const int k = 2 * kk + (lane >> 5);
       float fa[2], fb[2];
 #pragma unroll
-      for (int bm = 0; bm < 2; ++bm) fa[bm] = la[(wm * 64 + bm * 32 + (lane & 31)) * LA + k];
+      for (int bm = 0; bm < 2; ++bm) {
+        const int m = wm * 64 + bm * 32 + (lane & 31);
+        fa[bm] = AT ? la[k * LBN + m] : la[m * LA + k];
+      }
 #pragma unroll
       for (int bn = 0; bn < 2; ++bn) {
         const int n = wn * 64 + bn * 32 + (lane & 31);
@@ -166,7 +182,7 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
           acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[bm], fb[bn], acc[bm][bn], 0, 0, 0);
     }
     if (more) {
-      store_mk(lds_a[buf ^ 1], ra, g.M, m0, kn);
+      store_a(lds_a[buf ^ 1], ra, kn);
       if (BT) store_mk(lds_b[buf ^ 1], rb, g.N, n0, kn); else store_kn(lds_b[buf ^ 1], rb, kn);
     }
     __syncthreads();
@@ -194,7 +210,7 @@ __global__ __launch_bounds__(GNT, 2) void gemm_f32_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) {
         const int64_t gm = m0 + wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int64_t gn = n0 + wn * 64 + bn * 32 + (lane & 31);
-        if (gm < g.M && gn < g.N && (!g.lower_only || gm >= gn)) {
+        if (gm < g.M && gn < g.N && (!g.lower_only || gm >= gn) && (!g.upper_only || gm <= gn)) {
           const float prod = g.alpha * acc[bm][bn][r];
           C[gm * g.ldc + gn] = g.beta == 0.f ? prod : g.beta * cv[(bm * 2 + bn) * 16 + r] + prod;
         }
@@ -995,6 +1011,21 @@ int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream)
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
+  if (g.a_trans || g.upper_only) {   // the general kernel only
+    MQ_CHECK_ARG(batch <= 65535 && !g.a_lower && !g.b_lower && !g.lower_only,
+                 "gemm: transposed-A / upper-only products take no triangular options");
+    dim3 grid((unsigned)((g.N + GBN - 1) / GBN), (unsigned)((g.M + GBM - 1) / GBM), (unsigned)batch);
+    if (!g.a_trans && b_trans)
+      hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, dim3(GNT), 0, stream, g);
+    else if (!g.a_trans)
+      hipLaunchKernelGGL((gemm_f32_kernel<false, false>), grid, dim3(GNT), 0, stream, g);
+    else if (b_trans)
+      hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, dim3(GNT), 0, stream, g);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, dim3(GNT), 0, stream, g);
+    MQ_LAUNCH_CHECK();
+    return MI355Q_OK;
+  }
   // (at most 8 strided-batched library calls: the shorter batch level is looped)
   if (g.K >= 256 && !g.lower_only && g.M < (1ll << 31) && g.N < (1ll << 31) && g.K < (1ll << 31) &&
       (g.inner == 0 || (batch % g.inner == 0 && (g.inner <= 8 || batch / g.inner <= 8))))
@@ -1055,6 +1086,17 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
     hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(GNT), 0, stream, g);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
+}
+
+int syrk_f32_upper(const float* x, int64_t n, int64_t d, int64_t ldx, float* h, int64_t ldh, float alpha,
+                   float beta, hipStream_t stream) {
+  GemmArgs g{};
+  g.A = x; g.lda = ldx; g.a_trans = 1;
+  g.B = x; g.ldb = ldx;
+  g.C = h; g.ldc = ldh;
+  g.M = d; g.N = d; g.K = n;
+  g.alpha = alpha; g.beta = beta; g.upper_only = 1;
+  return gemm_f32(g, false, 1, stream);
 }
 
 }  // namespace mi355q

@@ -921,6 +921,7 @@ extern "C" int mi355q_calculate_qparams(const float* min_dev, const float* max_d
   MQ_CHECK_ARG(min_dev && max_dev && scale_out_dev && zp_out_dev, "calculate_qparams: null pointer");
   MQ_CHECK_ARG(qmin < 0.f && qmax > 0.f, "calculate_qparams: range must straddle zero");
   MQ_CHECK_ARG(!strict || symmetric, "calculate_qparams: strict requires symmetric");
+  MQ_CHECK_ARG(scale_dtype == MI355Q_BF16 || scale_dtype == MI355Q_F32, "calculate_qparams: scale dtype must be bf16 or fp32");
   if (n <= 0) return MI355Q_OK;
   hipLaunchKernelGGL(qparams_kernel, dim3(grid_for(n, NT, 1u << 30)), dim3(NT), 0,
                      reinterpret_cast<hipStream_t>(stream), min_dev, max_dev, n, qmin, qmax, symmetric,
@@ -1110,6 +1111,8 @@ extern "C" int mi355q_quantize_int(const void* x_dev, mi355q_dtype dtype, int64_
                                    mi355q_dtype div_dtype, int8_t* codes_dev, void* stream) {
   MQ_CHECK_ARG(x_dev && scale_dev && codes_dev, "quantize_int: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "quantize_int: bad shape");
+  MQ_CHECK_ARG((dtype == MI355Q_BF16 || dtype == MI355Q_F32) && (div_dtype == MI355Q_BF16 || div_dtype == MI355Q_F32),
+               "quantize_int: dtypes must be bf16 or fp32");
   MQ_CHECK_ARG(num_bits >= 2 && num_bits <= 8, "quantize_int: num_bits must be in [2, 8]");
   MQ_CHECK_ARG(strategy != MI355Q_GROUP || group_size > 0 || g_idx_dev, "quantize_int: group_size");
   MQ_CHECK_ARG(strategy != MI355Q_BLOCK || (block_h > 0 && block_w > 0), "quantize_int: block");
@@ -1191,6 +1194,8 @@ extern "C" int mi355q_quantize_fp8(const void* x_dev, mi355q_dtype dtype, int64_
                                    void* stream) {
   MQ_CHECK_ARG(x_dev && scale_dev && out_dev, "quantize_fp8: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && ldx >= cols, "quantize_fp8: bad shape");
+  MQ_CHECK_ARG((dtype == MI355Q_BF16 || dtype == MI355Q_F32) && (div_dtype == MI355Q_BF16 || div_dtype == MI355Q_F32),
+               "quantize_fp8: dtypes must be bf16 or fp32");
   MQ_CHECK_ARG(strategy == MI355Q_TENSOR || strategy == MI355Q_CHANNEL || strategy == MI355Q_TOKEN ||
                    (strategy == MI355Q_GROUP && group_size > 0),
                "quantize_fp8: unsupported strategy");

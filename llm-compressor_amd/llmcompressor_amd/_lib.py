@@ -13,7 +13,7 @@ import torch
 from ._build import LIB_PATH
 
 OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_POSITIVE_DEFINITE, HIP_ERROR = 0, 1, 2, 3, 4
-BF16, F32 = 0, 1
+BF16, F32, F16 = 0, 1, 2
 TENSOR, CHANNEL, GROUP, BLOCK, TOKEN = 0, 1, 2, 3, 4
 MX_RULE_CT, MX_RULE_OCP = 0, 1
 
@@ -26,7 +26,10 @@ SIGNATURES = {
     "mi355q_hessian_workspace_size": (_sz, [_i64, _i64]),
     "mi355q_hessian_syrk_bf16": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _f32, _vp, _sz, _vp]),
     "mi355q_hessian_syrk_scaled_bf16": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _f32, _f32, _vp, _sz, _vp]),
+    "mi355q_hessian_syrk_workspace_size": (_sz, [_i64, _i64, _i32]),
+    "mi355q_hessian_syrk": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _f32, _f32, _vp, _sz, _vp]),
     "mi355q_hessian_grouped_workspace_size": (_sz, [_vp, _i32, _i64]),
+    "mi355q_hessian_grouped_syrk": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _f32, _vp, _sz, _vp]),
     "mi355q_hessian_grouped_syrk_bf16": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _f32, _vp, _sz, _vp]),
     "mi355q_symmetrize_upper": (_i32, [_vp, _i64, _i64, _vp]),
     "mi355q_gptq_hinv_workspace_size": (_sz, [_i64]),

@@ -28,53 +28,71 @@ def _ws(nbytes: int, device) -> torch.Tensor | None:
 
 
 # ---------------------------------------------------------------- Hessian
+_HESS_DT = {torch.bfloat16: L.BF16, torch.float16: L.F16, torch.float32: L.F32}
+
+
+def _hessian_input(x: torch.Tensor) -> torch.Tensor:
+    """x as a row-major 2-D matrix of a type the Hessian kernels take: bf16 and
+    fp16 as they are (16-byte aligned rows, a multiple of 8 features), any
+    other floating type - and 16-bit inputs whose width is not a multiple
+    of 8 - converted to fp32, as the reference converts every input
+    (gptq_quantize.py:93)."""
+    if not x.dtype.is_floating_point:
+        raise TypeError(f"hessian input must be a floating-point tensor, got {x.dtype}")
+    if x.dim() != 2 or x.stride(1) != 1:
+        x = x.reshape(-1, x.shape[-1]).contiguous()
+    if x.dtype not in _HESS_DT or (x.dtype != torch.float32 and x.shape[1] % 8):
+        x = x.to(torch.float32)
+    if x.dtype != torch.float32 and (x.data_ptr() % 16 or x.stride(0) % 8):
+        x = x.contiguous()
+    return x
+
+
 def hessian_syrk_(H: torch.Tensor, x: torch.Tensor, alpha: float = 2.0, beta: float = 1.0) -> torch.Tensor:
     """H[i, j] = beta * H[i, j] + alpha * sum_t x[t, i] x[t, j] for i <= j, in
     place (beta == 1: H += ...).
 
-    ``x`` is [tokens, d] bf16 (row stride may exceed d); H is fp32 [d, d].
+    ``x`` is [tokens, d] (row stride may exceed d) bf16 or fp16 (16-bit MFMA,
+    exact products) or fp32 (fp32 MFMA); other floating types are converted
+    to fp32.  H is fp32 [d, d].
     """
     L.require_gpu(H, x)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"hessian input must be bf16, got {x.dtype}")
-    if x.dim() != 2 or x.stride(1) != 1:
-        x = x.reshape(-1, x.shape[-1]).contiguous()
-    if x.data_ptr() % 16 or x.stride(0) % 8:
-        x = x.contiguous()
+    x = _hessian_input(x)
     n, d = x.shape
     if H.dtype != torch.float32 or H.shape != (d, d) or H.stride(1) != 1:
         raise ValueError(f"H must be fp32 [{d}, {d}] row-major, got {tuple(H.shape)} {H.dtype}")
     lib = L.lib()
-    ws = _ws(lib.mi355q_hessian_workspace_size(n, d), x.device)
-    if beta == 1.0:
-        L.check(lib.mi355q_hessian_syrk_bf16(x.data_ptr(), n, d, x.stride(0), H.data_ptr(), H.stride(0),
-                                             C.c_float(alpha), L.ptr(ws), 0 if ws is None else ws.numel(),
-                                             L.stream_of(x)))
-    else:
-        L.check(lib.mi355q_hessian_syrk_scaled_bf16(x.data_ptr(), n, d, x.stride(0), H.data_ptr(), H.stride(0),
-                                                    C.c_float(alpha), C.c_float(beta), L.ptr(ws),
-                                                    0 if ws is None else ws.numel(), L.stream_of(x)))
+    dt = _HESS_DT[x.dtype]
+    ws = _ws(lib.mi355q_hessian_syrk_workspace_size(n, d, dt), x.device)
+    L.check(lib.mi355q_hessian_syrk(x.data_ptr(), dt, n, d, x.stride(0), H.data_ptr(), H.stride(0), C.c_float(alpha),
+                                    C.c_float(beta), L.ptr(ws), 0 if ws is None else ws.numel(), L.stream_of(x)))
     return H
 
 
 def hessian_grouped_syrk_(H: torch.Tensor, x: torch.Tensor, rows: torch.Tensor, offsets: list[int],
                           alpha: float = 2.0) -> torch.Tensor:
     """Per-group upper-triangle syrk: H[e] += alpha * X_e^T X_e where X_e are
-    the rows ``x[rows[offsets[e]:offsets[e+1]]]``.  H is [E, d, d] fp32."""
+    the rows ``x[rows[offsets[e]:offsets[e+1]]]``.  H is [E, d, d] fp32.  bf16
+    and fp16 ``x`` take one grouped launch; other types are converted to fp32
+    and each group's gathered rows take the dense fp32 product."""
     L.require_gpu(H, x, rows)
-    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.stride(1) != 1:
-        raise TypeError("grouped hessian input must be a row-major bf16 matrix")
     E = len(offsets) - 1
+    x = _hessian_input(x)
     d = x.shape[1]
     if H.shape != (E, d, d) or H.dtype != torch.float32 or not H.is_contiguous():
         raise ValueError(f"H must be contiguous fp32 [{E}, {d}, {d}]")
+    if x.dtype == torch.float32:
+        for e in range(E):
+            if offsets[e + 1] > offsets[e]:
+                hessian_syrk_(H[e], x[rows[offsets[e]:offsets[e + 1]].long()], alpha=alpha)
+        return H
     rows = rows.to(torch.int32).contiguous()
     off = (C.c_int64 * (E + 1))(*[int(o) for o in offsets])
     lib = L.lib()
     ws = _ws(lib.mi355q_hessian_grouped_workspace_size(off, E, d), x.device)
-    L.check(lib.mi355q_hessian_grouped_syrk_bf16(x.data_ptr(), x.stride(0), d, rows.data_ptr(), off, E,
-                                                 H.data_ptr(), d * d, C.c_float(alpha), L.ptr(ws),
-                                                 0 if ws is None else ws.numel(), L.stream_of(x)))
+    L.check(lib.mi355q_hessian_grouped_syrk(x.data_ptr(), _HESS_DT[x.dtype], x.stride(0), d, rows.data_ptr(), off, E,
+                                            H.data_ptr(), d * d, C.c_float(alpha), L.ptr(ws),
+                                            0 if ws is None else ws.numel(), L.stream_of(x)))
     return H
 
 

@@ -68,6 +68,62 @@ def test_hessian_syrk_parity(dev, n, d):
     assert torch.equal(H2.cpu(), got)  # deterministic
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.float64], ids=["fp16", "fp32", "fp64"])
+@pytest.mark.parametrize("n,d", [(777, 200), (5000, 384), (16384, 1024), (3000, 100)])
+def test_hessian_other_input_dtypes(dev, dtype, n, d):
+    """Calibration activations in fp16 / fp32 / fp64 through the drop-in
+    accumulate_hessian (the reference casts every input to fp32,
+    gptq_quantize.py:93): fp16 on the 16-bit MFMA kernels (exact products),
+    fp32 on the fp32 MFMA product, fp64 converted to fp32 first; d = 100 is
+    not a multiple of 8 (fp16 then also takes the fp32 product)."""
+    say(f"hessian {dtype} n={n} d={d}")
+    g = torch.Generator().manual_seed(n + d)
+    x = (torch.randn(n, d, generator=g) * torch.exp(torch.randn(d, generator=g))).to(dtype)
+    lin = torch.nn.Linear(d, 8, bias=False).to(dev)
+    H, cnt = gptq.make_empty_hessian(lin), torch.zeros((), device=dev)
+    H, cnt = gptq.accumulate_hessian(x.unsqueeze(0).to(dev), lin, H, cnt)
+    H, cnt = gptq.accumulate_hessian(x[: n // 3].unsqueeze(0).to(dev), lin, H, cnt)
+    Ho, no = og.accumulate_hessian(x.unsqueeze(0), og.make_empty_hessian(d), torch.zeros(()))
+    Ho, no = og.accumulate_hessian(x[: n // 3].unsqueeze(0), Ho, no)
+    assert float(cnt) == float(no) == 2.0
+    r = rel_fro(torch.triu(H.cpu()), torch.triu(Ho))
+    assert r <= HESS_TOL, r
+    assert torch.count_nonzero(torch.tril(H, -1)) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
+def test_hessian_grouped_other_dtypes(dev, dtype):
+    say(f"grouped hessian {dtype}")
+    T, d, E = 2000, 256, 5
+    g = torch.Generator().manual_seed(13)
+    hs = (torch.randn(T, d, generator=g) * 3).to(dtype)
+    idx = torch.randint(0, E, (T, 2), generator=g)
+    idx[:, 1] = (idx[:, 0] + 1 + torch.randint(0, E - 1, (T,), generator=g)) % E
+    rows, offsets, _ = moe.route_tokens(idx.to(dev), E)
+    H = torch.zeros(E, d, d, device=dev)
+    ns = torch.zeros(E, device=dev)
+    moe.accumulate_expert_hessians(hs.to(dev), rows, offsets, H, ns)
+    Ho, no = omoe.expert_hessians(hs, idx, E)
+    for e in range(E):
+        assert rel_fro(torch.triu(H[e].cpu()), torch.triu(Ho[e])) <= HESS_TOL, e
+
+
+def test_hessian_running_mean_fp16(dev):
+    """SparseGPT's running-mean Hessian (sgpt_sparsify.py:48-53) on fp16 input."""
+    from llmcompressor_amd import sparsegpt
+    from oracle import sparsegpt as osg
+    say("sparsegpt running-mean hessian fp16")
+    g = torch.Generator().manual_seed(3)
+    xs = [(torch.randn(2, 300, 256, generator=g) * 2).to(torch.float16) for _ in range(3)]
+    lin = torch.nn.Linear(256, 8, bias=False).to(dev)
+    H, n = sparsegpt.make_empty_hessian(lin), 0
+    Ho, no = osg.make_empty_hessian(256), 0
+    for x in xs:
+        H, n = sparsegpt.accumulate_hessian(x.to(dev), lin, H, n)
+        Ho, no = osg.accumulate_hessian(x, Ho, no)
+    assert rel_fro(torch.triu(H.cpu()), torch.triu(Ho)) <= HESS_TOL
+
+
 def test_hessian_syrk_many_tiles(dev):
     """d = 8192 (528 tiles, so at most two token splits): upper triangle
     against an fp64 product on the GPU."""
