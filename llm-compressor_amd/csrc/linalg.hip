@@ -19,10 +19,6 @@
 //   flip:     hinv[a][b] = X[d-1-a][d-1-b] for a <= b, 0 below
 #include "linalg.h"
 
-#include <rocblas/rocblas.h>
-
-#include <mutex>
-
 #pragma clang fp contract(off)
 
 namespace mi355q {
@@ -465,6 +461,250 @@ __global__ __launch_bounds__(GNT, 2) void gemm_k128_small_kernel(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------- large-K GEMM
+// The solve's products with K >= 256 (GPTQ mid- and super-block lazy
+// updates, the Cholesky chain's rank-512 trailing updates, the triangular
+// inverse's doubling products): C = beta C + alpha A op(B) on fp32 MFMA
+// 32x32x2, tiles of TM x TN on WGM x WGN waves, K in stages of 32.
+constexpr int LKK = 32;          // K per stage
+// The same products with the operand tiles streamed global -> LDS by the
+// gfx950 LDS-DMA load (global_load_lds_dwordx4: no registers, no VALU)
+// through a ring of NS stages, so NS - 1 stages of loads are in flight while
+// one is multiplied (one stage ahead, with register staging, does not cover
+// the memory latency when a CU runs a single workgroup).  Each wave DMA instruction fills 1 KB of LDS
+// with 16-byte chunks in lane order; the lanes pick which global chunk lands
+// where, which gives the swizzles:
+//   [row][k] tiles (A, B^T): 128-byte rows (32 floats), the chunk of k-quad c
+//     stored at position c ^ ((row >> 1) & 7), so the 16-byte operand reads of
+//     16 consecutive rows fall on 16 distinct bank quads;
+//   [k][n] tiles (B): TN * 4-byte rows, the chunk of n-quad c stored at
+//     c ^ (8 ((k >> 2) & 1)), so rows k and k + 4 (the two lane halves of one
+//     MFMA) read disjoint banks.
+// Elements past M, N or K (K, and N for [k][n] tiles, multiples of 4) are
+// fetched from a zero chunk.  The K order inside each group of 8 is permuted
+// so that one 16-byte LDS read gives a lane its [row][k] operand for four
+// MFMAs: MFMA s of group q contracts k = 8q + s (lanes 0-31) with
+// k = 8q + 4 + s (lanes 32-63).
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __attribute__((aligned(16))) const float kZeroF4[4] = {0.f, 0.f, 0.f, 0.f};
+
+__device__ __forceinline__ void dma16(const void* gaddr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_addr) : "memory", "m0");
+}
+
+template <int TM, int TN, int WGM, int WGN, bool BT, int NS>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(GemmArgs g) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WTM = TM / WGM, WTN = TN / WGN;      // wave tile
+  constexpr int MB = WTM / 32, NB2 = WTN / 32;
+  constexpr int NACC = MB * NB2 == 1 ? 2 : MB * NB2;
+  constexpr int ABYTES = TM * 128;                    // TM rows x 32 floats
+  constexpr int BBYTES = BT ? TN * 128 : LKK * TN * 4;
+  constexpr int SBYTES = ABYTES + BBYTES;
+  constexpr int DA = ABYTES / 1024 / NW, DB = BBYTES / 1024 / NW;   // DMA instructions per wave and stage
+  static_assert(DA * NW * 1024 == ABYTES && DB * NW * 1024 == BBYTES, "tile / wave split");
+  constexpr int BROW = TN * 4;                        // bytes per [k][n] row
+  constexpr int BRPI = 1024 / BROW;                   // [k][n] rows per DMA instruction
+  constexpr int BCH = TN / 4;                         // 16-byte chunks per [k][n] row
+  __shared__ __attribute__((aligned(1024))) char lds[NS * SBYTES];
+  {
+    const int64_t bz = blockIdx.z;
+    const int64_t b1 = g.inner > 0 ? bz % g.inner : bz, b2 = g.inner > 0 ? bz / g.inner : 0;
+    g.A += b1 * g.strideA + b2 * g.strideA2;
+    g.B += b1 * g.strideB + b2 * g.strideB2;
+    g.C += b1 * g.strideC + b2 * g.strideC2;
+  }
+  // tile of this workgroup (1-D grid over mt x nt tiles).  With a triangular
+  // operand the tiles with the longest K range are dispatched first (tiles
+  // of one n column for a lower B, of one m row from the bottom for a lower
+  // A); otherwise each XCD (workgroups are dispatched round-robin over the
+  // 8) takes a contiguous m-major run of tiles, which share A rows and B
+  // columns in its L2.
+  const int64_t mt = (g.M + TM - 1) / TM, ntl = (g.N + TN - 1) / TN, ntot = mt * ntl;
+  int64_t tm_i, tn_i;
+  {
+    const int64_t b = blockIdx.x;
+    if (g.b_lower) {
+      tn_i = b / mt; tm_i = b % mt;
+    } else if (g.a_lower) {
+      tm_i = mt - 1 - b / ntl; tn_i = b % ntl;
+    } else {
+      // (lower-only products keep the round-robin order: the tiles above the
+      // diagonal exit at once, so contiguous runs would load XCDs unevenly)
+      const int64_t t = ntot % 8 == 0 && !g.lower_only ? (b % 8) * (ntot / 8) + b / 8 : b;
+      tm_i = t / ntl; tn_i = t % ntl;
+    }
+  }
+  const int64_t m0 = tm_i * TM, n0 = tn_i * TN;
+  if (g.lower_only && m0 + TM - 1 < n0) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  const int64_t kbeg = g.b_lower ? (n0 / LKK) * LKK : 0;
+  const int64_t kend = g.a_lower ? (m0 + TM < g.K ? m0 + TM : g.K) : g.K;
+  const int64_t nst = kend > kbeg ? (kend - kbeg + LKK - 1) / LKK : 0;
+
+  // DMA sources of this lane: instruction j of the wave covers [row][k] rows
+  // 8 u .. 8 u + 7 (u = wave DA + j) or [k][n] rows BRPI u ..
+  const float* a_src[DA];
+  int a_ck[DA];
+  bool a_ok[DA];
+#pragma unroll
+  for (int j = 0; j < DA; ++j) {
+    const int r = 8 * (wave * DA + j) + (lane >> 3);
+    a_ck[j] = (lane & 7) ^ ((r >> 1) & 7);
+    a_ok[j] = m0 + r < g.M;
+    a_src[j] = g.A + (a_ok[j] ? m0 + r : 0) * g.lda + 4 * a_ck[j];
+  }
+  const float* b_src[DB];
+  int b_ck[DB], b_kr[DB];
+  bool b_ok[DB];
+#pragma unroll
+  for (int j = 0; j < DB; ++j) {
+    if (BT) {
+      const int r = 8 * (wave * DB + j) + (lane >> 3);
+      b_ck[j] = (lane & 7) ^ ((r >> 1) & 7);
+      b_kr[j] = 0;
+      b_ok[j] = n0 + r < g.N;
+      b_src[j] = g.B + (b_ok[j] ? n0 + r : 0) * g.ldb + 4 * b_ck[j];
+    } else {
+      const int kr = BRPI * (wave * DB + j) + lane / BCH;
+      const int ck = (lane % BCH) ^ (8 * ((kr >> 2) & 1));
+      b_ck[j] = ck;
+      b_kr[j] = kr;
+      b_ok[j] = n0 + 4 * ck < g.N;
+      b_src[j] = g.B + kr * g.ldb + n0 + (b_ok[j] ? 4 * ck : 0);
+    }
+  }
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)lds);
+  // DMA instruction i (A first, then B) of stage `stage` (clamped to the last
+  // one, so every wave issues the same count) into ring slot stage % NS
+  auto issue = [&](int64_t stage, int i) __attribute__((always_inline)) {
+    const int64_t sc = stage < nst ? stage : nst - 1;
+    const int64_t k0 = kbeg + sc * LKK;
+    const uint32_t slot = lds0 + (uint32_t)((stage % NS) * SBYTES);
+    if (i < DA) {
+      const bool ok = a_ok[i] && k0 + 4 * a_ck[i] < g.K;
+      dma16(ok ? (const void*)(a_src[i] + k0) : (const void*)kZeroF4, slot + (uint32_t)((wave * DA + i) * 1024));
+    } else {
+      const int j = i - DA;
+      if (BT) {
+        const bool ok = b_ok[j] && k0 + 4 * b_ck[j] < g.K;
+        dma16(ok ? (const void*)(b_src[j] + k0) : (const void*)kZeroF4,
+              slot + ABYTES + (uint32_t)((wave * DB + j) * 1024));
+      } else {
+        const bool ok = b_ok[j] && k0 + b_kr[j] < g.K;
+        dma16(ok ? (const void*)(b_src[j] + k0 * g.ldb) : (const void*)kZeroF4,
+              slot + ABYTES + (uint32_t)((wave * DB + j) * 1024));
+      }
+    }
+  };
+
+  f32x16_t acc[NACC];
+#pragma unroll
+  for (int a = 0; a < NACC; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[a][r] = 0.f;
+
+  const int half = lane >> 5, l32 = lane & 31;
+  const int xr = (l32 >> 1) & 7;                       // row swizzle of this lane's [row][k] rows
+  const int a_row = (wm * WTM + l32) * 128;            // + bm * 32 * 128
+  const int bt_row = (wn * WTN + l32) * 128;
+  // [k][n] read offset of column block bn (its 8 chunks form an aligned block of 8)
+  int bk_lane[NB2];
+#pragma unroll
+  for (int bn = 0; bn < NB2; ++bn)
+    bk_lane[bn] = 4 * half * BROW + (((wn * WTN + bn * 32 + l32) >> 2) ^ (8 * half)) * 16 + (l32 & 3) * 4;
+  struct Frag { f32x4_t a[MB], b[NB2]; };
+  auto read_group = [&](const char* sl, int q, Frag& f) __attribute__((always_inline)) {
+    const int ch = ((2 * q + half) ^ xr) * 16;
+#pragma unroll
+    for (int bm = 0; bm < MB; ++bm) f.a[bm] = *reinterpret_cast<const f32x4_t*>(sl + a_row + bm * 32 * 128 + ch);
+#pragma unroll
+    for (int bn = 0; bn < NB2; ++bn) {
+      if (BT) {
+        f.b[bn] = *reinterpret_cast<const f32x4_t*>(sl + ABYTES + bt_row + bn * 32 * 128 + ch);
+      } else {
+        // column block bn: 32 columns = 8 chunks, XOR by 8 keeps them a block
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+          f.b[bn][s2] = *reinterpret_cast<const float*>(sl + ABYTES + bk_lane[bn] + (8 * q + s2) * BROW);
+      }
+    }
+  };
+  auto mma_group = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+      for (int bm = 0; bm < MB; ++bm)
+#pragma unroll
+        for (int bn = 0; bn < NB2; ++bn) {
+          const int ai = MB * NB2 == 1 ? (s2 & 1) : bm * NB2 + bn;
+          acc[ai] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[bm][s2], f.b[bn][s2], acc[ai], 0, 0, 0);
+        }
+  };
+
+  constexpr int ND = DA + DB;
+  if (nst > 0) {
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+#pragma unroll
+      for (int i = 0; i < ND; ++i) issue(p, i);
+    for (int64_t st = 0; st < nst; ++st) {
+      // this wave's DMAs of stage st are done (those of the NS - 2 later
+      // stages may be in flight) and its LDS reads of stage st - 1 have
+      // returned; the barrier makes every wave's DMAs visible and frees the
+      // slot of stage st - 1, which takes stage st + NS - 1
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * ND) : "memory");
+      const char* sl = lds + (st % NS) * SBYTES;
+      Frag f0, f1;
+      read_group(sl, 0, f0);
+      read_group(sl, 1, f1);
+#pragma unroll
+      for (int i = 0; i < ND / 2; ++i) issue(st + NS - 1, i);
+      mma_group(f0);
+      read_group(sl, 2, f0);
+      mma_group(f1);
+#pragma unroll
+      for (int i = ND / 2; i < ND; ++i) issue(st + NS - 1, i);
+      read_group(sl, 3, f1);
+      mma_group(f0);
+      mma_group(f1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+
+  constexpr int NBLK = MB * NB2;
+  float cv[NBLK * 16];
+  auto gm_of = [&](int bm, int r) { return m0 + wm * WTM + bm * 32 + 8 * (r >> 2) + 4 * half + (r & 3); };
+  auto gn_of = [&](int bn) { return n0 + wn * WTN + bn * 32 + l32; };
+  if (g.beta != 0.f) {
+#pragma unroll
+    for (int bm = 0; bm < MB; ++bm)
+#pragma unroll
+      for (int bn = 0; bn < NB2; ++bn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t gm = gm_of(bm, r), gn = gn_of(bn);
+          cv[(bm * NB2 + bn) * 16 + r] = g.C[(gm < g.M ? gm : g.M - 1) * g.ldc + (gn < g.N ? gn : g.N - 1)];
+        }
+  }
+#pragma unroll
+  for (int bm = 0; bm < MB; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < NB2; ++bn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gm = gm_of(bm, r), gn = gn_of(bn);
+        if (gm < g.M && gn < g.N && (!g.lower_only || gm >= gn)) {
+          const float sum = NBLK == 1 ? acc[0][r] + acc[1][r] : acc[bm * NB2 + bn][r];
+          const float prod = g.alpha * sum;
+          g.C[gm * g.ldc + gn] = g.beta == 0.f ? prod : g.beta * cv[(bm * NB2 + bn) * 16 + r] + prod;
+        }
+      }
+}
+
 // ---------------------------------------------------------------- Cholesky pieces
 constexpr int NB = 128;        // panel width
 constexpr int SB = 32;         // register-resident sub-block of the diagonal kernel
@@ -897,6 +1137,20 @@ __global__ void fill_kernel(float* p, int64_t n, float v, int64_t wsf) {
   for (; i < n; i += stride) p[i] = v;
 }
 
+// dst[r][c] = src[r][c] for r < rows, c < cols (cols % 4 == 0, 16-byte
+// aligned rows): a strided panel into a compact buffer (matrix blockIdx.y
+// at src + y wsf, dst + y wsf)
+__global__ void copy_panel_kernel(const float* src, int64_t lds_, float* dst, int64_t ldd, int64_t rows,
+                                  int64_t cols, int64_t wsf) {
+  src += (int64_t)blockIdx.y * wsf;
+  dst += (int64_t)blockIdx.y * wsf;
+  const int64_t q = cols / 4, n = rows * q;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / q, c = 4 * (i % q);
+    *reinterpret_cast<f32x4_t*>(dst + r * ldd + c) = *reinterpret_cast<const f32x4_t*>(src + r * lds_ + c);
+  }
+}
+
 // Place diagonal-block inverses into X.
 __global__ void place_diag_inv_kernel(const float* linv, int64_t d, float* X, int64_t wsf) {
   linv += (int64_t)blockIdx.y * wsf;
@@ -940,75 +1194,6 @@ HinvLayout hinv_layout(int64_t d) {
 
 }  // namespace
 
-// Large-K products (K >= 256, not lower-only) are plain GEMMs that rocBLAS
-// runs near the fp32 MFMA peak; one handle per device, its stream set under
-// a lock for each call (rocBLAS keeps its own workspace).
-namespace {
-std::mutex g_blas_mu;
-rocblas_handle g_blas[64] = {};
-
-// Runs f(handle) under the lock with this device's handle bound to `stream`.
-template <class F>
-int with_blas(hipStream_t stream, F&& f) {
-  int dev = 0;
-  MQ_CHECK_HIP(hipGetDevice(&dev));
-  MQ_CHECK_ARG(dev >= 0 && dev < 64, "rocblas: device index out of range");
-  std::lock_guard<std::mutex> lock(g_blas_mu);
-  if (!g_blas[dev] && rocblas_create_handle(&g_blas[dev]) != rocblas_status_success) {
-    g_blas[dev] = nullptr;
-    set_error("rocblas_create_handle failed");
-    return MI355Q_HIP_ERROR;
-  }
-  rocblas_handle h = g_blas[dev];
-  if (rocblas_set_stream(h, stream) != rocblas_status_success) {
-    set_error("rocblas_set_stream failed");
-    return MI355Q_HIP_ERROR;
-  }
-  return f(h);
-}
-
-int blas_status(rocblas_status rs, const char* what) {
-  if (rs == rocblas_status_success) return MI355Q_OK;
-  set_error("%s failed: %s", what, rocblas_status_to_string(rs));
-  return MI355Q_HIP_ERROR;
-}
-
-// Two batch levels (GemmArgs::inner): one strided-batched library call per
-// index of the shorter level, batching over the longer one.  f(nbat, oa, ob,
-// oc, sa, sb, sc) issues one call.
-template <class F>
-int blas_batches(const GemmArgs& g, int batch, F&& f) {
-  const int64_t n1 = g.inner > 0 ? g.inner : batch, n2 = batch / n1;
-  const bool loop1 = n1 < n2;  // loop over level 1, batch over level 2
-  const int64_t nloop = loop1 ? n1 : n2, nbat = loop1 ? n2 : n1;
-  const int64_t sa = loop1 ? g.strideA2 : g.strideA, sb = loop1 ? g.strideB2 : g.strideB,
-                sc = loop1 ? g.strideC2 : g.strideC;
-  for (int64_t l = 0; l < nloop; ++l) {
-    const int64_t oa = l * (loop1 ? g.strideA : g.strideA2), ob = l * (loop1 ? g.strideB : g.strideB2),
-                  oc = l * (loop1 ? g.strideC : g.strideC2);
-    const int rc = f(nbat, oa, ob, oc, sa, sb, sc);
-    if (rc) return rc;
-  }
-  return MI355Q_OK;
-}
-
-// row-major C = alpha A op(B) + beta C  <=>  column-major C^T = alpha op(B)^T A^T + beta C^T
-int gemm_rocblas(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
-  return with_blas(stream, [&](rocblas_handle h) {
-    return blas_batches(g, batch, [&](int64_t nbat, int64_t oa, int64_t ob, int64_t oc, int64_t sa, int64_t sb,
-                                      int64_t sc) {
-      return blas_status(
-          rocblas_sgemm_strided_batched(h, b_trans ? rocblas_operation_transpose : rocblas_operation_none,
-                                        rocblas_operation_none, (rocblas_int)g.N, (rocblas_int)g.M, (rocblas_int)g.K,
-                                        &g.alpha, g.B + ob, (rocblas_int)g.ldb, sb, g.A + oa, (rocblas_int)g.lda, sa,
-                                        &g.beta, g.C + oc, (rocblas_int)g.ldc, sc, (rocblas_int)nbat),
-          "rocblas_sgemm_strided_batched");
-    });
-  });
-}
-
-}  // namespace
-
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
   if (g.a_trans || g.upper_only) {   // the general kernel only
@@ -1026,10 +1211,36 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
     MQ_LAUNCH_CHECK();
     return MI355Q_OK;
   }
-  // (at most 8 strided-batched library calls: the shorter batch level is looped)
-  if (g.K >= 256 && !g.lower_only && g.M < (1ll << 31) && g.N < (1ll << 31) && g.K < (1ll << 31) &&
-      (g.inner == 0 || (batch % g.inner == 0 && (g.inner <= 8 || batch / g.inner <= 8))))
-    return gemm_rocblas(g, b_trans, batch, stream);
+  // K >= 256: the LDS-DMA kernel with a two-stage ring (two or three
+  // workgroups per CU).  Tile shapes as measured best on the solve's
+  // products: 64 x 128 for plain products (118 TFLOP/s on 4096 x 3072 x
+  // 1024), 64 x 64 with a triangular operand, lower-only products 128 x 64
+  // above 2048 rows, else 64 x 64.
+  const bool v16 = g.K % 4 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && aligned16(g.A) && aligned16(g.B) &&
+                   (b_trans || g.N % 4 == 0) && g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 &&
+                   g.strideB2 % 4 == 0;
+  if (g.K >= 256 && v16 && batch <= 65535 && ((g.M + 63) / 64) * ((g.N + 63) / 64) < (1ll << 31)) {
+#define MQ_DMA(TM, TN, WM, WN)                                                                             \
+  do {                                                                                                     \
+    dim3 grid((unsigned)(((g.N + TN - 1) / TN) * ((g.M + TM - 1) / TM)), 1, (unsigned)batch);              \
+    if (b_trans)                                                                                           \
+      hipLaunchKernelGGL((gemm_dma_kernel<TM, TN, WM, WN, true, 2>), grid, dim3(64 * WM * WN), 0, stream, g); \
+    else                                                                                                   \
+      hipLaunchKernelGGL((gemm_dma_kernel<TM, TN, WM, WN, false, 2>), grid, dim3(64 * WM * WN), 0, stream, g); \
+  } while (0)
+    if (g.a_lower || g.b_lower) {
+      MQ_DMA(64, 64, 2, 2);        // uneven K ranges: small tiles, the longest dispatched first
+    } else if (!g.lower_only) {
+      MQ_DMA(64, 128, 2, 2);
+    } else if (g.M * batch > 2048) {
+      MQ_DMA(128, 64, 2, 2);
+    } else {
+      MQ_DMA(64, 64, 2, 2);
+    }
+#undef MQ_DMA
+    MQ_LAUNCH_CHECK();
+    return MI355Q_OK;
+  }
   // large-K lower-only products: K = 128 slices on the whole-tile kernel
   if (g.lower_only && g.K > KT && g.K % KT == 0 && g.M % KT == 0 && g.N % KT == 0) {
     GemmArgs s = g;
@@ -1119,6 +1330,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
   float* F = reinterpret_cast<float*>(ws + L.F);
   float* X = reinterpret_cast<float*>(ws + L.X);
   float* T = reinterpret_cast<float*>(ws + L.T);
+  const int64_t tfloats = (int64_t)((L.linv - L.T) / sizeof(float));
   float* linv = reinterpret_cast<float*>(ws + L.linv);
   float* damp = reinterpret_cast<float*>(ws + L.damp);
   const unsigned nb_ = (unsigned)batch;
@@ -1142,7 +1354,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
   // blocked right-looking Cholesky on F (lower), two levels: inside an outer
   // panel of OUTB blocks each 128-column block updates only the panel's
   // remaining columns (K = 128); the trailing matrix past the panel takes
-  // one rank-(OUTB * 128) update, a syrk with K up to 512 (rocBLAS)
+  // one rank-(OUTB * 128) lower-only update (K up to 512)
   constexpr int64_t OUTB = 4;
   const int64_t nblk = (d + NB - 1) / NB;
   for (int64_t ob = 0; ob < nblk; ob += OUTB) {
@@ -1176,36 +1388,29 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
         if (rc) return rc;
       }
     }
-    // past the outer panel: F[c_end:, c_end:] -= P P^T (lower), P = F[c_end:, c0:c_end]
+    // past the outer panel: F[c_end:, c_end:] -= P P^T (lower), P = F[c_end:, c0:c_end],
+    // one lower-only product (K up to OUTB * 128).  P is first copied into a
+    // compact buffer (the doubling scratch T, unused until the inverse): its
+    // rows d floats apart read markedly slower than rows kk floats apart.
     const int64_t rest2 = d - c_end, kk = c_end - c0;
     if (rest2 > 0) {
-      if (kk >= 256) {
-        // row strips of 1024: strip [r0, r1) takes columns [0, r1) in one
-        // library GEMM (K = kk), the lower triangle plus the upper half of its
-        // diagonal block, which nothing reads (the diagonal-block kernel
-        // masks it).  About 1.3x the triangle's multiply-adds at the
-        // library's GEMM rate, instead of its syrk at about a third of that
-        // rate (512-row strips get smaller library tiles and are slower).
-        constexpr int64_t SW = 1024;
-        for (int64_t r0 = 0; r0 < rest2; r0 += SW) {
-          const int64_t r1 = r0 + SW < rest2 ? r0 + SW : rest2;
-          GemmArgs s{};
-          s.A = F + (c_end + r0) * d + c0; s.lda = d; s.strideA = wsf;
-          s.B = F + c_end * d + c0; s.ldb = d; s.strideB = wsf;
-          s.C = F + (c_end + r0) * d + c_end; s.ldc = d; s.strideC = wsf;
-          s.M = r1 - r0; s.N = r1; s.K = kk; s.alpha = -1.f; s.beta = 1.f;
-          int rc = gemm_f32(s, true, (int)batch, st);
-          if (rc) return rc;
-        }
-      } else {
-        GemmArgs s{};
-        s.A = F + c_end * d + c0; s.lda = d; s.strideA = wsf;
-        s.B = F + c_end * d + c0; s.ldb = d; s.strideB = wsf;
-        s.C = F + c_end * d + c_end; s.ldc = d; s.strideC = wsf;
-        s.M = rest2; s.N = rest2; s.K = kk; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
-        int rc = gemm_f32(s, true, (int)batch, st);
-        if (rc) return rc;
+      const float* P = F + c_end * d + c0;
+      int64_t ldp = d;
+      if (rest2 * kk <= tfloats && kk % 4 == 0 && d % 4 == 0) {
+        const int64_t n4 = rest2 * kk / 4;
+        hipLaunchKernelGGL(copy_panel_kernel, dim3((unsigned)((n4 + 255) / 256 < 4096 ? (n4 + 255) / 256 : 4096), nb_),
+                           dim3(256), 0, st, P, d, T, kk, rest2, kk, wsf);
+        MQ_LAUNCH_CHECK();
+        P = T;
+        ldp = kk;
       }
+      GemmArgs s{};
+      s.A = P; s.lda = ldp; s.strideA = wsf;
+      s.B = P; s.ldb = ldp; s.strideB = wsf;
+      s.C = F + c_end * d + c_end; s.ldc = d; s.strideC = wsf;
+      s.M = rest2; s.N = rest2; s.K = kk; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
+      int rc = gemm_f32(s, true, (int)batch, st);
+      if (rc) return rc;
     }
   }
 
@@ -1231,38 +1436,26 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       if (npairs == 0) continue;
       const int64_t c0 = a0 + s;
       const int64_t stride_diag = 2 * s * (d + 1);
-      // Large levels (library GEMMs, which do not skip the zero triangle)
-      // run as `parts` strips, each with only the K range where the
-      // triangular operand can be nonzero: 5/8 of the multiply-adds at 4
-      // strips.  Smaller levels use the triangular K ranges of the MFMA
-      // kernel directly.
-      const int64_t parts = (s >= 1024 && s % 4 == 0 && s2 % 4 == 0) ? 4 : 1;
-      // T = L[c0:c0+s2, a0:a0+s] * X[a0:a0+s, a0:a0+s], column strip j of T
-      // needs rows k >= j w of the lower-triangular X11
-      for (int64_t j = 0; j < parts; ++j) {
-        const int64_t w = s / parts, k0 = j * w;
-        GemmArgs t1{};
-        t1.A = F + c0 * d + a0 + k0; t1.lda = d; t1.strideA = stride_diag; t1.strideA2 = wsf;
-        t1.B = X + (a0 + k0) * d + a0 + k0; t1.ldb = d; t1.strideB = stride_diag; t1.strideB2 = wsf;
-        t1.C = T + k0; t1.ldc = s; t1.strideC = s2 * s; t1.strideC2 = wsf;
-        t1.inner = npairs; t1.b_lower = 1;  // X11 is lower triangular
-        t1.M = s2; t1.N = w; t1.K = s - k0; t1.alpha = 1.f; t1.beta = 0.f;
-        const int rc = gemm_f32(t1, false, (int)(npairs * batch), st);
-        if (rc) return rc;
-      }
-      // X[c0:c0+s2, a0:a0+s] = -X[c0:c0+s2, c0:c0+s2] * T, row strip i of
-      // the result needs columns k < (i + 1) w of the lower-triangular X22
-      for (int64_t i = 0; i < parts; ++i) {
-        const int64_t w = s2 / parts, r0 = i * w;
-        GemmArgs t2{};
-        t2.A = X + (c0 + r0) * d + c0; t2.lda = d; t2.strideA = stride_diag; t2.strideA2 = wsf;
-        t2.B = T; t2.ldb = s; t2.strideB = s2 * s; t2.strideB2 = wsf;
-        t2.C = X + (c0 + r0) * d + a0; t2.ldc = d; t2.strideC = stride_diag; t2.strideC2 = wsf;
-        t2.inner = npairs; t2.a_lower = parts == 1 ? 1 : 0;  // X22 is lower triangular
-        t2.M = w; t2.N = s; t2.K = parts == 1 ? s2 : r0 + w; t2.alpha = -1.f; t2.beta = 0.f;
-        const int rc = gemm_f32(t2, false, (int)(npairs * batch), st);
-        if (rc) return rc;
-      }
+      // each tile of the two products runs only the K range where its
+      // triangular operand can be nonzero.
+      // T = L[c0:c0+s2, a0:a0+s] * X[a0:a0+s, a0:a0+s] (X11 lower triangular)
+      GemmArgs t1{};
+      t1.A = F + c0 * d + a0; t1.lda = d; t1.strideA = stride_diag; t1.strideA2 = wsf;
+      t1.B = X + a0 * d + a0; t1.ldb = d; t1.strideB = stride_diag; t1.strideB2 = wsf;
+      t1.C = T; t1.ldc = s; t1.strideC = s2 * s; t1.strideC2 = wsf;
+      t1.inner = npairs; t1.b_lower = 1;
+      t1.M = s2; t1.N = s; t1.K = s; t1.alpha = 1.f; t1.beta = 0.f;
+      int rc = gemm_f32(t1, false, (int)(npairs * batch), st);
+      if (rc) return rc;
+      // X[c0:c0+s2, a0:a0+s] = -X[c0:c0+s2, c0:c0+s2] * T (X22 lower triangular)
+      GemmArgs t2{};
+      t2.A = X + c0 * d + c0; t2.lda = d; t2.strideA = stride_diag; t2.strideA2 = wsf;
+      t2.B = T; t2.ldb = s; t2.strideB = s2 * s; t2.strideB2 = wsf;
+      t2.C = X + c0 * d + a0; t2.ldc = d; t2.strideC = stride_diag; t2.strideC2 = wsf;
+      t2.inner = npairs; t2.a_lower = 1;
+      t2.M = s2; t2.N = s; t2.K = s2; t2.alpha = -1.f; t2.beta = 0.f;
+      rc = gemm_f32(t2, false, (int)(npairs * batch), st);
+      if (rc) return rc;
     }
   }
   hipLaunchKernelGGL(flip_out_kernel, grid_for(vout), fb, 0, st, X, d, hinv_dev, wsf, shinv, vout ? 1 : 0);

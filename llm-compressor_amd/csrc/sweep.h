@@ -101,7 +101,7 @@ inline int lazy_update(float* w, int64_t rows, int64_t cols, int64_t batch, cons
 // thus get Sum_b Err_b Hinv[b, far] rounded once per mid- or super-block
 // instead of once per block, an fp32 rounding-order difference of the same
 // kind as a GEMM's summation order; most of the multiply-adds run at the
-// library GEMM's large-K rate instead of the K = 128 kernel's.  Block
+// large-K GEMM's rate instead of the K = 128 kernel's.  Block
 // boundaries stay those of the reference (whole blocks per mid- and
 // super-block).  Returns the first nonzero status.
 template <class Block, class Lazy>
