@@ -200,6 +200,24 @@ int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int
                               int8_t* codes_dev, float* losses_dev, void* workspace_dev,
                               size_t workspace_bytes, void* stream);
 
+/* mi355q_gptq_sweep_noalloc: mi355q_gptq_sweep without a workspace argument
+ * and without any allocation, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It has no counterpart in the reference.  The error workspace
+ * lives in a 64 MiB device array the library holds on each GPU it runs on
+ * until the process ends (mi355q_gptq_sweep_noalloc_max_bytes()): shapes whose
+ * mi355q_gptq_sweep_workspace_size (rows * min(1024, cols) fp32) exceeds it
+ * are rejected with MI355Q_INVALID_ARGUMENT.  Every call on a GPU shares that
+ * GPU's array, so calls that overlap on one GPU (other streams or threads)
+ * race; sequential calls need no clearing in between.  Arguments and results
+ * otherwise as mi355q_gptq_sweep, bit for bit. */
+size_t mi355q_gptq_sweep_noalloc_max_bytes(void);
+int mi355q_gptq_sweep_noalloc(float* w_work_dev, int64_t rows, int64_t cols, const float* hinv_dev,
+                              const float* scale_dev, const float* zp_dev, int64_t ld_scale,
+                              const int32_t* g_idx_dev, int strategy, int block_h, float qmin, float qmax,
+                              int dequant_bf16, int64_t blocksize, int8_t* codes_dev, float* losses_dev,
+                              void* stream);
+
 /* mi355q_gptq_store_weight: w_out[r][j] = w_work[r][invperm[j]] converted
  * to out_dtype (:279-284); codes are permuted the same way when
  * codes_in/codes_out are non-NULL.  invperm_dev may be NULL. */

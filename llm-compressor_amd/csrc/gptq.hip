@@ -13,6 +13,8 @@
 // GEMM whose output is rounded once and then subtracted, as in the reference.
 #include "sweep.h"
 
+#include <mutex>
+
 #pragma clang fp contract(off)
 
 namespace mi355q {
@@ -412,4 +414,59 @@ extern "C" int mi355q_gptq_store_weight(const float* w_work_dev, int64_t rows, i
                                         void* stream) {
   return mi355q_gptq_store_weight_batched(w_work_dev, rows, cols, 1, invperm_dev, 0, w_out_dev, out_dtype,
                                           ld_out, 0, codes_in_dev, codes_out_dev, stream);
+}
+
+// ---------------------------------------------------------------- sweep without allocation
+// The sweep's error workspace in a device array the library holds: one copy
+// per GPU (each device's own address, from hipGetSymbolAddress with that
+// device current, looked up once per device), alive until the process ends.
+// Every call on a GPU shares that GPU's array, so calls that overlap on one
+// GPU (different streams or threads) race; the sweep writes each error
+// column before any product reads it, so nothing needs clearing between calls.
+static constexpr size_t kSweepScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) float scratch[kSweepScratchBytes / sizeof(float)];
+
+namespace {
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+constexpr int kMaxDevices = 64;
+ScratchSlot g_scratch_slot[kMaxDevices];
+
+int sweep_scratch(void** out) {
+  int dev = 0;
+  MQ_CHECK_HIP(hipGetDevice(&dev));
+  MQ_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "gptq_sweep_noalloc: device index %d out of range", dev);
+  ScratchSlot& s = g_scratch_slot[dev];
+  std::call_once(s.once, [&s] { s.err = hipGetSymbolAddress(&s.ptr, HIP_SYMBOL(scratch)); });
+  if (s.err != hipSuccess || s.ptr == nullptr) {
+    set_error("gptq_sweep_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s", dev,
+              hipGetErrorString(s.err));
+    return MI355Q_HIP_ERROR;
+  }
+  *out = s.ptr;
+  return MI355Q_OK;
+}
+}  // namespace
+
+extern "C" size_t mi355q_gptq_sweep_noalloc_max_bytes(void) { return kSweepScratchBytes; }
+
+extern "C" int mi355q_gptq_sweep_noalloc(float* w_work_dev, int64_t rows, int64_t cols, const float* hinv_dev,
+                                         const float* scale_dev, const float* zp_dev, int64_t ld_scale,
+                                         const int32_t* g_idx_dev, int strategy, int block_h, float qmin, float qmax,
+                                         int dequant_bf16, int64_t blocksize, int8_t* codes_dev, float* losses_dev,
+                                         void* stream) {
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && blocksize > 0, "gptq_sweep_noalloc: bad shape");
+  const size_t need = mi355q_gptq_sweep_workspace_size(rows, cols, blocksize);
+  MQ_CHECK_ARG(need <= kSweepScratchBytes,
+               "gptq_sweep_noalloc: the error workspace of %lld x %lld needs %zu bytes, above the %zu-byte scratch "
+               "array (rows * min(1024, cols) fp32); use mi355q_gptq_sweep with a caller workspace",
+               (long long)rows, (long long)cols, need, kSweepScratchBytes);
+  void* ws = nullptr;
+  const int rc = sweep_scratch(&ws);
+  if (rc) return rc;
+  return mi355q_gptq_sweep(w_work_dev, rows, cols, hinv_dev, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h,
+                           qmin, qmax, dequant_bf16, blocksize, codes_dev, losses_dev, ws, kSweepScratchBytes, stream);
 }

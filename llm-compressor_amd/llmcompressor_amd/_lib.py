@@ -39,6 +39,9 @@ SIGNATURES = {
     "mi355q_gptq_sweep": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _f32, _f32, _i32,
                                  _i64, _vp, _vp, _vp, _sz, _vp]),
     "mi355q_gptq_store_weight": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i64, _vp, _vp, _vp]),
+    "mi355q_gptq_sweep_noalloc_max_bytes": (_sz, []),
+    "mi355q_gptq_sweep_noalloc": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _f32, _f32, _i32,
+                                         _i64, _vp, _vp, _vp]),
     "mi355q_gptq_hinv_batched": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _f32, _vp, _i64, _vp, _vp,
                                         _vp, _sz, _vp]),
     "mi355q_gptq_hinv_fallback": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp]),
