@@ -48,6 +48,13 @@ typedef enum {
   MI355Q_TOKEN = 4
 } mi355q_strategy;
 
+/* Value type of a quantized weight (compressed-tensors type + num_bits). */
+typedef enum {
+  MI355Q_QTYPE_INT = 0,        /* integers, num_bits <= 8 */
+  MI355Q_QTYPE_FP8_E4M3 = 1,   /* float8_e4m3fn (FP8 schemes) */
+  MI355Q_QTYPE_FP4_E2M1 = 2    /* fp4 e2m1 (MXFP4, NVFP4) */
+} mi355q_qtype;
+
 /* MXFP4 shared-exponent rule (see mi355q_mxfp4_quantize_pack). */
 typedef enum { MI355Q_MX_RULE_CT = 0, MI355Q_MX_RULE_OCP = 1 } mi355q_mx_rule;
 
@@ -200,6 +207,25 @@ int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int
                               int8_t* codes_dev, float* losses_dev, void* workspace_dev,
                               size_t workspace_bytes, void* stream);
 
+/* The sweep for every weight type the reference's GPTQ quantizes
+ * (gptq_quantize.py:215-257 call CT fake_quantize with the module's args and
+ * global_scale): qtype selects the rounding of x / scale after the clamp to
+ * [qmin, qmax] -- rint for integers, the float8_e4m3fn cast (round to
+ * nearest even) for FP8, CT's cast_to_fp4 thresholds for fp4 (MXFP4 with its
+ * power-of-two group scales; NVFP4 tensor-group with fp8 group scales and a
+ * global scale).  global_scale_dev (NULL: none) holds one fp32 value per
+ * matrix; the effective scale is scale / global_scale (CT's tensor-group
+ * rule).  Float types take no zero point and qmin = -qmax.  codes_dev holds
+ * the integer codes (QTYPE_INT), float8_e4m3fn bit patterns (FP8) or e2m1
+ * codes sign << 3 | grid index (FP4).  Otherwise as mi355q_gptq_sweep_batched. */
+int mi355q_gptq_sweep_typed_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
+                                    const float* hinv_dev, int64_t stride_hinv, const float* scale_dev,
+                                    const float* zp_dev, int64_t ld_scale, int64_t stride_scale,
+                                    const int32_t* g_idx_dev, int64_t stride_gidx, int strategy, int block_h,
+                                    int qtype, float qmin, float qmax, const float* global_scale_dev,
+                                    int dequant_bf16, int64_t blocksize, int8_t* codes_dev, float* losses_dev,
+                                    void* workspace_dev, size_t workspace_bytes, void* stream);
+
 /* mi355q_gptq_sweep_noalloc: mi355q_gptq_sweep without a workspace argument
  * and without any allocation, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
@@ -293,6 +319,16 @@ int mi355q_calculate_qparams(const float* min_dev, const float* max_dev, int64_t
  * values) and the scale 2^(e-127) as fp32.  Either output may be NULL. */
 int mi355q_mx_scales(const float* min_dev, const float* max_dev, int64_t n, int rule,
                      uint8_t* e8m0_out_dev, float* scale_out_dev, void* stream);
+
+/* NVFP4 tensor-group qparams from the n groups' min / max statistics (fp32
+ * holding values of stats_dtype, bf16 or fp32): the global scale
+ * (observers/base.py:78-96 -> CT generate_gparam: 448 * 6 / absmax of the
+ * whole weight, computed in stats_dtype, stored as fp32 in global_scale_dev[0])
+ * and each group's scale (CT calculate_qparams with that global scale:
+ * global * (absmax / 6) clamped to +-448 and cast to float8_e4m3fn, 0 -> the
+ * fp8 epsilon 0.125) as fp32 values (scale_out_dev) and / or e4m3 bits. */
+int mi355q_nvfp4_qparams(const float* min_dev, const float* max_dev, int64_t n, mi355q_dtype stats_dtype,
+                         float* global_scale_dev, float* scale_out_dev, uint8_t* e4m3_out_dev, void* stream);
 
 /* MSE observer grid search (observers/mse_quant.py:48-130,244-273; the
  * memoryless_mse / mse observers of observers/mse.py:12-98).  x [rows, cols]

@@ -69,4 +69,45 @@ __device__ __forceinline__ float sub_rn(float a, float b) { return a - b; }
 __device__ __forceinline__ float add_rn(float a, float b) { return a + b; }
 __device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
 
+// ---------------------------------------------------------------- float grids
+// float8_e4m3fn round to nearest even of |v| <= 448 (the clamp comes first):
+// the grid step is 2^(max(floor(log2 |v|), -6) - 3), a power of two, so the
+// scaling, rint and rescaling are exact; the sign (also of a zero) is kept,
+// as the cast keeps it.
+__device__ __forceinline__ float fp8e4m3_rne(float v) {
+  const float a = fabsf(v);
+  const int e = (int)((__float_as_uint(a) >> 23) & 0xffu) - 127;
+  const int qe = (e > -6 ? e : -6) - 3;
+  const float r = rintf(a * __uint_as_float((uint32_t)(127 - qe) << 23)) * __uint_as_float((uint32_t)(127 + qe) << 23);
+  return copysignf(r, v);
+}
+// its float8_e4m3fn bit pattern (v on the grid)
+__device__ __forceinline__ uint32_t fp8e4m3_bits(float v) {
+  const uint32_t sgn = (__float_as_uint(v) >> 31) << 7;
+  const float a = fabsf(v);
+  if (a == 0.f) return sgn;
+  const int e = (int)((__float_as_uint(a) >> 23) & 0xffu) - 127;
+  if (e < -6) return sgn | (uint32_t)rintf(a * 512.f);                       // subnormal: a / 2^-9
+  return sgn | ((uint32_t)(e + 7) << 3) | ((__float_as_uint(a) >> 20) & 7u);  // normal
+}
+// compressed-tensors cast_to_fp4 (e2m1) of |x| <= 6 (the clamp comes
+// first): its thresholds (<= .25, < .75, <= 1.25, < 1.75, <= 2.5, < 3.5,
+// <= 5) are round-to-nearest-even on the grid {0, .5, 1, 1.5, 2, 3, 4, 6},
+// whose step is .5 below 2, 1 below 4 and 2 above, so rint of |x| / step is
+// exact; the sign is applied by multiplying with sign(x) (so (-0.25, 0) gives
+// -0 and -0 gives +0)
+__device__ __forceinline__ float fp4e2m1_round(float x) {
+  const float a = fabsf(x);
+  const float step = a < 2.f ? 0.5f : a < 4.f ? 1.f : 2.f;
+  const float rstep = a < 2.f ? 2.f : a < 4.f ? 1.f : 0.5f;
+  const float o = rintf(a * rstep) * step;
+  return x < 0.f ? -o : o;
+}
+// its e2m1 code: sign << 3 | index of |v| in {0, .5, 1, 1.5, 2, 3, 4, 6}
+__device__ __forceinline__ uint32_t fp4e2m1_bits(float v) {
+  const float a = fabsf(v);
+  const uint32_t i = a < 2.f ? (uint32_t)(a * 2.f) : a < 4.f ? (uint32_t)(a) + 2u : a < 6.f ? 6u : 7u;
+  return ((__float_as_uint(v) >> 31) << 3) | i;
+}
+
 }  // namespace mi355q

@@ -35,19 +35,34 @@ struct SweepState {
 // instruction: two operations on the sweep's serial chain instead of four).
 __device__ __forceinline__ float bf16_rne(float f) { return (float)(__bf16)f; }
 
-// CT quantize / dequantize of one value: qq = clamp(rint(x / s + z)),
-// deq = (qq - z) * s, rounded to bf16 when the scale is bf16 (BF16).  ZP:
-// a zero point (asymmetric); without one, z = 0 and the additions drop out
-// (x + 0 = x, and the sign of a zero quotient changes neither the code nor
-// the error).
-template <bool BF16, bool ZP>
+// Value types of the sweep: integers, or the float grids of compressed-
+// tensors' round_to_quantized_type (float8_e4m3fn, fp4 e2m1).
+enum { QK_INT = 0, QK_FP8 = 1, QK_FP4 = 2 };
+
+// CT quantize / dequantize of one value: qq = round_to_type(clamp(x / s + z)),
+// deq = (qq - z) * s, rounded to bf16 when the scale is bf16 (BF16).  For
+// QK_INT, qq is the integer code; for the float grids it is the grid value
+// (no zero point).  ZP: a zero point (asymmetric); without one, z = 0 and the
+// additions drop out (x + 0 = x, and the sign of a zero quotient changes
+// neither the code nor the error).
+template <bool BF16, bool ZP, int QK>
 __device__ __forceinline__ void quant1(float x, float s, float rs, float z, float qmin, float qmax, float& qq,
                                        float& deq) {
   qq = div_by_recip(x, s, rs);
   if (ZP) qq = qq + z;
-  qq = rintf(fminf(fmaxf(qq, qmin), qmax));
+  qq = fminf(fmaxf(qq, qmin), qmax);
+  if (QK == QK_INT) qq = rintf(qq);
+  if (QK == QK_FP8) qq = fp8e4m3_rne(qq);
+  if (QK == QK_FP4) qq = fp4e2m1_round(qq);
   deq = (ZP ? qq - z : qq) * s;
   if (BF16) deq = bf16_rne(deq);
+}
+
+template <int QK>
+__device__ __forceinline__ int8_t code_of(float qq) {
+  if (QK == QK_FP8) return (int8_t)fp8e4m3_bits(qq);
+  if (QK == QK_FP4) return (int8_t)fp4e2m1_bits(qq);
+  return (int8_t)qq;
 }
 
 // One column of the sweep: column I = SW_G * TO + GO, owned by lane GO of
@@ -56,7 +71,7 @@ __device__ __forceinline__ void quant1(float x, float s, float rs, float z, floa
 // the row, and each lane updates its later columns.  A lane's slot is final
 // from its own step on, so its code, dequantised value and error are
 // recomputed once after the sweep instead of being selected at every step.
-template <int TO, int GO, bool FULL, bool BF16, bool ZP>
+template <int TO, int GO, bool FULL, bool BF16, bool ZP, int QK>
 __device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, const float* rdg, int g, int count,
                                            float qmin, float qmax) {
   constexpr int I = SW_G * TO + GO;
@@ -64,7 +79,7 @@ __device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, const
   const float dd = h1[hrow(I)];
   const float x = S.w[TO];
   float qq, deq;
-  quant1<BF16, ZP>(x, S.s[TO], S.rs[TO], S.z[TO], qmin, qmax, qq, deq);
+  quant1<BF16, ZP, QK>(x, S.s[TO], S.rs[TO], S.z[TO], qmin, qmax, qq, deq);
   const float err = div_by_recip(x - deq, dd, rdg[I]);
   const float e = row_bcast<GO>(err);
 #pragma unroll
@@ -81,16 +96,16 @@ __device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, const
   }
 }
 
-template <int I, bool FULL, bool BF16, bool ZP>
+template <int I, bool FULL, bool BF16, bool ZP, int QK>
 struct SweepSteps {
   static __device__ __forceinline__ void run(SweepState& S, const float* h1, const float* rdg, int g, int count,
                                              float qmin, float qmax) {
-    sweep_step<I / SW_G, I % SW_G, FULL, BF16, ZP>(S, h1, rdg, g, count, qmin, qmax);
-    SweepSteps<I + 1, FULL, BF16, ZP>::run(S, h1, rdg, g, count, qmin, qmax);
+    sweep_step<I / SW_G, I % SW_G, FULL, BF16, ZP, QK>(S, h1, rdg, g, count, qmin, qmax);
+    SweepSteps<I + 1, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax);
   }
 };
-template <bool FULL, bool BF16, bool ZP>
-struct SweepSteps<MAXB, FULL, BF16, ZP> {
+template <bool FULL, bool BF16, bool ZP, int QK>
+struct SweepSteps<MAXB, FULL, BF16, ZP, QK> {
   static __device__ __forceinline__ void run(SweepState&, const float*, const float*, int, int, float, float) {}
 };
 
@@ -100,14 +115,16 @@ struct SweepBatch {
   int64_t w, hinv, scale, gidx, codes, losses, err;
 };
 
-// FULL: a whole MAXB-column block; BF16: dequantise in bf16; ZP: zero points
-template <bool FULL, bool BF16, bool ZP>
+// FULL: a whole MAXB-column block; BF16: dequantise in bf16; ZP: zero
+// points; QK: value type.  gscale (NULL: 1): per-matrix global scale, the
+// effective scale being scale / gscale (CT's tensor-group scales).
+template <bool FULL, bool BF16, bool ZP, int QK>
 __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
     int count, const float* __restrict__ scale, const float* __restrict__ zp, int64_t ld_scale,
     const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax,
-    int8_t* __restrict__ codes, float* __restrict__ losses, float* __restrict__ err_out, int64_t lde,
-    int err_col, SweepBatch sb) {
+    const float* __restrict__ gscale, int8_t* __restrict__ codes, float* __restrict__ losses,
+    float* __restrict__ err_out, int64_t lde, int err_col, SweepBatch sb) {
   __shared__ float h1[HPK];
   __shared__ float rdg[MAXB];  // 1 / Hinv[i][i], correctly rounded
   __shared__ int gsh[MAXB];
@@ -127,6 +144,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
   const int64_t r = (int64_t)blockIdx.x * SW_ROWS + (tid / SW_G);
   const bool live = r < rows;
   const int64_t rr = live ? r : rows - 1;  // clamped row: every address below is in bounds
+  const float gsc = gscale ? gscale[blockIdx.y] : 1.f;
 
   SweepState S;
   // every global load is issued before the first LDS store: the row's
@@ -154,12 +172,12 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
   for (int t = 0; t < SW_T; ++t) {
     const int col = min(SW_G * t + g, count - 1);
     const int64_t si = sbase + gsh[col];
-    S.s[t] = scale[si];
+    S.s[t] = scale[si] / gsc;   // exact for gsc == 1
     S.rs[t] = 1.f / S.s[t];
     S.z[t] = ZP ? zp[si] : 0.f;
   }
 
-  SweepSteps<0, FULL, BF16, ZP>::run(S, h1, rdg, g, count, qmin, qmax);
+  SweepSteps<0, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax);
 
   // each slot is final: its code, dequantised value, error and loss
   float loss = 0.f;
@@ -169,7 +187,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     const int cc = min(col, count - 1);
     const float dd = h1[hrow(cc)];
     float qq, deq;
-    quant1<BF16, ZP>(S.w[t], S.s[t], S.rs[t], S.z[t], qmin, qmax, qq, deq);
+    quant1<BF16, ZP, QK>(S.w[t], S.s[t], S.rs[t], S.z[t], qmin, qmax, qq, deq);
     const float diff = S.w[t] - deq;
     const float err = div_by_recip(diff, dd, rdg[cc]);
     if (col < count) {
@@ -177,7 +195,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
       if (live) {
         const int64_t c = i1 + col;
         W[r * cols + c] = deq;
-        codes[r * cols + c] = (int8_t)qq;
+        codes[r * cols + c] = code_of<QK>(qq);
         err_out[r * lde + err_col + col] = err;
       }
     }
@@ -292,14 +310,22 @@ inline dim3 grid_rows(int64_t rows, int64_t cols, int64_t batch = 1) {
 
 // the kernel variant for (whole block, bf16 dequantisation, zero points)
 template <class... A>
-void launch_sweep(bool full, bool bf16, bool zp, dim3 grid, hipStream_t st, A... args) {
+void launch_sweep(bool full, bool bf16, bool zp, int qk, dim3 grid, hipStream_t st, A... args) {
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(SW_NT), 0, st, args...); };
-  if (full) {
-    if (bf16) zp ? go(sweep_block_kernel<true, true, true>) : go(sweep_block_kernel<true, true, false>);
-    else      zp ? go(sweep_block_kernel<true, false, true>) : go(sweep_block_kernel<true, false, false>);
+  if (qk == QK_INT) {
+    if (full) {
+      if (bf16) zp ? go(sweep_block_kernel<true, true, true, QK_INT>) : go(sweep_block_kernel<true, true, false, QK_INT>);
+      else      zp ? go(sweep_block_kernel<true, false, true, QK_INT>) : go(sweep_block_kernel<true, false, false, QK_INT>);
+    } else {
+      if (bf16) zp ? go(sweep_block_kernel<false, true, true, QK_INT>) : go(sweep_block_kernel<false, true, false, QK_INT>);
+      else      zp ? go(sweep_block_kernel<false, false, true, QK_INT>) : go(sweep_block_kernel<false, false, false, QK_INT>);
+    }
+  } else if (qk == QK_FP8) {
+    if (full) bf16 ? go(sweep_block_kernel<true, true, false, QK_FP8>) : go(sweep_block_kernel<true, false, false, QK_FP8>);
+    else      bf16 ? go(sweep_block_kernel<false, true, false, QK_FP8>) : go(sweep_block_kernel<false, false, false, QK_FP8>);
   } else {
-    if (bf16) zp ? go(sweep_block_kernel<false, true, true>) : go(sweep_block_kernel<false, true, false>);
-    else      zp ? go(sweep_block_kernel<false, false, true>) : go(sweep_block_kernel<false, false, false>);
+    if (full) bf16 ? go(sweep_block_kernel<true, true, false, QK_FP4>) : go(sweep_block_kernel<true, false, false, QK_FP4>);
+    else      bf16 ? go(sweep_block_kernel<false, true, false, QK_FP4>) : go(sweep_block_kernel<false, false, false, QK_FP4>);
   }
 }
 
@@ -337,13 +363,14 @@ extern "C" size_t mi355q_gptq_sweep_workspace_size(int64_t rows, int64_t cols, i
   return (size_t)rows * err_cols(cols, blocksize) * sizeof(float);
 }
 
-extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
-                                         const float* hinv_dev, int64_t stride_hinv, const float* scale_dev,
-                                         const float* zp_dev, int64_t ld_scale, int64_t stride_scale,
-                                         const int32_t* g_idx_dev, int64_t stride_gidx, int strategy, int block_h,
-                                         float qmin, float qmax, int dequant_bf16, int64_t blocksize,
-                                         int8_t* codes_dev, float* losses_dev, void* workspace_dev,
-                                         size_t workspace_bytes, void* stream) {
+extern "C" int mi355q_gptq_sweep_typed_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
+                                               const float* hinv_dev, int64_t stride_hinv, const float* scale_dev,
+                                               const float* zp_dev, int64_t ld_scale, int64_t stride_scale,
+                                               const int32_t* g_idx_dev, int64_t stride_gidx, int strategy,
+                                               int block_h, int qtype, float qmin, float qmax,
+                                               const float* global_scale_dev, int dequant_bf16, int64_t blocksize,
+                                               int8_t* codes_dev, float* losses_dev, void* workspace_dev,
+                                               size_t workspace_bytes, void* stream) {
   MQ_CHECK_ARG(w_work_dev && hinv_dev && scale_dev && codes_dev && losses_dev, "gptq_sweep: null pointer");
   MQ_CHECK_ARG(rows > 0 && cols > 0 && batch > 0 && batch <= 65535, "gptq_sweep: bad shape");
   MQ_CHECK_ARG(blocksize > 0, "gptq_sweep: blocksize must be positive");
@@ -353,7 +380,13 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
   MQ_CHECK_ARG((strategy != MI355Q_GROUP && strategy != MI355Q_BLOCK) || g_idx_dev,
                "gptq_sweep: group/block strategies need g_idx");
   MQ_CHECK_ARG(strategy != MI355Q_BLOCK || block_h > 0, "gptq_sweep: block_h must be positive");
-  MQ_CHECK_ARG(qmin < qmax && qmin >= -128.f && qmax <= 127.f, "gptq_sweep: integer range must fit int8");
+  MQ_CHECK_ARG(qtype == MI355Q_QTYPE_INT || qtype == MI355Q_QTYPE_FP8_E4M3 || qtype == MI355Q_QTYPE_FP4_E2M1,
+               "gptq_sweep: unknown value type %d", qtype);
+  if (qtype == MI355Q_QTYPE_INT)
+    MQ_CHECK_ARG(qmin < qmax && qmin >= -128.f && qmax <= 127.f, "gptq_sweep: integer range must fit int8");
+  else
+    MQ_CHECK_ARG(!zp_dev && qmin == -qmax && qmax <= (qtype == MI355Q_QTYPE_FP8_E4M3 ? 448.f : 6.f) && qmax > 0.f,
+                 "gptq_sweep: float types are symmetric within the type's range");
   MQ_CHECK_ARG(batch == 1 || stride_hinv >= cols * cols, "gptq_sweep: Hinv matrices overlap");
   const size_t need = mi355q_gptq_sweep_workspace_size(rows, cols, blocksize) * (size_t)batch;
   MQ_CHECK_ARG(workspace_dev && workspace_bytes >= need, "gptq_sweep: workspace too small");
@@ -361,6 +394,7 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
   float* err = static_cast<float*>(workspace_dev);
   const int64_t lde = err_cols(cols, blocksize);
   SweepBatch sb{rows * cols, stride_hinv, stride_scale, stride_gidx, rows * cols, rows, rows * lde};
+  const int qk = qtype == MI355Q_QTYPE_FP8_E4M3 ? QK_FP8 : qtype == MI355Q_QTYPE_FP4_E2M1 ? QK_FP4 : QK_INT;
   // the sweep kernel holds at most MAXB columns; larger reference block
   // sizes give the same result up to fp32 rounding of the lazy update, so
   // they are processed in MAXB-wide sub-blocks
@@ -368,9 +402,9 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
   const unsigned nwg = (unsigned)((rows + SW_ROWS - 1) / SW_ROWS);
   auto block = [&](int64_t i1, int64_t i2, int64_t s0) {
     const int count = (int)(i2 - i1);
-    launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, dim3(nwg, (unsigned)batch), st, w_work_dev,
+    launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, qk, dim3(nwg, (unsigned)batch), st, w_work_dev,
                  rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
-                 qmax, codes_dev, losses_dev, err, lde, (int)(i1 - s0), sb);
+                 qmax, global_scale_dev, codes_dev, losses_dev, err, lde, (int)(i1 - s0), sb);
     MQ_LAUNCH_CHECK();
     return MI355Q_OK;
   };
@@ -378,6 +412,19 @@ extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_
     return lazy_update(w_work_dev, rows, cols, batch, hinv_dev, stride_hinv, err, lde, k0, k1, s0, c0, c1, st);
   };
   return blocked_schedule(cols, B, block, lazy);
+}
+
+extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,
+                                         const float* hinv_dev, int64_t stride_hinv, const float* scale_dev,
+                                         const float* zp_dev, int64_t ld_scale, int64_t stride_scale,
+                                         const int32_t* g_idx_dev, int64_t stride_gidx, int strategy, int block_h,
+                                         float qmin, float qmax, int dequant_bf16, int64_t blocksize,
+                                         int8_t* codes_dev, float* losses_dev, void* workspace_dev,
+                                         size_t workspace_bytes, void* stream) {
+  return mi355q_gptq_sweep_typed_batched(w_work_dev, rows, cols, batch, hinv_dev, stride_hinv, scale_dev, zp_dev,
+                                         ld_scale, stride_scale, g_idx_dev, stride_gidx, strategy, block_h,
+                                         MI355Q_QTYPE_INT, qmin, qmax, nullptr, dequant_bf16, blocksize, codes_dev,
+                                         losses_dev, workspace_dev, workspace_bytes, stream);
 }
 
 extern "C" int mi355q_gptq_sweep(float* w_work_dev, int64_t rows, int64_t cols, const float* hinv_dev,

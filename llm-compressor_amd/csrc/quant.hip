@@ -845,6 +845,53 @@ __global__ __launch_bounds__(NT) void int8_per_token_vec_kernel(const uint16_t* 
   }
 }
 
+// NVFP4 (tensor-group fp4) qparams from min / max statistics (fp32 holding
+// values of the statistics' dtype; bf16 rounding of every step when stats16):
+// the global scale is CT generate_gparam over the whole weight's absmax
+// (observers/base.py:78-96): 448 * 6 / absmax in the statistics' dtype, then
+// fp32; each group's scale is CT calculate_qparams with that global scale:
+// global * (absmax_g / 6), clamped to +-448, cast to float8_e4m3fn (round to
+// nearest even), zero replaced by the fp8 epsilon 0.125.
+__global__ __launch_bounds__(1024) void nvfp4_global_kernel(const float* __restrict__ mn,
+                                                            const float* __restrict__ mx, int64_t n, int stats16,
+                                                            float* __restrict__ gscale) {
+  __shared__ float red[1024];
+  float a = -INFINITY;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) a = fmaxf(a, fmaxf(mx[i], -mn[i]));
+  red[threadIdx.x] = a;
+  __syncthreads();
+  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float g = red[0];
+    const float mvp = fmaxf(fabsf(fminf(-g, 0.f)), fabsf(fmaxf(g, 0.f)));
+    // CT writes fp8_max * fp4_max / absmax with a Python scalar over a tensor,
+    // which torch evaluates as reciprocal(absmax) * 2688, each result rounded
+    // to the statistics' dtype
+    float r = 1.f / mvp;
+    if (stats16) r = round_to_bf16(r);
+    const float gs = 2688.f * r;
+    gscale[0] = stats16 ? round_to_bf16(gs) : gs;
+  }
+}
+
+__global__ void nvfp4_scales_kernel(const float* __restrict__ mn, const float* __restrict__ mx, int64_t n,
+                                    int stats16, const float* __restrict__ gscale, float* __restrict__ scale_out,
+                                    uint8_t* __restrict__ bits_out) {
+  const float g = gscale[0];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float mvp = fmaxf(fabsf(fminf(mn[i], 0.f)), fabsf(fmaxf(mx[i], 0.f)));
+    float q = mvp / 6.f;
+    if (stats16) q = round_to_bf16(q);
+    float sc = fp8e4m3_rne(fminf(fmaxf(g * q, -448.f), 448.f));
+    if (sc == 0.f) sc = 0.125f;
+    if (scale_out) scale_out[i] = sc;
+    if (bits_out) bits_out[i] = (uint8_t)fp8e4m3_bits(sc);
+  }
+}
+
 inline unsigned grid_for(int64_t n, int64_t per_block = NT, unsigned cap = 65536u) {
   int64_t g = (n + per_block - 1) / per_block;
   if (g < 1) g = 1;
@@ -1100,6 +1147,22 @@ extern "C" int mi355q_mx_scales(const float* min_dev, const float* max_dev, int6
   hipLaunchKernelGGL(mx_scales_kernel, dim3(grid_for(n, NT, 1u << 30)), dim3(NT), 0,
                      reinterpret_cast<hipStream_t>(stream), min_dev, max_dev, n, rule, e8m0_out_dev,
                      scale_out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_nvfp4_qparams(const float* min_dev, const float* max_dev, int64_t n, mi355q_dtype stats_dtype,
+                                    float* global_scale_dev, float* scale_out_dev, uint8_t* e4m3_out_dev,
+                                    void* stream) {
+  MQ_CHECK_ARG(min_dev && max_dev && global_scale_dev, "nvfp4_qparams: null pointer");
+  MQ_CHECK_ARG(n > 0, "nvfp4_qparams: no statistics");
+  MQ_CHECK_ARG(stats_dtype == MI355Q_BF16 || stats_dtype == MI355Q_F32, "nvfp4_qparams: bad statistics dtype");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int s16 = stats_dtype == MI355Q_BF16 ? 1 : 0;
+  hipLaunchKernelGGL(nvfp4_global_kernel, dim3(1), dim3(1024), 0, st, min_dev, max_dev, n, s16, global_scale_dev);
+  MQ_LAUNCH_CHECK();
+  hipLaunchKernelGGL(nvfp4_scales_kernel, dim3(grid_for(n, NT, 1u << 16)), dim3(NT), 0, st, min_dev, max_dev, n, s16,
+                     global_scale_dev, scale_out_dev, e4m3_out_dev);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
 }

@@ -16,6 +16,7 @@ OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_POSITIVE_DEFINITE, HIP_ERROR = 0, 1, 2, 3
 BF16, F32, F16 = 0, 1, 2
 TENSOR, CHANNEL, GROUP, BLOCK, TOKEN = 0, 1, 2, 3, 4
 MX_RULE_CT, MX_RULE_OCP = 0, 1
+QTYPE_INT, QTYPE_FP8_E4M3, QTYPE_FP4_E2M1 = 0, 1, 2
 
 _vp, _i64, _i32, _f32, _f64, _sz = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double, C.c_size_t
 
@@ -49,6 +50,9 @@ SIGNATURES = {
                                                _vp]),
     "mi355q_gptq_sweep_batched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i32,
                                          _i32, _f32, _f32, _i32, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "mi355q_gptq_sweep_typed_batched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _i64,
+                                               _i32, _i32, _i32, _f32, _f32, _vp, _i32, _i64, _vp, _vp, _vp, _sz,
+                                               _vp]),
     "mi355q_gptq_store_weight_batched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _i64, _i64, _vp,
                                                 _vp, _vp]),
     "mi355q_sparsegpt_base_mask": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
@@ -64,6 +68,7 @@ SIGNATURES = {
     "mi355q_column_sumsq_workspace_size": (_sz, [_i64, _i64]),
     "mi355q_column_sumsq": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "mi355q_mx_scales": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp]),
+    "mi355q_nvfp4_qparams": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp]),
     "mi355q_quantize_int": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i32, _i64, _i32, _i32,
                                    _i32, _i32, _vp, _vp]),
     "mi355q_pack_int4_int32": (_i32, [_vp, _i64, _i64, _vp, _vp]),

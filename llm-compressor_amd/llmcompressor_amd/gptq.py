@@ -79,8 +79,30 @@ class GPTQResult:
     zero_point: torch.Tensor
     g_idx: torch.Tensor | None      # reference g_idx in working order (None if no groups)
     perm: torch.Tensor | None
-    codes: torch.Tensor             # int8 integer codes, original column order
+    codes: torch.Tensor             # int8, original column order: integer codes, or the
+                                    # float8_e4m3fn bits / e2m1 codes (sign << 3 | grid index)
     hinv_ok: bool
+    global_scale: torch.Tensor | None = None   # tensor-group (NVFP4) global scale, fp32 [1]
+
+
+_SWEEP_STRATEGIES = (QuantizationStrategy.TENSOR, QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP,
+                     QuantizationStrategy.TENSOR_GROUP, QuantizationStrategy.BLOCK)
+_GROUPED = (QuantizationStrategy.GROUP, QuantizationStrategy.TENSOR_GROUP)
+
+
+def _value_type(quant_args: QuantizationArgs) -> str:
+    """The sweep's value type: integers, or CT's float8_e4m3fn / fp4 e2m1 grids."""
+    if quant_args.strategy not in _SWEEP_STRATEGIES:
+        raise ValueError(f"Quantization strategy is not supported for GPTQ: {quant_args.strategy}")
+    if quant_args.type == QuantizationType.INT:
+        return "int"
+    if not quant_args.symmetric:
+        raise NotImplementedError("asymmetric float quantization")
+    if quant_args.num_bits == 8:
+        return "fp8"
+    if quant_args.num_bits == 4:
+        return "fp4"
+    raise NotImplementedError(f"float weights of {quant_args.num_bits} bits")
 
 
 def _qparams_for_sweep(scale: torch.Tensor, zero_point: torch.Tensor, strategy: QuantizationStrategy):
@@ -173,11 +195,7 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
     Cholesky chain for modules that share their input.
     """
     strategy = quant_args.strategy
-    if quant_args.type != QuantizationType.INT:
-        raise NotImplementedError("GPTQ on the GPU supports integer quantization types")
-    if strategy not in (QuantizationStrategy.TENSOR, QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP,
-                        QuantizationStrategy.BLOCK):
-        raise ValueError(f"Quantization strategy is not supported for GPTQ: {strategy}")
+    qtype = _value_type(quant_args)
     W = weight
     rows, cols = W.shape
     prep = prepared if prepared is not None else prepare_hessian(hessian, quant_args, num_samples, percdamp)
@@ -187,14 +205,14 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
         observer(ops.gptq_load_weight(W, perm))   # permuted fp32 weight
 
     g_idx = None
-    if strategy in (QuantizationStrategy.GROUP, QuantizationStrategy.BLOCK):
+    if strategy in _GROUPED + (QuantizationStrategy.BLOCK,):
         divisor = quant_args.group_size if strategy != QuantizationStrategy.BLOCK else quant_args.block_structure[1]
         g_idx = torch.arange(cols, device=W.device, dtype=torch.int) // divisor
         if actorder == ActivationOrdering.WEIGHT:
             g_idx = g_idx[perm]
 
     qp = observer.get_qparams()
-    scale, zero_point = qp["scale"], qp["zero_point"]
+    scale, zero_point, global_scale = qp["scale"], qp["zero_point"], qp.get("global_scale")
 
     hinv, dead = prep.hinv, prep.dead
     w_work = ops.gptq_load_weight(W, perm, dead)
@@ -204,14 +222,15 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
     qmin, qmax = quant_args.q_range()
     bh = quant_args.block_structure[0] if strategy == QuantizationStrategy.BLOCK else 1
     codes, losses = ops.gptq_sweep_(w_work, hinv, s, z, strategy.value, g_idx, qmin, qmax,
-                                    dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize, block_h=bh)
+                                    dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize, block_h=bh,
+                                    qtype=qtype, global_scale=global_scale)
     w_out, codes_out = ops.gptq_store_weight(w_work, invperm, W.dtype, codes)
     loss_ok = torch.stack([torch.sum(losses), (prep.status[0] == 0).float()]).cpu()  # the one sync
     ok = bool(loss_ok[1])
     if not ok:
         _hinv_fallback_warning()
     return GPTQResult(loss=float(loss_ok[0]), weight=w_out, scale=scale, zero_point=zero_point, g_idx=g_idx,
-                      perm=perm, codes=codes_out, hinv_ok=ok)
+                      perm=perm, codes=codes_out, hinv_ok=ok, global_scale=global_scale)
 
 
 def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, hessians: torch.Tensor,
@@ -233,11 +252,7 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
     from .observers import Observer
 
     strategy = quant_args.strategy
-    if quant_args.type != QuantizationType.INT:
-        raise NotImplementedError("GPTQ on the GPU supports integer quantization types")
-    if strategy not in (QuantizationStrategy.TENSOR, QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP,
-                        QuantizationStrategy.BLOCK):
-        raise ValueError(f"Quantization strategy is not supported for GPTQ: {strategy}")
+    qtype = _value_type(quant_args)
     B, rows, cols = weights.shape
     if hessians.shape != (B, cols, cols):
         raise ValueError(f"hessians must be [{B}, {cols}, {cols}], got {tuple(hessians.shape)}")
@@ -251,21 +266,26 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
         obs = Observer.load_from_registry(observer, base_name="weight", args=quant_args)
         obs(x)
         qp = obs.get_qparams()
-        return qp["scale"], qp["zero_point"]
+        return qp["scale"], qp["zero_point"], qp.get("global_scale")
 
+    # per-row statistics observe the stacked weights at once; tensor-wide
+    # ones (tensor scales, tensor-group global scales) member by member
     stackable = strategy in (QuantizationStrategy.CHANNEL, QuantizationStrategy.GROUP) or (
         strategy == QuantizationStrategy.BLOCK and rows % quant_args.block_structure[0] == 0)
+    global_scale = None
     if stackable:
-        sc, zp = observe(src.reshape(B * rows, cols))
+        sc, zp, _ = observe(src.reshape(B * rows, cols))
         scale, zero_point = sc.reshape(B, -1, sc.shape[-1]), zp.reshape(B, -1, zp.shape[-1])
     else:
         qps = [observe(src[b]) for b in range(B)]
         scale = torch.stack([q[0] for q in qps]).reshape(B, 1, 1) if strategy == QuantizationStrategy.TENSOR \
             else torch.stack([q[0] for q in qps])
         zero_point = torch.stack([q[1] for q in qps]).reshape(scale.shape)
+        if qps[0][2] is not None:
+            global_scale = torch.cat([q[2].reshape(1) for q in qps])
 
     g_idx = None
-    if strategy in (QuantizationStrategy.GROUP, QuantizationStrategy.BLOCK):
+    if strategy in _GROUPED + (QuantizationStrategy.BLOCK,):
         divisor = quant_args.group_size if strategy != QuantizationStrategy.BLOCK else quant_args.block_structure[1]
         g_idx = torch.arange(cols, device=dev, dtype=torch.int) // divisor
         if actorder == ActivationOrdering.WEIGHT:
@@ -279,7 +299,7 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
                                             None if quant_args.symmetric else zero_point.to(torch.float32),
                                             strategy.value, g_idx, qmin, qmax,
                                             dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize,
-                                            block_h=bh)
+                                            block_h=bh, qtype=qtype, global_scale=global_scale)
     w_out, codes_out = ops.gptq_store_weight_batched(w_work, invperm, weights.dtype, codes)
     loss_ok = torch.stack([torch.sum(losses, dim=1), (prep.status == 0).float()]).cpu()  # the one sync
     loss, ok = loss_ok[0], loss_ok[1] > 0
@@ -292,7 +312,8 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
             sb, zb = sb.reshape(-1), zb.reshape(-1)
         out.append(GPTQResult(loss=float(loss[b]), weight=w_out[b], scale=sb, zero_point=zb,
                               g_idx=None if g_idx is None else (g_idx[b] if g_idx.dim() == 2 else g_idx),
-                              perm=None if perm is None else perm[b], codes=codes_out[b], hinv_ok=bool(ok[b])))
+                              perm=None if perm is None else perm[b], codes=codes_out[b], hinv_ok=bool(ok[b]),
+                              global_scale=None if global_scale is None else global_scale[b:b + 1]))
     return out
 
 
@@ -306,6 +327,8 @@ def quantize_weight(module: torch.nn.Module, quant_args: QuantizationArgs, hessi
         "weight_scale": res.scale.to(dtype=final_dtype),
         "weight_zero_point": res.zero_point.to(dtype=quant_args.zp_dtype),
     }
+    if res.global_scale is not None:
+        q["weight_global_scale"] = res.global_scale.to(dtype=final_dtype)
     actorder = quant_args.actorder
     if actorder == ActivationOrdering.GROUP and quant_args.strategy in (QuantizationStrategy.GROUP,
                                                                         QuantizationStrategy.TENSOR_GROUP):

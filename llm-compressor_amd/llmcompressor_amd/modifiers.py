@@ -284,6 +284,8 @@ class GPTQModifier(QuantizationModifier, _SharedHessians):
             module.weight.data.copy_(res.weight)
             update = {"weight_scale": res.scale.to(module.weight.dtype),
                       "weight_zero_point": res.zero_point.to(qa.zp_dtype)}
+            if res.global_scale is not None:
+                update["weight_global_scale"] = res.global_scale.to(module.weight.dtype)
             if qa.actorder == ActivationOrdering.GROUP:
                 update["weight_g_idx"] = res.g_idx[torch.argsort(res.perm)]
             for k, v in update.items():

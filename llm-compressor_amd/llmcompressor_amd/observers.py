@@ -121,7 +121,13 @@ class Observer(torch.nn.Module):
             zp = torch.zeros(scale.shape, dtype=a.zp_dtype, device=scale.device)
             out = {"scale": scale.to(torch.bfloat16), "zero_point": zp, "global_scale": None}
         elif a.strategy == QuantizationStrategy.TENSOR_GROUP:
-            raise NotImplementedError("tensor_group (NVFP4 global scale) is not provided by this build")
+            # NVFP4: the global scale from this observer's statistics (a fusion
+            # group of one module), fp8 group scales (observers/base.py:78-123)
+            if a.type != QuantizationType.FLOAT or a.num_bits != 4 or not a.symmetric:
+                raise NotImplementedError("tensor_group quantization is symmetric fp4 (NVFP4)")
+            gs, scale = ops.nvfp4_qparams(self.min_vals, self.max_vals, dt)
+            zp = torch.zeros(scale.shape, dtype=a.zp_dtype, device=scale.device)
+            out = {"scale": scale, "zero_point": zp, "global_scale": gs}
         else:
             qmin, qmax = a.q_range()
             scale, zp = ops.calculate_qparams(self.min_vals, self.max_vals, qmin, qmax, a.symmetric, dt)

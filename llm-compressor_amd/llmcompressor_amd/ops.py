@@ -173,30 +173,27 @@ STRATEGY_CODE = {"tensor": L.TENSOR, "channel": L.CHANNEL, "group": L.GROUP, "te
                  "block": L.BLOCK, "token": L.TOKEN}
 
 
+QTYPE = {"int": L.QTYPE_INT, "fp8": L.QTYPE_FP8_E4M3, "fp4": L.QTYPE_FP4_E2M1}
+
+
 def gptq_sweep_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.Tensor, zero_point, strategy: str,
                 g_idx: torch.Tensor | None, qmin: float, qmax: float, dequant_bf16: bool,
-                blocksize: int = 128, block_h: int = 1):
-    """In-place GPTQ column sweep.  Returns (codes int8 [rows, cols], losses fp32 [rows])."""
+                blocksize: int = 128, block_h: int = 1, qtype: str = "int",
+                global_scale: torch.Tensor | None = None):
+    """In-place GPTQ column sweep.  Returns (codes int8 [rows, cols], losses
+    fp32 [rows]); ``qtype`` int / fp8 / fp4 (codes: integers, e4m3 bits, e2m1
+    codes), ``global_scale`` (fp32 [1]) divides the scales (tensor groups)."""
     L.require_gpu(w_work, hinv, scale)
     rows, cols = w_work.shape
-    dev = w_work.device
     if hinv.shape != (cols, cols) or hinv.dtype != torch.float32:
         raise ValueError(f"hinv must be fp32 [{cols}, {cols}], got {tuple(hinv.shape)} {hinv.dtype}")
-    hinv = hinv.contiguous()   # row-major (torch.linalg.cholesky(upper=True) returns a transposed view)
     s = scale.to(torch.float32).contiguous()
     if s.dim() == 1:
         s = s.reshape(-1, 1)
     z = None if zero_point is None else zero_point.to(torch.float32).reshape(s.shape).contiguous()
-    gi = None if g_idx is None else g_idx.to(torch.int32).contiguous()
-    codes = torch.empty((rows, cols), dtype=torch.int8, device=dev)
-    losses = torch.zeros(rows, dtype=torch.float32, device=dev)
-    lib = L.lib()
-    ws = _ws(lib.mi355q_gptq_sweep_workspace_size(rows, cols, blocksize), dev)
-    L.check(lib.mi355q_gptq_sweep(w_work.data_ptr(), rows, cols, hinv.data_ptr(), s.data_ptr(), L.ptr(z),
-                                  s.stride(0), L.ptr(gi), STRATEGY_CODE[strategy], block_h, C.c_float(qmin),
-                                  C.c_float(qmax), 1 if dequant_bf16 else 0, blocksize, codes.data_ptr(),
-                                  losses.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_of(w_work)))
-    return codes, losses
+    return gptq_sweep_batched_(w_work.unsqueeze(0), hinv.unsqueeze(0), s.unsqueeze(0),
+                               None if z is None else z.unsqueeze(0), strategy, g_idx, qmin, qmax, dequant_bf16,
+                               blocksize, block_h, qtype, global_scale, _unbatch=True)
 
 
 def gptq_store_weight(w_work: torch.Tensor, invperm, out_dtype: torch.dtype, codes=None):
@@ -255,9 +252,11 @@ def gptq_load_weight_batched(w: torch.Tensor, perm=None, dead=None) -> torch.Ten
 
 def gptq_sweep_batched_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.Tensor, zero_point, strategy: str,
                         g_idx: torch.Tensor | None, qmin: float, qmax: float, dequant_bf16: bool,
-                        blocksize: int = 128, block_h: int = 1):
+                        blocksize: int = 128, block_h: int = 1, qtype: str = "int",
+                        global_scale: torch.Tensor | None = None, _unbatch: bool = False):
     """``gptq_sweep_`` over a batch: w_work [B, rows, cols], hinv [B, cols, cols],
-    scale / zero_point [B, rows or 1, groups], g_idx [B, cols] or [cols] (shared)."""
+    scale / zero_point [B, rows or 1, groups], g_idx [B, cols] or [cols] (shared),
+    global_scale [B] (or one value for all)."""
     L.require_gpu(w_work, hinv, scale)
     B, rows, cols = w_work.shape
     dev = w_work.device
@@ -268,15 +267,21 @@ def gptq_sweep_batched_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.T
     s = scale.to(torch.float32).reshape(B, -1, scale.shape[-1] if scale.dim() == 3 else 1).contiguous()
     z = None if zero_point is None else zero_point.to(torch.float32).reshape(s.shape).contiguous()
     gi = None if g_idx is None else g_idx.to(torch.int32).contiguous()
+    gs = None
+    if global_scale is not None:
+        gs = global_scale.to(device=dev, dtype=torch.float32).reshape(-1)
+        gs = (gs.expand(B) if gs.numel() == 1 else gs).contiguous()
     codes = torch.empty((B, rows, cols), dtype=torch.int8, device=dev)
     losses = torch.zeros((B, rows), dtype=torch.float32, device=dev)
     lib = L.lib()
     ws = _ws(lib.mi355q_gptq_sweep_workspace_size(rows, cols, blocksize) * B, dev)
-    L.check(lib.mi355q_gptq_sweep_batched(
+    L.check(lib.mi355q_gptq_sweep_typed_batched(
         w_work.data_ptr(), rows, cols, B, hinv.data_ptr(), hinv.stride(0), s.data_ptr(), L.ptr(z), s.stride(1),
         s.stride(0), L.ptr(gi), 0 if gi is None or gi.dim() == 1 else gi.stride(0), STRATEGY_CODE[strategy],
-        block_h, C.c_float(qmin), C.c_float(qmax), 1 if dequant_bf16 else 0, blocksize, codes.data_ptr(),
-        losses.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_of(w_work)))
+        block_h, QTYPE[qtype], C.c_float(qmin), C.c_float(qmax), L.ptr(gs), 1 if dequant_bf16 else 0, blocksize,
+        codes.data_ptr(), losses.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_of(w_work)))
+    if _unbatch:
+        return codes[0], losses[0]
     return codes, losses
 
 
@@ -354,6 +359,19 @@ def mx_scales(mn: torch.Tensor, mx: torch.Tensor, rule: str = "ct"):
     L.call("mi355q_mx_scales", mn.data_ptr(), mx.data_ptr(), mn.numel(), MX_RULES[rule], e8.data_ptr(),
            sc.data_ptr(), L.stream_of(mn))
     return e8, sc
+
+
+def nvfp4_qparams(mn: torch.Tensor, mx: torch.Tensor, stats_dtype: torch.dtype):
+    """NVFP4 tensor-group qparams from group min / max statistics: (global
+    scale fp32 [1], group scales as float8_e4m3fn shaped like ``mn``)."""
+    L.require_gpu(mn, mx)
+    mn = mn.to(torch.float32).contiguous()
+    mx = mx.to(torch.float32).contiguous()
+    gs = torch.empty(1, dtype=torch.float32, device=mn.device)
+    bits = torch.empty(mn.shape, dtype=torch.uint8, device=mn.device)
+    L.call("mi355q_nvfp4_qparams", mn.data_ptr(), mx.data_ptr(), mn.numel(),
+           L.BF16 if stats_dtype == torch.bfloat16 else L.F32, gs.data_ptr(), None, bits.data_ptr(), L.stream_of(mn))
+    return gs, bits.view(torch.float8_e4m3fn)
 
 
 # ---------------------------------------------------------------- quantize / pack

@@ -142,6 +142,21 @@ PRESET_SCHEMES = {
         weights=QuantizationArgs(num_bits=8, type="float", symmetric=True, strategy="channel"),
         input_activations=QuantizationArgs(num_bits=8, type="float", symmetric=True, strategy="token",
                                            dynamic=True)),
+    "FP8": lambda: QuantizationScheme(
+        weights=QuantizationArgs(num_bits=8, type="float", symmetric=True, strategy="tensor"),
+        input_activations=QuantizationArgs(num_bits=8, type="float", symmetric=True, strategy="tensor")),
+    "NVFP4A16": lambda: QuantizationScheme(
+        weights=QuantizationArgs(num_bits=4, type="float", symmetric=True, strategy="tensor_group", group_size=16,
+                                 scale_dtype=torch.float8_e4m3fn, zp_dtype=torch.float8_e4m3fn)),
+    "NVFP4": lambda: QuantizationScheme(
+        weights=QuantizationArgs(num_bits=4, type="float", symmetric=True, strategy="tensor_group", group_size=16,
+                                 scale_dtype=torch.float8_e4m3fn, zp_dtype=torch.float8_e4m3fn),
+        input_activations=QuantizationArgs(num_bits=4, type="float", symmetric=True, strategy="tensor_group",
+                                           group_size=16, dynamic="local", scale_dtype=torch.float8_e4m3fn,
+                                           zp_dtype=torch.float8_e4m3fn)),
+    "MXFP4A16": lambda: QuantizationScheme(
+        weights=QuantizationArgs(num_bits=4, type="float", symmetric=True, strategy="group", group_size=32,
+                                 scale_dtype=torch.uint8, zp_dtype=torch.uint8)),
     "MXFP4": lambda: QuantizationScheme(
         weights=QuantizationArgs(num_bits=4, type="float", symmetric=True, strategy="group", group_size=32,
                                  scale_dtype=torch.uint8, zp_dtype=torch.uint8),

@@ -97,6 +97,32 @@ def fake_quantize(x, scale, zero_point, args: OArgs, global_scale=None,
     return dequantize(q, scale, zero_point, global_scale, dequant_in_scale_dtype)
 
 
+def float_codes(wq: torch.Tensor, s_eff: torch.Tensor, args: OArgs) -> torch.Tensor:
+    """Codes of fake-quantised float values ``wq`` (int32): float8_e4m3fn bit
+    patterns, or e2m1 codes sign << 3 | index in ``FP4_GRID``.  ``s_eff`` is
+    the effective scale per element (scale / global_scale); the grid value is
+    recovered as the nearest point to wq / s_eff (the dequantisation rounding
+    is far below the grid spacing)."""
+    q = wq.to(torch.float32) / s_eff.to(torch.float32)
+    sign = torch.signbit(q).to(torch.int32)
+    if args.num_bits == 8:
+        return q.to(torch.float8_e4m3fn).view(torch.uint8).to(torch.int32)
+    grid = torch.tensor(FP4_GRID, dtype=torch.float32)
+    idx = torch.argmin((q.abs().unsqueeze(-1) - grid).abs(), dim=-1).to(torch.int32)
+    return (sign << 3) | idx
+
+
+def signed_grid_index(codes: torch.Tensor, args: OArgs) -> torch.Tensor:
+    """Float codes as signed positions on the type's grid (monotonic in the
+    value), so one code step is one grid step."""
+    c = codes.to(torch.int32) & 0xFF
+    if args.num_bits == 8:
+        mag, sign = c & 0x7F, (c >> 7) & 1
+    else:
+        mag, sign = c & 0x7, (c >> 3) & 1
+    return torch.where(sign == 1, -mag, mag)
+
+
 def expand_qparams(t: torch.Tensor, shape, args: OArgs) -> torch.Tensor:
     """Expand a [rows, n] qparam tensor to per-element [rows, cols] for ``args.strategy``.
 

@@ -27,7 +27,7 @@ import math
 
 import torch
 
-from .fake_quant import fake_quantize
+from .fake_quant import fake_quantize, float_codes
 from .observers import OMinMax
 from .qargs import OArgs
 
@@ -176,6 +176,7 @@ def quantize_weight(weight: torch.Tensor, args: OArgs, hessian: torch.Tensor,
     if actorder:
         invperm = torch.argsort(perm)
         W = W[:, invperm]
+    W32 = W
     W = W.reshape(final_shape).to(final_dtype)
     loss = torch.sum(losses).item()
     out = {
@@ -189,13 +190,15 @@ def quantize_weight(weight: torch.Tensor, args: OArgs, hessian: torch.Tensor,
         out["weight_g_idx"] = g_idx[invperm]
     if not return_codes:
         return loss, out
-    codes = weight_codes(W, scale, zero_point, args, g_idx, perm, invperm)
+    codes = weight_codes(W32 if args.type == "float" else W, scale, zero_point, args, g_idx, perm, invperm,
+                         global_scale)
     return loss, out, {"codes": codes, "hinv": Hinv, "ok": ok, "perm": perm,
                        "scale_used": scale, "losses": losses}
 
 
-def weight_codes(Wq, scale, zero_point, args: OArgs, g_idx, perm, invperm):
-    """Integer codes of the fake-quantised weight, original column order."""
+def weight_codes(Wq, scale, zero_point, args: OArgs, g_idx, perm, invperm, global_scale=None):
+    """Codes of the fake-quantised weight, original column order: integers,
+    or for float types ``fake_quant.float_codes`` of the fp32 values."""
     rows, cols = Wq.shape
     if args.strategy == "tensor":
         s = scale.float().reshape(1, 1).expand(rows, cols)
@@ -212,4 +215,7 @@ def weight_codes(Wq, scale, zero_point, args: OArgs, g_idx, perm, invperm):
         else:
             s = scale.float()[:, gi.long()]
             z = zero_point.float()[:, gi.long()]
+    if args.type == "float":
+        s_eff = s if global_scale is None else s / global_scale.to(torch.float32)
+        return float_codes(Wq, s_eff, args)
     return torch.round(Wq.float() / s + z).to(torch.int32)

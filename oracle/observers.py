@@ -219,7 +219,11 @@ def strict_symmetric_qparams(min_vals, max_vals, args: OArgs):
 
 
 def generate_gparam(min_v, max_v):
-    """CT ``generate_gparam``: fp8_max * fp4_max / absmax, in the stats dtype."""
+    """CT ``generate_gparam``: fp8_max * fp4_max / absmax, in the stats dtype.
+
+    A Python scalar over a tensor is ``Tensor.__rtruediv__``, which torch
+    evaluates as ``reciprocal(absmax) * scalar`` with both results rounded to
+    the tensor's dtype (bf16 for bf16 statistics), not as one division."""
     mn = torch.min(min_v, torch.zeros_like(min_v))
     mx = torch.max(max_v, torch.zeros_like(max_v))
     mvp = torch.max(torch.abs(mn), torch.abs(mx))

@@ -20,6 +20,12 @@ oracle, then again with one of these changes, and reports the code spread:
 
 Usage: ``python tests/gptq_code_spread.py [seeds...]`` (about a minute per
 seed on 8 cores).
+
+``--formats [seeds...]`` runs the second study: for each weight format
+(int4 g128, int8 channel, FP8 channel / tensor, NVFP4, MXFP4) one 384 x 1024
+layer with a Hessian from 4096 tokens, quantized by the oracle on its own
+fp32 Hessian and on the same Hessian summed in fp64 and rounded to fp32.
+Float codes compare as signed grid positions.
 """
 from __future__ import annotations
 
@@ -112,5 +118,34 @@ def main(seeds):
     return out
 
 
+def formats(seeds):
+    from oracle.fake_quant import signed_grid_index
+    e4 = torch.float8_e4m3fn
+    cases = {"int4-g128": OArgs(num_bits=4, strategy="group", group_size=128, actorder="weight"),
+             "int8-channel": OArgs(num_bits=8, strategy="channel", actorder="weight"),
+             "fp8-channel": OArgs(num_bits=8, type="float", strategy="channel", actorder="weight"),
+             "fp8-tensor": OArgs(num_bits=8, type="float", strategy="tensor"),
+             "nvfp4": OArgs(num_bits=4, type="float", strategy="tensor_group", group_size=16, scale_dtype=e4),
+             "mxfp4": OArgs(num_bits=4, type="float", strategy="group", group_size=32, is_mx=True)}
+    for seed in seeds:
+        W = workloads.gptq_weight(384, 1024, seed=seed)
+        X = workloads.heavy_tailed_activations((2, 2048, 1024), seed=seed + 1)
+        H, n = og.accumulate_hessian(X, og.make_empty_hessian(1024), torch.zeros(()))
+        H = og.normalise_hessian(H, n)
+        Xd = X.reshape(-1, 1024).double() * 2 ** 0.5
+        H64 = ((Xd.t() @ Xd) / float(n)).float()
+        row = {}
+        for name, oa in cases.items():
+            a = og.quantize_weight(W, oa, H, return_codes=True)[2]["codes"]
+            b = og.quantize_weight(W, oa, H64, return_codes=True)[2]["codes"]
+            if oa.type == "float":
+                a, b = signed_grid_index(a, oa), signed_grid_index(b, oa)
+            row[name] = spread(b, a)
+        print(json.dumps({"seed": seed, **row}), flush=True)
+
+
 if __name__ == "__main__":
-    main([int(s) for s in sys.argv[1:]] or [0, 1, 2, 3])
+    if sys.argv[1:2] == ["--formats"]:
+        formats([int(s) for s in sys.argv[2:]] or [41, 43, 45])
+    else:
+        main([int(s) for s in sys.argv[1:]] or [0, 1, 2, 3])

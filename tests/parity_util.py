@@ -24,10 +24,15 @@ def code_agreement(a: torch.Tensor, b: torch.Tensor) -> dict:
             "frac_beyond_1": (d > 1).float().mean().item()}
 
 
-def code_bar(st: dict, rows: int) -> bool:
+def code_bar(st: dict, rows: int, rows_frac: float = 0.01) -> bool:
     """The end-to-end GPTQ code bar: >= 99.9 % of codes agree, every row's
-    first divergence is a one-code flip, and at most 1 % of the rows diverge
-    at all (codes after a row's first flip may differ by more than one, as
-    they do between two runs of the oracle itself under a different BLAS
-    thread count)."""
-    return st["agree"] >= 0.999 and st["first_divergence_max"] <= 1 and st["rows_diverged"] <= max(1, rows // 100)
+    first divergence is a one-code flip, and at most ``rows_frac`` of the rows
+    (1 %) diverge at all (codes after a row's first flip may differ by more
+    than one, as they do between two runs of the oracle itself under a
+    different BLAS thread count).  FP8 weights take 2 %: e4m3's grid step is
+    relative to each value rather than to the group's range, so more values
+    sit near a boundary; the oracle against itself with only the Hessian's
+    fp32 summation changed diverges in up to 3 of 384 rows at 384 x 1024
+    (``gptq_code_spread.py --formats``), where int4 diverges in at most one."""
+    return (st["agree"] >= 0.999 and st["first_divergence_max"] <= 1
+            and st["rows_diverged"] <= max(1, int(rows * rows_frac)))

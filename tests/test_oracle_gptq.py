@@ -154,3 +154,46 @@ def test_dead_columns_are_zeroed():
     args = OArgs(num_bits=4, strategy="channel")
     _, q, ex = og.quantize_weight(W, args, H, return_codes=True)
     assert torch.all(q["weight"][:, 3] == 0) and torch.all(ex["codes"][:, 3] == 0)
+
+
+FLOAT_ARGS = [OArgs(num_bits=4, type="float", strategy="tensor_group", group_size=16, scale_dtype=torch.float8_e4m3fn),
+              OArgs(num_bits=4, type="float", strategy="group", group_size=32, is_mx=True),
+              OArgs(num_bits=8, type="float", strategy="channel"),
+              OArgs(num_bits=8, type="float", strategy="tensor")]
+
+
+@pytest.mark.parametrize("args", FLOAT_ARGS, ids=["nvfp4", "mxfp4", "fp8-channel", "fp8-tensor"])
+def test_float_diagonal_hessian_is_round_to_nearest(args):
+    """Float weights (gptq_quantize.py:215-247 with global_scale): a diagonal
+    Hessian gives GPTQ == CT fake_quantize of the fp32 weight with the same
+    qparams, and the codes dequantise back to the weight."""
+    from oracle import fake_quant as ofq
+    W = _weight(24, 128, 9)
+    W[0, :5] = torch.tensor([0.0, -0.0, 1e-6, -1e-6, 0.3], dtype=torch.bfloat16)
+    H = torch.diag(torch.linspace(1.0, 4.0, 128))
+    _, out, ex = og.quantize_weight(W, args, H, return_codes=True)
+    obs = OMinMax("memoryless_minmax", "weight", args)
+    qp = obs(W).get_qparams()
+    s = ofq.expand_qparams(qp["scale"], W.shape, args)
+    rtn = ofq.fake_quantize(W.float(), s, None, args, qp["global_scale"]).to(W.dtype)
+    assert torch.equal(out["weight"], rtn)
+    # codes: grid value x effective scale = the dequantised weight (bf16)
+    s_eff = s.float() if qp["global_scale"] is None else s.float() / qp["global_scale"]
+    gi = ofq.signed_grid_index(ex["codes"], args)
+    if args.num_bits == 8:
+        vals = (ex["codes"] & 0xFF).to(torch.uint8).view(torch.float8_e4m3fn).float()
+    else:
+        grid = torch.tensor(ofq.FP4_GRID)
+        vals = grid[(ex["codes"] & 7).long()] * torch.where((ex["codes"] >> 3) & 1 == 1, -1.0, 1.0)
+    assert torch.equal((vals * s_eff).to(W.dtype), out["weight"])
+    assert int(gi.abs().max()) <= (126 if args.num_bits == 8 else 7)
+
+
+def test_nvfp4_global_scale_in_outputs():
+    """weight_global_scale (gptq_quantize.py:292-293) and fp8 group scales."""
+    W = _weight(16, 64, 10)
+    args = FLOAT_ARGS[0]
+    _, out, ex = og.quantize_weight(W, args, _spd(64, 11), return_codes=True)
+    gs = out["weight_global_scale"]
+    assert gs.dtype == W.dtype and gs.numel() == 1
+    assert float(gs) == pytest.approx(448 * 6 / float(W.abs().max()), rel=1e-2)
