@@ -426,7 +426,7 @@ def bench_moe(a):
     rows, offsets, _ = moe.route_tokens(idx.to(dev), E)
     counts = [offsets[e + 1] - offsets[e] for e in range(E)]
     inter_x = moe.expert_intermediate(hs, rows, offsets, gate, up)   # calibration forward (untimed)
-    ident = torch.arange(inter_x.shape[0], device=dev, dtype=torch.int32)
+    off_dev = torch.tensor(offsets, dtype=torch.int64, device=dev)
     qa = QuantizationArgs(num_bits=4, type="int", symmetric=True, strategy="group", group_size=128)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
 
@@ -435,8 +435,8 @@ def bench_moe(a):
         Hd = torch.zeros(E, inter, inter, device=dev)
         ns = torch.zeros(E, device=dev)
         ev[0].record()
-        moe.accumulate_expert_hessians(hs, rows, offsets, Hgu, ns)
-        moe.accumulate_expert_hessians(inter_x, ident, offsets, Hd, ns.clone())
+        moe.accumulate_expert_hessians(hs, rows, off_dev, Hgu, ns)
+        moe.accumulate_expert_hessians(inter_x, None, off_dev, Hd, ns.clone())
         ev[1].record()
         # all experts of one projection solved together (one launch per step);
         # gate and up share their input, hence their Hessian and its Cholesky chain

@@ -101,22 +101,24 @@ int mi355q_hessian_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_tokens,
                         size_t workspace_bytes, void* stream);
 
 /* Grouped (MoE) variant: expert e accumulates the rows
- * x[rows_dev[k]] for k in [offsets_host[e], offsets_host[e+1]) into
- * h_dev + e * h_stride (each d x d, leading dimension d, upper triangle).
- * Replaces the per-expert accumulate_hessian calls that
- * modeling/moe/linear_experts.py:244-277 triggers with routed tokens.
- */
-size_t mi355q_hessian_grouped_workspace_size(const int64_t* offsets_host, int n_experts, int64_t d);
-int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, int64_t d,
-                                     const int32_t* rows_dev, const int64_t* offsets_host,
-                                     int n_experts, float* h_dev, int64_t h_stride, float alpha,
-                                     void* workspace_dev, size_t workspace_bytes, void* stream);
-
-/* mi355q_hessian_grouped_syrk_bf16 for bf16 or fp16 hidden states (dtype). */
-int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype, int64_t ldx, int64_t d,
-                                const int32_t* rows_dev, const int64_t* offsets_host, int n_experts,
-                                float* h_dev, int64_t h_stride, float alpha, void* workspace_dev,
-                                size_t workspace_bytes, void* stream);
+ * x[rows_dev[k]] for k in [offsets_dev[e], offsets_dev[e+1]) into
+ * h_dev + e * h_stride (each d x d, leading dimension d, upper triangle):
+ * H_e += alpha * X_e^T X_e.  Replaces the per-expert accumulate_hessian
+ * calls that modeling/moe/linear_experts.py:244-277 triggers with routed
+ * tokens.  x is [n_x, d] (ldx), bf16 or fp16; rows_dev (n_rows int32
+ * indices into x) may be NULL when x's rows are already grouped (row k of
+ * expert e is x[k]; then n_rows <= n_x).  offsets_dev is int64 [n_experts+1]
+ * in device memory, non-decreasing with offsets[n_experts] <= n_rows: the
+ * work table is built on the device, so the call never waits for the host
+ * (offsets outside that contract are clamped and row indices outside
+ * [0, n_x) are clamped; nothing is read or written out of bounds).
+ * Workspace: mi355q_hessian_grouped_syrk_workspace_size(n_rows, n_experts,
+ * d) bytes. */
+size_t mi355q_hessian_grouped_syrk_workspace_size(int64_t n_rows, int n_experts, int64_t d);
+int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_x, int64_t ldx, int64_t d,
+                                const int32_t* rows_dev, int64_t n_rows, const int64_t* offsets_dev,
+                                int n_experts, float* h_dev, int64_t h_stride, float alpha,
+                                void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /* Mirror the upper triangle into the lower one (full symmetric matrix). */
 int mi355q_symmetrize_upper(float* h_dev, int64_t d, int64_t ldh, void* stream);

@@ -8,29 +8,40 @@
 // (v_mfma_f32_32x32x16_bf16).
 //
 // Two tile kernels share the work decomposition below:
-//  * syrk_stream_kernel (dense X, d >= 512): 256 x 256 tiles streamed
-//    global -> LDS by LDS-DMA in token-major layout and read back with the
-//    transposing LDS load (details at the kernel);
-//  * syrk_bf16_kernel (row-gathered X for per-expert Hessians, and d < 512):
-//    each thread loads an 8-token x 8-feature block with eight 16-byte loads
-//    and transposes it in registers (v_perm) before the LDS store; the
-//    transposed stores map lane -> (feature block, token block) with the
-//    token block fastest, which keeps 16 consecutive lanes on distinct LDS
-//    banks (row stride 144 B = 9 x 16 B).
+//  * syrk_stream_kernel (d >= 512, and every grouped call): 256 x 256 tiles
+//    streamed global -> LDS by LDS-DMA in token-major layout and read back
+//    with the transposing LDS load (details at the kernel); for per-expert
+//    Hessians the DMA gathers the routed rows itself;
+//  * syrk_bf16_kernel (dense X with d < 512): each thread loads an 8-token
+//    x 8-feature block with eight 16-byte loads and transposes it in
+//    registers (v_perm) before the LDS store; the transposed stores map
+//    lane -> (feature block, token block) with the token block fastest,
+//    which keeps 16 consecutive lanes on distinct LDS banks (row stride
+//    144 B = 9 x 16 B).
 // Tiles are TM x TM (TM = 256 for d >= 512, else 128).  syrk_bf16_kernel runs
 // them on a 2 x 2 grid of waves, each owning a (TM/2)^2 block of 32 x 32 MFMA
 // tiles; the streaming kernel on a 2 x 4 grid of 8 waves (two per SIMD, so
 // one wave's waits are covered by the other's MFMAs), each owning 128 x 64.
 // syrk_bf16_kernel writes partial tiles in its fragment order (one 16-float
 // run per thread and block); the streaming kernel in 1 KB chunks of one
-// float4 per lane, which its own reduction reads back coalesced.
+// float4 per lane, which its own reduction reads back coalesced, or, for a
+// single split, adds its tile to H through LDS one 1 KB row at a time.
 //
-// Work decomposition: a work item is (matrix e, upper tile t, token split s).
+// Dense work decomposition: a work item is (upper tile t, token split s).
 // Token splits are assigned by blockIdx % S, and workgroups are dispatched
 // round-robin over the 8 XCDs, so with S = 8 each XCD streams only its own
 // eighth of X through its L2.  With S > 1 each item writes its partial tile
 // to the workspace and a second kernel sums the partials in split order and
 // updates H, so results are deterministic.
+//
+// Grouped (per-expert) decomposition: each expert's routed tokens are cut
+// into chunks of kChunkTokens; a work item is (chunk, upper tile).  The
+// chunk table is built on the device from the expert offsets, so a call
+// never waits for the host.  The first chunk of an expert adds its tile to
+// H directly; later chunks write partial slots that a second kernel adds in
+// chunk order afterwards (deterministic).  Items are laid out chunk-major
+// and each XCD takes a contiguous eighth of them, so the tiles of one chunk
+// run on one XCD and share its rows through that XCD's L2.
 #include <vector>
 
 #include "common.h"
@@ -50,14 +61,19 @@ struct Matrix {            // one Hessian being accumulated
   float* h;                // d x d, leading dimension ldh
 };
 
-struct Item {              // grouped work item
-  int e, t, s, S;
-  int64_t slot;            // partial slot (>= 0 when S > 1)
+constexpr int kChunkTokens = 4096;  // tokens per grouped work chunk (its row indices fit in LDS)
+
+struct GChunk {            // one chunk of one expert's tokens (device-built table)
+  int e;                   // expert
+  int count;               // tokens, 1 .. kChunkTokens
+  int64_t tok_begin;       // first token: index into rows[] (or into x without rows)
+  int64_t sbase;           // partial slot of tile 0 (tile t -> sbase + t); -1: add to H directly
 };
 
-struct ReduceItem {        // one tile to finish from S partial slots
-  int e, t, S;
-  int64_t slot0;           // slots slot0 .. slot0 + S - 1
+struct GReduce {           // the later chunks of one expert, added to H in chunk order
+  int e;
+  int nslots;              // chunks after the first
+  int64_t sbase;           // slot of tile 0 of the second chunk; chunk k at sbase + (k - 1) T
 };
 
 struct SyrkParams {
@@ -68,15 +84,20 @@ struct SyrkParams {
   int nt;                  // tiles per edge
   float alpha;
   float beta;              // H = beta * H + alpha * X^T X (beta == 1: H += ...)
-  const int32_t* rows;     // optional token -> row indirection
-  Matrix single;           // single-matrix mode
+  Matrix single;           // dense mode
   int S;
   // dense tail: tiles t >= tail_start run as tail_f parts per split (see
   // plan_dense); tail_start = number of tiles when there is no tail
   int tail_start, tail_f;
-  const Item* items;       // grouped mode (items != nullptr)
-  const Matrix* mats;
   float* ws;               // partial tiles
+  // grouped mode
+  const int32_t* rows;     // token -> row of x (nullptr: x rows are already grouped)
+  int64_t n_x;             // rows of x (gathered indices are clamped into [0, n_x))
+  const GChunk* chunks;
+  const int* gcounts;      // [0] chunks, [1] reduce items (written by the planner)
+  int T;                   // upper tiles per matrix
+  float* h0;               // H of expert 0 (leading dimension d)
+  int64_t h_stride;
 };
 
 // The t-th tile on or above the diagonal, in super-block order: super-blocks
@@ -143,34 +164,21 @@ __device__ __forceinline__ f32x16_t mfma16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
 // out-of-range tokens / features read a clamped in-range address, and the
 // returned mask (bit tt = token tt valid) zeroes them when the block is
 // stored, so the eight loads issue back to back and nothing waits for them
-// before the MFMAs of the current stage.  Dense X is addressed as a
-// wave-uniform stage base plus a 32-bit lane offset; the gathered layout (G)
-// fetches its eight row indices first.
-template <bool G>
+// before the MFMAs of the current stage.  X is addressed as a wave-uniform
+// stage base plus a 32-bit lane offset.
 __device__ __forceinline__ unsigned load_block(const SyrkParams& p, int64_t stage0, int lt0, int64_t tok_end,
                                                int64_t row_base, int64_t f, u32x4_t r[8]) {
   const bool fin = f < p.d;
   const int64_t fc = fin ? f : 0;
   const int64_t rem = tok_end - stage0;           // >= 1 for a stage in range
   const int lim = rem < BK ? (int)rem : BK;
-  if (!G) {
-    const char* base = reinterpret_cast<const char*>(p.x + (row_base + stage0) * p.ldx);
+  const char* base = reinterpret_cast<const char*>(p.x + (row_base + stage0) * p.ldx);
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      const int lt = lt0 + tt;
-      const int ltc = lt < lim ? lt : lim - 1;
-      const uint32_t off = (uint32_t)(ltc * p.ldx + fc) * 2u;
-      r[tt] = *reinterpret_cast<const u32x4_t*>(base + off);
-    }
-  } else {
-    int64_t row[8];
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      const int lt = lt0 + tt;
-      row[tt] = p.rows[row_base + stage0 + (lt < lim ? lt : lim - 1)];
-    }
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt) r[tt] = *reinterpret_cast<const u32x4_t*>(p.x + row[tt] * p.ldx + fc);
+  for (int tt = 0; tt < 8; ++tt) {
+    const int lt = lt0 + tt;
+    const int ltc = lt < lim ? lt : lim - 1;
+    const uint32_t off = (uint32_t)(ltc * p.ldx + fc) * 2u;
+    r[tt] = *reinterpret_cast<const u32x4_t*>(base + off);
   }
   const int nv = lim - lt0;
   return !fin || nv <= 0 ? 0u : (nv >= 8 ? 0xffu : (1u << nv) - 1u);
@@ -209,7 +217,7 @@ struct Cfg {
   static constexpr int TILE = TM * TM;
 };
 
-template <int TM, bool G, bool F16 = false>
+template <int TM, bool F16 = false>
 __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkParams p) {
   using C = Cfg<TM>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][C::OPLDS];
@@ -219,20 +227,11 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  int t, s, S;
-  int64_t slot = -1;
-  Matrix mat;
-  if (p.items) {
-    const Item it = p.items[blockIdx.x];
-    t = it.t; s = it.s; S = it.S; slot = it.slot;
-    mat = p.mats[it.e];
-  } else {
-    S = p.S;
-    s = blockIdx.x % S;
-    t = blockIdx.x / S;
-    mat = p.single;
-    slot = (S > 1) ? (int64_t)t * S + s : -1;
-  }
+  const int S = p.S;
+  const int s = blockIdx.x % S;
+  const int t = blockIdx.x / S;
+  const Matrix mat = p.single;
+  const int64_t slot = (S > 1) ? (int64_t)t * S + s : -1;
   int ti, tj;
   tile_coords(t, p.nt, ti, tj);
 
@@ -271,7 +270,7 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
   if (nst > 0) {
 #pragma unroll
     for (int b = 0; b < NL; ++b)
-      vmask[b] = load_block<G>(p, st_begin * BK, 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
+      vmask[b] = load_block(p, st_begin * BK, 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
 #pragma unroll
     for (int b = 0; b < NL; ++b) store_block(lds[0][op[b]], fbk[b], kbk[b], regs[b], vmask[b]);
   }
@@ -283,7 +282,7 @@ __global__ __launch_bounds__(NT, TM == 128 ? 2 : 1) void syrk_bf16_kernel(SyrkPa
     if (more) {
 #pragma unroll
       for (int b = 0; b < NL; ++b)
-        vmask[b] = load_block<G>(p, (st_begin + st + 1) * BK, 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
+        vmask[b] = load_block(p, (st_begin + st + 1) * BK, 8 * kbk[b], n, mat.row_begin, fbase[b], regs[b]);
     }
     const uint16_t* la = lds[buf][0];
     const uint16_t* lb = lds[buf][1];
@@ -377,39 +376,68 @@ __device__ __forceinline__ bf16x8_t tr_pair(const char* lds, int off0, int off1)
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <bool F16 = false>
+enum StreamMode { kDense = 0, kGrouped = 1, kGroupedGather = 2 };
+
+template <bool F16, int MODE>
 __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   constexpr int MB = 4, NBN = 2;  // 32 x 32 MFMA blocks per wave: 128 rows x 64 columns
   using C = Cfg<256>;
   constexpr int TM = 256;
-  __shared__ __attribute__((aligned(1024))) char a0[SOP], a1[SOP], a2[SOP], a3[SOP];
-  __shared__ __attribute__((aligned(1024))) char b0[SOP], b1[SOP], b2[SOP], b3[SOP];
+  // LDS ring: operand A in stages 0..3, then operand B; after the loop it
+  // holds half an fp32 tile for the direct update of H
+  __shared__ __attribute__((aligned(1024))) char ring[8 * SOP];
+  char* const a0 = ring;
+  char* const a1 = ring + SOP;
+  char* const a2 = ring + 2 * SOP;
+  char* const a3 = ring + 3 * SOP;
+  char* const b0 = ring + 4 * SOP;
+  char* const b1 = ring + 5 * SOP;
+  char* const b2 = ring + 6 * SOP;
+  char* const b3 = ring + 7 * SOP;
+  // row indices of a gathered chunk
+  __shared__ int ridx[MODE == kGroupedGather ? kChunkTokens : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave >> 2, wn = wave & 3;
 
-  // work item: tile t, token split s (and, for tail tiles, part `part` of
-  // tail_f equal pieces of that split), partial slot
-  const int S = p.S;
-  const int64_t nfull = (int64_t)p.tail_start * S;
-  int t, s, part = 0, nparts = 1;
+  // work item: tile t, token split s (and, for dense tail tiles, part `part`
+  // of tail_f equal pieces of that split), partial slot
+  int t, s = 0, part = 0, nparts = 1, S = 1;
   int64_t slot;
-  if ((int64_t)blockIdx.x < nfull) {
-    s = blockIdx.x % S;
-    t = blockIdx.x / S;
-    slot = (S > 1) ? (int64_t)t * S + s : -1;
+  Matrix mat;
+  if constexpr (MODE == kDense) {
+    S = p.S;
+    const int64_t nfull = (int64_t)p.tail_start * S;
+    if ((int64_t)blockIdx.x < nfull) {
+      s = blockIdx.x % S;
+      t = blockIdx.x / S;
+      slot = (S > 1) ? (int64_t)t * S + s : -1;
+    } else {
+      const int b = (int)(blockIdx.x - nfull);
+      s = b % S;
+      const int j = b / S;
+      t = p.tail_start + j / p.tail_f;
+      part = j % p.tail_f;
+      nparts = p.tail_f;
+      slot = nfull + ((int64_t)(t - p.tail_start) * S + s) * p.tail_f + part;
+    }
+    mat = p.single;
   } else {
-    const int b = (int)(blockIdx.x - nfull);
-    s = b % S;
-    const int j = b / S;
-    t = p.tail_start + j / p.tail_f;
-    part = j % p.tail_f;
-    nparts = p.tail_f;
-    slot = nfull + ((int64_t)(t - p.tail_start) * S + s) * p.tail_f + part;
+    // grouped: item i = chunk * T + t; XCD x (= blockIdx % 8) runs items
+    // [x per, (x + 1) per) in order; the grid covers the largest possible
+    // table and the workgroups past the built one return at once
+    const int N = p.gcounts[0] * p.T;
+    const int per = (N + 7) >> 3;
+    const int k = (int)(blockIdx.x >> 3);
+    const int i = (int)(blockIdx.x & 7u) * per + k;
+    if (k >= per || i >= N) return;
+    const GChunk c = p.chunks[i / p.T];
+    t = i % p.T;
+    mat = Matrix{c.tok_begin, c.count < kChunkTokens ? c.count : kChunkTokens, p.h0 + (int64_t)c.e * p.h_stride};
+    slot = c.sbase < 0 ? -1 : c.sbase + t;
   }
-  const Matrix mat = p.single;
   int ti, tj;
   tile_coords(t, p.nt, ti, tj);
 
@@ -427,6 +455,14 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     st_end = e2;
   }
   const int64_t nst = st_end > st_begin ? st_end - st_begin : 0;
+
+  if constexpr (MODE == kGroupedGather) {
+    for (int i = tid; i < (int)n; i += SNT) {
+      const int64_t r = p.rows[mat.row_begin + i];
+      ridx[i] = (int)(r < 0 ? 0 : (r >= p.n_x ? p.n_x - 1 : r));
+    }
+    __syncthreads();
+  }
 
   // DMA roles: wave w copies token rows 4 w .. 4 w + 3 of each operand, two
   // rows (1 KB) per instruction j; lane L fills LDS position L & 31 of row
@@ -448,9 +484,9 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   // apart and would wait for all DMA in flight); completion is tracked
   // explicitly with vmcnt before each barrier and after the loop.  Whole
   // stages use the scalar-base form (stage base in SGPRs + the lane's 32-bit
-  // offset); partial stages and edge tiles redirect lanes past n or d to a
-  // zero chunk with per-lane 64-bit addresses.  M0 (the LDS destination of
-  // the wave's 1 KB) is formed in scalar registers.
+  // offset); partial stages, edge tiles and gathered rows use per-lane 64-bit
+  // addresses, with lanes past n or d sent to a zero chunk.  M0 (the LDS
+  // destination of the wave's 1 KB) is formed in scalar registers.
   auto lds_u32 = [](const char* ptr) { return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)ptr); };
   const uint32_t wave_lds = (uint32_t)wave * 2048u;
   const uint32_t sa[4] = {lds_u32(a0) + wave_lds, lds_u32(a1) + wave_lds, lds_u32(a2) + wave_lds,
@@ -468,28 +504,60 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   const int64_t sbytes = (int64_t)SK * p.ldx * 2;  // bytes per stage
   // stages [0, nwhole) hold SK tokens
   const int64_t nwhole = (n - st_begin * SK) / SK;
-  auto issue = [&](int64_t stage, int slot) __attribute__((always_inline)) {
+  const bool fast_ok = MODE != kGroupedGather && !edge;
+  // Per-lane global addresses of the 4 DMAs of a stage (A0, B0, A1, B1):
+  // lanes past n or d read the zero chunk.
+  auto dma_addrs = [&](int64_t stage, const void** ad) __attribute__((always_inline)) {
     const int64_t sc = stage < nst ? stage : nst - 1;
-    const char* xs = xbase + sc * sbytes;
-    const char* xa = xs + fa0 * 2;
-    const char* xb = xs + fb0 * 2;
-    if (!edge && sc < nwhole) {
+    const int64_t t0 = (st_begin + sc) * SK;
+    if constexpr (MODE == kGroupedGather) {
+      const char* xg = reinterpret_cast<const char*>(p.x);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        dma_s(doff[j], xa, sa[slot] + 1024u * j);
-        dma_s(doff[j], xb, sb[slot] + 1024u * j);
-      }
-    } else {
-      // partial stage or edge tile: rows past n and chunks past d read zeros
-      const int64_t t0 = (st_begin + sc) * SK;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const bool rok = t0 + drow[j] < n;
+        const int lt = (int)t0 + drow[j];
+        const bool rok = lt < n;
+        const char* xr = xg + (int64_t)ridx[rok ? lt : 0] * p.ldx * 2 + (int64_t)dchunk[j] * 16;
         const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
         const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
-        dma_v(aok ? (const void*)(xa + doff[j]) : (const void*)kZeroChunk, sa[slot] + 1024u * j);
-        dma_v(bok ? (const void*)(xb + doff[j]) : (const void*)kZeroChunk, sb[slot] + 1024u * j);
+        ad[2 * j] = aok ? (const void*)(xr + fa0 * 2) : (const void*)kZeroChunk;
+        ad[2 * j + 1] = bok ? (const void*)(xr + fb0 * 2) : (const void*)kZeroChunk;
       }
+    } else {
+      const char* xs = xbase + sc * sbytes;
+      const char* xa = xs + fa0 * 2;
+      const char* xb = xs + fb0 * 2;
+      if (fast_ok && sc < nwhole) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          ad[2 * j] = xa + doff[j];
+          ad[2 * j + 1] = xb + doff[j];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const bool rok = t0 + drow[j] < n;
+          const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
+          const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
+          ad[2 * j] = aok ? (const void*)(xa + doff[j]) : (const void*)kZeroChunk;
+          ad[2 * j + 1] = bok ? (const void*)(xb + doff[j]) : (const void*)kZeroChunk;
+        }
+      }
+    }
+  };
+  auto issue = [&](int64_t stage, int slot) __attribute__((always_inline)) {
+    const int64_t sc = stage < nst ? stage : nst - 1;
+    if (fast_ok && sc < nwhole) {
+      const char* xs = xbase + sc * sbytes;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        dma_s(doff[j], xs + fa0 * 2, sa[slot] + 1024u * j);
+        dma_s(doff[j], xs + fb0 * 2, sb[slot] + 1024u * j);
+      }
+    } else {
+      const void* ad[4];
+      dma_addrs(stage, ad);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
     }
   };
 
@@ -545,32 +613,6 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   };
-  // Per-lane global addresses of the 8 DMAs of a stage (A0, B0, A1, B1, ...):
-  // whole stages from the stage base; partial stages and edge tiles send the
-  // lanes past n or d to the zero chunk.
-  auto dma_addrs = [&](int64_t stage, const void** ad) __attribute__((always_inline)) {
-    const int64_t sc = stage < nst ? stage : nst - 1;
-    const char* xs = xbase + sc * sbytes;
-    const char* xa = xs + fa0 * 2;
-    const char* xb = xs + fb0 * 2;
-    if (!edge && sc < nwhole) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        ad[2 * j] = xa + doff[j];
-        ad[2 * j + 1] = xb + doff[j];
-      }
-    } else {
-      const int64_t t0 = (st_begin + sc) * SK;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const bool rok = t0 + drow[j] < n;
-        const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
-        const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
-        ad[2 * j] = aok ? (const void*)(xa + doff[j]) : (const void*)kZeroChunk;
-        ad[2 * j + 1] = bok ? (const void*)(xb + doff[j]) : (const void*)kZeroChunk;
-      }
-    }
-  };
   // Step MFMAs with the next step's reads and one DMA after every two MFMAs.
   // A burst of DMAs right after the barrier stalls the issuing wave until the
   // load path drains them (and its MFMAs with it); one DMA per 64 MFMA cycles
@@ -618,13 +660,83 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  // partial slot (single-split calls, which update H directly, take
-  // syrk_bf16_kernel: the direct update's registers next to 256 live
-  // accumulators would spill here).  Slot layout: 256 chunks of 64 lanes x
-  // 4 floats, chunk ((wave MB + x) NBN + y) 4 + r4 holding accumulator
-  // registers 4 r4 .. 4 r4 + 3 of block (x, y), so every store and every
-  // load of the reduction moves 1 KB of consecutive bytes.
-  if (slot < 0) return;
+  if (slot < 0) {
+    const bool diag = ti == tj;
+    const int64_t ldh = MODE == kDense ? p.ldh : p.d;
+    if ((ldh & 3) == 0 && (reinterpret_cast<uintptr_t>(mat.h) & 15) == 0) {
+      // direct update of the upper triangle of H through the LDS ring, one
+      // half of the tile (128 rows, the accumulators of waves wm == hh) at a
+      // time: the accumulators are written row-major into LDS, then wave w
+      // updates rows 16 w .. 16 w + 15 of the half, one 256-float row (1 KB,
+      // a float4 per lane) per load and store, all 16 loads in flight
+      // together.  A float4 that straddles the diagonal writes its lower
+      // elements back unchanged.
+      float* const tile = reinterpret_cast<float*>(ring);
+      const int64_t gj = fb0 + 4 * lane;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        __syncthreads();   // the ring (or the previous half) is no longer read
+        if (wm == hh) {
+#pragma unroll
+          for (int x = 0; x < MB; ++x)
+#pragma unroll
+            for (int y = 0; y < NBN; ++y)
+#pragma unroll
+              for (int r = 0; r < 16; ++r)
+                tile[(x * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 256 + wn * 64 + y * 32 + (lane & 31)] =
+                    acc[x][y][r];
+        }
+        __syncthreads();
+        f32x4_t hv[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int64_t gi = fa0 + hh * 128 + wave * 16 + k;
+          const bool ok = gi < p.d && gj < p.d && (!diag || gi <= gj + 3);
+          hv[k] = ok ? *reinterpret_cast<const f32x4_t*>(mat.h + gi * ldh + gj) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int lr = wave * 16 + k;
+          const int64_t gi = fa0 + hh * 128 + lr;
+          if (gi < p.d && gj < p.d && (!diag || gi <= gj + 3)) {
+            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(tile + lr * 256 + 4 * lane);
+            f32x4_t o;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              o[c] = (!diag || gi <= gj + c) ? scaled(hv[k][c], p.beta) + p.alpha * v[c] : hv[k][c];
+            *reinterpret_cast<f32x4_t*>(mat.h + gi * ldh + gj) = o;
+          }
+        }
+      }
+      return;
+    }
+    // unaligned H: one 32 x 32 block at a time: lanes 0..31 / 32..63 of
+    // register r hold columns 0..31 of rows 8 (r / 4) + r % 4 and that + 4
+    // (the scheduling barrier keeps the blocks' loads from being hoisted
+    // together)
+#pragma unroll
+    for (int x = 0; x < MB; ++x)
+#pragma unroll
+      for (int y = 0; y < NBN; ++y) {
+        const int mb = wm * 128 + x * 32, nb = wn * 64 + y * 32;
+        const int64_t gib = fa0 + mb, gjb = fb0 + nb;
+        float* hb = mat.h + gib * ldh + gjb;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int mi = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), nj = lane & 31;
+          if (gib + mi < p.d && gjb + nj < p.d && (!diag || mb + mi <= nb + nj)) {
+            float* hp = hb + (int64_t)mi * ldh + nj;
+            *hp = scaled(*hp, p.beta) + p.alpha * acc[x][y][r];
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    return;
+  }
+  // partial slot.  Slot layout: 256 chunks of 64 lanes x 4 floats, chunk
+  // ((wave MB + x) NBN + y) 4 + r4 holding accumulator registers
+  // 4 r4 .. 4 r4 + 3 of block (x, y), so every store and every load of the
+  // reduction moves 1 KB of consecutive bytes.
   float* dst = p.ws + slot * C::TILE + 4 * lane;
 #pragma unroll
   for (int x = 0; x < MB; ++x)
@@ -644,6 +756,33 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
 // wave, one float4 per lane of each slot's chunk; all loads of a wave are
 // issued before its first sum, and all H reads before its first store.
 constexpr int RED_CPW = 4;  // chunks per wave of the streaming reduction
+
+// H (upper triangle of tile (ti, tj)) = beta H + alpha tot for the RED_CPW
+// slot chunks ch0 .. ch0 + RED_CPW - 1 of this lane: chunk -> wave (wm, wn)
+// of the 2 x 4 layout, block (x, y), registers 4 r4 + q
+__device__ __forceinline__ void stream_update_h(const f32x4_t* tot, int ch0, int lane, int ti, int tj, float* hm,
+                                                int64_t d, int64_t ldh, float alpha, float beta) {
+  constexpr int TM = 256, MB = 4, NBN = 2;
+  int64_t gi[RED_CPW], gj[RED_CPW];
+  float h[RED_CPW][4];
+#pragma unroll
+  for (int c = 0; c < RED_CPW; ++c) {
+    const int ch = ch0 + c;
+    const int w = ch >> 5, x = (ch >> 3) & (MB - 1), y = (ch >> 2) & (NBN - 1), r4 = ch & 3;
+    gi[c] = (int64_t)ti * TM + (w >> 2) * 128 + x * 32 + 8 * r4 + 4 * (lane >> 5);
+    gj[c] = (int64_t)tj * TM + (w & 3) * 64 + y * 32 + (lane & 31);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      h[c][q] = (gi[c] + q < d && gj[c] < d && gi[c] + q <= gj[c]) ? hm[(gi[c] + q) * ldh + gj[c]] : 0.f;
+  }
+#pragma unroll
+  for (int c = 0; c < RED_CPW; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (gi[c] + q < d && gj[c] < d && gi[c] + q <= gj[c])
+        hm[(gi[c] + q) * ldh + gj[c]] = scaled(h[c][q], beta) + alpha * tot[c][q];
+}
+
 __global__ __launch_bounds__(NT) void syrk_stream_reduce_kernel(const float* __restrict__ ws, int S,
                                                                 int tail_start, int tail_f, Matrix single,
                                                                 int64_t d, int64_t ldh, int nt, float alpha,
@@ -696,33 +835,116 @@ __global__ __launch_bounds__(NT) void syrk_stream_reduce_kernel(const float* __r
       }
     }
   }
-  // chunk -> wave (wm, wn) of the 2 x 4 layout, block (x, y), registers 4 r4 + q
-  int64_t gi[RED_CPW], gj[RED_CPW];
-  float h[RED_CPW][4];
+  stream_update_h(tot, ch0, lane, ti, tj, single.h, d, ldh, alpha, beta);
+}
+
+// Grouped: adds the later chunks' slots of (expert, tile) to H in chunk
+// order (workgroup x: item x / T, tile x % T; y: 16-chunk group as above).
+__global__ __launch_bounds__(NT) void syrk_group_reduce_kernel(const float* __restrict__ ws,
+                                                               const GReduce* __restrict__ reds,
+                                                               const int* __restrict__ gcounts, int T, int nt,
+                                                               int64_t d, float* h0, int64_t h_stride, float alpha) {
+  constexpr int TILE = 256 * 256;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int item = (int)blockIdx.x / T, t = (int)blockIdx.x % T;
+  if (item >= gcounts[1]) return;
+  const GReduce rd = reds[item];
+  int ti, tj;
+  tile_coords(t, nt, ti, tj);
+  const int ch0 = (NT / 64) * RED_CPW * blockIdx.y + RED_CPW * wave;
+  const float* src = ws + ch0 * 256 + 4 * lane;
+  f32x4_t tot[RED_CPW];
 #pragma unroll
-  for (int c = 0; c < RED_CPW; ++c) {
-    const int ch = ch0 + c;
-    const int w = ch >> 5, x = (ch >> 3) & (MB - 1), y = (ch >> 2) & (NBN - 1), r4 = ch & 3;
-    gi[c] = (int64_t)ti * TM + (w >> 2) * 128 + x * 32 + 8 * r4 + 4 * (lane >> 5);
-    gj[c] = (int64_t)tj * TM + (w & 3) * 64 + y * 32 + (lane & 31);
+  for (int c = 0; c < RED_CPW; ++c) tot[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < rd.nslots; k0 += 4) {
+    f32x4_t v[4][RED_CPW];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      h[c][q] = (gi[c] + q < d && gj[c] < d && gi[c] + q <= gj[c]) ? single.h[(gi[c] + q) * ldh + gj[c]] : 0.f;
+    for (int k = 0; k < 4; ++k)
+      if (k0 + k < rd.nslots)
+#pragma unroll
+        for (int c = 0; c < RED_CPW; ++c)
+          v[k][c] = *reinterpret_cast<const f32x4_t*>(src + (rd.sbase + (int64_t)(k0 + k) * T + t) * TILE + c * 256);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k0 + k < rd.nslots)
+#pragma unroll
+        for (int c = 0; c < RED_CPW; ++c)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) tot[c][q] += v[k][c][q];
   }
-#pragma unroll
-  for (int c = 0; c < RED_CPW; ++c)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (gi[c] + q < d && gj[c] < d && gi[c] + q <= gj[c])
-        single.h[(gi[c] + q) * ldh + gj[c]] = scaled(h[c][q], beta) + alpha * tot[c][q];
+  stream_update_h(tot, ch0, lane, ti, tj, h0 + (int64_t)rd.e * h_stride, d, d, alpha, 1.f);
+}
+
+// Builds the grouped chunk table from the expert offsets (one workgroup of
+// 1024 threads, 1024 experts per round): expert e takes
+// m_e = ceil(n_e / kChunkTokens) chunks, its first adds to H directly and
+// the m_e - 1 others get T partial slots each.  Offsets are clamped into
+// [0, n_rows] and the table never exceeds its bounds (max_chunks, max_slot
+// chunks, max_reduce), which non-decreasing offsets with offsets[E] <= n_rows
+// never reach.
+__global__ __launch_bounds__(1024) void grouped_plan_kernel(const int64_t* __restrict__ offsets, int E,
+                                                            int64_t n_rows, int T, int max_chunks,
+                                                            int max_slot_chunks, int max_reduce, GChunk* chunks,
+                                                            GReduce* reds, int* gcounts) {
+  __shared__ int sm[1024], sr[1024], ss[1024];
+  const int tid = threadIdx.x;
+  int base_c = 0, base_r = 0, base_s = 0;
+  for (int e0 = 0; e0 < E; e0 += 1024) {
+    const int e = e0 + tid;
+    int64_t b = 0, n = 0;
+    if (e < E) {
+      b = offsets[e];
+      int64_t en = offsets[e + 1];
+      b = b < 0 ? 0 : (b > n_rows ? n_rows : b);
+      en = en < b ? b : (en > n_rows ? n_rows : en);
+      n = en - b;
+    }
+    const int m = (int)((n + kChunkTokens - 1) / kChunkTokens);
+    sm[tid] = m;
+    sr[tid] = m > 1 ? 1 : 0;
+    ss[tid] = m > 1 ? m - 1 : 0;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {   // inclusive scans
+      const int vm = tid >= o ? sm[tid - o] : 0, vr = tid >= o ? sr[tid - o] : 0, vs = tid >= o ? ss[tid - o] : 0;
+      __syncthreads();
+      sm[tid] += vm;
+      sr[tid] += vr;
+      ss[tid] += vs;
+      __syncthreads();
+    }
+    const int cm = base_c + sm[tid] - m;                       // this expert's first chunk
+    const int cs = base_s + ss[tid] - (m > 1 ? m - 1 : 0);     // its first slotted chunk
+    const int cr = base_r + sr[tid] - (m > 1 ? 1 : 0);
+    for (int k = 0; k < m; ++k) {
+      const int c = cm + k, sc = cs + k - 1;
+      if (c >= max_chunks) break;   // past the table (gcounts[0] stops before it)
+      const int64_t left = n - (int64_t)k * kChunkTokens;
+      // a chunk past the slot bound is written empty (adds nothing)
+      chunks[c] = (k == 0 || sc < max_slot_chunks)
+                      ? GChunk{e, (int)(left < kChunkTokens ? left : kChunkTokens), b + (int64_t)k * kChunkTokens,
+                               k == 0 ? -1 : (int64_t)sc * T}
+                      : GChunk{e, 0, 0, -1};
+    }
+    if (m > 1 && cr < max_reduce) {
+      const int room = cs < max_slot_chunks ? max_slot_chunks - cs : 0;
+      reds[cr] = GReduce{e, m - 1 < room ? m - 1 : room, (int64_t)cs * T};
+    }
+    base_c += sm[1023];
+    base_r += sr[1023];
+    base_s += ss[1023];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    gcounts[0] = base_c < max_chunks ? base_c : max_chunks;
+    gcounts[1] = base_r < max_reduce ? base_r : max_reduce;
+  }
 }
 
 // Sums the S partial slots of a tile in split order and updates H.  Each
 // workgroup finishes one row of 32 x 32 blocks of its wave tiles
 // (blockIdx.y = bm), so a TM = 256 tile is finished by four workgroups.
 template <int TM>
-__global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict__ ws, const ReduceItem* items,
-                                                         int single_S, Matrix single, const Matrix* mats,
+__global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict__ ws, int S, Matrix mat,
                                                          int64_t d, int64_t ldh, int nt, float alpha,
                                                          float beta) {
   using C = Cfg<TM>;
@@ -731,16 +953,8 @@ __global__ __launch_bounds__(NT) void syrk_reduce_kernel(const float* __restrict
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int bm = blockIdx.y;
-  int t, S;
-  int64_t slot0;
-  Matrix mat;
-  if (items) {
-    const ReduceItem it = items[blockIdx.x];
-    t = it.t; S = it.S; slot0 = it.slot0; mat = mats[it.e];
-  } else {
-    t = blockIdx.x; S = single_S; mat = single;
-    slot0 = (int64_t)t * S;
-  }
+  const int t = blockIdx.x;
+  const int64_t slot0 = (int64_t)t * S;
   int ti, tj;
   tile_coords(t, nt, ti, tj);
   float sum[C::NB * 16];
@@ -840,14 +1054,10 @@ DensePlan plan_dense(int64_t n, int64_t d) {
 
 template <bool F16>
 void launch_syrk_t(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
-  const bool g = p.rows != nullptr;
   if (tile_edge(d) == 256) {
-    if (g)             hipLaunchKernelGGL((syrk_bf16_kernel<256, true, F16>), dim3(grid), dim3(NT), 0, st, p);
-    else if (p.S == 1) hipLaunchKernelGGL((syrk_bf16_kernel<256, false, F16>), dim3(grid), dim3(NT), 0, st, p);
-    else               hipLaunchKernelGGL(syrk_stream_kernel<F16>, dim3(grid), dim3(SNT), 0, st, p);
+    hipLaunchKernelGGL((syrk_stream_kernel<F16, kDense>), dim3(grid), dim3(SNT), 0, st, p);
   } else {
-    if (g) hipLaunchKernelGGL((syrk_bf16_kernel<128, true, F16>), dim3(grid), dim3(NT), 0, st, p);
-    else   hipLaunchKernelGGL((syrk_bf16_kernel<128, false, F16>), dim3(grid), dim3(NT), 0, st, p);
+    hipLaunchKernelGGL((syrk_bf16_kernel<128, F16>), dim3(grid), dim3(NT), 0, st, p);
   }
 }
 
@@ -856,14 +1066,14 @@ void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st, 
 }
 
 // reduction of syrk_bf16_kernel partials (2 x 2 fragment order)
-void launch_reduce(const float* ws, const ReduceItem* items, int S, const Matrix& single, const Matrix* mats,
-                   int64_t d, int64_t ldh, int nt, float alpha, float beta, unsigned ntiles, hipStream_t st) {
+void launch_reduce(const float* ws, int S, const Matrix& single, int64_t d, int64_t ldh, int nt, float alpha,
+                   float beta, unsigned ntiles, hipStream_t st) {
   if (tile_edge(d) == 256)
-    hipLaunchKernelGGL(syrk_reduce_kernel<256>, dim3(ntiles, Cfg<256>::NB), dim3(NT), 0, st, ws, items, S,
-                       single, mats, d, ldh, nt, alpha, beta);
+    hipLaunchKernelGGL(syrk_reduce_kernel<256>, dim3(ntiles, Cfg<256>::NB), dim3(NT), 0, st, ws, S, single, d, ldh,
+                       nt, alpha, beta);
   else
-    hipLaunchKernelGGL(syrk_reduce_kernel<128>, dim3(ntiles, Cfg<128>::NB), dim3(NT), 0, st, ws, items, S,
-                       single, mats, d, ldh, nt, alpha, beta);
+    hipLaunchKernelGGL(syrk_reduce_kernel<128>, dim3(ntiles, Cfg<128>::NB), dim3(NT), 0, st, ws, S, single, d, ldh,
+                       nt, alpha, beta);
 }
 
 // H[i][j] *= beta on the upper triangle (a call without tokens)
@@ -919,13 +1129,10 @@ int hessian16_impl(const void* x_dev, bool f16, int64_t n_tokens, int64_t d, int
   p.nt = nt;
   p.alpha = alpha;
   p.beta = beta;
-  p.rows = nullptr;
   p.single = Matrix{0, n_tokens, h_dev};
   p.S = S;
   p.tail_start = pl.tail_start;
   p.tail_f = pl.tail_f;
-  p.items = nullptr;
-  p.mats = nullptr;
   p.ws = static_cast<float*>(workspace_dev);
   launch_syrk(p, d, (unsigned)pl.grid, st, f16);
   MQ_LAUNCH_CHECK();
@@ -934,7 +1141,7 @@ int hessian16_impl(const void* x_dev, bool f16, int64_t n_tokens, int64_t d, int
       hipLaunchKernelGGL(syrk_stream_reduce_kernel, dim3((unsigned)T, 256 / ((NT / 64) * RED_CPW)), dim3(NT), 0,
                          st, p.ws, S, pl.tail_start, pl.tail_f, p.single, d, ldh, nt, alpha, beta);
     else
-      launch_reduce(p.ws, nullptr, S, p.single, nullptr, d, ldh, nt, alpha, beta, (unsigned)T, st);
+      launch_reduce(p.ws, S, p.single, d, ldh, nt, alpha, beta, (unsigned)T, st);
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;
@@ -982,111 +1189,94 @@ extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int
 }
 
 namespace {
-// Grouped workspace layout: [partials][items][reduce items][matrices]
-struct GroupedPlan {
-  std::vector<Item> items;
-  std::vector<ReduceItem> reduces;
-  std::vector<Matrix> mats;
-  int64_t slots = 0;
-  size_t off_items = 0, off_reduces = 0, off_mats = 0, total = 0;
+// Grouped workspace: [partial slots][chunk table][reduce table][2 counts],
+// every part sized for the largest table the arguments allow.
+struct GroupedBounds {
+  int T = 0, max_chunks = 0, max_slot_chunks = 0, max_reduce = 0;
+  size_t off_chunks = 0, off_reds = 0, off_counts = 0, total = 0;
 };
-
-GroupedPlan plan_grouped(const int64_t* offsets, int E, int64_t d, float* h, int64_t h_stride) {
-  GroupedPlan g;
-  const int nt = tiles_per_edge(d);
-  const int T = upper_tiles(nt);
-  for (int e = 0; e < E; ++e) {
-    const int64_t n = offsets[e + 1] - offsets[e];
-    g.mats.push_back(Matrix{offsets[e], n, h ? h + (int64_t)e * h_stride : nullptr});
-    if (n <= 0) continue;
-    const int S = choose_splits(n, T);
-    for (int t = 0; t < T; ++t) {
-      const int64_t slot0 = S > 1 ? g.slots : -1;
-      for (int s = 0; s < S; ++s) g.items.push_back(Item{e, t, s, S, S > 1 ? slot0 + s : -1});
-      if (S > 1) {
-        g.reduces.push_back(ReduceItem{e, t, S, slot0});
-        g.slots += S;
-      }
-    }
-  }
+GroupedBounds grouped_bounds(int64_t n_rows, int E, int64_t d) {
+  GroupedBounds g;
+  g.T = upper_tiles((int)((d + 255) / 256));
+  const int64_t full = n_rows / kChunkTokens;   // chunks after an expert's first are whole
+  g.max_chunks = (int)(E + full);
+  g.max_slot_chunks = (int)full;
+  g.max_reduce = (int)(full < E ? full : E);
   auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  size_t off = align((size_t)g.slots * tile_floats(d) * sizeof(float));
-  g.off_items = off;
-  off = align(off + g.items.size() * sizeof(Item));
-  g.off_reduces = off;
-  off = align(off + g.reduces.size() * sizeof(ReduceItem));
-  g.off_mats = off;
-  off = align(off + g.mats.size() * sizeof(Matrix));
-  g.total = off;
+  size_t off = align((size_t)g.max_slot_chunks * g.T * 256 * 256 * sizeof(float));
+  g.off_chunks = off;
+  off = align(off + (size_t)g.max_chunks * sizeof(GChunk));
+  g.off_reds = off;
+  off = align(off + (size_t)(g.max_reduce > 0 ? g.max_reduce : 1) * sizeof(GReduce));
+  g.off_counts = off;
+  g.total = align(off + 2 * sizeof(int));
   return g;
 }
 }  // namespace
 
-extern "C" size_t mi355q_hessian_grouped_workspace_size(const int64_t* offsets_host, int n_experts,
-                                                        int64_t d) {
-  if (!offsets_host || n_experts <= 0 || d <= 0) return 0;
-  return plan_grouped(offsets_host, n_experts, d, nullptr, 0).total;
+extern "C" size_t mi355q_hessian_grouped_syrk_workspace_size(int64_t n_rows, int n_experts, int64_t d) {
+  if (n_rows < 0 || n_experts <= 0 || d <= 0) return 0;
+  return grouped_bounds(n_rows, n_experts, d).total;
 }
 
-extern "C" int mi355q_hessian_grouped_syrk_bf16(const void* x_dev, int64_t ldx, int64_t d,
-                                                const int32_t* rows_dev, const int64_t* offsets_host,
-                                                int n_experts, float* h_dev, int64_t h_stride,
-                                                float alpha, void* workspace_dev,
-                                                size_t workspace_bytes, void* stream) {
-  return mi355q_hessian_grouped_syrk(x_dev, MI355Q_BF16, ldx, d, rows_dev, offsets_host, n_experts, h_dev,
-                                     h_stride, alpha, workspace_dev, workspace_bytes, stream);
-}
-
-extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype, int64_t ldx, int64_t d,
-                                           const int32_t* rows_dev, const int64_t* offsets_host, int n_experts,
-                                           float* h_dev, int64_t h_stride, float alpha, void* workspace_dev,
+extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_x, int64_t ldx,
+                                           int64_t d, const int32_t* rows_dev, int64_t n_rows,
+                                           const int64_t* offsets_dev, int n_experts, float* h_dev,
+                                           int64_t h_stride, float alpha, void* workspace_dev,
                                            size_t workspace_bytes, void* stream) {
   MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F16, "grouped hessian: dtype must be bf16 or fp16");
   MQ_CHECK_ARG(d > 0 && d % 8 == 0, "grouped hessian: d must be a positive multiple of 8");
   MQ_CHECK_ARG(ldx >= d && ldx % 8 == 0, "grouped hessian: ldx must be >= d and a multiple of 8");
-  MQ_CHECK_ARG(n_experts > 0 && offsets_host != nullptr, "grouped hessian: bad expert table");
+  MQ_CHECK_ARG(ldx <= (int64_t(1) << 24), "grouped hessian: ldx above 2^24 elements is not supported");
+  MQ_CHECK_ARG(n_experts > 0 && offsets_dev != nullptr, "grouped hessian: bad expert table");
+  MQ_CHECK_ARG(n_x >= 0 && n_rows >= 0, "grouped hessian: negative row count");
+  MQ_CHECK_ARG(rows_dev != nullptr || n_rows <= n_x, "grouped hessian: n_rows > n_x without a row index");
   MQ_CHECK_ARG(h_dev != nullptr && h_stride >= d * d, "grouped hessian: bad H / stride");
-  for (int e = 0; e < n_experts; ++e)
-    MQ_CHECK_ARG(offsets_host[e + 1] >= offsets_host[e] && offsets_host[e] >= 0,
-                 "grouped hessian: offsets must be non-decreasing");
-  GroupedPlan g = plan_grouped(offsets_host, n_experts, d, h_dev, h_stride);
-  if (g.items.empty()) return MI355Q_OK;
-  MQ_CHECK_ARG(rows_dev != nullptr && x_dev != nullptr && aligned16(x_dev),
-               "grouped hessian: null or misaligned x / rows");
-  MQ_CHECK_ARG(workspace_dev != nullptr && workspace_bytes >= g.total,
-               "grouped hessian: workspace too small (%zu < %zu)", workspace_bytes, g.total);
+  if (n_rows == 0 || n_x == 0) return MI355Q_OK;
+  MQ_CHECK_ARG(x_dev != nullptr && aligned16(x_dev), "grouped hessian: null or misaligned x");
+  const GroupedBounds gb = grouped_bounds(n_rows, n_experts, d);
+  MQ_CHECK_ARG(workspace_dev != nullptr && workspace_bytes >= gb.total,
+               "grouped hessian: workspace too small (%zu < %zu)", workspace_bytes, gb.total);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace_dev);
-  MQ_CHECK_HIP(hipMemcpyAsync(ws + g.off_items, g.items.data(), g.items.size() * sizeof(Item),
-                              hipMemcpyHostToDevice, st));
-  if (!g.reduces.empty())
-    MQ_CHECK_HIP(hipMemcpyAsync(ws + g.off_reduces, g.reduces.data(),
-                                g.reduces.size() * sizeof(ReduceItem), hipMemcpyHostToDevice, st));
-  MQ_CHECK_HIP(hipMemcpyAsync(ws + g.off_mats, g.mats.data(), g.mats.size() * sizeof(Matrix),
-                              hipMemcpyHostToDevice, st));
-  // the host-side plan dies at return: wait for the copies
-  MQ_CHECK_HIP(hipStreamSynchronize(st));
+  GChunk* chunks = reinterpret_cast<GChunk*>(ws + gb.off_chunks);
+  GReduce* reds = reinterpret_cast<GReduce*>(ws + gb.off_reds);
+  int* counts = reinterpret_cast<int*>(ws + gb.off_counts);
+  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(1024), 0, st, offsets_dev, n_experts, n_rows, gb.T,
+                     gb.max_chunks, gb.max_slot_chunks, gb.max_reduce, chunks, reds, counts);
+  MQ_LAUNCH_CHECK();
 
   SyrkParams p{};
   p.x = static_cast<const uint16_t*>(x_dev);
   p.ldx = ldx;
   p.d = d;
   p.ldh = d;
-  p.nt = tiles_per_edge(d);
+  p.nt = (int)((d + 255) / 256);
   p.alpha = alpha;
   p.beta = 1.f;
-  p.rows = rows_dev;
   p.S = 1;
-  p.tail_start = 0;
-  p.tail_f = 1;
-  p.items = reinterpret_cast<const Item*>(ws + g.off_items);
-  p.mats = reinterpret_cast<const Matrix*>(ws + g.off_mats);
   p.ws = reinterpret_cast<float*>(ws);
-  launch_syrk(p, d, (unsigned)g.items.size(), st, dtype == MI355Q_F16);
+  p.rows = rows_dev;
+  p.n_x = n_x;
+  p.chunks = chunks;
+  p.gcounts = counts;
+  p.T = gb.T;
+  p.h0 = h_dev;
+  p.h_stride = h_stride;
+  const int64_t items = (int64_t)gb.max_chunks * gb.T;
+  const unsigned grid = (unsigned)(8 * ((items + 7) / 8));
+  const bool f16 = dtype == MI355Q_F16;
+  if (rows_dev) {
+    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGroupedGather>), dim3(grid), dim3(SNT), 0, st, p);
+    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGroupedGather>), dim3(grid), dim3(SNT), 0, st, p);
+  } else {
+    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGrouped>), dim3(grid), dim3(SNT), 0, st, p);
+    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGrouped>), dim3(grid), dim3(SNT), 0, st, p);
+  }
   MQ_LAUNCH_CHECK();
-  if (!g.reduces.empty()) {
-    launch_reduce(p.ws, reinterpret_cast<const ReduceItem*>(ws + g.off_reduces), 1, Matrix{}, p.mats, d, d,
-                  p.nt, alpha, 1.f, (unsigned)g.reduces.size(), st);
+  if (gb.max_reduce > 0) {
+    hipLaunchKernelGGL(syrk_group_reduce_kernel, dim3((unsigned)(gb.max_reduce * gb.T), 256 / ((NT / 64) * RED_CPW)),
+                       dim3(NT), 0, st, p.ws, reds, counts, gb.T, p.nt, d, h_dev, h_stride, alpha);
     MQ_LAUNCH_CHECK();
   }
   return MI355Q_OK;

@@ -64,9 +64,14 @@ def route_tokens(top_k_index: torch.Tensor, num_experts: int, num_tokens: int | 
     return sorted_tok.to(torch.int32), offsets, pos.reshape(-1)[order]
 
 
-def accumulate_expert_hessians(x: torch.Tensor, rows: torch.Tensor, offsets: list[int], H: torch.Tensor,
+def accumulate_expert_hessians(x: torch.Tensor, rows: torch.Tensor | None, offsets, H: torch.Tensor,
                                num_samples: torch.Tensor, calls: int = 1):
-    """H[e] += 2 * sum over the expert's rows of x x^T; num_samples[e] += calls."""
+    """H[e] += 2 * sum over the expert's rows of x x^T; num_samples[e] += calls.
+
+    ``rows`` None: x is already grouped by expert (expert e owns the rows
+    offsets[e] .. offsets[e+1] - 1, as ``expert_intermediate`` returns them).
+    ``offsets`` is a list or an int64 tensor (on the device the call waits
+    for nothing)."""
     ops.hessian_grouped_syrk_(H, x, rows, offsets, alpha=2.0)
     num_samples += calls
     return H, num_samples

@@ -69,29 +69,50 @@ def hessian_syrk_(H: torch.Tensor, x: torch.Tensor, alpha: float = 2.0, beta: fl
     return H
 
 
-def hessian_grouped_syrk_(H: torch.Tensor, x: torch.Tensor, rows: torch.Tensor, offsets: list[int],
+def hessian_grouped_syrk_(H: torch.Tensor, x: torch.Tensor, rows: torch.Tensor | None, offsets,
                           alpha: float = 2.0) -> torch.Tensor:
     """Per-group upper-triangle syrk: H[e] += alpha * X_e^T X_e where X_e are
-    the rows ``x[rows[offsets[e]:offsets[e+1]]]``.  H is [E, d, d] fp32.  bf16
-    and fp16 ``x`` take one grouped launch; other types are converted to fp32
-    and each group's gathered rows take the dense fp32 product."""
-    L.require_gpu(H, x, rows)
-    E = len(offsets) - 1
+    the rows ``x[rows[offsets[e]:offsets[e+1]]]`` (``rows`` None: the rows
+    ``x[offsets[e]:offsets[e+1]]``).  H is [E, d, d] fp32; ``offsets`` a list
+    or an int64 tensor of E + 1 non-decreasing entries.  bf16 and fp16 ``x``
+    take one grouped launch whose work table is built on the device; other
+    types are converted to fp32 and each group's rows take the dense fp32
+    product."""
+    L.require_gpu(H, x)
+    if isinstance(offsets, torch.Tensor):
+        off_dev = offsets.to(device=x.device, dtype=torch.int64).contiguous()
+        E = off_dev.numel() - 1
+        off_list = None
+    else:
+        off_list = [int(o) for o in offsets]
+        E = len(off_list) - 1
+        if any(b < a for a, b in zip(off_list, off_list[1:])) or (off_list and off_list[0] < 0):
+            raise ValueError("offsets must be non-negative and non-decreasing")
+        off_dev = None
     x = _hessian_input(x)
-    d = x.shape[1]
+    n_x, d = x.shape
+    n_rows = n_x if rows is None else rows.numel()
+    if off_list is not None and off_list[-1] > n_rows:
+        raise ValueError(f"offsets end at {off_list[-1]} > {n_rows} rows")
     if H.shape != (E, d, d) or H.dtype != torch.float32 or not H.is_contiguous():
         raise ValueError(f"H must be contiguous fp32 [{E}, {d}, {d}]")
     if x.dtype == torch.float32:
+        offs = off_list if off_list is not None else off_dev.tolist()
         for e in range(E):
-            if offsets[e + 1] > offsets[e]:
-                hessian_syrk_(H[e], x[rows[offsets[e]:offsets[e + 1]].long()], alpha=alpha)
+            if offs[e + 1] > offs[e]:
+                xe = x[offs[e]:offs[e + 1]] if rows is None else x[rows[offs[e]:offs[e + 1]].long()]
+                hessian_syrk_(H[e], xe, alpha=alpha)
         return H
-    rows = rows.to(torch.int32).contiguous()
-    off = (C.c_int64 * (E + 1))(*[int(o) for o in offsets])
+    if rows is not None:
+        L.require_gpu(rows)
+        rows = rows.to(torch.int32).contiguous()
+    if off_dev is None:
+        off_dev = torch.tensor(off_list, dtype=torch.int64).to(x.device, non_blocking=True)
     lib = L.lib()
-    ws = _ws(lib.mi355q_hessian_grouped_workspace_size(off, E, d), x.device)
-    L.check(lib.mi355q_hessian_grouped_syrk(x.data_ptr(), _HESS_DT[x.dtype], x.stride(0), d, rows.data_ptr(), off, E,
-                                            H.data_ptr(), d * d, C.c_float(alpha), L.ptr(ws),
+    ws = _ws(lib.mi355q_hessian_grouped_syrk_workspace_size(n_rows, E, d), x.device)
+    L.check(lib.mi355q_hessian_grouped_syrk(x.data_ptr(), _HESS_DT[x.dtype], n_x, x.stride(0), d,
+                                            None if rows is None else rows.data_ptr(), n_rows, off_dev.data_ptr(),
+                                            E, H.data_ptr(), d * d, C.c_float(alpha), L.ptr(ws),
                                             0 if ws is None else ws.numel(), L.stream_of(x)))
     return H
 

@@ -182,6 +182,69 @@ def test_hessian_grouped_parity(dev):
         assert rel_fro(torch.triu(H[e].cpu()), torch.triu(Ho[e])) <= HESS_TOL, e
 
 
+def _grouped_case(counts, n_x, d, dtype, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = (torch.randn(n_x, d, generator=g, device=dev) * torch.exp(torch.randn(d, generator=g, device=dev))).to(dtype)
+    rows = torch.cat([torch.randint(0, n_x, (c,), generator=g, device=dev) for c in counts]).to(torch.int32)
+    offsets = [0]
+    for c in counts:
+        offsets.append(offsets[-1] + c)
+    return x, rows, offsets
+
+
+def _grouped_check(H, x, rows, offsets, alpha=2.0):
+    for e in range(len(offsets) - 1):
+        a, b = offsets[e], offsets[e + 1]
+        if a == b:
+            assert torch.count_nonzero(H[e]) == 0, e
+            continue
+        xe = (x[a:b] if rows is None else x[rows[a:b].long()]).double()
+        ref = alpha * (xe.t().contiguous() @ xe)
+        up = torch.triu(torch.ones_like(ref, dtype=torch.bool))
+        r = ((H[e].double() - ref)[up].norm() / ref[up].norm()).item()
+        assert r <= HESS_TOL, (e, b - a, r)
+        assert torch.count_nonzero(torch.tril(H[e], -1)) == 0, e
+
+
+@pytest.mark.parametrize("d,dtype", [(2048, torch.bfloat16), (1000, torch.bfloat16), (768, torch.float16)],
+                         ids=["d2048-bf16", "d1000-bf16", "d768-fp16"])
+def test_hessian_grouped_multichunk(dev, d, dtype):
+    """Experts of 0 .. 9000 routed rows (1, 2 and 3 chunks of 4096, an empty
+    expert, one row): the device-built work table, the gathering DMA, the
+    direct first-chunk update and the ordered slot reduction, against an fp64
+    product per expert; a second call adds the same again and is bitwise
+    equal to twice the first (deterministic)."""
+    counts = [9000, 5000, 0, 100, 4096, 4097, 1, 2000, 300, 8192]
+    say(f"grouped hessian multi-chunk d={d} {dtype}")
+    x, rows, offsets = _grouped_case(counts, 7000, d, dtype, 21, dev)
+    H = torch.zeros(len(counts), d, d, device=dev)
+    ops.hessian_grouped_syrk_(H, x, rows, offsets, alpha=2.0)
+    _grouped_check(H, x, rows, offsets)
+    H1 = H.clone()
+    ops.hessian_grouped_syrk_(H, x, rows, torch.tensor(offsets, device=dev), alpha=2.0)
+    H2 = torch.zeros_like(H)
+    ops.hessian_grouped_syrk_(H2, x, rows, offsets, alpha=2.0)
+    assert torch.equal(H2, H1)
+    assert ((H - 2 * H1).norm() / H1.norm()).item() <= 1e-6
+
+
+def test_hessian_grouped_contiguous_rows(dev):
+    """rows None: x already grouped by expert (the down projection's inputs),
+    offsets given on the device."""
+    counts = [5000, 0, 4096, 33, 12000]
+    d = 768
+    say("grouped hessian contiguous rows")
+    g = torch.Generator(device=dev).manual_seed(22)
+    x = torch.randn(sum(counts) + 10, d, generator=g, device=dev).to(torch.bfloat16)
+    offsets = [0]
+    for c in counts:
+        offsets.append(offsets[-1] + c)
+    H = torch.zeros(len(counts), d, d, device=dev)
+    moe.accumulate_expert_hessians(x, None, torch.tensor(offsets, device=dev), H, torch.zeros(len(counts),
+                                                                                              device=dev))
+    _grouped_check(H, x, None, offsets)
+
+
 # ---------------------------------------------------------------- observers / quant / pack
 W_CASES = [
     dict(num_bits=4, strategy="group", group_size=128),
