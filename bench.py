@@ -134,7 +134,26 @@ def main():
     syrk_tflops = syrk_flop / (syrk_ms * 1e-3) / 1e12
     xf = x.reshape(-1, COLS)
     reps = 5
+
+    # the reference's per-batch calling pattern (batch_size=1 calibration:
+    # one accumulate_hessian call per 2048-token sample, 64 calls)
+    chunks64 = torch.chunk(x, BATCHES, dim=0)
+    H64 = gptq.make_empty_hessian(lin)
+    n64 = torch.zeros((), device=dev)
+    for ch in chunks64:
+        H64, n64 = gptq.accumulate_hessian(ch, lin, H64, n64)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps64 = 3
+    e0.record(stream)
+    for _ in range(reps64):
+        H64.zero_()
+        for ch in chunks64:
+            H64, n64 = gptq.accumulate_hessian(ch, lin, H64, n64)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    h64_ms = e0.elapsed_time(e1) / reps64
+    h64_rel = ((torch.triu(H64) - torch.triu(H_last)).norm() / torch.triu(H_last).norm()).item()
+    del H64
 
     # vendor GEMM on the same product: torch.mm (hipBLASLt) of X^T X as the
     # full 4096 x 4096 square with a bf16 result (twice the multiply-adds of
@@ -215,7 +234,12 @@ def main():
         "hessian": {"ms": round(syrk_ms, 4), "tflops": round(syrk_tflops, 1),
                     "frac_fp32_mfma_peak": round(syrk_tflops / PEAK_FP32_MFMA_TFLOPS, 3),
                     "frac_bf16_mfma_peak": round(syrk_tflops / PEAK_BF16_TFLOPS, 4),
-                    "vendor_gemm_full_square_bf16_out": {"ms": round(mm_ms, 4), "tflops": round(mm_tflops, 1)}},
+                    "vendor_gemm_full_square_bf16_out": {"ms": round(mm_ms, 4), "tflops": round(mm_tflops, 1)},
+                    "calls_64x2048": {"ms": round(h64_ms, 4),
+                                      "tflops": round(syrk_flop / (h64_ms * 1e-3) / 1e12, 1),
+                                      "frac_bf16_mfma_peak": round(syrk_flop / (h64_ms * 1e-3) / 1e12
+                                                                   / PEAK_BF16_TFLOPS, 4),
+                                      "rel_diff_vs_one_call": float(f"{h64_rel:.3g}")}},
         "mxfp4_quantize_pack": mx,
         "copy_1GiB_GB_s": round(copy_gbs, 1),
         "roofline": {"bound": "mfma", "achieved": round(syrk_tflops, 2), "peak": PEAK_BF16_TFLOPS,
