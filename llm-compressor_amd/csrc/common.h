@@ -49,13 +49,19 @@ __host__ __device__ inline float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 bit pattern (NaN kept quiet).
+// Round-to-nearest-even fp32 -> bf16 bit pattern (NaN kept quiet).  Device
+// code takes gfx950's v_cvt_pk_bf16_f32 (IEEE round to nearest even, NaN in
+// NaN out); the host pass the same rounding from the bits.
 __host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+#else
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
   uint32_t lsb = (u >> 16) & 1u;
   u += 0x7fffu + lsb;
   return static_cast<uint16_t>(u >> 16);
+#endif
 }
 
 __host__ __device__ inline float round_to_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }

@@ -737,6 +737,11 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 // x / s with 8-bit significands is either a bf16 midpoint exactly or at
 // least 2^-17 (relative) away from every midpoint.  Scales below 2^-100
 // (rows of denormal-sized values, refine false) take the IEEE division.
+// Codes of 8 bf16 values: rint(clamp(bf16(x / s), -128, 127)).  The clamp,
+// the round to nearest even and the byte packing are one v_cvt_pk_u8_f32 of
+// q + 128 (saturating to [0, 255]; adding the even integer 128 to the bf16
+// quotient is exact wherever it can change the rounded result and keeps
+// ties on the same side), and the xor with 0x80 per byte restores the sign.
 __device__ __forceinline__ void int8_chunk(const u32x4_t& v, float s, float rs, bool refine, uint32_t w[2]) {
   w[0] = w[1] = 0u;
 #pragma unroll
@@ -751,9 +756,10 @@ __device__ __forceinline__ void int8_chunk(const u32x4_t& v, float s, float rs, 
       q = xv / s;
     }
     q = round_to_bf16(q);
-    q = fminf(fmaxf(q, -128.f), 127.f);
-    w[e >> 2] |= ((uint32_t)(int32_t)rintf(q) & 0xffu) << (8 * (e & 3));
+    w[e >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(q + 128.f, e & 3, w[e >> 2]);
   }
+  w[0] ^= 0x80808080u;
+  w[1] ^= 0x80808080u;
 }
 
 // Per-token scale of one row from its absmax bit pattern: bf16(amax / 127.5),
