@@ -38,6 +38,8 @@ def parse():
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--headline-only", action="store_true",
+                   help="skip the W8A8, MoE and decoder-layer workloads the default line also reports")
     p.add_argument("--hessian-calls", type=int, default=1,
                    help="split the 64 x 2048 calibration tokens into this many accumulate_hessian calls")
     p.add_argument("--workload", default="gptq_w4a16",
@@ -216,6 +218,29 @@ def main():
     if not a.no_cpu_baseline:
         cpu, parity = cpu_baseline(torch, w.cpu(), x[:4].cpu(), H_last.cpu(), res)
 
+    # the W8A8, MoE and decoder-layer configurations, two timed steps each
+    # after one warm-up, reported inside this line (each also has its own
+    # --workload line)
+    others = None
+    if not a.headline_only:
+        global _COLLECT
+        del x, xf, w, lin, res, H_last, chunks, chunks64
+        torch.cuda.empty_cache()
+        _COLLECT = []
+        sub = argparse.Namespace(**{**vars(a), "steps": 2, "warmup": 1})
+        for fn in (bench_w8a8, bench_moe, bench_decoder):
+            fn(sub)
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+        others = {}
+        for ln in _COLLECT:
+            others[ln["config"]["workload"]] = {k: ln[k] for k in ("metric", "value", "unit", "steps", "warmup")
+                                                if k in ln}
+            for k in ("phases_ms", "hessian", "act_quant_int8_per_token", "tokens_per_expert"):
+                if k in ln:
+                    others[ln["config"]["workload"]][k] = ln[k]
+        _COLLECT = None
+
     line = {
         "metric": "GPTQ ms/layer (W4A16 g128, 4096x4096, Hessian over 64x2048 tokens + solve)",
         "value": round(ms_step, 3),
@@ -248,6 +273,7 @@ def main():
                                "131072 tokens)"},
         "cpu_baseline": cpu,
         "parity": parity,
+        "other_configs": others,
     }
     print(json.dumps(line), flush=True)
 
@@ -353,13 +379,19 @@ def _timed(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) * 1e3 / steps, out
 
 
+_COLLECT = None   # a list while the default line gathers the other workloads' lines
+
+
 def _line(metric, value, unit, a, ms, workload, extra, higher=False, dtype="bf16 inputs, fp32 accumulate/solve"):
     line = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": a.steps,
             "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": higher, "scaling": "weak",
             "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded, generated on the GPU)",
             "config": {"workload": workload}}
     line.update(extra)
-    print(json.dumps(line), flush=True)
+    if _COLLECT is not None:
+        _COLLECT.append(line)
+    else:
+        print(json.dumps(line), flush=True)
 
 
 def bench_mxfp4(a):
