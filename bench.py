@@ -209,10 +209,16 @@ def main():
     copy_gbs = 2 * src.numel() * 4 / (copy_ms * 1e-3) / 1e9
     del src, dst
 
-    traffic = None
-    tf = ROOT / "profiles" / "hessian_syrk_traffic.json"
+    # counters of the same kernels (rocprofv3 --pmc passes, commands in the file)
+    traffic = counters = None
+    tf = ROOT / "profiles" / "hessian_syrk_counters.json"
     if tf.exists():
-        traffic = json.loads(tf.read_text()).get("bytes_per_launch")
+        pmc = json.loads(tf.read_text())
+        traffic = pmc.get("bytes_per_launch")
+        counters = {"file": "profiles/hessian_syrk_counters.json",
+                    **{k: pmc.get(k) for k in ("algorithmic_bytes_per_launch", "mfma_busy_frac", "sclk_ghz_avg",
+                                               "mfma_instructions", "mfma_bf16_flop_issued",
+                                               "lds_instructions_per_mfma", "lds_bank_conflict_cycles")}}
 
     cpu = parity = None
     if not a.no_cpu_baseline:
@@ -269,6 +275,7 @@ def main():
         "copy_1GiB_GB_s": round(copy_gbs, 1),
         "roofline": {"bound": "mfma", "achieved": round(syrk_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(syrk_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "counters": counters,
                      "kernel": "syrk_stream_kernel + syrk_stream_reduce_kernel (the Hessian call of each timed step, "
                                "131072 tokens)"},
         "cpu_baseline": cpu,

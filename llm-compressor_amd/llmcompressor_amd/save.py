@@ -19,7 +19,9 @@ unpinned: the library is absent and no reference test holds a checkpoint):
 * ``pack-quantized``: ``weight_packed`` int32 [rows, ceil(cols * b / 32)]
   (offset-binary b-bit fields along columns, field e at bits b * e),
   ``weight_shape`` int64 [2], ``weight_scale``, ``weight_zero_point`` when
-  asymmetric, ``weight_g_idx`` with group activation order;
+  asymmetric (group / channel zero points packed the same way along the
+  output dimension: int32 [ceil(rows * b / 32), groups]), ``weight_g_idx``
+  with group activation order;
 * ``int-quantized`` / ``naive-quantized`` (int): ``weight`` int8 codes,
   ``weight_scale``, ``weight_zero_point`` when asymmetric;
 * ``float-quantized`` / ``naive-quantized`` (fp8): ``weight`` float8_e4m3fn,
@@ -37,7 +39,7 @@ import shutil
 import torch
 
 from . import ops
-from .quant_args import QuantizationArgs, QuantizationScheme, QuantizationType
+from .quant_args import QuantizationArgs, QuantizationScheme, QuantizationStrategy, QuantizationType
 
 __all__ = ["infer_quantization_format", "compress_module", "quantization_config", "save_compressed",
            "QuantConfigParser", "Int8Packer"]
@@ -93,7 +95,10 @@ def compress_module(module: torch.nn.Module, fmt: str | None = None) -> dict[str
         else:
             raise ValueError(f"format {fmt} cannot hold integer weights")
         if not w.symmetric:
-            out["weight_zero_point"] = module.weight_zero_point.data
+            zp = module.weight_zero_point.data
+            if fmt == "pack-quantized" and w.strategy in (QuantizationStrategy.GROUP, QuantizationStrategy.CHANNEL):
+                zp = ops.pack_int32(zp.to(torch.int8).t().contiguous(), w.num_bits).t().contiguous()
+            out["weight_zero_point"] = zp
         return out
     if w.num_bits == 8 and fmt in ("float-quantized", "naive-quantized"):
         out["weight"] = ops.quantize_fp8(module.weight, module.weight_scale, w.strategy.value, w.group_size)

@@ -6,9 +6,11 @@
   ``tests/llmcompressor/utils/test_pack_int4_to_int8.py:25-46``.
 * ``pack_to_int32``      - compressed-tensors ``pack_to_int32`` (the
   ``pack_quantized`` format of W4A16): codes offset by 2^(b-1), eight
-  4-bit fields per int32, field k at bits 4k along the column axis.
-  Parity unpinned against the reference (CT absent, no reference test);
-  pinned by a hand-computed vector and the unpack round trip.
+  4-bit fields per int32, field k at bits 4k along the column axis
+  (``packed_dim=0``: along the rows, as CT packs asymmetric group / channel
+  zero points).  Parity unpinned against the reference (CT absent, no
+  reference test); pinned by a hand-computed vector and the unpack round
+  trip.
 * ``mxfp4_quantize_pack`` - MXFP4 codes and e8m0 scales from bf16 bit
   patterns: shared exponent by the rule in ``oracle.observers.mx_scale_exponent``
   ("ct" default, "ocp" switch), e2m1 rounding with compressed-tensors
@@ -37,7 +39,9 @@ def pack_int4_to_int8(t: np.ndarray) -> np.ndarray:
     return ((high << 4) | low).astype(np.uint8).view(np.int8).reshape(rows, cols // 2)
 
 
-def pack_to_int32(codes: np.ndarray, num_bits: int = 4) -> np.ndarray:
+def pack_to_int32(codes: np.ndarray, num_bits: int = 4, packed_dim: int = 1) -> np.ndarray:
+    if packed_dim == 0:   # fields along the rows (CT's group / channel zero points)
+        return np.ascontiguousarray(pack_to_int32(np.ascontiguousarray(codes.T), num_bits).T)
     rows, cols = codes.shape
     per = 32 // num_bits
     v = (codes.astype(np.int32) + (1 << (num_bits - 1))).astype(np.uint32) & ((1 << num_bits) - 1)
@@ -48,7 +52,9 @@ def pack_to_int32(codes: np.ndarray, num_bits: int = 4) -> np.ndarray:
     return np.bitwise_or.reduce(v << shifts, axis=2).astype(np.uint32).view(np.int32)
 
 
-def unpack_from_int32(packed: np.ndarray, cols: int, num_bits: int = 4) -> np.ndarray:
+def unpack_from_int32(packed: np.ndarray, cols: int, num_bits: int = 4, packed_dim: int = 1) -> np.ndarray:
+    if packed_dim == 0:
+        return np.ascontiguousarray(unpack_from_int32(np.ascontiguousarray(packed.T), cols, num_bits).T)
     per = 32 // num_bits
     u = packed.view(np.uint32)
     shifts = (np.arange(per, dtype=np.uint32) * num_bits)

@@ -112,7 +112,12 @@ def test_save_formats(dev, tmp_path, scheme, fmt):
             oa = OArgs(num_bits=4, strategy="group", group_size=128, symmetric=False)
             codes = opack.unpack_from_int32(t[p + "weight_packed"].numpy(), lin.weight.shape[1], 4)
             assert np.array_equal(codes, _oracle_codes(lin, oa).to(torch.int8).numpy())
-            assert torch.equal(t[p + "weight_zero_point"], lin.weight_zero_point.detach().cpu())
+            zp = lin.weight_zero_point.detach().cpu()
+            packed_zp = t[p + "weight_zero_point"]
+            assert packed_zp.dtype == torch.int32 and packed_zp.shape == ((zp.shape[0] + 7) // 8, zp.shape[1])
+            assert np.array_equal(packed_zp.numpy(), opack.pack_to_int32(zp.numpy(), 4, packed_dim=0))
+            assert np.array_equal(opack.unpack_from_int32(packed_zp.numpy(), zp.shape[0], 4, packed_dim=0),
+                                  zp.numpy())
 
 
 def test_int8_packer_rewrites_int4_layers(dev, tmp_path):

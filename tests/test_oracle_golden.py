@@ -187,6 +187,14 @@ def test_int32_pack_known_vector_and_round_trip():
     assert np.array_equal(opack.pack_to_int32(codes), exp.reshape(1, 1))
     r = np.random.default_rng(0).integers(-8, 8, size=(16, 64)).astype(np.int8)
     assert np.array_equal(opack.unpack_from_int32(opack.pack_to_int32(r), 64), r)
+    # along the rows (zero points [rows, groups]): the same fields, transposed; ragged rows pad with 0
+    z = np.random.default_rng(1).integers(-8, 8, size=(13, 5)).astype(np.int8)
+    pz = opack.pack_to_int32(z, 4, packed_dim=0)
+    assert pz.shape == (2, 5)
+    assert np.array_equal(pz[:, 0:1].T, opack.pack_to_int32(np.ascontiguousarray(z[:, 0:1].T)))
+    assert np.array_equal(pz[0, :], np.stack([opack.pack_to_int32(np.ascontiguousarray(z[:8, g][None]))[0, 0]
+                                              for g in range(5)]))
+    assert np.array_equal(opack.unpack_from_int32(pz, 13, 4, packed_dim=0), z)
 
 
 def test_fp8_cast_is_torch_rne():
