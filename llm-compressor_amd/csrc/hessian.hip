@@ -362,7 +362,12 @@ constexpr int SK = 32;           // tokens per stage
 constexpr int NSTG = 4;          // stages in the LDS ring
 constexpr int SROW = 512;        // bytes per token row of a 256-feature operand
 constexpr int SOP = SK * SROW;   // bytes per operand per stage
-constexpr int SNT = 512;         // threads of the streaming kernel: 8 waves, 2 per SIMD
+// Waves of the streaming kernel.  The 4-wave layout (128 x 128 per wave, a
+// third fewer LDS reads per MFMA, one wave per SIMD) gives the same results
+// and was measured slower: 2.14 against 2.11 ms at 131072 x 4096, 76 against
+// 59 us at 2048 tokens.
+constexpr int kStreamWaves = 8;
+constexpr int SNT = 64 * kStreamWaves;             // its threads
 
 typedef short v4s16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s16_t lds_v4s16_t;
@@ -378,9 +383,16 @@ __device__ __forceinline__ bf16x8_t tr_pair(const char* lds, int off0, int off1)
 
 enum StreamMode { kDense = 0, kGrouped = 1, kGroupedGather = 2 };
 
-template <bool F16, int MODE>
-__global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
-  constexpr int MB = 4, NBN = 2;  // 32 x 32 MFMA blocks per wave: 128 rows x 64 columns
+template <bool F16, int MODE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p) {
+  // WAVES = 8: a 2 x 4 grid of waves (two per SIMD), each 4 x 2 MFMA blocks
+  // (128 rows x 64 columns); WAVES = 4: a 2 x 2 grid (one per SIMD), each
+  // 4 x 4 blocks (128 x 128), a third fewer LDS reads per MFMA
+  constexpr int MB = 4, NBN = WAVES == 8 ? 2 : 4;
+  constexpr int NTH = 64 * WAVES;
+  constexpr int RPW = 32 / WAVES;   // token rows per operand and stage each wave copies
+  constexpr int NJ = RPW / 2;       // DMA instructions per operand and stage (two rows each)
+  constexpr int NDMA = 2 * NJ;
   using C = Cfg<256>;
   constexpr int TM = 256;
   // LDS ring: operand A in stages 0..3, then operand B; after the loop it
@@ -400,7 +412,7 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = WAVES == 8 ? wave >> 2 : wave >> 1, wn = WAVES == 8 ? wave & 3 : wave & 1;
 
   // work item: tile t, token split s (and, for dense tail tiles, part `part`
   // of tail_f equal pieces of that split), partial slot
@@ -457,23 +469,23 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   const int64_t nst = st_end > st_begin ? st_end - st_begin : 0;
 
   if constexpr (MODE == kGroupedGather) {
-    for (int i = tid; i < (int)n; i += SNT) {
+    for (int i = tid; i < (int)n; i += NTH) {
       const int64_t r = p.rows[mat.row_begin + i];
       ridx[i] = (int)(r < 0 ? 0 : (r >= p.n_x ? p.n_x - 1 : r));
     }
     __syncthreads();
   }
 
-  // DMA roles: wave w copies token rows 4 w .. 4 w + 3 of each operand, two
-  // rows (1 KB) per instruction j; lane L fills LDS position L & 31 of row
-  // 4 w + 2 j + L / 32 with global chunk (L & 31) ^ 4 (row & 3).
+  // DMA roles: wave w copies token rows RPW w .. RPW w + RPW - 1 of each
+  // operand, two rows (1 KB) per instruction j; lane L fills LDS position
+  // L & 31 of row RPW w + 2 j + L / 32 with global chunk (L & 31) ^ 4 (row & 3).
   const int64_t fa0 = (int64_t)ti * TM, fb0 = (int64_t)tj * TM;
   const bool edge = fa0 + TM > p.d || fb0 + TM > p.d;
-  uint32_t doff[2];    // lane byte offsets from the stage's first token row
-  int drow[2], dchunk[2];
+  uint32_t doff[NJ];    // lane byte offsets from the stage's first token row
+  int drow[NJ], dchunk[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int row = 4 * wave + 2 * j + (lane >> 5);
+  for (int j = 0; j < NJ; ++j) {
+    const int row = RPW * wave + 2 * j + (lane >> 5);
     const int chunk = (lane & 31) ^ (4 * (row & 3));
     drow[j] = row;
     dchunk[j] = chunk;
@@ -488,7 +500,7 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   // addresses, with lanes past n or d sent to a zero chunk.  M0 (the LDS
   // destination of the wave's 1 KB) is formed in scalar registers.
   auto lds_u32 = [](const char* ptr) { return (uint32_t)reinterpret_cast<uintptr_t>((lds_void_t*)ptr); };
-  const uint32_t wave_lds = (uint32_t)wave * 2048u;
+  const uint32_t wave_lds = (uint32_t)wave * (RPW * SROW);
   const uint32_t sa[4] = {lds_u32(a0) + wave_lds, lds_u32(a1) + wave_lds, lds_u32(a2) + wave_lds,
                           lds_u32(a3) + wave_lds};
   const uint32_t sb[4] = {lds_u32(b0) + wave_lds, lds_u32(b1) + wave_lds, lds_u32(b2) + wave_lds,
@@ -505,7 +517,7 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   // stages [0, nwhole) hold SK tokens
   const int64_t nwhole = (n - st_begin * SK) / SK;
   const bool fast_ok = MODE != kGroupedGather && !edge;
-  // Per-lane global addresses of the 4 DMAs of a stage (A0, B0, A1, B1):
+  // Per-lane global addresses of the NDMA DMAs of a stage (A0, B0, A1, B1, ...):
   // lanes past n or d read the zero chunk.
   auto dma_addrs = [&](int64_t stage, const void** ad) __attribute__((always_inline)) {
     const int64_t sc = stage < nst ? stage : nst - 1;
@@ -513,7 +525,7 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     if constexpr (MODE == kGroupedGather) {
       const char* xg = reinterpret_cast<const char*>(p.x);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const int lt = (int)t0 + drow[j];
         const bool rok = lt < n;
         const char* xr = xg + (int64_t)ridx[rok ? lt : 0] * p.ldx * 2 + (int64_t)dchunk[j] * 16;
@@ -528,13 +540,13 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
       const char* xb = xs + fb0 * 2;
       if (fast_ok && sc < nwhole) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NJ; ++j) {
           ad[2 * j] = xa + doff[j];
           ad[2 * j + 1] = xb + doff[j];
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NJ; ++j) {
           const bool rok = t0 + drow[j] < n;
           const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
           const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
@@ -549,15 +561,15 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     if (fast_ok && sc < nwhole) {
       const char* xs = xbase + sc * sbytes;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         dma_s(doff[j], xs + fa0 * 2, sa[slot] + 1024u * j);
         dma_s(doff[j], xs + fb0 * 2, sb[slot] + 1024u * j);
       }
     } else {
-      const void* ad[4];
+      const void* ad[NDMA];
       dma_addrs(stage, ad);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
+      for (int i = 0; i < NDMA; ++i) dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
     }
   };
 
@@ -607,11 +619,11 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
       for (int y = 0; y < NBN; ++y)
         acc[x][y] = mfma16<F16>(fa[x], fb[y], acc[x][y]);
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
+    for (int i = 0; i < MB + NBN; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, MB * NBN - (MB + NBN), 0);
   };
   // Step MFMAs with the next step's reads and one DMA after every two MFMAs.
   // A burst of DMAs right after the barrier stalls the issuing wave until the
@@ -625,7 +637,12 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
       const int x = i / NBN, y = i % NBN;
       acc[x][y] = mfma16<F16>(fa[x], fb[y], acc[x][y]);
       if (i < MB + NBN) read_op(la, lb, kk, i, na, nb);
-      if (i < 4) dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
+      if constexpr (WAVES == 8) {
+        if (i < 4) dma_v(ad[i], ((i & 1) ? sb[slot] : sa[slot]) + 1024u * (i >> 1));
+      } else if ((i & 1) == 0) {
+        const int k = i >> 1;
+        dma_v(ad[k], ((k & 1) ? sb[slot] : sa[slot]) + 1024u * (k >> 1));
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -637,10 +654,13 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
   // for the DMA of stage st + 2.)
   auto stage = [&](int64_t st, int cur, const char* la, const char* lb, const char* lan, const char* lbn)
       __attribute__((always_inline)) {
-    const void* ad[4];
+    const void* ad[NDMA];
     dma_addrs(st + 3, ad);
     half(fa0r, fb0r, la, lb, 1, fa1r, fb1r);
-    asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+    if constexpr (NDMA == 4)
+      asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
     half_dma(fa1r, fb1r, lan, lbn, 0, fa0r, fb0r, ad, (cur + 3) & 3);
   };
 
@@ -648,7 +668,10 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     issue(0, 0);
     issue(1, 1);
     issue(2, 2);
-    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    if constexpr (NDMA == 4)
+      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (int i = 0; i < MB + NBN; ++i) read_op(a0, b0, 0, i, fa0r, fb0r);
     for (int64_t st = 0; st < nst; st += 4) {
@@ -667,10 +690,10 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
       // direct update of the upper triangle of H through the LDS ring, one
       // half of the tile (128 rows, the accumulators of waves wm == hh) at a
       // time: the accumulators are written row-major into LDS, then wave w
-      // updates rows 16 w .. 16 w + 15 of the half, one 256-float row (1 KB,
-      // a float4 per lane) per load and store, all 16 loads in flight
-      // together.  A float4 that straddles the diagonal writes its lower
-      // elements back unchanged.
+      // updates rows RR w .. RR w + RR - 1 of the half (RR = 128 / WAVES),
+      // one 256-float row (1 KB, a float4 per lane) per load and store, all
+      // RR loads in flight together.  A float4 that straddles the diagonal
+      // writes its lower elements back unchanged.
       float* const tile = reinterpret_cast<float*>(ring);
       const int64_t gj = fb0 + 4 * lane;
 #pragma unroll
@@ -683,28 +706,32 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
             for (int y = 0; y < NBN; ++y)
 #pragma unroll
               for (int r = 0; r < 16; ++r)
-                tile[(x * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 256 + wn * 64 + y * 32 + (lane & 31)] =
-                    acc[x][y][r];
+                tile[(x * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 256 + wn * NBN * 32 + y * 32 +
+                     (lane & 31)] = acc[x][y][r];
         }
         __syncthreads();
-        f32x4_t hv[16];
+        constexpr int RR = 128 / WAVES;   // rows per wave, in batches of 16 loads
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          const int64_t gi = fa0 + hh * 128 + wave * 16 + k;
-          const bool ok = gi < p.d && gj < p.d && (!diag || gi <= gj + 3);
-          hv[k] = ok ? *reinterpret_cast<const f32x4_t*>(mat.h + gi * ldh + gj) : f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int k0 = 0; k0 < RR; k0 += 16) {
+          f32x4_t hv[16];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          const int lr = wave * 16 + k;
-          const int64_t gi = fa0 + hh * 128 + lr;
-          if (gi < p.d && gj < p.d && (!diag || gi <= gj + 3)) {
-            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(tile + lr * 256 + 4 * lane);
-            f32x4_t o;
+          for (int k = 0; k < 16; ++k) {
+            const int64_t gi = fa0 + hh * 128 + wave * RR + k0 + k;
+            const bool ok = gi < p.d && gj < p.d && (!diag || gi <= gj + 3);
+            hv[k] = ok ? *reinterpret_cast<const f32x4_t*>(mat.h + gi * ldh + gj) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+          }
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-              o[c] = (!diag || gi <= gj + c) ? scaled(hv[k][c], p.beta) + p.alpha * v[c] : hv[k][c];
-            *reinterpret_cast<f32x4_t*>(mat.h + gi * ldh + gj) = o;
+          for (int k = 0; k < 16; ++k) {
+            const int lr = wave * RR + k0 + k;
+            const int64_t gi = fa0 + hh * 128 + lr;
+            if (gi < p.d && gj < p.d && (!diag || gi <= gj + 3)) {
+              const f32x4_t v = *reinterpret_cast<const f32x4_t*>(tile + lr * 256 + 4 * lane);
+              f32x4_t o;
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                o[c] = (!diag || gi <= gj + c) ? scaled(hv[k][c], p.beta) + p.alpha * v[c] : hv[k][c];
+              *reinterpret_cast<f32x4_t*>(mat.h + gi * ldh + gj) = o;
+            }
           }
         }
       }
@@ -718,7 +745,7 @@ __global__ __launch_bounds__(SNT, 1) void syrk_stream_kernel(SyrkParams p) {
     for (int x = 0; x < MB; ++x)
 #pragma unroll
       for (int y = 0; y < NBN; ++y) {
-        const int mb = wm * 128 + x * 32, nb = wn * 64 + y * 32;
+        const int mb = wm * 128 + x * 32, nb = wn * NBN * 32 + y * 32;
         const int64_t gib = fa0 + mb, gjb = fb0 + nb;
         float* hb = mat.h + gib * ldh + gjb;
 #pragma unroll
@@ -759,18 +786,21 @@ constexpr int RED_CPW = 4;  // chunks per wave of the streaming reduction
 
 // H (upper triangle of tile (ti, tj)) = beta H + alpha tot for the RED_CPW
 // slot chunks ch0 .. ch0 + RED_CPW - 1 of this lane: chunk -> wave (wm, wn)
-// of the 2 x 4 layout, block (x, y), registers 4 r4 + q
+// of the stream kernel's layout (2 x 4 waves of 4 x 2 blocks, or 2 x 2 of
+// 4 x 4), block (x, y), registers 4 r4 + q
+template <int WAVES>
 __device__ __forceinline__ void stream_update_h(const f32x4_t* tot, int ch0, int lane, int ti, int tj, float* hm,
                                                 int64_t d, int64_t ldh, float alpha, float beta) {
-  constexpr int TM = 256, MB = 4, NBN = 2;
+  constexpr int TM = 256, MB = 4, NBN = WAVES == 8 ? 2 : 4, WN = WAVES == 8 ? 4 : 2;
+  constexpr int PER_W = MB * NBN * 4;   // chunks per wave
   int64_t gi[RED_CPW], gj[RED_CPW];
   float h[RED_CPW][4];
 #pragma unroll
   for (int c = 0; c < RED_CPW; ++c) {
     const int ch = ch0 + c;
-    const int w = ch >> 5, x = (ch >> 3) & (MB - 1), y = (ch >> 2) & (NBN - 1), r4 = ch & 3;
-    gi[c] = (int64_t)ti * TM + (w >> 2) * 128 + x * 32 + 8 * r4 + 4 * (lane >> 5);
-    gj[c] = (int64_t)tj * TM + (w & 3) * 64 + y * 32 + (lane & 31);
+    const int w = ch / PER_W, x = (ch / (NBN * 4)) % MB, y = (ch >> 2) % NBN, r4 = ch & 3;
+    gi[c] = (int64_t)ti * TM + (w / WN) * 128 + x * 32 + 8 * r4 + 4 * (lane >> 5);
+    gj[c] = (int64_t)tj * TM + (w % WN) * (NBN * 32) + y * 32 + (lane & 31);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       h[c][q] = (gi[c] + q < d && gj[c] < d && gi[c] + q <= gj[c]) ? hm[(gi[c] + q) * ldh + gj[c]] : 0.f;
@@ -783,11 +813,12 @@ __device__ __forceinline__ void stream_update_h(const f32x4_t* tot, int ch0, int
         hm[(gi[c] + q) * ldh + gj[c]] = scaled(h[c][q], beta) + alpha * tot[c][q];
 }
 
+template <int WAVES>
 __global__ __launch_bounds__(NT) void syrk_stream_reduce_kernel(const float* __restrict__ ws, int S,
                                                                 int tail_start, int tail_f, Matrix single,
                                                                 int64_t d, int64_t ldh, int nt, float alpha,
                                                                 float beta) {
-  constexpr int TM = 256, TILE = TM * TM, MB = 4, NBN = 2;
+  constexpr int TM = 256, TILE = TM * TM;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x;
   int ti, tj;
@@ -835,11 +866,12 @@ __global__ __launch_bounds__(NT) void syrk_stream_reduce_kernel(const float* __r
       }
     }
   }
-  stream_update_h(tot, ch0, lane, ti, tj, single.h, d, ldh, alpha, beta);
+  stream_update_h<WAVES>(tot, ch0, lane, ti, tj, single.h, d, ldh, alpha, beta);
 }
 
 // Grouped: adds the later chunks' slots of (expert, tile) to H in chunk
 // order (workgroup x: item x / T, tile x % T; y: 16-chunk group as above).
+template <int WAVES>
 __global__ __launch_bounds__(NT) void syrk_group_reduce_kernel(const float* __restrict__ ws,
                                                                const GReduce* __restrict__ reds,
                                                                const int* __restrict__ gcounts, int T, int nt,
@@ -872,7 +904,7 @@ __global__ __launch_bounds__(NT) void syrk_group_reduce_kernel(const float* __re
 #pragma unroll
           for (int q = 0; q < 4; ++q) tot[c][q] += v[k][c][q];
   }
-  stream_update_h(tot, ch0, lane, ti, tj, h0 + (int64_t)rd.e * h_stride, d, d, alpha, 1.f);
+  stream_update_h<WAVES>(tot, ch0, lane, ti, tj, h0 + (int64_t)rd.e * h_stride, d, d, alpha, 1.f);
 }
 
 // Builds the grouped chunk table from the expert offsets (one workgroup of
@@ -1055,7 +1087,7 @@ DensePlan plan_dense(int64_t n, int64_t d) {
 template <bool F16>
 void launch_syrk_t(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
   if (tile_edge(d) == 256) {
-    hipLaunchKernelGGL((syrk_stream_kernel<F16, kDense>), dim3(grid), dim3(SNT), 0, st, p);
+    hipLaunchKernelGGL((syrk_stream_kernel<F16, kDense, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
   } else {
     hipLaunchKernelGGL((syrk_bf16_kernel<128, F16>), dim3(grid), dim3(NT), 0, st, p);
   }
@@ -1138,7 +1170,7 @@ int hessian16_impl(const void* x_dev, bool f16, int64_t n_tokens, int64_t d, int
   MQ_LAUNCH_CHECK();
   if (S > 1) {
     if (tile_edge(d) == 256)  // the streaming kernel's slots
-      hipLaunchKernelGGL(syrk_stream_reduce_kernel, dim3((unsigned)T, 256 / ((NT / 64) * RED_CPW)), dim3(NT), 0,
+      hipLaunchKernelGGL(syrk_stream_reduce_kernel<kStreamWaves>, dim3((unsigned)T, 256 / ((NT / 64) * RED_CPW)), dim3(NT), 0,
                          st, p.ws, S, pl.tail_start, pl.tail_f, p.single, d, ldh, nt, alpha, beta);
     else
       launch_reduce(p.ws, S, p.single, d, ldh, nt, alpha, beta, (unsigned)T, st);
@@ -1267,15 +1299,15 @@ extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype
   const unsigned grid = (unsigned)(8 * ((items + 7) / 8));
   const bool f16 = dtype == MI355Q_F16;
   if (rows_dev) {
-    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGroupedGather>), dim3(grid), dim3(SNT), 0, st, p);
-    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGroupedGather>), dim3(grid), dim3(SNT), 0, st, p);
+    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGroupedGather, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
+    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGroupedGather, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
   } else {
-    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGrouped>), dim3(grid), dim3(SNT), 0, st, p);
-    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGrouped>), dim3(grid), dim3(SNT), 0, st, p);
+    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGrouped, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
+    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGrouped, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
   }
   MQ_LAUNCH_CHECK();
   if (gb.max_reduce > 0) {
-    hipLaunchKernelGGL(syrk_group_reduce_kernel, dim3((unsigned)(gb.max_reduce * gb.T), 256 / ((NT / 64) * RED_CPW)),
+    hipLaunchKernelGGL(syrk_group_reduce_kernel<kStreamWaves>, dim3((unsigned)(gb.max_reduce * gb.T), 256 / ((NT / 64) * RED_CPW)),
                        dim3(NT), 0, st, p.ws, reds, counts, gb.T, p.nt, d, h_dev, h_stride, alpha);
     MQ_LAUNCH_CHECK();
   }

@@ -24,6 +24,9 @@ struct GemmArgs {
   // B lower (B[k][j] = 0 for k < j) limits each tile's K range to where the
   // operand can be nonzero
   int a_lower, b_lower;
+  // C is A itself (same rows, ldc == lda): every workgroup must own whole
+  // rows of C, so N fits one column tile and B is transposed
+  int in_place;
 };
 
 // Launches the batched GEMM (batch = total number of products) on `stream`;

@@ -461,6 +461,82 @@ __global__ __launch_bounds__(GNT, 2) void gemm_k128_small_kernel(GemmArgs g) {
   }
 }
 
+// In-place K = N = 128 products C = alpha A B^T with C the rows of A (the
+// Cholesky panel solve F[r, k0:k0+128] <- F[r, k0:k0+128] linv^T).  Each
+// workgroup owns whole rows of C - a 32 x 128 tile, all of N - and has read
+// all of its A rows before any of its waves writes, so no workgroup reads
+// what another one overwrites.  (Two 64-column tiles per row tile would let
+// one workgroup overwrite rows its neighbour had not read yet, which happens
+// whenever the two do not run at the same time.)  Four waves, each a 32 x 32
+// quadrant; A [row][k] and B [n][k] in LDS, 82.6 KB.
+constexpr int RT = 32;           // rows per workgroup
+
+__global__ __launch_bounds__(GNT, 1) void gemm_k128_rows_kernel(GemmArgs g) {
+  __shared__ float la[RT * KLA];
+  __shared__ float lb[KT * KLA];
+  {
+    const int64_t bz = blockIdx.z;
+    const int64_t b1 = g.inner > 0 ? bz % g.inner : bz, b2 = g.inner > 0 ? bz / g.inner : 0;
+    g.A += b1 * g.strideA + b2 * g.strideA2;
+    g.B += b1 * g.strideB + b2 * g.strideB2;
+    g.C += b1 * g.strideC + b2 * g.strideC2;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
+  const int64_t m0 = (int64_t)blockIdx.y * RT;
+  auto at = [](const float* base, uint32_t off) {
+    return reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off);
+  };
+  // float4 v of a [row][k] tile covers row 8 v + tid / 32, k 4 (tid % 32)
+  f32x4_t ra[RT / 8], rb[KT / 8];
+  {
+    const uint32_t off_a = (uint32_t)((tid >> 5) * g.lda + 4 * (tid & 31)) * 4u;
+    const float* pa = g.A + m0 * g.lda;
+#pragma unroll
+    for (int v = 0; v < RT / 8; ++v) ra[v] = *reinterpret_cast<const f32x4_t*>(at(pa + 8 * v * g.lda, off_a));
+    const uint32_t off_b = (uint32_t)((tid >> 5) * g.ldb + 4 * (tid & 31)) * 4u;
+#pragma unroll
+    for (int v = 0; v < KT / 8; ++v) rb[v] = *reinterpret_cast<const f32x4_t*>(at(g.B + 8 * v * g.ldb, off_b));
+  }
+  const uint32_t off_c = (uint32_t)(4 * (lane >> 5) * g.ldc + wn * 32 + (lane & 31)) * 4u;
+  float* cbase = g.C + m0 * g.ldc;
+  float cv[16];
+  if (g.beta != 0.f) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cv[r] = *at(cbase + (8 * (r >> 2) + (r & 3)) * g.ldc, off_c);
+  }
+  {
+    const int row = tid >> 5, k4 = 4 * (tid & 31);
+#pragma unroll
+    for (int v = 0; v < RT / 8; ++v)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) la[(8 * v + row) * KLA + k4 + e] = ra[v][e];
+#pragma unroll
+    for (int v = 0; v < KT / 8; ++v)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lb[(8 * v + row) * KLA + k4 + e] = rb[v][e];
+  }
+  __syncthreads();   // every A row of this tile is read before any C row is written
+
+  f32x16_t acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
+  const float* pa = la + (lane & 31) * KLA + (lane >> 5);
+  const float* pb = lb + (wn * 32 + (lane & 31)) * KLA + (lane >> 5);
+#pragma unroll
+  for (int kk = 0; kk < KT / 2; kk += 2) {
+    const float a0 = pa[2 * kk], a1 = pa[2 * kk + 2];
+    const float b0 = pb[2 * kk], b1 = pb[2 * kk + 2];
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc1, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float prod = g.alpha * (acc0[r] + acc1[r]);
+    const float out = g.beta == 0.f ? prod : g.beta * cv[r] + prod;
+    *const_cast<float*>(at(cbase + (8 * (r >> 2) + (r & 3)) * g.ldc, off_c)) = out;
+  }
+}
+
 // ---------------------------------------------------------------- large-K GEMM
 // The solve's products with K >= 256 (GPTQ mid- and super-block lazy
 // updates, the Cholesky chain's rank-512 trailing updates, the triangular
@@ -1196,6 +1272,25 @@ HinvLayout hinv_layout(int64_t d) {
 
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
+  if (g.in_place) {
+    // one workgroup per row tile: the whole-row K = 128 kernel, else the
+    // general kernel (N <= GBN: a single column tile)
+    MQ_CHECK_ARG(b_trans && !g.a_trans && !g.upper_only && !g.lower_only && !g.a_lower && !g.b_lower &&
+                     g.N <= GBN && batch <= 65535,
+                 "gemm: an in-place product takes B transposed, N <= %d and no triangular options", GBN);
+    const bool strides16 = g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 && g.strideB2 % 4 == 0;
+    if (g.K == KT && g.N == KT && g.M % RT == 0 && g.M / RT <= 65535 && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+        aligned16(g.A) && aligned16(g.B) && (batch == 1 || strides16) && (g.lda * 7 + KT) < (1 << 29) &&
+        (g.ldb * 7 + KT) < (1 << 29) && (g.ldc * 31 + KT) < (1 << 29)) {
+      hipLaunchKernelGGL(gemm_k128_rows_kernel, dim3(1, (unsigned)(g.M / RT), (unsigned)batch), dim3(GNT), 0,
+                         stream, g);
+    } else {
+      hipLaunchKernelGGL((gemm_f32_kernel<true, false>), dim3(1, (unsigned)((g.M + GBM - 1) / GBM), (unsigned)batch),
+                         dim3(GNT), 0, stream, g);
+    }
+    MQ_LAUNCH_CHECK();
+    return MI355Q_OK;
+  }
   if (g.a_trans || g.upper_only) {   // the general kernel only
     MQ_CHECK_ARG(batch <= 65535 && !g.a_lower && !g.b_lower && !g.lower_only,
                  "gemm: transposed-A / upper-only products take no triangular options");
@@ -1373,7 +1468,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       p.A = F + (k0 + nb) * d + k0; p.lda = d; p.strideA = wsf;
       p.B = linv + kb * NB * NB; p.ldb = NB; p.strideB = wsf;
       p.C = F + (k0 + nb) * d + k0; p.ldc = d; p.strideC = wsf;
-      p.M = rest; p.N = nb; p.K = nb; p.alpha = 1.f; p.beta = 0.f;
+      p.M = rest; p.N = nb; p.K = nb; p.alpha = 1.f; p.beta = 0.f; p.in_place = 1;
       int rc = gemm_f32(p, true, (int)batch, st);
       if (rc) return rc;
       // inside the outer panel: F[k0+nb:, k0+nb:c_end] -= P P[:c_end-k0-nb]^T (lower)

@@ -57,3 +57,31 @@ def test_two_threads_two_streams_match_sequential(dev):
     for i in range(2):
         for a, b in zip(out[i], seq[i]):
             assert torch.equal(a, b), i
+
+
+def test_hinv_beside_a_busy_stream_is_unchanged(dev):
+    """The Cholesky panel solve overwrites the panel in place; every
+    workgroup owns whole rows of it, so the result must not depend on which
+    workgroups run together.  Here a second stream keeps the CUs busy with
+    Hessian accumulations while the solve runs, which scatters the solve's
+    workgroups in time; the inverse must stay bit-identical to a solo run."""
+    print("gptq_hinv d=4096 beside Hessian accumulations on a second stream", flush=True)
+    d = 4096
+    X = workloads.heavy_tailed_activations((8192, d), seed=91).to(dev)
+    H = torch.zeros(d, d, device=dev)
+    ops.hessian_syrk_(H, X, alpha=2.0)
+    ref, _, ok = ops.gptq_hinv(H, None, float(X.shape[0]), 0.01)
+    assert ok
+    Xb = torch.randn(65536, d, device=dev, generator=torch.Generator(device=dev).manual_seed(92)).to(torch.bfloat16)
+    Hb = torch.zeros(d, d, device=dev)
+    busy, main = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        with torch.cuda.stream(busy):
+            for _ in range(4):
+                ops.hessian_syrk_(Hb, Xb, alpha=1.0)
+        with torch.cuda.stream(main):
+            got, _, ok = ops.gptq_hinv(H, None, float(X.shape[0]), 0.01)
+        torch.cuda.synchronize()
+        assert ok
+        assert torch.equal(got, ref), (rep, (got - ref).abs().max().item())
