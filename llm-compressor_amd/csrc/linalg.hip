@@ -916,30 +916,46 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
     float v[SB];
 #pragma unroll
     for (int c = 0; c < SB; ++c) v[c] = row_role ? a[(o + li) * LP + o + c] : ((c == li) ? 1.f : 0.f);
-#pragma unroll
-    for (int j = 0; j < SB; ++j) {
-      // every lane stores (column-role lanes into a scratch slot): no
-      // divergent branch around the LDS write that the reads could sink into
-      cb[lane] = v[j];
-      // only col[j..SB-1] is used: read the aligned quads that cover it
-      float col[SB];
+    // every lane stores (column-role lanes into a scratch slot): no
+    // divergent branch around the LDS write that the reads could sink into.
+    // Only col[j..SB-1] is used: the reads cover the aligned quads of it.
+    float col[SB];
+    auto read_col = [&](int j, float* c) __attribute__((always_inline)) {
 #pragma unroll
       for (int q = j / 4; q < SB / 4; ++q) {
         const f32x4_t w = *reinterpret_cast<const f32x4_t*>(cb + 4 * q);
-        col[4 * q] = w[0];
-        col[4 * q + 1] = w[1];
-        col[4 * q + 2] = w[2];
-        col[4 * q + 3] = w[3];
+        c[4 * q] = w[0];
+        c[4 * q + 1] = w[1];
+        c[4 * q + 2] = w[2];
+        c[4 * q + 3] = w[3];
       }
+    };
+    cb[lane] = v[0];
+    read_col(0, col);
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
       const float piv = col[j];
       pmin = fminf(pmin, piv);
       pnan += piv - piv;
       const float rl = __builtin_amdgcn_rsqf(piv);
       const float sj = v[j] * rl;
       const float m = sj * rl;
+      // software pipeline: the next column is updated, written and read
+      // back first, so the LDS round trip overlaps this step's other updates
+      float ncol[SB];
+      if (j + 1 < SB) {
+        v[j + 1] = fmaf(-m, col[j + 1], v[j + 1]);
+        cb[lane] = v[j + 1];
+        read_col(j + 1, ncol);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-      for (int k = j + 1; k < SB; ++k) v[k] = fmaf(-m, col[k], v[k]);
+      for (int k = j + 2; k < SB; ++k) v[k] = fmaf(-m, col[k], v[k]);
       v[j] = sj;
+      // (keeps the next step's chain from being scheduled into these updates)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = j + 1; k < SB; ++k) col[k] = ncol[k];
     }
     // column li of the sub-block inverse, zeros above the diagonal included
     if (!row_role) {
@@ -1308,9 +1324,13 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   }
   // K >= 256: the LDS-DMA kernel with a two-stage ring (two or three
   // workgroups per CU).  Tile shapes as measured best on the solve's
-  // products: 64 x 128 for plain products (118 TFLOP/s on 4096 x 3072 x
-  // 1024), 64 x 64 with a triangular operand, lower-only products 128 x 64
-  // above 2048 rows, else 64 x 64.
+  // products: plain products 128 x 128 on eight waves when one product
+  // fills the CUs at least once (117 TFLOP/s on 4096 x 3072 x 1024, against
+  // 98 for 64 x 128), else 64 x 128 (also for batches: the MoE experts' solves
+  // ran 6 % slower on the larger tile); 64 x 64 with a triangular operand;
+  // lower-only products 64 x 64 up to 4096 rows (the rank-512 Cholesky
+  // updates of 512 .. 3584 rows: within 5 % of the best of six shapes at
+  // every size), 128 x 64 above, and for batches above 2048 rows in total.
   const bool v16 = g.K % 4 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && aligned16(g.A) && aligned16(g.B) &&
                    (b_trans || g.N % 4 == 0) && g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 &&
                    g.strideB2 % 4 == 0;
@@ -1326,8 +1346,11 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
     if (g.a_lower || g.b_lower) {
       MQ_DMA(64, 64, 2, 2);        // uneven K ranges: small tiles, the longest dispatched first
     } else if (!g.lower_only) {
-      MQ_DMA(64, 128, 2, 2);
-    } else if (g.M * batch > 2048) {
+      if (batch == 1 && ((g.M + 127) / 128) * ((g.N + 127) / 128) >= 256)
+        MQ_DMA(128, 128, 2, 4);
+      else
+        MQ_DMA(64, 128, 2, 2);
+    } else if (g.M * batch > (batch > 1 ? 2048 : 4096)) {
       MQ_DMA(128, 64, 2, 2);
     } else {
       MQ_DMA(64, 64, 2, 2);
