@@ -46,6 +46,19 @@ def _is_linear_like(module) -> bool:
     return type(module).__name__ == "Conv1D"  # transformers.Conv1D
 
 
+def hessian_rows(inp: torch.Tensor, module: torch.nn.Module, device) -> tuple[torch.Tensor, int]:
+    """The 2-D rows of one accumulation call on ``device`` and the
+    reference's sample count for it: the leading dimension after a 2-D input
+    is unsqueezed to 3-D (``gptq_quantize.py:72-80``)."""
+    if inp.device != device:
+        inp = inp.to(device=device)
+    if inp.dim() == 2:
+        inp = inp.unsqueeze(0)
+    if not _is_linear_like(module):
+        raise NotImplementedError(f"GPTQ Hessian for {type(module).__name__} is not provided by this build")
+    return inp.reshape(-1, inp.shape[-1]), inp.shape[0]
+
+
 def accumulate_hessian(inp: torch.Tensor, module: torch.nn.Module, H: torch.Tensor,
                        num_samples: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """H += 2 * X^T X over the rows of ``inp`` (upper triangle, in place).
@@ -53,13 +66,7 @@ def accumulate_hessian(inp: torch.Tensor, module: torch.nn.Module, H: torch.Tens
     ``num_samples`` grows by the leading dimension after a 2-D input is
     unsqueezed to 3-D, exactly as the reference counts it.
     """
-    inp = inp.to(device=H.device)
-    if inp.dim() == 2:
-        inp = inp.unsqueeze(0)
-    num_added = inp.shape[0]
-    if not _is_linear_like(module):
-        raise NotImplementedError(f"GPTQ Hessian for {type(module).__name__} is not provided by this build")
-    x = inp.reshape(-1, inp.shape[-1])
+    x, num_added = hessian_rows(inp, module, H.device)
     num_samples += num_added
     if x.shape[0] > 0:
         ops.hessian_syrk_(H, x, alpha=2.0)

@@ -8,7 +8,9 @@ These mirror the reference's modifiers at the level the hot path needs
   targeted ``nn.Linear`` (``QuantizationMixin.initialize_quantization``);
 * ``on_calibration_start``: register the ``calibrate_module`` forward hook
   (``base.py:255-289``) that lazily creates H and ``num_samples`` and calls
-  ``accumulate_hessian``;
+  ``accumulate_hessian`` - here through a ``staging.HessianStage`` that
+  gathers calls of up to ``hessian_batch_tokens / 2`` rows into one syrk
+  (0 turns it off; so does ``offload_hessians``);
 * ``on_sequential_epoch_end``: ``observe(weight)`` then ``compress_modules``
   -> ``quantize_weight`` on H / num_samples (``base.py:578-601``), writing
   ``weight`` / ``weight_scale`` / ``weight_zero_point`` / ``weight_g_idx``;
@@ -33,7 +35,10 @@ import torch
 
 from .calibration import initialize_module_for_quantization, initialize_observer, observe, update_qparams
 from . import sparsegpt as sgpt
-from .gptq import _effective_actorder, accumulate_hessian, gptq_quantize, make_empty_hessian, prepare_hessian
+from . import ops
+from .gptq import (_effective_actorder, accumulate_hessian, gptq_quantize, hessian_rows, make_empty_hessian,
+                   prepare_hessian)
+from .staging import DEFAULT_TOKENS, HessianStage
 from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationScheme, preset_name_to_scheme
 
 logger = logging.getLogger("llmcompressor_amd")
@@ -193,12 +198,15 @@ class _SharedHessians:
 class GPTQModifier(QuantizationModifier, _SharedHessians):
     def __init__(self, scheme=None, targets=("Linear",), ignore=("lm_head",), config_groups=None,
                  block_size: int = 128, dampening_frac: float | None = 0.01, actorder="static",
-                 offload_hessians: bool = False, share_hessians: bool = True):
+                 offload_hessians: bool = False, share_hessians: bool = True,
+                 hessian_batch_tokens: int = DEFAULT_TOKENS):
         super().__init__(scheme, targets, ignore, config_groups)
         self.block_size = block_size
         self.dampening_frac = dampening_frac
         self.actorder = actorder
         self.offload_hessians = offload_hessians
+        self.hessian_batch_tokens = hessian_batch_tokens
+        self._stages: dict = {}
         # modules sharing an input also share one Cholesky chain per
         # activation ordering at compression
         self._init_sharing(share_hessians)
@@ -234,12 +242,33 @@ class GPTQModifier(QuantizationModifier, _SharedHessians):
             self._hessians[module] = make_empty_hessian(module, device="cpu" if self.offload_hessians else dev)
             self._num_samples[module] = torch.zeros(tuple(), device=dev)
         H = self._hessians[module]
-        if self.offload_hessians:
-            H = H.to(module.weight.device)
-        H, self._num_samples[module] = accumulate_hessian(inp, module, H, self._num_samples[module])
-        self._hessians[module] = H.to("cpu") if self.offload_hessians else H
+        if self.offload_hessians or not self.hessian_batch_tokens:
+            if self.offload_hessians:
+                H = H.to(module.weight.device)
+            H, self._num_samples[module] = accumulate_hessian(inp, module, H, self._num_samples[module])
+            self._hessians[module] = H.to("cpu") if self.offload_hessians else H
+        else:
+            x, added = hessian_rows(inp, module, H.device)
+            st = self._stages.get(module)
+            if st is None:
+                st = self._stages[module] = HessianStage(self.hessian_batch_tokens)
+            st.add(x, added, lambda rows, samples: self._accumulate(module, H, rows, samples))
         if self.share_hessians:
             self._note_accumulated(module, inp, self._modules.get)
+
+    def _accumulate(self, module, H, rows, samples):
+        # the sample count grows with the rows it counts (one device add per
+        # syrk instead of one per forward pass)
+        ops.hessian_syrk_(H, rows, alpha=2.0)
+        self._num_samples[module] += samples
+
+    def _flush(self, module):
+        """Accumulates the rows still staged for ``module``'s Hessian."""
+        st = self._stages.pop(module, None)
+        if st is not None:
+            H = self._hessians[module]
+            st.flush(lambda rows, samples: self._accumulate(module, H, rows, samples))
+            st.release()
 
     def on_calibration_start(self, model):
         for m in self._modules:
@@ -256,6 +285,7 @@ class GPTQModifier(QuantizationModifier, _SharedHessians):
 
     def compress_modules(self):
         for leader, members in self._take_groups(self._modules.get).items():
+            self._flush(leader)
             n = float(self._num_samples[leader].item())
             H = self._hessians.pop(leader).to(leader.weight.device)
             prepared: dict = {}
@@ -331,8 +361,12 @@ class SparseGPTModifier(_SharedHessians):
     def __init__(self, sparsity=None, sparsity_profile: str | None = None, mask_structure: str = "0:0",
                  owl_m: int | None = None, owl_lmbda: float | None = None, targets=("Linear",), ignore=(),
                  block_size: int = 128, dampening_frac: float | None = 0.01, preserve_sparsity_mask: bool = False,
-                 offload_hessians: bool = False, share_hessians: bool = True):
+                 offload_hessians: bool = False, share_hessians: bool = True,
+                 hessian_batch_tokens: int = DEFAULT_TOKENS):
         self._init_sharing(share_hessians)
+        self.hessian_batch_tokens = hessian_batch_tokens
+        self._stages: dict = {}
+        self._folded: dict = {}   # samples already in each staged Hessian's running mean
         if sparsity_profile is not None:
             sparsity_profile = sparsity_profile.lower()
             if sparsity_profile not in ["owl"]:
@@ -395,15 +429,36 @@ class SparseGPTModifier(_SharedHessians):
             self._hessians[module] = sgpt.make_empty_hessian(module, device="cpu" if self.offload_hessians else dev)
             self._num_samples[module] = 0
         H = self._hessians[module]
-        if self.offload_hessians:
-            H = H.to(module.weight.device)
-        H, self._num_samples[module] = sgpt.accumulate_hessian(inp, module, H, self._num_samples[module])
-        self._hessians[module] = H.to("cpu") if self.offload_hessians else H
+        if self.offload_hessians or not self.hessian_batch_tokens:
+            if self.offload_hessians:
+                H = H.to(module.weight.device)
+            H, self._num_samples[module] = sgpt.accumulate_hessian(inp, module, H, self._num_samples[module])
+            self._hessians[module] = H.to("cpu") if self.offload_hessians else H
+        else:
+            x, added = sgpt.hessian_rows(inp, module, H.device)
+            self._num_samples[module] += added
+            st = self._stages.get(module)
+            if st is None:
+                st = self._stages[module] = HessianStage(self.hessian_batch_tokens)
+            st.add(x, added, lambda rows, samples: self._fold(module, H, rows, samples))
         if self.share_hessians:
             self._note_accumulated(module, inp, self._module_names.get)
 
+    def _fold(self, module, H, rows, samples):
+        self._folded[module] = sgpt.fold_rows(H, rows, self._folded.get(module, 0), samples)
+
+    def _flush(self, module):
+        """Folds the rows still staged for ``module`` into its running mean."""
+        st = self._stages.pop(module, None)
+        if st is not None:
+            H = self._hessians[module]
+            st.flush(lambda rows, samples: self._fold(module, H, rows, samples))
+            st.release()
+        self._folded.pop(module, None)
+
     def compress_modules(self):
         for leader, members in self._take_groups(self._module_names.get).items():
+            self._flush(leader)
             n = self._num_samples[leader]
             H = self._hessians.pop(leader).to(leader.weight.device)
             for module in members:

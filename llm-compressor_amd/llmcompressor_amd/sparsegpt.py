@@ -43,17 +43,29 @@ def accumulate_hessian(inp: torch.Tensor, module: torch.nn.Module, H: torch.Tens
     """Running mean: H *= n / (n + added); H += (2 / (n + added)) X^T X (upper
     triangle, in place; one kernel call), ``added`` = the leading dimension
     after a 2-D input is unsqueezed to 3-D."""
-    inp = inp.to(device=H.device)
+    x, num_added = hessian_rows(inp, module, H.device)
+    return H, fold_rows(H, x, num_samples, num_added)
+
+
+def hessian_rows(inp: torch.Tensor, module: torch.nn.Module, device) -> tuple[torch.Tensor, int]:
+    """The 2-D rows of one accumulation call on ``device`` and the
+    reference's sample count for it (the leading dimension after a 2-D input
+    is unsqueezed to 3-D)."""
+    inp = inp.to(device=device)
     if len(inp.shape) == 2:
         inp = inp.unsqueeze(0)
-    num_added = inp.shape[0]
     if not _is_linear_like(module):
         raise NotImplementedError(f"SparseGPT Hessian for {type(module).__name__} is not provided by this build")
+    return inp.reshape(-1, inp.shape[-1]), inp.shape[0]
+
+
+def fold_rows(H: torch.Tensor, x: torch.Tensor, num_samples: int, num_added: int) -> int:
+    """The running mean over ``num_samples`` samples extended by the rows x of
+    ``num_added`` more; returns the new count."""
     beta = num_samples / (num_samples + num_added)
     num_samples += num_added
-    x = inp.reshape(-1, inp.shape[-1])
     ops.hessian_syrk_(H, x, alpha=2 / num_samples, beta=beta)
-    return H, num_samples
+    return num_samples
 
 
 class SparsifyResult:

@@ -23,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from llmcompressor_amd import GPTQModifier, gptq, ops
+from llmcompressor_amd.staging import HessianStage
 from llmcompressor_amd.quant_args import QuantizationArgs
 from oracle import gptq as og
 from oracle.qargs import OArgs
@@ -116,13 +117,18 @@ def test_decoder_layer_gptq_modifier_vs_oracle(dev):
     for name, m in layer.named_children():
         xs = seen[name]
         cols = xs[0].shape[-1]
-        # the GPU Hessian the modifier accumulated (same kernel, inputs and call order: the same bits)
+        # the GPU Hessian the modifier accumulated (same kernel, rows and
+        # staged calls: the same bits)
         lin = torch.nn.Linear(cols, 1, bias=False, device=dev)
         Hg, ng = gptq.make_empty_hessian(lin), torch.zeros((), device=dev)
         Ho, no = og.make_empty_hessian(cols), torch.zeros(())
+        stage = HessianStage()
         for x in xs:
-            Hg, ng = gptq.accumulate_hessian(x.to(dev), lin, Hg, ng)
+            rows, added = gptq.hessian_rows(x, lin, dev)
+            ng += added
+            stage.add(rows, added, lambda r, _s: ops.hessian_syrk_(Hg, r, alpha=2.0))
             Ho, no = og.accumulate_hessian(x, Ho, no)
+        stage.flush(lambda r, _s: ops.hessian_syrk_(Hg, r, alpha=2.0))
         Hg = Hg.cpu()
         assert float(ng) == float(no) == 8.0
         r = rel_fro(torch.triu(Hg), torch.triu(Ho))

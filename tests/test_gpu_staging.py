@@ -1,0 +1,74 @@
+"""GPU: Hessians accumulated through the modifiers' staging (calibration
+calls gathered into longer syrk calls) equal the per-call accumulation up to
+the order of fp32 additions - both the GPTQ sum (H += 2 X^T X) and the
+SparseGPT running mean - and match the oracle."""
+import pytest
+import torch
+
+from llmcompressor_amd import gptq, ops, sparsegpt, workloads
+from llmcompressor_amd.staging import HessianStage
+from oracle import gptq as og
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [2048] * 7 + [12000] + [2048] * 3 + [1000]   # one call past half the buffer, a ragged tail
+
+
+def _rel(a, b):
+    return float(torch.linalg.norm(a - b) / torch.linalg.norm(b))
+
+
+def _batches(d, dev):
+    return [workloads.heavy_tailed_activations((1, n, d), seed=300 + i).to(dev) for i, n in enumerate(SIZES)]
+
+
+def test_gptq_staged_hessian_matches_per_call(dev):
+    print("GPTQ Hessian: staged calls vs one syrk per call vs the oracle", flush=True)
+    d = 1024
+    lin = torch.nn.Linear(d, 1, bias=False, device=dev)
+    xs = _batches(d, dev)
+    H1, n1 = gptq.make_empty_hessian(lin), torch.zeros((), device=dev)
+    for x in xs:
+        H1, n1 = gptq.accumulate_hessian(x, lin, H1, n1)
+    H2, n2 = gptq.make_empty_hessian(lin), torch.zeros((), device=dev)
+    stage, calls = HessianStage(), []
+
+    def flush(rows, samples):
+        calls.append(rows.shape[0])
+        ops.hessian_syrk_(H2, rows, alpha=2.0)
+    for x in xs:
+        rows, added = gptq.hessian_rows(x, lin, dev)
+        n2 += added
+        stage.add(rows, added, flush)
+    stage.flush(flush)
+    assert calls == [14336, 12000, 7144], calls
+    assert float(n1) == float(n2) == len(SIZES)
+    r = _rel(torch.triu(H2), torch.triu(H1))
+    assert r <= 2e-6, r
+    Ho, no = og.make_empty_hessian(d), torch.zeros(())
+    for x in xs:
+        Ho, no = og.accumulate_hessian(x.cpu(), Ho, no)
+    assert _rel(torch.triu(H2).cpu(), torch.triu(Ho)) <= 1e-5
+
+
+def test_sparsegpt_staged_running_mean_matches_per_call(dev):
+    print("SparseGPT running-mean Hessian: staged calls vs one syrk per call", flush=True)
+    d = 768
+    lin = torch.nn.Linear(d, 1, bias=False, device=dev)
+    xs = _batches(d, dev)
+    H1, n1 = sparsegpt.make_empty_hessian(lin), 0
+    for x in xs:
+        H1, n1 = sparsegpt.accumulate_hessian(x, lin, H1, n1)
+    H2, n2, folded = sparsegpt.make_empty_hessian(lin), 0, [0]
+    stage = HessianStage()
+
+    def flush(rows, samples):
+        folded[0] = sparsegpt.fold_rows(H2, rows, folded[0], samples)
+    for x in xs:
+        rows, added = sparsegpt.hessian_rows(x, lin, dev)
+        n2 += added
+        stage.add(rows, added, flush)
+    stage.flush(flush)
+    assert n1 == n2 == folded[0] == len(SIZES)
+    r = _rel(torch.triu(H2), torch.triu(H1))
+    assert r <= 2e-6, r

@@ -1,0 +1,71 @@
+"""Host logic of the Hessian staging (no GPU): every row reaches the
+accumulation exactly once, in call order, with the calls' sample counts."""
+import torch
+import pytest
+
+from llmcompressor_amd.staging import HessianStage
+
+
+class Recorder:
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, rows, samples):
+        self.calls.append((rows.clone(), samples))
+
+
+def _run(sizes, tokens, dtypes=None, d=8):
+    rec, stage = Recorder(), HessianStage(tokens)
+    sent, total = [], 0
+    for i, n in enumerate(sizes):
+        dt = dtypes[i] if dtypes else torch.float32
+        x = (torch.arange(n * d, dtype=torch.float32).reshape(n, d) + 1000 * i).to(dt)
+        sent.append(x)
+        stage.add(x, i + 1, rec)
+        total += i + 1
+    stage.flush(rec)
+    return rec, sent, total
+
+
+@pytest.mark.parametrize("sizes", [[3, 3, 3, 3, 3], [8, 8, 1], [2, 9, 2, 2], [16], [5, 11, 4, 4, 4, 4]],
+                         ids=["small", "exact-fill", "pass-through", "one-big", "mixed"])
+def test_rows_in_order_once(sizes):
+    tokens = 16
+    rec, sent, total = _run(sizes, tokens)
+    got = torch.cat([r for r, _ in rec.calls])
+    assert torch.equal(got, torch.cat(sent))
+    assert sum(s for _, s in rec.calls) == total
+    for rows, _ in rec.calls:
+        assert rows.shape[0] <= max(tokens, max(sizes))
+
+
+def test_full_buffer_flushes_at_once():
+    rec, stage = Recorder(), HessianStage(8)
+    for i in range(4):
+        stage.add(torch.ones(2, 4) * i, 1, rec)
+    assert len(rec.calls) == 1 and rec.calls[0][0].shape[0] == 8 and rec.calls[0][1] == 4
+    stage.flush(rec)
+    assert len(rec.calls) == 1           # nothing left
+
+
+def test_large_call_goes_through_after_staged_rows():
+    rec, stage = Recorder(), HessianStage(16)
+    stage.add(torch.zeros(3, 4), 1, rec)
+    stage.add(torch.ones(9, 4), 2, rec)   # more than half the buffer
+    assert [c[0].shape[0] for c in rec.calls] == [3, 9] and [c[1] for c in rec.calls] == [1, 2]
+
+
+def test_dtype_or_width_change_flushes_first():
+    rec, _, _ = _run([3, 3, 3], 16, dtypes=[torch.float32, torch.bfloat16, torch.bfloat16])
+    assert [c[0].dtype for c in rec.calls] == [torch.float32, torch.bfloat16]
+    assert [c[0].shape[0] for c in rec.calls] == [3, 6]
+    rec, stage = Recorder(), HessianStage(16)
+    stage.add(torch.zeros(2, 4), 1, rec)
+    stage.add(torch.zeros(2, 6), 1, rec)
+    stage.flush(rec)
+    assert [tuple(c[0].shape) for c in rec.calls] == [(2, 4), (2, 6)]
+
+
+def test_rejects_empty_buffer():
+    with pytest.raises(ValueError):
+        HessianStage(0)
