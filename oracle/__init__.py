@@ -4,7 +4,8 @@ TEST INFRASTRUCTURE ONLY.  This package is a CPU restatement of the
 reference's algorithm (llm-compressor's GPTQ Hessian/solve, min-max
 observers and the compressed-tensors quantize/pack arithmetic it calls).
 It is imported only by ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py``, and there only as the checker.  The
+``cpu_baseline`` leg of ``bench.py``, and there only as the reference the GPU
+results are compared with, never as the thing measured.  The
 product path (``llmcompressor_amd``) never imports it and fails loudly when
 its HIP library is missing.
 

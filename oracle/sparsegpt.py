@@ -1,6 +1,6 @@
 """SparseGPT Hessian accumulation and pruning solve, restated for the CPU oracle.
 
-Test infrastructure only: the checker the GPU path is compared against.
+Test infrastructure only: what the GPU path is compared against.
 Follows ``modifiers/pruning/sparsegpt/sgpt_sparsify.py`` line by line:
 
 * ``make_empty_hessian``  - ``:10-16``
