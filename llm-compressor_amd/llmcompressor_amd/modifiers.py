@@ -10,7 +10,8 @@ These mirror the reference's modifiers at the level the hot path needs
   (``base.py:255-289``) that lazily creates H and ``num_samples`` and calls
   ``accumulate_hessian`` - here through a ``staging.HessianStage`` that
   gathers calls of up to ``hessian_batch_tokens / 2`` rows into one syrk
-  (0 turns it off; so does ``offload_hessians``);
+  while the stages fit in ``hessian_stage_bytes`` (0 tokens turns it off;
+  so does ``offload_hessians``);
 * ``on_sequential_epoch_end``: ``observe(weight)`` then ``compress_modules``
   -> ``quantize_weight`` on H / num_samples (``base.py:578-601``), writing
   ``weight`` / ``weight_scale`` / ``weight_zero_point`` / ``weight_g_idx``;
@@ -38,7 +39,7 @@ from . import sparsegpt as sgpt
 from . import ops
 from .gptq import (_effective_actorder, accumulate_hessian, gptq_quantize, hessian_rows, make_empty_hessian,
                    prepare_hessian)
-from .staging import DEFAULT_TOKENS, HessianStage
+from .staging import DEFAULT_BUDGET, DEFAULT_TOKENS, HessianStage
 from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationScheme, preset_name_to_scheme
 
 logger = logging.getLogger("llmcompressor_amd")
@@ -195,18 +196,51 @@ class _SharedHessians:
         return groups
 
 
-class GPTQModifier(QuantizationModifier, _SharedHessians):
+class _Staging:
+    """Hessian staging of the forward hooks within a memory budget: a module
+    gets a ``HessianStage`` (``hessian_batch_tokens`` x d elements of its
+    input dtype) while the stages already held fit in ``hessian_stage_bytes``;
+    past it (an MoE layer's many experts) a module accumulates every call at
+    once.  A stage is released when its Hessian is read."""
+
+    def _init_staging(self, tokens: int, budget: int):
+        self.hessian_batch_tokens = tokens
+        self.hessian_stage_bytes = budget
+        self._stages: dict = {}      # module -> HessianStage, or None: accumulated per call
+        self._reserved: dict = {}    # module -> bytes its stage holds
+        self._stage_held = 0
+
+    def _stage_for(self, module, x):
+        if module in self._stages:
+            return self._stages[module]
+        need = self.hessian_batch_tokens * x.shape[1] * x.element_size()
+        st = None
+        if self._stage_held + need <= self.hessian_stage_bytes:
+            st = HessianStage(self.hessian_batch_tokens)
+            self._reserved[module] = need
+            self._stage_held += need
+        self._stages[module] = st
+        return st
+
+    def _drop_stage(self, module, flush):
+        st = self._stages.pop(module, None)
+        if st is not None:
+            st.flush(flush)
+            st.release()
+            self._stage_held -= self._reserved.pop(module)
+
+
+class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
     def __init__(self, scheme=None, targets=("Linear",), ignore=("lm_head",), config_groups=None,
                  block_size: int = 128, dampening_frac: float | None = 0.01, actorder="static",
                  offload_hessians: bool = False, share_hessians: bool = True,
-                 hessian_batch_tokens: int = DEFAULT_TOKENS):
+                 hessian_batch_tokens: int = DEFAULT_TOKENS, hessian_stage_bytes: int = DEFAULT_BUDGET):
         super().__init__(scheme, targets, ignore, config_groups)
         self.block_size = block_size
         self.dampening_frac = dampening_frac
         self.actorder = actorder
         self.offload_hessians = offload_hessians
-        self.hessian_batch_tokens = hessian_batch_tokens
-        self._stages: dict = {}
+        self._init_staging(hessian_batch_tokens, hessian_stage_bytes)
         # modules sharing an input also share one Cholesky chain per
         # activation ordering at compression
         self._init_sharing(share_hessians)
@@ -249,10 +283,11 @@ class GPTQModifier(QuantizationModifier, _SharedHessians):
             self._hessians[module] = H.to("cpu") if self.offload_hessians else H
         else:
             x, added = hessian_rows(inp, module, H.device)
-            st = self._stages.get(module)
+            st = self._stage_for(module, x)
             if st is None:
-                st = self._stages[module] = HessianStage(self.hessian_batch_tokens)
-            st.add(x, added, lambda rows, samples: self._accumulate(module, H, rows, samples))
+                self._accumulate(module, H, x, added)
+            else:
+                st.add(x, added, lambda rows, samples: self._accumulate(module, H, rows, samples))
         if self.share_hessians:
             self._note_accumulated(module, inp, self._modules.get)
 
@@ -264,11 +299,8 @@ class GPTQModifier(QuantizationModifier, _SharedHessians):
 
     def _flush(self, module):
         """Accumulates the rows still staged for ``module``'s Hessian."""
-        st = self._stages.pop(module, None)
-        if st is not None:
-            H = self._hessians[module]
-            st.flush(lambda rows, samples: self._accumulate(module, H, rows, samples))
-            st.release()
+        H = self._hessians.get(module)
+        self._drop_stage(module, lambda rows, samples: self._accumulate(module, H, rows, samples))
 
     def on_calibration_start(self, model):
         for m in self._modules:
@@ -345,7 +377,7 @@ class GPTQModifier(QuantizationModifier, _SharedHessians):
         return model
 
 
-class SparseGPTModifier(_SharedHessians):
+class SparseGPTModifier(_SharedHessians, _Staging):
     """One-shot SparseGPT (``modifiers/pruning/sparsegpt/base.py:24-173``).
 
     ``targets`` name the layers that carry a sparsity (a float for all, or
@@ -362,10 +394,9 @@ class SparseGPTModifier(_SharedHessians):
                  owl_m: int | None = None, owl_lmbda: float | None = None, targets=("Linear",), ignore=(),
                  block_size: int = 128, dampening_frac: float | None = 0.01, preserve_sparsity_mask: bool = False,
                  offload_hessians: bool = False, share_hessians: bool = True,
-                 hessian_batch_tokens: int = DEFAULT_TOKENS):
+                 hessian_batch_tokens: int = DEFAULT_TOKENS, hessian_stage_bytes: int = DEFAULT_BUDGET):
         self._init_sharing(share_hessians)
-        self.hessian_batch_tokens = hessian_batch_tokens
-        self._stages: dict = {}
+        self._init_staging(hessian_batch_tokens, hessian_stage_bytes)
         self._folded: dict = {}   # samples already in each staged Hessian's running mean
         if sparsity_profile is not None:
             sparsity_profile = sparsity_profile.lower()
@@ -437,10 +468,11 @@ class SparseGPTModifier(_SharedHessians):
         else:
             x, added = sgpt.hessian_rows(inp, module, H.device)
             self._num_samples[module] += added
-            st = self._stages.get(module)
+            st = self._stage_for(module, x)
             if st is None:
-                st = self._stages[module] = HessianStage(self.hessian_batch_tokens)
-            st.add(x, added, lambda rows, samples: self._fold(module, H, rows, samples))
+                self._fold(module, H, x, added)
+            else:
+                st.add(x, added, lambda rows, samples: self._fold(module, H, rows, samples))
         if self.share_hessians:
             self._note_accumulated(module, inp, self._module_names.get)
 
@@ -449,11 +481,8 @@ class SparseGPTModifier(_SharedHessians):
 
     def _flush(self, module):
         """Folds the rows still staged for ``module`` into its running mean."""
-        st = self._stages.pop(module, None)
-        if st is not None:
-            H = self._hessians[module]
-            st.flush(lambda rows, samples: self._fold(module, H, rows, samples))
-            st.release()
+        H = self._hessians.get(module)
+        self._drop_stage(module, lambda rows, samples: self._fold(module, H, rows, samples))
         self._folded.pop(module, None)
 
     def compress_modules(self):

@@ -17,6 +17,7 @@ from __future__ import annotations
 import torch
 
 DEFAULT_TOKENS = 16384
+DEFAULT_BUDGET = 2 << 30   # bytes of stage buffers one modifier holds at a time
 
 
 class HessianStage:

@@ -72,3 +72,29 @@ def test_sparsegpt_staged_running_mean_matches_per_call(dev):
     assert n1 == n2 == folded[0] == len(SIZES)
     r = _rel(torch.triu(H2), torch.triu(H1))
     assert r <= 2e-6, r
+
+
+def test_gptq_modifier_staged_matches_unstaged(dev):
+    """Three layers fed different inputs, six 2048-token batches; a budget
+    for one stage (the other two layers accumulate per call), against the
+    modifier without staging: the same scales, codes within the GPTQ code
+    bar (the Hessians differ in the order of fp32 additions)."""
+    print("GPTQModifier: staged (one stage in the budget) vs per-call Hessians", flush=True)
+    import copy
+    from llmcompressor_amd import GPTQModifier
+    from parity_util import code_agreement, code_bar
+    torch.manual_seed(0)
+    model = torch.nn.Sequential(*[torch.nn.Linear(512, 512, bias=False) for _ in range(3)]).to(dev).to(torch.bfloat16)
+    batches = [workloads.heavy_tailed_activations((1, 2048, 512), seed=400 + i).to(dev) for i in range(6)]
+    ref = copy.deepcopy(model)
+    # no activation ordering: a permutation from diag(H) could swap two near-equal entries
+    GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), actorder=None,
+                 hessian_batch_tokens=0).apply(ref, batches)
+    mod = GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), actorder=None,
+                       hessian_stage_bytes=16384 * 512 * 2)
+    mod.apply(model, batches)
+    assert mod._stage_held == 0 and not mod._stages
+    for a, b in zip(model, ref):
+        assert torch.equal(a.weight_scale, b.weight_scale)
+        st = code_agreement(a.gptq_codes.cpu().int(), b.gptq_codes.cpu().int())
+        assert code_bar(st, a.weight.shape[0]), st

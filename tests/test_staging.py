@@ -69,3 +69,26 @@ def test_dtype_or_width_change_flushes_first():
 def test_rejects_empty_buffer():
     with pytest.raises(ValueError):
         HessianStage(0)
+
+
+def test_modifier_stage_budget():
+    """A module gets a stage while the stages held fit in the budget; the
+    rest accumulate every call at once, and a dropped stage frees its share."""
+    from llmcompressor_amd.modifiers import _Staging
+
+    class M(_Staging):
+        pass
+
+    m = M()
+    m._init_staging(tokens=1024, budget=3 * 1024 * 64 * 2)   # three stages of 1024 x 64 bf16
+    x = torch.zeros(16, 64, dtype=torch.bfloat16)
+    mods = [object() for _ in range(5)]
+    got = [m._stage_for(k, x) for k in mods]
+    assert [g is not None for g in got] == [True, True, True, False, False]
+    assert m._stage_for(mods[3], x) is None and m._stage_held == 3 * 1024 * 64 * 2
+    rec = Recorder()
+    got[0].add(x, 1, rec)
+    m._drop_stage(mods[0], rec)
+    assert len(rec.calls) == 1 and rec.calls[0][0].shape == (16, 64)
+    assert m._stage_held == 2 * 1024 * 64 * 2 and mods[0] not in m._stages
+    assert m._stage_for(mods[0], x) is not None            # room again
