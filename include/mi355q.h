@@ -421,6 +421,19 @@ int mi355q_mxfp4_quantize_pack(const void* x_dev, int64_t rows, int64_t cols, in
 int mi355q_mxfp4_dequantize(const uint8_t* codes_dev, const uint8_t* scales_dev, int64_t rows,
                             int64_t cols, void* out_dev, void* stream);
 
+/* fp4 e2m1 quantize + pack with given group scales (the NVFP4 weight of
+ * an nvfp4-pack-quantized checkpoint, docs/guides/compression_schemes.md:57-64):
+ * q = e2m1(x / (scale[r][c / group_size] / global_scale)), the effective
+ * scale and the quotient in fp32 as CT's quantize forms them (no global
+ * scale: NULL), e2m1 rounding, codes and byte layout as
+ * mi355q_mxfp4_quantize_pack.  scale is fp32 [rows, >= ceil(cols /
+ * group_size)] (ld_scale), codes [rows, cols / 2] uint8, cols even.
+ * Replaces the CT nvfp4_pack_quantized compressor at save
+ * (transformers/compression/compressed_tensors_utils.py:191). */
+int mi355q_fp4_quantize_pack(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
+                             const float* scale_dev, int64_t ld_scale, int64_t group_size,
+                             const float* global_scale_dev, uint8_t* codes_dev, void* stream);
+
 /* fp8 e4m3 (float8_e4m3fn) quantize: q = fp8_rne(clamp(x / scale, -448,
  * 448)) with the scale indexing of mi355q_quantize_int; division in
  * div_dtype.  Output bytes are e4m3fn bit patterns. */

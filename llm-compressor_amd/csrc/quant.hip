@@ -669,6 +669,29 @@ __global__ void mxfp4_dequant_kernel(const uint8_t* codes, const uint8_t* scales
   }
 }
 
+// ---------------------------------------------------------------- fp4 with given scales
+// e2m1 codes of x / (scale / global_scale) for group scales computed
+// elsewhere (NVFP4: fp8 group scales and an fp32 global scale), the
+// effective scale and the quotient formed in fp32 as CT's quantize forms
+// them; two codes per byte, even column in the low nibble.  The gfx950 fp4
+// conversion rounds to nearest-even on the e2m1 grid and saturates at 6
+// (CT's cast_to_fp4); -0.0 becomes +0.0 first, so only values below zero
+// carry the sign bit.  One thread per output byte.
+__global__ void fp4_quantize_pack_kernel(const void* x, mi355q_dtype dt, int64_t rows, int64_t cols, int64_t ldx,
+                                         const float* scale, int64_t ld_scale, int64_t group_size,
+                                         const float* gscale, uint8_t* out) {
+  const int64_t half = cols / 2, total = rows * half;
+  const float gs = gscale ? gscale[0] : 1.f;
+  for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < total; i += (int64_t)gridDim.x * NT) {
+    const int64_t r = i / half, c = 2 * (i - r * half);
+    const float s0 = scale[r * ld_scale + c / group_size] / gs;
+    const float s1 = scale[r * ld_scale + (c + 1) / group_size] / gs;
+    const float v0 = load_elem(x, dt, r * ldx + c) / s0, v1 = load_elem(x, dt, r * ldx + c + 1) / s1;
+    const uint32_t w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, v0 + 0.f, v1 + 0.f, 1.f, 0);
+    out[i] = (uint8_t)(w & 0xffu);
+  }
+}
+
 // ---------------------------------------------------------------- fp8 e4m3fn
 __device__ __forceinline__ uint8_t f32_to_e4m3fn(float v) {
   const uint32_t sign = (__float_as_uint(v) >> 31) << 7;
@@ -1271,6 +1294,21 @@ extern "C" int mi355q_quantize_fp8(const void* x_dev, mi355q_dtype dtype, int64_
   hipLaunchKernelGGL(quantize_fp8_kernel, dim3(grid_for(rows * cols, NT, 1u << 16)), dim3(NT), 0,
                      reinterpret_cast<hipStream_t>(stream), x_dev, dtype, rows, cols, ldx, scale_dev, ld_scale,
                      strategy, group_size, div_dtype == MI355Q_BF16 ? 1 : 0, out_dev);
+  MQ_LAUNCH_CHECK();
+  return MI355Q_OK;
+}
+
+extern "C" int mi355q_fp4_quantize_pack(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
+                                        int64_t ldx, const float* scale_dev, int64_t ld_scale, int64_t group_size,
+                                        const float* global_scale_dev, uint8_t* codes_dev, void* stream) {
+  MQ_CHECK_ARG(x_dev && scale_dev && codes_dev, "fp4_quantize_pack: null pointer");
+  MQ_CHECK_ARG(rows > 0 && cols > 0 && cols % 2 == 0 && ldx >= cols, "fp4_quantize_pack: bad shape (cols even)");
+  MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F32, "fp4_quantize_pack: dtype must be bf16 or fp32");
+  MQ_CHECK_ARG(group_size > 0 && ld_scale >= (cols + group_size - 1) / group_size,
+               "fp4_quantize_pack: group_size and ld_scale must cover the columns");
+  hipLaunchKernelGGL(fp4_quantize_pack_kernel, dim3(grid_for(rows * (cols / 2), NT, 1u << 16)), dim3(NT), 0,
+                     reinterpret_cast<hipStream_t>(stream), x_dev, dtype, rows, cols, ldx, scale_dev, ld_scale,
+                     group_size, global_scale_dev, codes_dev);
   MQ_LAUNCH_CHECK();
   return MI355Q_OK;
 }

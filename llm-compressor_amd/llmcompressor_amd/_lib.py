@@ -77,6 +77,7 @@ SIGNATURES = {
     "mi355q_mxfp4_quantize_pack": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
     "mi355q_mxfp4_dequantize": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "mi355q_quantize_fp8": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _i32, _i64, _i32, _vp, _vp]),
+    "mi355q_fp4_quantize_pack": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp]),
     "mi355q_quantize_int8_per_token": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
 }
 

@@ -23,7 +23,8 @@ __all__ = ["initialize_observer", "observe", "update_qparams", "initialize_modul
 
 def initialize_module_for_quantization(module: Module, scheme: QuantizationScheme) -> None:
     """Attach ``quantization_scheme`` and empty ``weight_scale`` /
-    ``weight_zero_point`` parameters shaped for the weight strategy."""
+    ``weight_zero_point`` parameters shaped for the weight strategy (and
+    ``weight_global_scale`` for tensor groups)."""
     module.quantization_scheme = scheme
     wa = scheme.weights
     if wa is None or not hasattr(module, "weight"):
@@ -47,6 +48,9 @@ def initialize_module_for_quantization(module: Module, scheme: QuantizationSchem
                                                                  requires_grad=False))
     module.register_parameter("weight_zero_point", torch.nn.Parameter(
         torch.zeros(shape, dtype=wa.zp_dtype, device=dev), requires_grad=False))
+    if s == "tensor_group":   # NVFP4: the per-tensor global scale beside the group scales
+        module.register_parameter("weight_global_scale", torch.nn.Parameter(
+            torch.ones((1,), dtype=torch.float32, device=dev), requires_grad=False))
     if wa.actorder is not None and wa.actorder.value == "group":
         module.register_parameter("weight_g_idx", torch.nn.Parameter(
             torch.full((cols,), -1, dtype=torch.int, device=dev), requires_grad=False))

@@ -546,6 +546,25 @@ def quantize_fp8(x: torch.Tensor, scale: torch.Tensor, strategy: str, group_size
     return out.view(torch.float8_e4m3fn)
 
 
+def fp4_quantize_pack(x: torch.Tensor, scale: torch.Tensor, group_size: int,
+                      global_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """e2m1 codes of x / (scale / global_scale) per column group, two per byte
+    (even column in the low nibble): uint8 [rows, cols / 2] (the NVFP4
+    ``weight_packed`` tensor)."""
+    L.require_gpu(x, scale)
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.float()
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    rows, cols = x.shape
+    s = scale.to(torch.float32).reshape(rows, -1).contiguous()
+    gs = None if global_scale is None else global_scale.to(torch.float32).reshape(1).contiguous()
+    out = torch.empty((rows, cols // 2), dtype=torch.uint8, device=x.device)
+    L.call("mi355q_fp4_quantize_pack", x.data_ptr(), _dt(x), rows, cols, x.stride(0), s.data_ptr(), s.stride(0),
+           group_size, L.ptr(gs), out.data_ptr(), L.stream_of(x))
+    return out
+
+
 def quantize_int8_per_token(x: torch.Tensor):
     """Dynamic per-token int8: (codes int8 [rows, cols], scale bf16 [rows, 1])."""
     L.require_gpu(x)

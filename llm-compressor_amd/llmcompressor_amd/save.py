@@ -11,7 +11,9 @@ Format of a module (``infer_quantization_format``), as
 ``tests/llmcompressor/transformers/compression/test_compress_tensor_utils.py:289-322``
 fixes it: W8A8 int -> ``int-quantized``, W4A16 / W8A16 int -> ``pack-quantized``,
 W8A8 fp8 -> ``float-quantized``, weight-only fp8 -> ``naive-quantized``; MXFP4 ->
-``mxfp4-pack-quantized`` (``docs/guides/compression_schemes.md:68-77``).
+``mxfp4-pack-quantized`` (``docs/guides/compression_schemes.md:68-77``); NVFP4
+(fp4 tensor-group weights) -> ``nvfp4-pack-quantized`` (its tensor names pinned
+by ``tests/llmcompressor/entrypoints/model_free/test_convert_checkpoint.py:81-109``).
 
 Tensors written per format follow compressed-tensors as recalled (parity
 unpinned: the library is absent and no reference test holds a checkpoint):
@@ -27,7 +29,11 @@ unpinned: the library is absent and no reference test holds a checkpoint):
 * ``float-quantized`` / ``naive-quantized`` (fp8): ``weight`` float8_e4m3fn,
   ``weight_scale``;
 * ``mxfp4-pack-quantized``: ``weight_packed`` uint8 [rows, cols / 2] (even
-  column in the low nibble), ``weight_scale`` uint8 e8m0 [rows, cols / 32].
+  column in the low nibble), ``weight_scale`` uint8 e8m0 [rows, cols / 32];
+* ``nvfp4-pack-quantized``: ``weight_packed`` uint8 [rows, cols / 2] (the
+  same code layout, e2m1 of weight / (scale / global_scale)),
+  ``weight_scale`` float8_e4m3fn [rows, cols / 16], ``weight_global_scale``
+  float32 [1].
 """
 from __future__ import annotations
 
@@ -55,6 +61,8 @@ def infer_quantization_format(scheme: QuantizationScheme | None) -> str | None:
         return None
     if w.is_mx:
         return "mxfp4-pack-quantized"
+    if w.type == QuantizationType.FLOAT and w.num_bits == 4 and w.strategy == QuantizationStrategy.TENSOR_GROUP:
+        return "nvfp4-pack-quantized"
     a = scheme.input_activations
     if w.type == QuantizationType.INT:
         if a is None or w.num_bits < 8:
@@ -81,6 +89,15 @@ def compress_module(module: torch.nn.Module, fmt: str | None = None) -> dict[str
     if fmt == "mxfp4-pack-quantized":
         codes, e8 = ops.mxfp4_quantize_pack(module.weight)
         return {"weight_packed": codes, "weight_scale": e8}
+    if fmt == "nvfp4-pack-quantized":
+        gs = getattr(module, "weight_global_scale", None)
+        if gs is None:
+            raise ValueError("nvfp4-pack-quantized needs the module's weight_global_scale")
+        scale = module.weight_scale.data
+        packed = ops.fp4_quantize_pack(module.weight, scale, w.group_size, gs.data)
+        # the group scales are fp8 values held in a wider dtype: the cast is exact
+        return {"weight_packed": packed, "weight_scale": scale.to(torch.float8_e4m3fn),
+                "weight_global_scale": gs.data.to(torch.float32).reshape(1)}
     out = {"weight_scale": module.weight_scale.data}
     if w.type == QuantizationType.INT:
         codes = _codes(module, w)

@@ -19,6 +19,11 @@
   Parity unpinned against the reference (no test, CT absent); pinned
   against the torch fake-quant path of this oracle and a brute-force
   nearest-grid-point search with ties to even.
+* ``fp4_group_quantize_pack`` - the NVFP4 ``weight_packed`` tensor: the same
+  codes and layout for x / (scale / global_scale) with given fp8 group
+  scales.  Format name and tensor names pinned by
+  ``tests/llmcompressor/entrypoints/model_free/test_convert_checkpoint.py:81-109``;
+  the code layout parity unpinned as for MXFP4, and pinned the same way.
 """
 from __future__ import annotations
 
@@ -99,6 +104,29 @@ def mxfp4_quantize_pack(x_bits: np.ndarray, rule: str = "ct"):
     c = e2m1_codes(v)
     packed = (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
     return packed, e8
+
+
+def fp4_group_quantize_pack(x: np.ndarray, scale: np.ndarray, group: int, global_scale=None) -> np.ndarray:
+    """NVFP4 weight codes (``nvfp4-pack-quantized``): e2m1 codes of
+    x / (scale / global_scale), the effective scale and the quotient in
+    float32 as the oracle's ``fake_quant.quantize`` forms them; x float32
+    [rows, cols], scale float32 [rows, ceil(cols / group)].  Packed as
+    ``mxfp4_quantize_pack``."""
+    s = scale.astype(np.float32)
+    if global_scale is not None:
+        s = (s / np.float32(global_scale)).astype(np.float32)
+    cols = x.shape[1]
+    v = (x.astype(np.float32) / s[:, np.arange(cols) // group]).astype(np.float32)
+    c = e2m1_codes(v)
+    return (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
+
+
+def fp4_unpack(packed: np.ndarray) -> np.ndarray:
+    """e2m1 grid values (float32) of packed codes [rows, cols / 2]."""
+    rows, half = packed.shape
+    c = np.empty((rows, half * 2), dtype=np.uint8)
+    c[:, 0::2], c[:, 1::2] = packed & 0x0F, packed >> 4
+    return (E2M1_GRID[c & 7] * np.where(c & 8, -1.0, 1.0)).astype(np.float32)
 
 
 def mxfp4_unpack(packed: np.ndarray, e8: np.ndarray) -> np.ndarray:

@@ -82,7 +82,8 @@ def test_save_w4a16_checkpoint(dev, tmp_path):
 
 
 @pytest.mark.parametrize("scheme,fmt", [("W8A8", "int-quantized"), ("FP8_DYNAMIC", "float-quantized"),
-                                        ("MXFP4", "mxfp4-pack-quantized"), ("W4A16_ASYM", "pack-quantized")])
+                                        ("MXFP4", "mxfp4-pack-quantized"), ("W4A16_ASYM", "pack-quantized"),
+                                        ("NVFP4A16", "nvfp4-pack-quantized")])
 def test_save_formats(dev, tmp_path, scheme, fmt):
     say(f"save {scheme}")
     model = _model(dev)
@@ -101,6 +102,22 @@ def test_save_formats(dev, tmp_path, scheme, fmt):
             # the module keeps the scales as float powers of two, the file as e8m0
             e8 = t[p + "weight_scale"].to(torch.float32)
             assert torch.equal(torch.exp2(e8 - 127), lin.weight_scale.detach().cpu().float())
+        elif scheme == "NVFP4A16":
+            w = lin.weight.detach().cpu().float().numpy()
+            sc = lin.weight_scale.detach().cpu().float().numpy()
+            gs = lin.weight_global_scale.detach().cpu().float()
+            assert np.array_equal(t[p + "weight_packed"].numpy(), opack.fp4_group_quantize_pack(w, sc, 16, float(gs)))
+            assert t[p + "weight_scale"].dtype == torch.float8_e4m3fn
+            assert torch.equal(t[p + "weight_scale"].float(), torch.from_numpy(sc))
+            assert t[p + "weight_global_scale"].dtype == torch.float32
+            assert torch.equal(t[p + "weight_global_scale"], gs.reshape(1))
+            # decoded codes x effective scales = the oracle's fake-quantized weight
+            idx = np.arange(w.shape[1]) // 16
+            dec = opack.fp4_unpack(t[p + "weight_packed"].numpy()) * (sc / np.float32(gs)).astype(np.float32)[:, idx]
+            oa = OArgs(num_bits=4, type="float", strategy="tensor_group", group_size=16)
+            fq = ofq.fake_quantize(torch.from_numpy(w), torch.from_numpy(sc[:, idx]), None, oa,
+                                   global_scale=gs.reshape(1))
+            assert np.array_equal(dec, fq.numpy())
         elif scheme == "W8A8":
             oa = OArgs(num_bits=8, strategy="channel")
             assert torch.equal(t[p + "weight"], _oracle_codes(lin, oa).to(torch.int8))
@@ -118,6 +135,64 @@ def test_save_formats(dev, tmp_path, scheme, fmt):
             assert np.array_equal(packed_zp.numpy(), opack.pack_to_int32(zp.numpy(), 4, packed_dim=0))
             assert np.array_equal(opack.unpack_from_int32(packed_zp.numpy(), zp.shape[0], 4, packed_dim=0),
                                   zp.numpy())
+
+
+def test_fp4_quantize_pack_matches_oracle(dev):
+    """NVFP4 weight codes with given scales against the oracle, bit for bit:
+    bf16 and fp32 inputs, quotients on and next to every rounding threshold,
+    negative values rounding to zero, zeros of both signs."""
+    say("fp4_quantize_pack vs oracle")
+    rng = np.random.default_rng(21)
+    rows, cols, g = 37, 96, 16
+    sc = (2.0 ** rng.integers(-6, 3, size=(rows, cols // g))).astype(np.float32) * \
+        rng.choice(np.array([1.0, 1.125, 1.5, 1.75], np.float32), size=(rows, cols // g))
+    gs = np.float32(448.0 * 6.0 / 3.7)
+    s_eff = (sc / gs).astype(np.float32)[:, np.arange(cols) // g]
+    thr = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0, 7.0, 0.1], np.float32)
+    t = rng.choice(thr, size=(rows, cols)) * rng.choice(np.array([1.0, 1.0 + 2 ** -20, 1.0 - 2 ** -20], np.float32),
+                                                      size=(rows, cols))
+    t *= rng.choice(np.array([1.0, -1.0], np.float32), size=(rows, cols))
+    x = (t * s_eff).astype(np.float32)
+    x[0, :4] = [0.0, -0.0, -1e-30, 1e-30]
+    for dtype in (torch.float32, torch.bfloat16):
+        xt = torch.from_numpy(x).to(dtype)
+        got = ops.fp4_quantize_pack(xt.to(dev), torch.from_numpy(sc).to(dev), g, torch.tensor([gs]).to(dev))
+        want = opack.fp4_group_quantize_pack(xt.float().numpy(), sc, g, float(gs))
+        assert np.array_equal(got.cpu().numpy(), want), dtype
+    none = ops.fp4_quantize_pack(torch.from_numpy(x).to(dev), torch.from_numpy(sc).to(dev), g)
+    assert np.array_equal(none.cpu().numpy(), opack.fp4_group_quantize_pack(x, sc, g))
+
+
+def test_save_gptq_nvfp4_checkpoint(dev, tmp_path):
+    """GPTQ with NVFP4 weights, then the checkpoint: the file's codes are
+    the oracle's codes of the stored weight, group scales and global scale
+    (the global scale stored in the weight dtype, as the reference stores
+    it), and they decode to the GPTQ weight the module holds, on the fp4
+    grid, up to the rounding of the stored global scale and of the weight
+    to bf16 (2^-8 each)."""
+    from llmcompressor_amd import GPTQModifier
+    say("save GPTQ NVFP4A16")
+    model = _model(dev)
+    g = torch.Generator(device=dev).manual_seed(3)
+    batches = [torch.randn(4, 64, 256, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
+    GPTQModifier(scheme="NVFP4A16", targets=("Linear",), ignore=()).apply(model, batches)
+    save_compressed(model, str(tmp_path))
+    t = _load_dir(tmp_path)
+    assert json.loads((tmp_path / "config.json").read_text())["quantization_config"]["format"] == \
+        "nvfp4-pack-quantized"
+    for i in (0, 2, 3):
+        lin, p = model[i], f"{i}."
+        w = lin.weight.detach().cpu().float().numpy()
+        sc = lin.weight_scale.detach().cpu().float().numpy()
+        gs = float(lin.weight_global_scale.detach().cpu().float())
+        packed = t[p + "weight_packed"].numpy()
+        assert np.array_equal(packed, opack.fp4_group_quantize_pack(w, sc, 16, gs))
+        assert t[p + "weight_scale"].dtype == torch.float8_e4m3fn
+        assert t[p + "weight_global_scale"].tolist() == [gs]
+        dec = opack.fp4_unpack(packed) * (sc / np.float32(gs)).astype(np.float32)[:, np.arange(w.shape[1]) // 16]
+        err = np.abs(dec - w)
+        say(f"  layer {i}: decoded vs GPTQ weight, max rel {float(np.max(err / np.maximum(np.abs(w), 1e-30))):.2e}")
+        assert bool(np.all(err <= 2.0 ** -7 * np.abs(w))), i
 
 
 def test_int8_packer_rewrites_int4_layers(dev, tmp_path):

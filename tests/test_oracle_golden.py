@@ -168,6 +168,37 @@ def test_mxfp4_numpy_matches_torch_fake_quant_path():
         del obs_abs
 
 
+def test_nvfp4_packer_matches_torch_fake_quant_path():
+    """The numpy NVFP4 packer (codes of x / (scale / global_scale)) decodes to
+    the torch ``fake_quantize`` of the same weight with the same fp8 group
+    scales and global scale, element for element, and each code is the
+    nearest e2m1 value of its quotient (ties to even)."""
+    g = torch.Generator().manual_seed(6)
+    x = (torch.randn(48, 128, generator=g) * torch.exp(torch.randn(48, 1, generator=g) * 2)).to(torch.bfloat16)
+    x[0, :16] = 0
+    x[1, 3] = -1e-30
+    xf = x.float()
+    amax = xf.abs().reshape(48, 8, 16).amax(dim=2)
+    gs = torch.tensor([448.0 * 6.0], dtype=torch.float32) / xf.abs().max()
+    sc = (gs * amax / 6.0).clamp(min=2.0 ** -9).to(torch.float8_e4m3fn).float()
+    packed = opack.fp4_group_quantize_pack(xf.numpy(), sc.numpy(), 16, float(gs))
+    assert packed.shape == (48, 64) and packed.dtype == np.uint8
+    s_full = sc.repeat_interleave(16, dim=1)
+    args = OArgs(num_bits=4, type="float", strategy="tensor_group", group_size=16)
+    fq = ofq.fake_quantize(xf, s_full, None, args, global_scale=gs)
+    s_eff = s_full / gs
+    back = opack.fp4_unpack(packed) * s_eff.numpy()
+    assert np.array_equal(back, fq.numpy())
+    # brute force: the decoded grid value is the nearest to the clamped quotient
+    q = (xf / s_eff).clamp(-6, 6)
+    grid = torch.tensor([-6, -4, -3, -2, -1.5, -1, -0.5, 0, 0.5, 1, 1.5, 2, 3, 4, 6], dtype=torch.float32)
+    dist = (q.reshape(-1, 1) - grid).abs().min(dim=1).values.reshape(q.shape)
+    assert torch.equal((q - torch.from_numpy(opack.fp4_unpack(packed))).abs(), dist)
+    # without a global scale the quotient is x / scale
+    p1 = opack.fp4_group_quantize_pack(xf.numpy(), (sc / gs).numpy(), 16)
+    assert np.array_equal(p1, packed)
+
+
 def test_mx_scale_rules_bound_the_group():
     """OCP: amax / scale in [4, 8); CT rule: amax / scale in [3.5, 7)."""
     bits = _all_finite_bf16()
