@@ -65,48 +65,78 @@ __device__ __forceinline__ int8_t code_of(float qq) {
   return (int8_t)qq;
 }
 
+// The Hinv values one step uses (diagonal, its reciprocal, and row I at the
+// lane's columns from slot TO on), read from LDS two steps ahead so that the
+// reads' latency stays off the serial chain.
+struct StepH {
+  float dd, rd, h[SW_T];
+};
+
+template <int I>
+__device__ __forceinline__ void load_step(StepH& p, const float* h1, const float* rdg, int g) {
+  if constexpr (I < MAXB) {
+    constexpr int TO = I / SW_G;
+    p.dd = h1[hrow(I)];
+    p.rd = rdg[I];
+    // (col < I reads a neighbouring entry, in bounds, and is never taken)
+#pragma unroll
+    for (int t = TO; t < SW_T; ++t) p.h[t] = h1[hrow(I) - I + SW_G * t + g];
+  }
+}
+
 // One column of the sweep: column I = SW_G * TO + GO, owned by lane GO of
 // each row.  Every lane quantises its own slot TO (only the owner's value is
 // column I; the others are discarded), the owner's error is broadcast within
 // the row, and each lane updates its later columns.  A lane's slot is final
 // from its own step on, so its code, dequantised value and error are
 // recomputed once after the sweep instead of being selected at every step.
+// The update of the slot holding column I + 1 comes first and ends the
+// step's scheduling region: the other updates then interleave with the next
+// step's chain, and the reads issued with them (two steps ahead) cannot sink
+// into the step that uses them.
 template <int TO, int GO, bool FULL, bool BF16, bool ZP, int QK>
-__device__ __forceinline__ void sweep_step(SweepState& S, const float* h1, const float* rdg, int g, int count,
-                                           float qmin, float qmax) {
+__device__ __forceinline__ void sweep_step(SweepState& S, const StepH& p, int g, int count, float qmin,
+                                           float qmax) {
   constexpr int I = SW_G * TO + GO;
   if (!FULL && I >= count) return;
-  const float dd = h1[hrow(I)];
+  constexpr int TN = GO == SW_G - 1 ? TO + 1 : TO;  // slot of column I + 1
   const float x = S.w[TO];
   float qq, deq;
   quant1<BF16, ZP, QK>(x, S.s[TO], S.rs[TO], S.z[TO], qmin, qmax, qq, deq);
-  const float err = div_by_recip(x - deq, dd, rdg[I]);
+  const float err = div_by_recip(x - deq, p.dd, p.rd);
   const float e = row_bcast<GO>(err);
-#pragma unroll
-  for (int t = TO; t < SW_T; ++t) {
+  auto update = [&](int t) __attribute__((always_inline)) {
     const int col = SW_G * t + g;
-    // (col < I reads a neighbouring entry, in bounds, and is never taken)
-    const float upd = S.w[t] - e * h1[hrow(I) - I + col];
+    const float upd = S.w[t] - e * p.h[t];
     if (t == TO)
       S.w[t] = g > GO ? upd : S.w[t];
     else if (FULL)
       S.w[t] = upd;
     else
       S.w[t] = col < count ? upd : S.w[t];
-  }
+  };
+  if (TN < SW_T) update(TN);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = TO; t < SW_T; ++t)
+    if (t != TN) update(t);
 }
 
+// cur: the values of step I, nxt: those of step I + 1
 template <int I, bool FULL, bool BF16, bool ZP, int QK>
 struct SweepSteps {
   static __device__ __forceinline__ void run(SweepState& S, const float* h1, const float* rdg, int g, int count,
-                                             float qmin, float qmax) {
-    sweep_step<I / SW_G, I % SW_G, FULL, BF16, ZP, QK>(S, h1, rdg, g, count, qmin, qmax);
-    SweepSteps<I + 1, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax);
+                                             float qmin, float qmax, const StepH& cur, const StepH& nxt) {
+    StepH nn;
+    load_step<I + 2>(nn, h1, rdg, g);
+    sweep_step<I / SW_G, I % SW_G, FULL, BF16, ZP, QK>(S, cur, g, count, qmin, qmax);
+    SweepSteps<I + 1, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax, nxt, nn);
   }
 };
 template <bool FULL, bool BF16, bool ZP, int QK>
 struct SweepSteps<MAXB, FULL, BF16, ZP, QK> {
-  static __device__ __forceinline__ void run(SweepState&, const float*, const float*, int, int, float, float) {}
+  static __device__ __forceinline__ void run(SweepState&, const float*, const float*, int, int, float, float,
+                                             const StepH&, const StepH&) {}
 };
 
 // Element strides between the matrices of a batch (blockIdx.y); zero for a
@@ -177,7 +207,10 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     S.z[t] = ZP ? zp[si] : 0.f;
   }
 
-  SweepSteps<0, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax);
+  StepH p0, p1;
+  load_step<0>(p0, h1, rdg, g);
+  load_step<1>(p1, h1, rdg, g);
+  SweepSteps<0, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax, p0, p1);
 
   // each slot is final: its code, dequantised value, error and loss
   float loss = 0.f;

@@ -909,7 +909,11 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
   // block), so its dependency chain is kept short: rl = 1 / L[j][j] straight
   // from the hardware reciprocal square root (within 1 ulp), and the column
   // is scaled by the reciprocal, as LAPACK's potf2 scales it (dscal by
-  // 1 / ajj).
+  // 1 / ajj).  The values on the chain from one step to the next, the pivot
+  // col[j] and col[j + 1], col[j + 2] (the updates of the next two columns,
+  // made first), are taken from their lanes with v_readlane; the rest of the
+  // column goes through LDS, written and read a step ahead of its use, so
+  // the LDS round trip stays off the chain.
   auto factor = [&](int o) __attribute__((always_inline)) {
     const int li = lane & 31;
     const bool row_role = lane < SB;
@@ -918,44 +922,72 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
     for (int c = 0; c < SB; ++c) v[c] = row_role ? a[(o + li) * LP + o + c] : ((c == li) ? 1.f : 0.f);
     // every lane stores (column-role lanes into a scratch slot): no
     // divergent branch around the LDS write that the reads could sink into.
-    // Only col[j..SB-1] is used: the reads cover the aligned quads of it.
+    // Only col[j + 3 .. SB - 1] is read from LDS, exactly those elements (a
+    // loaded element that is never used frees its register while the load
+    // may still be in flight, and the register's next use would wait for it)
     float col[SB];
     auto read_col = [&](int j, float* c) __attribute__((always_inline)) {
+      int k = j;
+      if (k & 1) {
+        c[k] = cb[k];
+        ++k;
+      }
+      if ((k & 3) == 2) {
+        const f32x2_t w = *reinterpret_cast<const f32x2_t*>(cb + k);
+        c[k] = w[0];
+        c[k + 1] = w[1];
+        k += 2;
+      }
 #pragma unroll
-      for (int q = j / 4; q < SB / 4; ++q) {
-        const f32x4_t w = *reinterpret_cast<const f32x4_t*>(cb + 4 * q);
-        c[4 * q] = w[0];
-        c[4 * q + 1] = w[1];
-        c[4 * q + 2] = w[2];
-        c[4 * q + 3] = w[3];
+      for (; k < SB; k += 4) {
+        const f32x4_t w = *reinterpret_cast<const f32x4_t*>(cb + k);
+        c[k] = w[0];
+        c[k + 1] = w[1];
+        c[k + 2] = w[2];
+        c[k + 3] = w[3];
       }
     };
+    // lane l's x (l a constant below SB: a row-role lane)
+    auto from_lane = [](float x, int l) __attribute__((always_inline)) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+    };
+    // chain values of step j: piv = col[j], c1 = col[j + 1], c2 = col[j + 2]
+    float piv = from_lane(v[0], 0), c1 = from_lane(v[0], 1), c2 = from_lane(v[0], 2);
     cb[lane] = v[0];
-    read_col(0, col);
+    read_col(3, col);
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
-      const float piv = col[j];
       pmin = fminf(pmin, piv);
       pnan += piv - piv;
       const float rl = __builtin_amdgcn_rsqf(piv);
       const float sj = v[j] * rl;
       const float m = sj * rl;
-      // software pipeline: the next column is updated, written and read
-      // back first, so the LDS round trip overlaps this step's other updates
-      float ncol[SB];
+      // software pipeline: the next two columns are updated first, the
+      // next step's chain values read from their lanes and the next column
+      // written and read back, then this step's other updates
+      float ncol[SB], npiv = 0.f, nc1 = 0.f, nc2 = 0.f;
       if (j + 1 < SB) {
-        v[j + 1] = fmaf(-m, col[j + 1], v[j + 1]);
-        cb[lane] = v[j + 1];
-        read_col(j + 1, ncol);
+        v[j + 1] = fmaf(-m, c1, v[j + 1]);
+        if (j + 2 < SB) v[j + 2] = fmaf(-m, c2, v[j + 2]);
+        npiv = from_lane(v[j + 1], j + 1);
+        if (j + 2 < SB) nc1 = from_lane(v[j + 1], j + 2);
+        if (j + 3 < SB) nc2 = from_lane(v[j + 1], j + 3);
+        if (j + 4 < SB) {
+          cb[lane] = v[j + 1];
+          read_col(j + 4, ncol);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int k = j + 2; k < SB; ++k) v[k] = fmaf(-m, col[k], v[k]);
+      for (int k = j + 3; k < SB; ++k) v[k] = fmaf(-m, col[k], v[k]);
       v[j] = sj;
       // (keeps the next step's chain from being scheduled into these updates)
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int k = j + 1; k < SB; ++k) col[k] = ncol[k];
+      for (int k = j + 4; k < SB; ++k) col[k] = ncol[k];
+      piv = npiv;
+      c1 = nc1;
+      c2 = nc2;
     }
     // column li of the sub-block inverse, zeros above the diagonal included
     if (!row_role) {
