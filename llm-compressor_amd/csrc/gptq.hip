@@ -65,25 +65,6 @@ __device__ __forceinline__ int8_t code_of(float qq) {
   return (int8_t)qq;
 }
 
-// The Hinv values one step uses (diagonal, its reciprocal, and row I at the
-// lane's columns from slot TO on), read from LDS two steps ahead so that the
-// reads' latency stays off the serial chain.
-struct StepH {
-  float dd, rd, h[SW_T];
-};
-
-template <int I>
-__device__ __forceinline__ void load_step(StepH& p, const float* h1, const float* rdg, int g) {
-  if constexpr (I < MAXB) {
-    constexpr int TO = I / SW_G;
-    p.dd = h1[hrow(I)];
-    p.rd = rdg[I];
-    // (col < I reads a neighbouring entry, in bounds, and is never taken)
-#pragma unroll
-    for (int t = TO; t < SW_T; ++t) p.h[t] = h1[hrow(I) - I + SW_G * t + g];
-  }
-}
-
 // One column of the sweep: column I = SW_G * TO + GO, owned by lane GO of
 // each row.  Every lane quantises its own slot TO (only the owner's value is
 // column I; the others are discarded), the owner's error is broadcast within

@@ -168,21 +168,22 @@ struct PruneState {
   unsigned qbits;
 };
 
-// Number of lanes L..SW_G-1 of the row whose broadcast (v, rotated lane
-// index) orders before this lane's (v, t): smaller v, or equal v and smaller
-// index.  Lanes outside the group broadcast +inf and have rotated indices
-// past the group's, so they never order before a group member.
-template <int L>
+// Number of the group's lanes with rotated index U..m-1 (lane (I + U) % 16
+// of the row) whose broadcast (v, rotated index) orders before this lane's
+// (v, t): smaller v, or equal v and smaller index.  Only the m lanes a group
+// can hold are visited (m is uniform); members past the block's end
+// broadcast +inf and have rotated indices past every real member's, so they
+// never order before one.
+template <int I, int U>
 struct RankBefore {
-  static __device__ __forceinline__ int run(float v, int t, int I) {
-    const float sv = row_bcast<L>(v);
-    const int st = (L - I) & (SW_G - 1);
-    const int here = (sv < v || (sv == v && st < t)) ? 1 : 0;
-    return here + RankBefore<L + 1>::run(v, t, I);
+  static __device__ __forceinline__ int run(float v, int t, int m) {
+    const float sv = row_bcast<(I + U) & (SW_G - 1)>(v);
+    const int here = (sv < v || (sv == v && U < t)) ? 1 : 0;
+    return here + (U + 1 < m ? RankBefore<I, U + 1>::run(v, t, m) : 0);
   }
 };
-template <>
-struct RankBefore<SW_G> {
+template <int I>
+struct RankBefore<I, SW_G> {
   static __device__ __forceinline__ int run(float, int, int) { return 0; }
 };
 
@@ -192,8 +193,9 @@ struct RankBefore<SW_G> {
 // end), so the rotated lane index t orders them by column.  Each member
 // ranks its tmp among the group's (lower column first on equal values) and is
 // pruned when fewer than n rank before it.
-template <int TO, bool PRESERVE>
-__device__ __forceinline__ void nm_select(PruneState& S, const float* dd2, int g, int I, int we, int n) {
+template <int TO, int GO, bool PRESERVE>
+__device__ __forceinline__ void nm_select(PruneState& S, const float* dd2, int g, int we, int n, int m) {
+  constexpr int I = SW_G * TO + GO;
   const int t = (g - I) & (SW_G - 1);
   const bool member = t < we - I;
   const bool in_a = g >= (I & (SW_G - 1));  // the member's column is in slot TO
@@ -205,34 +207,39 @@ __device__ __forceinline__ void nm_select(PruneState& S, const float* dd2, int g
   const bool q = PRESERVE && ((S.qbits >> slot) & 1u);
   float tmp = saliency(v, dd2[min(col, MAXB - 1)], q);
   if (!member) tmp = __builtin_inff();
-  const int rank = RankBefore<0>::run(tmp, t, I);
+  const int rank = RankBefore<I, 0>::run(tmp, t, m);
   if (member && rank < n) S.bits |= 1u << slot;
 }
 
-// One column of the sweep: column I = SW_G * TO + GO, owned by lane GO.
+// One column of the sweep: column I = SW_G * TO + GO, owned by lane GO.  The
+// update of the slot holding column I + 1 comes first and ends the step's
+// scheduling region, so the Hinv reads issued before it (two steps ahead)
+// cannot sink into the step that uses them.
 template <int TO, int GO, bool NM, bool PRESERVE>
-__device__ __forceinline__ void prune_step(PruneState& S, const float* h1, const float* rdg, const float* dd2, int g,
-                                           int count, int n, int m, int& next_group) {
+__device__ __forceinline__ void prune_step(PruneState& S, const StepH& p, const float* dd2, int g, int count, int n,
+                                           int m, int& next_group) {
   constexpr int I = SW_G * TO + GO;
   if (NM && I == next_group && I < count) {
     next_group += m;
-    nm_select<TO, PRESERVE>(S, dd2, g, I, min(I + m, count), n);
+    nm_select<TO, GO, PRESERVE>(S, dd2, g, min(I + m, count), n, m);
   }
-  const float dd = h1[hrow(I)];
+  constexpr int TN = GO == SW_G - 1 ? TO + 1 : TO;  // slot of column I + 1
   const float x = S.w[TO];
   const float diff = ((S.bits >> TO) & 1u) ? x : 0.f;  // w - q
-  const float err = div_by_recip(diff, dd, rdg[I]);
+  const float err = div_by_recip(diff, p.dd, p.rd);
   const float e = row_bcast<GO>(err);
-#pragma unroll
-  for (int t = TO; t < SW_T; ++t) {
-    const int col = SW_G * t + g;
-    // (col < I reads a neighbouring entry, in bounds, and is never taken)
-    const float upd = S.w[t] - e * h1[hrow(I) - I + col];
+  auto update = [&](int t) __attribute__((always_inline)) {
+    const float upd = S.w[t] - e * p.h[t];
     if (t == TO)
       S.w[t] = g > GO ? upd : S.w[t];
     else
       S.w[t] = upd;
-  }
+  };
+  if (TN < SW_T) update(TN);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = TO; t < SW_T; ++t)
+    if (t != TN) update(t);
   // The updated values are materialised here: without this the compiler sinks
   // each slot's updates past the N:M and mask branches into one chain at the
   // slot's next use, keeping every earlier step's error alive (and spilled).
@@ -240,18 +247,22 @@ __device__ __forceinline__ void prune_step(PruneState& S, const float* h1, const
   for (int t = TO; t < SW_T; ++t) asm volatile("" : "+v"(S.w[t]));
 }
 
+// cur: the Hinv values of step I, nxt: those of step I + 1
 template <int I, bool NM, bool PRESERVE>
 struct PruneSteps {
   static __device__ __forceinline__ void run(PruneState& S, const float* h1, const float* rdg, const float* dd2,
-                                             int g, int count, int n, int m, int& next_group) {
-    prune_step<I / SW_G, I % SW_G, NM, PRESERVE>(S, h1, rdg, dd2, g, count, n, m, next_group);
-    PruneSteps<I + 1, NM, PRESERVE>::run(S, h1, rdg, dd2, g, count, n, m, next_group);
+                                             int g, int count, int n, int m, int& next_group, const StepH& cur,
+                                             const StepH& nxt) {
+    StepH nn;
+    load_step<I + 2>(nn, h1, rdg, g);
+    prune_step<I / SW_G, I % SW_G, NM, PRESERVE>(S, cur, dd2, g, count, n, m, next_group);
+    PruneSteps<I + 1, NM, PRESERVE>::run(S, h1, rdg, dd2, g, count, n, m, next_group, nxt, nn);
   }
 };
 template <bool NM, bool PRESERVE>
 struct PruneSteps<MAXB, NM, PRESERVE> {
   static __device__ __forceinline__ void run(PruneState&, const float*, const float*, const float*, int, int, int,
-                                             int, int&) {}
+                                             int, int&, const StepH&, const StepH&) {}
 };
 
 // NM: N:M groups (else the unstructured threshold in sel); PRESERVE: mask
@@ -324,7 +335,10 @@ __global__ __launch_bounds__(SW_NT, 4) void sgpt_sweep_kernel(float* __restrict_
   }
 
   int next_group = 0;
-  PruneSteps<0, NM, PRESERVE>::run(S, h1, rdg, dd2, g, count, n, m, next_group);
+  StepH p0, p1;
+  load_step<0>(p0, h1, rdg, g);
+  load_step<1>(p1, h1, rdg, g);
+  PruneSteps<0, NM, PRESERVE>::run(S, h1, rdg, dd2, g, count, n, m, next_group, p0, p1);
 
   // each slot is final: kept or zeroed value, error, loss
   float loss = 0.f;

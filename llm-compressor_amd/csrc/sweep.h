@@ -41,6 +41,25 @@ __device__ __forceinline__ float row_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xF, 0xF, false));
 }
 
+// The Hinv values step I of a sweep uses (diagonal, its reciprocal, and row I
+// at the lane's columns from slot I / SW_G on), read from LDS two steps ahead
+// so that the reads' latency stays off the serial chain.
+struct StepH {
+  float dd, rd, h[SW_T];
+};
+
+template <int I>
+__device__ __forceinline__ void load_step(StepH& p, const float* h1, const float* rdg, int g) {
+  if constexpr (I < MAXB) {
+    constexpr int TO = I / SW_G;
+    p.dd = h1[hrow(I)];
+    p.rd = rdg[I];
+    // (col < I reads a neighbouring entry, in bounds, and is never taken)
+#pragma unroll
+    for (int t = TO; t < SW_T; ++t) p.h[t] = h1[hrow(I) - I + SW_G * t + g];
+  }
+}
+
 // Loads Hinv[i1 + i][i1 + j] (j >= i, i, j < count) into the packed LDS
 // triangle h1 with all SW_NT threads (16-byte loads for a whole aligned block).
 __device__ __forceinline__ void load_hinv_block(float* h1, const float* __restrict__ hinv, int64_t cols,
