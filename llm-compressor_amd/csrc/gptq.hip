@@ -120,6 +120,71 @@ struct SweepSteps<MAXB, FULL, BF16, ZP, QK> {
                                              const StepH&, const StepH&) {}
 };
 
+// The K = 128 lazy updates of a block's columns from the npre earlier
+// blocks of its mid-block, applied by the block's own sweep workgroups
+// before the sweep: for p = 0 .. npre-1 in order,
+//   W[rows, i1 : i1 + 128] += -(Err[rows, block p] Hinv[block p, i1 : i1 + 128]),
+// each product formed as the separate K = 128 GEMM forms it (fp32 MFMA
+// 32x32x2, k pairs (4j, 4j+1) on one accumulator and (4j+2, 4j+3) on a
+// second, the two added, negated, then added to W), so the result is the
+// one the lazy products would give.  The workgroup's 16 rows fill half of
+// the MFMA's 32 (rows 16..31 are zero); each wave forms 32 columns.  The
+// error tile and the product pass through LDS (the space the Hinv block
+// fills afterwards); the Hinv panel goes from global memory straight into
+// the B operand.  Rows past the matrix's end hold copies of its last row.
+constexpr int PLD = MAXB + 1;  // LDS row stride of the error and product tiles
+
+__device__ __forceinline__ void pull_updates(SweepState& S, float* lds, const float* __restrict__ err, int64_t lde,
+                                             int err_col0, const float* __restrict__ hinv, int64_t cols,
+                                             int64_t k0, int64_t i1, int64_t row0, int64_t rows, int tid,
+                                             int npre) {
+  float* ea = lds;             // [32][PLD] error tile, rows 16..31 zero
+  float* pt = lds + 32 * PLD;  // [16][PLD] product tile
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = tid & (SW_G - 1), rw = tid / SW_G;
+  for (int e = tid; e < 16 * PLD; e += SW_NT) ea[16 * PLD + e] = 0.f;
+  for (int p = 0; p < npre; ++p) {
+    f32x4_t ev[2];
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int e = v * SW_NT + tid, m = e >> 5, c4 = 4 * (e & 31);
+      const int64_t r = row0 + m < rows ? row0 + m : rows - 1;
+      ev[v] = *reinterpret_cast<const f32x4_t*>(err + r * lde + err_col0 + MAXB * p + c4);
+    }
+    // B operand: b[j] = Hinv[k0 + 128 p + 2 j + lane / 32][i1 + 32 wave + lane % 32]
+    const float* hb = hinv + (k0 + MAXB * p + (lane >> 5)) * cols + i1 + 32 * wave + (lane & 31);
+    float b[MAXB / 2];
+#pragma unroll
+    for (int j = 0; j < MAXB / 2; ++j) b[j] = hb[2 * j * cols];
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int e = v * SW_NT + tid, m = e >> 5, c4 = 4 * (e & 31);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ea[m * PLD + c4 + q] = ev[v][q];
+    }
+    __syncthreads();
+    f32x16_t acc0, acc1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
+    const float* pa = ea + (lane & 31) * PLD + (lane >> 5);
+#pragma unroll
+    for (int kk = 0; kk < MAXB / 2; kk += 2) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[2 * kk], b[kk], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[2 * kk + 2], b[kk + 1], acc1, 0, 0, 0);
+    }
+    // rows 0..15 of the product: registers r < 8
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int m = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      pt[m * PLD + 32 * wave + (lane & 31)] = -1.f * (acc0[r] + acc1[r]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < SW_T; ++t) S.w[t] = 1.f * S.w[t] + pt[rw * PLD + SW_G * t + g];
+    __syncthreads();
+  }
+}
+
 // Element strides between the matrices of a batch (blockIdx.y); zero for a
 // shared operand.
 struct SweepBatch {
@@ -127,15 +192,19 @@ struct SweepBatch {
 };
 
 // FULL: a whole MAXB-column block; BF16: dequantise in bf16; ZP: zero
-// points; QK: value type.  gscale (NULL: 1): per-matrix global scale, the
-// effective scale being scale / gscale (CT's tensor-group scales).
-template <bool FULL, bool BF16, bool ZP, int QK>
+// points; QK: value type; PULL: the block first applies the updates from
+// the npre earlier blocks of its mid-block (a separate variant: its
+// prologue needs more registers than the plain sweep's).  gscale (NULL: 1):
+// per-matrix global scale, the effective scale being scale / gscale (CT's
+// tensor-group scales).
+template <bool FULL, bool BF16, bool ZP, int QK, bool PULL = false>
 __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
     float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
     int count, const float* __restrict__ scale, const float* __restrict__ zp, int64_t ld_scale,
     const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax,
     const float* __restrict__ gscale, int8_t* __restrict__ codes, float* __restrict__ losses,
-    float* __restrict__ err_out, int64_t lde, int err_col, SweepBatch sb) {
+    float* __restrict__ err_out, int64_t lde, int err_col, int npre, int64_t pre_k0, int pre_err_col,
+    SweepBatch sb) {
   __shared__ float h1[HPK];
   __shared__ float rdg[MAXB];  // 1 / Hinv[i][i], correctly rounded
   __shared__ int gsh[MAXB];
@@ -171,6 +240,10 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
   const int dcol = tid < count ? tid : count - 1;
   const float diag = hinv[(i1 + dcol) * cols + i1 + dcol];
   const int gval = uses_gidx ? g_idx[i1 + dcol] : 0;
+  if constexpr (FULL && PULL)
+    if (npre > 0)
+      pull_updates(S, h1, err_out, lde, pre_err_col, hinv, cols, pre_k0, i1, (int64_t)blockIdx.x * SW_ROWS, rows,
+                   tid, npre);
   load_hinv_block(h1, hinv, cols, i1, count, tid);
   if (tid < MAXB) gsh[tid] = tid < count ? gval : 0;
   if (tid < MAXB) rdg[tid] = tid < count ? 1.f / diag : 1.f;
@@ -322,12 +395,16 @@ inline dim3 grid_rows(int64_t rows, int64_t cols, int64_t batch = 1) {
   return dim3((unsigned)gx, (unsigned)rows, (unsigned)batch);
 }
 
-// the kernel variant for (whole block, bf16 dequantisation, zero points)
+// the kernel variant for (whole block, bf16 dequantisation, zero points,
+// pulled updates: integer values only)
 template <class... A>
-void launch_sweep(bool full, bool bf16, bool zp, int qk, dim3 grid, hipStream_t st, A... args) {
+void launch_sweep(bool full, bool bf16, bool zp, int qk, bool pull, dim3 grid, hipStream_t st, A... args) {
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(SW_NT), 0, st, args...); };
   if (qk == QK_INT) {
-    if (full) {
+    if (full && pull) {
+      if (bf16) zp ? go(sweep_block_kernel<true, true, true, QK_INT, true>) : go(sweep_block_kernel<true, true, false, QK_INT, true>);
+      else      zp ? go(sweep_block_kernel<true, false, true, QK_INT, true>) : go(sweep_block_kernel<true, false, false, QK_INT, true>);
+    } else if (full) {
       if (bf16) zp ? go(sweep_block_kernel<true, true, true, QK_INT>) : go(sweep_block_kernel<true, true, false, QK_INT>);
       else      zp ? go(sweep_block_kernel<true, false, true, QK_INT>) : go(sweep_block_kernel<true, false, false, QK_INT>);
     } else {
@@ -414,18 +491,30 @@ extern "C" int mi355q_gptq_sweep_typed_batched(float* w_work_dev, int64_t rows, 
   // they are processed in MAXB-wide sub-blocks
   const int64_t B = blocksize < MAXB ? blocksize : MAXB;
   const unsigned nwg = (unsigned)((rows + SW_ROWS - 1) / SW_ROWS);
-  auto block = [&](int64_t i1, int64_t i2, int64_t s0) {
+  // (npre > 0 only for whole blocks: the schedule pulls only in mid-blocks of whole blocks)
+  auto block = [&](int64_t i1, int64_t i2, int64_t s0, int npre, int64_t m0) {
     const int count = (int)(i2 - i1);
-    launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, qk, dim3(nwg, (unsigned)batch), st, w_work_dev,
-                 rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy, block_h, qmin,
-                 qmax, global_scale_dev, codes_dev, losses_dev, err, lde, (int)(i1 - s0), sb);
+    MQ_CHECK_ARG(npre == 0 || (count == MAXB && qk == QK_INT), "gptq_sweep: pulled updates need whole integer blocks");
+    launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, qk, npre > 0, dim3(nwg, (unsigned)batch), st,
+                 w_work_dev, rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy,
+                 block_h, qmin, qmax, global_scale_dev, codes_dev, losses_dev, err, lde, (int)(i1 - s0), npre, m0,
+                 (int)(m0 - s0), sb);
     MQ_LAUNCH_CHECK();
     return MI355Q_OK;
   };
   auto lazy = [&](int64_t k0, int64_t k1, int64_t s0, int64_t c0, int64_t c1) {
     return lazy_update(w_work_dev, rows, cols, batch, hinv_dev, stride_hinv, err, lde, k0, k1, s0, c0, c1, st);
   };
-  return blocked_schedule(cols, B, block, lazy);
+  // The sweep workgroups apply a mid-block's K = 128 updates themselves for
+  // integer values when the sweep leaves the CUs room for it (at most two of
+  // its workgroups per CU; with more, the separate products use the CUs
+  // better) and the error tile can be read in 16-byte pieces.
+  int dev = 0, ncu = 0;
+  MQ_CHECK_HIP(hipGetDevice(&dev));
+  MQ_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+  const bool can_pull = qk == QK_INT && (int64_t)nwg * batch <= 2 * (int64_t)ncu && lde % 4 == 0 &&
+                        (reinterpret_cast<uintptr_t>(err) & 15) == 0;
+  return blocked_schedule_pull(cols, B, can_pull, block, lazy);
 }
 
 extern "C" int mi355q_gptq_sweep_batched(float* w_work_dev, int64_t rows, int64_t cols, int64_t batch,

@@ -149,5 +149,39 @@ int blocked_schedule(int64_t cols, int64_t B, Block block, Lazy lazy) {
   return MI355Q_OK;
 }
 
+// blocked_schedule for a sweep that applies the K = B updates inside a
+// mid-block itself: when the mid-block's blocks are all whole (B == MAXB),
+// its block q runs as block(i1, i2, s0, q, m0) and first applies the errors
+// of the q blocks before it, in block order, to its own columns, in place of
+// the products lazy(i1, i2, s0, i2, m1) after each of those blocks; other
+// mid-blocks, and all of them without can_pull, run as in blocked_schedule
+// (with q = 0).
+template <class Block, class Lazy>
+int blocked_schedule_pull(int64_t cols, int64_t B, bool can_pull, Block block, Lazy lazy) {
+  const int64_t sup = (SUPER / B) * B, mid = (MID / B) * B;
+  for (int64_t s0 = 0; s0 < cols; s0 += sup) {
+    const int64_t s1 = s0 + sup < cols ? s0 + sup : cols;
+    for (int64_t m0 = s0; m0 < s1; m0 += mid) {
+      const int64_t m1 = m0 + mid < s1 ? m0 + mid : s1;
+      const bool pull = can_pull && B == MAXB && (m1 - m0) % MAXB == 0;
+      for (int64_t i1 = m0; i1 < m1; i1 += B) {
+        const int64_t i2 = (i1 + B < m1) ? i1 + B : m1;
+        int rc = block(i1, i2, s0, pull ? (int)((i1 - m0) / B) : 0, m0);
+        if (rc) return rc;
+        if (!pull && i2 < m1 && (rc = lazy(i1, i2, s0, i2, m1))) return rc;
+      }
+      if (m1 < s1) {
+        const int rc = lazy(m0, m1, s0, m1, s1);
+        if (rc) return rc;
+      }
+    }
+    if (s1 < cols) {
+      const int rc = lazy(s0, s1, s0, s1, cols);
+      if (rc) return rc;
+    }
+  }
+  return MI355Q_OK;
+}
+
 }  // namespace sweep
 }  // namespace mi355q

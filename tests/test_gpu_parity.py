@@ -529,6 +529,28 @@ def test_gptq_batched_equals_single(dev, case):
         assert abs(res[b].loss - single.loss) <= 1e-5 * abs(single.loss) + 1e-12
 
 
+@pytest.mark.parametrize("symmetric", [True, False])
+def test_gptq_pulled_updates_equal_pushed(dev, symmetric):
+    """A 4096-row solve fills at most two sweep workgroups per CU, so each
+    block applies the K = 128 updates of the earlier blocks of its mid-block
+    itself; the same matrix in a batch of three (768 workgroups) gets them
+    from separate K = 128 products after each block.  Both form each product
+    in the same MFMA order, so the results agree bit for bit."""
+    say(f"gptq pulled vs pushed mid-block updates, symmetric={symmetric}")
+    rows, d = 4096, 512
+    qa = QuantizationArgs(type="int", num_bits=4, strategy="group", group_size=128, symmetric=symmetric)
+    W = workloads.gptq_weight(rows, d, seed=41).to(dev)
+    H = torch.triu(_spd_from_tokens(d, 2048, seed=42)).to(dev)
+    obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+    obs(W)
+    single = gptq.gptq_quantize(W, qa, H.clone(), obs, num_samples=1.0)
+    res = gptq.gptq_quantize_batched(W.unsqueeze(0).repeat(3, 1, 1).contiguous(), qa,
+                                     H.unsqueeze(0).repeat(3, 1, 1).contiguous(), num_samples=1.0)
+    for b in range(3):
+        assert torch.equal(res[b].codes, single.codes), b
+        assert torch.equal(res[b].weight, single.weight), b
+
+
 def test_gptq_prepared_hessian_shared(dev):
     """Modules with the same input (q/k/v, gate/up) may share the Cholesky
     chain: a prepared Hessian gives exactly the results of separate solves."""
