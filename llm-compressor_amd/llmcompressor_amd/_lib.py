@@ -124,7 +124,13 @@ def call(name: str, *args) -> None:
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
+    """Device address of an optional operand (None: a null pointer); a
+    tensor on the host is refused, as the kernels would read it as device
+    memory."""
+    if t is None:
+        return None
+    require_gpu(t)
+    return t.data_ptr()
 
 
 def stream_of(t: torch.Tensor) -> int:

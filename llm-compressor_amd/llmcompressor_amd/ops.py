@@ -211,7 +211,8 @@ def gptq_sweep_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.Tensor, z
     s = scale.to(torch.float32).contiguous()
     if s.dim() == 1:
         s = s.reshape(-1, 1)
-    z = None if zero_point is None else zero_point.to(torch.float32).reshape(s.shape).contiguous()
+    z = None if zero_point is None else \
+        zero_point.to(device=w_work.device, dtype=torch.float32).reshape(s.shape).contiguous()
     return gptq_sweep_batched_(w_work.unsqueeze(0), hinv.unsqueeze(0), s.unsqueeze(0),
                                None if z is None else z.unsqueeze(0), strategy, g_idx, qmin, qmax, dequant_bf16,
                                blocksize, block_h, qtype, global_scale, _unbatch=True)
@@ -286,8 +287,8 @@ def gptq_sweep_batched_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.T
     if hinv.stride(2) != 1 or hinv.stride(1) != cols:
         hinv = hinv.contiguous()   # row-major matrices, any batch stride
     s = scale.to(torch.float32).reshape(B, -1, scale.shape[-1] if scale.dim() == 3 else 1).contiguous()
-    z = None if zero_point is None else zero_point.to(torch.float32).reshape(s.shape).contiguous()
-    gi = None if g_idx is None else g_idx.to(torch.int32).contiguous()
+    z = None if zero_point is None else zero_point.to(device=dev, dtype=torch.float32).reshape(s.shape).contiguous()
+    gi = None if g_idx is None else g_idx.to(device=dev, dtype=torch.int32).contiguous()
     gs = None
     if global_scale is not None:
         gs = global_scale.to(device=dev, dtype=torch.float32).reshape(-1)
@@ -406,8 +407,9 @@ def quantize_int(x: torch.Tensor, scale: torch.Tensor, zero_point, strategy: str
     rows, cols = x.shape
     s = scale.to(torch.float32).contiguous()
     s2 = s.reshape(-1, 1) if s.dim() < 2 else s
-    z = None if zero_point is None else zero_point.to(torch.float32).reshape(s2.shape).contiguous()
-    gi = None if g_idx is None else g_idx.to(torch.int32).contiguous()
+    z = None if zero_point is None else \
+        zero_point.to(device=x.device, dtype=torch.float32).reshape(s2.shape).contiguous()
+    gi = None if g_idx is None else g_idx.to(device=x.device, dtype=torch.int32).contiguous()
     bh, bw = block_structure if block_structure else (1, 1)
     if div_dtype is None:
         div_dtype = torch.promote_types(x.dtype, scale.dtype)
@@ -558,7 +560,8 @@ def fp4_quantize_pack(x: torch.Tensor, scale: torch.Tensor, group_size: int,
         x = x.contiguous()
     rows, cols = x.shape
     s = scale.to(torch.float32).reshape(rows, -1).contiguous()
-    gs = None if global_scale is None else global_scale.to(torch.float32).reshape(1).contiguous()
+    gs = None if global_scale is None else \
+        global_scale.to(device=x.device, dtype=torch.float32).reshape(1).contiguous()
     out = torch.empty((rows, cols // 2), dtype=torch.uint8, device=x.device)
     L.call("mi355q_fp4_quantize_pack", x.data_ptr(), _dt(x), rows, cols, x.stride(0), s.data_ptr(), s.stride(0),
            group_size, L.ptr(gs), out.data_ptr(), L.stream_of(x))

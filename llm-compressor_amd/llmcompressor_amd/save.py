@@ -33,7 +33,7 @@ unpinned: the library is absent and no reference test holds a checkpoint):
 * ``nvfp4-pack-quantized``: ``weight_packed`` uint8 [rows, cols / 2] (the
   same code layout, e2m1 of weight / (scale / global_scale)),
   ``weight_scale`` float8_e4m3fn [rows, cols / 16], ``weight_global_scale``
-  float32 [1].
+  [1] in the module's dtype for it.
 """
 from __future__ import annotations
 
@@ -96,8 +96,11 @@ def compress_module(module: torch.nn.Module, fmt: str | None = None) -> dict[str
         scale = module.weight_scale.data
         packed = ops.fp4_quantize_pack(module.weight, scale, w.group_size, gs.data)
         # the group scales are fp8 values held in a wider dtype: the cast is exact
+        # the global scale is written as the module holds it (fp32 after
+        # calibration, the weight dtype after GPTQ), as a parameter the
+        # compressor passes through
         return {"weight_packed": packed, "weight_scale": scale.to(torch.float8_e4m3fn),
-                "weight_global_scale": gs.data.to(torch.float32).reshape(1)}
+                "weight_global_scale": gs.data.reshape(1)}
     out = {"weight_scale": module.weight_scale.data}
     if w.type == QuantizationType.INT:
         codes = _codes(module, w)

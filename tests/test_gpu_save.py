@@ -159,6 +159,9 @@ def test_fp4_quantize_pack_matches_oracle(dev):
         got = ops.fp4_quantize_pack(xt.to(dev), torch.from_numpy(sc).to(dev), g, torch.tensor([gs]).to(dev))
         want = opack.fp4_group_quantize_pack(xt.float().numpy(), sc, g, float(gs))
         assert np.array_equal(got.cpu().numpy(), want), dtype
+    # a global scale held on the host is moved to the weight's device
+    host_gs = ops.fp4_quantize_pack(torch.from_numpy(x).to(dev), torch.from_numpy(sc).to(dev), g, torch.tensor([gs]))
+    assert np.array_equal(host_gs.cpu().numpy(), opack.fp4_group_quantize_pack(x, sc, g, float(gs)))
     none = ops.fp4_quantize_pack(torch.from_numpy(x).to(dev), torch.from_numpy(sc).to(dev), g)
     assert np.array_equal(none.cpu().numpy(), opack.fp4_group_quantize_pack(x, sc, g))
 
@@ -189,6 +192,7 @@ def test_save_gptq_nvfp4_checkpoint(dev, tmp_path):
         assert np.array_equal(packed, opack.fp4_group_quantize_pack(w, sc, 16, gs))
         assert t[p + "weight_scale"].dtype == torch.float8_e4m3fn
         assert t[p + "weight_global_scale"].tolist() == [gs]
+        assert t[p + "weight_global_scale"].dtype == lin.weight_global_scale.dtype
         dec = opack.fp4_unpack(packed) * (sc / np.float32(gs)).astype(np.float32)[:, np.arange(w.shape[1]) // 16]
         err = np.abs(dec - w)
         say(f"  layer {i}: decoded vs GPTQ weight, max rel {float(np.max(err / np.maximum(np.abs(w), 1e-30))):.2e}")

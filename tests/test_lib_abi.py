@@ -92,3 +92,12 @@ def test_sparsegpt_limits_are_reported_unsupported():
     rc = lib.mi355q_sparsegpt_sweep(C.c_void_p(16), 4, 512, C.c_void_p(16), C.c_double(0.5), 16, 32, 128, None,
                                     C.c_void_p(16), C.c_void_p(16), 1 << 24, None)
     assert rc == _lib.UNSUPPORTED and "wider than 16" in lib.mi355q_last_error().decode()
+
+
+def test_host_tensors_are_refused_as_device_operands():
+    """An optional operand left on the host would be read as device memory;
+    the pointer helper refuses it before any call."""
+    import torch
+    assert _lib.ptr(None) is None
+    with pytest.raises(RuntimeError, match="GPU only"):
+        _lib.ptr(torch.zeros(4))
