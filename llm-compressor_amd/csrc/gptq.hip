@@ -292,6 +292,160 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
   if (live && g == 0) losses[r] = losses[r] + loss / 2.f;
 }
 
+// ---------------------------------------------------------------- wide sweep
+// The same sweep with 4 lanes per row (lane g holds block columns 4 t + g,
+// t = 0..31) and 64 rows per workgroup, for batches large enough to keep
+// every SIMD busy several times over (the MoE projections: 98304 rows and
+// more per launch).  There the 16-lane sweep is bound by instruction issue:
+// every lane of a row repeats the owner's quantisation, 8 VALU instructions
+// per row and column against about 3 here.  Each element sees the same
+// operations in the same order as in the 16-lane sweep (quantise, error,
+// rounded product, rounded subtract), so the results are the same bits.
+// Symmetric scales only: a zero point per slot would not fit the registers
+// of three waves per SIMD, which the chain needs to hide its latency.
+constexpr int W4_G = 4;                  // lanes per row
+constexpr int W4_T = MAXB / W4_G;        // columns per lane
+constexpr int W4_ROWS = SW_NT / W4_G;    // rows per workgroup
+
+struct Sweep4State {
+  float w[W4_T], s[W4_T], rs[W4_T];
+};
+
+struct StepH4 {
+  float dd, rd, h[W4_T];
+};
+
+template <int I>
+__device__ __forceinline__ void load_step4(StepH4& p, const float* h1, const float* rdg, int g) {
+  if constexpr (I < MAXB) {
+    constexpr int TO = I / W4_G;
+    p.dd = h1[hrow(I)];
+    p.rd = rdg[I];
+    // (col < I reads a neighbouring entry, in bounds, and is never taken)
+#pragma unroll
+    for (int t = TO; t < W4_T; ++t) p.h[t] = h1[hrow(I) - I + W4_G * t + g];
+  }
+}
+
+// Broadcast lane L of every group of 4 lanes to the group (DPP quad_perm).
+template <int L>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), L * 0x55, 0xF, 0xF, false));
+}
+
+template <int TO, int GO, bool BF16>
+__device__ __forceinline__ void sweep4_step(Sweep4State& S, const StepH4& p, int g, float qmin, float qmax) {
+  constexpr int TN = GO == W4_G - 1 ? TO + 1 : TO;  // slot of column I + 1
+  const float x = S.w[TO];
+  float qq, deq;
+  quant1<BF16, false, QK_INT>(x, S.s[TO], S.rs[TO], 0.f, qmin, qmax, qq, deq);
+  const float err = div_by_recip(x - deq, p.dd, p.rd);
+  const float e = quad_bcast<GO>(err);
+  auto update = [&](int t) __attribute__((always_inline)) {
+    const float upd = S.w[t] - e * p.h[t];
+    S.w[t] = t == TO ? (g > GO ? upd : S.w[t]) : upd;
+  };
+  if (TN < W4_T) update(TN);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = TO; t < W4_T; ++t)
+    if (t != TN) update(t);
+}
+
+// cur: the Hinv values of step I (read one step ahead: two, as in the
+// 16-lane sweep, would leave registers for only two waves per SIMD)
+template <int I, bool BF16>
+struct Sweep4Steps {
+  static __device__ __forceinline__ void run(Sweep4State& S, const float* h1, const float* rdg, int g, float qmin,
+                                             float qmax, const StepH4& cur) {
+    StepH4 nn;
+    load_step4<I + 1>(nn, h1, rdg, g);
+    sweep4_step<I / W4_G, I % W4_G, BF16>(S, cur, g, qmin, qmax);
+    Sweep4Steps<I + 1, BF16>::run(S, h1, rdg, g, qmin, qmax, nn);
+  }
+};
+template <bool BF16>
+struct Sweep4Steps<MAXB, BF16> {
+  static __device__ __forceinline__ void run(Sweep4State&, const float*, const float*, int, float, float,
+                                             const StepH4&) {}
+};
+
+// Whole MAXB-column blocks of integer values with symmetric scales;
+// arguments as sweep_block_kernel.
+template <bool BF16>
+__global__ __launch_bounds__(SW_NT, 3) void sweep4_block_kernel(
+    float* __restrict__ W, int64_t rows, int64_t cols, const float* __restrict__ hinv, int64_t i1,
+    const float* __restrict__ scale, int64_t ld_scale,
+    const int32_t* __restrict__ g_idx, int strategy, int block_h, float qmin, float qmax,
+    const float* __restrict__ gscale, int8_t* __restrict__ codes, float* __restrict__ losses,
+    float* __restrict__ err_out, int64_t lde, int err_col, SweepBatch sb) {
+  __shared__ float h1[HPK];
+  __shared__ float rdg[MAXB];
+  __shared__ int gsh[MAXB];
+  {
+    const int64_t b = blockIdx.y;
+    W += b * sb.w;
+    hinv += b * sb.hinv;
+    scale += b * sb.scale;
+    if (g_idx) g_idx += b * sb.gidx;
+    codes += b * sb.codes;
+    losses += b * sb.losses;
+    err_out += b * sb.err;
+  }
+  const int tid = threadIdx.x;
+  const int g = tid & (W4_G - 1);
+  const int64_t r = (int64_t)blockIdx.x * W4_ROWS + (tid / W4_G);
+  const bool live = r < rows;
+  const int64_t rr = live ? r : rows - 1;
+  const float gsc = gscale ? gscale[blockIdx.y] : 1.f;
+
+  Sweep4State S;
+#pragma unroll
+  for (int t = 0; t < W4_T; ++t) S.w[t] = W[rr * cols + i1 + W4_G * t + g];
+  const bool uses_gidx = strategy == MI355Q_GROUP || strategy == MI355Q_BLOCK;
+  const float diag = hinv[(i1 + (tid & (MAXB - 1))) * cols + i1 + (tid & (MAXB - 1))];
+  const int gval = uses_gidx ? g_idx[i1 + (tid & (MAXB - 1))] : 0;
+  load_hinv_block(h1, hinv, cols, i1, MAXB, tid);
+  if (tid < MAXB) gsh[tid] = gval;
+  if (tid < MAXB) rdg[tid] = 1.f / diag;
+  __syncthreads();
+
+  int64_t sbase = 0;
+  if (strategy == MI355Q_CHANNEL || strategy == MI355Q_GROUP) sbase = rr * ld_scale;
+  if (strategy == MI355Q_BLOCK) sbase = (rr / block_h) * ld_scale;
+#pragma unroll
+  for (int t = 0; t < W4_T; ++t) {
+    const int64_t si = sbase + gsh[W4_G * t + g];
+    S.s[t] = scale[si] / gsc;
+    S.rs[t] = 1.f / S.s[t];
+  }
+
+  StepH4 p0;
+  load_step4<0>(p0, h1, rdg, g);
+  Sweep4Steps<0, BF16>::run(S, h1, rdg, g, qmin, qmax, p0);
+
+  float loss = 0.f;
+#pragma unroll
+  for (int t = 0; t < W4_T; ++t) {
+    const int col = W4_G * t + g;
+    const float dd = h1[hrow(col)];
+    float qq, deq;
+    quant1<BF16, false, QK_INT>(S.w[t], S.s[t], S.rs[t], 0.f, qmin, qmax, qq, deq);
+    const float diff = S.w[t] - deq;
+    const float err = div_by_recip(diff, dd, rdg[col]);
+    loss = loss + diff * diff / (dd * dd);
+    if (live) {
+      const int64_t c = i1 + col;
+      W[r * cols + c] = deq;
+      codes[r * cols + c] = code_of<QK_INT>(qq);
+      err_out[r * lde + err_col + col] = err;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < W4_G; o <<= 1) loss += __shfl_xor(loss, o, W4_G);
+  if (live && g == 0) losses[r] = losses[r] + loss / 2.f;
+}
+
 // One row per blockIdx.y, four consecutive output columns per thread.
 // (matrix blockIdx.z of a batch: w + z sw elements, perm + z sp, dead + z cols,
 // out + z rows cols)
@@ -491,10 +645,28 @@ extern "C" int mi355q_gptq_sweep_typed_batched(float* w_work_dev, int64_t rows, 
   // they are processed in MAXB-wide sub-blocks
   const int64_t B = blocksize < MAXB ? blocksize : MAXB;
   const unsigned nwg = (unsigned)((rows + SW_ROWS - 1) / SW_ROWS);
+  int dev = 0, ncu = 0;
+  MQ_CHECK_HIP(hipGetDevice(&dev));
+  MQ_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+  // Whole integer blocks with symmetric scales of grids with at least eight
+  // 16-lane workgroups per CU take the 4-lane sweep (instruction issue, not
+  // latency, bounds the 16-lane sweep there).
+  const bool wide = (int64_t)nwg * batch >= 8 * (int64_t)ncu;
   // (npre > 0 only for whole blocks: the schedule pulls only in mid-blocks of whole blocks)
   auto block = [&](int64_t i1, int64_t i2, int64_t s0, int npre, int64_t m0) {
     const int count = (int)(i2 - i1);
     MQ_CHECK_ARG(npre == 0 || (count == MAXB && qk == QK_INT), "gptq_sweep: pulled updates need whole integer blocks");
+    if (wide && count == MAXB && qk == QK_INT && !zp_dev && npre == 0) {
+      const dim3 grid4((unsigned)((rows + W4_ROWS - 1) / W4_ROWS), (unsigned)batch);
+      auto go4 = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid4, dim3(SW_NT), 0, st, w_work_dev, rows, cols, hinv_dev, i1, scale_dev,
+                           ld_scale, g_idx_dev, strategy, block_h, qmin, qmax, global_scale_dev, codes_dev,
+                           losses_dev, err, lde, (int)(i1 - s0), sb);
+      };
+      dequant_bf16 ? go4(sweep4_block_kernel<true>) : go4(sweep4_block_kernel<false>);
+      MQ_LAUNCH_CHECK();
+      return MI355Q_OK;
+    }
     launch_sweep(count == MAXB, dequant_bf16 != 0, zp_dev != nullptr, qk, npre > 0, dim3(nwg, (unsigned)batch), st,
                  w_work_dev, rows, cols, hinv_dev, i1, count, scale_dev, zp_dev, ld_scale, g_idx_dev, strategy,
                  block_h, qmin, qmax, global_scale_dev, codes_dev, losses_dev, err, lde, (int)(i1 - s0), npre, m0,
@@ -509,9 +681,6 @@ extern "C" int mi355q_gptq_sweep_typed_batched(float* w_work_dev, int64_t rows, 
   // integer values when the sweep leaves the CUs room for it (at most two of
   // its workgroups per CU; with more, the separate products use the CUs
   // better) and the error tile can be read in 16-byte pieces.
-  int dev = 0, ncu = 0;
-  MQ_CHECK_HIP(hipGetDevice(&dev));
-  MQ_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
   const bool can_pull = qk == QK_INT && (int64_t)nwg * batch <= 2 * (int64_t)ncu && lde % 4 == 0 &&
                         (reinterpret_cast<uintptr_t>(err) & 15) == 0;
   return blocked_schedule_pull(cols, B, can_pull, block, lazy);

@@ -551,6 +551,32 @@ def test_gptq_pulled_updates_equal_pushed(dev, symmetric):
         assert torch.equal(res[b].weight, single.weight), b
 
 
+@pytest.mark.parametrize("cols,kw", [(128, dict(num_bits=8, strategy="channel")),
+                                     (256, dict(num_bits=4, strategy="group", group_size=64)),
+                                     (256, dict(num_bits=4, strategy="group", group_size=64, symmetric=False))])
+def test_gptq_wide_sweep_equals_single(dev, cols, kw):
+    """A batch of eight 4096-row matrices (2048 sixteen-lane workgroups) is
+    swept with 4 lanes per row when its scales are symmetric; each matrix
+    alone with 16.  Every element sees the same operations in the same order
+    either way, so codes and weights agree bit for bit (the per-row losses
+    are summed in another order).  Zero points keep the 16-lane sweep."""
+    say(f"gptq 4-lane batched sweep vs single 16-lane sweeps, cols={cols} {kw}")
+    B, rows = 8, 4096
+    qa = QuantizationArgs(type="int", **kw)
+    Ws = [workloads.gptq_weight(rows, cols, seed=60 + b) for b in range(B)]
+    Hs = [torch.triu(_spd_from_tokens(cols, 1024, seed=70 + b)) for b in range(B)]
+    W = torch.stack(Ws).to(dev)
+    H = torch.stack(Hs).to(dev)
+    res = gptq.gptq_quantize_batched(W, qa, H.clone(), num_samples=1.0)
+    for b in range(B):
+        obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+        obs(W[b])
+        single = gptq.gptq_quantize(W[b], qa, H[b].clone(), obs, num_samples=1.0)
+        assert torch.equal(res[b].codes, single.codes), b
+        assert torch.equal(res[b].weight, single.weight), b
+        assert abs(res[b].loss - single.loss) <= 1e-5 * abs(single.loss) + 1e-12
+
+
 def test_gptq_prepared_hessian_shared(dev):
     """Modules with the same input (q/k/v, gate/up) may share the Cholesky
     chain: a prepared Hessian gives exactly the results of separate solves."""
