@@ -24,7 +24,14 @@ struct SweepState {
 
 // bf16 round-to-nearest-even of a finite fp32 value (the gfx950 conversion
 // instruction: two operations on the sweep's serial chain instead of four).
-__device__ __forceinline__ float bf16_rne(float f) { return (float)(__bf16)f; }
+// (as a pair (0, f): the conversion leaves bf16(f) in the high half, which is
+// its fp32 value, without a separate shift)
+__device__ __forceinline__ float bf16_rne(float f) {
+  typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+  const f32x2v_t pair = {0.f, f};
+  return __builtin_bit_cast(float, __builtin_convertvector(pair, bf16x2v_t));
+}
 
 // Value types of the sweep: integers, or the float grids of compressed-
 // tensors' round_to_quantized_type (float8_e4m3fn, fp4 e2m1).
@@ -41,7 +48,7 @@ __device__ __forceinline__ void quant1(float x, float s, float rs, float z, floa
                                        float& deq) {
   qq = div_by_recip(x, s, rs);
   if (ZP) qq = qq + z;
-  qq = fminf(fmaxf(qq, qmin), qmax);
+  qq = __builtin_amdgcn_fmed3f(qq, qmin, qmax);  // clamp (qmin <= qmax) in one operation
   if (QK == QK_INT) qq = rintf(qq);
   if (QK == QK_FP8) qq = fp8e4m3_rne(qq);
   if (QK == QK_FP4) qq = fp4e2m1_round(qq);
@@ -66,13 +73,16 @@ __device__ __forceinline__ int8_t code_of(float qq) {
 // step's scheduling region: the other updates then interleave with the next
 // step's chain, and the reads issued with them (two steps ahead) cannot sink
 // into the step that uses them.
+// x: the lane's value of slot TO as the previous step's update left it (the
+// owner's, column I, is S.w[TO]; the other lanes' values are not used), and
+// on return the same for column I + 1, so the owner select stays off the
+// serial chain.
 template <int TO, int GO, bool FULL, bool BF16, bool ZP, int QK>
-__device__ __forceinline__ void sweep_step(SweepState& S, const StepH& p, int g, int count, float qmin,
+__device__ __forceinline__ void sweep_step(SweepState& S, const StepH& p, float& x, int g, int count, float qmin,
                                            float qmax) {
   constexpr int I = SW_G * TO + GO;
   if (!FULL && I >= count) return;
   constexpr int TN = GO == SW_G - 1 ? TO + 1 : TO;  // slot of column I + 1
-  const float x = S.w[TO];
   float qq, deq;
   quant1<BF16, ZP, QK>(x, S.s[TO], S.rs[TO], S.z[TO], qmin, qmax, qq, deq);
   const float err = div_by_recip(x - deq, p.dd, p.rd);
@@ -86,8 +96,9 @@ __device__ __forceinline__ void sweep_step(SweepState& S, const StepH& p, int g,
       S.w[t] = upd;
     else
       S.w[t] = col < count ? upd : S.w[t];
+    return upd;
   };
-  if (TN < SW_T) update(TN);
+  if (TN < SW_T) x = update(TN);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = TO; t < SW_T; ++t)
@@ -98,17 +109,17 @@ __device__ __forceinline__ void sweep_step(SweepState& S, const StepH& p, int g,
 template <int I, bool FULL, bool BF16, bool ZP, int QK>
 struct SweepSteps {
   static __device__ __forceinline__ void run(SweepState& S, const float* h1, const float* rdg, int g, int count,
-                                             float qmin, float qmax, const StepH& cur, const StepH& nxt) {
+                                             float qmin, float qmax, const StepH& cur, const StepH& nxt, float x) {
     StepH nn;
     load_step<I + 2>(nn, h1, rdg, g);
-    sweep_step<I / SW_G, I % SW_G, FULL, BF16, ZP, QK>(S, cur, g, count, qmin, qmax);
-    SweepSteps<I + 1, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax, nxt, nn);
+    sweep_step<I / SW_G, I % SW_G, FULL, BF16, ZP, QK>(S, cur, x, g, count, qmin, qmax);
+    SweepSteps<I + 1, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax, nxt, nn, x);
   }
 };
 template <bool FULL, bool BF16, bool ZP, int QK>
 struct SweepSteps<MAXB, FULL, BF16, ZP, QK> {
   static __device__ __forceinline__ void run(SweepState&, const float*, const float*, int, int, float, float,
-                                             const StepH&, const StepH&) {}
+                                             const StepH&, const StepH&, float) {}
 };
 
 // The K = 128 lazy updates of a block's columns from the npre earlier
@@ -255,7 +266,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sweep_block_kernel(
   StepH p0, p1;
   load_step<0>(p0, h1, rdg, g);
   load_step<1>(p1, h1, rdg, g);
-  SweepSteps<0, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax, p0, p1);
+  SweepSteps<0, FULL, BF16, ZP, QK>::run(S, h1, rdg, g, count, qmin, qmax, p0, p1, S.w[0]);
 
   // each slot is final: its code, dequantised value, error and loss
   float loss = 0.f;
@@ -325,9 +336,9 @@ __device__ __forceinline__ float quad_bcast(float v) {
 }
 
 template <int TO, int GO, bool BF16>
-__device__ __forceinline__ void sweep4_step(Sweep4State& S, const StepH4& p, int g, float qmin, float qmax) {
-  constexpr int TN = GO == W4_G - 1 ? TO + 1 : TO;  // slot of column I + 1
-  const float x = S.w[TO];
+__device__ __forceinline__ void sweep4_step(Sweep4State& S, const StepH4& p, float& x, int g, float qmin,
+                                            float qmax) {
+  constexpr int TN = GO == W4_G - 1 ? TO + 1 : TO;  // slot of column I + 1 (x: as in sweep_step)
   float qq, deq;
   quant1<BF16, false, QK_INT>(x, S.s[TO], S.rs[TO], 0.f, qmin, qmax, qq, deq);
   const float err = div_by_recip(x - deq, p.dd, p.rd);
@@ -335,8 +346,9 @@ __device__ __forceinline__ void sweep4_step(Sweep4State& S, const StepH4& p, int
   auto update = [&](int t) __attribute__((always_inline)) {
     const float upd = S.w[t] - e * p.h[t];
     S.w[t] = t == TO ? (g > GO ? upd : S.w[t]) : upd;
+    return upd;
   };
-  if (TN < W4_T) update(TN);
+  if (TN < W4_T) x = update(TN);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = TO; t < W4_T; ++t)
@@ -348,17 +360,17 @@ __device__ __forceinline__ void sweep4_step(Sweep4State& S, const StepH4& p, int
 template <int I, bool BF16>
 struct Sweep4Steps {
   static __device__ __forceinline__ void run(Sweep4State& S, const float* h1, const float* rdg, int g, float qmin,
-                                             float qmax, const StepH4& cur) {
+                                             float qmax, const StepH4& cur, float x) {
     StepH4 nn;
     load_step4<I + 1>(nn, h1, rdg, g);
-    sweep4_step<I / W4_G, I % W4_G, BF16>(S, cur, g, qmin, qmax);
-    Sweep4Steps<I + 1, BF16>::run(S, h1, rdg, g, qmin, qmax, nn);
+    sweep4_step<I / W4_G, I % W4_G, BF16>(S, cur, x, g, qmin, qmax);
+    Sweep4Steps<I + 1, BF16>::run(S, h1, rdg, g, qmin, qmax, nn, x);
   }
 };
 template <bool BF16>
 struct Sweep4Steps<MAXB, BF16> {
   static __device__ __forceinline__ void run(Sweep4State&, const float*, const float*, int, float, float,
-                                             const StepH4&) {}
+                                             const StepH4&, float) {}
 };
 
 // Whole MAXB-column blocks of integer values with symmetric scales;
@@ -413,7 +425,7 @@ __global__ __launch_bounds__(SW_NT, 3) void sweep4_block_kernel(
 
   StepH4 p0;
   load_step4<0>(p0, h1, rdg, g);
-  Sweep4Steps<0, BF16>::run(S, h1, rdg, g, qmin, qmax, p0);
+  Sweep4Steps<0, BF16>::run(S, h1, rdg, g, qmin, qmax, p0, S.w[0]);
 
   float loss = 0.f;
 #pragma unroll
