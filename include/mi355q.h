@@ -188,7 +188,8 @@ int mi355q_gptq_load_weight_batched(const void* w_dev, mi355q_dtype w_dtype, int
  *   after each block: w[:, block_end:] -= Err_block @ hinv[block, block_end:]
  * On return w_work holds the dequantised values, codes_dev[r][j] the integer
  * codes q (int8, working column order) and losses_dev[r] the per-row loss
- * (fp32, accumulated onto its input).  Integer types only (num_bits <= 8).
+ * (fp32, accumulated onto its input).  Integer types only (num_bits <= 8);
+ * mi355q_gptq_sweep_typed_batched takes the fp8 / fp4 grids.
  * zp_dev may be NULL: zero points 0 (symmetric), a faster kernel variant.
  */
 size_t mi355q_gptq_sweep_workspace_size(int64_t rows, int64_t cols, int64_t blocksize);
