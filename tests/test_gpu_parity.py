@@ -561,10 +561,20 @@ def test_gptq_wide_sweep_equals_single(dev, cols, kw):
     either way, so codes and weights agree bit for bit (the per-row losses
     are summed in another order).  Zero points keep the 16-lane sweep."""
     say(f"gptq 4-lane batched sweep vs single 16-lane sweeps, cols={cols} {kw}")
-    B, rows = 8, 4096
+    _wide_vs_single(dev, 8, 4096, cols, kw, seed=60)
+
+
+def test_gptq_wide_sweep_ragged_rows(dev):
+    """Forty 1000-row matrices (2520 sixteen-lane workgroups): the 4-lane
+    sweep's last workgroup of each matrix holds 40 live rows of 64."""
+    say("gptq 4-lane batched sweep, 40 x 1000 rows")
+    _wide_vs_single(dev, 40, 1000, 128, dict(num_bits=4, strategy="group", group_size=128), seed=90)
+
+
+def _wide_vs_single(dev, B, rows, cols, kw, seed):
     qa = QuantizationArgs(type="int", **kw)
-    Ws = [workloads.gptq_weight(rows, cols, seed=60 + b) for b in range(B)]
-    Hs = [torch.triu(_spd_from_tokens(cols, 1024, seed=70 + b)) for b in range(B)]
+    Ws = [workloads.gptq_weight(rows, cols, seed=seed + b) for b in range(B)]
+    Hs = [torch.triu(_spd_from_tokens(cols, 1024, seed=seed + 100 + b)) for b in range(B)]
     W = torch.stack(Ws).to(dev)
     H = torch.stack(Hs).to(dev)
     res = gptq.gptq_quantize_batched(W, qa, H.clone(), num_samples=1.0)
