@@ -345,11 +345,14 @@ int mi355q_nvfp4_qparams(const float* min_dev, const float* max_dev, int64_t n, 
  * exponent rounded to bf16, as torch's pow does); each cell keeps its
  * first best candidate over the steps before the first run of `patience`
  * steps without an improvement in any cell.  Writes the chosen min / max
- * (float values of the observed dtype) to min_out / max_out.  Integer types. */
+ * (float values of the observed dtype) to min_out / max_out.  qtype
+ * MI355Q_QTYPE_INT: the integer grid (rint); MI355Q_QTYPE_FP8_E4M3: the fp8
+ * e4m3 grid (symmetric, qmin = -qmax <= 448; round to nearest even after the
+ * clamp, as the cast to float8_e4m3fn in CT round_to_quantized_type does). */
 size_t mi355q_observe_mse_workspace_size(int64_t rows, int64_t cols, int64_t cell_rows, int64_t cell_cols,
                                          int total_steps);
 int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
-                       int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric,
+                       int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric, int qtype,
                        int total_steps, int patience, double grid, float norm, const float* min_dev,
                        const float* max_dev, float* min_out_dev, float* max_out_dev, void* workspace_dev,
                        size_t workspace_bytes, void* stream);
@@ -361,7 +364,7 @@ int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int6
  * NULL: uniform), and no early stop when patience is 0. */
 int mi355q_observe_imatrix_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
                                int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric,
-                               int total_steps, int patience, double grid, float norm,
+                               int qtype, int total_steps, int patience, double grid, float norm,
                                const float* importance_dev, const float* min_dev, const float* max_dev,
                                float* min_out_dev, float* max_out_dev, void* workspace_dev,
                                size_t workspace_bytes, void* stream);

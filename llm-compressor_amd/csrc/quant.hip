@@ -264,7 +264,9 @@ __device__ __forceinline__ float shrink_p(int i, double grid) { return (float)(1
 // and the power from the LDS table.
 // IM (imatrix observer): |fq(x) - x| and its power in fp32 (fq in the
 // observed dtype), times the column's importance w.
-template <bool B, bool ZP, bool IM>
+// FQ: the fp8 e4m3 grid (round to nearest even after the clamp, as the
+// cast to float8_e4m3fn does) instead of the integer one.
+template <bool B, bool ZP, bool IM, bool FQ = false>
 __device__ __forceinline__ float mse_term(float v, float s, float rs, float z, float qmin, float qmax, float norm,
                                           const uint16_t* tab, float w) {
   float t;
@@ -275,7 +277,8 @@ __device__ __forceinline__ float mse_term(float v, float s, float rs, float z, f
     t = v / s;
   }
   if (ZP) t = rb<B>(t + z);
-  t = rintf(fminf(fmaxf(t, qmin), qmax));
+  t = fminf(fmaxf(t, qmin), qmax);
+  t = FQ ? fp8e4m3_rne(t) : rintf(t);
   if (ZP) t = rb<B>(t - z);
   if (IM) return pow_norm<false>(fabsf(rb<B>(t * s) - v), norm) * w;
   const float d = fabsf(rb<B>(rb<B>(t * s) - v));
@@ -303,7 +306,7 @@ __device__ __forceinline__ void load_pow_table(uint16_t* tab, const uint16_t* ta
 
 // Cells of at most 8 * LG <= 512 values: LG lanes per cell, 8 values per
 // lane; workgroups loop over the cells (the table is loaded once each).
-template <bool B, bool ZP, bool IM>
+template <bool B, bool ZP, bool IM, bool FQ = false>
 __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log2, const uint16_t* table,
                                                            float* err) {
   constexpr bool TAB = B && !IM;
@@ -337,7 +340,7 @@ __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (ok[k]) acc += mse_term<B, ZP, IM>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab, w[k]);
+        if (ok[k]) acc += mse_term<B, ZP, IM, FQ>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab, w[k]);
       for (int o = 1; o < LG; o <<= 1) acc += __shfl_xor(acc, o, LG);
       if (live && l == 0) err[cell * a.T + i] = IM ? acc : rb<B>(acc);
     }
@@ -347,7 +350,7 @@ __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log
 // Larger cells: chunks of 16 * NT values, one fp32 partial sum per chunk and
 // candidate (summed in chunk order by mse_flags_kernel); workgroups loop over
 // the (cell, chunk) items.
-template <bool B, bool ZP, bool IM>
+template <bool B, bool ZP, bool IM, bool FQ = false>
 __global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nchunk, const uint16_t* table,
                                                            float* part) {
   constexpr bool TAB = B && !IM;
@@ -379,7 +382,7 @@ __global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nc
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < 16; ++k)
-        if (ok[k]) acc += mse_term<B, ZP, IM>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab, w[k]);
+        if (ok[k]) acc += mse_term<B, ZP, IM, FQ>(v[k], s, rs, z, a.qmin, a.qmax, a.norm, tab, w[k]);
       for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
       if ((tid & 63) == 0) red[tid >> 6] = acc;
       __syncthreads();
@@ -1017,7 +1020,8 @@ namespace {
 // Both MSE observers: im = the imatrix observer's mode (fp32 error sums,
 // weighted by imp when given, patience 0 = no early stop).
 int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
-                     int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric, int total_steps,
+                     int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric, int qtype,
+                     int total_steps,
                      int patience, double grid, float norm, bool im, const float* imp, const float* min_dev,
                      const float* max_dev, float* min_out_dev, float* max_out_dev, void* workspace_dev,
                      size_t workspace_bytes, void* stream) {
@@ -1026,6 +1030,10 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
   MQ_CHECK_ARG(cell_rows > 0 && cell_cols > 0, "observe_mse: bad cell shape");
   MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F32, "observe_mse: dtype must be bf16 or fp32");
   MQ_CHECK_ARG(qmin < 0.f && qmax > 0.f, "observe_mse: range must straddle zero");
+  MQ_CHECK_ARG(qtype == MI355Q_QTYPE_INT ||
+                   (qtype == MI355Q_QTYPE_FP8_E4M3 && symmetric && qmin == -qmax && qmax <= 448.f),
+               "observe_mse: value type must be integer, or fp8 e4m3 symmetric within +-448");
+  const bool fq = qtype == MI355Q_QTYPE_FP8_E4M3;
   MQ_CHECK_ARG(total_steps >= 0 && grid != 0.0, "observe_mse: bad search grid");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t ncells = ((rows + cell_rows - 1) / cell_rows) * ((cols + cell_cols - 1) / cell_cols);
@@ -1054,9 +1062,12 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
   }
   constexpr int64_t kMaxWg = 1024;  // persistent workgroups (each loads the power table once)
   // kernel variant for (bf16, zero points, imatrix mode)
+  // (the fp8 grid: symmetric only; f00 .. f11 are its (bf16, imatrix) variants)
   auto pick = [&](auto k000, auto k001, auto k010, auto k011, auto k100, auto k101, auto k110, auto k111,
-                  auto&& go) {
-    if (b) {
+                  auto f00, auto f01, auto f10, auto f11, auto&& go) {
+    if (fq) {
+      if (b) im ? go(f11) : go(f10); else im ? go(f01) : go(f00);
+    } else if (b) {
       if (zp) im ? go(k111) : go(k110); else im ? go(k101) : go(k100);
     } else {
       if (zp) im ? go(k011) : go(k010); else im ? go(k001) : go(k000);
@@ -1069,6 +1080,8 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
          mse_err_small_kernel<false, true, false>, mse_err_small_kernel<false, true, true>,
          mse_err_small_kernel<true, false, false>, mse_err_small_kernel<true, false, true>,
          mse_err_small_kernel<true, true, false>, mse_err_small_kernel<true, true, true>,
+         mse_err_small_kernel<false, false, false, true>, mse_err_small_kernel<false, false, true, true>,
+         mse_err_small_kernel<true, false, false, true>, mse_err_small_kernel<true, false, true, true>,
          [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.lg_log2, tab, err); });
   } else {
     const dim3 g((unsigned)min(ncells * pl.nchunk, kMaxWg));
@@ -1076,6 +1089,8 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
          mse_err_large_kernel<false, true, false>, mse_err_large_kernel<false, true, true>,
          mse_err_large_kernel<true, false, false>, mse_err_large_kernel<true, false, true>,
          mse_err_large_kernel<true, true, false>, mse_err_large_kernel<true, true, true>,
+         mse_err_large_kernel<false, false, false, true>, mse_err_large_kernel<false, false, true, true>,
+         mse_err_large_kernel<true, false, false, true>, mse_err_large_kernel<true, false, true, true>,
          [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.nchunk, tab, part); });
   }
   MQ_LAUNCH_CHECK();
@@ -1122,22 +1137,23 @@ __global__ void column_sumsq_add_kernel(const float* part, int64_t nchunk, int64
 
 extern "C" int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,
                                   int64_t cell_rows, int64_t cell_cols, float qmin, float qmax, int symmetric,
-                                  int total_steps, int patience, double grid, float norm, const float* min_dev,
+                                  int qtype, int total_steps, int patience, double grid, float norm, const float* min_dev,
                                   const float* max_dev, float* min_out_dev, float* max_out_dev,
                                   void* workspace_dev, size_t workspace_bytes, void* stream) {
-  return observe_mse_impl(x_dev, dtype, rows, cols, ldx, cell_rows, cell_cols, qmin, qmax, symmetric, total_steps,
-                          patience, grid, norm, false, nullptr, min_dev, max_dev, min_out_dev, max_out_dev,
+  return observe_mse_impl(x_dev, dtype, rows, cols, ldx, cell_rows, cell_cols, qmin, qmax, symmetric, qtype,
+                          total_steps, patience, grid, norm, false, nullptr, min_dev, max_dev, min_out_dev, max_out_dev,
                           workspace_dev, workspace_bytes, stream);
 }
 
 extern "C" int mi355q_observe_imatrix_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols,
                                           int64_t ldx, int64_t cell_rows, int64_t cell_cols, float qmin, float qmax,
-                                          int symmetric, int total_steps, int patience, double grid, float norm,
+                                          int symmetric, int qtype, int total_steps, int patience, double grid,
+                                          float norm,
                                           const float* importance_dev, const float* min_dev, const float* max_dev,
                                           float* min_out_dev, float* max_out_dev, void* workspace_dev,
                                           size_t workspace_bytes, void* stream) {
-  return observe_mse_impl(x_dev, dtype, rows, cols, ldx, cell_rows, cell_cols, qmin, qmax, symmetric, total_steps,
-                          patience, grid, norm, true, importance_dev, min_dev, max_dev, min_out_dev, max_out_dev,
+  return observe_mse_impl(x_dev, dtype, rows, cols, ldx, cell_rows, cell_cols, qmin, qmax, symmetric, qtype,
+                          total_steps, patience, grid, norm, true, importance_dev, min_dev, max_dev, min_out_dev, max_out_dev,
                           workspace_dev, workspace_bytes, stream);
 }
 

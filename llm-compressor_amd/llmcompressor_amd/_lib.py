@@ -61,10 +61,10 @@ SIGNATURES = {
     "mi355q_observe_minmax": (_i32, [_vp, _i32, _i64, _i64, _i64, _i32, _i64, _i32, _i32, _vp, _vp, _vp]),
     "mi355q_calculate_qparams": (_i32, [_vp, _vp, _i64, _f32, _f32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "mi355q_observe_mse_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
-    "mi355q_observe_mse": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _i32, _i32, _f64,
-                                  _f32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mi355q_observe_mse": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _i32, _i32, _i32,
+                                  _f64, _f32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mi355q_observe_imatrix_mse": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _i32, _i32,
-                                          _f64, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+                                          _i32, _f64, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mi355q_column_sumsq_workspace_size": (_sz, [_i64, _i64]),
     "mi355q_column_sumsq": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "mi355q_mx_scales": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp]),

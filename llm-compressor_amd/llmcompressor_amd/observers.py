@@ -222,15 +222,27 @@ class _MSEObserver(Observer):
             return x2, x2.shape[0], a.group_size
         raise ValueError(f"{s.value} quantization cannot be observed for activations here")
 
+    def _grid(self) -> str:
+        """The value grid of the search: integers, or fp8 e4m3 (symmetric;
+        the candidates' scales as calculate_qparams gives them without a
+        global scale, mse_quant.py:255-262)."""
+        a = self.args
+        if a.type == QuantizationType.INT and not a.is_mx:
+            return "int"
+        if a.type == QuantizationType.FLOAT and a.num_bits == 8 and not a.is_mx and a.symmetric \
+                and a.strategy != QuantizationStrategy.TENSOR_GROUP:
+            return "fp8"
+        raise NotImplementedError("MSE observers for fp4 (MXFP4, NVFP4) and asymmetric float types are not "
+                                  "provided by this build")
+
     def _min_max(self, observed: torch.Tensor):
         a = self.args
-        if a.type != QuantizationType.INT or a.is_mx:
-            raise NotImplementedError("MSE observers for float types are not provided by this build")
+        qtype = self._grid()
         mn, mx = super()._min_max(observed)
         x2, ch, cw = self._cells(observed)
         qmin, qmax = a.q_range()
         mn2, mx2 = ops.observe_mse(x2, ch, cw, mn.reshape(-1), mx.reshape(-1), qmin, qmax, a.symmetric,
-                                   int(self.maxshrink * self.grid), self.patience, self.grid, self.norm)
+                                   int(self.maxshrink * self.grid), self.patience, self.grid, self.norm, qtype=qtype)
         return mn2.reshape(mn.shape), mx2.reshape(mx.shape)
 
 
@@ -368,15 +380,14 @@ class IMatrixMSEObserver(_MSEObserver):
 
     def _min_max(self, observed: torch.Tensor):
         a = self.args
-        if a.type != QuantizationType.INT or a.is_mx:
-            raise NotImplementedError("MSE observers for float types are not provided by this build")
+        qtype = self._grid()
         imp = self._importance(observed)
         mn, mx = Observer._min_max(self, observed)
         x2, ch, cw = self._cells(observed)
         qmin, qmax = a.q_range()
         steps = max(1, int(self.maxshrink * self.grid)) + 1
         mn2, mx2 = ops.observe_mse(x2, ch, cw, mn.reshape(-1), mx.reshape(-1), qmin, qmax, a.symmetric, steps,
-                                   self.patience, self.grid, self.norm, importance=imp, imatrix=True)
+                                   self.patience, self.grid, self.norm, importance=imp, imatrix=True, qtype=qtype)
         return mn2.reshape(mn.shape), mx2.reshape(mx.shape)
 
     def update_statistics_from_observed(self, mn, mx):

@@ -431,11 +431,12 @@ def pack_int4_int32(codes: torch.Tensor) -> torch.Tensor:
 
 def observe_mse(x: torch.Tensor, cell_rows: int, cell_cols: int, mn: torch.Tensor, mx: torch.Tensor, qmin: float,
                 qmax: float, symmetric: bool, total_steps: int, patience: int, grid: float, norm: float,
-                importance: torch.Tensor | None = None, imatrix: bool = False):
+                importance: torch.Tensor | None = None, imatrix: bool = False, qtype: str = "int"):
     """MSE grid search over the cells of x (``mi355q_observe_mse``, or with
     ``imatrix`` ``mi355q_observe_imatrix_mse`` weighted by ``importance``
-    [cols]): returns the chosen (min, max) per cell as fp32 tensors shaped
-    like ``mn``."""
+    [cols]) on the integer grid or, with ``qtype="fp8"``, the fp8 e4m3 grid:
+    returns the chosen (min, max) per cell as fp32 tensors shaped like
+    ``mn``."""
     L.require_gpu(x, mn, mx, importance)
     if x.dim() != 2 or x.stride(1) != 1:
         x = x.reshape(-1, x.shape[-1]).contiguous()
@@ -445,7 +446,7 @@ def observe_mse(x: torch.Tensor, cell_rows: int, cell_cols: int, mn: torch.Tenso
     lib = L.lib()
     ws = _ws(lib.mi355q_observe_mse_workspace_size(rows, cols, cell_rows, cell_cols, total_steps), x.device)
     common = (x.data_ptr(), _dt(x), rows, cols, x.stride(0), cell_rows, cell_cols, C.c_float(qmin), C.c_float(qmax),
-              1 if symmetric else 0, int(total_steps), int(patience), C.c_double(grid), C.c_float(norm))
+              1 if symmetric else 0, QTYPE[qtype], int(total_steps), int(patience), C.c_double(grid), C.c_float(norm))
     tail = (mn32.data_ptr(), mx32.data_ptr(), out_mn.data_ptr(), out_mx.data_ptr(), L.ptr(ws),
             0 if ws is None else ws.numel(), L.stream_of(x))
     if imatrix:

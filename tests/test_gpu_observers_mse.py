@@ -76,6 +76,66 @@ def test_mse_observer_matches_oracle(dev, case, dtype):
     assert l_gpu == l_ora
 
 
+FP8_CASES = [dict(strategy="channel"), dict(strategy="tensor"), dict(strategy="group", group_size=128),
+             dict(strategy="block", block_structure=[64, 128])]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("case", FP8_CASES, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+def test_mse_observer_fp8_matches_oracle(dev, case, dtype):
+    """The search on the fp8 e4m3 grid (mse_quant.py:255-262 with float
+    args: scale max|x| / 448, fake-quantised through float8_e4m3fn): the
+    chosen min / max equal the oracle's in every cell."""
+    g = torch.Generator().manual_seed(17)
+    w = torch.randn(192, 1024, generator=g) * torch.exp(torch.randn(192, 1, generator=g))
+    w[torch.rand(192, 1024, generator=g) < 0.002] *= 40       # outliers: shrinking pays
+    w = w.to(dtype)
+    say(f"mse observer fp8 {case} {dtype}")
+    kw = dict(num_bits=8, type="float", symmetric=True, **case)
+    obs = Observer.load_from_registry("memoryless_mse", base_name="weight",
+                                      args=QuantizationArgs(observer="memoryless_mse", **kw))
+    obs(w.to(dev))
+    mn, mx = obs.min_vals.cpu(), obs.max_vals.cpu()
+    qp = obs.get_qparams()
+    a = OArgs(observer="mse", **kw)
+    omn, omx, steps = oobs.mse_grid_search(oobs.flatten_weight(w, a), a, return_steps=True)
+    agree = ((mn == omn.reshape(mn.shape)) & (mx == omx.reshape(mx.shape))).float().mean().item()
+    shrunk = ((omx.abs() < oobs.flatten_weight(w, a).abs().amax(dim=(0, -1))).float().mean().item())
+    s_o, z_o = oobs.calculate_qparams(omn, omx, a)
+    assert torch.equal(qp["scale"].cpu().reshape(s_o.shape).float(), s_o.float())
+    say(f"  agreement {agree:.5f} over {steps} steps, {shrunk:.3f} of the cells shrunk")
+    assert agree == 1.0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_imatrix_fp8_matches_oracle(dev, dtype):
+    say(f"imatrix fp8 channel {dtype}")
+    g = torch.Generator().manual_seed(6)
+    w = (torch.randn(192, 1024, generator=g) * 0.02).to(dtype)
+    s2 = torch.exp(2 * torch.randn(1024, generator=g))
+    args = QuantizationArgs(num_bits=8, type="float", symmetric=True, strategy="channel", observer="imatrix_mse")
+    obs = Observer.load_from_registry("imatrix_mse", base_name="weight", args=args)
+    obs._imatrix_sum, obs._imatrix_count = s2.clone().to(dev), torch.tensor(3, dtype=torch.int64)
+    obs(w.to(dev))
+    mn, mx = obs.min_vals.cpu(), obs.max_vals.cpu()
+    a = OArgs(num_bits=8, type="float", symmetric=True, strategy="channel", observer="imatrix_mse")
+    flat = oobs.flatten_weight(w, a)
+    imp = oobs.imatrix_importance(s2, 3, flat, a)
+    omn, omx = oobs.imatrix_grid_search(flat, a, importance=imp)
+    agree = ((mn == omn.reshape(mn.shape)) & (mx == omx.reshape(mx.shape))).float().mean().item()
+    say(f"  agreement {agree:.5f}")
+    assert agree == 1.0
+
+
+def test_mse_observer_fp4_still_refused(dev):
+    """fp4 grids (MXFP4 / NVFP4) are not searched: the observer raises."""
+    args = QuantizationArgs(num_bits=4, type="float", symmetric=True, strategy="tensor_group", group_size=16,
+                            observer="memoryless_mse")
+    obs = Observer.load_from_registry("memoryless_mse", base_name="weight", args=args)
+    with pytest.raises(NotImplementedError):
+        obs(torch.randn(32, 64, device=dev))
+
+
 @pytest.mark.parametrize("strategy", ["tensor", "group"])
 def test_mse_activation_moving_average(dev, strategy):
     say(f"mse activations {strategy}")
