@@ -348,7 +348,10 @@ int mi355q_nvfp4_qparams(const float* min_dev, const float* max_dev, int64_t n, 
  * (float values of the observed dtype) to min_out / max_out.  qtype
  * MI355Q_QTYPE_INT: the integer grid (rint); MI355Q_QTYPE_FP8_E4M3: the fp8
  * e4m3 grid (symmetric, qmin = -qmax <= 448; round to nearest even after the
- * clamp, as the cast to float8_e4m3fn in CT round_to_quantized_type does). */
+ * clamp, as the cast to float8_e4m3fn in CT round_to_quantized_type does);
+ * MI355Q_QTYPE_FP4_E2M1: the e2m1 grid (symmetric, qmin = -qmax <= 6; CT
+ * cast_to_fp4).  The candidates' scales are calculate_qparams' without a
+ * global scale (observers/mse_quant.py:255-262). */
 size_t mi355q_observe_mse_workspace_size(int64_t rows, int64_t cols, int64_t cell_rows, int64_t cell_cols,
                                          int total_steps);
 int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,

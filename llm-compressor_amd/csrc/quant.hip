@@ -264,9 +264,10 @@ __device__ __forceinline__ float shrink_p(int i, double grid) { return (float)(1
 // and the power from the LDS table.
 // IM (imatrix observer): |fq(x) - x| and its power in fp32 (fq in the
 // observed dtype), times the column's importance w.
-// FQ: the fp8 e4m3 grid (round to nearest even after the clamp, as the
-// cast to float8_e4m3fn does) instead of the integer one.
-template <bool B, bool ZP, bool IM, bool FQ = false>
+// FQ: the value grid after the clamp: 0 integers (rint), 1 fp8 e4m3 (round
+// to nearest even, as the cast to float8_e4m3fn does), 2 fp4 e2m1 (CT
+// cast_to_fp4's nearest value, ties to even).
+template <bool B, bool ZP, bool IM, int FQ = 0>
 __device__ __forceinline__ float mse_term(float v, float s, float rs, float z, float qmin, float qmax, float norm,
                                           const uint16_t* tab, float w) {
   float t;
@@ -278,7 +279,7 @@ __device__ __forceinline__ float mse_term(float v, float s, float rs, float z, f
   }
   if (ZP) t = rb<B>(t + z);
   t = fminf(fmaxf(t, qmin), qmax);
-  t = FQ ? fp8e4m3_rne(t) : rintf(t);
+  t = FQ == 1 ? fp8e4m3_rne(t) : FQ == 2 ? fp4e2m1_round(t) : rintf(t);
   if (ZP) t = rb<B>(t - z);
   if (IM) return pow_norm<false>(fabsf(rb<B>(t * s) - v), norm) * w;
   const float d = fabsf(rb<B>(rb<B>(t * s) - v));
@@ -306,7 +307,7 @@ __device__ __forceinline__ void load_pow_table(uint16_t* tab, const uint16_t* ta
 
 // Cells of at most 8 * LG <= 512 values: LG lanes per cell, 8 values per
 // lane; workgroups loop over the cells (the table is loaded once each).
-template <bool B, bool ZP, bool IM, bool FQ = false>
+template <bool B, bool ZP, bool IM, int FQ = 0>
 __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log2, const uint16_t* table,
                                                            float* err) {
   constexpr bool TAB = B && !IM;
@@ -350,7 +351,7 @@ __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log
 // Larger cells: chunks of 16 * NT values, one fp32 partial sum per chunk and
 // candidate (summed in chunk order by mse_flags_kernel); workgroups loop over
 // the (cell, chunk) items.
-template <bool B, bool ZP, bool IM, bool FQ = false>
+template <bool B, bool ZP, bool IM, int FQ = 0>
 __global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nchunk, const uint16_t* table,
                                                            float* part) {
   constexpr bool TAB = B && !IM;
@@ -1031,9 +1032,10 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
   MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F32, "observe_mse: dtype must be bf16 or fp32");
   MQ_CHECK_ARG(qmin < 0.f && qmax > 0.f, "observe_mse: range must straddle zero");
   MQ_CHECK_ARG(qtype == MI355Q_QTYPE_INT ||
-                   (qtype == MI355Q_QTYPE_FP8_E4M3 && symmetric && qmin == -qmax && qmax <= 448.f),
-               "observe_mse: value type must be integer, or fp8 e4m3 symmetric within +-448");
-  const bool fq = qtype == MI355Q_QTYPE_FP8_E4M3;
+                   (qtype == MI355Q_QTYPE_FP8_E4M3 && symmetric && qmin == -qmax && qmax <= 448.f) ||
+                   (qtype == MI355Q_QTYPE_FP4_E2M1 && symmetric && qmin == -qmax && qmax <= 6.f),
+               "observe_mse: value type must be integer, or fp8 e4m3 / fp4 e2m1 symmetric within their range");
+  const int fq = qtype == MI355Q_QTYPE_FP8_E4M3 ? 1 : qtype == MI355Q_QTYPE_FP4_E2M1 ? 2 : 0;
   MQ_CHECK_ARG(total_steps >= 0 && grid != 0.0, "observe_mse: bad search grid");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t ncells = ((rows + cell_rows - 1) / cell_rows) * ((cols + cell_cols - 1) / cell_cols);
@@ -1062,11 +1064,14 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
   }
   constexpr int64_t kMaxWg = 1024;  // persistent workgroups (each loads the power table once)
   // kernel variant for (bf16, zero points, imatrix mode)
-  // (the fp8 grid: symmetric only; f00 .. f11 are its (bf16, imatrix) variants)
+  // (the float grids: symmetric only; f00 .. f11 (fp8) and h00 .. h11 (fp4)
+  // are their (bf16, imatrix) variants)
   auto pick = [&](auto k000, auto k001, auto k010, auto k011, auto k100, auto k101, auto k110, auto k111,
-                  auto f00, auto f01, auto f10, auto f11, auto&& go) {
-    if (fq) {
+                  auto f00, auto f01, auto f10, auto f11, auto h00, auto h01, auto h10, auto h11, auto&& go) {
+    if (fq == 1) {
       if (b) im ? go(f11) : go(f10); else im ? go(f01) : go(f00);
+    } else if (fq == 2) {
+      if (b) im ? go(h11) : go(h10); else im ? go(h01) : go(h00);
     } else if (b) {
       if (zp) im ? go(k111) : go(k110); else im ? go(k101) : go(k100);
     } else {
@@ -1080,8 +1085,10 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
          mse_err_small_kernel<false, true, false>, mse_err_small_kernel<false, true, true>,
          mse_err_small_kernel<true, false, false>, mse_err_small_kernel<true, false, true>,
          mse_err_small_kernel<true, true, false>, mse_err_small_kernel<true, true, true>,
-         mse_err_small_kernel<false, false, false, true>, mse_err_small_kernel<false, false, true, true>,
-         mse_err_small_kernel<true, false, false, true>, mse_err_small_kernel<true, false, true, true>,
+         mse_err_small_kernel<false, false, false, 1>, mse_err_small_kernel<false, false, true, 1>,
+         mse_err_small_kernel<true, false, false, 1>, mse_err_small_kernel<true, false, true, 1>,
+         mse_err_small_kernel<false, false, false, 2>, mse_err_small_kernel<false, false, true, 2>,
+         mse_err_small_kernel<true, false, false, 2>, mse_err_small_kernel<true, false, true, 2>,
          [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.lg_log2, tab, err); });
   } else {
     const dim3 g((unsigned)min(ncells * pl.nchunk, kMaxWg));
@@ -1089,8 +1096,10 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
          mse_err_large_kernel<false, true, false>, mse_err_large_kernel<false, true, true>,
          mse_err_large_kernel<true, false, false>, mse_err_large_kernel<true, false, true>,
          mse_err_large_kernel<true, true, false>, mse_err_large_kernel<true, true, true>,
-         mse_err_large_kernel<false, false, false, true>, mse_err_large_kernel<false, false, true, true>,
-         mse_err_large_kernel<true, false, false, true>, mse_err_large_kernel<true, false, true, true>,
+         mse_err_large_kernel<false, false, false, 1>, mse_err_large_kernel<false, false, true, 1>,
+         mse_err_large_kernel<true, false, false, 1>, mse_err_large_kernel<true, false, true, 1>,
+         mse_err_large_kernel<false, false, false, 2>, mse_err_large_kernel<false, false, true, 2>,
+         mse_err_large_kernel<true, false, false, 2>, mse_err_large_kernel<true, false, true, 2>,
          [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.nchunk, tab, part); });
   }
   MQ_LAUNCH_CHECK();

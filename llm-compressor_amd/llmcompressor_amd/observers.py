@@ -209,7 +209,8 @@ class _MSEObserver(Observer):
         if self.is_weight_obs:
             rows, cols = observed.shape
             cell = {QuantizationStrategy.TENSOR: (rows, cols), QuantizationStrategy.CHANNEL: (1, cols),
-                    QuantizationStrategy.GROUP: (1, a.group_size)}.get(s)
+                    QuantizationStrategy.GROUP: (1, a.group_size),
+                    QuantizationStrategy.TENSOR_GROUP: (1, a.group_size)}.get(s)
             if s == QuantizationStrategy.BLOCK:
                 cell = tuple(a.block_structure)
             if cell is None:
@@ -223,17 +224,24 @@ class _MSEObserver(Observer):
         raise ValueError(f"{s.value} quantization cannot be observed for activations here")
 
     def _grid(self) -> str:
-        """The value grid of the search: integers, or fp8 e4m3 (symmetric;
-        the candidates' scales as calculate_qparams gives them without a
-        global scale, mse_quant.py:255-262)."""
+        """The value grid of the search: integers, fp8 e4m3 or fp4 e2m1
+        (symmetric; the candidates' scales as calculate_qparams gives them
+        without a global scale, mse_quant.py:255-262 - for NVFP4 the global
+        scale then comes from the searched statistics, observers/base.py:78-96)."""
         a = self.args
         if a.type == QuantizationType.INT and not a.is_mx:
             return "int"
-        if a.type == QuantizationType.FLOAT and a.num_bits == 8 and not a.is_mx and a.symmetric \
-                and a.strategy != QuantizationStrategy.TENSOR_GROUP:
-            return "fp8"
-        raise NotImplementedError("MSE observers for fp4 (MXFP4, NVFP4) and asymmetric float types are not "
-                                  "provided by this build")
+        if a.type == QuantizationType.FLOAT and not a.is_mx and a.symmetric:
+            if a.num_bits == 8 and a.strategy != QuantizationStrategy.TENSOR_GROUP:
+                return "fp8"
+            # with fp8 scales (the NVFP4 preset) each candidate's scale would
+            # be cast to float8 and the bf16 / fp32 value divided by it, a
+            # promotion torch refuses: the reference's search there is not
+            # pinned, so only searches without a scale dtype are provided
+            if a.num_bits == 4 and a.scale_dtype is None:
+                return "fp4"
+        raise NotImplementedError("MSE observers for MXFP4 (e8m0 candidate scales), fp4 with fp8 scales and "
+                                  "asymmetric float types are not provided by this build")
 
     def _min_max(self, observed: torch.Tensor):
         a = self.args

@@ -127,13 +127,46 @@ def test_imatrix_fp8_matches_oracle(dev, dtype):
     assert agree == 1.0
 
 
-def test_mse_observer_fp4_still_refused(dev):
-    """fp4 grids (MXFP4 / NVFP4) are not searched: the observer raises."""
-    args = QuantizationArgs(num_bits=4, type="float", symmetric=True, strategy="tensor_group", group_size=16,
-                            observer="memoryless_mse")
-    obs = Observer.load_from_registry("memoryless_mse", base_name="weight", args=args)
-    with pytest.raises(NotImplementedError):
-        obs(torch.randn(32, 64, device=dev))
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("case", [dict(strategy="tensor_group", group_size=16), dict(strategy="group", group_size=32)],
+                         ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+def test_mse_observer_fp4_matches_oracle(dev, case, dtype):
+    """The search on the e2m1 grid (scale max|x| / 6 per candidate, CT
+    cast_to_fp4): the chosen min / max equal the oracle's in every group.
+    For tensor groups the global scale and fp8 group scales then come from
+    these statistics (observers/base.py:78-123)."""
+    g = torch.Generator().manual_seed(23)
+    w = (torch.randn(192, 1024, generator=g) * torch.exp(torch.randn(192, 1, generator=g))).to(dtype)
+    say(f"mse observer fp4 {case} {dtype}")
+    kw = dict(num_bits=4, type="float", symmetric=True, **case)
+    obs = Observer.load_from_registry("memoryless_mse", base_name="weight",
+                                      args=QuantizationArgs(observer="memoryless_mse", **kw))
+    obs(w.to(dev))
+    mn, mx = obs.min_vals.cpu(), obs.max_vals.cpu()
+    a = OArgs(observer="mse", **kw)
+    flat = oobs.flatten_weight(w, a)
+    omn, omx, steps = oobs.mse_grid_search(flat, a, return_steps=True)
+    agree = ((mn == omn.reshape(mn.shape)) & (mx == omx.reshape(mx.shape))).float().mean().item()
+    shrunk = (omx.abs() < flat.abs().amax(dim=(0, -1))).float().mean().item()
+    say(f"  agreement {agree:.5f} over {steps} steps, {shrunk:.3f} of the groups shrunk")
+    assert agree == 1.0
+    if case["strategy"] == "tensor_group":
+        qp = obs.get_qparams()
+        gs = oobs.global_scale_from_stats([(omn, omx)])
+        s_o, _ = oobs.calculate_qparams(omn, omx, a, global_scale=gs)
+        assert torch.equal(qp["global_scale"].cpu().float().reshape(1), gs.float().reshape(1))
+        assert torch.equal(qp["scale"].cpu().float().reshape(s_o.shape), s_o.float())
+
+
+def test_mse_observer_mx_and_fp8_scaled_fp4_refused(dev):
+    """MXFP4 (e8m0 candidate scales) and fp4 with fp8 scales (the NVFP4
+    preset) are not searched: the observer raises."""
+    for kw in (dict(strategy="tensor_group", group_size=16, scale_dtype=torch.float8_e4m3fn),
+               dict(strategy="group", group_size=32, scale_dtype=torch.uint8, zp_dtype=torch.uint8)):
+        args = QuantizationArgs(num_bits=4, type="float", symmetric=True, observer="memoryless_mse", **kw)
+        obs = Observer.load_from_registry("memoryless_mse", base_name="weight", args=args)
+        with pytest.raises(NotImplementedError):
+            obs(torch.randn(32, 64, device=dev))
 
 
 @pytest.mark.parametrize("strategy", ["tensor", "group"])
