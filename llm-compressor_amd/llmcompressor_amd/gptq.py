@@ -46,14 +46,28 @@ def _is_linear_like(module) -> bool:
     return type(module).__name__ == "Conv1D"  # transformers.Conv1D
 
 
+def conv2d_rows(inp: torch.Tensor, module: torch.nn.Conv2d) -> torch.Tensor:
+    """The patches a Conv2d sees, one row each: [batch * positions,
+    in_channels * kh * kw] in the order of ``gptq_quantize.py:80-89``'s
+    unfold, permute and flatten (the transpose of its columns)."""
+    cols = torch.nn.functional.unfold(inp, module.kernel_size, dilation=module.dilation, padding=module.padding,
+                                      stride=module.stride)
+    return cols.transpose(1, 2).reshape(-1, cols.shape[1])
+
+
 def hessian_rows(inp: torch.Tensor, module: torch.nn.Module, device) -> tuple[torch.Tensor, int]:
     """The 2-D rows of one accumulation call on ``device`` and the
     reference's sample count for it: the leading dimension after a 2-D input
-    is unsqueezed to 3-D (``gptq_quantize.py:72-80``)."""
+    is unsqueezed to 3-D (``gptq_quantize.py:72-80``); a Conv2d's input
+    becomes its unfolded patches (``:80-89``; its Hessian has in_channels *
+    kh * kw columns, which ``make_empty_hessian``'s weight.shape[1] matches
+    for 1 x 1 kernels only, as in the reference)."""
     if inp.device != device:
         inp = inp.to(device=device)
     if inp.dim() == 2:
         inp = inp.unsqueeze(0)
+    if isinstance(module, torch.nn.Conv2d):
+        return conv2d_rows(inp, module), inp.shape[0]
     if not _is_linear_like(module):
         raise NotImplementedError(f"GPTQ Hessian for {type(module).__name__} is not provided by this build")
     return inp.reshape(-1, inp.shape[-1]), inp.shape[0]

@@ -10,9 +10,9 @@ Same names, signatures, return values and error behaviour as
 
 As for GPTQ, ``accumulate_hessian`` maintains the upper triangle of the
 running-mean Hessian (diagonal included) and ``sparsify_weight`` reads only
-that triangle.  Differences, all raising instead of computing: Conv2d
-modules (the unfold branch), calibration inputs that are not bf16, block sizes
-above 128 and N:M groups wider than 16 columns.
+that triangle.  Conv2d inputs are unfolded into their patches for the
+Hessian, as the reference does; pruning a Conv2d weight, block sizes above
+128 and N:M groups wider than 16 columns raise instead of computing.
 """
 from __future__ import annotations
 
@@ -22,7 +22,7 @@ import torch
 
 from . import ops
 from ._lib import UNSUPPORTED, Mi355qError
-from .gptq import _is_linear_like
+from .gptq import _is_linear_like, conv2d_rows
 
 logger = logging.getLogger("llmcompressor_amd")
 
@@ -54,6 +54,8 @@ def hessian_rows(inp: torch.Tensor, module: torch.nn.Module, device) -> tuple[to
     inp = inp.to(device=device)
     if len(inp.shape) == 2:
         inp = inp.unsqueeze(0)
+    if isinstance(module, torch.nn.Conv2d):   # sgpt_sparsify.py:37-45: the unfolded patches
+        return conv2d_rows(inp, module), inp.shape[0]
     if not _is_linear_like(module):
         raise NotImplementedError(f"SparseGPT Hessian for {type(module).__name__} is not provided by this build")
     return inp.reshape(-1, inp.shape[-1]), inp.shape[0]

@@ -38,6 +38,23 @@ def make_empty_hessian(num_columns: int, device="cpu") -> torch.Tensor:
     return torch.zeros((num_columns, num_columns), device=device, dtype=GPTQ_PRECISION)
 
 
+def accumulate_hessian_conv2d(inp: torch.Tensor, H: torch.Tensor, num_samples: torch.Tensor, kernel_size,
+                              dilation=1, padding=0, stride=1):
+    """Conv2d branch of ``gptq_quantize.py:63-97`` (``:80-89``): the input
+    [B, C, h, w] unfolded into its patches, features x samples."""
+    inp = inp.to(device=H.device)
+    num_added = inp.shape[0]
+    unfold = torch.nn.Unfold(kernel_size, dilation=dilation, padding=padding, stride=stride)
+    inp = unfold(inp)
+    inp = inp.permute([1, 0, 2])
+    inp = inp.flatten(1)
+    num_samples += num_added
+    inp = inp.to(dtype=GPTQ_PRECISION)
+    inp = math.sqrt(2) * inp
+    H += inp.matmul(inp.t())
+    return H, num_samples
+
+
 def accumulate_hessian(inp: torch.Tensor, H: torch.Tensor, num_samples: torch.Tensor):
     """Linear / Conv1D branch of ``gptq_quantize.py:63-97``."""
     inp = inp.to(device=H.device)

@@ -159,6 +159,44 @@ def test_hessian_dropin_counts_and_strided_input(dev):
     assert rel_fro(H.cpu(), Ho) <= HESS_TOL
 
 
+@pytest.mark.parametrize("k,stride,pad,dil", [(1, 1, 0, 1), (3, 1, 1, 1), (3, 2, 1, 2)])
+def test_hessian_conv2d_unfold(dev, k, stride, pad, dil):
+    """Conv2d inputs through the drop-in accumulate_hessian (gptq_quantize.py:
+    80-89): the unfolded patches' Hessian against the oracle's, the batch as
+    the sample count; the 1 x 1 kernel with make_empty_hessian's size."""
+    say(f"conv2d hessian k={k} stride={stride} pad={pad} dil={dil}")
+    C = 96
+    conv = torch.nn.Conv2d(C, 16, k, stride=stride, padding=pad, dilation=dil).to(dev)
+    d = C * k * k
+    x = workloads.heavy_tailed_activations((4 * 20 * 24, C), seed=k + stride).reshape(4, 20, 24, C)
+    x = x.permute(0, 3, 1, 2).contiguous()        # [B, C, h, w] bf16
+    H = gptq.make_empty_hessian(conv) if k == 1 else torch.zeros(d, d, device=dev)
+    n = torch.zeros((), device=dev)
+    H, n = gptq.accumulate_hessian(x.to(dev), conv, H, n)
+    Ho, no = og.accumulate_hessian_conv2d(x, torch.zeros(d, d), torch.zeros(()), k, dil, pad, stride)
+    assert float(n) == float(no) == 4.0
+    assert rel_fro(torch.triu(H.cpu()), torch.triu(Ho)) <= HESS_TOL
+
+
+def test_sparsegpt_hessian_conv2d_unfold(dev):
+    """The running-mean Hessian of a 1 x 1 Conv2d (sgpt_sparsify.py:37-45)."""
+    from llmcompressor_amd import sparsegpt
+    from oracle import sparsegpt as osg
+    say("sparsegpt conv2d hessian")
+    C = 64
+    conv = torch.nn.Conv2d(C, 8, 1).to(dev)
+    xs = [workloads.heavy_tailed_activations((2 * 10 * 12, C), seed=40 + i).reshape(2, 10, 12, C)
+          .permute(0, 3, 1, 2).contiguous() for i in range(3)]
+    H, n = sparsegpt.make_empty_hessian(conv), 0
+    Ho, no = osg.make_empty_hessian(C), 0
+    for x in xs:
+        H, n = sparsegpt.accumulate_hessian(x.to(dev), conv, H, n)
+        # the 1 x 1 patches are the pixels' channel vectors: the Linear form of the oracle
+        Ho, no = osg.accumulate_hessian(x.permute(0, 2, 3, 1).reshape(2, -1, C), Ho, no)
+    assert n == no == 6
+    assert rel_fro(torch.triu(H.cpu()), torch.triu(Ho)) <= HESS_TOL
+
+
 def test_hessian_grouped_parity(dev):
     say("grouped hessian")
     T, d, E = 3000, 256, 6

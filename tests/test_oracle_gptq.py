@@ -197,3 +197,31 @@ def test_nvfp4_global_scale_in_outputs():
     gs = out["weight_global_scale"]
     assert gs.dtype == W.dtype and gs.numel() == 1
     assert float(gs) == pytest.approx(448 * 6 / float(W.abs().max()), rel=1e-2)
+
+
+@pytest.mark.parametrize("k,stride,pad,dil", [(3, 1, 1, 1), (3, 2, 0, 2), (1, 1, 0, 1), (2, 3, 1, 1)])
+def test_conv2d_hessian_is_the_patch_gram_matrix(k, stride, pad, dil):
+    """The oracle's Conv2d branch (unfold, permute, flatten) against patches
+    cut out by explicit loops: H = 2 sum over (image, position) of p p^T,
+    p the (channel, ky, kx)-ordered receptive field, zero outside the image."""
+    g = torch.Generator().manual_seed(k * 7 + stride)
+    B, C, h, w = 2, 3, 6, 5
+    x = torch.randn(B, C, h, w, generator=g, dtype=torch.float64)
+    d = C * k * k
+    H, n = og.accumulate_hessian_conv2d(x.float(), torch.zeros(d, d), torch.zeros(()), k, dil, pad, stride)
+    ho = (h + 2 * pad - dil * (k - 1) - 1) // stride + 1
+    wo = (w + 2 * pad - dil * (k - 1) - 1) // stride + 1
+    ref = torch.zeros(d, d, dtype=torch.float64)
+    for b in range(B):
+        for oy in range(ho):
+            for ox in range(wo):
+                p = torch.zeros(d, dtype=torch.float64)
+                for c in range(C):
+                    for ky in range(k):
+                        for kx in range(k):
+                            iy, ix = oy * stride - pad + ky * dil, ox * stride - pad + kx * dil
+                            if 0 <= iy < h and 0 <= ix < w:
+                                p[(c * k + ky) * k + kx] = x[b, c, iy, ix]
+                ref += 2 * torch.outer(p, p)
+    assert float(n) == B
+    assert torch.allclose(H.double(), ref, rtol=1e-5, atol=1e-5)
