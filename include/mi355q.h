@@ -52,7 +52,9 @@ typedef enum {
 typedef enum {
   MI355Q_QTYPE_INT = 0,        /* integers, num_bits <= 8 */
   MI355Q_QTYPE_FP8_E4M3 = 1,   /* float8_e4m3fn (FP8 schemes) */
-  MI355Q_QTYPE_FP4_E2M1 = 2    /* fp4 e2m1 (MXFP4, NVFP4) */
+  MI355Q_QTYPE_FP4_E2M1 = 2,   /* fp4 e2m1 (MXFP4, NVFP4) */
+  MI355Q_QTYPE_MXFP4_CT = 3,   /* e2m1 with e8m0 group scales, CT rule (MSE searches only) */
+  MI355Q_QTYPE_MXFP4_OCP = 4   /* e2m1 with e8m0 group scales, OCP rule (MSE searches only) */
 } mi355q_qtype;
 
 /* MXFP4 shared-exponent rule (see mi355q_mxfp4_quantize_pack). */
@@ -351,7 +353,9 @@ int mi355q_nvfp4_qparams(const float* min_dev, const float* max_dev, int64_t n, 
  * clamp, as the cast to float8_e4m3fn in CT round_to_quantized_type does);
  * MI355Q_QTYPE_FP4_E2M1: the e2m1 grid (symmetric, qmin = -qmax <= 6; CT
  * cast_to_fp4).  The candidates' scales are calculate_qparams' without a
- * global scale (observers/mse_quant.py:255-262). */
+ * global scale (observers/mse_quant.py:255-262); MI355Q_QTYPE_MXFP4_CT /
+ * _OCP: the e2m1 grid with each candidate's scale 2^(e - 127), e the e8m0
+ * exponent of max(|min|, |max|) by that rule (as mi355q_mx_scales). */
 size_t mi355q_observe_mse_workspace_size(int64_t rows, int64_t cols, int64_t cell_rows, int64_t cell_cols,
                                          int total_steps);
 int mi355q_observe_mse(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_t cols, int64_t ldx,

@@ -206,6 +206,29 @@ __global__ void qparams_kernel(const float* mn_in, const float* mx_in, int64_t n
   zp_out[i] = zp;
 }
 
+// e8m0 exponent byte of an MX group scale from the group absmax (rule:
+// MI355Q_MX_RULE_CT / _OCP)
+__device__ __forceinline__ int mx_exponent(float amax, int rule) {
+  // amax is a bf16 value (exact in fp32), >= 0
+  if (amax == 0.f) return 0;
+  int e;
+  if (rule == MI355Q_MX_RULE_CT) {
+    uint32_t bits = (__float_as_uint(amax) >> 16) & 0xffffu;
+    bits = (bits + 32u) & 0xff80u;
+    e = (int)((bits >> 7) & 0xffu) - 127;
+  } else {
+    uint32_t u = __float_as_uint(amax);
+    int ef = (int)((u >> 23) & 0xffu);
+    if (ef == 0) {  // fp32 subnormal (not reachable from bf16 normal data)
+      e = -127 - __clz(u & 0x7fffffu) + 9 - 1;
+    } else {
+      e = ef - 127;
+    }
+  }
+  int e8 = e + 127 - 2;
+  return e8 < 0 ? 0 : (e8 > 254 ? 254 : e8);
+}
+
 // ---------------------------------------------------------------- MSE observer
 // observers/mse_quant.py:48-130,244-273.  A matrix is split into cells of
 // cell_rows x cell_cols (clipped at the edges, row-major) - a group, a channel,
@@ -226,6 +249,7 @@ struct MseArgs {
   const float* mn;
   const float* mx;
   const float* imp;  // weighted (imatrix) mode: per-column importance, or NULL
+  int mx_rule;       // MX candidate scales (FQ == 3): the e8m0 rule
 };
 
 // bf16 rounding (hardware round-to-nearest-even) when the observed dtype is bf16
@@ -266,7 +290,8 @@ __device__ __forceinline__ float shrink_p(int i, double grid) { return (float)(1
 // observed dtype), times the column's importance w.
 // FQ: the value grid after the clamp: 0 integers (rint), 1 fp8 e4m3 (round
 // to nearest even, as the cast to float8_e4m3fn does), 2 fp4 e2m1 (CT
-// cast_to_fp4's nearest value, ties to even).
+// cast_to_fp4's nearest value, ties to even), 3 e2m1 with MX (power of two)
+// scales.
 template <bool B, bool ZP, bool IM, int FQ = 0>
 __device__ __forceinline__ float mse_term(float v, float s, float rs, float z, float qmin, float qmax, float norm,
                                           const uint16_t* tab, float w) {
@@ -279,12 +304,27 @@ __device__ __forceinline__ float mse_term(float v, float s, float rs, float z, f
   }
   if (ZP) t = rb<B>(t + z);
   t = fminf(fmaxf(t, qmin), qmax);
-  t = FQ == 1 ? fp8e4m3_rne(t) : FQ == 2 ? fp4e2m1_round(t) : rintf(t);
+  t = FQ == 1 ? fp8e4m3_rne(t) : FQ >= 2 ? fp4e2m1_round(t) : rintf(t);
   if (ZP) t = rb<B>(t - z);
   if (IM) return pow_norm<false>(fabsf(rb<B>(t * s) - v), norm) * w;
   const float d = fabsf(rb<B>(rb<B>(t * s) - v));
   if (B) return __uint_as_float((uint32_t)tab[__float_as_uint(d) >> 16] << 16);
   return pow_norm<false>(d, norm);
+}
+
+// A candidate's scale and zero point from its shrunk min / max: CT
+// calculate_qparams in the observed dtype, or for MX the power of two of the
+// e8m0 exponent of max(|min|, |max|) (as a bf16 value for the CT rule).
+template <bool B, bool ZP, int FQ>
+__device__ __forceinline__ void cand_qparams(const MseArgs& a, float mn, float mx, float& s, float& z) {
+  if constexpr (FQ == 3) {
+    const float amax = fmaxf(fabsf(fminf(mn, 0.f)), fmaxf(mx, 0.f));
+    const int e8 = mx_exponent(a.mx_rule == MI355Q_MX_RULE_CT ? round_to_bf16(amax) : amax, a.mx_rule);
+    s = e8 > 0 ? __uint_as_float((uint32_t)e8 << 23) : __uint_as_float(0x00400000u);  // 2^(e8 - 127)
+    z = 0.f;
+  } else {
+    qparams_one(mn, mx, a.qmin, a.qmax, !ZP, false, B, s, z);
+  }
 }
 
 __device__ __forceinline__ void cell_geom(const MseArgs& a, int64_t cell, int64_t& r0, int64_t& c0, int64_t& cwe,
@@ -336,7 +376,7 @@ __global__ __launch_bounds__(NT) void mse_err_small_kernel(MseArgs a, int lg_log
     for (int i = 0; i < a.T; ++i) {
       const float p = shrink_p(i, a.grid);
       float s, z;
-      qparams_one(rb<B>(mn * p), rb<B>(mx * p), a.qmin, a.qmax, !ZP, false, B, s, z);
+      cand_qparams<B, ZP, FQ>(a, rb<B>(mn * p), rb<B>(mx * p), s, z);
       const float rs = 1.f / s;
       float acc = 0.f;
 #pragma unroll
@@ -378,7 +418,7 @@ __global__ __launch_bounds__(NT) void mse_err_large_kernel(MseArgs a, int64_t nc
     for (int i = 0; i < a.T; ++i) {
       const float p = shrink_p(i, a.grid);
       float s, z;
-      qparams_one(rb<B>(mn * p), rb<B>(mx * p), a.qmin, a.qmax, !ZP, false, B, s, z);
+      cand_qparams<B, ZP, FQ>(a, rb<B>(mn * p), rb<B>(mx * p), s, z);
       const float rs = 1.f / s;
       float acc = 0.f;
 #pragma unroll
@@ -558,26 +598,6 @@ __global__ void pack_int4_int8_kernel(const int8_t* codes, int64_t rows, int64_t
 }
 
 // ---------------------------------------------------------------- MXFP4
-__device__ __forceinline__ int mx_exponent(float amax, int rule) {
-  // amax is a bf16 value (exact in fp32), >= 0
-  if (amax == 0.f) return 0;
-  int e;
-  if (rule == MI355Q_MX_RULE_CT) {
-    uint32_t bits = (__float_as_uint(amax) >> 16) & 0xffffu;
-    bits = (bits + 32u) & 0xff80u;
-    e = (int)((bits >> 7) & 0xffu) - 127;
-  } else {
-    uint32_t u = __float_as_uint(amax);
-    int ef = (int)((u >> 23) & 0xffu);
-    if (ef == 0) {  // fp32 subnormal (not reachable from bf16 normal data)
-      e = -127 - __clz(u & 0x7fffffu) + 9 - 1;
-    } else {
-      e = ef - 127;
-    }
-  }
-  int e8 = e + 127 - 2;
-  return e8 < 0 ? 0 : (e8 > 254 ? 254 : e8);
-}
 
 __device__ __forceinline__ float exp2i(int k) {  // 2^k for k in [-149, 127]
   if (k >= -126) return __uint_as_float((uint32_t)(k + 127) << 23);
@@ -1031,11 +1051,12 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
   MQ_CHECK_ARG(cell_rows > 0 && cell_cols > 0, "observe_mse: bad cell shape");
   MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F32, "observe_mse: dtype must be bf16 or fp32");
   MQ_CHECK_ARG(qmin < 0.f && qmax > 0.f, "observe_mse: range must straddle zero");
+  const bool mx = qtype == MI355Q_QTYPE_MXFP4_CT || qtype == MI355Q_QTYPE_MXFP4_OCP;
   MQ_CHECK_ARG(qtype == MI355Q_QTYPE_INT ||
                    (qtype == MI355Q_QTYPE_FP8_E4M3 && symmetric && qmin == -qmax && qmax <= 448.f) ||
-                   (qtype == MI355Q_QTYPE_FP4_E2M1 && symmetric && qmin == -qmax && qmax <= 6.f),
+                   ((qtype == MI355Q_QTYPE_FP4_E2M1 || mx) && symmetric && qmin == -qmax && qmax <= 6.f),
                "observe_mse: value type must be integer, or fp8 e4m3 / fp4 e2m1 symmetric within their range");
-  const int fq = qtype == MI355Q_QTYPE_FP8_E4M3 ? 1 : qtype == MI355Q_QTYPE_FP4_E2M1 ? 2 : 0;
+  const int fq = qtype == MI355Q_QTYPE_FP8_E4M3 ? 1 : qtype == MI355Q_QTYPE_FP4_E2M1 ? 2 : mx ? 3 : 0;
   MQ_CHECK_ARG(total_steps >= 0 && grid != 0.0, "observe_mse: bad search grid");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t ncells = ((rows + cell_rows - 1) / cell_rows) * ((cols + cell_cols - 1) / cell_cols);
@@ -1054,7 +1075,7 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
   uint16_t* tab = reinterpret_cast<uint16_t*>(ws + pl.off_tab);
   MseArgs a{x_dev, rows, cols, ldx, cell_rows, cell_cols, (rows + cell_rows - 1) / cell_rows,
             (cols + cell_cols - 1) / cell_cols, qmin, qmax, total_steps, grid, norm, min_dev, max_dev,
-            im ? imp : nullptr};
+            im ? imp : nullptr, qtype == MI355Q_QTYPE_MXFP4_OCP ? MI355Q_MX_RULE_OCP : MI355Q_MX_RULE_CT};
   const bool b = dtype == MI355Q_BF16, zp = symmetric == 0;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(NT), 0, st, any, total_steps);
   MQ_LAUNCH_CHECK();
@@ -1067,8 +1088,11 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
   // (the float grids: symmetric only; f00 .. f11 (fp8) and h00 .. h11 (fp4)
   // are their (bf16, imatrix) variants)
   auto pick = [&](auto k000, auto k001, auto k010, auto k011, auto k100, auto k101, auto k110, auto k111,
-                  auto f00, auto f01, auto f10, auto f11, auto h00, auto h01, auto h10, auto h11, auto&& go) {
-    if (fq == 1) {
+                  auto f00, auto f01, auto f10, auto f11, auto h00, auto h01, auto h10, auto h11, auto m00,
+                  auto m01, auto m10, auto m11, auto&& go) {
+    if (fq == 3) {
+      if (b) im ? go(m11) : go(m10); else im ? go(m01) : go(m00);
+    } else if (fq == 1) {
       if (b) im ? go(f11) : go(f10); else im ? go(f01) : go(f00);
     } else if (fq == 2) {
       if (b) im ? go(h11) : go(h10); else im ? go(h01) : go(h00);
@@ -1089,6 +1113,8 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
          mse_err_small_kernel<true, false, false, 1>, mse_err_small_kernel<true, false, true, 1>,
          mse_err_small_kernel<false, false, false, 2>, mse_err_small_kernel<false, false, true, 2>,
          mse_err_small_kernel<true, false, false, 2>, mse_err_small_kernel<true, false, true, 2>,
+         mse_err_small_kernel<false, false, false, 3>, mse_err_small_kernel<false, false, true, 3>,
+         mse_err_small_kernel<true, false, false, 3>, mse_err_small_kernel<true, false, true, 3>,
          [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.lg_log2, tab, err); });
   } else {
     const dim3 g((unsigned)min(ncells * pl.nchunk, kMaxWg));
@@ -1100,6 +1126,8 @@ int observe_mse_impl(const void* x_dev, mi355q_dtype dtype, int64_t rows, int64_
          mse_err_large_kernel<true, false, false, 1>, mse_err_large_kernel<true, false, true, 1>,
          mse_err_large_kernel<false, false, false, 2>, mse_err_large_kernel<false, false, true, 2>,
          mse_err_large_kernel<true, false, false, 2>, mse_err_large_kernel<true, false, true, 2>,
+         mse_err_large_kernel<false, false, false, 3>, mse_err_large_kernel<false, false, true, 3>,
+         mse_err_large_kernel<true, false, false, 3>, mse_err_large_kernel<true, false, true, 3>,
          [&](auto kernel) { hipLaunchKernelGGL(kernel, g, dim3(NT), 0, st, a, pl.nchunk, tab, part); });
   }
   MQ_LAUNCH_CHECK();

@@ -16,7 +16,7 @@ OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_POSITIVE_DEFINITE, HIP_ERROR = 0, 1, 2, 3
 BF16, F32, F16 = 0, 1, 2
 TENSOR, CHANNEL, GROUP, BLOCK, TOKEN = 0, 1, 2, 3, 4
 MX_RULE_CT, MX_RULE_OCP = 0, 1
-QTYPE_INT, QTYPE_FP8_E4M3, QTYPE_FP4_E2M1 = 0, 1, 2
+QTYPE_INT, QTYPE_FP8_E4M3, QTYPE_FP4_E2M1, QTYPE_MXFP4_CT, QTYPE_MXFP4_OCP = 0, 1, 2, 3, 4
 
 _vp, _i64, _i32, _f32, _f64, _sz = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double, C.c_size_t
 

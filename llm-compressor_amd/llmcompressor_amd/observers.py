@@ -224,14 +224,18 @@ class _MSEObserver(Observer):
         raise ValueError(f"{s.value} quantization cannot be observed for activations here")
 
     def _grid(self) -> str:
-        """The value grid of the search: integers, fp8 e4m3 or fp4 e2m1
+        """The value grid of the search: integers, fp8 e4m3, fp4 e2m1 or MXFP4
         (symmetric; the candidates' scales as calculate_qparams gives them
         without a global scale, mse_quant.py:255-262 - for NVFP4 the global
         scale then comes from the searched statistics, observers/base.py:78-96)."""
         a = self.args
         if a.type == QuantizationType.INT and not a.is_mx:
             return "int"
-        if a.type == QuantizationType.FLOAT and not a.is_mx and a.symmetric:
+        if a.is_mx:
+            # candidates' scales: the power of two of the e8m0 exponent of
+            # their shrunk absmax, by the observer's MX rule
+            return "mxfp4_" + a.observer_kwargs.get("mx_rule", "ct")
+        if a.type == QuantizationType.FLOAT and a.symmetric:
             if a.num_bits == 8 and a.strategy != QuantizationStrategy.TENSOR_GROUP:
                 return "fp8"
             # with fp8 scales (the NVFP4 preset) each candidate's scale would
@@ -240,8 +244,8 @@ class _MSEObserver(Observer):
             # pinned, so only searches without a scale dtype are provided
             if a.num_bits == 4 and a.scale_dtype is None:
                 return "fp4"
-        raise NotImplementedError("MSE observers for MXFP4 (e8m0 candidate scales), fp4 with fp8 scales and "
-                                  "asymmetric float types are not provided by this build")
+        raise NotImplementedError("MSE observers for fp4 with fp8 scales and asymmetric float types are not "
+                                  "provided by this build")
 
     def _min_max(self, observed: torch.Tensor):
         a = self.args

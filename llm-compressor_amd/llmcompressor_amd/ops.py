@@ -194,7 +194,8 @@ STRATEGY_CODE = {"tensor": L.TENSOR, "channel": L.CHANNEL, "group": L.GROUP, "te
                  "block": L.BLOCK, "token": L.TOKEN}
 
 
-QTYPE = {"int": L.QTYPE_INT, "fp8": L.QTYPE_FP8_E4M3, "fp4": L.QTYPE_FP4_E2M1}
+QTYPE = {"int": L.QTYPE_INT, "fp8": L.QTYPE_FP8_E4M3, "fp4": L.QTYPE_FP4_E2M1, "mxfp4_ct": L.QTYPE_MXFP4_CT,
+         "mxfp4_ocp": L.QTYPE_MXFP4_OCP}
 
 
 def gptq_sweep_(w_work: torch.Tensor, hinv: torch.Tensor, scale: torch.Tensor, zero_point, strategy: str,

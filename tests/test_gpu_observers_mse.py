@@ -158,15 +158,41 @@ def test_mse_observer_fp4_matches_oracle(dev, case, dtype):
         assert torch.equal(qp["scale"].cpu().float().reshape(s_o.shape), s_o.float())
 
 
-def test_mse_observer_mx_and_fp8_scaled_fp4_refused(dev):
-    """MXFP4 (e8m0 candidate scales) and fp4 with fp8 scales (the NVFP4
-    preset) are not searched: the observer raises."""
-    for kw in (dict(strategy="tensor_group", group_size=16, scale_dtype=torch.float8_e4m3fn),
-               dict(strategy="group", group_size=32, scale_dtype=torch.uint8, zp_dtype=torch.uint8)):
-        args = QuantizationArgs(num_bits=4, type="float", symmetric=True, observer="memoryless_mse", **kw)
-        obs = Observer.load_from_registry("memoryless_mse", base_name="weight", args=args)
-        with pytest.raises(NotImplementedError):
-            obs(torch.randn(32, 64, device=dev))
+def test_mse_observer_fp8_scaled_fp4_refused(dev):
+    """fp4 with fp8 scales (the NVFP4 preset) is not searched: the observer
+    raises."""
+    args = QuantizationArgs(num_bits=4, type="float", symmetric=True, observer="memoryless_mse",
+                            strategy="tensor_group", group_size=16, scale_dtype=torch.float8_e4m3fn)
+    obs = Observer.load_from_registry("memoryless_mse", base_name="weight", args=args)
+    with pytest.raises(NotImplementedError):
+        obs(torch.randn(32, 64, device=dev))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_mse_observer_mxfp4_matches_oracle(dev, dtype):
+    """MXFP4 (group 32): each candidate's scale is the power of two of the
+    e8m0 exponent of its shrunk absmax (calculate_qparams' MX branch, CT
+    rule); the chosen min / max equal the oracle's in every group, and so do
+    the resulting e8m0 scales."""
+    g = torch.Generator().manual_seed(29)
+    w = (torch.randn(192, 1024, generator=g) * torch.exp(torch.randn(192, 1, generator=g) * 2)).to(dtype)
+    say(f"mse observer mxfp4 {dtype}")
+    args = QuantizationArgs(num_bits=4, type="float", symmetric=True, strategy="group", group_size=32,
+                            scale_dtype=torch.uint8, zp_dtype=torch.uint8, observer="memoryless_mse")
+    obs = Observer.load_from_registry("memoryless_mse", base_name="weight", args=args)
+    obs(w.to(dev))
+    mn, mx = obs.min_vals.cpu(), obs.max_vals.cpu()
+    qp = obs.get_qparams()
+    a = OArgs(num_bits=4, type="float", symmetric=True, strategy="group", group_size=32, is_mx=True,
+              observer="mse")
+    flat = oobs.flatten_weight(w, a)
+    omn, omx, steps = oobs.mse_grid_search(flat, a, return_steps=True)
+    agree = ((mn == omn.reshape(mn.shape)) & (mx == omx.reshape(mx.shape))).float().mean().item()
+    shrunk = (omx.abs() < flat.abs().amax(dim=(0, -1))).float().mean().item()
+    say(f"  agreement {agree:.5f} over {steps} steps, {shrunk:.3f} of the groups shrunk")
+    assert agree == 1.0
+    s_o, _ = oobs.calculate_qparams(omn, omx, a)
+    assert torch.equal(qp["scale"].cpu().float().reshape(s_o.shape), s_o.float())
 
 
 @pytest.mark.parametrize("strategy", ["tensor", "group"])
