@@ -215,13 +215,16 @@ __device__ __forceinline__ void nm_select(PruneState& S, const float* dd2, int g
 // update of the slot holding column I + 1 comes first and ends the step's
 // scheduling region, so the Hinv reads issued before it (two steps ahead)
 // cannot sink into the step that uses them.
-template <int TO, int GO, bool NM, bool PRESERVE>
+template <int TO, int GO, bool NM, bool PRESERVE, int MC>
 __device__ __forceinline__ void prune_step(PruneState& S, const StepH& p, const float* dd2, int g, int count, int n,
                                            int m, int& next_group) {
+  // MC > 0: the group width known at compile time (groups start at I % MC == 0)
   constexpr int I = SW_G * TO + GO;
-  if (NM && I == next_group && I < count) {
-    next_group += m;
-    nm_select<TO, GO, PRESERVE>(S, dd2, g, min(I + m, count), n, m);
+  constexpr bool start_known = MC > 0;
+  if (NM && (start_known ? I % (MC > 0 ? MC : 1) == 0 : I == next_group) && I < count) {
+    const int mm = MC > 0 ? MC : m;
+    next_group += mm;
+    nm_select<TO, GO, PRESERVE>(S, dd2, g, min(I + mm, count), n, mm);
   }
   constexpr int TN = GO == SW_G - 1 ? TO + 1 : TO;  // slot of column I + 1
   const float x = S.w[TO];
@@ -248,19 +251,19 @@ __device__ __forceinline__ void prune_step(PruneState& S, const StepH& p, const 
 }
 
 // cur: the Hinv values of step I, nxt: those of step I + 1
-template <int I, bool NM, bool PRESERVE>
+template <int I, bool NM, bool PRESERVE, int MC>
 struct PruneSteps {
   static __device__ __forceinline__ void run(PruneState& S, const float* h1, const float* rdg, const float* dd2,
                                              int g, int count, int n, int m, int& next_group, const StepH& cur,
                                              const StepH& nxt) {
     StepH nn;
     load_step<I + 2>(nn, h1, rdg, g);
-    prune_step<I / SW_G, I % SW_G, NM, PRESERVE>(S, cur, dd2, g, count, n, m, next_group);
-    PruneSteps<I + 1, NM, PRESERVE>::run(S, h1, rdg, dd2, g, count, n, m, next_group, nxt, nn);
+    prune_step<I / SW_G, I % SW_G, NM, PRESERVE, MC>(S, cur, dd2, g, count, n, m, next_group);
+    PruneSteps<I + 1, NM, PRESERVE, MC>::run(S, h1, rdg, dd2, g, count, n, m, next_group, nxt, nn);
   }
 };
-template <bool NM, bool PRESERVE>
-struct PruneSteps<MAXB, NM, PRESERVE> {
+template <bool NM, bool PRESERVE, int MC>
+struct PruneSteps<MAXB, NM, PRESERVE, MC> {
   static __device__ __forceinline__ void run(PruneState&, const float*, const float*, const float*, int, int, int,
                                              int, int&, const StepH&, const StepH&) {}
 };
@@ -270,7 +273,7 @@ struct PruneSteps<MAXB, NM, PRESERVE> {
 // block of count < MAXB columns the slots past count hold copies and LDS
 // entries that are never written back, and a step only updates later
 // columns, so they never reach the count columns that are.
-template <bool NM, bool PRESERVE>
+template <bool NM, bool PRESERVE, int MC = 0>
 __global__ __launch_bounds__(SW_NT, 4) void sgpt_sweep_kernel(float* __restrict__ W, int64_t rows, int64_t cols,
                                                               const float* __restrict__ hinv, int64_t i1, int count,
                                                               uint8_t* __restrict__ mask,
@@ -338,7 +341,7 @@ __global__ __launch_bounds__(SW_NT, 4) void sgpt_sweep_kernel(float* __restrict_
   StepH p0, p1;
   load_step<0>(p0, h1, rdg, g);
   load_step<1>(p1, h1, rdg, g);
-  PruneSteps<0, NM, PRESERVE>::run(S, h1, rdg, dd2, g, count, n, m, next_group, p0, p1);
+  PruneSteps<0, NM, PRESERVE, MC>::run(S, h1, rdg, dd2, g, count, n, m, next_group, p0, p1);
 
   // each slot is final: kept or zeroed value, error, loss
   float loss = 0.f;
@@ -367,9 +370,12 @@ __global__ __launch_bounds__(SW_NT, 4) void sgpt_sweep_kernel(float* __restrict_
 }
 
 template <class... A>
-void launch_prune(bool nm, bool preserve, dim3 grid, hipStream_t st, A... args) {
+void launch_prune(bool nm, bool preserve, int prune_m, dim3 grid, hipStream_t st, A... args) {
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(SW_NT), 0, st, args...); };
-  if (nm) preserve ? go(sgpt_sweep_kernel<true, true>) : go(sgpt_sweep_kernel<true, false>);
+  // 2:4 and other groups of four columns: the group starts and the rank
+  // loop's length known at compile time
+  if (nm && prune_m == 4) preserve ? go(sgpt_sweep_kernel<true, true, 4>) : go(sgpt_sweep_kernel<true, false, 4>);
+  else if (nm) preserve ? go(sgpt_sweep_kernel<true, true>) : go(sgpt_sweep_kernel<true, false>);
   else    preserve ? go(sgpt_sweep_kernel<false, true>) : go(sgpt_sweep_kernel<false, false>);
 }
 
@@ -486,7 +492,7 @@ extern "C" int mi355q_sparsegpt_sweep(float* w_work_dev, int64_t rows, int64_t c
         MQ_LAUNCH_CHECK();
       }
     }
-    launch_prune(nm, preserve, dim3(nwg), st, w_work_dev, rows, cols, hinv_dev, i1, count, mask_dev,
+    launch_prune(nm, preserve, prune_m, dim3(nwg), st, w_work_dev, rows, cols, hinv_dev, i1, count, mask_dev,
                  (const unsigned*)hs, hs_next, k, prune_n, prune_m, losses_dev, err, lde, (int)(i1 - s0));
     MQ_LAUNCH_CHECK();
     return MI355Q_OK;
