@@ -888,9 +888,10 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
   }
   __syncthreads();
 
-  // pivot checks, off the dependency chain: min over the pivots and a
-  // running sum of (piv - piv), NaN once any pivot is inf or NaN
-  float pmin = 1.f, pnan = 0.f;
+  // pivot check, off the dependency chain: every pivot positive and finite
+  // (denormals included), tested on the bits of the wave-uniform pivot with
+  // integer compares, which run on the scalar unit beside the column updates
+  int pd_ok = 1;
 
   // Factor + invert the 32 x 32 diagonal sub-block at o (wave 0 only).
   // Lanes 0..31 hold the rows of the sub-block (row role), lanes 32..63 the
@@ -957,8 +958,10 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
     read_col(3, col);
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
-      pmin = fminf(pmin, piv);
-      pnan += piv - piv;
+      {
+        const int pb = __builtin_bit_cast(int, piv);
+        pd_ok &= (pb > 0) & (pb < 0x7f800000);
+      }
       const float rl = __builtin_amdgcn_rsqf(piv);
       const float sj = v[j] * rl;
       const float m = sj * rl;
@@ -1099,7 +1102,7 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
     }
     __syncthreads();
   }
-  if (wave == 0 && lane == 0 && status && !(pmin > 0.f && pnan == 0.f)) *status = MI355Q_NOT_POSITIVE_DEFINITE;
+  if (wave == 0 && lane == 0 && status && !pd_ok) *status = MI355Q_NOT_POSITIVE_DEFINITE;
 
   // pair (2, 3): T_1 = L[96:128][64:96] X[64:96][64:96]; X[96:128][64:96] = -X[96:128][96:128] T_1
   {
