@@ -1043,6 +1043,9 @@ int choose_splits(int64_t n, int T) {
   const int64_t s = n / 2048;
   int S = s >= 8 ? 8 : s >= 4 ? 4 : s >= 2 ? 2 : 1;
   if (T > 512 && S > 2) S = 2;
+  // two splits of 128 < T <= 256 tiles take two rounds of half the tokens
+  // on the 256 CUs, as long as one split's single round, plus a reduction
+  if (S == 2 && T > 128 && T <= 256) S = 1;
   return S;
 }
 
