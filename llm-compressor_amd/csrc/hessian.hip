@@ -1043,10 +1043,16 @@ int choose_splits(int64_t n, int T) {
   const int64_t s = n / 2048;
   int S = s >= 8 ? 8 : s >= 4 ? 4 : s >= 2 ? 2 : 1;
   if (T > 512 && S > 2) S = 2;
-  // two splits of 128 < T <= 256 tiles take two rounds of half the tokens
-  // on the 256 CUs, as long as one split's single round, plus a reduction
-  if (S == 2 && T > 128 && T <= 256) S = 1;
-  return S;
+  if (S == 8) return S;  // the dense plan's tail parts even out its rounds
+  // Below that, the fewest splits that reach the shortest time: k splits
+  // take ceil(T k / 256) rounds on the 256 CUs, each 1 / k of the tokens,
+  // and every split beyond one adds a reduction (d = 4096 and 4096 tokens:
+  // one split, one round of 136 tiles, rather than two rounds of halves).
+  const auto rounds_x4 = [T](int k) { return (T * k + 255) / 256 * (4 / k); };
+  int best = 1;
+  for (int k = 2; k <= S; k *= 2)
+    if (rounds_x4(k) < rounds_x4(best)) best = k;
+  return best;
 }
 
 inline int tile_edge(int64_t d) { return d >= 512 ? 256 : 128; }
