@@ -271,7 +271,7 @@ def main():
         for ln in _COLLECT:
             others[ln["config"]["workload"]] = {k: ln[k] for k in ("metric", "value", "unit", "steps", "warmup")
                                                 if k in ln}
-            for k in ("phases_ms", "hessian", "act_quant_int8_per_token", "tokens_per_expert"):
+            for k in ("phases_ms", "hessian", "act_quant_int8_per_token", "tokens_per_expert", "modifier_path"):
                 if k in ln:
                     others[ln["config"]["workload"]][k] = ln[k]
         _COLLECT = None
@@ -519,7 +519,7 @@ def bench_moe(a):
     up = (torch.randn(E, inter, hid, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     down = (torch.randn(E, hid, inter, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     hs = _gpu_heavy(torch, dev, tokens, hid, 7)
-    idx, _ = workloads.moe_routing(tokens, E, k)
+    idx, wts = workloads.moe_routing(tokens, E, k)
     rows, offsets, _ = moe.route_tokens(idx.to(dev), E)
     counts = [offsets[e + 1] - offsets[e] for e in range(E)]
     inter_x = moe.expert_intermediate(hs, rows, offsets, gate, up)   # calibration forward (untimed)
@@ -547,9 +547,53 @@ def bench_moe(a):
     torch.cuda.synchronize()
     hess_ms, solve_ms = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
     flop = sum(c * (hid * (hid + 1) + inter * (inter + 1)) for c in counts)
+    del inter_x
+
+    # the same layer through GPTQModifier: a LinearExperts forward (the
+    # reference's per-expert loop) with the modifier's hooks on its 384 expert
+    # Linears (grouped accumulation per family), then the batched solves; the
+    # modifier's own cost is that time less the same forward without hooks
+    from llmcompressor_amd import GPTQModifier
+    from llmcompressor_amd.moe import LinearExperts
+    idx_d = idx.to(dev)
+    wts_d = wts.to(dev).to(torch.bfloat16)
+
+    def block():
+        return LinearExperts.from_stacked(gate.clone(), up.clone(), down.clone())
+
+    def plain():
+        with torch.no_grad():
+            block()(hs, idx_d, wts_d)
+
+    def modifier():
+        m = block()
+        mod = GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), actorder=None)
+        mod.on_initialize(m)
+        mod.on_calibration_start(m)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            m(hs, idx_d, wts_d)
+        mod.on_calibration_end()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        mod.on_sequential_epoch_end(list(mod._modules))
+        mod.on_finalize()
+        torch.cuda.synchronize()
+        return (t1 - t0) * 1e3, (time.perf_counter() - t1) * 1e3
+
+    plain_ms, _p = _timed(torch, plain, max(1, a.steps), 1)
+    modifier()   # warm-up
+    runs = [modifier() for _ in range(max(1, a.steps))]
+    fwd_ms = sum(r[0] for r in runs) / len(runs)
+    comp_ms = sum(r[1] for r in runs) / len(runs)
+    mod_ms = fwd_ms - plain_ms + comp_ms
     _line("MoE GPTQ ms/layer (128 experts W4A16 g128, 32768 tokens top-8: grouped Hessians + 384 solves)",
           ms, "ms/layer", a, ms, "moe_128x(768x2048,2048x768)_32768tok_top8",
           {"phases_ms": {"grouped_hessians": round(hess_ms, 3), "solves": round(solve_ms, 3)},
+           "modifier_path": {"ms": round(mod_ms, 3), "ratio_to_direct": round(mod_ms / ms, 3),
+                             "calibration_forward_with_hooks_ms": round(fwd_ms, 3),
+                             "forward_without_hooks_ms": round(plain_ms, 3), "compress_ms": round(comp_ms, 3)},
            "hessian": {"tflops": round(flop / hess_ms / 1e9, 1),
                        "frac_bf16_mfma_peak": round(flop / hess_ms / 1e9 / PEAK_BF16_TFLOPS, 4)},
            "tokens_per_expert": {"min": min(counts), "max": max(counts), "mean": sum(counts) / E}})

@@ -10,12 +10,12 @@ from .gptq import GPTQResult, PreparedHessian, accumulate_hessian, gptq_quantize
     make_empty_hessian, prepare_hessian, prepare_hessians_batched, quantize_weight, symmetrize_hessian
 from . import pipeline, save, sparsegpt
 from .modifiers import GPTQModifier, QuantizationModifier, SparseGPTModifier
-from .observers import Observer
-from .quant_args import (ActivationOrdering, QuantizationArgs, QuantizationScheme, QuantizationStrategy,
-                         QuantizationType, preset_name_to_scheme)
+from .observers import FUSED_LAYER_NAMES, Observer, fuse_weight_observers
+from .quant_args import (CT_ARG_FIELDS, ActivationOrdering, QuantizationArgs, QuantizationScheme,
+                         QuantizationStrategy, QuantizationType, preset_name_to_scheme, resolve_args)
 
 __all__ = [
-    "ActivationOrdering", "GPTQModifier", "GPTQResult", "Observer", "QuantizationArgs", "QuantizationModifier",
+    "CT_ARG_FIELDS", "FUSED_LAYER_NAMES", "fuse_weight_observers", "resolve_args", "ActivationOrdering", "GPTQModifier", "GPTQResult", "Observer", "QuantizationArgs", "QuantizationModifier",
     "QuantizationScheme", "QuantizationStrategy", "QuantizationType", "SparseGPTModifier", "pipeline", "save", "sparsegpt", "accumulate_hessian", "gptq_quantize",
     "gptq_quantize_batched", "initialize_module_for_quantization", "initialize_observer", "make_empty_hessian",
     "observe", "prepare_hessian", "prepare_hessians_batched", "PreparedHessian", "preset_name_to_scheme",

@@ -16,7 +16,7 @@ import torch
 from torch.nn import Module
 
 from .observers import Observer
-from .quant_args import QuantizationScheme
+from .quant_args import QuantizationScheme, resolve_args
 
 __all__ = ["initialize_observer", "observe", "update_qparams", "initialize_module_for_quantization"]
 
@@ -26,9 +26,9 @@ def initialize_module_for_quantization(module: Module, scheme: QuantizationSchem
     ``weight_zero_point`` parameters shaped for the weight strategy (and
     ``weight_global_scale`` for tensor groups)."""
     module.quantization_scheme = scheme
-    wa = scheme.weights
-    if wa is None or not hasattr(module, "weight"):
+    if scheme.weights is None or not hasattr(module, "weight"):
         return
+    wa = resolve_args(scheme.weights)
     rows, cols = module.weight.shape
     s = wa.strategy.value
     if s == "tensor":
@@ -62,6 +62,7 @@ def initialize_observer(module: Module, base_name: str) -> None:
     args = getattr(scheme, arg_name, None) if scheme is not None else None
     if args is None:
         return
+    args = resolve_args(args)
     observer = args.observer
     if base_name == "weight" and observer in ("static_minmax", "minmax"):
         observer = "memoryless_minmax"

@@ -22,7 +22,7 @@ from dataclasses import dataclass
 import torch
 
 from . import ops
-from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationStrategy, QuantizationType
+from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationStrategy, QuantizationType, resolve_args
 
 logger = logging.getLogger("llmcompressor_amd")
 
@@ -161,6 +161,7 @@ class PreparedHessian:
 
 
 def _effective_actorder(quant_args: QuantizationArgs):
+    quant_args = resolve_args(quant_args)
     actorder = quant_args.actorder
     if actorder == ActivationOrdering.GROUP and quant_args.strategy not in (QuantizationStrategy.GROUP,
                                                                             QuantizationStrategy.TENSOR_GROUP):
@@ -180,6 +181,7 @@ def prepare_hessian(hessian: torch.Tensor, quant_args: QuantizationArgs, num_sam
                     percdamp: float = 0.01) -> PreparedHessian:
     """Permutation, dead columns and Hinv for one upper-triangle Hessian
     (``gptq_quantize.py:130-196``)."""
+    quant_args = resolve_args(quant_args)
     actorder = _effective_actorder(quant_args)
     perm = invperm = None
     if actorder:
@@ -192,6 +194,7 @@ def prepare_hessian(hessian: torch.Tensor, quant_args: QuantizationArgs, num_sam
 def prepare_hessians_batched(hessians: torch.Tensor, quant_args: QuantizationArgs, num_samples=1.0,
                              percdamp: float = 0.01) -> PreparedHessian:
     """``prepare_hessian`` for a stack [B, d, d] (one launch per step)."""
+    quant_args = resolve_args(quant_args)
     actorder = _effective_actorder(quant_args)
     B, d, _ = hessians.shape
     ns = torch.as_tensor(num_samples, dtype=torch.float32, device=hessians.device).expand(B).contiguous()
@@ -213,8 +216,11 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
     ``modifiers/gptq/base.py:594``).  ``observer`` must already hold the
     weight statistics (``observe``), as in the reference.  ``prepared`` (from
     ``prepare_hessian`` on the same Hessian and quantization args) skips the
-    Cholesky chain for modules that share their input.
+    Cholesky chain for modules that share their input.  ``quant_args`` is
+    this package's ``QuantizationArgs`` or any object with compressed-tensors'
+    field names (``resolve_args``).
     """
+    quant_args = resolve_args(quant_args)
     strategy = quant_args.strategy
     qtype = _value_type(quant_args)
     W = weight
@@ -272,6 +278,7 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
     """
     from .observers import Observer
 
+    quant_args = resolve_args(quant_args)
     strategy = quant_args.strategy
     qtype = _value_type(quant_args)
     B, rows, cols = weights.shape
@@ -340,18 +347,25 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
 
 def quantize_weight(module: torch.nn.Module, quant_args: QuantizationArgs, hessian: torch.Tensor,
                     blocksize: int = 128, percdamp: float = 0.01):
-    """Drop-in for ``gptq_quantize.quantize_weight``: returns ``(loss, q_param_dict)``."""
-    res = gptq_quantize(module.weight, quant_args, hessian, module.weight_observer, blocksize, percdamp)
+    """Drop-in for ``gptq_quantize.quantize_weight``: returns ``(loss, q_param_dict)``.
+
+    ``quant_args`` may be compressed-tensors' ``QuantizationArgs`` (as
+    ``modifiers/gptq/base.py:591-597`` passes it) or any object with its
+    field names; only ``CT_ARG_FIELDS`` are read.  ``module.weight_observer``
+    is used through ``__call__``, ``get_qparams()`` and
+    ``delete_statistics(check_fused=False)`` only, as ``gptq_quantize.py:145-172``
+    uses it."""
+    zp_dtype = getattr(quant_args, "zp_dtype", None)
+    qa = resolve_args(quant_args)
+    res = gptq_quantize(module.weight, qa, hessian, module.weight_observer, blocksize, percdamp)
     final_dtype = module.weight.dtype
     q = {
         "weight": res.weight.reshape(module.weight.shape),
         "weight_scale": res.scale.to(dtype=final_dtype),
-        "weight_zero_point": res.zero_point.to(dtype=quant_args.zp_dtype),
+        "weight_zero_point": res.zero_point.to(dtype=zp_dtype if zp_dtype is not None else qa.zp_dtype),
     }
     if res.global_scale is not None:
         q["weight_global_scale"] = res.global_scale.to(dtype=final_dtype)
-    actorder = quant_args.actorder
-    if actorder == ActivationOrdering.GROUP and quant_args.strategy in (QuantizationStrategy.GROUP,
-                                                                        QuantizationStrategy.TENSOR_GROUP):
+    if qa.actorder == ActivationOrdering.GROUP and qa.strategy in _GROUPED:
         q["weight_g_idx"] = res.g_idx[torch.argsort(res.perm)]
     return res.loss, q

@@ -35,12 +35,15 @@ import time
 import torch
 
 from .calibration import initialize_module_for_quantization, initialize_observer, observe, update_qparams
+from .moe import expert_families
+from .observers import MemorylessMinMaxObserver, fuse_weight_observers
 from . import sparsegpt as sgpt
 from . import ops
-from .gptq import (_effective_actorder, accumulate_hessian, gptq_quantize, hessian_rows, make_empty_hessian,
-                   prepare_hessian)
+from .gptq import (_effective_actorder, accumulate_hessian, gptq_quantize, gptq_quantize_batched, hessian_rows,
+                   make_empty_hessian, prepare_hessian, prepare_hessians_batched)
 from .staging import DEFAULT_BUDGET, DEFAULT_TOKENS, HessianStage
-from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationScheme, preset_name_to_scheme
+from .quant_args import (ActivationOrdering, QuantizationArgs, QuantizationScheme, preset_name_to_scheme,
+                         resolve_args)
 
 logger = logging.getLogger("llmcompressor_amd")
 
@@ -60,6 +63,19 @@ def matches_target(name: str, type_name: str | None, patterns) -> bool:
 
 def _matches(name: str, module: torch.nn.Module, patterns) -> bool:
     return matches_target(name, type(module).__name__, patterns)
+
+
+def _update_parameter(module: torch.nn.Module, name: str, value: torch.Tensor) -> None:
+    """Writes ``value`` into the module's registered parameter ``name`` in
+    place, converted to that parameter's dtype (as the reference's
+    ``update_offload_parameter`` does at ``modifiers/gptq/base.py:600-601``:
+    an NVFP4 ``weight_global_scale`` stays fp32); a parameter of another
+    shape, or a missing one, is replaced by ``value``."""
+    p = getattr(module, name, None)
+    if isinstance(p, torch.Tensor) and p.shape == value.shape:
+        p.data.copy_(value)
+    else:
+        setattr(module, name, torch.nn.Parameter(value, requires_grad=False))
 
 
 class QuantizationModifier:
@@ -98,12 +114,16 @@ class QuantizationModifier:
     def on_initialize(self, model):
         self._modules = {}
         for name, m, sch in self.target_modules(model):
-            sch = QuantizationScheme(targets=sch.targets, weights=sch.weights.model_copy() if sch.weights else None,
+            w = None if sch.weights is None else resolve_args(sch.weights).model_copy()
+            sch = QuantizationScheme(targets=sch.targets, weights=w,
                                      input_activations=sch.input_activations, output_activations=sch.output_activations)
             self._resolve_actorder(sch)
             initialize_module_for_quantization(m, sch)
             initialize_observer(m, "weight")
             self._modules[m] = name
+        # q/k/v and gate/up NVFP4 observers share one global scale
+        # (modifiers/quantization/quantization/mixin.py:381-382)
+        fuse_weight_observers(model)
         return True
 
     def _resolve_actorder(self, sch):
@@ -140,7 +160,8 @@ class _SharedHessians:
 
     @staticmethod
     def _same_tensor(a, b) -> bool:
-        return b is not None and (a is b or (a.data_ptr() == b.data_ptr() and a.shape == b.shape
+        # empty tensors can share the null address: only the same object counts
+        return b is not None and (a is b or (a.numel() > 0 and a.data_ptr() == b.data_ptr() and a.shape == b.shape
                                              and a.stride() == b.stride() and a.dtype == b.dtype
                                              and a._version == b._version))
 
@@ -231,15 +252,32 @@ class _Staging:
 
 
 class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
+    """GPTQ over the targeted Linear modules (``modifiers/gptq/base.py``).
+
+    Beyond the reference's arguments: ``share_hessians`` (modules fed the
+    same tensor accumulate one Hessian), ``hessian_batch_tokens`` /
+    ``hessian_stage_bytes`` (rows of small calls are copied into device
+    buffers of 16384 rows and accumulated one long syrk at a time, while the
+    buffers of one modifier stay within 2 GiB by default) and
+    ``batch_experts``: the same-shaped projections of an MoE expert list
+    (``<experts>.<e>.gate_proj`` ...) keep their Hessians in one stacked
+    tensor, accumulate each forward's routed rows in one grouped syrk launch
+    (holding references to the rows of up to ``hessian_stage_bytes``) and,
+    with the default min-max observer and channel or group scales, are solved
+    together (one launch per solve step for all experts)."""
+
     def __init__(self, scheme=None, targets=("Linear",), ignore=("lm_head",), config_groups=None,
                  block_size: int = 128, dampening_frac: float | None = 0.01, actorder="static",
                  offload_hessians: bool = False, share_hessians: bool = True,
-                 hessian_batch_tokens: int = DEFAULT_TOKENS, hessian_stage_bytes: int = DEFAULT_BUDGET):
+                 hessian_batch_tokens: int = DEFAULT_TOKENS, hessian_stage_bytes: int = DEFAULT_BUDGET,
+                 batch_experts: bool = True):
         super().__init__(scheme, targets, ignore, config_groups)
         self.block_size = block_size
         self.dampening_frac = dampening_frac
         self.actorder = actorder
         self.offload_hessians = offload_hessians
+        self.batch_experts = batch_experts
+        self._families: dict = {}
         self._init_staging(hessian_batch_tokens, hessian_stage_bytes)
         # modules sharing an input also share one Cholesky chain per
         # activation ordering at compression
@@ -265,11 +303,41 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
         if w.actorder == ActivationOrdering.GROUP and w.strategy.value not in ("group", "tensor_group"):
             w.actorder = None
 
+    def on_initialize(self, model):
+        super().on_initialize(model)
+        self._families = {}
+        if self.batch_experts and not self.offload_hessians:
+            self._families = expert_families(model.named_modules(), set(self._modules),
+                                             lambda m: resolve_args(m.quantization_scheme.weights),
+                                             self.hessian_stage_bytes)
+        return True
+
+    @staticmethod
+    def _stacked_observation(module) -> bool:
+        """Min-max statistics per row: the stacked weights of a family are
+        observed at once, with the same result as each module's observer."""
+        if type(getattr(module, "weight_observer", None)) is not MemorylessMinMaxObserver:
+            return False
+        qa = resolve_args(module.quantization_scheme.weights)
+        return qa.strategy.value in ("channel", "group")
+
     def calibrate_module(self, module, args, _output):
         if getattr(self, "_hooks_disabled", False):   # a propagation pass of the sequential pipeline
             return
         inp = args[0]
         if self.share_hessians and self._shared(module, inp, self._modules.get):
+            return
+        fam = self._families.get(module)
+        if fam is not None:
+            H = fam.hessian(module)
+            if module not in self._num_samples:
+                self._hessians[module] = H
+                self._num_samples[module] = 0
+            x, added = hessian_rows(inp, module, H.device)
+            fam.add(module, x, added)
+            self._num_samples[module] += added
+            if self.share_hessians:
+                self._note_accumulated(module, inp, self._modules.get)
             return
         if module not in self._num_samples:
             dev = module.weight.device
@@ -299,6 +367,10 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
 
     def _flush(self, module):
         """Accumulates the rows still staged for ``module``'s Hessian."""
+        fam = self._families.get(module)
+        if fam is not None:
+            fam.flush()
+            return
         H = self._hessians.get(module)
         self._drop_stage(module, lambda rows, samples: self._accumulate(module, H, rows, samples))
 
@@ -312,24 +384,120 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
 
     def on_sequential_epoch_end(self, modules):
         modules = [m for m in modules if getattr(m, "quantization_scheme", None) is not None]
-        observe(modules, "weight")
+        # expert families observed as one stack at compression are skipped here
+        observe([m for m in modules if not (m in self._families and self._stacked_observation(m))], "weight")
         self.compress_modules()
 
     def compress_modules(self):
-        for leader, members in self._take_groups(self._modules.get).items():
+        groups = self._take_groups(self._modules.get)
+        done = self._compress_families(groups)
+        for leader, members in groups.items():
+            if leader in done:
+                continue
             self._flush(leader)
-            n = float(self._num_samples[leader].item())
+            n = float(self._num_samples[leader])
             H = self._hessians.pop(leader).to(leader.weight.device)
             prepared: dict = {}
             for module in members:
                 del self._num_samples[module]
+                if module in self._families and not module.weight_observer.has_statistics:
+                    observe(module, "weight")    # a family member solved on its own
                 self._compress_one(module, H, n, prepared if len(members) > 1 else None)
+        for fam in set(self._families.values()):
+            if fam.H is not None and not any(m in self._num_samples for m in fam.members):
+                fam.release()
+
+    def _family_roles(self, fam, leaders, groups):
+        """The modules of a batched family solve by role, [[gate_0, ...],
+        [up_0, ...]] (each leader's Hessian sharers in the same order), or
+        None when the family must be solved module by module: not every
+        member was called, sharers that do not form families of the same
+        slots and arguments, or observers whose statistics are not per row."""
+        if set(leaders) != set(fam.members):
+            return None
+        by_slot = [groups[m] for m in fam.members]
+        n_roles = len(by_slot[0])
+        if any(len(g) != n_roles for g in by_slot):
+            return None
+        qa = resolve_args(fam.members[0].quantization_scheme.weights)
+        roles = []
+        for r in range(n_roles):
+            mods = [g[r] for g in by_slot]
+            fr = self._families.get(mods[0])
+            if fr is None or any(self._families.get(m) is not fr or fr.slot[m] != i for i, m in enumerate(mods)):
+                return None
+            if resolve_args(mods[0].quantization_scheme.weights) != qa:
+                return None
+            if not all(self._stacked_observation(m) for m in mods):
+                return None
+            roles.append(mods)
+        return roles
+
+    def _compress_families(self, groups) -> set:
+        """Solves every expert family whose members are all pending in one
+        batched solve per role; returns the leaders done."""
+        leaders_of: dict = {}
+        for leader in groups:
+            fam = self._families.get(leader)
+            if fam is not None:
+                leaders_of.setdefault(fam, []).append(leader)
+        done = set()
+        for fam, leaders in leaders_of.items():
+            roles = self._family_roles(fam, leaders, groups)
+            if roles is None:
+                continue
+            t0 = time.perf_counter()
+            fam.flush()
+            qa = resolve_args(fam.members[0].quantization_scheme.weights)
+            ns = torch.tensor([float(self._num_samples[m]) for m in fam.members], dtype=torch.float32,
+                              device=fam.H.device)
+            prep = prepare_hessians_batched(fam.H, qa, ns, self.dampening_frac)
+            for mods in roles:
+                for m in mods:     # statistics from an earlier observe() are not used
+                    m.weight_observer.delete_statistics(check_fused=False)
+                res = gptq_quantize_batched(torch.stack([m.weight for m in mods]), qa, fam.H, num_samples=ns,
+                                            blocksize=self.block_size, percdamp=self.dampening_frac,
+                                            observer="memoryless_minmax", prepared=prep)
+                self._write_back(mods, res, qa)
+            dt = (time.perf_counter() - t0) / max(1, sum(len(r) for r in roles))
+            for mods in roles:
+                for m in mods:
+                    self.timings[self._modules[m]] = dt
+                    del self._num_samples[m]
+                    self._hessians.pop(m, None)
+            logger.info("Quantized %d modules of %s together, loss %.4f", sum(len(r) for r in roles), fam.key,
+                        sum(r.loss for r in res))
+            fam.release()
+            done.update(leaders)
+        return done
+
+    @staticmethod
+    def _write_back(mods, res, qa):
+        """Parameters of a batched solve written in a few multi-tensor copies."""
+        with torch.no_grad():
+            torch._foreach_copy_([m.weight.data for m in mods], [r.weight for r in res])
+            dt = mods[0].weight.dtype
+            scale = torch.stack([r.scale for r in res]).to(dt)
+            zp = torch.stack([r.zero_point for r in res]).to(qa.zp_dtype)
+            update = {"weight_scale": scale.unbind(0), "weight_zero_point": zp.unbind(0)}
+            if qa.actorder == ActivationOrdering.GROUP:
+                g_idx, perm = torch.stack([r.g_idx for r in res]), torch.stack([r.perm for r in res])
+                update["weight_g_idx"] = torch.gather(g_idx, 1, torch.argsort(perm, dim=1)).unbind(0)
+            for k, vals in update.items():
+                ps = [getattr(m, k, None) for m in mods]
+                if all(isinstance(p, torch.Tensor) and p.shape == v.shape for p, v in zip(ps, vals)):
+                    torch._foreach_copy_([p.data for p in ps], list(vals))
+                else:
+                    for m, v in zip(mods, vals):
+                        _update_parameter(m, k, v)
+        for m, r in zip(mods, res):
+            m.gptq_codes = r.codes
 
     def _compress_one(self, module, H, n, prepared):
         """GPTQ of one module; ``prepared`` caches the Cholesky chain of a
         shared Hessian per activation ordering."""
         name = self._modules[module]
-        qa = module.quantization_scheme.weights
+        qa = resolve_args(module.quantization_scheme.weights)
         t0 = time.perf_counter()
         prep = None
         if prepared is not None:
@@ -351,7 +519,7 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
             if qa.actorder == ActivationOrdering.GROUP:
                 update["weight_g_idx"] = res.g_idx[torch.argsort(res.perm)]
             for k, v in update.items():
-                setattr(module, k, torch.nn.Parameter(v, requires_grad=False))
+                _update_parameter(module, k, v)
         module.gptq_codes = res.codes
 
     def on_calibration_end(self):
@@ -362,6 +530,8 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
     def on_finalize(self):
         if self._num_samples:
             raise ValueError(f"Failed to compress {len(self._num_samples)} modules")
+        for fam in set(self._families.values()):
+            fam.release()
         return True
 
     def apply(self, model, batches):

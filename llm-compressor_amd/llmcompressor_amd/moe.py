@@ -14,6 +14,7 @@ grouped syrk launch over (expert, tile, token-split) work items.
 from __future__ import annotations
 
 import contextlib
+import re
 
 import torch
 
@@ -91,3 +92,173 @@ def expert_intermediate(hidden: torch.Tensor, rows: torch.Tensor, offsets: list[
     if not outs:
         return torch.empty((0, gate.shape[1]), dtype=hidden.dtype, device=hidden.device)
     return torch.cat(outs, 0).contiguous()
+
+
+class ExpertMLP(torch.nn.Module):
+    """One expert of a gated MoE MLP: ``down_proj(act(gate_proj(h)) *
+    up_proj(h))`` as separate ``nn.Linear`` modules, so that calibration
+    hooks see each projection (``modeling/moe/linear_experts.py:26-95``,
+    ``ExpertMLPWithGate``; its gate is applied to the concatenation
+    [gate, up], which multiplies the same two halves)."""
+
+    def __init__(self, hidden: int, intermediate: int, bias: bool = False, act=torch.nn.functional.silu,
+                 dtype=None, device=None):
+        super().__init__()
+        self.intermediate_size = intermediate
+        self.gate_proj = torch.nn.Linear(hidden, intermediate, bias=bias, dtype=dtype, device=device)
+        self.up_proj = torch.nn.Linear(hidden, intermediate, bias=bias, dtype=dtype, device=device)
+        self.down_proj = torch.nn.Linear(intermediate, hidden, bias=bias, dtype=dtype, device=device)
+        self.act = act
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(self.act(self.gate_proj(hidden_states)) * self.up_proj(hidden_states))
+
+
+class LinearExperts(torch.nn.ModuleList):
+    """The experts of an MoE layer as a list of ``ExpertMLP`` with the
+    reference's calibration forward (``modeling/moe/linear_experts.py:159-277``,
+    ``LinearExperts2D``): for each expert in index order its routed tokens
+    ``torch.where(one_hot(top_k_index)[..., e].T)`` (all tokens under
+    ``moe_calibration_context``, the outputs then taken at the routed rows),
+    weighted by their top-k weights and summed into the output with
+    ``index_add_``."""
+
+    def __init__(self, num_experts: int, hidden: int, intermediate: int, bias: bool = False,
+                 act=torch.nn.functional.silu, dtype=None, device=None):
+        super().__init__([ExpertMLP(hidden, intermediate, bias, act, dtype, device) for _ in range(num_experts)])
+        self.num_experts = num_experts
+        self.intermediate_size = intermediate
+
+    @classmethod
+    @torch.no_grad()
+    def from_stacked(cls, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor, act=torch.nn.functional.silu):
+        """Experts from stacked weights gate / up [E, I, H] and down [E, H, I]
+        (``copy_from_experts_module``, ``linear_experts.py:51-74``)."""
+        E, inter, hidden = gate.shape
+        self = cls(E, hidden, inter, act=act, dtype=gate.dtype, device=gate.device)
+        for e, expert in enumerate(self):
+            expert.gate_proj.weight.data = gate[e].contiguous()
+            expert.up_proj.weight.data = up[e].contiguous()
+            expert.down_proj.weight.data = down[e].contiguous()
+        return self
+
+    def forward(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
+                top_k_weights: torch.Tensor) -> torch.Tensor:
+        final = torch.zeros_like(hidden_states)
+        with torch.no_grad():
+            mask = torch.nn.functional.one_hot(top_k_index, self.num_experts).permute(2, 1, 0)
+        for e in range(self.num_experts):
+            top_k_pos, token_indices = torch.where(mask[e])
+            expert = self[e]
+            if get_calibrate_all_experts_flag():
+                out = expert(hidden_states)[token_indices]
+            else:
+                out = expert(hidden_states[token_indices])
+            weighted = out * top_k_weights[token_indices, top_k_pos, None]
+            final.index_add_(0, token_indices, weighted.to(final.dtype))
+        return final
+
+
+class ExpertFamily:
+    """Same-shaped modules of one expert list that share quantization
+    arguments (``experts.<e>.gate_proj`` for every e): their Hessians live
+    in one [E, d, d] tensor, and the rows their forward hooks receive are
+    held until a flush hands them, grouped by expert, to one grouped syrk
+    launch (instead of one accumulation per expert call).  Rows are held as
+    references to the hooks' inputs, up to ``budget`` bytes; a flush copies
+    them into one grouped buffer.  Repeated calls of one expert before a
+    flush go into the same group (another order of fp32 additions)."""
+
+    def __init__(self, key: str, members: list, budget: int):
+        self.key = key
+        self.members = list(members)
+        self.slot = {m: i for i, m in enumerate(self.members)}
+        self.budget = budget
+        self.H: torch.Tensor | None = None
+        self.samples = [0] * len(self.members)
+        self._parts: list = []      # (slot, call index, rows)
+        self._held = 0
+
+    def hessian(self, module) -> torch.Tensor:
+        """The member's [d, d] view of the family's Hessians (allocated with
+        the first call of any member)."""
+        if self.H is None:
+            w = self.members[0].weight
+            d = w.shape[1]
+            self.H = torch.zeros((len(self.members), d, d), dtype=torch.float32, device=w.device)
+        return self.H[self.slot[module]]
+
+    def add(self, module, rows: torch.Tensor, samples: int) -> None:
+        slot = self.slot[module]
+        self.samples[slot] += samples
+        if rows.shape[0] == 0:
+            return
+        nbytes = rows.numel() * rows.element_size()
+        if self._parts and self._held + nbytes > self.budget:
+            self.flush()
+        self._parts.append((slot, len(self._parts), rows))
+        self._held += nbytes
+
+    def flush(self) -> None:
+        """Accumulates the held rows: one grouped syrk over the experts."""
+        if not self._parts:
+            return
+        parts = sorted(self._parts, key=lambda p: (p[0], p[1]))
+        self._parts, self._held = [], 0
+        counts = [0] * len(self.members)
+        for slot, _, rows in parts:
+            counts[slot] += rows.shape[0]
+        offsets = [0]
+        for c in counts:
+            offsets.append(offsets[-1] + c)
+        dtypes = {rows.dtype for _, _, rows in parts}
+        dt = dtypes.pop() if len(dtypes) == 1 else torch.float32
+        x = torch.cat([rows.to(dt) for _, _, rows in parts]) if len(parts) > 1 else parts[0][2]
+        ops.hessian_grouped_syrk_(self.H, x, None, offsets, alpha=2.0)
+
+    def release(self) -> None:
+        self._parts, self._held = [], 0
+        self.H = None
+        self.samples = [0] * len(self.members)
+
+
+_INDEXED = re.compile(r"(?:^|\.)(\d+)(?=\.|$)")
+
+
+def expert_families(named_modules, targets, args_of, budget: int) -> dict:
+    """{module: ExpertFamily} for the ``targets`` among ``named_modules``
+    that belong to expert lists: modules named ``<list>.<e>.<rest>`` where
+    ``<list>`` is a module with an integer ``num_experts`` or whose name ends
+    in ``experts``, grouped by (``<list>``, ``<rest>``) when at least two
+    share one weight shape, dtype, device and quantization arguments
+    (``args_of(module)``)."""
+    modules = dict(named_modules)
+    groups: dict = {}
+    for name, m in modules.items():
+        if m not in targets:
+            continue
+        found = list(_INDEXED.finditer(name))
+        if not found or not isinstance(getattr(m, "weight", None), torch.Tensor) or m.weight.dim() != 2:
+            continue
+        f = found[-1]
+        parent = name[:f.start()]
+        container = modules.get(parent)
+        is_experts = parent.split(".")[-1] == "experts" or isinstance(getattr(container, "num_experts", None), int)
+        if not is_experts:
+            continue
+        w = m.weight
+        key = (parent, name[f.end():], tuple(w.shape), w.dtype, str(w.device))
+        groups.setdefault(key, []).append((int(f.group(1)), m))
+    out: dict = {}
+    for key, items in groups.items():
+        if len(items) < 2:
+            continue
+        items.sort(key=lambda t: t[0])
+        members = [m for _, m in items]
+        a0 = args_of(members[0])
+        if any(args_of(m) != a0 for m in members[1:]):
+            continue
+        fam = ExpertFamily(f"{key[0]}.*{key[1]}" if key[0] else f"*{key[1]}", members, budget)
+        for m in members:
+            out[m] = fam
+    return out

@@ -19,11 +19,53 @@ import torch
 
 import logging
 import math
+import weakref
 
 from . import ops
-from .quant_args import QuantizationArgs, QuantizationStrategy, QuantizationType
+from .quant_args import QuantizationArgs, QuantizationStrategy, QuantizationType, resolve_args
 
 ACTIVATION_OBS = ("input", "output", "q", "k", "v")
+
+# Layer names whose weight observers share one NVFP4 global scale
+# (``observers/helpers.py:161-174``): the modules a runtime fuses into one
+# GEMM (gate / up, q / k / v, DeepSeek's fused q_a / kv_a, w1 / w3 experts).
+FUSED_LAYER_NAMES = [
+    ("gate_proj", "up_proj"),
+    ("q_proj", "k_proj", "v_proj"),
+    ("q_a_proj", "kv_a_proj_with_mqa"),
+    ("w1", "w3"),
+]
+
+
+class _FusionGroup:
+    """Weight observers of one fused layer set (``observers/fusion.py:17-105``
+    behaviour): each member's NVFP4 global scale comes from the statistics of
+    every member, a member without statistics observes its module's weight
+    first (modules held by weak reference), and statistics are deleted only
+    once every member has asked for its qparams."""
+
+    def __init__(self, pairs):
+        self.members = [(obs, weakref.ref(mod)) for obs, mod in pairs]
+        self.done: set[int] = set()
+
+    def statistics(self, first):
+        """[first's (min, max)] + the other members' (min, max), observing
+        each member that holds none."""
+        order = [first] + [o for o, _ in self.members if o is not first]
+        refs = {id(o): r for o, r in self.members}
+        for obs in order:
+            if not obs.has_statistics:
+                mod = refs[id(obs)]()
+                assert mod is not None, "Fused module has been garbage collected before its weight was observed"
+                obs(mod.weight)
+        return [(o.min_vals, o.max_vals) for o in order]
+
+    def release(self, obs) -> None:
+        self.done.add(id(obs))
+        if len(self.done) == len(self.members):
+            self.done.clear()
+            for o, _ in self.members:
+                o.delete_statistics(check_fused=False)
 
 
 class Observer(torch.nn.Module):
@@ -33,10 +75,11 @@ class Observer(torch.nn.Module):
     def __init__(self, base_name: str, args: QuantizationArgs, **observer_kwargs):
         super().__init__()
         self.base_name = base_name
-        self.args = args
+        self.args = resolve_args(args)
         self.args.observer_kwargs = dict(self.args.observer_kwargs or {})
         self.args.observer_kwargs.update(observer_kwargs)
         self._observed_dtype: torch.dtype | None = None
+        self._fusion: _FusionGroup | None = None
 
     # -- registry (compressed-tensors RegistryMixin semantics)
     @classmethod
@@ -62,7 +105,16 @@ class Observer(torch.nn.Module):
     def is_weight_obs(self) -> bool:
         return self.base_name == "weight"
 
+    @property
+    def is_fused(self) -> bool:
+        return self._fusion is not None
+
     def delete_statistics(self, check_fused: bool = True) -> None:
+        """Drop the statistics; with ``check_fused`` a fused member's are kept
+        until every member of its group has asked (``fusion.py:82-105``)."""
+        if check_fused and self._fusion is not None:
+            self._fusion.release(self)
+            return
         for a in self._stats_attrs:
             if hasattr(self, a):
                 delattr(self, a)
@@ -121,11 +173,17 @@ class Observer(torch.nn.Module):
             zp = torch.zeros(scale.shape, dtype=a.zp_dtype, device=scale.device)
             out = {"scale": scale.to(torch.bfloat16), "zero_point": zp, "global_scale": None}
         elif a.strategy == QuantizationStrategy.TENSOR_GROUP:
-            # NVFP4: the global scale from this observer's statistics (a fusion
-            # group of one module), fp8 group scales (observers/base.py:78-123)
+            # NVFP4: the global scale from the absmax over this observer's and
+            # its fused members' statistics, fp8 group scales
+            # (observers/base.py:78-123)
             if a.type != QuantizationType.FLOAT or a.num_bits != 4 or not a.symmetric:
                 raise NotImplementedError("tensor_group quantization is symmetric fp4 (NVFP4)")
-            gs, scale = ops.nvfp4_qparams(self.min_vals, self.max_vals, dt)
+            stats = self._fusion.statistics(self) if self._fusion is not None else [(self.min_vals, self.max_vals)]
+            n_own = self.min_vals.numel()
+            mn = torch.cat([m.reshape(-1).to(self.min_vals.dtype) for m, _ in stats])
+            mx = torch.cat([m.reshape(-1).to(self.max_vals.dtype) for _, m in stats])
+            gs, scale = ops.nvfp4_qparams(mn, mx, dt)
+            scale = scale[:n_own].reshape(self.min_vals.shape)
             zp = torch.zeros(scale.shape, dtype=a.zp_dtype, device=scale.device)
             out = {"scale": scale, "zero_point": zp, "global_scale": gs}
         else:
@@ -404,3 +462,38 @@ class IMatrixMSEObserver(_MSEObserver):
 
     def update_statistics_from_observed(self, mn, mx):
         self.min_vals, self.max_vals = mn, mx
+
+
+def fuse_weight_observers(model: torch.nn.Module) -> None:
+    """Link the tensor-group (NVFP4) weight observers of each fused layer set
+    in ``FUSED_LAYER_NAMES`` so that they share one global scale
+    (``observers/helpers.py:177-215``).  A set is linked when a submodule
+    holds all of its names; members that are None are skipped, and a set
+    mixing tensor-group observers with missing or other observers fails the
+    same assertions as the reference."""
+    for sub in model.modules():
+        for names in FUSED_LAYER_NAMES:
+            if not all(hasattr(sub, n) for n in names):
+                continue
+            only_obs = only_tensor_group = True
+            pairs = []
+            for layer in (getattr(sub, n) for n in names):
+                if layer is None:
+                    continue
+                obs = getattr(layer, "weight_observer", None)
+                if obs is None:
+                    only_obs = False
+                    continue
+                if obs.args.strategy != QuantizationStrategy.TENSOR_GROUP:
+                    only_tensor_group = False
+                    continue
+                pairs.append((obs, layer))
+            if not pairs:
+                continue
+            start = f"Some layers in fused group: {names} have"
+            end = ", need all fused layers to have same quantization"
+            assert only_obs, f"{start} no weight observer{end}"
+            assert only_tensor_group, f"{start} non-TENSOR_GROUP quantization{end}"
+            group = _FusionGroup(pairs)
+            for obs, _ in pairs:
+                obs._fusion = group

@@ -116,6 +116,48 @@ class QuantizationArgs:
         return copy.deepcopy(self)
 
 
+# The members of compressed-tensors' ``QuantizationArgs`` this package reads
+# from a caller's arguments object; ``resolve_args`` reads nothing else.
+CT_ARG_FIELDS = ("num_bits", "type", "symmetric", "group_size", "strategy", "block_structure", "dynamic",
+                 "actorder", "scale_dtype", "zp_dtype", "observer", "observer_kwargs")
+
+
+def _plain(v):
+    """An enum member's value (compressed-tensors' str enums, or any other
+    enum class), else the value itself."""
+    return v.value if isinstance(v, Enum) else v
+
+
+def resolve_args(args) -> QuantizationArgs:
+    """This package's ``QuantizationArgs`` for ``args``.
+
+    ``args`` is returned as it is when it already is one; any other object
+    (compressed-tensors' ``QuantizationArgs``, as the reference hands to
+    ``quantize_weight`` at ``modifiers/gptq/base.py:591-597``, or a namespace
+    with the same field names) is read through the fields in
+    ``CT_ARG_FIELDS`` only, enum members by their values, into a new
+    dataclass that derives the integer / float range and the MX layout from
+    them.  Missing fields take compressed-tensors' defaults.  The caller's
+    object is never modified."""
+    if isinstance(args, QuantizationArgs):
+        return args
+    kw = {}
+    for f in CT_ARG_FIELDS:
+        if hasattr(args, f):
+            kw[f] = getattr(args, f)
+    for f in ("type", "strategy", "dynamic", "observer"):
+        if f in kw:
+            kw[f] = _plain(kw[f])
+    if "actorder" in kw:
+        kw["actorder"] = _plain(kw["actorder"])
+    if kw.get("block_structure") is not None:
+        kw["block_structure"] = [int(v) for v in kw["block_structure"]]
+    kw["observer_kwargs"] = dict(kw.get("observer_kwargs") or {})
+    if kw.get("zp_dtype", 0) is None:
+        del kw["zp_dtype"]     # filled by type and width, as compressed-tensors does
+    return QuantizationArgs(**kw)
+
+
 @dataclass
 class QuantizationScheme:
     targets: list[str] = field(default_factory=lambda: ["Linear"])

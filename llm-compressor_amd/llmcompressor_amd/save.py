@@ -45,7 +45,7 @@ import shutil
 import torch
 
 from . import ops
-from .quant_args import QuantizationArgs, QuantizationScheme, QuantizationStrategy, QuantizationType
+from .quant_args import QuantizationArgs, QuantizationScheme, QuantizationStrategy, QuantizationType, resolve_args
 
 __all__ = ["infer_quantization_format", "compress_module", "quantization_config", "save_compressed",
            "QuantConfigParser", "Int8Packer"]
@@ -59,11 +59,13 @@ def infer_quantization_format(scheme: QuantizationScheme | None) -> str | None:
     w = getattr(scheme, "weights", None)
     if w is None:
         return None
+    w = resolve_args(w)
     if w.is_mx:
         return "mxfp4-pack-quantized"
     if w.type == QuantizationType.FLOAT and w.num_bits == 4 and w.strategy == QuantizationStrategy.TENSOR_GROUP:
         return "nvfp4-pack-quantized"
-    a = scheme.input_activations
+    a = getattr(scheme, "input_activations", None)
+    a = None if a is None else resolve_args(a)
     if w.type == QuantizationType.INT:
         if a is None or w.num_bits < 8:
             return "pack-quantized"
@@ -84,7 +86,7 @@ def compress_module(module: torch.nn.Module, fmt: str | None = None) -> dict[str
     """The tensors ``fmt`` stores for ``module``'s weight (names without the
     module prefix), computed on the module's GPU by this package's kernels."""
     scheme = module.quantization_scheme
-    w = scheme.weights
+    w = resolve_args(scheme.weights)
     fmt = fmt or infer_quantization_format(scheme)
     if fmt == "mxfp4-pack-quantized":
         codes, e8 = ops.mxfp4_quantize_pack(module.weight)
@@ -95,10 +97,9 @@ def compress_module(module: torch.nn.Module, fmt: str | None = None) -> dict[str
             raise ValueError("nvfp4-pack-quantized needs the module's weight_global_scale")
         scale = module.weight_scale.data
         packed = ops.fp4_quantize_pack(module.weight, scale, w.group_size, gs.data)
-        # the group scales are fp8 values held in a wider dtype: the cast is exact
-        # the global scale is written as the module holds it (fp32 after
-        # calibration, the weight dtype after GPTQ), as a parameter the
-        # compressor passes through
+        # the group scales are fp8 values held in a wider dtype: the cast is
+        # exact; the global scale is written as the module holds it (its fp32
+        # parameter), as a parameter the compressor passes through
         return {"weight_packed": packed, "weight_scale": scale.to(torch.float8_e4m3fn),
                 "weight_global_scale": gs.data.reshape(1)}
     out = {"weight_scale": module.weight_scale.data}
@@ -129,6 +130,7 @@ def compress_module(module: torch.nn.Module, fmt: str | None = None) -> dict[str
 def _args_dict(a: QuantizationArgs | None):
     if a is None:
         return None
+    a = resolve_args(a)
     dt = lambda t: None if t is None else str(t).replace("torch.", "")  # noqa: E731
     return {"num_bits": a.num_bits, "type": a.type.value, "symmetric": a.symmetric, "group_size": a.group_size,
             "strategy": a.strategy.value, "block_structure": a.block_structure, "dynamic": a.dynamic,

@@ -92,6 +92,10 @@ class OMinMax:
         self.kind, self.base_name, self.args = kind, base_name, args
         self.avg = args.observer_kwargs.get("averaging_constant", averaging_constant)
         self.min_vals = self.max_vals = None
+        # (min, max) statistics of the other members of a fused layer set
+        # (q/k/v, gate/up): the tensor-group global scale is taken over all
+        # of them (observers/base.py:78-96, observers/fusion.py:58-80)
+        self.fused_stats: list = []
 
     @property
     def has_statistics(self):
@@ -122,7 +126,7 @@ class OMinMax:
         else:
             gs = None
             if self.args.strategy == "tensor_group" and not self.args.is_mx:
-                gs = global_scale_from_stats([(self.min_vals, self.max_vals)])
+                gs = global_scale_from_stats([(self.min_vals, self.max_vals)] + list(self.fused_stats))
             s, z = calculate_qparams(self.min_vals, self.max_vals, self.args, gs, mx_rule)
             out = {"scale": s, "zero_point": z, "global_scale": gs}
         self.min_vals = self.max_vals = None

@@ -26,6 +26,14 @@ seed on 8 cores).
 layer with a Hessian from 4096 tokens, quantized by the oracle on its own
 fp32 Hessian and on the same Hessian summed in fp64 and rounded to fp32.
 Float codes compare as signed grid positions.
+
+``--configs [seeds...]`` runs the third study at two configurations' own
+shapes: the W8A8 weights (14336 x 4096 int8 per channel, actorder=weight,
+Hessian from 4 x 2048 tokens) and the Llama-3-8B down projection (4096 x
+14336 W4A16 g128, actorder=weight, 8 x 2048 tokens); each quantized by the
+oracle and again with the flip-identity chain and with the fp64 chain.
+Longer rows and finer grids give a rounding boundary more chances per row,
+so more rows diverge than at 4096 x 4096 int4 (several minutes on 8 cores).
 """
 from __future__ import annotations
 
@@ -144,8 +152,33 @@ def formats(seeds):
         print(json.dumps({"seed": seed, **row}), flush=True)
 
 
+def configs(seeds):
+    cases = {"w8a8-14336x4096": (14336, 4096, 4, OArgs(num_bits=8, strategy="channel", actorder="weight")),
+             "down-4096x14336": (4096, 14336, 8, OArgs(num_bits=4, strategy="group", group_size=128,
+                                                        actorder="weight"))}
+    for seed in seeds:
+        for name, (rows, cols, samples, oa) in cases.items():
+            W = (torch.randn(rows, cols, generator=torch.Generator().manual_seed(seed)) * 0.02).to(torch.bfloat16)
+            X = workloads.heavy_tailed_activations((samples, 2048, cols), seed=seed + 1)
+            H, n = og.accumulate_hessian(X, og.make_empty_hessian(cols), torch.zeros(()))
+            H = og.normalise_hessian(H, n)
+            del X
+            orig = og.cholesky_chain
+            base = og.quantize_weight(W, oa, H, return_codes=True)[2]["codes"]
+            row = {}
+            for chain_name, ch in (("flip_chain", flip_chain), ("fp64_chain", fp64_chain)):
+                og.cholesky_chain = ch
+                try:
+                    row[chain_name] = spread(og.quantize_weight(W, oa, H, return_codes=True)[2]["codes"], base)
+                finally:
+                    og.cholesky_chain = orig
+            print(json.dumps({"seed": seed, "config": name, "rows": rows, **row}), flush=True)
+
+
 if __name__ == "__main__":
-    if sys.argv[1:2] == ["--formats"]:
+    if sys.argv[1:2] == ["--configs"]:
+        configs([int(s) for s in sys.argv[2:]] or [4, 9])
+    elif sys.argv[1:2] == ["--formats"]:
         formats([int(s) for s in sys.argv[2:]] or [41, 43, 45])
     else:
         main([int(s) for s in sys.argv[1:]] or [0, 1, 2, 3])

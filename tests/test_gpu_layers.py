@@ -14,7 +14,10 @@
 * The Cholesky chain at d = 14336 (the Llama-3-8B down projection) against the
   oracle's three-call chain on the same Hessian.
 * One batched solve of 128 experts of 768 x 2048 (an MoE gate/up projection)
-  against oracle solves of sampled experts.
+  and of 2048 x 768 (the down projection) against oracle solves of sampled
+  experts.
+* NVFP4 through GPTQModifier on a Llama-shaped layer: q/k/v and gate/up
+  share their global scales, as the oracle computes them.
 
 GPTQ code bars as in test_gpu_parity.py's end-to-end tests.
 """
@@ -26,6 +29,8 @@ from llmcompressor_amd import GPTQModifier, gptq, ops
 from llmcompressor_amd.staging import HessianStage
 from llmcompressor_amd.quant_args import QuantizationArgs
 from oracle import gptq as og
+from oracle.fake_quant import signed_grid_index
+from oracle.observers import OMinMax, global_scale_from_stats
 from oracle.qargs import OArgs
 from parity_util import code_agreement, code_bar
 
@@ -97,16 +102,43 @@ class LlamaLayer(torch.nn.Module):
         return x + self.down_proj(F.silu(self.gate_proj(h)) * self.up_proj(h))
 
 
-def test_decoder_layer_gptq_modifier_vs_oracle(dev):
-    say("decoder layer (hidden 1024, inter 8192) through GPTQModifier vs the oracle")
-    layer = LlamaLayer().to(dev)
-    W0 = {n: m.weight.detach().cpu().clone() for n, m in layer.named_children()}
-    seen = {n: [] for n in W0}
+def _modifier_hessian(xs, dev, name):
+    """The Hessian GPTQModifier accumulated from the inputs ``xs`` (same
+    kernel, rows and staged calls: the same bits), on the host, checked
+    against the oracle's to 1e-5: (H upper, num_samples, relative error)."""
+    cols = xs[0].shape[-1]
+    lin = torch.nn.Linear(cols, 1, bias=False, device=dev)
+    Hg, ng = gptq.make_empty_hessian(lin), torch.zeros((), device=dev)
+    Ho, no = og.make_empty_hessian(cols), torch.zeros(())
+    stage = HessianStage()
+    for x in xs:
+        rows, added = gptq.hessian_rows(x, lin, dev)
+        ng += added
+        stage.add(rows, added, lambda r, _s: ops.hessian_syrk_(Hg, r, alpha=2.0))
+        Ho, no = og.accumulate_hessian(x, Ho, no)
+    stage.flush(lambda r, _s: ops.hessian_syrk_(Hg, r, alpha=2.0))
+    Hg = Hg.cpu()
+    assert float(ng) == float(no)
+    r = rel_fro(torch.triu(Hg), torch.triu(Ho))
+    assert r <= 1e-5, (name, r)
+    return Hg, float(no), r
+
+
+def _capture_inputs(layer):
+    seen = {n: [] for n, _ in layer.named_children()}
 
     def capture(name):
         return lambda mod, args: seen[name].append(args[0].detach().cpu())
 
     hooks = [m.register_forward_pre_hook(capture(n)) for n, m in layer.named_children()]
+    return seen, hooks
+
+
+def test_decoder_layer_gptq_modifier_vs_oracle(dev):
+    say("decoder layer (hidden 1024, inter 8192) through GPTQModifier vs the oracle")
+    layer = LlamaLayer().to(dev)
+    W0 = {n: m.weight.detach().cpu().clone() for n, m in layer.named_children()}
+    seen, hooks = _capture_inputs(layer)
     batches = [_gpu_heavy((2, 2048, 1024), 100 + b, dev) for b in range(4)]
     mod = GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=())   # actorder static -> weight
     mod.apply(layer, batches)
@@ -115,28 +147,76 @@ def test_decoder_layer_gptq_modifier_vs_oracle(dev):
         h.remove()
     oa = OArgs(num_bits=4, strategy="group", group_size=128, actorder="weight")
     for name, m in layer.named_children():
-        xs = seen[name]
-        cols = xs[0].shape[-1]
-        # the GPU Hessian the modifier accumulated (same kernel, rows and
-        # staged calls: the same bits)
-        lin = torch.nn.Linear(cols, 1, bias=False, device=dev)
-        Hg, ng = gptq.make_empty_hessian(lin), torch.zeros((), device=dev)
-        Ho, no = og.make_empty_hessian(cols), torch.zeros(())
-        stage = HessianStage()
-        for x in xs:
-            rows, added = gptq.hessian_rows(x, lin, dev)
-            ng += added
-            stage.add(rows, added, lambda r, _s: ops.hessian_syrk_(Hg, r, alpha=2.0))
-            Ho, no = og.accumulate_hessian(x, Ho, no)
-        stage.flush(lambda r, _s: ops.hessian_syrk_(Hg, r, alpha=2.0))
-        Hg = Hg.cpu()
-        assert float(ng) == float(no) == 8.0
-        r = rel_fro(torch.triu(Hg), torch.triu(Ho))
-        assert r <= 1e-5, (name, r)
-        _, out_o, ex = og.quantize_weight(W0[name], oa, _full(Hg) / float(no), return_codes=True)
+        Hg, no, r = _modifier_hessian(seen[name], dev, name)
+        assert no == 8.0
+        _, out_o, ex = og.quantize_weight(W0[name], oa, _full(Hg) / no, return_codes=True)
         assert torch.equal(m.weight_scale.detach().cpu(), out_o["weight_scale"]), name
         _check_codes(f"{name} {tuple(W0[name].shape)} H rel {r:.2e}", m.gptq_codes, ex["codes"], W0[name],
-                     m.weight.detach(), out_o["weight"], xs[0][:1])
+                     m.weight.detach(), out_o["weight"], seen[name][0][:1])
+
+
+FUSED = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))
+
+
+def test_decoder_layer_nvfp4_fused_global_scales_vs_oracle(dev):
+    """NVFP4 (tensor-group 16, fp8 group scales, one global scale) through
+    GPTQModifier on a Llama-shaped layer: q/k/v and gate/up share one global
+    scale each (observers/fusion.py:17-105, observers/helpers.py:161-215,
+    wired at modifiers/quantization/quantization/mixin.py:381-382; the
+    reference's test_gptq_quantize.py:179-213 asserts the equalities), equal
+    to the oracle's generate_gparam over the group's combined statistics,
+    rounded to bf16 as quantize_weight returns it and held in the fp32
+    parameter; o and down keep their own.  Codes pass the bar against oracle
+    solves with the fused global scale."""
+    say("decoder layer NVFP4 through GPTQModifier: fused global scales")
+    layer = LlamaLayer(hidden=512, heads=8, kv_heads=2, inter=1536, seed=19).to(dev)
+    with torch.no_grad():   # members of one set with different ranges
+        layer.k_proj.weight.mul_(3)
+        layer.up_proj.weight.mul_(2)
+    W0 = {n: m.weight.detach().cpu().clone() for n, m in layer.named_children()}
+    seen, hooks = _capture_inputs(layer)
+    batches = [_gpu_heavy((2, 1024, 512), 200 + b, dev) for b in range(2)]
+    GPTQModifier(scheme="NVFP4A16", targets=("Linear",), ignore=()).apply(layer, batches)
+    torch.cuda.synchronize()
+    for h in hooks:
+        h.remove()
+    E4 = torch.float8_e4m3fn
+    oa = OArgs(num_bits=4, type="float", strategy="tensor_group", group_size=16, scale_dtype=E4,
+               actorder="weight")
+    stats = {}
+    for n, w in W0.items():
+        o = OMinMax("memoryless_minmax", "weight", oa)
+        o(w)
+        stats[n] = (o.min_vals, o.max_vals)
+    gs = {n: getattr(layer, n).weight_global_scale for n in W0}
+    assert all(v.dtype == torch.float32 and v.shape == (1,) for v in gs.values())
+    group_of = {n: grp for grp in FUSED for n in grp}
+    for n in W0:
+        grp = group_of.get(n, (n,))
+        want = global_scale_from_stats([stats[m] for m in grp]).to(torch.bfloat16).float()
+        assert float(gs[n]) == float(want), n
+        assert float(gs[n]) == float(gs[grp[0]]), n
+    assert float(gs["q_proj"]) != float(gs["gate_proj"])
+    # fused scales differ from what each member alone would get
+    own_k = global_scale_from_stats([stats["k_proj"]]).to(torch.bfloat16).float()
+    own_q = global_scale_from_stats([stats["q_proj"]]).to(torch.bfloat16).float()
+    assert float(own_q) != float(gs["q_proj"]) and float(own_k) == float(gs["q_proj"])
+    for name, m in layer.named_children():
+        Hg, no, r = _modifier_hessian(seen[name], dev, name)
+        obs = OMinMax("memoryless_minmax", "weight", oa)
+        obs(W0[name])
+        obs.fused_stats = [stats[o] for o in group_of.get(name, (name,)) if o != name]
+        _, out_o, ex = og.quantize_weight(W0[name], oa, _full(Hg) / no, observer=obs, return_codes=True)
+        assert torch.equal(m.weight_scale.detach().cpu().float(), out_o["weight_scale"].float()), name
+        gi = signed_grid_index(m.gptq_codes.cpu().to(torch.int32), oa)
+        gio = signed_grid_index(ex["codes"], oa)
+        st = code_agreement(gi, gio)
+        Xf = seen[name][0][:1].reshape(-1, W0[name].shape[1]).float()
+        e_gpu = (Xf @ (W0[name].float() - m.weight.detach().cpu().float()).t()).norm().item()
+        e_ora = (Xf @ (W0[name].float() - out_o["weight"].float()).t()).norm().item()
+        say(f"  {name}: gs {float(gs[name]):.6g} {st} err {e_gpu:.6g} vs {e_ora:.6g}")
+        assert code_bar(st, W0[name].shape[0]), name
+        assert abs(e_gpu - e_ora) <= 0.005 * e_ora, name
 
 
 def test_hinv_d14336_vs_oracle_chain(dev):
@@ -159,8 +239,11 @@ def test_hinv_d14336_vs_oracle_chain(dev):
     assert torch.equal(hinv, torch.triu(hinv))
 
 
-def test_moe_batched_solve_128_experts_vs_oracle(dev):
-    B, rows, cols, tok = 128, 768, 2048, 1024
+@pytest.mark.parametrize("rows,cols,tok", [(768, 2048, 1024), (2048, 768, 512)], ids=["gate_up", "down"])
+def test_moe_batched_solve_128_experts_vs_oracle(dev, rows, cols, tok):
+    """One batched solve of 128 experts of an MoE projection: gate / up
+    (768 x 2048) and down (2048 x 768, the 262144-row batch)."""
+    B = 128
     say(f"batched GPTQ of {B} experts {rows}x{cols} vs oracle solves of sampled experts")
     g = torch.Generator(device=dev).manual_seed(6)
     W = (torch.randn(B, rows, cols, generator=g, device=dev) * 0.02).to(torch.bfloat16)

@@ -209,3 +209,106 @@ def test_shared_hessians_divergence_raises(dev):
     with pytest.raises(RuntimeError, match="share_hessians=False"):
         _gptq().apply(model, batches)
     GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), share_hessians=False).apply(ref, batches)
+
+
+def test_pipeline_with_propagation_vs_oracle_loop(dev):
+    """pipelines/sequential/pipeline.py:136-178 against an oracle loop: per
+    layer the oracle runs the layer's forward on the CPU with its original
+    weights and accumulates every module's Hessian from the inputs that
+    forward gives it (calibration pass), solves each module with the
+    oracle's GPTQ (compression), then runs the layer again with the
+    compressed weights to make the next layer's inputs (propagation).  The
+    propagation uses the GPU's compressed weights, whose codes pass the bar
+    against the oracle's (so later layers compare the pipeline's order, not
+    the cascades of a few flipped codes); the model is fp32 so that the
+    CPU's forward and the GPU's agree to fp32 rounding.  Every module of both
+    layers: the Hessian the pipeline's modifier solved is within 1e-5 of the
+    oracle's, the codes pass the bar and the scales are equal.  Layer 2's
+    inputs are the compressed layer 1's outputs, not the original layer's."""
+    from oracle import gptq as og
+    from oracle.qargs import OArgs
+    from parity_util import code_agreement, code_bar
+
+    say("pipeline propagate_error=True vs an oracle calibrate / compress / propagate loop")
+    torch.manual_seed(0)
+    model = Toy(n=2).to(dev)
+    for p in model.parameters():
+        p.data.mul_(0.5)
+    batches = [workloads.heavy_tailed_activations((2, 128, 256), seed=60 + s).float().to(dev) for s in range(4)]
+    cpu_layers = [copy.deepcopy(l).cpu() for l in model.layers]
+    mod = _gptq()
+    solved = {}
+    compress_one = mod._compress_one
+
+    def spy(module, H, n, prepared):
+        solved[module] = (torch.triu(H).cpu(), float(n))
+        return compress_one(module, H, n, prepared)
+
+    mod._compress_one = spy
+    sequential_calibrate(model, model.layers, batches, mod, propagate_error=True)
+
+    oa = OArgs(num_bits=4, strategy="group", group_size=128, actorder="weight")
+    scale = torch.full((256,), 0.5)
+    xs = [b.cpu() for b in batches]
+    names = ("q", "o", "up", "gate", "down")
+    for li, (layer, ref) in enumerate(zip(model.layers, cpu_layers)):
+        seen = {n: [] for n in names}
+        hooks = [getattr(ref, n).register_forward_pre_hook(
+            lambda m, a, _n=n: seen[_n].append(a[0].detach().clone())) for n in names]
+        with torch.no_grad():
+            for x in xs:                              # calibration pass, original weights
+                ref(x, scale=scale)
+        for h in hooks:
+            h.remove()
+        for n in names:
+            m = getattr(layer, n)
+            Ho, no = og.make_empty_hessian(m.weight.shape[1]), torch.zeros(())
+            for x in seen[n]:
+                Ho, no = og.accumulate_hessian(x, Ho, no)
+            Hg, ng = solved[m]
+            assert ng == float(no) == 8.0
+            r = ((Hg.double() - torch.triu(Ho).double()).norm() / torch.triu(Ho).double().norm()).item()
+            W0 = getattr(ref, n).weight.detach()
+            _, out_o, ex = og.quantize_weight(W0, oa, og.normalise_hessian(Ho, no), return_codes=True)
+            st = code_agreement(m.gptq_codes.cpu().to(torch.int32), ex["codes"])
+            Xf = torch.cat([x.reshape(-1, x.shape[-1]) for x in seen[n]])[:512]
+            e_gpu = (Xf @ (W0 - m.weight.detach().cpu()).t()).norm().item()
+            e_ora = (Xf @ (W0 - out_o["weight"]).t()).norm().item()
+            say(f"  layer {li} {n}: H rel {r:.2e} {st} err {e_gpu:.6g} vs {e_ora:.6g}")
+            assert r <= 1e-5, (li, n, r)
+            assert torch.equal(m.weight_scale.detach().cpu(), out_o["weight_scale"]), (li, n)
+            assert code_bar(st, W0.shape[0]), (li, n)
+            assert abs(e_gpu - e_ora) <= 0.005 * e_ora, (li, n)
+        with torch.no_grad():
+            plain = [ref(x, scale=scale) for x in xs]
+            for n in names:                           # propagation pass, compressed weights
+                getattr(ref, n).weight.copy_(getattr(layer, n).weight.detach().cpu())
+            xs_next = [ref(x, scale=scale) for x in xs]
+        d_q = max(((a - b).norm() / b.norm()).item() for a, b in zip(plain, xs_next))
+        say(f"  layer {li}: compressed vs original outputs differ by {d_q:.3e} (relative)")
+        assert d_q > 1e-3   # the next layer's Hessians tell the two apart by far more than 1e-5
+        xs = xs_next
+
+
+def test_offload_hessians_equals_on_device(dev):
+    """offload_hessians=True (modifiers/gptq/base.py:664-674): the Hessians
+    wait in host memory between calls and are moved to the device for each
+    accumulation and for the solve; the weights equal those of on-device
+    accumulation of the same calls (hessian_batch_tokens=0: one syrk per
+    call, as the offloaded path runs)."""
+    say("offload_hessians=True vs on-device accumulation")
+    model, batches = _setup(dev)
+    ref = copy.deepcopy(model)
+    GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), hessian_batch_tokens=0).apply(ref, batches)
+    mod = GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), offload_hessians=True)
+    where = set()
+    epoch_end = mod.on_sequential_epoch_end
+
+    def check(modules):
+        where.update(str(h.device) for h in mod._hessians.values())
+        return epoch_end(modules)
+
+    mod.on_sequential_epoch_end = check
+    mod.apply(model, batches)
+    assert where == {"cpu"}
+    _assert_same(_weights(model), _weights(ref))

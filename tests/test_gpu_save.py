@@ -169,8 +169,10 @@ def test_fp4_quantize_pack_matches_oracle(dev):
 def test_save_gptq_nvfp4_checkpoint(dev, tmp_path):
     """GPTQ with NVFP4 weights, then the checkpoint: the file's codes are
     the oracle's codes of the stored weight, group scales and global scale
-    (the global scale stored in the weight dtype, as the reference stores
-    it), and they decode to the GPTQ weight the module holds, on the fp4
+    (the global scale rounded to the weight dtype, as the reference's
+    ``quantize_weight`` returns it, and written into the fp32 parameter, as
+    ``update_offload_parameter`` writes it: fp32 in every NVFP4 checkpoint),
+    and they decode to the GPTQ weight the module holds, on the fp4
     grid, up to the rounding of the stored global scale and of the weight
     to bf16 (2^-8 each)."""
     from llmcompressor_amd import GPTQModifier
@@ -192,7 +194,9 @@ def test_save_gptq_nvfp4_checkpoint(dev, tmp_path):
         assert np.array_equal(packed, opack.fp4_group_quantize_pack(w, sc, 16, gs))
         assert t[p + "weight_scale"].dtype == torch.float8_e4m3fn
         assert t[p + "weight_global_scale"].tolist() == [gs]
-        assert t[p + "weight_global_scale"].dtype == lin.weight_global_scale.dtype
+        assert t[p + "weight_global_scale"].dtype == torch.float32
+        assert lin.weight_global_scale.dtype == torch.float32
+        assert gs == float(torch.tensor(gs).to(torch.bfloat16).float())   # rounded to bf16 first
         dec = opack.fp4_unpack(packed) * (sc / np.float32(gs)).astype(np.float32)[:, np.arange(w.shape[1]) // 16]
         err = np.abs(dec - w)
         say(f"  layer {i}: decoded vs GPTQ weight, max rel {float(np.max(err / np.maximum(np.abs(w), 1e-30))):.2e}")

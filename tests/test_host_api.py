@@ -163,3 +163,144 @@ def test_shared_hessian_member_missing_the_last_forward_raises():
         book._take_groups(name)
     with pytest.raises(RuntimeError, match="share_hessians=False"):   # a middle batch missed
         _hook_sequence([("a", x[0]), ("b", x[0]), ("a", x[1]), ("a", x[2]), ("b", x[2])])
+
+
+def test_resolve_args_reads_compressed_tensors_fields_only():
+    """A caller's arguments object (compressed-tensors' QuantizationArgs at
+    modifiers/gptq/base.py:591-597) is read through CT's field names only,
+    enum members by value, aliases and defaults as compressed-tensors has
+    them; the caller's object is not modified."""
+    from enum import Enum
+    from types import SimpleNamespace
+
+    from llmcompressor_amd import CT_ARG_FIELDS, resolve_args
+
+    class S(str, Enum):
+        GROUP = "group"
+        CHANNEL = "channel"
+
+    class A(str, Enum):
+        STATIC = "static"
+        DYNAMIC = "dynamic"
+
+    class T(str, Enum):
+        INT = "int"
+        FLOAT = "float"
+
+    read = []
+
+    class Recording(SimpleNamespace):
+        def __getattribute__(self, name):
+            if not name.startswith("__"):
+                read.append(name)
+            return object.__getattribute__(self, name)
+
+    ns = Recording(num_bits=4, type=T.INT, symmetric=True, group_size=128, strategy=S.GROUP,
+                   block_structure=None, dynamic=False, actorder=A.STATIC, scale_dtype=None, zp_dtype=None,
+                   observer="minmax", observer_kwargs={"maxshrink": 0.3}, unrelated_member=1)
+    a = resolve_args(ns)
+    assert set(read) <= set(CT_ARG_FIELDS) and "unrelated_member" not in read
+    assert a.strategy == QuantizationStrategy.GROUP and a.actorder == ActivationOrdering.WEIGHT
+    assert a.q_range() == (-8.0, 7.0) and a.zp_dtype == torch.int8 and not a.is_mx
+    assert a.observer_kwargs == {"maxshrink": 0.3} and a.observer_kwargs is not ns.observer_kwargs
+    assert ns.actorder is A.STATIC and ns.zp_dtype is None
+    assert resolve_args(SimpleNamespace(num_bits=8, group_size=-1)).strategy == QuantizationStrategy.CHANNEL
+    assert resolve_args(SimpleNamespace(num_bits=8, actorder=A.DYNAMIC, group_size=64)).actorder == \
+        ActivationOrdering.GROUP
+    assert resolve_args(SimpleNamespace(num_bits=8, actorder=True, group_size=64)).actorder == \
+        ActivationOrdering.GROUP
+    mx = resolve_args(SimpleNamespace(num_bits=4, type=T.FLOAT, strategy=S.GROUP, group_size=32,
+                                      scale_dtype=torch.uint8, zp_dtype=torch.uint8))
+    assert mx.is_mx and mx.q_range() == (-6.0, 6.0)
+    fp8 = resolve_args(SimpleNamespace(num_bits=8, type="float", strategy="channel"))
+    assert fp8.q_range() == (-448.0, 448.0) and fp8.zp_dtype == torch.float8_e4m3fn
+    own = QuantizationArgs(num_bits=4, group_size=128)
+    assert resolve_args(own) is own
+
+
+def test_fused_observers_release_statistics_together():
+    """observers/helpers.py:177-215 + fusion.py:82-105: q/k/v and gate/up
+    NVFP4 weight observers are linked; each member's statistics stay until
+    every member has asked for its qparams.  Non-tensor-group schemes are
+    not linked; a set mixing tensor-group with other observers fails the
+    reference's assertion."""
+    from llmcompressor_amd import fuse_weight_observers
+
+    def block(scheme_qkv, scheme_o="NVFP4A16"):
+        attn = torch.nn.Module()
+        for n in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            lin = torch.nn.Linear(32, 16, bias=False)
+            initialize_module_for_quantization(lin, preset_name_to_scheme(
+                scheme_qkv if n != "o_proj" else scheme_o, ["Linear"]))
+            initialize_observer(lin, "weight")
+            setattr(attn, n, lin)
+        return attn
+
+    attn = block("NVFP4A16")
+    fuse_weight_observers(attn)
+    obs = [getattr(attn, n).weight_observer for n in ("q_proj", "k_proj", "v_proj")]
+    assert all(o.is_fused for o in obs) and not attn.o_proj.weight_observer.is_fused
+    for o in obs:
+        o.min_vals, o.max_vals = torch.zeros(16, 2), torch.ones(16, 2)
+    obs[0].delete_statistics()
+    obs[1].delete_statistics()
+    assert all(o.has_statistics for o in obs)
+    obs[2].delete_statistics()
+    assert not any(o.has_statistics for o in obs)
+    obs[0].min_vals, obs[0].max_vals = torch.zeros(16, 2), torch.ones(16, 2)
+    obs[0].delete_statistics(check_fused=False)
+    assert not obs[0].has_statistics
+
+    w4 = block("W4A16", "W4A16")
+    fuse_weight_observers(w4)
+    assert not w4.q_proj.weight_observer.is_fused
+
+    mixed = block("NVFP4A16")
+    initialize_module_for_quantization(mixed.k_proj, preset_name_to_scheme("W4A16", ["Linear"]))
+    initialize_observer(mixed.k_proj, "weight")
+    with pytest.raises(AssertionError, match="non-TENSOR_GROUP"):
+        fuse_weight_observers(mixed)
+
+
+def test_expert_families_group_expert_lists_only():
+    """Projections of an expert list (a container with num_experts, or named
+    ...experts) form families by relative name; decoder-layer lists do not;
+    members with different quantization arguments are left alone."""
+    from llmcompressor_amd.moe import LinearExperts, expert_families
+    from llmcompressor_amd.quant_args import resolve_args
+
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.experts = LinearExperts(4, 16, 8)
+            self.layers = torch.nn.ModuleList(torch.nn.Linear(16, 16) for _ in range(3))
+
+    blk = Block()
+    for m in blk.modules():
+        if isinstance(m, torch.nn.Linear):
+            initialize_module_for_quantization(m, preset_name_to_scheme("W4A16", ["Linear"]))
+    targets = {m for m in blk.modules() if isinstance(m, torch.nn.Linear)}
+    args_of = lambda m: resolve_args(m.quantization_scheme.weights)  # noqa: E731
+    fams = expert_families(blk.named_modules(), targets, args_of, 1 << 20)
+    keys = sorted({f.key for f in fams.values()})
+    assert keys == ["experts.*.down_proj", "experts.*.gate_proj", "experts.*.up_proj"]
+    f = fams[blk.experts[2].up_proj]
+    assert f.members == [blk.experts[e].up_proj for e in range(4)] and f.slot[blk.experts[2].up_proj] == 2
+    assert not any(l in fams for l in blk.layers)
+    initialize_module_for_quantization(blk.experts[1].down_proj, preset_name_to_scheme("W8A16", ["Linear"]))
+    fams = expert_families(blk.named_modules(), targets, args_of, 1 << 20)
+    assert blk.experts[0].down_proj not in fams and blk.experts[0].gate_proj in fams
+
+
+def test_expert_families_of_a_bare_expert_list():
+    """The expert list itself as the model: members named <e>.gate_proj."""
+    from llmcompressor_amd.moe import LinearExperts, expert_families
+    from llmcompressor_amd.quant_args import resolve_args
+
+    ex = LinearExperts(3, 16, 8)
+    for m in ex.modules():
+        if isinstance(m, torch.nn.Linear):
+            initialize_module_for_quantization(m, preset_name_to_scheme("W4A16", ["Linear"]))
+    fams = expert_families(ex.named_modules(), {m for m in ex.modules() if isinstance(m, torch.nn.Linear)},
+                           lambda m: resolve_args(m.quantization_scheme.weights), 1 << 20)
+    assert sorted({f.key for f in fams.values()}) == ["*.down_proj", "*.gate_proj", "*.up_proj"]

@@ -225,3 +225,34 @@ def test_conv2d_hessian_is_the_patch_gram_matrix(k, stride, pad, dil):
                 ref += 2 * torch.outer(p, p)
     assert float(n) == B
     assert torch.allclose(H.double(), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_nvfp4_fused_global_scale_is_the_groups_absmax():
+    """observers/base.py:78-96 over a fused set (q/k/v): every member's
+    global scale is 448 * 6 / the absmax over all members' weights (so the
+    largest member sets it and each member's own scale is at least it), the
+    same for every member whatever its own range, and a member fused with
+    nothing gets its own."""
+    args = FLOAT_ARGS[0]
+    ws = [_weight(16, 64, 20), _weight(8, 64, 21) * 3, _weight(8, 64, 22)]
+    obs = []
+    for w in ws:
+        o = OMinMax("memoryless_minmax", "weight", args)
+        o(w)
+        obs.append(o)
+    stats = [(o.min_vals, o.max_vals) for o in obs]
+    gss = []
+    for i, o in enumerate(obs):
+        o.fused_stats = [s for j, s in enumerate(stats) if j != i]
+        gss.append(float(o.get_qparams()["global_scale"]))
+    absmax = max(float(w.abs().max()) for w in ws)
+    assert gss[0] == gss[1] == gss[2]
+    # torch evaluates the scalar quotient as reciprocal(absmax) * 2688 in the
+    # statistics' dtype (bf16 here)
+    want = (torch.tensor(absmax, dtype=torch.bfloat16).reciprocal() * 2688.0).to(torch.bfloat16)
+    assert gss[0] == float(want)
+    own = []
+    for w in ws:
+        o = OMinMax("memoryless_minmax", "weight", args)
+        own.append(float(o(w).get_qparams()["global_scale"]))
+    assert all(g >= gss[0] for g in own) and gss[0] == min(own)
