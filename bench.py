@@ -251,7 +251,7 @@ def main():
 
     cpu = parity = None
     if not a.no_cpu_baseline:
-        cpu, parity = cpu_baseline(torch, w.cpu(), x[:4].cpu(), H_last.cpu(), res)
+        cpu, parity = cpu_baseline(torch, w.cpu(), x[:16].cpu(), H_last.cpu(), res)
 
     # the W8A8, MoE and decoder-layer configurations, two timed steps each
     # after one warm-up, reported inside this line (each also has its own
@@ -277,7 +277,9 @@ def main():
         _COLLECT = None
 
     line = {
-        "metric": "GPTQ ms/layer (W4A16 g128, 4096x4096, Hessian over 64x2048 tokens + solve)",
+        "metric": ("GPTQ ms/layer (W4A16 g128, 4096x4096: Hessian of 64x2048 tokens in "
+                   + ("one accumulate_hessian call" if a.hessian_calls == 1 else f"{a.hessian_calls} calls")
+                   + " + solve)"),
         "value": round(ms_step, 3),
         "unit": "ms/layer",
         "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -291,6 +293,9 @@ def main():
                    "tokens": n_tok, "group_size": GROUP, "blocksize": 128, "damp": 0.01, "actorder": None,
                    "hessian_calls": a.hessian_calls},
         "phases_ms": {"hessian": round(hess_ms, 3), "solve": round(solve_ms, 3)},
+        # the same layer calibrated through the modifiers' forward hook (64
+        # calls of one 2048-token sample, staged): its Hessian time plus the solve
+        "hook_path_ms_per_layer": round(hs_ms + solve_ms, 3),
         "hessian": {"ms": round(syrk_ms, 4), "tflops": round(syrk_tflops, 1),
                     "frac_fp32_mfma_peak": round(syrk_tflops / PEAK_FP32_MFMA_TFLOPS, 3),
                     "frac_bf16_mfma_peak": round(syrk_tflops / PEAK_BF16_TFLOPS, 4),
@@ -320,16 +325,32 @@ def main():
 
 
 def _host_info(torch):
-    """CPU model (lscpu) and the BLAS / LAPACK backends torch was built with."""
+    """CPU model (lscpu's model name with vendor, family, model and stepping,
+    and /proc/cpuinfo's model name where it says more) and the BLAS / LAPACK
+    backends torch was built with."""
     import re
     import subprocess
-    model = None
+    fields = {}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        m = re.search(r"Model name:\s*(.+)", out)
-        model = m.group(1).strip() if m else None
+        for key in ("Vendor ID", "Model name", "CPU family", "Model", "Stepping", "Socket(s)",
+                    "Core(s) per socket", "Thread(s) per core", "CPU max MHz"):
+            m = re.search(rf"^\s*{re.escape(key)}:\s*(.+)$", out, re.M)
+            if m:
+                fields[key] = m.group(1).strip()
     except (OSError, subprocess.SubprocessError):
         pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            m = re.search(r"^model name\s*:\s*(.+)$", f.read(), re.M)
+        if m and m.group(1).strip() != fields.get("Model name"):
+            fields["cpuinfo model name"] = m.group(1).strip()
+    except OSError:
+        pass
+    model = None
+    if fields:
+        model = fields.get("Model name", "?") + " (" + ", ".join(
+            f"{k} {v}" for k, v in fields.items() if k != "Model name") + ")"
     cfg = torch.__config__.show()
     blas = re.search(r"BLAS_INFO=(\w+)", cfg)
     lapack = re.search(r"LAPACK_INFO=(\w+)", cfg)
@@ -337,33 +358,44 @@ def _host_info(torch):
             "lapack": lapack.group(1) if lapack else None}
 
 
+def _median_ms(fn, runs=5, warmup=1):
+    """Median of ``runs`` timed calls after ``warmup`` untimed ones (ms), and
+    the last call's result."""
+    for _ in range(warmup):
+        out = fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        out = fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return sorted(times)[len(times) // 2], out
+
+
 def cpu_baseline(torch, w_cpu, x_sample, h_gpu, res):
     """The oracle (torch-CPU restatement of the reference) on the host cores.
 
-    Sample: the Hessian over 4 x 2048 tokens (scaled to the layer's 64 x 2048)
-    plus one full 4096 x 4096 oracle solve.  The solve runs on the GPU's own
-    Hessian of the timed step (upper triangle mirrored, / num_samples), so its
-    integer codes compare with the GPU's: code agreement, the largest code
-    difference, and the layer output error ||X (W - Q)|| of both on 2048 of
-    the tokens."""
+    Sample, each phase the median of 5 runs after one warm-up: the Hessian
+    over 16 x 2048 tokens (scaled x4 to the layer's 64 x 2048) and the full
+    4096 x 4096 oracle solve.  The solve runs on the GPU's own Hessian of the
+    timed step (upper triangle mirrored, / num_samples), so its integer codes
+    compare with the GPU's: code agreement, the largest code difference, and
+    the layer output error ||X (W - Q)|| of both on 2048 of the tokens."""
     from oracle import gptq as og
     from oracle.qargs import OArgs
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    t0 = time.perf_counter()
-    H, n = og.accumulate_hessian(x_sample, og.make_empty_hessian(COLS), torch.zeros(()))
-    t_h = time.perf_counter() - t0
+    t_h, _h = _median_ms(lambda: og.accumulate_hessian(x_sample, og.make_empty_hessian(COLS), torch.zeros(())))
+    del _h
     scale = (BATCHES * SEQ) / (x_sample.shape[0] * x_sample.shape[1])
     Hf = torch.triu(h_gpu) + torch.triu(h_gpu, 1).t()
-    t0 = time.perf_counter()
-    _, out_o, ex = og.quantize_weight(w_cpu, OArgs(num_bits=4, strategy="group", group_size=GROUP),
-                                      Hf / float(BATCHES), return_codes=True)
-    t_s = time.perf_counter() - t0
-    cpu = {"value": round((t_h * scale + t_s) * 1e3, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
-           "sample": f"Hessian over {x_sample.shape[0]}x{x_sample.shape[1]} tokens x{scale:g} + one full "
-                     f"{ROWS}x{COLS} GPTQ solve (oracle, torch-CPU) on the GPU's Hessian",
-           "hessian_ms_scaled": round(t_h * scale * 1e3, 1), "solve_ms": round(t_s * 1e3, 1), **_host_info(torch)}
+    t_s, (_, out_o, ex) = _median_ms(lambda: og.quantize_weight(
+        w_cpu, OArgs(num_bits=4, strategy="group", group_size=GROUP), Hf / float(BATCHES), return_codes=True))
+    cpu = {"value": round(t_h * scale + t_s, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
+           "sample": f"median of 5 runs after one warm-up per phase: Hessian over {x_sample.shape[0]}x"
+                     f"{x_sample.shape[1]} tokens x{scale:g} + the full {ROWS}x{COLS} GPTQ solve (oracle, "
+                     f"torch-CPU) on the GPU's Hessian",
+           "hessian_ms_scaled": round(t_h * scale, 1), "solve_ms": round(t_s, 1), **_host_info(torch)}
     a, b = res.codes.cpu().to(torch.int32), ex["codes"]
     d = (a - b).abs()
     nz = d != 0

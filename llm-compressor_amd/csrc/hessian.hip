@@ -1039,16 +1039,26 @@ __global__ void symmetrize_kernel(float* h, int64_t d, int64_t ldh) {
 // with more than two rounds of tiles per CU, at most 2 (each split slot
 // costs a 256 KiB partial written and read back: at d = 14336 and 16384
 // tokens, 8 splits move 6.7 GB for 3.4 TFLOP of work).
-int choose_splits(int64_t n, int T) {
+// Compute units of the current device (256 on an MI355X: 8 XCDs of 32).
+int device_cus() {
+  int dev = 0, ncu = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) !=
+      hipSuccess || ncu <= 0)
+    return 256;
+  return ncu;
+}
+
+int choose_splits(int64_t n, int T, int cus) {
   const int64_t s = n / 2048;
   int S = s >= 8 ? 8 : s >= 4 ? 4 : s >= 2 ? 2 : 1;
-  if (T > 512 && S > 2) S = 2;
+  if (T > 2 * cus && S > 2) S = 2;
   if (S == 8) return S;  // the dense plan's tail parts even out its rounds
   // Below that, the fewest splits that reach the shortest time: k splits
-  // take ceil(T k / 256) rounds on the 256 CUs, each 1 / k of the tokens,
-  // and every split beyond one adds a reduction (d = 4096 and 4096 tokens:
-  // one split, one round of 136 tiles, rather than two rounds of halves).
-  const auto rounds_x4 = [T](int k) { return (T * k + 255) / 256 * (4 / k); };
+  // take ceil(T k / cus) rounds on the CUs, each 1 / k of the tokens, and
+  // every split beyond one adds a reduction (d = 4096 and 4096 tokens on
+  // 256 CUs: one split, one round of 136 tiles, rather than two rounds of
+  // halves).
+  const auto rounds_x4 = [T, cus](int k) { return (T * k + cus - 1) / cus * (4 / k); };
   int best = 1;
   for (int k = 2; k <= S; k *= 2)
     if (rounds_x4(k) < rounds_x4(best)) best = k;
@@ -1070,20 +1080,23 @@ inline size_t tile_floats(int64_t d) { return (size_t)tile_edge(d) * tile_edge(d
 // tiles are therefore cut into f = min(4, 32 / rem) parts per split, so the
 // last round takes 1 / f of a full one (d = 4096: T = 136, rem = 8, f = 4,
 // 4.25 rounds instead of 5).  The reduction sums their f part slots per
-// split, in part order, before adding the split.
-constexpr int kCusPerXcd = 32;
+// split, in part order, before adding the split.  The CU count is the
+// device's (queried), so the workspace size and the launch agree on it.
+constexpr int kXcds = 8;
 struct DensePlan {
   int S = 1, T = 0, tail_start = 0, tail_f = 1;
   int64_t grid = 0, slots = 0;
 };
 DensePlan plan_dense(int64_t n, int64_t d) {
   DensePlan pl;
+  const int cus = device_cus();
+  const int per_xcd = cus / kXcds > 0 ? cus / kXcds : 1;
   pl.T = upper_tiles(tiles_per_edge(d));
-  pl.S = choose_splits(n, pl.T);
+  pl.S = choose_splits(n, pl.T, cus);
   pl.tail_start = pl.T;
-  const int rem = pl.T % kCusPerXcd;
-  if (pl.S == 8 && tile_edge(d) == 256 && rem > 0 && rem <= kCusPerXcd / 2) {
-    pl.tail_f = kCusPerXcd / rem < 4 ? kCusPerXcd / rem : 4;
+  const int rem = pl.T % per_xcd;
+  if (pl.S == 8 && tile_edge(d) == 256 && rem > 0 && rem <= per_xcd / 2) {
+    pl.tail_f = per_xcd / rem < 4 ? per_xcd / rem : 4;
     pl.tail_start = pl.T - rem;
   }
   const int64_t nfull = (int64_t)pl.tail_start * pl.S;

@@ -41,7 +41,7 @@ from . import sparsegpt as sgpt
 from . import ops
 from .gptq import (_effective_actorder, accumulate_hessian, gptq_quantize, gptq_quantize_batched, hessian_rows,
                    make_empty_hessian, prepare_hessian, prepare_hessians_batched)
-from .staging import DEFAULT_BUDGET, DEFAULT_TOKENS, HessianStage
+from .staging import DEFAULT_BUDGET, DEFAULT_TOKENS, HessianStage, stage_tokens
 from .quant_args import (ActivationOrdering, QuantizationArgs, QuantizationScheme, preset_name_to_scheme,
                          resolve_args)
 
@@ -209,6 +209,9 @@ class _SharedHessians:
             leader = next(iter(self._pending))
             member = next(m for m, l in self._leader.items() if l is leader)
             self._init_sharing(self.share_hessians)
+            release = getattr(self, "_release_stages", None)
+            if release is not None:     # no staged rows outlive the error
+                release()
             self._diverged(member, leader, name or (lambda m: type(m).__name__))
         groups: dict = {}
         for module in self._num_samples:
@@ -234,10 +237,11 @@ class _Staging:
     def _stage_for(self, module, x):
         if module in self._stages:
             return self._stages[module]
-        need = self.hessian_batch_tokens * x.shape[1] * x.element_size()
+        tokens = stage_tokens(self.hessian_batch_tokens, x.shape[1], x.element_size())
+        need = tokens * x.shape[1] * x.element_size()
         st = None
         if self._stage_held + need <= self.hessian_stage_bytes:
-            st = HessianStage(self.hessian_batch_tokens)
+            st = HessianStage(tokens)
             self._reserved[module] = need
             self._stage_held += need
         self._stages[module] = st
@@ -250,6 +254,16 @@ class _Staging:
             st.release()
             self._stage_held -= self._reserved.pop(module)
 
+    def _release_stages(self):
+        """Frees every stage without accumulating its rows (after an error,
+        and at finalisation)."""
+        for st in self._stages.values():
+            if st is not None:
+                st.release()
+        self._stages, self._reserved, self._stage_held = {}, {}, 0
+        for fam in set(getattr(self, "_families", {}).values()):
+            fam.release()
+
 
 class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
     """GPTQ over the targeted Linear modules (``modifiers/gptq/base.py``).
@@ -257,8 +271,9 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
     Beyond the reference's arguments: ``share_hessians`` (modules fed the
     same tensor accumulate one Hessian), ``hessian_batch_tokens`` /
     ``hessian_stage_bytes`` (rows of small calls are copied into device
-    buffers of 16384 rows and accumulated one long syrk at a time, while the
-    buffers of one modifier stay within 2 GiB by default) and
+    buffers of up to 65536 rows and 512 MiB and accumulated one long syrk at
+    a time, while the buffers of one modifier stay within 2 GiB by default)
+    and
     ``batch_experts``: the same-shaped projections of an MoE expert list
     (``<experts>.<e>.gate_proj`` ...) keep their Hessians in one stacked
     tensor, accumulate each forward's routed rows in one grouped syrk launch
@@ -528,10 +543,9 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
         self._hooks = []
 
     def on_finalize(self):
+        self._release_stages()
         if self._num_samples:
             raise ValueError(f"Failed to compress {len(self._num_samples)} modules")
-        for fam in set(self._families.values()):
-            fam.release()
         return True
 
     def apply(self, model, batches):
@@ -557,7 +571,10 @@ class SparseGPTModifier(_SharedHessians, _Staging):
     is ``"N:M"`` (``"0:0"``: unstructured).  OWL layer sparsities
     (``sparsity_profile="owl"``) are not provided by this build.
     ``share_hessians``: modules fed the same tensor accumulate one Hessian
-    (as ``GPTQModifier``).
+    (as ``GPTQModifier``).  ``hessian_batch_tokens`` / ``hessian_stage_bytes``:
+    the rows of small calls are staged on the device and folded in long
+    syrk calls, with the stage buffers of one modifier within 2 GiB by
+    default (0 tokens folds every call at once, as the reference does).
     """
 
     def __init__(self, sparsity=None, sparsity_profile: str | None = None, mask_structure: str = "0:0",
@@ -684,6 +701,7 @@ class SparseGPTModifier(_SharedHessians, _Staging):
         self._hooks = []
 
     def on_finalize(self):
+        self._release_stages()
         if self._num_samples:
             raise ValueError(f"Failed to compress {len(self._num_samples)} modules")
         self._hessians, self._num_samples = {}, {}

@@ -10,14 +10,25 @@ rate of a long call.  ``HessianStage`` copies the rows of small calls into a
 [tokens, d] buffer of the input dtype and hands them to the syrk when the
 buffer is full or when the Hessian is read, so the same sum is formed in
 fewer, longer calls (another order of fp32 additions; the sample count is
-the reference's).
+the reference's).  A stage holds up to 65536 rows and at most 512 MiB
+(18432 rows of a 14336-wide bf16 input), so that each syrk call runs the
+eight token splits of 8192 rows a one-call Hessian of a 4096-wide layer
+runs.
 """
 from __future__ import annotations
 
 import torch
 
-DEFAULT_TOKENS = 16384
+DEFAULT_TOKENS = 65536
 DEFAULT_BUDGET = 2 << 30   # bytes of stage buffers one modifier holds at a time
+STAGE_BYTES_MAX = 512 << 20
+
+
+def stage_tokens(tokens: int, d: int, element_size: int) -> int:
+    """Rows of one stage for a [*, d] input: ``tokens``, lowered to a
+    multiple of 2048 that fits in ``STAGE_BYTES_MAX`` (at least 2048)."""
+    fit = STAGE_BYTES_MAX // max(1, d * element_size) // 2048 * 2048
+    return min(tokens, max(2048, fit))
 
 
 class HessianStage:

@@ -31,7 +31,7 @@ def test_gptq_staged_hessian_matches_per_call(dev):
     for x in xs:
         H1, n1 = gptq.accumulate_hessian(x, lin, H1, n1)
     H2, n2 = gptq.make_empty_hessian(lin), torch.zeros((), device=dev)
-    stage, calls = HessianStage(), []
+    stage, calls = HessianStage(16384), []
 
     def flush(rows, samples):
         calls.append(rows.shape[0])
@@ -91,7 +91,7 @@ def test_gptq_modifier_staged_matches_unstaged(dev):
     GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), actorder=None,
                  hessian_batch_tokens=0).apply(ref, batches)
     mod = GPTQModifier(scheme="W4A16", targets=("Linear",), ignore=(), actorder=None,
-                       hessian_stage_bytes=16384 * 512 * 2)
+                       hessian_stage_bytes=65536 * 512 * 2)
     mod.apply(model, batches)
     assert mod._stage_held == 0 and not mod._stages
     for a, b in zip(model, ref):

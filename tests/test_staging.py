@@ -92,3 +92,13 @@ def test_modifier_stage_budget():
     assert len(rec.calls) == 1 and rec.calls[0][0].shape == (16, 64)
     assert m._stage_held == 2 * 1024 * 64 * 2 and mods[0] not in m._stages
     assert m._stage_for(mods[0], x) is not None            # room again
+
+
+def test_stage_rows_capped_at_512_mib():
+    from llmcompressor_amd.staging import DEFAULT_TOKENS, stage_tokens
+    assert DEFAULT_TOKENS == 65536
+    assert stage_tokens(DEFAULT_TOKENS, 4096, 2) == 65536        # 512 MiB
+    assert stage_tokens(DEFAULT_TOKENS, 14336, 2) == 18432       # 504 MiB
+    assert stage_tokens(DEFAULT_TOKENS, 14336, 4) == 8192
+    assert stage_tokens(1024, 64, 2) == 1024
+    assert stage_tokens(DEFAULT_TOKENS, 1 << 20, 4) == 2048      # never below one 2048-row sample
