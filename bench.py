@@ -560,12 +560,13 @@ def bench_moe(a):
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
 
     def step():
-        Hgu = torch.zeros(E, hid, hid, device=dev)
-        Hd = torch.zeros(E, inter, inter, device=dev)
+        # uncleared: the grouped syrk writes every upper triangle (fresh=True)
+        Hgu = torch.empty(E, hid, hid, device=dev)
+        Hd = torch.empty(E, inter, inter, device=dev)
         ns = torch.zeros(E, device=dev)
         ev[0].record()
-        moe.accumulate_expert_hessians(hs, rows, off_dev, Hgu, ns)
-        moe.accumulate_expert_hessians(inter_x, None, off_dev, Hd, ns.clone())
+        moe.accumulate_expert_hessians(hs, rows, off_dev, Hgu, ns, fresh=True)
+        moe.accumulate_expert_hessians(inter_x, None, off_dev, Hd, ns.clone(), fresh=True)
         ev[1].record()
         # all experts of one projection solved together (one launch per step);
         # gate and up share their input, hence their Hessian and its Cholesky chain

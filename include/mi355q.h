@@ -105,7 +105,9 @@ int mi355q_hessian_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_tokens,
 /* Grouped (MoE) variant: expert e accumulates the rows
  * x[rows_dev[k]] for k in [offsets_dev[e], offsets_dev[e+1]) into
  * h_dev + e * h_stride (each d x d, leading dimension d, upper triangle):
- * H_e += alpha * X_e^T X_e.  Replaces the per-expert accumulate_hessian
+ * H_e = beta * H_e + alpha * X_e^T X_e, beta 1 (add) or 0 (H_e's upper
+ * triangle is written without being read, zeros for an expert without
+ * rows: a freshly allocated stack need not be cleared).  Replaces the per-expert accumulate_hessian
  * calls that modeling/moe/linear_experts.py:244-277 triggers with routed
  * tokens.  x is [n_x, d] (ldx), bf16 or fp16; rows_dev (n_rows int32
  * indices into x) may be NULL when x's rows are already grouped (row k of
@@ -119,7 +121,7 @@ int mi355q_hessian_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_tokens,
 size_t mi355q_hessian_grouped_syrk_workspace_size(int64_t n_rows, int n_experts, int64_t d);
 int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_x, int64_t ldx, int64_t d,
                                 const int32_t* rows_dev, int64_t n_rows, const int64_t* offsets_dev,
-                                int n_experts, float* h_dev, int64_t h_stride, float alpha,
+                                int n_experts, float* h_dev, int64_t h_stride, float alpha, float beta,
                                 void* workspace_dev, size_t workspace_bytes, void* stream);
 
 /* Mirror the upper triangle into the lower one (full symmetric matrix). */

@@ -446,6 +446,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
     const int i = (int)(blockIdx.x & 7u) * per + k;
     if (k >= per || i >= N) return;
     const GChunk c = p.chunks[i / p.T];
+    if (c.e < 0) return;
     t = i % p.T;
     mat = Matrix{c.tok_begin, c.count < kChunkTokens ? c.count : kChunkTokens, p.h0 + (int64_t)c.e * p.h_stride};
     slot = c.sbase < 0 ? -1 : c.sbase + t;
@@ -717,7 +718,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
 #pragma unroll
           for (int k = 0; k < 16; ++k) {
             const int64_t gi = fa0 + hh * 128 + wave * RR + k0 + k;
-            const bool ok = gi < p.d && gj < p.d && (!diag || gi <= gj + 3);
+            // beta == 0 reads H only for a float4 that straddles the
+            // diagonal (its lower elements are written back unchanged)
+            const bool ok = gi < p.d && gj < p.d && (!diag || gi <= gj + 3) && (p.beta != 0.f || (diag && gi > gj));
             hv[k] = ok ? *reinterpret_cast<const f32x4_t*>(mat.h + gi * ldh + gj) : f32x4_t{0.f, 0.f, 0.f, 0.f};
           }
 #pragma unroll
@@ -729,7 +732,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
               f32x4_t o;
 #pragma unroll
               for (int c = 0; c < 4; ++c)
-                o[c] = (!diag || gi <= gj + c) ? scaled(hv[k][c], p.beta) + p.alpha * v[c] : hv[k][c];
+                o[c] = (!diag || gi <= gj + c)
+                           ? (p.beta == 0.f ? p.alpha * v[c] : scaled(hv[k][c], p.beta) + p.alpha * v[c])
+                           : hv[k][c];
               *reinterpret_cast<f32x4_t*>(mat.h + gi * ldh + gj) = o;
             }
           }
@@ -753,7 +758,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
           const int mi = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), nj = lane & 31;
           if (gib + mi < p.d && gjb + nj < p.d && (!diag || mb + mi <= nb + nj)) {
             float* hp = hb + (int64_t)mi * ldh + nj;
-            *hp = scaled(*hp, p.beta) + p.alpha * acc[x][y][r];
+            *hp = p.beta == 0.f ? p.alpha * acc[x][y][r] : scaled(*hp, p.beta) + p.alpha * acc[x][y][r];
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -916,8 +921,8 @@ __global__ __launch_bounds__(NT) void syrk_group_reduce_kernel(const float* __re
 // never reach.
 __global__ __launch_bounds__(1024) void grouped_plan_kernel(const int64_t* __restrict__ offsets, int E,
                                                             int64_t n_rows, int T, int max_chunks,
-                                                            int max_slot_chunks, int max_reduce, GChunk* chunks,
-                                                            GReduce* reds, int* gcounts) {
+                                                            int max_slot_chunks, int max_reduce, int all_experts,
+                                                            GChunk* chunks, GReduce* reds, int* gcounts) {
   __shared__ int sm[1024], sr[1024], ss[1024];
   const int tid = threadIdx.x;
   int base_c = 0, base_r = 0, base_s = 0;
@@ -931,7 +936,8 @@ __global__ __launch_bounds__(1024) void grouped_plan_kernel(const int64_t* __res
       en = en < b ? b : (en > n_rows ? n_rows : en);
       n = en - b;
     }
-    const int m = (int)((n + kChunkTokens - 1) / kChunkTokens);
+    int m = (int)((n + kChunkTokens - 1) / kChunkTokens);
+    if (all_experts && e < E && m == 0) m = 1;   // an expert without rows still writes its H
     sm[tid] = m;
     sr[tid] = m > 1 ? 1 : 0;
     ss[tid] = m > 1 ? m - 1 : 0;
@@ -951,11 +957,11 @@ __global__ __launch_bounds__(1024) void grouped_plan_kernel(const int64_t* __res
       const int c = cm + k, sc = cs + k - 1;
       if (c >= max_chunks) break;   // past the table (gcounts[0] stops before it)
       const int64_t left = n - (int64_t)k * kChunkTokens;
-      // a chunk past the slot bound is written empty (adds nothing)
+      // a chunk past the slot bound is skipped (expert -1: adds nothing)
       chunks[c] = (k == 0 || sc < max_slot_chunks)
                       ? GChunk{e, (int)(left < kChunkTokens ? left : kChunkTokens), b + (int64_t)k * kChunkTokens,
                                k == 0 ? -1 : (int64_t)sc * T}
-                      : GChunk{e, 0, 0, -1};
+                      : GChunk{-1, 0, 0, -1};
     }
     if (m > 1 && cr < max_reduce) {
       const int room = cs < max_slot_chunks ? max_slot_chunks - cs : 0;
@@ -1276,7 +1282,7 @@ extern "C" size_t mi355q_hessian_grouped_syrk_workspace_size(int64_t n_rows, int
 extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_x, int64_t ldx,
                                            int64_t d, const int32_t* rows_dev, int64_t n_rows,
                                            const int64_t* offsets_dev, int n_experts, float* h_dev,
-                                           int64_t h_stride, float alpha, void* workspace_dev,
+                                           int64_t h_stride, float alpha, float beta, void* workspace_dev,
                                            size_t workspace_bytes, void* stream) {
   MQ_CHECK_ARG(dtype == MI355Q_BF16 || dtype == MI355Q_F16, "grouped hessian: dtype must be bf16 or fp16");
   MQ_CHECK_ARG(d > 0 && d % 8 == 0, "grouped hessian: d must be a positive multiple of 8");
@@ -1286,8 +1292,11 @@ extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype
   MQ_CHECK_ARG(n_x >= 0 && n_rows >= 0, "grouped hessian: negative row count");
   MQ_CHECK_ARG(rows_dev != nullptr || n_rows <= n_x, "grouped hessian: n_rows > n_x without a row index");
   MQ_CHECK_ARG(h_dev != nullptr && h_stride >= d * d, "grouped hessian: bad H / stride");
-  if (n_rows == 0 || n_x == 0) return MI355Q_OK;
-  MQ_CHECK_ARG(x_dev != nullptr && aligned16(x_dev), "grouped hessian: null or misaligned x");
+  MQ_CHECK_ARG(beta == 0.f || beta == 1.f, "grouped hessian: beta must be 0 (H is written) or 1 (H is added to)");
+  const bool fresh = beta == 0.f;
+  if ((n_rows == 0 || n_x == 0) && !fresh) return MI355Q_OK;
+  if (n_x == 0) n_rows = 0;   // nothing to read: every H is written as zero
+  MQ_CHECK_ARG(n_rows == 0 || (x_dev != nullptr && aligned16(x_dev)), "grouped hessian: null or misaligned x");
   const GroupedBounds gb = grouped_bounds(n_rows, n_experts, d);
   MQ_CHECK_ARG(workspace_dev != nullptr && workspace_bytes >= gb.total,
                "grouped hessian: workspace too small (%zu < %zu)", workspace_bytes, gb.total);
@@ -1297,7 +1306,7 @@ extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype
   GReduce* reds = reinterpret_cast<GReduce*>(ws + gb.off_reds);
   int* counts = reinterpret_cast<int*>(ws + gb.off_counts);
   hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(1024), 0, st, offsets_dev, n_experts, n_rows, gb.T,
-                     gb.max_chunks, gb.max_slot_chunks, gb.max_reduce, chunks, reds, counts);
+                     gb.max_chunks, gb.max_slot_chunks, gb.max_reduce, fresh ? 1 : 0, chunks, reds, counts);
   MQ_LAUNCH_CHECK();
 
   SyrkParams p{};
@@ -1307,7 +1316,7 @@ extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype
   p.ldh = d;
   p.nt = (int)((d + 255) / 256);
   p.alpha = alpha;
-  p.beta = 1.f;
+  p.beta = beta;
   p.S = 1;
   p.ws = reinterpret_cast<float*>(ws);
   p.rows = rows_dev;

@@ -66,14 +66,15 @@ def route_tokens(top_k_index: torch.Tensor, num_experts: int, num_tokens: int | 
 
 
 def accumulate_expert_hessians(x: torch.Tensor, rows: torch.Tensor | None, offsets, H: torch.Tensor,
-                               num_samples: torch.Tensor, calls: int = 1):
+                               num_samples: torch.Tensor, calls: int = 1, fresh: bool = False):
     """H[e] += 2 * sum over the expert's rows of x x^T; num_samples[e] += calls.
 
     ``rows`` None: x is already grouped by expert (expert e owns the rows
     offsets[e] .. offsets[e+1] - 1, as ``expert_intermediate`` returns them).
     ``offsets`` is a list or an int64 tensor (on the device the call waits
-    for nothing)."""
-    ops.hessian_grouped_syrk_(H, x, rows, offsets, alpha=2.0)
+    for nothing).  ``fresh``: H holds no earlier sum (it may be freshly
+    allocated, uncleared): its upper triangles are written, not read."""
+    ops.hessian_grouped_syrk_(H, x, rows, offsets, alpha=2.0, beta=0.0 if fresh else 1.0)
     num_samples += calls
     return H, num_samples
 
@@ -175,6 +176,7 @@ class ExpertFamily:
         self.slot = {m: i for i, m in enumerate(self.members)}
         self.budget = budget
         self.H: torch.Tensor | None = None
+        self._fresh = False        # H allocated, nothing accumulated yet
         self.samples = [0] * len(self.members)
         self._parts: list = []      # (slot, call index, rows)
         self._held = 0
@@ -185,7 +187,9 @@ class ExpertFamily:
         if self.H is None:
             w = self.members[0].weight
             d = w.shape[1]
-            self.H = torch.zeros((len(self.members), d, d), dtype=torch.float32, device=w.device)
+            # uncleared: the first grouped syrk writes every upper triangle
+            self.H = torch.empty((len(self.members), d, d), dtype=torch.float32, device=w.device)
+            self._fresh = True
         return self.H[self.slot[module]]
 
     def add(self, module, rows: torch.Tensor, samples: int) -> None:
@@ -200,8 +204,13 @@ class ExpertFamily:
         self._held += nbytes
 
     def flush(self) -> None:
-        """Accumulates the held rows: one grouped syrk over the experts."""
+        """Accumulates the held rows: one grouped syrk over the experts (the
+        first one writes the upper triangles of the uncleared stack, experts
+        without rows as zeros)."""
         if not self._parts:
+            if self._fresh:
+                self.H.zero_()
+                self._fresh = False
             return
         parts = sorted(self._parts, key=lambda p: (p[0], p[1]))
         self._parts, self._held = [], 0
@@ -214,11 +223,13 @@ class ExpertFamily:
         dtypes = {rows.dtype for _, _, rows in parts}
         dt = dtypes.pop() if len(dtypes) == 1 else torch.float32
         x = torch.cat([rows.to(dt) for _, _, rows in parts]) if len(parts) > 1 else parts[0][2]
-        ops.hessian_grouped_syrk_(self.H, x, None, offsets, alpha=2.0)
+        ops.hessian_grouped_syrk_(self.H, x, None, offsets, alpha=2.0, beta=0.0 if self._fresh else 1.0)
+        self._fresh = False
 
     def release(self) -> None:
         self._parts, self._held = [], 0
         self.H = None
+        self._fresh = False
         self.samples = [0] * len(self.members)
 
 

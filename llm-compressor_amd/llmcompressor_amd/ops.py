@@ -70,14 +70,18 @@ def hessian_syrk_(H: torch.Tensor, x: torch.Tensor, alpha: float = 2.0, beta: fl
 
 
 def hessian_grouped_syrk_(H: torch.Tensor, x: torch.Tensor, rows: torch.Tensor | None, offsets,
-                          alpha: float = 2.0) -> torch.Tensor:
-    """Per-group upper-triangle syrk: H[e] += alpha * X_e^T X_e where X_e are
-    the rows ``x[rows[offsets[e]:offsets[e+1]]]`` (``rows`` None: the rows
-    ``x[offsets[e]:offsets[e+1]]``).  H is [E, d, d] fp32; ``offsets`` a list
-    or an int64 tensor of E + 1 non-decreasing entries.  bf16 and fp16 ``x``
-    take one grouped launch whose work table is built on the device; other
-    types are converted to fp32 and each group's rows take the dense fp32
-    product."""
+                          alpha: float = 2.0, beta: float = 1.0) -> torch.Tensor:
+    """Per-group upper-triangle syrk: H[e] = beta * H[e] + alpha * X_e^T X_e
+    where X_e are the rows ``x[rows[offsets[e]:offsets[e+1]]]`` (``rows``
+    None: the rows ``x[offsets[e]:offsets[e+1]]``).  H is [E, d, d] fp32;
+    ``offsets`` a list or an int64 tensor of E + 1 non-decreasing entries.
+    ``beta`` is 1 (add) or 0: H's upper triangle is written without being
+    read (a freshly allocated H need not be zeroed; groups without rows get
+    zeros).  bf16 and fp16 ``x`` take one grouped launch whose work table is
+    built on the device; other types are converted to fp32 and each group's
+    rows take the dense fp32 product."""
+    if beta not in (0.0, 1.0):
+        raise ValueError("beta must be 0 or 1")
     L.require_gpu(H, x)
     if isinstance(offsets, torch.Tensor):
         off_dev = offsets.to(device=x.device, dtype=torch.int64).contiguous()
@@ -101,7 +105,11 @@ def hessian_grouped_syrk_(H: torch.Tensor, x: torch.Tensor, rows: torch.Tensor |
         for e in range(E):
             if offs[e + 1] > offs[e]:
                 xe = x[offs[e]:offs[e + 1]] if rows is None else x[rows[offs[e]:offs[e + 1]].long()]
+                if beta == 0.0:
+                    H[e].zero_()
                 hessian_syrk_(H[e], xe, alpha=alpha)
+            elif beta == 0.0:
+                H[e].zero_()
         return H
     if rows is not None:
         L.require_gpu(rows)
@@ -112,7 +120,7 @@ def hessian_grouped_syrk_(H: torch.Tensor, x: torch.Tensor, rows: torch.Tensor |
     ws = _ws(lib.mi355q_hessian_grouped_syrk_workspace_size(n_rows, E, d), x.device)
     L.check(lib.mi355q_hessian_grouped_syrk(x.data_ptr(), _HESS_DT[x.dtype], n_x, x.stride(0), d,
                                             None if rows is None else rows.data_ptr(), n_rows, off_dev.data_ptr(),
-                                            E, H.data_ptr(), d * d, C.c_float(alpha), L.ptr(ws),
+                                            E, H.data_ptr(), d * d, C.c_float(alpha), C.c_float(beta), L.ptr(ws),
                                             0 if ws is None else ws.numel(), L.stream_of(x)))
     return H
 

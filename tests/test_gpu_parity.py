@@ -266,6 +266,30 @@ def test_hessian_grouped_multichunk(dev, d, dtype):
     assert ((H - 2 * H1).norm() / H1.norm()).item() <= 1e-6
 
 
+@pytest.mark.parametrize("gather", [True, False], ids=["gathered", "grouped"])
+def test_hessian_grouped_fresh_h_is_written_not_read(dev, gather):
+    """beta = 0 (a freshly allocated, uncleared stack): every expert's upper
+    triangle equals the add-to-zeros result bit for bit (zeros for an expert
+    without rows, a second chunk still reduced after the first), and the
+    strictly-lower triangle keeps whatever it held."""
+    counts = [9000, 0, 100, 4097, 1]
+    d = 768
+    say(f"grouped hessian beta=0 gather={gather}")
+    x, rows, offsets = _grouped_case(counts, 7000, d, torch.bfloat16, 23, dev)
+    if not gather:
+        x, rows = x[rows.long()].contiguous(), None
+    ref = torch.zeros(len(counts), d, d, device=dev)
+    ops.hessian_grouped_syrk_(ref, x, rows, offsets, alpha=2.0)
+    H = torch.full((len(counts), d, d), float("nan"), device=dev)
+    ops.hessian_grouped_syrk_(H, x, rows, torch.tensor(offsets, device=dev), alpha=2.0, beta=0.0)
+    up = torch.triu(torch.ones(d, d, dtype=torch.bool, device=dev))
+    for e in range(len(counts)):
+        assert torch.equal(H[e][up], ref[e][up]), e
+        assert bool(torch.isnan(H[e][~up]).all()), e
+    with pytest.raises(ValueError):
+        ops.hessian_grouped_syrk_(H, x, rows, offsets, alpha=2.0, beta=0.5)
+
+
 def test_hessian_grouped_contiguous_rows(dev):
     """rows None: x already grouped by expert (the down projection's inputs),
     offsets given on the device."""

@@ -70,15 +70,18 @@ def test_hessian_grouped_host_checks():
     an ungathered call with more rows than x, and the workspace bound."""
     lib = _lib.load_library()
     rc = lib.mi355q_hessian_grouped_syrk(C.c_void_p(16), _lib.BF16, 100, 8, 8, None, 100, C.c_void_p(16), 2,
-                                         C.c_void_p(16), 63, C.c_float(2.0), None, 0, None)
+                                         C.c_void_p(16), 63, C.c_float(2.0), C.c_float(1.0), None, 0, None)
     assert rc == _lib.INVALID_ARGUMENT and "stride" in lib.mi355q_last_error().decode()
     rc = lib.mi355q_hessian_grouped_syrk(C.c_void_p(16), _lib.BF16, 100, 8, 8, None, 101, C.c_void_p(16), 2,
-                                         C.c_void_p(16), 64, C.c_float(2.0), None, 0, None)
+                                         C.c_void_p(16), 64, C.c_float(2.0), C.c_float(1.0), None, 0, None)
     assert rc == _lib.INVALID_ARGUMENT and "n_rows > n_x" in lib.mi355q_last_error().decode()
     need = lib.mi355q_hessian_grouped_syrk_workspace_size(100, 2, 8)
     rc = lib.mi355q_hessian_grouped_syrk(C.c_void_p(16), _lib.BF16, 100, 8, 8, None, 100, C.c_void_p(16), 2,
-                                         C.c_void_p(16), 64, C.c_float(2.0), C.c_void_p(16), need - 1, None)
+                                         C.c_void_p(16), 64, C.c_float(2.0), C.c_float(1.0), C.c_void_p(16), need - 1, None)
     assert rc == _lib.INVALID_ARGUMENT and "workspace too small" in lib.mi355q_last_error().decode()
+    rc = lib.mi355q_hessian_grouped_syrk(C.c_void_p(16), _lib.BF16, 100, 8, 8, None, 100, C.c_void_p(16), 2,
+                                         C.c_void_p(16), 64, C.c_float(2.0), C.c_float(0.5), C.c_void_p(16), need, None)
+    assert rc == _lib.INVALID_ARGUMENT and "beta must be 0" in lib.mi355q_last_error().decode()
     # slots: one per later chunk of 4096 rows and upper 256-tile
     big = lib.mi355q_hessian_grouped_syrk_workspace_size(3 * 4096, 2, 512)
     assert big >= 3 * 3 * 256 * 256 * 4
