@@ -95,6 +95,7 @@ struct SyrkParams {
   int64_t n_x;             // rows of x (gathered indices are clamped into [0, n_x))
   const GChunk* chunks;
   const int* gcounts;      // [0] chunks, [1] reduce items (written by the planner)
+  int* queues;             // 8 work-queue counters (zeroed by the planner)
   int T;                   // upper tiles per matrix
   float* h0;               // H of expert 0 (leading dimension d)
   int64_t h_stride;
@@ -383,8 +384,13 @@ __device__ __forceinline__ bf16x8_t tr_pair(const char* lds, int off0, int off1)
 
 enum StreamMode { kDense = 0, kGrouped = 1, kGroupedGather = 2 };
 
+// One work item of the streaming kernel: tile t of matrix `mat` over token
+// split s (and part `part` of `nparts` for dense tail tiles), into partial
+// slot `slot` (-1: H directly).  `ring` is the workgroup's 128 KiB LDS ring,
+// `ridx` its row-index cache (gathered chunks).
 template <bool F16, int MODE, int WAVES>
-__global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p) {
+__device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int* ridx, int t, int s, int part,
+                                            int nparts, int S, int64_t slot, Matrix mat) {
   // WAVES = 8: a 2 x 4 grid of waves (two per SIMD), each 4 x 2 MFMA blocks
   // (128 rows x 64 columns); WAVES = 4: a 2 x 2 grid (one per SIMD), each
   // 4 x 4 blocks (128 x 128), a third fewer LDS reads per MFMA
@@ -397,7 +403,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
   constexpr int TM = 256;
   // LDS ring: operand A in stages 0..3, then operand B; after the loop it
   // holds half an fp32 tile for the direct update of H
-  __shared__ __attribute__((aligned(1024))) char ring[8 * SOP];
   char* const a0 = ring;
   char* const a1 = ring + SOP;
   char* const a2 = ring + 2 * SOP;
@@ -406,51 +411,15 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
   char* const b1 = ring + 5 * SOP;
   char* const b2 = ring + 6 * SOP;
   char* const b3 = ring + 7 * SOP;
-  // row indices of a gathered chunk
-  __shared__ int ridx[MODE == kGroupedGather ? kChunkTokens : 1];
 
-  const int tid = threadIdx.x;
+  // the thread index through an opaque copy: in the grouped kernel's item
+  // loop nothing derived from it is hoisted out of the loop and kept live
+  // across items (which spilled the loop's registers to scratch)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = WAVES == 8 ? wave >> 2 : wave >> 1, wn = WAVES == 8 ? wave & 3 : wave & 1;
-
-  // work item: tile t, token split s (and, for dense tail tiles, part `part`
-  // of tail_f equal pieces of that split), partial slot
-  int t, s = 0, part = 0, nparts = 1, S = 1;
-  int64_t slot;
-  Matrix mat;
-  if constexpr (MODE == kDense) {
-    S = p.S;
-    const int64_t nfull = (int64_t)p.tail_start * S;
-    if ((int64_t)blockIdx.x < nfull) {
-      s = blockIdx.x % S;
-      t = blockIdx.x / S;
-      slot = (S > 1) ? (int64_t)t * S + s : -1;
-    } else {
-      const int b = (int)(blockIdx.x - nfull);
-      s = b % S;
-      const int j = b / S;
-      t = p.tail_start + j / p.tail_f;
-      part = j % p.tail_f;
-      nparts = p.tail_f;
-      slot = nfull + ((int64_t)(t - p.tail_start) * S + s) * p.tail_f + part;
-    }
-    mat = p.single;
-  } else {
-    // grouped: item i = chunk * T + t; XCD x (= blockIdx % 8) runs items
-    // [x per, (x + 1) per) in order; the grid covers the largest possible
-    // table and the workgroups past the built one return at once
-    const int N = p.gcounts[0] * p.T;
-    const int per = (N + 7) >> 3;
-    const int k = (int)(blockIdx.x >> 3);
-    const int i = (int)(blockIdx.x & 7u) * per + k;
-    if (k >= per || i >= N) return;
-    const GChunk c = p.chunks[i / p.T];
-    if (c.e < 0) return;
-    t = i % p.T;
-    mat = Matrix{c.tok_begin, c.count < kChunkTokens ? c.count : kChunkTokens, p.h0 + (int64_t)c.e * p.h_stride};
-    slot = c.sbase < 0 ? -1 : c.sbase + t;
-  }
   int ti, tj;
   tile_coords(t, p.nt, ti, tj);
 
@@ -781,6 +750,73 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
       }
 }
 
+// Dense mode: one work item per workgroup (tile t, token split s = blockIdx
+// % S, so each XCD streams its own split; dense tail tiles in tail_f parts
+// per split).  Grouped modes: persistent workgroups (one per CU) take items
+// i = chunk * T + t from eight queues, queue x holding items [x per, (x + 1)
+// per) in chunk-major order: a workgroup first drains the queue of its XCD
+// (blockIdx % 8, workgroups being dispatched round-robin over the XCDs) so
+// the tiles of one chunk run on one XCD and share its rows in L2, then
+// takes what is left in the others.  Chunks hold 1 .. 4096 routed rows, so
+// equal item counts per XCD can mean very unequal work (routed rows per
+// expert vary 85-fold in the Zipf-routed MoE layer); the queues even it out.
+// Every queue ends, so every workgroup exits.
+template <bool F16, int MODE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p) {
+  __shared__ __attribute__((aligned(1024))) char ring[8 * SOP];
+  // row indices of a gathered chunk
+  __shared__ int ridx[MODE == kGroupedGather ? kChunkTokens : 1];
+  if constexpr (MODE == kDense) {
+    const int S = p.S;
+    int t, s, part = 0, nparts = 1;
+    int64_t slot;
+    const int64_t nfull = (int64_t)p.tail_start * S;
+    if ((int64_t)blockIdx.x < nfull) {
+      s = blockIdx.x % S;
+      t = blockIdx.x / S;
+      slot = (S > 1) ? (int64_t)t * S + s : -1;
+    } else {
+      const int b = (int)(blockIdx.x - nfull);
+      s = b % S;
+      const int j = b / S;
+      t = p.tail_start + j / p.tail_f;
+      part = j % p.tail_f;
+      nparts = p.tail_f;
+      slot = nfull + ((int64_t)(t - p.tail_start) * S + s) * p.tail_f + part;
+    }
+    stream_item<F16, MODE, WAVES>(p, ring, ridx, t, s, part, nparts, S, slot, p.single);
+  } else {
+    __shared__ int s_item;
+    const int N = p.gcounts[0] * p.T;
+    const int per = (N + 7) >> 3;
+    const int home = (int)(blockIdx.x & 7u);
+    for (;;) {
+      if (threadIdx.x == 0) {
+        int it = -1;
+        for (int q = 0; q < 8 && it < 0; ++q) {
+          const int x = (home + q) & 7;
+          const int b = x * per, e = b + per < N ? b + per : N;
+          if (b >= e) continue;
+          const int v = __hip_atomic_fetch_add(p.queues + x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (v < e - b) it = b + v;
+        }
+        s_item = it;
+      }
+      __syncthreads();
+      const int i = s_item;
+      if (i < 0) break;
+      const GChunk c = p.chunks[i / p.T];
+      if (c.e >= 0) {
+        const int t = i % p.T;
+        const Matrix mat{c.tok_begin, c.count < kChunkTokens ? c.count : kChunkTokens,
+                         p.h0 + (int64_t)c.e * p.h_stride};
+        stream_item<F16, MODE, WAVES>(p, ring, ridx, t, 0, 0, 1, 1, c.sbase < 0 ? -1 : c.sbase + t, mat);
+      }
+      __syncthreads();   // the ring, the row cache and s_item are free for the next item
+    }
+  }
+}
+
 // Finishes the streaming kernel's tiles: for each tile the S split slots
 // are summed in split order (a tail tile's split being first the sum of its
 // tail_f part slots, in part order) and H is updated.  Workgroup
@@ -976,6 +1012,7 @@ __global__ __launch_bounds__(1024) void grouped_plan_kernel(const int64_t* __res
     gcounts[0] = base_c < max_chunks ? base_c : max_chunks;
     gcounts[1] = base_r < max_reduce ? base_r : max_reduce;
   }
+  if (tid < 8) gcounts[2 + tid] = 0;   // the stream kernel's work-queue counters
 }
 
 // Sums the S partial slots of a tile in split order and updates H.  Each
@@ -1269,7 +1306,7 @@ GroupedBounds grouped_bounds(int64_t n_rows, int E, int64_t d) {
   g.off_reds = off;
   off = align(off + (size_t)(g.max_reduce > 0 ? g.max_reduce : 1) * sizeof(GReduce));
   g.off_counts = off;
-  g.total = align(off + 2 * sizeof(int));
+  g.total = align(off + 10 * sizeof(int));   // chunk and reduce counts, 8 work-queue counters
   return g;
 }
 }  // namespace
@@ -1323,11 +1360,14 @@ extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype
   p.n_x = n_x;
   p.chunks = chunks;
   p.gcounts = counts;
+  p.queues = counts + 2;
   p.T = gb.T;
   p.h0 = h_dev;
   p.h_stride = h_stride;
+  // persistent workgroups, one per CU (no more than there are items)
   const int64_t items = (int64_t)gb.max_chunks * gb.T;
-  const unsigned grid = (unsigned)(8 * ((items + 7) / 8));
+  const int cus = device_cus();
+  const unsigned grid = (unsigned)(items < cus ? items : cus);
   const bool f16 = dtype == MI355Q_F16;
   if (rows_dev) {
     if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGroupedGather, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
