@@ -80,7 +80,7 @@ def _solve_vs_oracle(dev, W, X, qa, oa, tag, rows_frac=0.01):
 # Longer rows (14336 columns) and finer grids (int8) give each row more
 # chances to meet a rounding boundary: the oracle against itself with only
 # its Cholesky chain's fp32 order changed (flip identity or fp64) diverges in
-# 172-190 of 14336 rows (1.2-1.3 %) at the W8A8 shape and in 57-68 of 4096
+# 172-190 of 14336 rows (1.2-1.3 %) at the W8A8 shape and in 57-69 of 4096
 # rows (1.4-1.7 %, codes up to 3 apart) at the down projection's
 # (tests/gptq_code_spread.py --configs, seeds 4 and 9).  Those two allow
 # 2.5 % of the rows to diverge; agreement >= 99.9 %, +-1 first divergences
