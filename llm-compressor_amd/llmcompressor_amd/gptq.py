@@ -29,7 +29,7 @@ logger = logging.getLogger("llmcompressor_amd")
 GPTQ_PRECISION = torch.float32
 
 __all__ = ["make_empty_hessian", "accumulate_hessian", "quantize_weight", "symmetrize_hessian",
-           "GPTQResult", "gptq_quantize", "gptq_quantize_batched", "PreparedHessian", "prepare_hessian",
+           "GPTQResult", "GPTQBatch", "gptq_quantize", "gptq_quantize_batched", "PreparedHessian", "prepare_hessian",
            "prepare_hessians_batched"]
 
 
@@ -260,10 +260,28 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
                       perm=perm, codes=codes_out, hinv_ok=ok, global_scale=global_scale)
 
 
+@dataclass
+class GPTQBatch:
+    """The results of a batched solve as stacked tensors (member b at [b]):
+    loss and hinv_ok on the host [B], weight [B, rows, cols], scale and
+    zero_point [B, rows, groups] (TENSOR: [B, 1, 1]), codes [B, rows, cols],
+    g_idx [B, cols] or [cols] or None, perm [B, cols] or None, global_scale
+    [B] or None."""
+    loss: torch.Tensor
+    weight: torch.Tensor
+    scale: torch.Tensor
+    zero_point: torch.Tensor
+    g_idx: torch.Tensor | None
+    perm: torch.Tensor | None
+    codes: torch.Tensor
+    hinv_ok: torch.Tensor
+    global_scale: torch.Tensor | None = None
+
+
 def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, hessians: torch.Tensor,
                           num_samples=1.0, blocksize: int = 128, percdamp: float = 0.01,
                           observer: str = "memoryless_minmax",
-                          prepared: PreparedHessian | None = None) -> list[GPTQResult]:
+                          prepared: PreparedHessian | None = None, stacked: bool = False):
     """``gptq_quantize`` for B same-shaped modules at once (the experts of an
     MoE layer): weights [B, rows, cols], hessians [B, cols, cols] (upper
     triangles), num_samples a number or [B].  Each module gets the result of
@@ -275,6 +293,8 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
     here on the stacked weights (its statistics are per row for channel and
     group strategies).  ``prepared`` (``prepare_hessians_batched`` on the same
     stack and args) is shared by projections with the same input (gate, up).
+    ``stacked`` returns one ``GPTQBatch`` of stacked tensors instead of the
+    list (no per-member Python objects).
     """
     from .observers import Observer
 
@@ -333,6 +353,9 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
     loss, ok = loss_ok[0], loss_ok[1] > 0
     for _ in range(int((~ok).sum())):
         _hinv_fallback_warning()
+    if stacked:
+        return GPTQBatch(loss=loss, weight=w_out, scale=scale, zero_point=zero_point, g_idx=g_idx, perm=perm,
+                         codes=codes_out, hinv_ok=ok, global_scale=global_scale)
     out = []
     for b in range(B):
         sb, zb = scale[b], zero_point[b]

@@ -470,10 +470,18 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
             for mods in roles:
                 for m in mods:     # statistics from an earlier observe() are not used
                     m.weight_observer.delete_statistics(check_fused=False)
-                res = gptq_quantize_batched(torch.stack([m.weight for m in mods]), qa, fam.H, num_samples=ns,
-                                            blocksize=self.block_size, percdamp=self.dampening_frac,
-                                            observer="memoryless_minmax", prepared=prep)
-                self._write_back(mods, res, qa)
+            # the roles sharing this Hessian (gate and up) as one stack of
+            # rows: rows are independent given Hinv and their own scales
+            stacks = [torch.stack([m.weight for m in mods]) for mods in roles]
+            bounds = [0]
+            for w in stacks:
+                bounds.append(bounds[-1] + w.shape[1])
+            res = gptq_quantize_batched(stacks[0] if len(stacks) == 1 else torch.cat(stacks, dim=1), qa, fam.H,
+                                        num_samples=ns, blocksize=self.block_size, percdamp=self.dampening_frac,
+                                        observer="memoryless_minmax", prepared=prep, stacked=True)
+            del stacks
+            for r, mods in enumerate(roles):
+                self._write_back(mods, res, bounds[r], bounds[r + 1], qa)
             dt = (time.perf_counter() - t0) / max(1, sum(len(r) for r in roles))
             for mods in roles:
                 for m in mods:
@@ -481,23 +489,22 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
                     del self._num_samples[m]
                     self._hessians.pop(m, None)
             logger.info("Quantized %d modules of %s together, loss %.4f", sum(len(r) for r in roles), fam.key,
-                        sum(r.loss for r in res))
+                        float(res.loss.sum()))
             fam.release()
             done.update(leaders)
         return done
 
     @staticmethod
-    def _write_back(mods, res, qa):
-        """Parameters of a batched solve written in a few multi-tensor copies."""
+    def _write_back(mods, res, a: int, b: int, qa):
+        """Rows a .. b - 1 of a stacked batched solve (``GPTQBatch``) written
+        into the modules' parameters in a few multi-tensor copies."""
         with torch.no_grad():
-            torch._foreach_copy_([m.weight.data for m in mods], [r.weight for r in res])
+            torch._foreach_copy_([m.weight.data for m in mods], list(res.weight[:, a:b].unbind(0)))
             dt = mods[0].weight.dtype
-            scale = torch.stack([r.scale for r in res]).to(dt)
-            zp = torch.stack([r.zero_point for r in res]).to(qa.zp_dtype)
-            update = {"weight_scale": scale.unbind(0), "weight_zero_point": zp.unbind(0)}
+            update = {"weight_scale": res.scale[:, a:b].to(dt).unbind(0),
+                      "weight_zero_point": res.zero_point[:, a:b].to(qa.zp_dtype).unbind(0)}
             if qa.actorder == ActivationOrdering.GROUP:
-                g_idx, perm = torch.stack([r.g_idx for r in res]), torch.stack([r.perm for r in res])
-                update["weight_g_idx"] = torch.gather(g_idx, 1, torch.argsort(perm, dim=1)).unbind(0)
+                update["weight_g_idx"] = torch.gather(res.g_idx, 1, torch.argsort(res.perm, dim=1)).unbind(0)
             for k, vals in update.items():
                 ps = [getattr(m, k, None) for m in mods]
                 if all(isinstance(p, torch.Tensor) and p.shape == v.shape for p, v in zip(ps, vals)):
@@ -505,8 +512,8 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
                 else:
                     for m, v in zip(mods, vals):
                         _update_parameter(m, k, v)
-        for m, r in zip(mods, res):
-            m.gptq_codes = r.codes
+        for m, c in zip(mods, res.codes[:, a:b].unbind(0)):
+            m.gptq_codes = c
 
     def _compress_one(self, module, H, n, prepared):
         """GPTQ of one module; ``prepared`` caches the Cholesky chain of a

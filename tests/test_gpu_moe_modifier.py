@@ -75,7 +75,7 @@ def test_moe_experts_through_gptq_modifier_vs_oracle(dev, monkeypatch, calibrate
     real = modifiers.gptq_quantize_batched
 
     def counting(weights, *a, **k):
-        batched.append(weights.shape[0])
+        batched.append(tuple(weights.shape))
         return real(weights, *a, **k)
 
     monkeypatch.setattr(modifiers, "gptq_quantize_batched", counting)
@@ -109,7 +109,8 @@ def test_moe_experts_through_gptq_modifier_vs_oracle(dev, monkeypatch, calibrate
     torch.cuda.synchronize()
     for h in hooks:
         h.remove()
-    assert batched == [E, E, E]               # gate, up (one shared Hessian each) and down
+    # gate and up (one shared Hessian) as one stack of rows, then down
+    assert batched == [(E, 2 * INTER, HIDDEN), (E, HIDDEN, INTER)]
     assert set(hess) == {"experts.*.gate_proj", "experts.*.down_proj"}   # up shares gate's
     oa = OArgs(num_bits=4, strategy="group", group_size=128, actorder="weight")
     counts = [seen[f"experts.{e}.gate_proj"] for e in range(E)]
