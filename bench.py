@@ -686,11 +686,14 @@ def bench_decoder(a):
             Hs.append(H)
         ev[1].record()
         for (names, _), H in zip(groups, Hs):
-            prep = gptq.prepare_hessian(H, qa, float(batches))   # shared by modules with the same input
-            for nm in names:
-                obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
-                obs(lin[nm].weight)
-                gptq.gptq_quantize(lin[nm].weight, qa, H, obs, num_samples=float(batches), prepared=prep)
+            # modules with the same input share the Hessian and its Cholesky
+            # chain, and are solved as one stack of rows (rows are independent
+            # given Hinv and their own scales)
+            prep = gptq.prepare_hessian(H, qa, float(batches))
+            w = lin[names[0]].weight if len(names) == 1 else torch.cat([lin[nm].weight for nm in names])
+            obs = Observer.load_from_registry("memoryless_minmax", base_name="weight", args=qa)
+            obs(w)
+            gptq.gptq_quantize(w, qa, H, obs, num_samples=float(batches), prepared=prep)
         ev[2].record()
 
     ms, _ = _timed(torch, step, a.steps, a.warmup)

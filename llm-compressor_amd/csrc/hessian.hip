@@ -771,7 +771,20 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
     int t, s, part = 0, nparts = 1;
     int64_t slot;
     const int64_t nfull = (int64_t)p.tail_start * S;
-    if ((int64_t)blockIdx.x < nfull) {
+    if (S < 8) {
+      // Fewer splits than XCDs (large d, short calls): XCD x (= blockIdx % 8)
+      // takes split x % S and the (x / S)-th of 8 / S contiguous runs of its
+      // tiles, so the tiles resident on one XCD at once are neighbours in
+      // super-block order and share their feature slices in that XCD's L2
+      // (tiles strided across XCDs shared none).
+      const int G = 8 / S;
+      const int x = (int)(blockIdx.x & 7u), k = (int)(blockIdx.x >> 3);
+      const int per = (p.tail_start + G - 1) / G;   // tail_start = T: no tail parts below 8 splits
+      s = x % S;
+      t = (x / S) * per + k;
+      if (k >= per || t >= p.tail_start) return;
+      slot = S > 1 ? (int64_t)t * S + s : -1;
+    } else if ((int64_t)blockIdx.x < nfull) {
       s = blockIdx.x % S;
       t = blockIdx.x / S;
       slot = (S > 1) ? (int64_t)t * S + s : -1;
@@ -1146,6 +1159,14 @@ DensePlan plan_dense(int64_t n, int64_t d) {
   const int64_t ntail = (int64_t)(pl.T - pl.tail_start) * pl.S;
   pl.grid = nfull + ntail * pl.tail_f;
   pl.slots = pl.S > 1 ? pl.grid : 0;
+  if (pl.S < kXcds && tile_edge(d) == 256) {
+    // fewer splits than XCDs: each split's tiles in 8 / S contiguous runs,
+    // one per XCD (the stream kernel's dense decode; the 128-tile kernel of
+    // d < 512 keeps one item per workgroup in item order)
+    const int G = kXcds / pl.S;
+    pl.grid = (int64_t)kXcds * ((pl.T + G - 1) / G);
+    pl.slots = pl.S > 1 ? (int64_t)pl.T * pl.S : 0;
+  }
   return pl;
 }
 
