@@ -34,7 +34,11 @@ typedef enum {
   MI355Q_INVALID_ARGUMENT = 1,
   MI355Q_UNSUPPORTED = 2,
   MI355Q_NOT_POSITIVE_DEFINITE = 3,
-  MI355Q_HIP_ERROR = 4
+  MI355Q_HIP_ERROR = 4,
+  /* a per-matrix status of the hinv entry points: the factorisation's
+     workgroups stopped waiting for each other (results invalid; the caller
+     raises instead of falling back) */
+  MI355Q_TIMEOUT = 5
 } mi355q_status;
 
 typedef enum { MI355Q_BF16 = 0, MI355Q_F32 = 1, MI355Q_F16 = 2 } mi355q_dtype;

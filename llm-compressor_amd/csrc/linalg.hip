@@ -781,6 +781,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(GemmArgs g)
       }
 }
 
+// Global-memory pointers of the dataflow factorisation's task functions
+// carry their address space: through generic pointers every access becomes
+// a flat instruction, which also counts against the LDS counter, so waiting
+// for an LDS read would wait for the tile fetches in flight.
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) int32_t gint;
+__device__ __forceinline__ void store4(float* p, const f32x4_t& v) { *reinterpret_cast<f32x4_t*>(p) = v; }
+__device__ __forceinline__ void store4(gfloat* p, const f32x4_t& v) {
+  *reinterpret_cast<__attribute__((address_space(1))) f32x4_t*>(p) = v;
+}
+
 // ---------------------------------------------------------------- Cholesky pieces
 constexpr int NB = 128;        // panel width
 constexpr int SB = 32;         // register-resident sub-block of the diagonal kernel
@@ -827,12 +838,10 @@ __device__ __forceinline__ f32x4_t zero4() {
   return z;
 }
 
-// Inverse X = L^-1 of the lower Cholesky factor of the NB x NB diagonal
-// block at (k0, k0) of F, into linv (NB x NB, zeros above the diagonal).
-// nb <= NB is the block size; rows / columns beyond nb are padded with the
-// identity so the whole NB block factors uniformly.  L itself is not
-// written back: the blocked Cholesky only consumes L^-1 (panel solves and
-// the triangular inverse) and the off-diagonal panels.
+// Inverse X = L^-1 of the lower Cholesky factor of an NB x NB diagonal
+// block.  L itself is not written back: the blocked Cholesky only consumes
+// L^-1 (panel solves and the triangular inverse) and the off-diagonal
+// panels.
 //
 // The block is processed in 32-wide steps.  Wave 0 factors the 32 x 32
 // diagonal sub-block in registers and inverts it on the way; all four waves
@@ -842,52 +851,18 @@ __device__ __forceinline__ f32x4_t zero4() {
 // inverse is assembled from the four sub-block inverses by two doubling
 // steps, inv([[A,0],[B,C]]) = [[A^-1,0],[-C^-1 B A^-1, C^-1]], partly under
 // the last factorisations.
-__global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t ldf, int64_t k0, int nb,
-                                                        float* linv, int32_t* status, int64_t wsf) {
-  __shared__ float a[NB * LP];
-  __shared__ float x[NB * LP];
-  // product scratch: rows 0..63 the first level-2 product (and, earlier, the
-  // pair (0, 1) in rows 32..63), rows 64..95 the pair (2, 3)
-  __shared__ __attribute__((aligned(16))) float t[3 * SB * LT];
-  __shared__ __attribute__((aligned(16))) float cb[2 * SB];  // column broadcast of the factorisation
+//
+// On entry `a` (NB x NB, row
+// stride LP, LDS) holds the lower triangle of the block with zeros above,
+// visible to the whole workgroup; on exit the rows of L^-1 (zeros above the
+// diagonal) are in `out` (row stride ldo) and in `x` (LDS, row stride LP;
+// x's strictly upper 32 x 32 sub-blocks are never written).  `t` and `cb`
+// are scratch (3 SB LT and 2 SB floats, 16-byte aligned).  Every thread of
+// the PNT-thread workgroup calls it.
+template <typename OutPtr>
+__device__ __forceinline__ void potf2_inv_lds(float* a, float* x, float* t, float* cb, OutPtr out, int64_t ldo,
+                                              int32_t* status) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // matrix blockIdx.x of a batch: workspaces wsf floats apart
-  F += (int64_t)blockIdx.x * wsf;
-  linv += (int64_t)blockIdx.x * wsf;
-  status += blockIdx.x;
-
-  // load the lower triangle (zeros above): thread tid covers columns
-  // 4 (tid % 32) .. + 3 of rows 8 v + tid / 32
-  if (nb == NB && (ldf & 3) == 0) {
-    const int i0 = tid >> 5, j = 4 * (tid & 31);
-    const float* src = F + (k0 + i0) * ldf + k0 + j;
-    f32x4_t lv[NB * NB / (4 * PNT)];
-#pragma unroll
-    for (int v = 0; v < NB * NB / (4 * PNT); ++v) lv[v] = *reinterpret_cast<const f32x4_t*>(src + 8 * v * ldf);
-#pragma unroll
-    for (int v = 0; v < NB * NB / (4 * PNT); ++v) {
-      const int i = 8 * v + i0;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) a[i * LP + j + c] = (j + c <= i) ? lv[v][c] : 0.f;
-    }
-  } else {
-    // ragged block: addresses clamped into the block, identity padding
-    float lv[NB * NB / PNT];
-#pragma unroll
-    for (int v = 0; v < NB * NB / PNT; ++v) {
-      const int e = v * PNT + tid;
-      const int i = min(e / NB, nb - 1), j = min(e % NB, nb - 1);
-      lv[v] = F[(k0 + i) * ldf + (k0 + j)];
-    }
-#pragma unroll
-    for (int v = 0; v < NB * NB / PNT; ++v) {
-      const int e = v * PNT + tid;
-      const int i = e / NB, j = e % NB;
-      a[i * LP + j] = (i < nb && j < nb && j <= i) ? lv[v] : ((i == j) ? 1.f : 0.f);
-    }
-  }
-  __syncthreads();
-
   // pivot check, off the dependency chain: every pivot positive and finite
   // (denormals included), tested on the bits of the wave-uniform pivot with
   // integer compares, which run on the scalar unit beside the column updates
@@ -1053,7 +1028,7 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
       f32x4_t o4;
 #pragma unroll
       for (int c = 0; c < 4; ++c) o4[c] = (j + c <= i) ? x[i * LP + j + c] : 0.f;
-      *reinterpret_cast<f32x4_t*>(linv + i * NB + j) = o4;
+      store4(out + i * ldo + j, o4);
     }
   };
 
@@ -1148,6 +1123,570 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
   store_rows(2 * SB, tid, PNT);
 }
 
+// The diagonal block at (k0, k0) of F into linv (NB x NB, zeros above the
+// diagonal).  nb <= NB is the block size; rows / columns beyond nb are
+// padded with the identity so the whole NB block factors uniformly.
+__global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t ldf, int64_t k0, int nb,
+                                                        float* linv, int32_t* status, int64_t wsf) {
+  __shared__ float a[NB * LP];
+  __shared__ float x[NB * LP];
+  // product scratch: rows 0..63 the first level-2 product (and, earlier, the
+  // pair (0, 1) in rows 32..63), rows 64..95 the pair (2, 3)
+  __shared__ __attribute__((aligned(16))) float t[3 * SB * LT];
+  __shared__ __attribute__((aligned(16))) float cb[2 * SB];  // column broadcast of the factorisation
+  const int tid = threadIdx.x;
+  // matrix blockIdx.x of a batch: workspaces wsf floats apart
+  F += (int64_t)blockIdx.x * wsf;
+  linv += (int64_t)blockIdx.x * wsf;
+  status += blockIdx.x;
+
+  // load the lower triangle (zeros above): thread tid covers columns
+  // 4 (tid % 32) .. + 3 of rows 8 v + tid / 32
+  if (nb == NB && (ldf & 3) == 0) {
+    const int i0 = tid >> 5, j = 4 * (tid & 31);
+    const float* src = F + (k0 + i0) * ldf + k0 + j;
+    f32x4_t lv[NB * NB / (4 * PNT)];
+#pragma unroll
+    for (int v = 0; v < NB * NB / (4 * PNT); ++v) lv[v] = *reinterpret_cast<const f32x4_t*>(src + 8 * v * ldf);
+#pragma unroll
+    for (int v = 0; v < NB * NB / (4 * PNT); ++v) {
+      const int i = 8 * v + i0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) a[i * LP + j + c] = (j + c <= i) ? lv[v][c] : 0.f;
+    }
+  } else {
+    // ragged block: addresses clamped into the block, identity padding
+    float lv[NB * NB / PNT];
+#pragma unroll
+    for (int v = 0; v < NB * NB / PNT; ++v) {
+      const int e = v * PNT + tid;
+      const int i = min(e / NB, nb - 1), j = min(e % NB, nb - 1);
+      lv[v] = F[(k0 + i) * ldf + (k0 + j)];
+    }
+#pragma unroll
+    for (int v = 0; v < NB * NB / PNT; ++v) {
+      const int e = v * PNT + tid;
+      const int i = e / NB, j = e % NB;
+      a[i * LP + j] = (i < nb && j < nb && j <= i) ? lv[v] : ((i == j) ? 1.f : 0.f);
+    }
+  }
+  __syncthreads();
+  potf2_inv_lds(a, x, t, cb, linv, NB, status);
+}
+
+// ---------------------------------------------------------------- dataflow Cholesky + inverse
+// For d a multiple of NB, one persistent launch does the work of the blocked
+// chain and of the doubling inverse: it factors F = L L^T in NB x NB tiles
+// and builds X = L^-1 alongside, with no launch boundary between dependent
+// steps (each costs about 4 us on gfx950, and the chain is a sequence of
+// small dependent steps).  For tile (i, j), i >= j, of matrix b:
+//   chain (one workgroup per matrix: the critical path), j = 0, 1, ...:
+//     A_jj -= L_{j,j-1} L_{j,j-1}^T (its last update; the earlier ones come
+//     accumulated by a helper), factor and invert it into X_jj = L_jj^-1,
+//     then L_{j+1,j} = A_{j+1,j} X_jj^T (A_{j+1,j} accumulated by a helper),
+//     kept in LDS for the next diagonal update;
+//   H(i, c), helper: A_ic -= sum_{k < kend} L_ik L_ck^T, kend = c - 1 on the
+//     diagonal (the chain applies k = c - 1) and c below it; for i >= c + 2
+//     then L_ic = A_ic X_cc^T;
+//   V(c, j), helper: X_cj = -X_cc sum_{k=j}^{c-1} L_ck X_kj.
+// Helpers take tasks from one counter in an order where every input comes
+// earlier - level c: H(c, c) and H(c+1, c) (the chain's inputs), H(c+2.., c),
+// then V(c, 0..c-1), the chain's step c counted right after H(c+1, c) - so
+// the earliest unfinished task always has its inputs: the launch needs no
+// co-residency beyond one helper next to the chains.  A tile is published by
+// a release store of its flag after its data; consumers poll with relaxed
+// loads and acquire once.  Every wait is bounded: past `timeout` wall-clock
+// ticks the waiter marks its matrix MI355Q_TIMEOUT and raises the abort word,
+// after which every wait returns at once and all workgroups drain.
+//
+// Flags (int32, per matrix in its workspace): lf[i T + j] = 1 when tile
+// (i, j) of F holds A accumulated as the chain consumes it, 2 when it holds
+// L_ij (i > j) or X_jj is in X (i == j); xf[i T + j] = 1 when X_ij (i > j)
+// is in X.  Matrix 0's area also holds the task counter and the abort word.
+constexpr int DSM = 2 * NB * LP + 3 * SB * LT + 2 * SB;  // LDS floats (157 KB: one workgroup per CU)
+
+constexpr int DLB = NB + 32;                             // LDS row stride of [k][n] tiles
+constexpr int DAG_LF_ACC = 1, DAG_LF_FINAL = 2;
+
+struct DagParams {
+  float* F;          // workspaces, wsf floats apart
+  float* X;
+  int32_t* flags;    // 2 T^2 flags per matrix (wsf apart), then matrix 0's counter and abort word
+  int32_t* status;   // [batch]
+  int64_t d, wsf;
+  int T, batch, ntasks;
+  uint64_t timeout;  // wall-clock ticks per wait
+};
+
+// thread tid's share of a 128 x 128 global tile: float4 v at row 8 v + tid / 32, columns 4 (tid % 32)
+__device__ __forceinline__ void dag_fetch(const gfloat* g, int64_t ld, f32x4_t (&v)[16]) {
+  typedef __attribute__((address_space(1))) const f32x4_t gf4;
+  const int tid = threadIdx.x;
+  const gfloat* p = g + (tid >> 5) * ld + 4 * (tid & 31);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = *reinterpret_cast<gf4*>(p + 8 * i * ld);
+}
+// ... into LDS as [r][k] (row stride LP)
+__device__ __forceinline__ void dag_put_rk(const f32x4_t (&v)[16], float* l) {
+  const int tid = threadIdx.x, r0 = tid >> 5, c = 4 * (tid & 31);
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) l[(8 * i + r0) * LP + c + e] = v[i][e];
+}
+// ... into LDS as [k][n] (row stride DLB)
+__device__ __forceinline__ void dag_put_kn(const f32x4_t (&v)[16], float* l) {
+  const int tid = threadIdx.x, r0 = tid >> 5, c = 4 * (tid & 31);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) *reinterpret_cast<f32x4_t*>(l + (8 * i + r0) * DLB + c) = v[i];
+}
+
+// 128 x 128 accumulator over four waves: wave (wm, wn) holds the 64 x 64
+// quadrant (wm, wn) as 2 x 2 fp32 32x32 MFMA tiles; element r of tile
+// (bm, bn) is row 64 wm + 32 bm + 8 (r / 4) + 4 (lane / 32) + r % 4, column
+// 64 wn + 32 bn + lane % 32.
+struct DagAcc {
+  f32x16_t t[2][2];
+};
+template <typename Fn>
+__device__ __forceinline__ void dag_each(Fn&& fn) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+  for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        fn(bm, bn, r, wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), wn * 64 + bn * 32 + (lane & 31));
+}
+__device__ __forceinline__ void dag_zero(DagAcc& acc) {
+  dag_each([&](int bm, int bn, int r, int, int) { acc.t[bm][bn][r] = 0.f; });
+}
+__device__ __forceinline__ void dag_load_acc(DagAcc& acc, const gfloat* g, int64_t ld) {
+  dag_each([&](int bm, int bn, int r, int row, int col) { acc.t[bm][bn][r] = g[row * ld + col]; });
+}
+__device__ __forceinline__ void dag_store_acc(const DagAcc& acc, gfloat* g, int64_t ld) {
+  dag_each([&](int bm, int bn, int r, int row, int col) { g[row * ld + col] = acc.t[bm][bn][r]; });
+}
+
+// acc += sign * A op(B): A in LDS as [r][k] (stride LP); B as [k][n]
+// (stride DLB) if BKN, else as [n][k] (stride LP); K = 128.  Operands of
+// step kk + 1 are read while the MFMAs of step kk run.
+template <bool BKN>
+__device__ __forceinline__ void dag_mma(DagAcc& acc, const float* la, const float* lb, float sign) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), wm = wave >> 1, wn = wave & 1;
+  const float* pa = la + (wm * 64 + (lane & 31)) * LP + (lane >> 5);
+  const float* pb = BKN ? lb + (lane >> 5) * DLB + wn * 64 + (lane & 31) : lb + (wn * 64 + (lane & 31)) * LP + (lane >> 5);
+  for (int c = 0; c < NB / 32; ++c) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int k2 = 32 * c + 2 * q;
+      const float a0 = sign * pa[k2], a1 = sign * pa[32 * LP + k2];
+      const float b0 = BKN ? pb[k2 * DLB] : pb[k2], b1 = BKN ? pb[k2 * DLB + 32] : pb[32 * LP + k2];
+      acc.t[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc.t[0][0], 0, 0, 0);
+      acc.t[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc.t[0][1], 0, 0, 0);
+      acc.t[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc.t[1][0], 0, 0, 0);
+      acc.t[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc.t[1][1], 0, 0, 0);
+    }
+  }
+}
+
+// The chain's two products, shaped by the triangles.  Sub-diagonal solve
+// L = A X^T with X lower triangular: out[r][n] = sum_{k < 32 (n / 32 + 1)}
+// A[r][k] X[n][k]; wave (wm, wn) holds row blocks 2 wm, 2 wm + 1 and column
+// blocks 3 - wn, wn (K = 128 + 32 or 96 + 64: equal work per wave).
+template <typename Fn>
+__device__ __forceinline__ void dag_each_tri(Fn&& fn) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+  for (int bm = 0; bm < 2; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < 2; ++bn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        fn(bm, bn, r, wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3),
+           32 * (bn == 0 ? 3 - wn : wn) + (lane & 31));
+}
+__device__ __forceinline__ void dag_mma_tri(DagAcc& acc, const float* la, const float* x) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), wm = wave >> 1, wn = wave & 1;
+  const int ca = 3 - wn, cbk = wn;
+  const float* pa = la + (wm * 64 + (lane & 31)) * LP + (lane >> 5);
+  const float* pba = x + (32 * ca + (lane & 31)) * LP + (lane >> 5);
+  const float* pbb = x + (32 * cbk + (lane & 31)) * LP + (lane >> 5);
+  // K in chunks of 32 (16 MFMA steps): both column blocks while the
+  // shorter one lasts, then the longer one alone.  The operands of step
+  // k + 1 are read while the MFMAs of step k run (one read after each MFMA).
+  float f[2][4];
+  auto rd = [&](int k2, float* g) __attribute__((always_inline)) {
+    g[0] = pa[k2];
+    g[1] = pa[32 * LP + k2];
+    g[2] = pba[k2];
+    g[3] = pbb[k2];
+  };
+  rd(0, f[0]);
+  for (int c = 0; c <= cbk; ++c) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const float* cur = f[q & 1];
+      float* nxt = f[(q + 1) & 1];
+      rd(32 * c + 2 * q + 2, nxt);  // (past the short block: read, unused)
+      acc.t[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[0], cur[2], acc.t[0][0], 0, 0, 0);
+      acc.t[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[0], cur[3], acc.t[0][1], 0, 0, 0);
+      acc.t[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[1], cur[2], acc.t[1][0], 0, 0, 0);
+      acc.t[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[1], cur[3], acc.t[1][1], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+  }
+  for (int c = cbk + 1; c <= ca; ++c) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const float* cur = f[q & 1];
+      float* nxt = f[(q + 1) & 1];
+      if (c < ca || q < 15) {
+        const int k2 = 32 * c + 2 * q + 2;
+        nxt[0] = pa[k2];
+        nxt[1] = pa[32 * LP + k2];
+        nxt[2] = pba[k2];
+      }
+      acc.t[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[0], cur[2], acc.t[0][0], 0, 0, 0);
+      acc.t[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur[1], cur[2], acc.t[1][0], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  }
+}
+
+// Diagonal update C -= L L^T on the lower 32 x 32 blocks (rb >= cb), three
+// per wave: (3,0) (3,1) (3,2) | (3,3) (2,0) (2,1) | (2,2) (1,0) - | (1,1)
+// (0,0) -; the last two waves repeat a block they discard.
+struct DagSyrk {
+  f32x16_t t[3];
+};
+__device__ __forceinline__ int dag_syrk_rb(int wave, int i) {
+  return wave == 0 ? 3 : wave == 1 ? (i == 0 ? 3 : 2) : wave == 2 ? (i == 0 ? 2 : 1) : (i == 0 ? 1 : 0);
+}
+__device__ __forceinline__ int dag_syrk_cb(int wave, int i) {
+  return wave == 0 ? i : wave == 1 ? (i == 0 ? 3 : i - 1) : wave == 2 ? (i == 0 ? 2 : 0) : (i == 0 ? 1 : 0);
+}
+template <typename Fn>
+__device__ __forceinline__ void dag_each_syrk(Fn&& fn) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nblk = wave < 2 ? 3 : 2;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      fn(i, r, i < nblk, 32 * dag_syrk_rb(wave, i) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3),
+         32 * dag_syrk_cb(wave, i) + (lane & 31));
+}
+__device__ __forceinline__ void dag_mma_syrk(DagSyrk& acc, const float* l) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const float* pa[3];
+  const float* pb[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    pa[i] = l + (32 * dag_syrk_rb(wave, i) + (lane & 31)) * LP + (lane >> 5);
+    pb[i] = l + (32 * dag_syrk_cb(wave, i) + (lane & 31)) * LP + (lane >> 5);
+  }
+  float f[2][6];
+  auto rd = [&](int k2, float* g) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      g[i] = pa[i][k2];
+      g[3 + i] = pb[i][k2];
+    }
+  };
+  rd(0, f[0]);
+  for (int c = 0; c < NB / 32; ++c) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const float* cur = f[q & 1];
+      float* nxt = f[(q + 1) & 1];
+      if (c < NB / 32 - 1 || q < 15) rd(32 * c + 2 * q + 2, nxt);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) acc.t[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(-cur[i], cur[3 + i], acc.t[i], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+    }
+  }
+}
+
+// Publish: every wave's stores complete and written back, then the flag.
+__device__ __forceinline__ void dag_publish(gint* flag, int v) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One LDS allocation shared by the task functions below (157 KB: one
+// workgroup per CU); separate functions keep the chain's register
+// allocation apart from the helpers'.
+__shared__ __attribute__((aligned(16))) float dag_smem[DSM];
+__shared__ int dag_word;
+
+// Wait until *flag >= v; false when the wait was abandoned (time-out or
+// abort).  Thread 0 polls; the workgroup leaves together.
+__device__ __forceinline__ bool dag_wait(const gint* flag, int v, const DagParams& p, int b) {
+  if (threadIdx.x == 0) {
+    gint* abort_word = (gint*)p.flags + 2 * p.T * p.T + 1;
+    int ok = 1;
+    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < v) {
+      const uint64_t t0 = wall_clock64();
+      for (;;) {
+        __builtin_amdgcn_s_sleep(1);
+        if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= v) break;
+        if (__hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+          p.status[b] = MI355Q_TIMEOUT;  // this matrix's results are incomplete too
+          ok = 0;
+          break;
+        }
+        if (wall_clock64() - t0 > p.timeout) {
+          p.status[b] = MI355Q_TIMEOUT;
+          __hip_atomic_store(abort_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0;
+          break;
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    dag_word = ok;
+  }
+  __syncthreads();
+  const bool ok = dag_word != 0;
+  __syncthreads();
+  return ok;
+}
+
+__device__ __forceinline__ gfloat* dag_tile(float* base, const DagParams& p, int b, int i, int j) {
+  return (gfloat*)base + (int64_t)b * p.wsf + (int64_t)i * NB * p.d + (int64_t)j * NB;
+}
+__device__ __forceinline__ gint* dag_lf(const DagParams& p, int b) { return (gint*)p.flags + (int64_t)b * p.wsf; }
+
+// The chain of matrix b.
+__device__ __noinline__ void dag_chain(DagParams p, int b) {
+  const int T = p.T;
+  const int64_t d = p.d;
+  gint* lf = dag_lf(p, b);
+  float* a = dag_smem;
+  float* x = dag_smem + NB * LP;
+  float* t = dag_smem + 2 * NB * LP;
+  float* cb = t + 3 * SB * LT;
+  f32x4_t v[16];
+  DagAcc acc;
+  DagSyrk sy;
+  for (int e = threadIdx.x; e < NB * LP; e += PNT) x[e] = 0.f;  // X_jj's upper blocks stay zero
+  {
+    dag_fetch(dag_tile(p.F, p, b, 0, 0), d, v);
+    const int r0 = threadIdx.x >> 5, c = 4 * (threadIdx.x & 31);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[(8 * i + r0) * LP + c + e] = (c + e <= 8 * i + r0) ? v[i][e] : 0.f;
+  }
+  __syncthreads();
+  for (int j = 0;; ++j) {
+    potf2_inv_lds(a, x, t, cb, dag_tile(p.X, p, b, j, j), d, p.status + b);
+    dag_publish(lf + j * T + j, DAG_LF_FINAL);
+    if (j + 1 == T) break;
+    // L_{j+1,j} = A_{j+1,j} X_jj^T; the diagonal tile's lower blocks are
+    // fetched meanwhile
+    if (j >= 1 && !dag_wait(lf + (j + 1) * T + j, DAG_LF_ACC, p, b)) break;
+    gfloat* lt = dag_tile(p.F, p, b, j + 1, j);
+    dag_fetch(lt, d, v);
+    dag_put_rk(v, a);
+    if (j + 1 >= 2 && !dag_wait(lf + (j + 1) * T + j + 1, DAG_LF_ACC, p, b)) break;
+    __syncthreads();  // a is written
+    {
+      const gfloat* dg = dag_tile(p.F, p, b, j + 1, j + 1);
+      dag_each_syrk([&](int i, int r, bool, int row, int col) { sy.t[i][r] = dg[row * d + col]; });
+    }
+    dag_zero(acc);
+    dag_mma_tri(acc, a, x);
+    dag_each_tri([&](int bm, int bn, int r, int row, int col) { lt[row * d + col] = acc.t[bm][bn][r]; });
+    __syncthreads();  // every wave is done reading a
+    dag_each_tri([&](int bm, int bn, int r, int row, int col) { a[row * LP + col] = acc.t[bm][bn][r]; });
+    dag_publish(lf + (j + 1) * T + j, DAG_LF_FINAL);
+    // A_{j+1,j+1} -= L_{j+1,j} L_{j+1,j}^T on the lower blocks, into a
+    dag_mma_syrk(sy, a);
+    __syncthreads();
+    dag_each_syrk([&](int i, int r, bool own, int row, int col) {
+      if (own) a[row * LP + col] = col <= row ? sy.t[i][r] : 0.f;
+    });
+    for (int e = threadIdx.x; e < 6 * 32 * 32; e += PNT) {  // the blocks above the diagonal
+      const int q = e >> 10, rr = (e >> 5) & 31, cc = e & 31;
+      const int rb = q < 3 ? 0 : q < 5 ? 1 : 2, cbb = q < 3 ? q + 1 : q < 5 ? q - 1 : 3;
+      a[(32 * rb + rr) * LP + 32 * cbb + cc] = 0.f;
+    }
+    __syncthreads();
+  }
+}
+
+// H(i, c): A_ic -= sum_{k < kend} L_ik L_ck^T, then L_ic = A_ic X_cc^T below
+// the sub-diagonal.  The tiles of step k + 1 are fetched while step k's
+// MFMAs run.
+__device__ __noinline__ void dag_task_h(DagParams p, int b, int i, int c) {
+  const int T = p.T;
+  const int64_t d = p.d;
+  gint* lf = dag_lf(p, b);
+  float* la = dag_smem;
+  float* lb = dag_smem + NB * LP;
+  f32x4_t va[16], vb[16];
+  DagAcc acc;
+  const int kend = i == c ? c - 1 : c;
+  gfloat* out = dag_tile(p.F, p, b, i, c);
+  dag_load_acc(acc, out, d);
+  auto ready = [&](int k) {
+    return dag_wait(lf + i * T + k, DAG_LF_FINAL, p, b) && dag_wait(lf + c * T + k, DAG_LF_FINAL, p, b);
+  };
+  if (kend > 0) {
+    if (!ready(0)) return;
+    dag_fetch(dag_tile(p.F, p, b, i, 0), d, va);
+    dag_fetch(dag_tile(p.F, p, b, c, 0), d, vb);
+  }
+  for (int k = 0; k < kend; ++k) {
+    dag_put_rk(va, la);
+    dag_put_rk(vb, lb);
+    __syncthreads();
+    if (k + 1 < kend) {
+      if (!ready(k + 1)) return;
+      dag_fetch(dag_tile(p.F, p, b, i, k + 1), d, va);
+      dag_fetch(dag_tile(p.F, p, b, c, k + 1), d, vb);
+    }
+    dag_mma<false>(acc, la, lb, -1.f);
+    __syncthreads();
+  }
+  if (i < c + 2) {
+    dag_store_acc(acc, out, d);
+    dag_publish(lf + i * T + c, DAG_LF_ACC);
+    return;
+  }
+  if (!dag_wait(lf + c * T + c, DAG_LF_FINAL, p, b)) return;
+  dag_fetch(dag_tile(p.X, p, b, c, c), d, vb);
+  dag_put_rk(vb, lb);
+  dag_each([&](int bm, int bn, int r, int row, int col) { la[row * LP + col] = acc.t[bm][bn][r]; });
+  __syncthreads();
+  dag_zero(acc);
+  dag_mma_tri(acc, la, lb);
+  dag_each_tri([&](int bm, int bn, int r, int row, int col) { out[row * d + col] = acc.t[bm][bn][r]; });
+  dag_publish(lf + i * T + c, DAG_LF_FINAL);
+}
+
+// V(c, j): X_cj = -X_cc sum_{k=j}^{c-1} L_ck X_kj (fetches of step k + 1
+// under step k's MFMAs).
+__device__ __noinline__ void dag_task_v(DagParams p, int b, int c, int j) {
+  const int T = p.T;
+  const int64_t d = p.d;
+  gint* lf = dag_lf(p, b);
+  gint* xf = lf + T * T;
+  float* la = dag_smem;
+  float* lb = dag_smem + NB * LP;
+  f32x4_t va[16], vb[16];
+  DagAcc acc;
+  dag_zero(acc);
+  auto ready = [&](int k) {
+    return dag_wait(lf + c * T + k, DAG_LF_FINAL, p, b) &&
+           (k == j ? dag_wait(lf + j * T + j, DAG_LF_FINAL, p, b) : dag_wait(xf + k * T + j, 1, p, b));
+  };
+  if (!ready(j)) return;
+  dag_fetch(dag_tile(p.F, p, b, c, j), d, va);
+  dag_fetch(dag_tile(p.X, p, b, j, j), d, vb);
+  for (int k = j; k < c; ++k) {
+    dag_put_rk(va, la);
+    dag_put_kn(vb, lb);
+    __syncthreads();
+    if (k + 1 < c) {
+      if (!ready(k + 1)) return;
+      dag_fetch(dag_tile(p.F, p, b, c, k + 1), d, va);
+      dag_fetch(dag_tile(p.X, p, b, k + 1, j), d, vb);
+    }
+    dag_mma<true>(acc, la, lb, 1.f);
+    __syncthreads();
+  }
+  if (!dag_wait(lf + c * T + c, DAG_LF_FINAL, p, b)) return;
+  dag_fetch(dag_tile(p.X, p, b, c, c), d, va);
+  dag_put_rk(va, la);
+  dag_each([&](int bm, int bn, int r, int row, int col) { lb[row * DLB + col] = acc.t[bm][bn][r]; });
+  __syncthreads();
+  dag_zero(acc);
+  dag_mma<true>(acc, la, lb, -1.f);
+  dag_store_acc(acc, dag_tile(p.X, p, b, c, j), d);
+  dag_publish(xf + c * T + j, 1);
+}
+
+// task index -> kind (0 chain, 1 H, 2 V), matrix b, tile (i, j).  Order:
+// chains 0..B-1, then levels c = 0, 1, ..., each with matrices 0..B-1, each
+// with H(i0.., c) then V(c, 0..c-1); level c has T - 2, T - 1, T tasks per
+// matrix for c = 0, 1, >= 2 (H(0,0), H(1,0), H(1,1) carry no work).
+__device__ __forceinline__ void dag_decode(int idx, int T, int B, int& kind, int& b, int& i, int& j) {
+  if (idx < B) {
+    kind = 0;
+    b = idx;
+    i = j = 0;
+    return;
+  }
+  int r = idx - B, c, nc;
+  if (r < B * (T - 2)) {
+    c = 0;
+    nc = T - 2;
+  } else if ((r -= B * (T - 2)) < B * (T - 1)) {
+    c = 1;
+    nc = T - 1;
+  } else {
+    r -= B * (T - 1);
+    c = 2 + r / (B * T);
+    r %= B * T;
+    nc = T;
+  }
+  b = r / nc;
+  const int u = r % nc, i0 = c < 2 ? 2 : c, nh = T - i0;
+  if (u < nh) {
+    kind = 1;
+    i = i0 + u;
+    j = c;
+  } else {
+    kind = 2;
+    i = c;
+    j = u - nh;
+  }
+}
+
+__global__ __launch_bounds__(PNT, 1) void chol_dag_kernel(DagParams p) {
+  int32_t* ctl = p.flags + 2 * p.T * p.T;
+  for (;;) {
+    if (threadIdx.x == 0) {
+      const bool aborted = __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+      dag_word = aborted ? p.ntasks : __hip_atomic_fetch_add(ctl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const int task = dag_word;
+    __syncthreads();
+    if (task >= p.ntasks) break;
+    int kind, b, i, j;
+    dag_decode(task, p.T, p.batch, kind, b, i, j);
+    if (kind == 0)
+      dag_chain(p, b);
+    else if (kind == 1)
+      dag_task_h(p, b, i, j);
+    else
+      dag_task_v(p, b, i, j);
+  }
+}
+
 // diag'[j] = H[p(j)][p(j)] / n with 0 -> 1 (dead), damp = percdamp * mean(diag')
 // (one workgroup per matrix of a batch)
 __global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t ldh, int64_t sh, int64_t d,
@@ -1183,10 +1722,15 @@ __global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t
 }
 
 // F (lower) = flip(permute(H / n)) with dead / damping rules on the diagonal.
+// Block (0, 0) of matrix z also clears the matrix's nflags dataflow flags
+// (flags + z wsf, int32).
 __global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t sh, int64_t d, const int32_t* perm,
                                     int64_t sp, const float* ns_arr, float ns0, const float* damp, float* F,
-                                    int64_t wsf, int vec) {
+                                    int64_t wsf, int vec, int32_t* flags, int nflags) {
   const int64_t bm = blockIdx.z;
+  if (flags && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int e = threadIdx.y * blockDim.x + threadIdx.x; e < nflags; e += blockDim.x * blockDim.y)
+      flags[bm * wsf + e] = 0;
   H += bm * sh;
   if (perm) perm += bm * sp;
   damp += bm * wsf;
@@ -1303,7 +1847,7 @@ __global__ void identity_on_failure_kernel(float* hinv, int64_t d, int64_t strid
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct HinvLayout {
-  size_t F, X, T, linv, damp, total;
+  size_t F, X, T, linv, damp, flags, total;
 };
 
 HinvLayout hinv_layout(int64_t d) {
@@ -1315,6 +1859,8 @@ HinvLayout hinv_layout(int64_t d) {
   L.T = off; off = align256(off + (size_t)(d * ((d + 1) / 2 + NB)) * sizeof(float));
   L.linv = off; off = align256(off + (size_t)nblk * NB * NB * sizeof(float));
   L.damp = off; off = align256(off + 64);
+  // dataflow factorisation: 2 T^2 tile flags, then (matrix 0) the task counter and abort word
+  L.flags = off; off = align256(off + (size_t)(2 * nblk * nblk + 2) * sizeof(int32_t));
   L.total = off;
   return L;
 }
@@ -1472,6 +2018,16 @@ extern "C" size_t mi355q_gptq_hinv_workspace_size(int64_t d) { return d > 0 ? hi
 namespace mi355q {
 namespace {
 
+// The dataflow factorisation takes orders that are multiples of NB with at
+// least 4 and at most 64 blocks (past that the blocked chain's large
+// products are at least as fast), in batches of at most 8 (one chain
+// workgroup per matrix).  MI355Q_HINV_DAG=0 in the environment turns it off.
+bool dag_eligible(int64_t d, int64_t batch) {
+  if (d % NB != 0 || d / NB < 4 || d / NB > 64 || batch > 8) return false;
+  const char* e = getenv("MI355Q_HINV_DAG");
+  return !(e && e[0] == '0');
+}
+
 // The hinv pipeline for `batch` matrices of order d: matrix b reads
 // H + b sh (and perm + b sp), writes hinv + b shinv, dead + b d, status[b],
 // and uses workspace bytes [b L.total, (b + 1) L.total).
@@ -1500,16 +2056,40 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
     return dim3((unsigned)((d + cpb - 1) / cpb), (unsigned)((d + 15) / 16), nb_);
   };
   const dim3 fb(64, 16);
+  const int64_t nblk = (d + NB - 1) / NB;
+  const bool dag = dag_eligible(d, batch);
+  int32_t* flags = reinterpret_cast<int32_t*>(ws + L.flags);
   hipLaunchKernelGGL(prepare_flip_kernel, grid_for(vin), fb, 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0, damp, F,
-                     wsf, vin ? 1 : 0);
+                     wsf, vin ? 1 : 0, dag ? flags : nullptr, (int)(2 * nblk * nblk + 2));
   MQ_LAUNCH_CHECK();
+  if (dag) {
+    DagParams p{};
+    p.F = F; p.X = X; p.flags = flags; p.status = status_dev;
+    p.d = d; p.wsf = wsf; p.T = (int)nblk; p.batch = (int)batch;
+    p.ntasks = (int)(batch * (nblk * nblk - 2));
+    int dev = 0, ncu = 0, khz = 0;
+    MQ_CHECK_HIP(hipGetDevice(&dev));
+    MQ_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    MQ_CHECK_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    // 2 s per wait; MI355Q_HINV_DAG_TIMEOUT_US overrides it (the tests force
+    // the time-out path with a tiny value)
+    uint64_t us = 2000000;
+    if (const char* e = getenv("MI355Q_HINV_DAG_TIMEOUT_US")) us = strtoull(e, nullptr, 10);
+    p.timeout = (uint64_t)(khz > 0 ? khz : 100000) * us / 1000ull;
+    const int grid = p.ntasks < ncu ? p.ntasks : ncu;
+    MQ_CHECK_ARG(grid > batch, "gptq_hinv: %d compute units leave no helper for %d chains", ncu, (int)batch);
+    hipLaunchKernelGGL(chol_dag_kernel, dim3((unsigned)grid), dim3(PNT), 0, st, p);
+    MQ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(flip_out_kernel, grid_for(vout), fb, 0, st, X, d, hinv_dev, wsf, shinv, vout ? 1 : 0);
+    MQ_LAUNCH_CHECK();
+    return MI355Q_OK;
+  }
 
   // blocked right-looking Cholesky on F (lower), two levels: inside an outer
   // panel of OUTB blocks each 128-column block updates only the panel's
   // remaining columns (K = 128); the trailing matrix past the panel takes
   // one rank-(OUTB * 128) lower-only update (K up to 512)
   constexpr int64_t OUTB = 4;
-  const int64_t nblk = (d + NB - 1) / NB;
   for (int64_t ob = 0; ob < nblk; ob += OUTB) {
     const int64_t oe = ob + OUTB < nblk ? ob + OUTB : nblk;
     const int64_t c0 = ob * NB, c_end = oe * NB < d ? oe * NB : d;

@@ -12,7 +12,7 @@ import torch
 
 from ._build import LIB_PATH
 
-OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_POSITIVE_DEFINITE, HIP_ERROR = 0, 1, 2, 3, 4
+OK, INVALID_ARGUMENT, UNSUPPORTED, NOT_POSITIVE_DEFINITE, HIP_ERROR, TIMEOUT = 0, 1, 2, 3, 4, 5
 BF16, F32, F16 = 0, 1, 2
 TENSOR, CHANNEL, GROUP, BLOCK, TOKEN = 0, 1, 2, 3, 4
 MX_RULE_CT, MX_RULE_OCP = 0, 1
@@ -121,6 +121,14 @@ def check(status: int) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args))
+
+
+def check_hinv_status(values) -> None:
+    """Raise if a per-matrix hinv status (host values) reports that the
+    factorisation's workgroups stopped waiting for each other: its results
+    are invalid, unlike a Hessian that is not positive definite."""
+    if any(int(v) == TIMEOUT for v in values):
+        raise Mi355qError(TIMEOUT, "hinv: the dataflow factorisation timed out waiting between workgroups")
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -21,7 +21,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import ops
+from . import _lib, ops
 from .quant_args import ActivationOrdering, QuantizationArgs, QuantizationStrategy, QuantizationType, resolve_args
 
 logger = logging.getLogger("llmcompressor_amd")
@@ -156,7 +156,9 @@ class PreparedHessian:
     def ok(self):
         """Positive definite: a bool (single) or a host bool tensor [B]
         (synchronises)."""
-        ok = self.status.cpu() == 0
+        st = self.status.cpu()
+        _lib.check_hinv_status(st.tolist())
+        ok = st == 0
         return bool(ok[0]) if ok.numel() == 1 and self.hinv.dim() == 2 else ok
 
 
@@ -252,7 +254,9 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
                                     dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize, block_h=bh,
                                     qtype=qtype, global_scale=global_scale)
     w_out, codes_out = ops.gptq_store_weight(w_work, invperm, W.dtype, codes)
-    loss_ok = torch.stack([torch.sum(losses), (prep.status[0] == 0).float()]).cpu()  # the one sync
+    loss_st = torch.stack([torch.sum(losses), prep.status[0].float()]).cpu()  # the one sync
+    _lib.check_hinv_status([loss_st[1]])
+    loss_ok = torch.stack([loss_st[0], (loss_st[1] == 0).float()])
     ok = bool(loss_ok[1])
     if not ok:
         _hinv_fallback_warning()
@@ -349,8 +353,9 @@ def gptq_quantize_batched(weights: torch.Tensor, quant_args: QuantizationArgs, h
                                             dequant_bf16=scale.dtype == torch.bfloat16, blocksize=blocksize,
                                             block_h=bh, qtype=qtype, global_scale=global_scale)
     w_out, codes_out = ops.gptq_store_weight_batched(w_work, invperm, weights.dtype, codes)
-    loss_ok = torch.stack([torch.sum(losses, dim=1), (prep.status == 0).float()]).cpu()  # the one sync
-    loss, ok = loss_ok[0], loss_ok[1] > 0
+    loss_st = torch.stack([torch.sum(losses, dim=1), prep.status.float()]).cpu()  # the one sync
+    _lib.check_hinv_status(loss_st[1].tolist())
+    loss, ok = loss_st[0], loss_st[1] == 0
     for _ in range(int((~ok).sum())):
         _hinv_fallback_warning()
     if stacked:

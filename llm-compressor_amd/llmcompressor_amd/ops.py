@@ -161,8 +161,9 @@ def gptq_hinv(H: torch.Tensor, perm: torch.Tensor | None, num_samples: float, pe
     L.check(lib.mi355q_gptq_hinv(H.data_ptr(), H.stride(0), d, L.ptr(p), C.c_float(num_samples),
                                  C.c_float(percdamp), hinv.data_ptr(), dead.data_ptr(), status.data_ptr(),
                                  ws.data_ptr(), ws.numel(), L.stream_of(H)))
-    ok = int(status.item()) == 0
-    return hinv, dead, ok
+    st = int(status.item())
+    L.check_hinv_status([st])
+    return hinv, dead, st == 0
 
 
 def gptq_hinv_rtn(H: torch.Tensor, perm: torch.Tensor | None, num_samples: float, percdamp: float):
@@ -267,7 +268,9 @@ def gptq_hinv_batched(H: torch.Tensor, perm: torch.Tensor | None, num_samples: t
     if not sync:
         L.call("mi355q_gptq_hinv_fallback", hinv.data_ptr(), d, d * d, B, status.data_ptr(), L.stream_of(H))
         return hinv, dead, status
-    return hinv, dead, status.cpu() == 0
+    st = status.cpu()
+    L.check_hinv_status(st.tolist())
+    return hinv, dead, st == 0
 
 
 def gptq_load_weight_batched(w: torch.Tensor, perm=None, dead=None) -> torch.Tensor:

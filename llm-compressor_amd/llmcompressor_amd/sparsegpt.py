@@ -20,7 +20,7 @@ import logging
 
 import torch
 
-from . import ops
+from . import _lib, ops
 from ._lib import UNSUPPORTED, Mi355qError
 from .gptq import _is_linear_like, conv2d_rows
 
@@ -125,7 +125,9 @@ def sparsegpt_prune(weight: torch.Tensor, hessian: torch.Tensor, sparsity, prune
             raise NotImplementedError(str(e)) from e
         raise
     w_out, _ = ops.gptq_store_weight(w_work, None, weight.dtype)
-    loss_ok = torch.stack([torch.sum(losses), (status[0] == 0).float()]).cpu()  # the one sync
+    loss_st = torch.stack([torch.sum(losses), status[0].float()]).cpu()  # the one sync
+    _lib.check_hinv_status([loss_st[1]])
+    loss_ok = torch.stack([loss_st[0], (loss_st[1] == 0).float()])
     ok = bool(loss_ok[1])
     if not ok:
         logger.warning("Failed to invert hessian due to numerical instability. Consider increasing "
