@@ -1181,37 +1181,45 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
 // steps (each costs about 4 us on gfx950, and the chain is a sequence of
 // small dependent steps).  For tile (i, j), i >= j, of matrix b:
 //   chain (one workgroup per matrix: the critical path), j = 0, 1, ...:
-//     A_jj -= L_{j,j-1} L_{j,j-1}^T (its last update; the earlier ones come
-//     accumulated by a helper), factor and invert it into X_jj = L_jj^-1,
-//     then L_{j+1,j} = A_{j+1,j} X_jj^T (A_{j+1,j} accumulated by a helper),
-//     kept in LDS for the next diagonal update;
-//   H(i, c), helper: A_ic -= sum_{k < kend} L_ik L_ck^T, kend = c - 1 on the
-//     diagonal (the chain applies k = c - 1) and c below it; for i >= c + 2
-//     then L_ic = A_ic X_cc^T;
-//   V(c, j), helper: X_cj = -X_cc sum_{k=j}^{c-1} L_ck X_kj.
+//     wait for the diagonal tile A_jj fully updated, factor and invert it
+//     into X_jj = L_jj^-1;
+//   S(c, s), s = 0..3 (helpers, one per 32-row strip of tile row c + 1):
+//     accumulate strip s of A_{c+1,c} and of the diagonal tile's lower
+//     blocks A_{c+1,c+1}[s][0..s] over k < c, then (once X_cc is out) its
+//     rows of L_{c+1,c} = A_{c+1,c} X_cc^T, then (once the strips above are
+//     out) A_{c+1,c+1}[s][0..s] -= L_{c+1,c}[s] L_{c+1,c}[0..s]^T.  Four
+//     workgroups share the chain's step between two factorisations;
+//   H(i, c), i >= c + 2 (helpers): A_ic -= sum_{k < c} L_ik L_ck^T, then
+//     L_ic = A_ic X_cc^T;
+//   V(c, j) (helpers): X_cj = -X_cc sum_{k=j}^{c-1} L_ck X_kj.
 // Helpers take tasks from one counter in an order where every input comes
-// earlier - level c: H(c, c) and H(c+1, c) (the chain's inputs), H(c+2.., c),
-// then V(c, 0..c-1), the chain's step c counted right after H(c+1, c) - so
-// the earliest unfinished task always has its inputs: the launch needs no
+// earlier - level 0: H(2.., 0); level c >= 1: S(c-1, 0..3), H(c+2.., c),
+// V(c, 0..c-1); the chain's step c counted right after S(c-1, 3) - so the
+// earliest unfinished task always has its inputs: the launch needs no
 // co-residency beyond one helper next to the chains.  A tile is published by
 // a release store of its flag after its data; consumers poll with relaxed
 // loads and acquire once.  Every wait is bounded: past `timeout` wall-clock
 // ticks the waiter marks its matrix MI355Q_TIMEOUT and raises the abort word,
 // after which every wait returns at once and all workgroups drain.
 //
-// Flags (int32, per matrix in its workspace): lf[i T + j] = 1 when tile
-// (i, j) of F holds A accumulated as the chain consumes it, 2 when it holds
-// L_ij (i > j) or X_jj is in X (i == j); xf[i T + j] = 1 when X_ij (i > j)
-// is in X.  Matrix 0's area also holds the task counter and the abort word.
+// Flags (int32, per matrix in its workspace): lf[i T + j] = 2 when tile
+// (i, j) of F holds L_ij (i > j) or X_jj is in X (i == j), 1 when the
+// diagonal tile holds A_jj fully updated; xf[i T + j] = 1 when X_ij (i > j)
+// is in X; st[4 c + s] = 1 when strip s of L_{c+1,c} is out; nl[c] and
+// nd[c] count the strips of column c done with L and with the diagonal
+// update (the last one sets the tile's lf).  Matrix 0's area then holds the
+// task counter and the abort word.
 constexpr int DSM = 2 * NB * LP + 3 * SB * LT + 2 * SB;  // LDS floats (157 KB: one workgroup per CU)
 
 constexpr int DLB = NB + 32;                             // LDS row stride of [k][n] tiles
 constexpr int DAG_LF_ACC = 1, DAG_LF_FINAL = 2;
+// flags per matrix: lf, xf (T^2 each), st (4 T), nl, nd (T each), then counter and abort word
+__host__ __device__ constexpr int64_t dag_nflags(int64_t T) { return 2 * T * T + 6 * T + 2; }
 
 struct DagParams {
   float* F;          // workspaces, wsf floats apart
   float* X;
-  int32_t* flags;    // 2 T^2 flags per matrix (wsf apart), then matrix 0's counter and abort word
+  int32_t* flags;    // DAG_NFLAGS(T) flags per matrix (wsf apart); matrix 0's end with the counter and abort word
   int32_t* status;   // [batch]
   int64_t d, wsf;
   int T, batch, ntasks;
@@ -1368,64 +1376,6 @@ __device__ __forceinline__ void dag_mma_tri(DagAcc& acc, const float* la, const 
   }
 }
 
-// Diagonal update C -= L L^T on the lower 32 x 32 blocks (rb >= cb), three
-// per wave: (3,0) (3,1) (3,2) | (3,3) (2,0) (2,1) | (2,2) (1,0) - | (1,1)
-// (0,0) -; the last two waves repeat a block they discard.
-struct DagSyrk {
-  f32x16_t t[3];
-};
-__device__ __forceinline__ int dag_syrk_rb(int wave, int i) {
-  return wave == 0 ? 3 : wave == 1 ? (i == 0 ? 3 : 2) : wave == 2 ? (i == 0 ? 2 : 1) : (i == 0 ? 1 : 0);
-}
-__device__ __forceinline__ int dag_syrk_cb(int wave, int i) {
-  return wave == 0 ? i : wave == 1 ? (i == 0 ? 3 : i - 1) : wave == 2 ? (i == 0 ? 2 : 0) : (i == 0 ? 1 : 0);
-}
-template <typename Fn>
-__device__ __forceinline__ void dag_each_syrk(Fn&& fn) {
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nblk = wave < 2 ? 3 : 2;
-#pragma unroll
-  for (int i = 0; i < 3; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      fn(i, r, i < nblk, 32 * dag_syrk_rb(wave, i) + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3),
-         32 * dag_syrk_cb(wave, i) + (lane & 31));
-}
-__device__ __forceinline__ void dag_mma_syrk(DagSyrk& acc, const float* l) {
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const float* pa[3];
-  const float* pb[3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    pa[i] = l + (32 * dag_syrk_rb(wave, i) + (lane & 31)) * LP + (lane >> 5);
-    pb[i] = l + (32 * dag_syrk_cb(wave, i) + (lane & 31)) * LP + (lane >> 5);
-  }
-  float f[2][6];
-  auto rd = [&](int k2, float* g) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      g[i] = pa[i][k2];
-      g[3 + i] = pb[i][k2];
-    }
-  };
-  rd(0, f[0]);
-  for (int c = 0; c < NB / 32; ++c) {
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const float* cur = f[q & 1];
-      float* nxt = f[(q + 1) & 1];
-      if (c < NB / 32 - 1 || q < 15) rd(32 * c + 2 * q + 2, nxt);
-#pragma unroll
-      for (int i = 0; i < 3; ++i) acc.t[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(-cur[i], cur[3 + i], acc.t[i], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-    }
-  }
-}
-
 // Publish: every wave's stores complete and written back, then the flag.
 __device__ __forceinline__ void dag_publish(gint* flag, int v) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -1443,7 +1393,7 @@ __shared__ int dag_word;
 // abort).  Thread 0 polls; the workgroup leaves together.
 __device__ __forceinline__ bool dag_wait(const gint* flag, int v, const DagParams& p, int b) {
   if (threadIdx.x == 0) {
-    gint* abort_word = (gint*)p.flags + 2 * p.T * p.T + 1;
+    gint* abort_word = (gint*)p.flags + dag_nflags(p.T) - 1;
     int ok = 1;
     if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < v) {
       const uint64_t t0 = wall_clock64();
@@ -1477,7 +1427,8 @@ __device__ __forceinline__ gfloat* dag_tile(float* base, const DagParams& p, int
 }
 __device__ __forceinline__ gint* dag_lf(const DagParams& p, int b) { return (gint*)p.flags + (int64_t)b * p.wsf; }
 
-// The chain of matrix b.
+// The chain of matrix b: factor and invert each diagonal tile once it is
+// fully updated.
 __device__ __noinline__ void dag_chain(DagParams p, int b) {
   const int T = p.T;
   const int64_t d = p.d;
@@ -1487,58 +1438,158 @@ __device__ __noinline__ void dag_chain(DagParams p, int b) {
   float* t = dag_smem + 2 * NB * LP;
   float* cb = t + 3 * SB * LT;
   f32x4_t v[16];
-  DagAcc acc;
-  DagSyrk sy;
-  for (int e = threadIdx.x; e < NB * LP; e += PNT) x[e] = 0.f;  // X_jj's upper blocks stay zero
-  {
-    dag_fetch(dag_tile(p.F, p, b, 0, 0), d, v);
+  for (int j = 0; j < T; ++j) {
+    if (j >= 1 && !dag_wait(lf + j * T + j, DAG_LF_ACC, p, b)) return;
+    dag_fetch(dag_tile(p.F, p, b, j, j), d, v);
     const int r0 = threadIdx.x >> 5, c = 4 * (threadIdx.x & 31);
 #pragma unroll
     for (int i = 0; i < 16; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) a[(8 * i + r0) * LP + c + e] = (c + e <= 8 * i + r0) ? v[i][e] : 0.f;
-  }
-  __syncthreads();
-  for (int j = 0;; ++j) {
+    __syncthreads();
     potf2_inv_lds(a, x, t, cb, dag_tile(p.X, p, b, j, j), d, p.status + b);
     dag_publish(lf + j * T + j, DAG_LF_FINAL);
-    if (j + 1 == T) break;
-    // L_{j+1,j} = A_{j+1,j} X_jj^T; the diagonal tile's lower blocks are
-    // fetched meanwhile
-    if (j >= 1 && !dag_wait(lf + (j + 1) * T + j, DAG_LF_ACC, p, b)) break;
-    gfloat* lt = dag_tile(p.F, p, b, j + 1, j);
-    dag_fetch(lt, d, v);
-    dag_put_rk(v, a);
-    if (j + 1 >= 2 && !dag_wait(lf + (j + 1) * T + j + 1, DAG_LF_ACC, p, b)) break;
-    __syncthreads();  // a is written
-    {
-      const gfloat* dg = dag_tile(p.F, p, b, j + 1, j + 1);
-      dag_each_syrk([&](int i, int r, bool, int row, int col) { sy.t[i][r] = dg[row * d + col]; });
-    }
-    dag_zero(acc);
-    dag_mma_tri(acc, a, x);
-    dag_each_tri([&](int bm, int bn, int r, int row, int col) { lt[row * d + col] = acc.t[bm][bn][r]; });
-    __syncthreads();  // every wave is done reading a
-    dag_each_tri([&](int bm, int bn, int r, int row, int col) { a[row * LP + col] = acc.t[bm][bn][r]; });
-    dag_publish(lf + (j + 1) * T + j, DAG_LF_FINAL);
-    // A_{j+1,j+1} -= L_{j+1,j} L_{j+1,j}^T on the lower blocks, into a
-    dag_mma_syrk(sy, a);
-    __syncthreads();
-    dag_each_syrk([&](int i, int r, bool own, int row, int col) {
-      if (own) a[row * LP + col] = col <= row ? sy.t[i][r] : 0.f;
-    });
-    for (int e = threadIdx.x; e < 6 * 32 * 32; e += PNT) {  // the blocks above the diagonal
-      const int q = e >> 10, rr = (e >> 5) & 31, cc = e & 31;
-      const int rb = q < 3 ? 0 : q < 5 ? 1 : 2, cbb = q < 3 ? q + 1 : q < 5 ? q - 1 : 3;
-      a[(32 * rb + rr) * LP + 32 * cbb + cc] = 0.f;
-    }
-    __syncthreads();
   }
 }
 
-// H(i, c): A_ic -= sum_{k < kend} L_ik L_ck^T, then L_ic = A_ic X_cc^T below
-// the sub-diagonal.  The tiles of step k + 1 are fetched while step k's
-// MFMAs run.
+// Strip accumulators: wave w holds the 32 x 32 block (strip rows, column
+// block w) of A_{c+1,c} (and of the diagonal tile for w <= s), each as two
+// MFMA chains (even and odd k) summed at the end.
+template <typename Fn>
+__device__ __forceinline__ void dag_each_strip(Fn&& fn) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) fn(r, 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), lane & 31);
+}
+
+// One strip-row operand and one or two [n][k] operands from LDS (stride LP),
+// k in [0, 2 kk_end): acc0/acc1 += A B0^T, acc2/acc3 += A B1^T (if two).
+template <bool TWO>
+__device__ __forceinline__ void dag_mma_strip(f32x16_t& s0, f32x16_t& s1, f32x16_t& d0, f32x16_t& d1, const float* pa,
+                                              const float* pb0, const float* pb1, int kk_end, float sign) {
+  for (int c = 0; c < kk_end; c += 16) {
+#pragma unroll
+    for (int q = 0; q < 16; q += 2) {
+      const int k2 = 2 * (c + q);
+      const float a0 = sign * pa[k2], a1 = sign * pa[k2 + 2];
+      const float b0 = pb0[k2], b1 = pb0[k2 + 2];
+      s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, s1, 0, 0, 0);
+      if (TWO) {
+        const float e0 = pb1[k2], e1 = pb1[k2 + 2];
+        d0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, e0, d0, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, e1, d1, 0, 0, 0);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void dag_fetch_rows(const gfloat* g, int64_t ld, int rows, f32x4_t (&v)[16]) {
+  typedef __attribute__((address_space(1))) const f32x4_t gf4;
+  const int tid = threadIdx.x;
+  const gfloat* p = g + (tid >> 5) * ld + 4 * (tid & 31);
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (8 * i < rows) v[i] = *reinterpret_cast<gf4*>(p + 8 * i * ld);
+}
+__device__ __forceinline__ void dag_put_rows(const f32x4_t (&v)[16], int rows, float* l) {
+  const int tid = threadIdx.x, r0 = tid >> 5, c = 4 * (tid & 31);
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (8 * i < rows)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) l[(8 * i + r0) * LP + c + e] = v[i][e];
+}
+
+// S(c, s): strip s (rows 32 s ..) of tile row c + 1.
+__device__ __noinline__ void dag_task_s(DagParams p, int b, int c, int s) {
+  const int T = p.T;
+  const int64_t d = p.d;
+  gint* lf = dag_lf(p, b);
+  gint* st = lf + 2 * T * T;
+  gint* nl = st + 4 * T;
+  gint* nd = nl + T;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r0 = 32 * s, r1 = 32 * (s + 1);
+  const bool dw = w <= s;  // this wave has a block of the diagonal strip
+  float* la = dag_smem;              // rows 0 .. r1 of L_{c+1,k} (the strip's own among them)
+  float* lb = dag_smem + NB * LP;    // L_{c,k}, then X_cc
+  gfloat* sub = dag_tile(p.F, p, b, c + 1, c) + (int64_t)r0 * d + 32 * w;
+  gfloat* dia = dag_tile(p.F, p, b, c + 1, c + 1) + (int64_t)r0 * d + 32 * w;
+  f32x16_t s0, s1, d0, d1;
+  dag_each_strip([&](int r, int row, int col) {
+    s0[r] = sub[row * d + col];
+    s1[r] = 0.f;
+    d0[r] = dw ? dia[row * d + col] : 0.f;
+    d1[r] = 0.f;
+  });
+  const float* pa = la + (r0 + (lane & 31)) * LP + (lane >> 5);
+  const float* pbs = lb + (32 * w + (lane & 31)) * LP + (lane >> 5);
+  const float* pbd = la + (32 * w + (lane & 31)) * LP + (lane >> 5);
+  f32x4_t va[16], vb[16];
+  auto ready = [&](int k) {
+    return dag_wait(lf + (c + 1) * T + k, DAG_LF_FINAL, p, b) && dag_wait(lf + c * T + k, DAG_LF_FINAL, p, b);
+  };
+  if (c > 0) {
+    if (!ready(0)) return;
+    dag_fetch_rows(dag_tile(p.F, p, b, c + 1, 0), d, r1, va);
+    dag_fetch(dag_tile(p.F, p, b, c, 0), d, vb);
+  }
+  for (int k = 0; k < c; ++k) {
+    dag_put_rows(va, r1, la);
+    dag_put_rk(vb, lb);
+    __syncthreads();
+    if (k + 1 < c) {
+      if (!ready(k + 1)) return;
+      dag_fetch_rows(dag_tile(p.F, p, b, c + 1, k + 1), d, r1, va);
+      dag_fetch(dag_tile(p.F, p, b, c, k + 1), d, vb);
+    }
+    if (dw)
+      dag_mma_strip<true>(s0, s1, d0, d1, pa, pbs, pbd, NB / 2, -1.f);
+    else
+      dag_mma_strip<false>(s0, s1, d0, d1, pa, pbs, pbd, NB / 2, -1.f);
+    __syncthreads();
+  }
+  // L_{c+1,c}[s] = A_{c+1,c}[s] X_cc^T (X_cc lower: column block w needs k < 32 (w + 1))
+  if (!dag_wait(lf + c * T + c, DAG_LF_FINAL, p, b)) return;
+  dag_fetch(dag_tile(p.X, p, b, c, c), d, vb);
+  dag_put_rk(vb, lb);
+  dag_each_strip([&](int r, int row, int col) { la[row * LP + 32 * w + col] = s0[r] + s1[r]; });
+  __syncthreads();
+  {
+    f32x16_t l0, l1, u0, u1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) l0[r] = l1[r] = u0[r] = u1[r] = 0.f;
+    dag_mma_strip<false>(l0, l1, u0, u1, la + (lane & 31) * LP + (lane >> 5), pbs, pbs, 16 * (w + 1), 1.f);
+    dag_each_strip([&](int r, int row, int col) { s0[r] = l0[r] + l1[r]; });
+  }
+  dag_each_strip([&](int r, int row, int col) { sub[row * d + col] = s0[r]; });
+  dag_publish(st + 4 * c + s, 1);
+  if (threadIdx.x == 0 &&
+      __hip_atomic_fetch_add(nl + c, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == 3)
+    __hip_atomic_store(lf + (c + 1) * T + c, DAG_LF_FINAL, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  // A_{c+1,c+1}[s][0..s] -= L[s] L[0..s]^T
+  for (int q = 0; q < s; ++q)
+    if (!dag_wait(st + 4 * c + q, 1, p, b)) return;
+  // (this workgroup read its strip's rows of A_{c+1,c} before storing them
+  // as L: drop any cached copy before reading them back)
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  dag_fetch_rows(dag_tile(p.F, p, b, c + 1, c), d, r1, va);
+  dag_put_rows(va, r1, la);
+  __syncthreads();
+  if (dw) {
+    dag_mma_strip<false>(d0, d1, s0, s1, pa, pbd, pbd, NB / 2, -1.f);
+    dag_each_strip([&](int r, int row, int col) { dia[row * d + col] = d0[r] + d1[r]; });
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0 &&
+      __hip_atomic_fetch_add(nd + c, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == 3)
+    __hip_atomic_store(lf + (c + 1) * T + c + 1, DAG_LF_ACC, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// H(i, c), i >= c + 2: A_ic -= sum_{k < c} L_ik L_ck^T, then L_ic = A_ic
+// X_cc^T.  The tiles of step k + 1 are fetched while step k's MFMAs run.
 __device__ __noinline__ void dag_task_h(DagParams p, int b, int i, int c) {
   const int T = p.T;
   const int64_t d = p.d;
@@ -1547,33 +1598,27 @@ __device__ __noinline__ void dag_task_h(DagParams p, int b, int i, int c) {
   float* lb = dag_smem + NB * LP;
   f32x4_t va[16], vb[16];
   DagAcc acc;
-  const int kend = i == c ? c - 1 : c;
   gfloat* out = dag_tile(p.F, p, b, i, c);
   dag_load_acc(acc, out, d);
   auto ready = [&](int k) {
     return dag_wait(lf + i * T + k, DAG_LF_FINAL, p, b) && dag_wait(lf + c * T + k, DAG_LF_FINAL, p, b);
   };
-  if (kend > 0) {
+  if (c > 0) {
     if (!ready(0)) return;
     dag_fetch(dag_tile(p.F, p, b, i, 0), d, va);
     dag_fetch(dag_tile(p.F, p, b, c, 0), d, vb);
   }
-  for (int k = 0; k < kend; ++k) {
+  for (int k = 0; k < c; ++k) {
     dag_put_rk(va, la);
     dag_put_rk(vb, lb);
     __syncthreads();
-    if (k + 1 < kend) {
+    if (k + 1 < c) {
       if (!ready(k + 1)) return;
       dag_fetch(dag_tile(p.F, p, b, i, k + 1), d, va);
       dag_fetch(dag_tile(p.F, p, b, c, k + 1), d, vb);
     }
     dag_mma<false>(acc, la, lb, -1.f);
     __syncthreads();
-  }
-  if (i < c + 2) {
-    dag_store_acc(acc, out, d);
-    dag_publish(lf + i * T + c, DAG_LF_ACC);
-    return;
   }
   if (!dag_wait(lf + c * T + c, DAG_LF_FINAL, p, b)) return;
   dag_fetch(dag_tile(p.X, p, b, c, c), d, vb);
@@ -1628,10 +1673,10 @@ __device__ __noinline__ void dag_task_v(DagParams p, int b, int c, int j) {
   dag_publish(xf + c * T + j, 1);
 }
 
-// task index -> kind (0 chain, 1 H, 2 V), matrix b, tile (i, j).  Order:
-// chains 0..B-1, then levels c = 0, 1, ..., each with matrices 0..B-1, each
-// with H(i0.., c) then V(c, 0..c-1); level c has T - 2, T - 1, T tasks per
-// matrix for c = 0, 1, >= 2 (H(0,0), H(1,0), H(1,1) carry no work).
+// task index -> kind (0 chain, 1 H, 2 V, 3 S), matrix b, (i, j).  Order:
+// chains 0..B-1, then per level c = 0, 1, ... the matrices 0..B-1 in turn,
+// each with level 0: H(2.., 0) (T - 2 tasks); level c >= 1: S(c-1, 0..3),
+// H(c+2.., c), V(c, 0..c-1) (T + 2 tasks, T + 3 on the last level).
 __device__ __forceinline__ void dag_decode(int idx, int T, int B, int& kind, int& b, int& i, int& j) {
   if (idx < B) {
     kind = 0;
@@ -1639,24 +1684,38 @@ __device__ __forceinline__ void dag_decode(int idx, int T, int B, int& kind, int
     i = j = 0;
     return;
   }
-  int r = idx - B, c, nc;
+  int r = idx - B;
   if (r < B * (T - 2)) {
-    c = 0;
-    nc = T - 2;
-  } else if ((r -= B * (T - 2)) < B * (T - 1)) {
-    c = 1;
-    nc = T - 1;
+    kind = 1;
+    b = r / (T - 2);
+    i = 2 + r % (T - 2);
+    j = 0;
+    return;
+  }
+  r -= B * (T - 2);
+  int c, nc;
+  if (r < B * (T + 2) * (T - 2)) {
+    c = 1 + r / (B * (T + 2));
+    r %= B * (T + 2);
+    nc = T + 2;
   } else {
-    r -= B * (T - 1);
-    c = 2 + r / (B * T);
-    r %= B * T;
-    nc = T;
+    r -= B * (T + 2) * (T - 2);
+    c = T - 1;
+    nc = T + 3;
   }
   b = r / nc;
-  const int u = r % nc, i0 = c < 2 ? 2 : c, nh = T - i0;
+  int u = r % nc;
+  if (u < 4) {
+    kind = 3;
+    i = c - 1;
+    j = u;
+    return;
+  }
+  u -= 4;
+  const int nh = T - c - 2 > 0 ? T - c - 2 : 0;
   if (u < nh) {
     kind = 1;
-    i = i0 + u;
+    i = c + 2 + u;
     j = c;
   } else {
     kind = 2;
@@ -1666,7 +1725,7 @@ __device__ __forceinline__ void dag_decode(int idx, int T, int B, int& kind, int
 }
 
 __global__ __launch_bounds__(PNT, 1) void chol_dag_kernel(DagParams p) {
-  int32_t* ctl = p.flags + 2 * p.T * p.T;
+  int32_t* ctl = p.flags + dag_nflags(p.T) - 2;
   for (;;) {
     if (threadIdx.x == 0) {
       const bool aborted = __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
@@ -1682,8 +1741,10 @@ __global__ __launch_bounds__(PNT, 1) void chol_dag_kernel(DagParams p) {
       dag_chain(p, b);
     else if (kind == 1)
       dag_task_h(p, b, i, j);
-    else
+    else if (kind == 2)
       dag_task_v(p, b, i, j);
+    else
+      dag_task_s(p, b, i, j);
   }
 }
 
@@ -1860,7 +1921,7 @@ HinvLayout hinv_layout(int64_t d) {
   L.linv = off; off = align256(off + (size_t)nblk * NB * NB * sizeof(float));
   L.damp = off; off = align256(off + 64);
   // dataflow factorisation: 2 T^2 tile flags, then (matrix 0) the task counter and abort word
-  L.flags = off; off = align256(off + (size_t)(2 * nblk * nblk + 2) * sizeof(int32_t));
+  L.flags = off; off = align256(off + (size_t)dag_nflags(nblk) * sizeof(int32_t));
   L.total = off;
   return L;
 }
@@ -2019,9 +2080,12 @@ namespace mi355q {
 namespace {
 
 // The dataflow factorisation takes orders that are multiples of NB with at
-// least 4 and at most 64 blocks (past that the blocked chain's large
-// products are at least as fast), in batches of at most 8 (one chain
-// workgroup per matrix).  MI355Q_HINV_DAG=0 in the environment turns it off.
+// least 4 and at most 64 blocks, in batches of at most 8 (measured on
+// MI355X: 4096 1.45 ms against the blocked chain's 1.85, 8192 5.9 against
+// 6.4, but 14336 27.7 against 23.9 - the helpers' single-workgroup tile
+// products lose to the chain's large GEMMs - and 2048 x 16 2.55 against
+// 2.20: one chain workgroup per matrix).  MI355Q_HINV_DAG=0 in the
+// environment turns it off.
 bool dag_eligible(int64_t d, int64_t batch) {
   if (d % NB != 0 || d / NB < 4 || d / NB > 64 || batch > 8) return false;
   const char* e = getenv("MI355Q_HINV_DAG");
@@ -2060,13 +2124,13 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
   const bool dag = dag_eligible(d, batch);
   int32_t* flags = reinterpret_cast<int32_t*>(ws + L.flags);
   hipLaunchKernelGGL(prepare_flip_kernel, grid_for(vin), fb, 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0, damp, F,
-                     wsf, vin ? 1 : 0, dag ? flags : nullptr, (int)(2 * nblk * nblk + 2));
+                     wsf, vin ? 1 : 0, dag ? flags : nullptr, (int)dag_nflags(nblk));
   MQ_LAUNCH_CHECK();
   if (dag) {
     DagParams p{};
     p.F = F; p.X = X; p.flags = flags; p.status = status_dev;
     p.d = d; p.wsf = wsf; p.T = (int)nblk; p.batch = (int)batch;
-    p.ntasks = (int)(batch * (nblk * nblk - 2));
+    p.ntasks = (int)(batch * (nblk * nblk + 2 * nblk - 2));
     int dev = 0, ncu = 0, khz = 0;
     MQ_CHECK_HIP(hipGetDevice(&dev));
     MQ_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
