@@ -500,7 +500,10 @@ def _spd_from_tokens(d, tokens, seed):
     return H / n
 
 
-@pytest.mark.parametrize("d,perm", [(256, False), (1000, False), (384, True)])
+# d = 256, 384, 1000: the blocked chain; 512, 1024, 2048 (multiples of 128
+# with at least 4 blocks): the dataflow factorisation
+@pytest.mark.parametrize("d,perm", [(256, False), (1000, False), (384, True), (512, False), (1024, True),
+                                    (2048, False)])
 def test_gptq_hinv_matches_oracle_chain(dev, d, perm):
     say(f"hinv d={d} perm={perm}")
     H = _spd_from_tokens(d, 4 * d, seed=d)
