@@ -1192,6 +1192,9 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
 //   H(i, c), i >= c + 2 (helpers): A_ic -= sum_{k < c} L_ik L_ck^T, then
 //     L_ic = A_ic X_cc^T;
 //   V(c, j) (helpers): X_cj = -X_cc sum_{k=j}^{c-1} L_ck X_kj.
+// hinv = J X J is written by the tasks themselves (V its tile and the zero
+// tile mirrored below the diagonal, S(c, 0) the diagonal tile of X_cc once
+// its own work is done, the chain the last one), so no flip pass follows.
 // Helpers take tasks from one counter in an order where every input comes
 // earlier - level 0: H(2.., 0); level c >= 1: S(c-1, 0..3), H(c+2.., c),
 // V(c, 0..c-1); the chain's step c counted right after S(c-1, 3) - so the
@@ -1208,7 +1211,7 @@ __global__ __launch_bounds__(PNT) void potf2_inv_kernel(const float* F, int64_t 
 // is in X; st[4 c + s] = 1 when strip s of L_{c+1,c} is out; nl[c] and
 // nd[c] count the strips of column c done with L and with the diagonal
 // update (the last one sets the tile's lf).  Matrix 0's area then holds the
-// task counter and the abort word.
+// task counter and the abort word.  diag_damp_kernel clears them.
 constexpr int DSM = 2 * NB * LP + 3 * SB * LT + 2 * SB;  // LDS floats (157 KB: one workgroup per CU)
 
 constexpr int DLB = NB + 32;                             // LDS row stride of [k][n] tiles
@@ -1224,6 +1227,9 @@ struct DagParams {
   int64_t d, wsf;
   int T, batch, ntasks;
   uint64_t timeout;  // wall-clock ticks per wait
+  // hinv = J X J (upper), written by the tasks that produce X's tiles
+  float* hinv;
+  int64_t shinv;
 };
 
 // thread tid's share of a 128 x 128 global tile: float4 v at row 8 v + tid / 32, columns 4 (tid % 32)
@@ -1427,6 +1433,39 @@ __device__ __forceinline__ gfloat* dag_tile(float* base, const DagParams& p, int
 }
 __device__ __forceinline__ gint* dag_lf(const DagParams& p, int b) { return (gint*)p.flags + (int64_t)b * p.wsf; }
 
+// F[a][c] of matrix b as the preparation kernel wrote it (read once, by the
+// task that owns the tile).  (Reading H itself instead, with the flip, the
+// scaling and the diagonal rules in the tasks, measured slower than the
+// preparation kernel: 1.448 against 1.438 ms at d = 4096, 6.07 against 5.86
+// at 8192.)
+__device__ __forceinline__ float dag_orig(const DagParams& p, int b, int64_t a, int64_t c) {
+  return ((const gfloat*)p.F)[(int64_t)b * p.wsf + a * p.d + c];
+}
+
+// X tile (i, j) of matrix b into hinv = J X J: element (r, c) of the tile
+// goes to hinv[d-1-(128 i + r)][d-1-(128 j + c)]
+__device__ __forceinline__ gfloat* dag_hinv_at(const DagParams& p, int b, int i, int j, int r, int c) {
+  return (gfloat*)p.hinv + (int64_t)b * p.shinv + (p.d - 1 - ((int64_t)i * NB + r)) * p.d +
+         (p.d - 1 - ((int64_t)j * NB + c));
+}
+// hinv's diagonal tile T-1-j from X_jj in LDS (row stride LP, only its lower
+// triangle read): reversed in both directions, zeros below the diagonal
+__device__ __forceinline__ void dag_hinv_diag(const DagParams& p, int b, int j, const float* x) {
+  for (int e = threadIdx.x; e < NB * NB; e += PNT) {
+    const int r = e >> 7, cc = e & (NB - 1);
+    *dag_hinv_at(p, b, j, j, r, cc) = cc <= r ? x[r * LP + cc] : 0.f;
+  }
+}
+// zeros over hinv tile (i, j) (the lower half of J X J: tile (T-1-j', T-1-i') of X's mirror)
+__device__ __forceinline__ void dag_hinv_zero_tile(const DagParams& p, int b, int ti, int tj) {
+  typedef __attribute__((address_space(1))) f32x4_t gf4;
+  const int tid = threadIdx.x;
+  gfloat* base = (gfloat*)p.hinv + (int64_t)b * p.shinv + (int64_t)ti * NB * p.d + (int64_t)tj * NB;
+  const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) *reinterpret_cast<gf4*>(base + (8 * i + (tid >> 5)) * p.d + 4 * (tid & 31)) = z;
+}
+
 // The chain of matrix b: factor and invert each diagonal tile once it is
 // fully updated.
 __device__ __noinline__ void dag_chain(DagParams p, int b) {
@@ -1439,9 +1478,10 @@ __device__ __noinline__ void dag_chain(DagParams p, int b) {
   float* cb = t + 3 * SB * LT;
   f32x4_t v[16];
   for (int j = 0; j < T; ++j) {
+    const int r0 = threadIdx.x >> 5, c = 4 * (threadIdx.x & 31);
+    // (the first diagonal tile has no update: as prepared)
     if (j >= 1 && !dag_wait(lf + j * T + j, DAG_LF_ACC, p, b)) return;
     dag_fetch(dag_tile(p.F, p, b, j, j), d, v);
-    const int r0 = threadIdx.x >> 5, c = 4 * (threadIdx.x & 31);
 #pragma unroll
     for (int i = 0; i < 16; ++i)
 #pragma unroll
@@ -1449,6 +1489,7 @@ __device__ __noinline__ void dag_chain(DagParams p, int b) {
     __syncthreads();
     potf2_inv_lds(a, x, t, cb, dag_tile(p.X, p, b, j, j), d, p.status + b);
     dag_publish(lf + j * T + j, DAG_LF_FINAL);
+    if (j == T - 1) dag_hinv_diag(p, b, j, x);  // (strip task S(j, 0) writes the others)
   }
 }
 
@@ -1517,10 +1558,11 @@ __device__ __noinline__ void dag_task_s(DagParams p, int b, int c, int s) {
   gfloat* sub = dag_tile(p.F, p, b, c + 1, c) + (int64_t)r0 * d + 32 * w;
   gfloat* dia = dag_tile(p.F, p, b, c + 1, c + 1) + (int64_t)r0 * d + 32 * w;
   f32x16_t s0, s1, d0, d1;
+  const int64_t ra = (int64_t)(c + 1) * NB + r0;  // first row of the strip in F
   dag_each_strip([&](int r, int row, int col) {
-    s0[r] = sub[row * d + col];
+    s0[r] = dag_orig(p, b, ra + row, (int64_t)c * NB + 32 * w + col);
     s1[r] = 0.f;
-    d0[r] = dw ? dia[row * d + col] : 0.f;
+    d0[r] = dw ? dag_orig(p, b, ra + row, (int64_t)(c + 1) * NB + 32 * w + col) : 0.f;
     d1[r] = 0.f;
   });
   const float* pa = la + (r0 + (lane & 31)) * LP + (lane >> 5);
@@ -1586,6 +1628,8 @@ __device__ __noinline__ void dag_task_s(DagParams p, int b, int c, int s) {
   if (threadIdx.x == 0 &&
       __hip_atomic_fetch_add(nd + c, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == 3)
     __hip_atomic_store(lf + (c + 1) * T + c + 1, DAG_LF_ACC, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  // off the chain's path: hinv's diagonal tile for X_cc, still in lb
+  if (s == 0) dag_hinv_diag(p, b, c, lb);
 }
 
 // H(i, c), i >= c + 2: A_ic -= sum_{k < c} L_ik L_ck^T, then L_ic = A_ic
@@ -1599,7 +1643,9 @@ __device__ __noinline__ void dag_task_h(DagParams p, int b, int i, int c) {
   f32x4_t va[16], vb[16];
   DagAcc acc;
   gfloat* out = dag_tile(p.F, p, b, i, c);
-  dag_load_acc(acc, out, d);
+  dag_each([&](int bm, int bn, int r, int row, int col) {
+    acc.t[bm][bn][r] = dag_orig(p, b, (int64_t)i * NB + row, (int64_t)c * NB + col);
+  });
   auto ready = [&](int k) {
     return dag_wait(lf + i * T + k, DAG_LF_FINAL, p, b) && dag_wait(lf + c * T + k, DAG_LF_FINAL, p, b);
   };
@@ -1670,6 +1716,8 @@ __device__ __noinline__ void dag_task_v(DagParams p, int b, int c, int j) {
   dag_zero(acc);
   dag_mma<true>(acc, la, lb, -1.f);
   dag_store_acc(acc, dag_tile(p.X, p, b, c, j), d);
+  dag_each([&](int bm, int bn, int r, int row, int col) { *dag_hinv_at(p, b, c, j, row, col) = acc.t[bm][bn][r]; });
+  dag_hinv_zero_tile(p, b, T - 1 - j, T - 1 - c);
   dag_publish(xf + c * T + j, 1);
 }
 
@@ -1750,12 +1798,16 @@ __global__ __launch_bounds__(PNT, 1) void chol_dag_kernel(DagParams p) {
 
 // diag'[j] = H[p(j)][p(j)] / n with 0 -> 1 (dead), damp = percdamp * mean(diag')
 // (one workgroup per matrix of a batch)
+// (also clears the matrix's nflags dataflow flags, flags + bm wsf, when set)
 __global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t ldh, int64_t sh, int64_t d,
                                                          const int32_t* perm, int64_t sp, const float* ns_arr,
                                                          float ns0, float percdamp, int32_t* dead,
-                                                         float* damp_out, int64_t wsf, int32_t* status) {
+                                                         float* damp_out, int64_t wsf, int32_t* status,
+                                                         int32_t* flags, int nflags) {
   __shared__ float part[1024 / 64];
   const int64_t bm = blockIdx.x;
+  if (flags)
+    for (int e = threadIdx.x; e < nflags; e += 1024) flags[bm * wsf + e] = 0;
   H += bm * sh;
   if (perm) perm += bm * sp;
   if (dead) dead += bm * d;
@@ -1783,15 +1835,10 @@ __global__ __launch_bounds__(1024) void diag_damp_kernel(const float* H, int64_t
 }
 
 // F (lower) = flip(permute(H / n)) with dead / damping rules on the diagonal.
-// Block (0, 0) of matrix z also clears the matrix's nflags dataflow flags
-// (flags + z wsf, int32).
 __global__ void prepare_flip_kernel(const float* H, int64_t ldh, int64_t sh, int64_t d, const int32_t* perm,
                                     int64_t sp, const float* ns_arr, float ns0, const float* damp, float* F,
-                                    int64_t wsf, int vec, int32_t* flags, int nflags) {
+                                    int64_t wsf, int vec) {
   const int64_t bm = blockIdx.z;
-  if (flags && blockIdx.x == 0 && blockIdx.y == 0)
-    for (int e = threadIdx.y * blockDim.x + threadIdx.x; e < nflags; e += blockDim.x * blockDim.y)
-      flags[bm * wsf + e] = 0;
   H += bm * sh;
   if (perm) perm += bm * sp;
   damp += bm * wsf;
@@ -2107,9 +2154,12 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
   float* linv = reinterpret_cast<float*>(ws + L.linv);
   float* damp = reinterpret_cast<float*>(ws + L.damp);
   const unsigned nb_ = (unsigned)batch;
+  const int64_t nblk = (d + NB - 1) / NB;
+  const bool dag = dag_eligible(d, batch);
+  int32_t* flags = reinterpret_cast<int32_t*>(ws + L.flags);
 
   hipLaunchKernelGGL(diag_damp_kernel, dim3(nb_), dim3(1024), 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0,
-                     percdamp, dead_dev, damp, wsf, status_dev);
+                     percdamp, dead_dev, damp, wsf, status_dev, dag ? flags : nullptr, (int)dag_nflags(nblk));
   MQ_LAUNCH_CHECK();
   // 64 x 16 threads; the vectorised paths take four columns per thread, so a
   // block row covers 256 columns instead of 64
@@ -2120,16 +2170,14 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
     return dim3((unsigned)((d + cpb - 1) / cpb), (unsigned)((d + 15) / 16), nb_);
   };
   const dim3 fb(64, 16);
-  const int64_t nblk = (d + NB - 1) / NB;
-  const bool dag = dag_eligible(d, batch);
-  int32_t* flags = reinterpret_cast<int32_t*>(ws + L.flags);
-  hipLaunchKernelGGL(prepare_flip_kernel, grid_for(vin), fb, 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0, damp, F,
-                     wsf, vin ? 1 : 0, dag ? flags : nullptr, (int)dag_nflags(nblk));
+  hipLaunchKernelGGL(prepare_flip_kernel, grid_for(vin), fb, 0, st, h_dev, ldh, sh, d, perm_dev, sp, ns_dev, ns0,
+                     damp, F, wsf, vin ? 1 : 0);
   MQ_LAUNCH_CHECK();
   if (dag) {
     DagParams p{};
     p.F = F; p.X = X; p.flags = flags; p.status = status_dev;
     p.d = d; p.wsf = wsf; p.T = (int)nblk; p.batch = (int)batch;
+    p.hinv = hinv_dev; p.shinv = shinv;
     p.ntasks = (int)(batch * (nblk * nblk + 2 * nblk - 2));
     int dev = 0, ncu = 0, khz = 0;
     MQ_CHECK_HIP(hipGetDevice(&dev));
@@ -2143,8 +2191,6 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
     const int grid = p.ntasks < ncu ? p.ntasks : ncu;
     MQ_CHECK_ARG(grid > batch, "gptq_hinv: %d compute units leave no helper for %d chains", ncu, (int)batch);
     hipLaunchKernelGGL(chol_dag_kernel, dim3((unsigned)grid), dim3(PNT), 0, st, p);
-    MQ_LAUNCH_CHECK();
-    hipLaunchKernelGGL(flip_out_kernel, grid_for(vout), fb, 0, st, X, d, hinv_dev, wsf, shinv, vout ? 1 : 0);
     MQ_LAUNCH_CHECK();
     return MI355Q_OK;
   }
