@@ -146,7 +146,7 @@ def main():
     for ch in chunks64:
         H64, n64 = gptq.accumulate_hessian(ch, lin, H64, n64)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps64 = 3
+    reps64 = 10   # each pass is a few ms: fewer repetitions time the clock ramp more than the path
     e0.record(stream)
     for _ in range(reps64):
         H64.zero_()
@@ -158,23 +158,27 @@ def main():
     h64_rel = ((torch.triu(H64) - torch.triu(H_last)).norm() / torch.triu(H_last).norm()).item()
     del H64
 
-    # the same 64 calls through the modifiers' forward hook, which stages
-    # the rows of small calls and accumulates them 16384 rows at a time
+    # the same 64 calls through the modifiers' forward hook, which holds the
+    # calls' rows (by reference) and accumulates them 65536 rows at a time in
+    # one segmented syrk; each call's input is a tensor of its own, as a
+    # forward pass makes it (a view into one 1 GiB tensor would be copied)
+    calls64 = [ch.clone() for ch in chunks64]
     Hs = gptq.make_empty_hessian(lin)
     ns = torch.zeros((), device=dev)
     stage = HessianStage()
 
-    def flush(rows, samples):
-        ops.hessian_syrk_(Hs, rows, alpha=2.0)
+    def flush(segs, samples):
+        ops.hessian_syrk_segments_(Hs, segs, alpha=2.0)
         ns.add_(samples)
 
     def staged_calls():
-        for ch in chunks64:
+        for ch in calls64:
             rows, added = gptq.hessian_rows(ch, lin, dev)
             stage.add(rows, added, flush)
         stage.flush(flush)
 
-    staged_calls()
+    for _ in range(2):
+        staged_calls()
     e0.record(stream)
     for _ in range(reps64):
         Hs.zero_()
@@ -184,7 +188,7 @@ def main():
     hs_ms = e0.elapsed_time(e1) / reps64
     hs_rel = ((torch.triu(Hs) - torch.triu(H_last)).norm() / torch.triu(H_last).norm()).item()
     stage.release()
-    del Hs
+    del Hs, calls64
 
     # vendor GEMM on the same product: torch.mm (hipBLASLt) of X^T X as the
     # full 4096 x 4096 square with a bf16 result (twice the multiply-adds of

@@ -106,6 +106,26 @@ int mi355q_hessian_syrk(const void* x_dev, mi355q_dtype dtype, int64_t n_tokens,
                         float* h_dev, int64_t ldh, float alpha, float beta, void* workspace_dev,
                         size_t workspace_bytes, void* stream);
 
+/* The same over the rows of several calls at once, left where the calls
+ * put them: H = beta * H + alpha * sum_k X_k^T X_k, X_k = [n_tokens[k], d]
+ * at x_devs[k] (host arrays of n_segments device pointers and row counts;
+ * every segment with the common row stride ldx; empty segments skipped).
+ * The reference's hook (modifiers/gptq/base.py:255-289 calling
+ * gptq_quantize.py:22-32, and modifiers/pruning/sparsegpt/base.py with
+ * sgpt_sparsify.py:36-59) adds each forward pass to H at once; a caller that
+ * holds the activations of its small calls by reference sums them here in
+ * one launch per 64 segments instead of copying them into one buffer.  Each
+ * segment starts a new 32-row stage, so segments whose row counts are
+ * multiples of 32 give bit for bit the sums of one call over their
+ * concatenation.  Workspace: mi355q_hessian_syrk_segments_workspace_size
+ * (0 for fp32, which runs one fp32 product per segment). */
+size_t mi355q_hessian_syrk_segments_workspace_size(const int64_t* n_tokens, int n_segments, int64_t d,
+                                                   mi355q_dtype dtype);
+int mi355q_hessian_syrk_segments(const void* const* x_devs, const int64_t* n_tokens, int n_segments,
+                                 mi355q_dtype dtype, int64_t d, int64_t ldx, float* h_dev, int64_t ldh,
+                                 float alpha, float beta, void* workspace_dev, size_t workspace_bytes,
+                                 void* stream);
+
 /* Grouped (MoE) variant: expert e accumulates the rows
  * x[rows_dev[k]] for k in [offsets_dev[e], offsets_dev[e+1]) into
  * h_dev + e * h_stride (each d x d, leading dimension d, upper triangle):

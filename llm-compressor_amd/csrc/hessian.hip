@@ -101,6 +101,19 @@ struct SyrkParams {
   int64_t h_stride;
 };
 
+// Dense syrk over rows held in separate buffers (the calls a Hessian hook
+// keeps by reference until it flushes): segment k has rows[k] > 0 rows at
+// x[k], all with the call's ldx, and takes stages stage0[k] .. stage0[k + 1]
+// - 1 of the concatenated stage sequence (its last stage zero-padded past
+// rows[k]).  Passed by value as a kernel argument.
+constexpr int kMaxSegments = 64;
+struct SegTable {
+  int n;
+  int64_t stage0[kMaxSegments + 1];
+  int64_t rows[kMaxSegments];
+  const uint16_t* x[kMaxSegments];
+};
+
 // The t-th tile on or above the diagonal, in super-block order: super-blocks
 // of SBK x SBK tiles (I <= J, row-major), tiles inside row-major.  Workgroups
 // of one XCD run consecutive t together, so a round of concurrent tiles
@@ -382,15 +395,17 @@ __device__ __forceinline__ bf16x8_t tr_pair(const char* lds, int off0, int off1)
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-enum StreamMode { kDense = 0, kGrouped = 1, kGroupedGather = 2 };
+enum StreamMode { kDense = 0, kGrouped = 1, kGroupedGather = 2, kDenseSeg = 3 };
 
 // One work item of the streaming kernel: tile t of matrix `mat` over token
 // split s (and part `part` of `nparts` for dense tail tiles), into partial
 // slot `slot` (-1: H directly).  `ring` is the workgroup's 128 KiB LDS ring,
-// `ridx` its row-index cache (gathered chunks).
+// `ridx` its row-index cache (gathered chunks); `sg` the segment table of
+// kDenseSeg (whose `mat` counts the padded stages' rows).
 template <bool F16, int MODE, int WAVES>
 __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int* ridx, int t, int s, int part,
-                                            int nparts, int S, int64_t slot, Matrix mat) {
+                                            int nparts, int S, int64_t slot, Matrix mat,
+                                            const SegTable* sg = nullptr) {
   // WAVES = 8: a 2 x 4 grid of waves (two per SIMD), each 4 x 2 MFMA blocks
   // (128 rows x 64 columns); WAVES = 4: a 2 x 2 grid (one per SIMD), each
   // 4 x 4 blocks (128 x 128), a third fewer LDS reads per MFMA
@@ -484,15 +499,52 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
   };
   const char* xbase = reinterpret_cast<const char*>(p.x + (mat.row_begin + st_begin * SK) * p.ldx);
   const int64_t sbytes = (int64_t)SK * p.ldx * 2;  // bytes per stage
-  // stages [0, nwhole) hold SK tokens
-  const int64_t nwhole = (n - st_begin * SK) / SK;
   const bool fast_ok = MODE != kGroupedGather && !edge;
+  // kDenseSeg: a cursor over the segment table, kept in scalar registers.
+  // Stages are asked for in non-decreasing order (issue, then dma_addrs of
+  // stage + 3), so it only moves forward; a binary search places it on the
+  // segment of the item's first stage.
+  int sk = 0;
+  const char* seg_x = nullptr;
+  int64_t seg_b = 0, seg_e = 0, seg_rows = 0;
+  auto seg_load = [&]() __attribute__((always_inline)) {
+    seg_x = reinterpret_cast<const char*>(sg->x[sk]);
+    seg_b = sg->stage0[sk];
+    seg_e = sg->stage0[sk + 1];
+    seg_rows = sg->rows[sk];
+  };
+  if constexpr (MODE == kDenseSeg) {
+    int lo = 0, hi = sg->n - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (sg->stage0[mid] <= st_begin) lo = mid; else hi = mid - 1;
+    }
+    sk = lo;
+    seg_load();
+  }
+  // stage sc of this item: its first token row and how many of its SK rows
+  // exist (>= SK: a whole stage)
+  auto stage_rows = [&](int64_t sc, const char*& xs, int64_t& avail) __attribute__((always_inline)) {
+    if constexpr (MODE == kDenseSeg) {
+      const int64_t G = st_begin + sc;
+      while (G >= seg_e && sk + 1 < sg->n) {
+        ++sk;
+        seg_load();
+      }
+      const int64_t l = G - seg_b;
+      xs = seg_x + l * sbytes;
+      avail = seg_rows - l * SK;
+    } else {
+      xs = xbase + sc * sbytes;
+      avail = n - (st_begin + sc) * SK;
+    }
+  };
   // Per-lane global addresses of the NDMA DMAs of a stage (A0, B0, A1, B1, ...):
   // lanes past n or d read the zero chunk.
   auto dma_addrs = [&](int64_t stage, const void** ad) __attribute__((always_inline)) {
     const int64_t sc = stage < nst ? stage : nst - 1;
-    const int64_t t0 = (st_begin + sc) * SK;
     if constexpr (MODE == kGroupedGather) {
+      const int64_t t0 = (st_begin + sc) * SK;
       const char* xg = reinterpret_cast<const char*>(p.x);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
@@ -505,10 +557,12 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
         ad[2 * j + 1] = bok ? (const void*)(xr + fb0 * 2) : (const void*)kZeroChunk;
       }
     } else {
-      const char* xs = xbase + sc * sbytes;
+      const char* xs;
+      int64_t avail;
+      stage_rows(sc, xs, avail);
       const char* xa = xs + fa0 * 2;
       const char* xb = xs + fb0 * 2;
-      if (fast_ok && sc < nwhole) {
+      if (fast_ok && avail >= SK) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           ad[2 * j] = xa + doff[j];
@@ -517,7 +571,7 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
       } else {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          const bool rok = t0 + drow[j] < n;
+          const bool rok = drow[j] < avail;
           const bool aok = rok && fa0 + 8 * dchunk[j] < p.d;
           const bool bok = rok && fb0 + 8 * dchunk[j] < p.d;
           ad[2 * j] = aok ? (const void*)(xa + doff[j]) : (const void*)kZeroChunk;
@@ -528,8 +582,10 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
   };
   auto issue = [&](int64_t stage, int slot) __attribute__((always_inline)) {
     const int64_t sc = stage < nst ? stage : nst - 1;
-    if (fast_ok && sc < nwhole) {
-      const char* xs = xbase + sc * sbytes;
+    const char* xs = nullptr;
+    int64_t avail = 0;
+    if constexpr (MODE != kGroupedGather) stage_rows(sc, xs, avail);
+    if (fast_ok && avail >= SK) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         dma_s(doff[j], xs + fa0 * 2, sa[slot] + 1024u * j);
@@ -655,7 +711,7 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
 
   if (slot < 0) {
     const bool diag = ti == tj;
-    const int64_t ldh = MODE == kDense ? p.ldh : p.d;
+    const int64_t ldh = (MODE == kDense || MODE == kDenseSeg) ? p.ldh : p.d;
     if ((ldh & 3) == 0 && (reinterpret_cast<uintptr_t>(mat.h) & 15) == 0) {
       // direct update of the upper triangle of H through the LDS ring, one
       // half of the tile (128 rows, the accumulators of waves wm == hh) at a
@@ -761,12 +817,16 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
 // equal item counts per XCD can mean very unequal work (routed rows per
 // expert vary 85-fold in the Zipf-routed MoE layer); the queues even it out.
 // Every queue ends, so every workgroup exits.
+// The segment table is a kernel argument of kDenseSeg only.
+template <int MODE> struct SegArg { int unused; };
+template <> struct SegArg<kDenseSeg> { SegTable t; };
+
 template <bool F16, int MODE, int WAVES>
-__global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p) {
+__global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p, SegArg<MODE> sa) {
   __shared__ __attribute__((aligned(1024))) char ring[8 * SOP];
   // row indices of a gathered chunk
   __shared__ int ridx[MODE == kGroupedGather ? kChunkTokens : 1];
-  if constexpr (MODE == kDense) {
+  if constexpr (MODE == kDense || MODE == kDenseSeg) {
     const int S = p.S;
     int t, s, part = 0, nparts = 1;
     int64_t slot;
@@ -797,7 +857,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void syrk_stream_kernel(SyrkParams p
       nparts = p.tail_f;
       slot = nfull + ((int64_t)(t - p.tail_start) * S + s) * p.tail_f + part;
     }
-    stream_item<F16, MODE, WAVES>(p, ring, ridx, t, s, part, nparts, S, slot, p.single);
+    const SegTable* sg = nullptr;
+    if constexpr (MODE == kDenseSeg) sg = &sa.t;
+    stream_item<F16, MODE, WAVES>(p, ring, ridx, t, s, part, nparts, S, slot, p.single, sg);
   } else {
     __shared__ int s_item;
     const int N = p.gcounts[0] * p.T;
@@ -1173,7 +1235,8 @@ DensePlan plan_dense(int64_t n, int64_t d) {
 template <bool F16>
 void launch_syrk_t(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
   if (tile_edge(d) == 256) {
-    hipLaunchKernelGGL((syrk_stream_kernel<F16, kDense, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
+    hipLaunchKernelGGL((syrk_stream_kernel<F16, kDense, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p,
+                       SegArg<kDense>{});
   } else {
     hipLaunchKernelGGL((syrk_bf16_kernel<128, F16>), dim3(grid), dim3(NT), 0, st, p);
   }
@@ -1213,6 +1276,25 @@ extern "C" size_t mi355q_hessian_workspace_size(int64_t n_tokens, int64_t d) {
 }
 
 namespace {
+// Kernel parameters of a dense call over n_tokens rows at x.
+SyrkParams dense_params(const uint16_t* x, int64_t n_tokens, int64_t d, int64_t ldx, float* h_dev, int64_t ldh,
+                        float alpha, float beta, const DensePlan& pl, void* workspace_dev) {
+  SyrkParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.d = d;
+  p.ldh = ldh;
+  p.nt = tiles_per_edge(d);
+  p.alpha = alpha;
+  p.beta = beta;
+  p.single = Matrix{0, n_tokens, h_dev};
+  p.S = pl.S;
+  p.tail_start = pl.tail_start;
+  p.tail_f = pl.tail_f;
+  p.ws = static_cast<float*>(workspace_dev);
+  return p;
+}
+
 // H = beta H + alpha X^T X (upper) for 16-bit X: bf16, or fp16 (f16)
 int hessian16_impl(const void* x_dev, bool f16, int64_t n_tokens, int64_t d, int64_t ldx, float* h_dev,
                    int64_t ldh, float alpha, float beta, void* workspace_dev, size_t workspace_bytes, void* stream) {
@@ -1239,19 +1321,8 @@ int hessian16_impl(const void* x_dev, bool f16, int64_t n_tokens, int64_t d, int
                "hessian: workspace too small (%zu < %zu)", workspace_bytes, need);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 
-  SyrkParams p{};
-  p.x = static_cast<const uint16_t*>(x_dev);
-  p.ldx = ldx;
-  p.d = d;
-  p.ldh = ldh;
-  p.nt = nt;
-  p.alpha = alpha;
-  p.beta = beta;
-  p.single = Matrix{0, n_tokens, h_dev};
-  p.S = S;
-  p.tail_start = pl.tail_start;
-  p.tail_f = pl.tail_f;
-  p.ws = static_cast<float*>(workspace_dev);
+  SyrkParams p = dense_params(static_cast<const uint16_t*>(x_dev), n_tokens, d, ldx, h_dev, ldh, alpha, beta, pl,
+                              workspace_dev);
   launch_syrk(p, d, (unsigned)pl.grid, st, f16);
   MQ_LAUNCH_CHECK();
   if (S > 1) {
@@ -1261,6 +1332,118 @@ int hessian16_impl(const void* x_dev, bool f16, int64_t n_tokens, int64_t d, int
     else
       launch_reduce(p.ws, S, p.single, d, ldh, nt, alpha, beta, (unsigned)T, st);
     MQ_LAUNCH_CHECK();
+  }
+  return MI355Q_OK;
+}
+
+// Stages of a segment of `rows` rows (the last one zero-padded).
+inline int64_t seg_stages(int64_t rows) { return (rows + SK - 1) / SK; }
+
+// Workspace of a segmented call: d >= 512 runs the non-empty segments in
+// groups of kMaxSegments, one launch over each group's padded rows; d < 512
+// runs one dense call per segment.
+size_t seg_workspace(const int64_t* rows, int nseg, int64_t d) {
+  size_t need = 0;
+  auto upd = [&need](size_t v) { need = v > need ? v : need; };
+  if (tile_edge(d) != 256) {
+    for (int k = 0; k < nseg; ++k)
+      if (rows[k] > 0) upd(mi355q_hessian_workspace_size(rows[k], d));
+    return need;
+  }
+  int in_group = 0;
+  int64_t stages = 0;
+  for (int k = 0; k < nseg; ++k) {
+    if (rows[k] <= 0) continue;
+    stages += seg_stages(rows[k]);
+    if (++in_group == kMaxSegments) {
+      upd(mi355q_hessian_workspace_size(stages * SK, d));
+      in_group = 0;
+      stages = 0;
+    }
+  }
+  if (in_group) upd(mi355q_hessian_workspace_size(stages * SK, d));
+  return need;
+}
+
+// H = beta H + alpha sum_k X_k^T X_k over row segments X_k (host arrays of
+// device pointers and row counts), summed as the rows of one call would be:
+// segments in order, each starting a new stage.
+int hessian_seg_impl(const void* const* xs, const int64_t* rows, int nseg, mi355q_dtype dtype, int64_t d,
+                     int64_t ldx, float* h_dev, int64_t ldh, float alpha, float beta, void* workspace_dev,
+                     size_t workspace_bytes, void* stream) {
+  MQ_CHECK_ARG(nseg >= 0 && (nseg == 0 || (xs != nullptr && rows != nullptr)),
+               "hessian segments: null segment arrays");
+  int nz = 0;
+  for (int k = 0; k < nseg; ++k) {
+    MQ_CHECK_ARG(rows[k] >= 0, "hessian segments: negative row count in segment %d", k);
+    MQ_CHECK_ARG(rows[k] == 0 || xs[k] != nullptr, "hessian segments: null rows in segment %d", k);
+    nz += rows[k] > 0;
+  }
+  const bool seg16 = (dtype == MI355Q_BF16 || dtype == MI355Q_F16) && d >= 512;
+  if (!seg16 || nz <= 1) {
+    // one dense call per non-empty segment, beta with the first
+    float b = beta;
+    for (int k = 0; k < nseg; ++k) {
+      if (rows[k] == 0) continue;
+      const int rc = mi355q_hessian_syrk(xs[k], dtype, rows[k], d, ldx, h_dev, ldh, alpha, b, workspace_dev,
+                                         workspace_bytes, stream);
+      if (rc != MI355Q_OK) return rc;
+      b = 1.f;
+    }
+    if (nz == 0) return mi355q_hessian_syrk(nullptr, dtype, 0, d, ldx, h_dev, ldh, alpha, beta, nullptr, 0, stream);
+    return MI355Q_OK;
+  }
+  const bool f16 = dtype == MI355Q_F16;
+  MQ_CHECK_ARG(d % 8 == 0, "hessian: d must be a positive multiple of 8 (got %lld)", (long long)d);
+  MQ_CHECK_ARG(ldx >= d && ldx % 8 == 0, "hessian: ldx must be >= d and a multiple of 8");
+  MQ_CHECK_ARG(ldx <= (int64_t(1) << 24), "hessian: ldx above 2^24 elements is not supported");
+  MQ_CHECK_ARG(ldh >= d, "hessian: ldh must be >= d");
+  MQ_CHECK_ARG(h_dev != nullptr, "hessian: null H");
+  for (int k = 0; k < nseg; ++k)
+    MQ_CHECK_ARG(rows[k] == 0 || aligned16(xs[k]), "hessian segments: segment %d is not 16-byte aligned", k);
+  const size_t need = seg_workspace(rows, nseg, d);
+  MQ_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace_dev != nullptr),
+               "hessian: workspace too small (%zu < %zu)", workspace_bytes, need);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int nt = tiles_per_edge(d);
+  float b = beta;
+  for (int k = 0; k < nseg;) {
+    SegArg<kDenseSeg> sa{};
+    SegTable& tb = sa.t;
+    int64_t stages = 0;
+    for (; k < nseg && tb.n < kMaxSegments; ++k) {
+      if (rows[k] == 0) continue;
+      tb.stage0[tb.n] = stages;
+      tb.rows[tb.n] = rows[k];
+      tb.x[tb.n] = static_cast<const uint16_t*>(xs[k]);
+      stages += seg_stages(rows[k]);
+      ++tb.n;
+    }
+    if (tb.n == 0) break;
+    tb.stage0[tb.n] = stages;
+    int rc = MI355Q_OK;
+    if (tb.n == 1) {
+      rc = hessian16_impl(tb.x[0], f16, tb.rows[0], d, ldx, h_dev, ldh, alpha, b, workspace_dev, workspace_bytes,
+                          stream);
+    } else {
+      const int64_t n_eff = stages * SK;   // the padded stages' rows
+      const DensePlan pl = plan_dense(n_eff, d);
+      const SyrkParams p = dense_params(tb.x[0], n_eff, d, ldx, h_dev, ldh, alpha, b, pl, workspace_dev);
+      if (f16)
+        hipLaunchKernelGGL((syrk_stream_kernel<true, kDenseSeg, kStreamWaves>), dim3((unsigned)pl.grid), dim3(SNT),
+                           0, st, p, sa);
+      else
+        hipLaunchKernelGGL((syrk_stream_kernel<false, kDenseSeg, kStreamWaves>), dim3((unsigned)pl.grid), dim3(SNT),
+                           0, st, p, sa);
+      MQ_LAUNCH_CHECK();
+      if (pl.S > 1) {
+        hipLaunchKernelGGL(syrk_stream_reduce_kernel<kStreamWaves>, dim3((unsigned)pl.T, 256 / ((NT / 64) * RED_CPW)),
+                           dim3(NT), 0, st, p.ws, pl.S, pl.tail_start, pl.tail_f, p.single, d, ldh, nt, alpha, b);
+        MQ_LAUNCH_CHECK();
+      }
+    }
+    if (rc != MI355Q_OK) return rc;
+    b = 1.f;
   }
   return MI355Q_OK;
 }
@@ -1304,6 +1487,20 @@ extern "C" int mi355q_hessian_syrk_bf16(const void* x_dev, int64_t n_tokens, int
                                         size_t workspace_bytes, void* stream) {
   return mi355q_hessian_syrk_scaled_bf16(x_dev, n_tokens, d, ldx, h_dev, ldh, alpha, 1.f, workspace_dev,
                                          workspace_bytes, stream);
+}
+
+extern "C" size_t mi355q_hessian_syrk_segments_workspace_size(const int64_t* n_tokens, int n_segments, int64_t d,
+                                                              mi355q_dtype dtype) {
+  if (dtype == MI355Q_F32 || n_segments <= 0 || n_tokens == nullptr || d <= 0) return 0;
+  return seg_workspace(n_tokens, n_segments, d);
+}
+
+extern "C" int mi355q_hessian_syrk_segments(const void* const* x_devs, const int64_t* n_tokens, int n_segments,
+                                            mi355q_dtype dtype, int64_t d, int64_t ldx, float* h_dev, int64_t ldh,
+                                            float alpha, float beta, void* workspace_dev, size_t workspace_bytes,
+                                            void* stream) {
+  return hessian_seg_impl(x_devs, n_tokens, n_segments, dtype, d, ldx, h_dev, ldh, alpha, beta, workspace_dev,
+                          workspace_bytes, stream);
 }
 
 namespace {
@@ -1391,11 +1588,15 @@ extern "C" int mi355q_hessian_grouped_syrk(const void* x_dev, mi355q_dtype dtype
   const unsigned grid = (unsigned)(items < cus ? items : cus);
   const bool f16 = dtype == MI355Q_F16;
   if (rows_dev) {
-    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGroupedGather, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
-    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGroupedGather, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
+    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGroupedGather, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p,
+                                  SegArg<kGroupedGather>{});
+    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGroupedGather, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p,
+                                  SegArg<kGroupedGather>{});
   } else {
-    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGrouped, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
-    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGrouped, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p);
+    if (f16) hipLaunchKernelGGL((syrk_stream_kernel<true, kGrouped, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p,
+                                  SegArg<kGrouped>{});
+    else     hipLaunchKernelGGL((syrk_stream_kernel<false, kGrouped, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p,
+                                  SegArg<kGrouped>{});
   }
   MQ_LAUNCH_CHECK();
   if (gb.max_reduce > 0) {

@@ -29,6 +29,8 @@ SIGNATURES = {
     "mi355q_hessian_syrk_scaled_bf16": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _f32, _f32, _vp, _sz, _vp]),
     "mi355q_hessian_syrk_workspace_size": (_sz, [_i64, _i64, _i32]),
     "mi355q_hessian_syrk": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _f32, _f32, _vp, _sz, _vp]),
+    "mi355q_hessian_syrk_segments_workspace_size": (_sz, [_vp, _i32, _i64, _i32]),
+    "mi355q_hessian_syrk_segments": (_i32, [_vp, _vp, _i32, _i32, _i64, _i64, _vp, _i64, _f32, _f32, _vp, _sz, _vp]),
     "mi355q_hessian_grouped_syrk_workspace_size": (_sz, [_i64, _i32, _i64]),
     "mi355q_hessian_grouped_syrk": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _i64, _f32, _f32, _vp,
                                            _sz, _vp]),

@@ -270,9 +270,10 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
 
     Beyond the reference's arguments: ``share_hessians`` (modules fed the
     same tensor accumulate one Hessian), ``hessian_batch_tokens`` /
-    ``hessian_stage_bytes`` (rows of small calls are copied into device
-    buffers of up to 65536 rows and 512 MiB and accumulated one long syrk at
-    a time, while the buffers of one modifier stay within 2 GiB by default)
+    ``hessian_stage_bytes`` (the rows of small calls are held, by reference
+    or copied, up to 65536 rows and 512 MiB per module, and accumulated one
+    long syrk at a time, while the rows one modifier holds stay within 2 GiB
+    by default)
     and
     ``batch_experts``: the same-shaped projections of an MoE expert list
     (``<experts>.<e>.gate_proj`` ...) keep their Hessians in one stacked
@@ -368,16 +369,16 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
             x, added = hessian_rows(inp, module, H.device)
             st = self._stage_for(module, x)
             if st is None:
-                self._accumulate(module, H, x, added)
+                self._accumulate(module, H, [x], added)
             else:
                 st.add(x, added, lambda rows, samples: self._accumulate(module, H, rows, samples))
         if self.share_hessians:
             self._note_accumulated(module, inp, self._modules.get)
 
-    def _accumulate(self, module, H, rows, samples):
+    def _accumulate(self, module, H, segs, samples):
         # the sample count grows with the rows it counts (one device add per
         # syrk instead of one per forward pass)
-        ops.hessian_syrk_(H, rows, alpha=2.0)
+        ops.hessian_syrk_segments_(H, segs, alpha=2.0)
         self._num_samples[module] += samples
 
     def _flush(self, module):
@@ -664,14 +665,14 @@ class SparseGPTModifier(_SharedHessians, _Staging):
             self._num_samples[module] += added
             st = self._stage_for(module, x)
             if st is None:
-                self._fold(module, H, x, added)
+                self._fold(module, H, [x], added)
             else:
                 st.add(x, added, lambda rows, samples: self._fold(module, H, rows, samples))
         if self.share_hessians:
             self._note_accumulated(module, inp, self._module_names.get)
 
-    def _fold(self, module, H, rows, samples):
-        self._folded[module] = sgpt.fold_rows(H, rows, self._folded.get(module, 0), samples)
+    def _fold(self, module, H, segs, samples):
+        self._folded[module] = sgpt.fold_rows(H, segs, self._folded.get(module, 0), samples)
 
     def _flush(self, module):
         """Folds the rows still staged for ``module`` into its running mean."""

@@ -19,6 +19,7 @@ import re
 import torch
 
 from . import ops
+from .staging import hold, held
 
 _CALIBRATE_ALL_EXPERTS = False
 
@@ -166,7 +167,8 @@ class ExpertFamily:
     in one [E, d, d] tensor, and the rows their forward hooks receive are
     held until a flush hands them, grouped by expert, to one grouped syrk
     launch (instead of one accumulation per expert call).  Rows are held as
-    references to the hooks' inputs, up to ``budget`` bytes; a flush copies
+    references to the hooks' inputs (``staging.hold``: a flush raises if one
+    was modified in place since), up to ``budget`` bytes; a flush copies
     them into one grouped buffer.  Repeated calls of one expert before a
     flush go into the same group (another order of fp32 additions)."""
 
@@ -200,7 +202,8 @@ class ExpertFamily:
         nbytes = rows.numel() * rows.element_size()
         if self._parts and self._held + nbytes > self.budget:
             self.flush()
-        self._parts.append((slot, len(self._parts), rows))
+        x, version = hold(rows)
+        self._parts.append((slot, len(self._parts), x, version))
         self._held += nbytes
 
     def flush(self) -> None:
@@ -212,7 +215,7 @@ class ExpertFamily:
                 self.H.zero_()
                 self._fresh = False
             return
-        parts = sorted(self._parts, key=lambda p: (p[0], p[1]))
+        parts = [(slot, i, held(x, v)) for slot, i, x, v in sorted(self._parts, key=lambda p: (p[0], p[1]))]
         self._parts, self._held = [], 0
         counts = [0] * len(self.members)
         for slot, _, rows in parts:

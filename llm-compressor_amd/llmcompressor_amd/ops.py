@@ -69,6 +69,43 @@ def hessian_syrk_(H: torch.Tensor, x: torch.Tensor, alpha: float = 2.0, beta: fl
     return H
 
 
+def hessian_syrk_segments_(H: torch.Tensor, xs, alpha: float = 2.0, beta: float = 1.0) -> torch.Tensor:
+    """``hessian_syrk_`` over the rows of several [n_k, d] tensors at once:
+    H = beta * H + alpha * sum_k X_k^T X_k (upper triangle, in place), the
+    sum a single call over their concatenation forms (segments of
+    multiples of 32 rows: bit for bit) without the concatenation.  16-bit
+    segments sharing one dtype and row stride run in one launch per 64
+    segments; others take one ``hessian_syrk_`` per segment."""
+    xs = [_hessian_input(x) for x in xs]
+    if len(xs) == 1:
+        return hessian_syrk_(H, xs[0], alpha=alpha, beta=beta)
+    L.require_gpu(H, *xs)
+    d = H.shape[-1]
+    if any(x.shape[1] != d for x in xs):
+        raise ValueError(f"every segment needs {d} columns, got {[tuple(x.shape) for x in xs]}")
+    if H.dtype != torch.float32 or H.shape != (d, d) or H.stride(1) != 1:
+        raise ValueError(f"H must be fp32 [{d}, {d}] row-major, got {tuple(H.shape)} {H.dtype}")
+    dts = {x.dtype for x in xs}
+    ldx = {x.stride(0) for x in xs if x.shape[0] > 0}
+    if len(dts) != 1 or len(ldx) > 1 or xs[0].dtype == torch.float32 or any(x.device != H.device for x in xs):
+        b = beta
+        for x in xs:
+            if x.shape[0] > 0 or x is xs[-1]:
+                hessian_syrk_(H, x, alpha=alpha, beta=b)
+                b = 1.0
+        return H
+    lib = L.lib()
+    dt = _HESS_DT[xs[0].dtype]
+    n = len(xs)
+    ptrs = (C.c_void_p * n)(*[x.data_ptr() for x in xs])
+    rows = (C.c_int64 * n)(*[x.shape[0] for x in xs])
+    ws = _ws(lib.mi355q_hessian_syrk_segments_workspace_size(rows, n, d, dt), H.device)
+    L.check(lib.mi355q_hessian_syrk_segments(ptrs, rows, n, dt, d, ldx.pop() if ldx else d, H.data_ptr(), H.stride(0),
+                                             C.c_float(alpha), C.c_float(beta), L.ptr(ws),
+                                             0 if ws is None else ws.numel(), L.stream_of(xs[0])))
+    return H
+
+
 def hessian_grouped_syrk_(H: torch.Tensor, x: torch.Tensor, rows: torch.Tensor | None, offsets,
                           alpha: float = 2.0, beta: float = 1.0) -> torch.Tensor:
     """Per-group upper-triangle syrk: H[e] = beta * H[e] + alpha * X_e^T X_e

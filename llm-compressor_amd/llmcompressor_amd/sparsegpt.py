@@ -61,12 +61,14 @@ def hessian_rows(inp: torch.Tensor, module: torch.nn.Module, device) -> tuple[to
     return inp.reshape(-1, inp.shape[-1]), inp.shape[0]
 
 
-def fold_rows(H: torch.Tensor, x: torch.Tensor, num_samples: int, num_added: int) -> int:
-    """The running mean over ``num_samples`` samples extended by the rows x of
-    ``num_added`` more; returns the new count."""
+def fold_rows(H: torch.Tensor, x, num_samples: int, num_added: int) -> int:
+    """The running mean over ``num_samples`` samples extended by the rows x (a
+    2-D tensor, or a list of them summed as one) of ``num_added`` more;
+    returns the new count."""
     beta = num_samples / (num_samples + num_added)
     num_samples += num_added
-    ops.hessian_syrk_(H, x, alpha=2 / num_samples, beta=beta)
+    ops.hessian_syrk_segments_(H, list(x) if isinstance(x, (list, tuple)) else [x], alpha=2 / num_samples,
+                               beta=beta)
     return num_samples
 
 

@@ -1,0 +1,123 @@
+"""GPU: the segmented Hessian syrk (``mi355q_hessian_syrk_segments``) over
+rows left in separate tensors.
+
+Segments whose row counts are multiples of 32 fill the same 32-row stages
+as one call over their concatenation, so the result equals that call's bit
+for bit; ragged segments (zero-padded stages) meet the Hessian bar against
+the oracle.  Also: beta scaling once per call, more than 64 segments (one
+launch per 64), empty segments, the per-segment routes (fp32, d < 512), the
+strictly-lower triangle untouched, and the modifiers' stage holding calls
+by reference against the same stage copying them.
+"""
+import pytest
+import torch
+
+from llmcompressor_amd import gptq, ops, workloads
+from llmcompressor_amd.staging import HessianStage
+from oracle import gptq as og
+
+pytestmark = pytest.mark.gpu
+
+HESS_TOL = 1e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def rel_fro(a, b):
+    return ((a.double() - b.double()).norm() / b.double().norm()).item()
+
+
+def _segs(sizes, d, dtype, dev, seed):
+    return [workloads.heavy_tailed_activations((n, d), seed=seed + i).to(dtype).to(dev) for i, n in enumerate(sizes)]
+
+
+def _h0(d, dev):
+    return torch.randn(d, d, generator=torch.Generator().manual_seed(5)).to(dev)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("sizes,d", [([2048] * 32, 4096), ([2048] * 8, 4096), ([4096, 32, 1024, 2048], 1024),
+                                     ([512] * 5, 1000), ([8192, 8192, 4096], 2304)],
+                         ids=["hook32x2048-4096", "8x2048-4096", "mixed-1024", "edge-tiles-1000", "long-2304"])
+def test_segments_equal_concatenated_call(dev, dtype, sizes, d):
+    say(f"segmented syrk {dtype} d={d} segments={sizes[:4]}{'...' if len(sizes) > 4 else ''} ({len(sizes)})")
+    xs = _segs(sizes, d, dtype, dev, seed=11)
+    H1, H2 = _h0(d, dev), _h0(d, dev)
+    ops.hessian_syrk_(H1, torch.cat(xs), alpha=2.0)
+    ops.hessian_syrk_segments_(H2, xs, alpha=2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(H1, H2)
+
+
+@pytest.mark.parametrize("sizes,d", [([1000, 333, 2048, 1, 45], 1024), ([300] * 70, 512), ([2049, 0, 4095], 4096)],
+                         ids=["ragged-1024", "70-segments-512", "empty-4096"])
+def test_ragged_segments_vs_oracle(dev, sizes, d):
+    say(f"ragged segmented syrk d={d} {len(sizes)} segments")
+    xs = _segs(sizes, d, torch.bfloat16, dev, seed=21)
+    h0 = _h0(d, dev)
+    H = h0.clone()
+    ops.hessian_syrk_segments_(H, xs, alpha=2.0)
+    H2 = h0.clone()
+    ops.hessian_syrk_segments_(H2, xs, alpha=2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(H, H2)   # deterministic
+    Ho, _ = og.accumulate_hessian(torch.cat([x.cpu() for x in xs]), h0.cpu(), torch.zeros(()))
+    iu = torch.triu_indices(d, d)
+    got = H.cpu()
+    r = rel_fro(got[iu[0], iu[1]], Ho[iu[0], iu[1]])
+    assert r <= HESS_TOL, r
+    il = torch.tril_indices(d, d, -1)
+    assert torch.equal(got[il[0], il[1]], h0.cpu()[il[0], il[1]])
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 2048), (torch.float32, 1024), (torch.bfloat16, 384)],
+                         ids=["bf16-2048", "fp32-1024", "bf16-384"])
+def test_running_mean_beta_once(dev, dtype, d):
+    """H = beta H + alpha sum_k X_k^T X_k: beta applies once per call (on the
+    one-launch route and on the per-segment routes)."""
+    say(f"segmented syrk with beta {dtype} d={d}")
+    sizes = [1024, 2048, 96]
+    xs = _segs(sizes, d, dtype, dev, seed=31)
+    h0 = _h0(d, dev)
+    H = h0.clone()
+    ops.hessian_syrk_segments_(H, xs, alpha=0.25, beta=0.5)
+    ref = h0.double().cpu() * 0.5
+    xc = torch.cat([x.cpu().double() for x in xs])
+    ref += 0.25 * (xc.t() @ xc)
+    iu = torch.triu_indices(d, d)
+    r = rel_fro(H.cpu()[iu[0], iu[1]], ref[iu[0], iu[1]])
+    assert r <= HESS_TOL, r
+    Hz = h0.clone()
+    ops.hessian_syrk_segments_(Hz, [x[:0] for x in xs], alpha=0.25, beta=0.5)   # no rows: H scaled once
+    assert torch.equal(Hz.cpu()[iu[0], iu[1]], (h0 * 0.5).cpu()[iu[0], iu[1]])
+
+
+def test_stage_by_reference_equals_stage_by_copy(dev):
+    """The GPTQ hook's stage holding 2048-row calls by reference gives bit
+    for bit the Hessian of the same stage copying them into one buffer."""
+    say("HessianStage: held calls vs copied calls, 40 calls of 2048 x 4096")
+    d = 4096
+    lin = torch.nn.Linear(d, 1, bias=False, device=dev)
+    xs = [workloads.heavy_tailed_activations((1, 2048, d), seed=500 + i).to(dev) for i in range(40)]
+    H1, H2 = gptq.make_empty_hessian(lin), gptq.make_empty_hessian(lin)
+    st1, st2 = HessianStage(), HessianStage()
+    flushed = []
+
+    def by_ref(segs, samples):
+        flushed.append([s.data_ptr() for s in segs])
+        ops.hessian_syrk_segments_(H1, segs, alpha=2.0)
+
+    def by_copy(segs, samples):
+        ops.hessian_syrk_(H2, torch.cat(segs), alpha=2.0)
+    for x in xs:
+        rows, added = gptq.hessian_rows(x, lin, dev)
+        st1.add(rows, added, by_ref)
+        st2.add(rows.clone(), added, by_copy)
+    st1.flush(by_ref)
+    st2.flush(by_copy)
+    torch.cuda.synchronize()
+    assert [len(f) for f in flushed] == [32, 8]
+    assert flushed[0][0] == xs[0].data_ptr()     # the hook's own tensor, not a copy
+    assert torch.equal(H1, H2)

@@ -114,9 +114,9 @@ def _modifier_hessian(xs, dev, name):
     for x in xs:
         rows, added = gptq.hessian_rows(x, lin, dev)
         ng += added
-        stage.add(rows, added, lambda r, _s: ops.hessian_syrk_(Hg, r, alpha=2.0))
+        stage.add(rows, added, lambda segs, _s: ops.hessian_syrk_segments_(Hg, segs, alpha=2.0))
         Ho, no = og.accumulate_hessian(x, Ho, no)
-    stage.flush(lambda r, _s: ops.hessian_syrk_(Hg, r, alpha=2.0))
+    stage.flush(lambda segs, _s: ops.hessian_syrk_segments_(Hg, segs, alpha=2.0))
     Hg = Hg.cpu()
     assert float(ng) == float(no)
     r = rel_fro(torch.triu(Hg), torch.triu(Ho))

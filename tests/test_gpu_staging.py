@@ -33,9 +33,9 @@ def test_gptq_staged_hessian_matches_per_call(dev):
     H2, n2 = gptq.make_empty_hessian(lin), torch.zeros((), device=dev)
     stage, calls = HessianStage(16384), []
 
-    def flush(rows, samples):
-        calls.append(rows.shape[0])
-        ops.hessian_syrk_(H2, rows, alpha=2.0)
+    def flush(segs, samples):
+        calls.append(sum(s.shape[0] for s in segs))
+        ops.hessian_syrk_segments_(H2, segs, alpha=2.0)
     for x in xs:
         rows, added = gptq.hessian_rows(x, lin, dev)
         n2 += added
@@ -62,8 +62,8 @@ def test_sparsegpt_staged_running_mean_matches_per_call(dev):
     H2, n2, folded = sparsegpt.make_empty_hessian(lin), 0, [0]
     stage = HessianStage()
 
-    def flush(rows, samples):
-        folded[0] = sparsegpt.fold_rows(H2, rows, folded[0], samples)
+    def flush(segs, samples):
+        folded[0] = sparsegpt.fold_rows(H2, segs, folded[0], samples)
     for x in xs:
         rows, added = sparsegpt.hessian_rows(x, lin, dev)
         n2 += added

@@ -1,5 +1,7 @@
 """Host logic of the Hessian staging (no GPU): every row reaches the
-accumulation exactly once, in call order, with the calls' sample counts."""
+accumulation exactly once, in call order, with the calls' sample counts;
+16-bit rows at least 512 wide are handed over as the callers' own tensors
+(no copy) unless they are small, cannot be held, or were modified in place."""
 import torch
 import pytest
 
@@ -9,9 +11,12 @@ from llmcompressor_amd.staging import HessianStage
 class Recorder:
     def __init__(self):
         self.calls = []
+        self.segs = []
 
-    def __call__(self, rows, samples):
-        self.calls.append((rows.clone(), samples))
+    def __call__(self, segs, samples):
+        assert isinstance(segs, list) and segs
+        self.segs.append(list(segs))
+        self.calls.append((torch.cat([s.clone() for s in segs]), samples))
 
 
 def _run(sizes, tokens, dtypes=None, d=8):
@@ -102,3 +107,73 @@ def test_stage_rows_capped_at_512_mib():
     assert stage_tokens(DEFAULT_TOKENS, 14336, 4) == 8192
     assert stage_tokens(1024, 64, 2) == 1024
     assert stage_tokens(DEFAULT_TOKENS, 1 << 20, 4) == 2048      # never below one 2048-row sample
+
+
+def _bf(n, d=512, tag=0):
+    return (torch.arange(n * d, dtype=torch.float32).reshape(n, d) % 251 + tag).to(torch.bfloat16)
+
+
+def test_wide_16bit_calls_held_by_reference():
+    """2048-row bf16 calls are the segments themselves (no copy), in call
+    order; small calls are copied into one buffer segment after them."""
+    rec, stage = Recorder(), HessianStage(8192)
+    xs = [_bf(2048, tag=i) for i in range(3)]
+    small = [_bf(100, tag=10 + i) for i in range(2)]
+    stage.add(xs[0], 1, rec)
+    stage.add(small[0], 1, rec)
+    stage.add(xs[1], 1, rec)
+    stage.add(small[1], 1, rec)
+    stage.add(xs[2], 1, rec)
+    stage.flush(rec)
+    assert len(rec.segs) == 1 and rec.calls[0][1] == 5
+    segs = rec.segs[0]
+    assert [s.data_ptr() for s in segs[:3]] == [x.data_ptr() for x in xs]
+    assert torch.equal(segs[3], torch.cat(small))
+    assert stage.fill == 0 and not stage._segs
+
+
+def test_held_rows_modified_in_place_raise():
+    rec, stage = Recorder(), HessianStage(8192)
+    x = _bf(1024)
+    stage.add(x, 1, rec)
+    x.add_(1)
+    with pytest.raises(RuntimeError, match="modified in place"):
+        stage.flush(rec)
+    assert not rec.calls
+
+
+def test_unholdable_calls_are_copied():
+    """A view into a much larger tensor, another row stride and an inference
+    tensor are held as copies (still one segment each)."""
+    rec, stage = Recorder(), HessianStage(16384)
+    big = _bf(8192)
+    view = big[:1024]                     # storage eight times the rows
+    strided = _bf(1024, d=1024)[:, :512]  # row stride 1024
+    with torch.inference_mode():
+        inf = _bf(1024, tag=3)
+    for x in (view, strided, inf):
+        stage.add(x, 1, rec)
+    stage.flush(rec)
+    segs = rec.segs[0]
+    assert len(segs) == 3
+    for s, x in zip(segs, (view, strided, inf)):
+        assert s.data_ptr() != x.data_ptr() and s.is_contiguous() and torch.equal(s, x)
+
+
+def test_segment_count_flushes():
+    from llmcompressor_amd.staging import MAX_SEGMENTS
+    rec, stage = Recorder(), HessianStage(1 << 20)
+    for i in range(MAX_SEGMENTS + 3):
+        stage.add(_bf(256, tag=i % 7), 1, rec)
+    stage.flush(rec)
+    assert [len(s) for s in rec.segs] == [MAX_SEGMENTS, 3]
+    assert [c[1] for c in rec.calls] == [MAX_SEGMENTS, 3]
+
+
+def test_narrow_or_fp32_rows_stay_copied():
+    rec, stage = Recorder(), HessianStage(8192)
+    xs = [_bf(1024, d=256, tag=i) for i in range(3)]
+    for x in xs:
+        stage.add(x, 1, rec)
+    stage.flush(rec)
+    assert len(rec.segs[0]) == 1 and torch.equal(rec.segs[0][0], torch.cat(xs))
