@@ -27,7 +27,14 @@ struct GemmArgs {
   // C is A itself (same rows, ldc == lda): every workgroup must own whole
   // rows of C, so N fits one column tile and B is transposed
   int in_place;
+  // fp32-accurate product on the bf16 MFMA (each operand split into three
+  // bf16 parts, six products per 16-deep slice) where the large-K kernel
+  // takes it: plain products with K >= 256
+  int x6;
 };
+
+// Whether products asking for x6 take it (MI355Q_GEMM_X6=0 turns it off).
+bool x6_enabled();
 
 // Launches the batched GEMM (batch = total number of products) on `stream`;
 // returns a status code.

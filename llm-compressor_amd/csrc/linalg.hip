@@ -568,7 +568,50 @@ __device__ __forceinline__ void dma16(const void* gaddr, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_addr) : "memory", "m0");
 }
 
-template <int TM, int TN, int WGM, int WGN, bool BT, int NS>
+// fp32-accurate products on the bf16 MFMA ("x6"): every fp32 operand value
+// v is split exactly into three bf16 parts, v = h + m + l (h = bf16(v),
+// m = bf16(v - h), l = v - h - m, which has at most 8 significant bits and
+// is exact in bf16; the subtractions are exact in fp32), and a 16-deep slice
+// of A B is summed as the six products h h', h m', m h', h l', m m', l h'
+// on v_mfma_f32_32x32x16_bf16 (exact products, fp32 accumulation).  The
+// three dropped products are below 2^-24 of |a| |b| each, about the rounding
+// of one fp32 product; the sum is rounded in the MFMA's fp32 accumulator, as
+// on the fp32 MFMA.  Six bf16 MFMAs (192 cycles) replace the eight fp32
+// MFMAs (512 cycles) of a 16-deep slice; the splits (44 VALU instructions
+// per eight values, each wave splitting its own fragments) then bound the
+// kernel, since a wave's VALU work and its MFMAs were measured not to
+// overlap (busy cycles add up): the GPTQ lazy update 4096 x 3072 x 1024
+// takes 202 us against 248 us on the fp32 MFMA.  (Operands beyond 3.39e38,
+// where bf16 rounding overflows, do not occur in the solve's products.)
+
+// two fp32 values to a packed bf16 pair (one v_cvt_pk_bf16_f32, round to
+// nearest even), first value in the low half
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  typedef float f32x2v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){a, b}, bf16x2v));
+}
+// the exact three-part split of a pair: 11 VALU instructions (the bf16
+// halves read back as fp32 by a shift and a mask)
+__device__ __forceinline__ void split_x6_pair(float a, float b, uint32_t& h, uint32_t& m, uint32_t& l) {
+  h = pk_bf16(a, b);
+  const float ra = a - __uint_as_float(h << 16), rb = b - __uint_as_float(h & 0xffff0000u);
+  m = pk_bf16(ra, rb);
+  const float sa = ra - __uint_as_float(m << 16), sb = rb - __uint_as_float(m & 0xffff0000u);
+  l = pk_bf16(sa, sb);
+}
+__device__ __forceinline__ void split_x6(const f32x4_t& lo4, const f32x4_t& hi4, bf16x8_t* o) {
+  uint32_t h[4], m[4], l[4];
+  split_x6_pair(lo4[0], lo4[1], h[0], m[0], l[0]);
+  split_x6_pair(lo4[2], lo4[3], h[1], m[1], l[1]);
+  split_x6_pair(hi4[0], hi4[1], h[2], m[2], l[2]);
+  split_x6_pair(hi4[2], hi4[3], h[3], m[3], l[3]);
+  o[0] = __builtin_bit_cast(bf16x8_t, (u32x4_t){h[0], h[1], h[2], h[3]});
+  o[1] = __builtin_bit_cast(bf16x8_t, (u32x4_t){m[0], m[1], m[2], m[3]});
+  o[2] = __builtin_bit_cast(bf16x8_t, (u32x4_t){l[0], l[1], l[2], l[3]});
+}
+
+template <int TM, int TN, int WGM, int WGN, bool BT, int NS, bool X6 = false>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(GemmArgs g) {
   constexpr int NW = WGM * WGN;
   constexpr int WTM = TM / WGM, WTN = TN / WGN;      // wave tile
@@ -722,7 +765,84 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(GemmArgs g)
   };
 
   constexpr int ND = DA + DB;
-  if (nst > 0) {
+  if constexpr (X6) {
+    static_assert(NS >= 3 && (NS - 1) * ND < 64 && MB * NB2 > 1, "x6: three or more ring slots, two or more 32 x 32 blocks per wave");
+    // Per stage two 16-deep steps (groups 0, 1 and 2, 3).  The barrier that
+    // publishes stage st + 1 sits between them: the MFMAs of a step run
+    // interleaved with the splits of the next step's operands, also across
+    // the stage boundary, so the MFMA pipe is fed while the VALU splits.
+    struct Split { bf16x8_t a[MB][3], b[NB2][3]; };
+    auto split_step = [&](const Frag& fe, const Frag& fo, Split& sp) __attribute__((always_inline)) {
+#pragma unroll
+      for (int bm = 0; bm < MB; ++bm) split_x6(fe.a[bm], fo.a[bm], sp.a[bm]);
+#pragma unroll
+      for (int bn = 0; bn < NB2; ++bn) split_x6(fe.b[bn], fo.b[bn], sp.b[bn]);
+    };
+    // the six products per block, term-major so that consecutive MFMAs
+    // update different accumulators
+    auto mma_x6 = [&](const Split& sp) __attribute__((always_inline)) {
+      constexpr int TA[6] = {1, 2, 0, 1, 0, 0}, TB[6] = {1, 0, 2, 0, 1, 0};
+#pragma unroll
+      for (int t = 0; t < 6; ++t)
+#pragma unroll
+        for (int bm = 0; bm < MB; ++bm)
+#pragma unroll
+          for (int bn = 0; bn < NB2; ++bn)
+            acc[bm * NB2 + bn] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(sp.a[bm][TA[t]], sp.b[bn][TB[t]], acc[bm * NB2 + bn], 0, 0, 0);
+    };
+    // MFMAs of one step with the VALU work of the next step's split between
+    // them (44 VALU instructions per eight values split; a 32-cycle MFMA
+    // leaves room for about seven)
+    constexpr int VPM = (44 * (MB + NB2) + 6 * MB * NB2 - 1) / (6 * MB * NB2);
+    auto interleave = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < 6 * MB * NB2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+      }
+    };
+    if (nst > 0) {
+#pragma unroll
+      for (int p = 0; p < NS; ++p)
+#pragma unroll
+        for (int i = 0; i < ND; ++i) issue(p, i);
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 1) * ND) : "memory");
+      Split s0, s1;
+      {
+        Frag fe, fo;
+        read_group(lds, 0, fe);
+        read_group(lds, 1, fo);
+        split_step(fe, fo, s0);
+      }
+      for (int64_t st = 0; st < nst; ++st) {
+        const char* sl = lds + (st % NS) * SBYTES;
+        {
+          Frag fe, fo;
+          read_group(sl, 2, fe);
+          read_group(sl, 3, fo);
+          mma_x6(s0);
+          split_step(fe, fo, s1);
+          interleave();
+        }
+        // stage st + 1 complete (st + 2 may be in flight) and every wave
+        // done reading stage st, whose slot then takes stage st + 3
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * ND) : "memory");
+#pragma unroll
+        for (int i = 0; i < ND; ++i) issue(st + NS, i);
+        {
+          Frag fe, fo;
+          const char* sn = lds + ((st + 1) % NS) * SBYTES;
+          read_group(sn, 0, fe);
+          read_group(sn, 1, fo);
+          mma_x6(s1);
+          split_step(fe, fo, s0);   // past the last stage: a re-read of the last stage, never used
+          interleave();
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+  } else if (nst > 0) {
 #pragma unroll
     for (int p = 0; p < NS - 1; ++p)
 #pragma unroll
@@ -1975,6 +2095,15 @@ HinvLayout hinv_layout(int64_t d) {
 
 }  // namespace
 
+// The x6 products, unless MI355Q_GEMM_X6=0 (every product then on the fp32 MFMA).
+bool x6_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("MI355Q_GEMM_X6");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   if (g.M <= 0 || g.N <= 0 || batch <= 0) return MI355Q_OK;
   if (g.in_place) {
@@ -2023,6 +2152,28 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   const bool v16 = g.K % 4 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && aligned16(g.A) && aligned16(g.B) &&
                    (b_trans || g.N % 4 == 0) && g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 &&
                    g.strideB2 % 4 == 0;
+  if (g.K >= 256 && v16 && batch <= 65535 && ((g.M + 63) / 64) * ((g.N + 63) / 64) < (1ll << 31) && g.x6 &&
+      x6_enabled() && !g.lower_only && !g.a_lower && !g.b_lower) {
+    // fp32-accurate bf16 products: 128 x 128 tiles on four waves (64 x 64
+    // each) when they fill the CUs, else 64 x 128
+#define MQ_DMA_X6(TM, TN, WM, WN, NSX)                                                                              \
+  do {                                                                                                         \
+    dim3 grid((unsigned)(((g.N + TN - 1) / TN) * ((g.M + TM - 1) / TM)), 1, (unsigned)batch);                  \
+    if (b_trans)                                                                                               \
+      hipLaunchKernelGGL((gemm_dma_kernel<TM, TN, WM, WN, true, NSX, true>), grid, dim3(64 * WM * WN), 0, stream, g); \
+    else                                                                                                       \
+      hipLaunchKernelGGL((gemm_dma_kernel<TM, TN, WM, WN, false, NSX, true>), grid, dim3(64 * WM * WN), 0, stream, g); \
+  } while (0)
+    // (eight waves of 64 x 32, and rings of four to six stages, measured no
+    // faster: the splits' VALU work bounds the kernel, not the loads)
+    if (((g.M + 127) / 128) * ((g.N + 127) / 128) * batch >= 256)
+      MQ_DMA_X6(128, 128, 2, 2, 3);
+    else
+      MQ_DMA_X6(64, 128, 2, 2, 3);
+#undef MQ_DMA_X6
+    MQ_LAUNCH_CHECK();
+    return MI355Q_OK;
+  }
   if (g.K >= 256 && v16 && batch <= 65535 && ((g.M + 63) / 64) * ((g.N + 63) / 64) < (1ll << 31)) {
 #define MQ_DMA(TM, TN, WM, WN)                                                                             \
   do {                                                                                                     \

@@ -106,6 +106,7 @@ inline int lazy_update(float* w, int64_t rows, int64_t cols, int64_t batch, cons
   g.C = w + c0; g.ldc = cols; g.strideC = rows * cols;
   g.M = rows; g.N = c1 - c0; g.K = k1 - k0;
   g.alpha = -1.f; g.beta = 1.f;
+  g.x6 = 1;
   return gemm_f32(g, false, (int)batch, st);
 }
 
