@@ -29,7 +29,9 @@ struct GemmArgs {
   int in_place;
   // fp32-accurate product on the bf16 MFMA (each operand split into three
   // bf16 parts, six products per 16-deep slice) where the large-K kernel
-  // takes it: plain products with K >= 256
+  // takes it (K >= 256: the GPTQ / SparseGPT lazy updates, the blocked
+  // Cholesky's rank-512 updates and the triangular inverse's doubling
+  // products)
   int x6;
 };
 

@@ -2153,7 +2153,7 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
                    (b_trans || g.N % 4 == 0) && g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 &&
                    g.strideB2 % 4 == 0;
   if (g.K >= 256 && v16 && batch <= 65535 && ((g.M + 63) / 64) * ((g.N + 63) / 64) < (1ll << 31) && g.x6 &&
-      x6_enabled() && !g.lower_only && !g.a_lower && !g.b_lower) {
+      x6_enabled()) {
     // fp32-accurate bf16 products: 128 x 128 tiles on four waves (64 x 64
     // each) when they fill the CUs, else 64 x 128
 #define MQ_DMA_X6(TM, TN, WM, WN, NSX)                                                                              \
@@ -2166,7 +2166,9 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   } while (0)
     // (eight waves of 64 x 32, and rings of four to six stages, measured no
     // faster: the splits' VALU work bounds the kernel, not the loads)
-    if (((g.M + 127) / 128) * ((g.N + 127) / 128) * batch >= 256)
+    // (triangular and lower-only products: the smaller tile, whose K
+    // ranges and diagonal waste are finer)
+    if (!g.lower_only && !g.a_lower && !g.b_lower && ((g.M + 127) / 128) * ((g.N + 127) / 128) * batch >= 256)
       MQ_DMA_X6(128, 128, 2, 2, 3);
     else
       MQ_DMA_X6(64, 128, 2, 2, 3);
@@ -2403,6 +2405,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       s.B = P; s.ldb = ldp; s.strideB = wsf;
       s.C = F + c_end * d + c_end; s.ldc = d; s.strideC = wsf;
       s.M = rest2; s.N = rest2; s.K = kk; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
+      s.x6 = 1;
       int rc = gemm_f32(s, true, (int)batch, st);
       if (rc) return rc;
     }
@@ -2439,6 +2442,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       t1.C = T; t1.ldc = s; t1.strideC = s2 * s; t1.strideC2 = wsf;
       t1.inner = npairs; t1.b_lower = 1;
       t1.M = s2; t1.N = s; t1.K = s; t1.alpha = 1.f; t1.beta = 0.f;
+      t1.x6 = 1;
       int rc = gemm_f32(t1, false, (int)(npairs * batch), st);
       if (rc) return rc;
       // X[c0:c0+s2, a0:a0+s] = -X[c0:c0+s2, c0:c0+s2] * T (X22 lower triangular)
@@ -2448,6 +2452,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
       t2.C = X + c0 * d + a0; t2.ldc = d; t2.strideC = stride_diag; t2.strideC2 = wsf;
       t2.inner = npairs; t2.a_lower = 1;
       t2.M = s2; t2.N = s; t2.K = s2; t2.alpha = -1.f; t2.beta = 0.f;
+      t2.x6 = 1;
       rc = gemm_f32(t2, false, (int)(npairs * batch), st);
       if (rc) return rc;
     }
