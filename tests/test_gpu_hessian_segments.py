@@ -121,3 +121,25 @@ def test_stage_by_reference_equals_stage_by_copy(dev):
     assert [len(f) for f in flushed] == [32, 8]
     assert flushed[0][0] == xs[0].data_ptr()     # the hook's own tensor, not a copy
     assert torch.equal(H1, H2)
+
+
+def test_wide_long_call_equals_segmented_call(dev):
+    """A 12288-wide Hessian over 131072 tokens (1176 upper tiles, two token
+    splits of 65536) takes the 4-wave layout of the one-call syrk; the
+    segmented syrk keeps the 8-wave layout.  Both accumulate every element
+    over the same 32-row stages in the same order, so they agree bit for bit;
+    a block of columns is also checked against an fp64 product."""
+    n, d = 131072, 12288
+    say(f"one-call syrk (4-wave layout) vs segmented syrk (8-wave layout) d={d} n={n}")
+    x = workloads.heavy_tailed_activations((n, d), seed=41).to(torch.bfloat16).to(dev)
+    H1 = torch.zeros(d, d, device=dev)
+    H2 = torch.zeros(d, d, device=dev)
+    ops.hessian_syrk_(H1, x, alpha=2.0)
+    ops.hessian_syrk_segments_(H2, [x[: n // 2], x[n // 2:]], alpha=2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(H1, H2)
+    c0 = d - 1024                # the last columns, over every row of the upper triangle
+    ref = 2.0 * (x.double().t() @ x[:, c0:].double())
+    up = torch.arange(d, device=dev)[:, None] <= torch.arange(c0, d, device=dev)[None, :]
+    r = rel_fro(H1[:, c0:][up], ref[up])
+    assert r <= HESS_TOL, r
