@@ -1186,7 +1186,13 @@ int device_cus() {
 int choose_splits(int64_t n, int T, int cus) {
   const int64_t s = n / 2048;
   int S = s >= 8 ? 8 : s >= 4 ? 4 : s >= 2 ? 2 : 1;
-  if (T > 2 * cus && S > 2) S = 2;
+  // Wide Hessians (over two rounds of tiles) take at most 4 splits, and 4
+  // only over 131072 tokens or more, where the rounds saved outweigh the
+  // larger reduction: d = 14336 over 524288 tokens 25 rounds of a quarter of
+  // the tokens instead of 13 of half, 101.4 -> 99.1 ms; d = 8192 over 262144
+  // tokens 9 instead of 10 half-rounds, 17.7 -> 16.5 ms (65536 tokens at
+  // d = 14336: 12.3 -> 12.5 ms, so shorter calls keep two).
+  if (T > 2 * cus && S > 2) S = n >= 131072 ? 4 : 2;
   if (S == 8) return S;  // the dense plan's tail parts even out its rounds
   // Below that, the fewest splits that reach the shortest time: k splits
   // take ceil(T k / cus) rounds on the CUs, each 1 / k of the tokens, and

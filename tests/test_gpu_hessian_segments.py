@@ -124,14 +124,19 @@ def test_stage_by_reference_equals_stage_by_copy(dev):
 
 
 def test_wide_long_call_equals_segmented_call(dev):
-    """A 12288-wide Hessian over 131072 tokens (1176 upper tiles, two token
+    """A 12288-wide Hessian over 262144 tokens (1176 upper tiles, four token
     splits of 65536) takes the 4-wave layout of the one-call syrk; the
     segmented syrk keeps the 8-wave layout.  Both accumulate every element
     over the same 32-row stages in the same order, so they agree bit for bit;
     a block of columns is also checked against an fp64 product."""
-    n, d = 131072, 12288
+    n, d = 262144, 12288
     say(f"one-call syrk (4-wave layout) vs segmented syrk (8-wave layout) d={d} n={n}")
-    x = workloads.heavy_tailed_activations((n, d), seed=41).to(torch.bfloat16).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(41)
+    x = torch.empty(n, d, dtype=torch.bfloat16, device=dev)   # per-column lognormal scales, made on the GPU
+    scale = torch.exp(torch.randn(d, generator=g, device=dev))
+    for r0 in range(0, n, 32768):
+        x[r0:r0 + 32768] = torch.randn(32768, d, generator=g, device=dev) * scale
     H1 = torch.zeros(d, d, device=dev)
     H2 = torch.zeros(d, d, device=dev)
     ops.hessian_syrk_(H1, x, alpha=2.0)
@@ -139,7 +144,11 @@ def test_wide_long_call_equals_segmented_call(dev):
     torch.cuda.synchronize()
     assert torch.equal(H1, H2)
     c0 = d - 1024                # the last columns, over every row of the upper triangle
-    ref = 2.0 * (x.double().t() @ x[:, c0:].double())
+    ref = torch.zeros(d, 1024, dtype=torch.float64, device=dev)
+    for r0 in range(0, n, 32768):
+        xc = x[r0:r0 + 32768].double()
+        ref += 2.0 * (xc.t() @ xc[:, c0:])
+    del xc
     up = torch.arange(d, device=dev)[:, None] <= torch.arange(c0, d, device=dev)[None, :]
     r = rel_fro(H1[:, c0:][up], ref[up])
     assert r <= HESS_TOL, r
