@@ -712,23 +712,37 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
   if (slot < 0) {
     const bool diag = ti == tj;
     const int64_t ldh = (MODE == kDense || MODE == kDenseSeg) ? p.ldh : p.d;
+    if (p.beta == 0.f) {
+      // H not read: each accumulator register goes straight to its row of H
+      // (a store covers 32 consecutive columns of two rows, lanes 0..31 and
+      // 32..63), with no pass through LDS and no barrier
+#pragma unroll
+      for (int x = 0; x < MB; ++x)
+#pragma unroll
+        for (int y = 0; y < NBN; ++y)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t gi = fa0 + wm * 128 + x * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int64_t gj = fb0 + wn * NBN * 32 + y * 32 + (lane & 31);
+            if (gi < p.d && gj < p.d && (!diag || gi <= gj)) mat.h[gi * ldh + gj] = p.alpha * acc[x][y][r];
+          }
+      return;
+    }
     if ((ldh & 3) == 0 && (p.d & 3) == 0 && (reinterpret_cast<uintptr_t>(mat.h) & 15) == 0) {
-      // direct update of the upper triangle of H through the LDS ring, one
-      // half of the tile (128 rows, the accumulators of waves wm == hh) at a
-      // time: the accumulators are written row-major into LDS, then wave w
-      // updates rows RR w .. RR w + RR - 1 of the half (RR = 128 / WAVES),
-      // one 256-float row (1 KB, a float4 per lane) per store.  With
-      // beta != 0 all RR reads of H are issued before the first store, from
-      // clamped in-range addresses so that none is conditional: a
-      // conditional read makes the compiler wait for every memory operation
-      // in flight at each use, the earlier rows' stores included, which
-      // serialised the stores (19 us per tile instead of 4).  A float4 that
-      // straddles the diagonal writes its lower elements back unchanged
-      // (beta != 0) or only its upper elements (beta == 0, H not read).
+      // H = beta H + alpha acc on the upper triangle through the LDS ring,
+      // one half of the tile (128 rows, the accumulators of waves wm == hh)
+      // at a time: the accumulators are written row-major into LDS, then
+      // wave w updates rows RR w .. RR w + RR - 1 of the half (RR = 128 /
+      // WAVES), one 256-float row (1 KB, a float4 per lane) per store.  All
+      // RR reads of H are issued before the first store, from clamped
+      // in-range addresses so that none is conditional: a conditional read
+      // makes the compiler wait for every memory operation in flight at each
+      // use, the earlier rows' stores included, which serialised the stores.
+      // A float4 that straddles the diagonal writes its lower elements back
+      // unchanged.
       float* const tile = reinterpret_cast<float*>(ring);
       const int64_t gj = fb0 + 4 * lane;
       const int64_t gjc = gj < p.d ? gj : p.d - 4;
-      const bool beta0 = p.beta == 0.f;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         __syncthreads();   // the ring (or the previous half) is no longer read
@@ -747,37 +761,25 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
 #pragma unroll
         for (int k0 = 0; k0 < RR; k0 += 16) {
           f32x4_t hv[16];
-          if (!beta0) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-              const int64_t gi = fa0 + hh * 128 + wave * RR + k0 + k;
-              hv[k] = *reinterpret_cast<const f32x4_t*>(mat.h + (gi < p.d ? gi : p.d - 1) * ldh + gjc);
-            }
-            // the reads complete here, before any store
-#pragma unroll
-            for (int k = 0; k < 16; ++k) asm volatile("" ::"v"(hv[k]) : "memory");
+          for (int k = 0; k < 16; ++k) {
+            const int64_t gi = fa0 + hh * 128 + wave * RR + k0 + k;
+            hv[k] = *reinterpret_cast<const f32x4_t*>(mat.h + (gi < p.d ? gi : p.d - 1) * ldh + gjc);
           }
+          // the reads complete here, before any store
+#pragma unroll
+          for (int k = 0; k < 16; ++k) asm volatile("" ::"v"(hv[k]) : "memory");
 #pragma unroll
           for (int k = 0; k < 16; ++k) {
             const int lr = wave * RR + k0 + k;
             const int64_t gi = fa0 + hh * 128 + lr;
             if (gi < p.d && gj < p.d && (!diag || gi <= gj + 3)) {
               const f32x4_t v = *reinterpret_cast<const f32x4_t*>(tile + lr * 256 + 4 * lane);
-              float* const hp = mat.h + gi * ldh + gj;
-              if (!beta0) {
-                f32x4_t o;
+              f32x4_t o;
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                  o[c] = (!diag || gi <= gj + c) ? scaled(hv[k][c], p.beta) + p.alpha * v[c] : hv[k][c];
-                *reinterpret_cast<f32x4_t*>(hp) = o;
-              } else if (!diag || gi <= gj) {
-                *reinterpret_cast<f32x4_t*>(hp) =
-                    f32x4_t{p.alpha * v[0], p.alpha * v[1], p.alpha * v[2], p.alpha * v[3]};
-              } else {
-#pragma unroll
-                for (int c = 1; c < 4; ++c)
-                  if (gi <= gj + c) hp[c] = p.alpha * v[c];
-              }
+              for (int c = 0; c < 4; ++c)
+                o[c] = (!diag || gi <= gj + c) ? scaled(hv[k][c], p.beta) + p.alpha * v[c] : hv[k][c];
+              *reinterpret_cast<f32x4_t*>(mat.h + gi * ldh + gj) = o;
             }
           }
         }
@@ -800,7 +802,7 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
           const int mi = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), nj = lane & 31;
           if (gib + mi < p.d && gjb + nj < p.d && (!diag || mb + mi <= nb + nj)) {
             float* hp = hb + (int64_t)mi * ldh + nj;
-            *hp = p.beta == 0.f ? p.alpha * acc[x][y][r] : scaled(*hp, p.beta) + p.alpha * acc[x][y][r];
+            *hp = scaled(*hp, p.beta) + p.alpha * acc[x][y][r];
           }
         }
         __builtin_amdgcn_sched_barrier(0);
