@@ -376,10 +376,11 @@ constexpr int SK = 32;           // tokens per stage
 constexpr int NSTG = 4;          // stages in the LDS ring
 constexpr int SROW = 512;        // bytes per token row of a 256-feature operand
 constexpr int SOP = SK * SROW;   // bytes per operand per stage
-// Waves of the streaming kernel.  The 4-wave layout (128 x 128 per wave, a
-// third fewer LDS reads per MFMA, one wave per SIMD) gives the same results
-// and was measured slower: 2.14 against 2.11 ms at 131072 x 4096, 76 against
-// 59 us at 2048 tokens.
+// Waves of the streaming kernel by default.  The 4-wave layout (128 x 128
+// per wave, a third fewer LDS reads per MFMA, one wave per SIMD) gives the
+// same results; it is slower on short items and narrower Hessians (2.14
+// against 2.11 ms at 131072 x 4096, 76 against 59 us at 2048 tokens) and
+// faster on wide ones with long token splits, which the dense plan gives it.
 constexpr int kStreamWaves = 8;
 constexpr int SNT = 64 * kStreamWaves;             // its threads
 
