@@ -29,9 +29,11 @@ struct GemmArgs {
   int in_place;
   // fp32-accurate product on the bf16 MFMA (each operand split into three
   // bf16 parts, six products per 16-deep slice) where the large-K kernel
-  // takes it (K >= 256: the GPTQ / SparseGPT lazy updates, the blocked
+  // takes it: 1 for K >= 256 (the GPTQ / SparseGPT lazy updates, the blocked
   // Cholesky's rank-512 updates and the triangular inverse's doubling
-  // products)
+  // products; the sweep's K = 128 updates stay on the fp32 MFMA, as the
+  // sweep kernel computes the ones it pulls), 2 also for K = 128 (the
+  // blocked Cholesky's inner updates)
   int x6;
 };
 

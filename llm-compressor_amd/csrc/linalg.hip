@@ -2152,8 +2152,8 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
   const bool v16 = g.K % 4 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && aligned16(g.A) && aligned16(g.B) &&
                    (b_trans || g.N % 4 == 0) && g.strideA % 4 == 0 && g.strideB % 4 == 0 && g.strideA2 % 4 == 0 &&
                    g.strideB2 % 4 == 0;
-  if (g.K >= 256 && v16 && batch <= 65535 && ((g.M + 63) / 64) * ((g.N + 63) / 64) < (1ll << 31) && g.x6 &&
-      x6_enabled()) {
+  if ((g.K >= 256 || (g.K >= 128 && g.x6 == 2)) && v16 && batch <= 65535 &&
+      ((g.M + 63) / 64) * ((g.N + 63) / 64) < (1ll << 31) && g.x6 && x6_enabled()) {
     // fp32-accurate bf16 products: 128 x 128 tiles on four waves (64 x 64
     // each) when they fill the CUs, else 64 x 128
 #define MQ_DMA_X6(TM, TN, WM, WN, NSX)                                                                              \
@@ -2380,6 +2380,7 @@ int hinv_impl(const float* h_dev, int64_t ldh, int64_t sh, int64_t d, int64_t ba
         s.B = F + (k0 + nb) * d + k0; s.ldb = d; s.strideB = wsf;
         s.C = F + (k0 + nb) * d + (k0 + nb); s.ldc = d; s.strideC = wsf;
         s.M = rest; s.N = nin; s.K = nb; s.alpha = -1.f; s.beta = 1.f; s.lower_only = 1;
+        s.x6 = 2;
         rc = gemm_f32(s, true, (int)batch, st);
         if (rc) return rc;
       }
