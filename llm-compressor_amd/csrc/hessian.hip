@@ -376,11 +376,14 @@ constexpr int SK = 32;           // tokens per stage
 constexpr int NSTG = 4;          // stages in the LDS ring
 constexpr int SROW = 512;        // bytes per token row of a 256-feature operand
 constexpr int SOP = SK * SROW;   // bytes per operand per stage
-// Waves of the streaming kernel by default.  The 4-wave layout (128 x 128
-// per wave, a third fewer LDS reads per MFMA, one wave per SIMD) gives the
-// same results; it is slower on short items and narrower Hessians (2.14
-// against 2.11 ms at 131072 x 4096, 76 against 59 us at 2048 tokens) and
-// faster on wide ones with long token splits, which the dense plan gives it.
+// Waves of the streaming kernel.  The 4-wave layout (128 x 128 per wave, a
+// third fewer LDS reads per MFMA, one wave per SIMD) gives the same results
+// bit for bit and was measured slower on heavy-tailed activations: 2.14
+// against 2.11 ms at 131072 x 4096, 76 against 59 us at 2048 tokens, 105.0
+// against 101.5 ms at 524288 x 14336 (four token splits), 202.5 against
+// 197.9 ms at 262144 x 28672; it won only on Gaussian inputs at 524288 x
+// 14336 (93.9 against 97.4 ms, two splits), where the chip ran more
+// power-limited.
 constexpr int kStreamWaves = 8;
 constexpr int SNT = 64 * kStreamWaves;             // its threads
 
@@ -1230,7 +1233,6 @@ constexpr int kXcds = 8;
 struct DensePlan {
   int S = 1, T = 0, tail_start = 0, tail_f = 1;
   int64_t grid = 0, slots = 0;
-  int waves = kStreamWaves;   // of the streaming kernel (and its reduction's slot layout)
 };
 DensePlan plan_dense(int64_t n, int64_t d) {
   DensePlan pl;
@@ -1256,20 +1258,12 @@ DensePlan plan_dense(int64_t n, int64_t d) {
     pl.grid = (int64_t)kXcds * ((pl.T + G - 1) / G);
     pl.slots = pl.S > 1 ? (int64_t)pl.T * pl.S : 0;
   }
-  // Wide Hessians (over four rounds of tiles on the CUs) with long token
-  // splits take the 4-wave layout, whose third fewer LDS reads per MFMA pay
-  // off once latency is not the limit: d = 14336 over 524288 tokens 97.4 ->
-  // 93.9 ms, d = 28672 over 131072 95.0 -> 90.9 ms; below (d = 4096 to
-  // 11008) the 8-wave layout is 1-3 % faster.
-  if (tile_edge(d) == 256 && pl.T > 4 * cus && n / pl.S >= 65536) pl.waves = 4;
   return pl;
 }
 
 template <bool F16>
-void launch_syrk_t(const SyrkParams& p, int64_t d, unsigned grid, int waves, hipStream_t st) {
-  if (tile_edge(d) == 256 && waves == 4) {
-    hipLaunchKernelGGL((syrk_stream_kernel<F16, kDense, 4>), dim3(grid), dim3(256), 0, st, p, SegArg<kDense>{});
-  } else if (tile_edge(d) == 256) {
+void launch_syrk_t(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st) {
+  if (tile_edge(d) == 256) {
     hipLaunchKernelGGL((syrk_stream_kernel<F16, kDense, kStreamWaves>), dim3(grid), dim3(SNT), 0, st, p,
                        SegArg<kDense>{});
   } else {
@@ -1277,8 +1271,8 @@ void launch_syrk_t(const SyrkParams& p, int64_t d, unsigned grid, int waves, hip
   }
 }
 
-void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, int waves, hipStream_t st, bool f16) {
-  if (f16) launch_syrk_t<true>(p, d, grid, waves, st); else launch_syrk_t<false>(p, d, grid, waves, st);
+void launch_syrk(const SyrkParams& p, int64_t d, unsigned grid, hipStream_t st, bool f16) {
+  if (f16) launch_syrk_t<true>(p, d, grid, st); else launch_syrk_t<false>(p, d, grid, st);
 }
 
 // reduction of syrk_bf16_kernel partials (2 x 2 fragment order)
@@ -1358,13 +1352,10 @@ int hessian16_impl(const void* x_dev, bool f16, int64_t n_tokens, int64_t d, int
 
   SyrkParams p = dense_params(static_cast<const uint16_t*>(x_dev), n_tokens, d, ldx, h_dev, ldh, alpha, beta, pl,
                               workspace_dev);
-  launch_syrk(p, d, (unsigned)pl.grid, pl.waves, st, f16);
+  launch_syrk(p, d, (unsigned)pl.grid, st, f16);
   MQ_LAUNCH_CHECK();
   if (S > 1) {
-    if (tile_edge(d) == 256 && pl.waves == 4)  // the streaming kernel's slots, in its wave layout
-      hipLaunchKernelGGL(syrk_stream_reduce_kernel<4>, dim3((unsigned)T, 256 / ((NT / 64) * RED_CPW)), dim3(NT), 0,
-                         st, p.ws, S, pl.tail_start, pl.tail_f, p.single, d, ldh, nt, alpha, beta);
-    else if (tile_edge(d) == 256)
+    if (tile_edge(d) == 256)  // the streaming kernel's slots
       hipLaunchKernelGGL(syrk_stream_reduce_kernel<kStreamWaves>, dim3((unsigned)T, 256 / ((NT / 64) * RED_CPW)), dim3(NT), 0,
                          st, p.ws, S, pl.tail_start, pl.tail_f, p.single, d, ldh, nt, alpha, beta);
     else

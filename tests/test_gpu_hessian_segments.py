@@ -124,13 +124,13 @@ def test_stage_by_reference_equals_stage_by_copy(dev):
 
 
 def test_wide_long_call_equals_segmented_call(dev):
-    """A 12288-wide Hessian over 262144 tokens (1176 upper tiles, four token
-    splits of 65536) takes the 4-wave layout of the one-call syrk; the
-    segmented syrk keeps the 8-wave layout.  Both accumulate every element
-    over the same 32-row stages in the same order, so they agree bit for bit;
-    a block of columns is also checked against an fp64 product."""
+    """A 12288-wide Hessian over 262144 tokens (1176 upper tiles: four token
+    splits of 65536, the wide-matrix plan) in one call and as two segments:
+    both accumulate every element over the same 32-row stages in the same
+    order, so they agree bit for bit; a block of columns is also checked
+    against an fp64 product."""
     n, d = 262144, 12288
-    say(f"one-call syrk (4-wave layout) vs segmented syrk (8-wave layout) d={d} n={n}")
+    say(f"one-call syrk vs segmented syrk, four token splits, d={d} n={n}")
     g = torch.Generator(device=dev)
     g.manual_seed(41)
     x = torch.empty(n, d, dtype=torch.bfloat16, device=dev)   # per-column lognormal scales, made on the GPU
