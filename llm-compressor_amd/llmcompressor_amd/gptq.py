@@ -126,14 +126,19 @@ def _value_type(quant_args: QuantizationArgs) -> str:
     raise NotImplementedError(f"float weights of {quant_args.num_bits} bits")
 
 
-def _qparams_for_sweep(scale: torch.Tensor, zero_point: torch.Tensor, strategy: QuantizationStrategy):
+def _qparams_for_sweep(scale: torch.Tensor, zero_point: torch.Tensor, strategy: QuantizationStrategy,
+                       symmetric: bool = False):
+    """fp32 scales and zero points shaped for the sweep; symmetric: no zero
+    points (the sweep's variant without them)."""
     s = scale.to(torch.float32)
-    z = zero_point.to(torch.float32)
+    z = None if symmetric else zero_point.to(torch.float32)
     if strategy == QuantizationStrategy.TENSOR:
-        s, z = s.reshape(1, 1), z.reshape(1, 1)
+        s = s.reshape(1, 1)
+        z = None if z is None else z.reshape(1, 1)
     elif s.dim() == 1:
-        s, z = s.reshape(-1, 1), z.reshape(-1, 1)
-    return s.contiguous(), z.contiguous()
+        s = s.reshape(-1, 1)
+        z = None if z is None else z.reshape(-1, 1)
+    return s.contiguous(), None if z is None else z.contiguous()
 
 
 @dataclass
@@ -245,9 +250,7 @@ def gptq_quantize(weight: torch.Tensor, quant_args: QuantizationArgs, hessian: t
 
     hinv, dead = prep.hinv, prep.dead
     w_work = ops.gptq_load_weight(W, perm, dead)
-    s, z = _qparams_for_sweep(scale, zero_point, strategy)
-    if quant_args.symmetric:
-        z = None  # zero points are 0: the sweep's variant without them
+    s, z = _qparams_for_sweep(scale, zero_point, strategy, quant_args.symmetric)
     qmin, qmax = quant_args.q_range()
     bh = quant_args.block_structure[0] if strategy == QuantizationStrategy.BLOCK else 1
     codes, losses = ops.gptq_sweep_(w_work, hinv, s, z, strategy.value, g_idx, qmin, qmax,

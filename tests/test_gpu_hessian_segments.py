@@ -152,3 +152,4 @@ def test_wide_long_call_equals_segmented_call(dev):
     up = torch.arange(d, device=dev)[:, None] <= torch.arange(c0, d, device=dev)[None, :]
     r = rel_fro(H1[:, c0:][up], ref[up])
     assert r <= HESS_TOL, r
+
