@@ -500,6 +500,38 @@ def _spd_from_tokens(d, tokens, seed):
     return H / n
 
 
+@pytest.mark.parametrize("d,batch", [(1000, 1), (384, 1), (2048, 16)], ids=["ragged-1000", "3-blocks-384",
+                                                                          "batch16-2048"])
+def test_blocked_chain_reads_no_uninitialised_workspace(dev, d, batch):
+    """The blocked chain (orders not a multiple of 128, fewer than 4 blocks,
+    batches over 8) builds X = L^-1 in its workspace without clearing it:
+    every element it reads was written first.  With the workspace filled
+    with NaN beforehand, hinv equals bit for bit the one from a zeroed
+    workspace."""
+    import ctypes as C
+    from llmcompressor_amd import _lib as L
+    say(f"blocked chain on a NaN workspace d={d} batch={batch}")
+    Hs = torch.stack([torch.triu(_spd_from_tokens(d, 2 * d, seed=70 + b)) for b in range(batch)]).to(dev)
+    ns = torch.ones(batch, dtype=torch.float32, device=dev)
+    lib = L.lib()
+    nbytes = lib.mi355q_gptq_hinv_workspace_size(d) * batch
+    out = []
+    for fill in (0.0, float("nan")):
+        ws = torch.full(((nbytes + 3) // 4,), fill, dtype=torch.float32, device=dev)
+        hinv = torch.empty((batch, d, d), dtype=torch.float32, device=dev)
+        dead = torch.empty((batch, d), dtype=torch.int32, device=dev)
+        status = torch.zeros(batch, dtype=torch.int32, device=dev)
+        L.check(lib.mi355q_gptq_hinv_batched(Hs.data_ptr(), Hs.stride(1), Hs.stride(0), d, batch, None, 0,
+                                             ns.data_ptr(), C.c_float(0.01), hinv.data_ptr(), d * d,
+                                             dead.data_ptr(), status.data_ptr(), ws.data_ptr(), nbytes,
+                                             L.stream_of(Hs)))
+        torch.cuda.synchronize()
+        assert int(status.abs().sum()) == 0
+        out.append(hinv.cpu())
+    assert torch.isfinite(out[1]).all()
+    assert torch.equal(out[0], out[1])
+
+
 # d = 256, 384, 1000: the blocked chain; 512, 1024, 2048 (multiples of 128
 # with at least 4 blocks): the dataflow factorisation
 @pytest.mark.parametrize("d,perm", [(256, False), (1000, False), (384, True), (512, False), (1024, True),
