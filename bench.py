@@ -159,7 +159,7 @@ def main():
     del H64
 
     # the same 64 calls through the modifiers' forward hook, which holds the
-    # calls' rows (by reference) and accumulates them 65536 rows at a time in
+    # calls' rows (by reference) and accumulates them 131072 rows at a time in
     # one segmented syrk; each call's input is a tensor of its own, as a
     # forward pass makes it (a view into one 1 GiB tensor would be copied)
     calls64 = [ch.clone() for ch in chunks64]

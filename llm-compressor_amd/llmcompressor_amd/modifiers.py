@@ -271,8 +271,8 @@ class GPTQModifier(QuantizationModifier, _SharedHessians, _Staging):
     Beyond the reference's arguments: ``share_hessians`` (modules fed the
     same tensor accumulate one Hessian), ``hessian_batch_tokens`` /
     ``hessian_stage_bytes`` (the rows of small calls are held, by reference
-    or copied, up to 65536 rows and 512 MiB per module, and accumulated one
-    long syrk at a time, while the rows one modifier holds stay within 2 GiB
+    or copied, up to 131072 rows and 1 GiB per module, and accumulated one
+    long syrk at a time, while the rows one modifier holds stay within 4 GiB
     by default)
     and
     ``batch_experts``: the same-shaped projections of an MoE expert list
@@ -581,7 +581,7 @@ class SparseGPTModifier(_SharedHessians, _Staging):
     ``share_hessians``: modules fed the same tensor accumulate one Hessian
     (as ``GPTQModifier``).  ``hessian_batch_tokens`` / ``hessian_stage_bytes``:
     the rows of small calls are staged on the device and folded in long
-    syrk calls, with the stage buffers of one modifier within 2 GiB by
+    syrk calls, with the stage buffers of one modifier within 4 GiB by
     default (0 tokens folds every call at once, as the reference does).
     """
 

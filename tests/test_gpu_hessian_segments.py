@@ -102,7 +102,7 @@ def test_stage_by_reference_equals_stage_by_copy(dev):
     lin = torch.nn.Linear(d, 1, bias=False, device=dev)
     xs = [workloads.heavy_tailed_activations((1, 2048, d), seed=500 + i).to(dev) for i in range(40)]
     H1, H2 = gptq.make_empty_hessian(lin), gptq.make_empty_hessian(lin)
-    st1, st2 = HessianStage(), HessianStage()
+    st1, st2 = HessianStage(65536), HessianStage(65536)   # 32 held calls per flush
     flushed = []
 
     def by_ref(segs, samples):

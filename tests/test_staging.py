@@ -99,12 +99,12 @@ def test_modifier_stage_budget():
     assert m._stage_for(mods[0], x) is not None            # room again
 
 
-def test_stage_rows_capped_at_512_mib():
+def test_stage_rows_capped_at_1_gib():
     from llmcompressor_amd.staging import DEFAULT_TOKENS, stage_tokens
-    assert DEFAULT_TOKENS == 65536
-    assert stage_tokens(DEFAULT_TOKENS, 4096, 2) == 65536        # 512 MiB
-    assert stage_tokens(DEFAULT_TOKENS, 14336, 2) == 18432       # 504 MiB
-    assert stage_tokens(DEFAULT_TOKENS, 14336, 4) == 8192
+    assert DEFAULT_TOKENS == 131072
+    assert stage_tokens(DEFAULT_TOKENS, 4096, 2) == 131072       # 1 GiB: 64 calls of 2048 rows
+    assert stage_tokens(DEFAULT_TOKENS, 14336, 2) == 36864       # 1008 MiB
+    assert stage_tokens(DEFAULT_TOKENS, 14336, 4) == 18432
     assert stage_tokens(1024, 64, 2) == 1024
     assert stage_tokens(DEFAULT_TOKENS, 1 << 20, 4) == 2048      # never below one 2048-row sample
 
