@@ -2050,6 +2050,9 @@ __global__ void place_diag_inv_kernel(const float* linv, int64_t d, float* X, in
   for (int e = threadIdx.x; e < NB * NB; e += blockDim.x) {
     const int i = e / NB, j = e % NB;
     if (k0 + i < d && k0 + j < d) X[(k0 + i) * d + (k0 + j)] = linv[(int64_t)blk * NB * NB + e];
+    // zeros in the block right of it: the 256-row tiles of a lower-triangular
+    // operand read that far above the diagonal
+    if (k0 + i < d && k0 + NB + j < d) X[(k0 + i) * d + (k0 + NB + j)] = 0.f;
   }
 }
 
@@ -2160,13 +2163,14 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
     // (triangular and lower-only products: the smaller tile, whose K
     // ranges and diagonal waste are finer)
     // 256 x 128 tiles on eight waves (64 x 64 each, two per SIMD: one
-    // wave's splits run beside the other's MFMAs) for plain and lower-only
-    // products that fill the CUs with them: the d = 14336 solve's lazy
-    // updates 8.53 -> 8.04 ms, its Cholesky chain 20.4 -> 19.5 ms, 128
-    // batched d = 2048 chains 10.89 -> 10.66 ms, C0 unchanged
+    // wave's splits run beside the other's MFMAs) for products that fill
+    // the CUs with them: the d = 14336 solve's lazy updates 8.53 -> 8.04 ms,
+    // its Cholesky chain 20.4 -> 19.5 ms (lower-only rank-512 updates) ->
+    // 18.4 ms (triangular doubling products), 128 batched d = 2048 chains
+    // 10.89 -> 10.66 ms, C0 unchanged
     const bool plain = !g.lower_only && !g.a_lower && !g.b_lower;
     const int64_t wide_tiles = ((g.M + 255) / 256) * ((g.N + 127) / 128) * batch;
-    if ((plain && wide_tiles >= 128) || (g.lower_only && !g.a_lower && !g.b_lower && wide_tiles >= 256))
+    if ((plain && wide_tiles >= 128) || (!plain && wide_tiles >= 256))
       MQ_DMA_X6(256, 128, 4, 2, 3);
     else if (plain && ((g.M + 127) / 128) * ((g.N + 127) / 128) * batch >= 256)
       MQ_DMA_X6(128, 128, 2, 2, 3);
