@@ -2089,6 +2089,15 @@ HinvLayout hinv_layout(int64_t d) {
 
 }  // namespace
 
+// Compute units of the current device (256 on an MI355X).
+int64_t gemm_cus() {
+  int dev = 0, ncu = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) !=
+      hipSuccess || ncu <= 0)
+    return 256;
+  return ncu;
+}
+
 // The x6 products, unless MI355Q_GEMM_X6=0 (every product then on the fp32 MFMA).
 bool x6_enabled() {
   static const bool on = [] {
@@ -2168,11 +2177,21 @@ int gemm_f32(const GemmArgs& g, bool b_trans, int batch, hipStream_t stream) {
     // its Cholesky chain 20.4 -> 19.5 ms (lower-only rank-512 updates) ->
     // 18.4 ms (triangular doubling products), 128 batched d = 2048 chains
     // 10.89 -> 10.66 ms, C0 unchanged
+    // The tile whose rounds on the CUs, in 64 x 128-tile units of work, are
+    // fewest wins, the eight-wave tile credited with the 8 % it measured
+    // faster per tile (C0's 4096 x 3072 update: 384 wide tiles are two
+    // rounds, 768 of 128 x 128 three, so the latter stays)
     const bool plain = !g.lower_only && !g.a_lower && !g.b_lower;
-    const int64_t wide_tiles = ((g.M + 255) / 256) * ((g.N + 127) / 128) * batch;
-    if ((plain && wide_tiles >= 128) || (!plain && wide_tiles >= 256))
+    const int64_t cus = gemm_cus();
+    auto rounds = [cus](int64_t tiles) { return (tiles + cus - 1) / cus; };
+    const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 127) / 128) * batch;
+    const int64_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128) * batch;
+    const int64_t t64 = ((g.M + 63) / 64) * ((g.N + 127) / 128) * batch;
+    const bool mid = plain && t128 >= 256;   // 128 x 128 on four waves, else 64 x 128
+    const int64_t alt = mid ? 200 * rounds(t128) : 100 * rounds(t64);
+    if (t256 >= (plain ? 128 : 256) && 400 * rounds(t256) * 100 <= 108 * alt)
       MQ_DMA_X6(256, 128, 4, 2, 3);
-    else if (plain && ((g.M + 127) / 128) * ((g.N + 127) / 128) * batch >= 256)
+    else if (mid)
       MQ_DMA_X6(128, 128, 2, 2, 3);
     else
       MQ_DMA_X6(64, 128, 2, 2, 3);
