@@ -334,20 +334,27 @@ __global__ __launch_bounds__(GNT, 1) void gemm_k128_kernel(GemmArgs g) {
         }
       }
     }
-    const bool diag = g.lower_only && n0 == m0;  // only the diagonal tile straddles gm >= gn
+    // Only the diagonal tile of a lower-only product straddles gm >= gn; the
+    // stores of every other tile are emitted without a test (a test on a
+    // value the compiler cannot see is uniform put each of the 64 stores in
+    // a branch of its own, behind exec-mask updates).
+    const bool diag = g.lower_only && n0 == m0;
+    auto put = [&](auto masked) __attribute__((always_inline)) {
 #pragma unroll
-    for (int bm = 0; bm < 2; ++bm)
+      for (int bm = 0; bm < 2; ++bm)
 #pragma unroll
-      for (int bn = 0; bn < 2; ++bn)
+        for (int bn = 0; bn < 2; ++bn)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int tm = wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          const int tn = wn * 64 + bn * 32 + (lane & 31);
-          const float prod = g.alpha * acc[bm][bn][r];
-          const float out = g.beta == 0.f ? prod : g.beta * cv[(bm * 2 + bn) * 16 + r] + prod;
-          if (!diag || tm >= tn)
-            *const_cast<float*>(at(cbase + (bm * 32 + 8 * (r >> 2) + (r & 3)) * g.ldc + bn * 32, off_c)) = out;
-        }
+          for (int r = 0; r < 16; ++r) {
+            const int tm = wm * 64 + bm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int tn = wn * 64 + bn * 32 + (lane & 31);
+            const float prod = g.alpha * acc[bm][bn][r];
+            const float out = g.beta == 0.f ? prod : g.beta * cv[(bm * 2 + bn) * 16 + r] + prod;
+            if (!decltype(masked)::value || tm >= tn)
+              *const_cast<float*>(at(cbase + (bm * 32 + 8 * (r >> 2) + (r & 3)) * g.ldc + bn * 32, off_c)) = out;
+          }
+    };
+    if (diag) put(std::true_type{}); else put(std::false_type{});
     if (!more) break;
     __syncthreads();  // every wave is done reading lb
     if (BT) store_rk(lb, rv); else store_kn(rv);
@@ -886,19 +893,26 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(GemmArgs g)
           cv[(bm * NB2 + bn) * 16 + r] = g.C[(gm < g.M ? gm : g.M - 1) * g.ldc + (gn < g.N ? gn : g.N - 1)];
         }
   }
+  // A tile inside C and (lower-only products) wholly on or below the
+  // diagonal stores every element without a test; the per-element tests of
+  // edge and diagonal tiles put each store in a branch of its own.
+  const bool whole = m0 + TM <= g.M && n0 + TN <= g.N && (!g.lower_only || m0 >= n0 + TN - 1);
+  auto put = [&](auto masked) __attribute__((always_inline)) {
 #pragma unroll
-  for (int bm = 0; bm < MB; ++bm)
+    for (int bm = 0; bm < MB; ++bm)
 #pragma unroll
-    for (int bn = 0; bn < NB2; ++bn)
+      for (int bn = 0; bn < NB2; ++bn)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t gm = gm_of(bm, r), gn = gn_of(bn);
-        if (gm < g.M && gn < g.N && (!g.lower_only || gm >= gn)) {
-          const float sum = NBLK == 1 ? acc[0][r] + acc[1][r] : acc[bm * NB2 + bn][r];
-          const float prod = g.alpha * sum;
-          g.C[gm * g.ldc + gn] = g.beta == 0.f ? prod : g.beta * cv[(bm * NB2 + bn) * 16 + r] + prod;
+        for (int r = 0; r < 16; ++r) {
+          const int64_t gm = gm_of(bm, r), gn = gn_of(bn);
+          if (!decltype(masked)::value || (gm < g.M && gn < g.N && (!g.lower_only || gm >= gn))) {
+            const float sum = NBLK == 1 ? acc[0][r] + acc[1][r] : acc[bm * NB2 + bn][r];
+            const float prod = g.alpha * sum;
+            g.C[gm * g.ldc + gn] = g.beta == 0.f ? prod : g.beta * cv[(bm * NB2 + bn) * 16 + r] + prod;
+          }
         }
-      }
+  };
+  if (whole) put(std::false_type{}); else put(std::true_type{});
 }
 
 // Global-memory pointers of the dataflow factorisation's task functions
