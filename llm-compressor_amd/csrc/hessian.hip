@@ -719,17 +719,23 @@ __device__ __forceinline__ void stream_item(const SyrkParams& p, char* ring, int
     if (p.beta == 0.f) {
       // H not read: each accumulator register goes straight to its row of H
       // (a store covers 32 consecutive columns of two rows, lanes 0..31 and
-      // 32..63), with no pass through LDS and no barrier
+      // 32..63), with no pass through LDS and no barrier.  An off-diagonal
+      // tile inside H stores without a test (per-element tests put each of
+      // the 128 stores per lane in a branch of its own).
+      auto put = [&](auto masked) __attribute__((always_inline)) {
 #pragma unroll
-      for (int x = 0; x < MB; ++x)
+        for (int x = 0; x < MB; ++x)
 #pragma unroll
-        for (int y = 0; y < NBN; ++y)
+          for (int y = 0; y < NBN; ++y)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int64_t gi = fa0 + wm * 128 + x * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            const int64_t gj = fb0 + wn * NBN * 32 + y * 32 + (lane & 31);
-            if (gi < p.d && gj < p.d && (!diag || gi <= gj)) mat.h[gi * ldh + gj] = p.alpha * acc[x][y][r];
-          }
+            for (int r = 0; r < 16; ++r) {
+              const int64_t gi = fa0 + wm * 128 + x * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+              const int64_t gj = fb0 + wn * NBN * 32 + y * 32 + (lane & 31);
+              if (!decltype(masked)::value || (gi < p.d && gj < p.d && (!diag || gi <= gj)))
+                mat.h[gi * ldh + gj] = p.alpha * acc[x][y][r];
+            }
+      };
+      if (!diag && fa0 + TM <= p.d && fb0 + TM <= p.d) put(std::false_type{}); else put(std::true_type{});
       return;
     }
     if ((ldh & 3) == 0 && (p.d & 3) == 0 && (reinterpret_cast<uintptr_t>(mat.h) & 15) == 0) {
